@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""HXQ decode-GEMV benchmark (Qwen2.5-3B shape, bs=1).
+
+One step = one decoded token's worth of HXQ GEMVs: 36 layers x
+{q, k, v, o, gate, up, down}, each a random-init HXQ layer built as in
+config 0 (codebook + uint8 indices + group-128 affine + 0.1% sidecar), bf16
+activations, fp32 arithmetic.  q/k/v share one launch (same input), gate/up
+share one, o and down one each: 144 launches per step, captured in a HIP
+graph and replayed.  Weights total ~3 GB, far above the 256 MB Infinity
+Cache, so every step streams them from HBM.
+
+Prints one JSON line: value = whole-step HBM GB/s on algorithmic bytes
+(compressed weights + activation in/out), roofline of the dominant kernel
+(the gate/up launch) from HIP events, and the CPU baseline (the reference's
+torch-CPU path restated in oracle/cpu_path.py) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "helix-substrate_amd"))
+
+HBM_PEAK_GBS = 8000.0
+HIDDEN, INTER, KV = 2048, 11008, 256
+N_LAYERS = 36
+PROJ = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
+        ("gate", INTER, HIDDEN), ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=N_LAYERS)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="target CPU time of the cpu_baseline sample (0 = skip)")
+    return ap.parse_args()
+
+
+def build_layers(n_layers, dev):
+    import torch
+    from helix_substrate import synth
+    from helix_substrate.helix_linear import HelixLinear
+
+    layers = []
+    for li in range(n_layers):
+        mods = {}
+        for pi, (name, out_f, in_f) in enumerate(PROJ):
+            L = synth.make_layer_torch(out_f, in_f, seed=1000 + 16 * li + pi, device=dev)
+            mods[name] = HelixLinear(in_f, out_f, L["codebook"], L["indices"],
+                                     L["sidecar_positions"], L["sidecar_values"],
+                                     group_scale=L["group_scale"], group_offset=L["group_offset"],
+                                     group_size=128)
+            del L
+        layers.append(mods)
+        torch.cuda.synchronize(dev)
+    return layers
+
+
+def mat_desc(m):
+    return dict(indices=m.indices, codebook=m.codebook, group_scale=m.group_scale,
+                group_offset=m.group_offset, sc_row_ptr=m._sc_row_ptr, sc_col=m._sc_col,
+                sc_delta=m._sc_delta, bias=m.bias)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the HXQ path has no multi-GPU "
+              "component here); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from helix_substrate import _hxq
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    layers = build_layers(args.layers, dev)
+    print(f"[bench] built {args.layers} layers in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    x_attn = torch.randn(1, HIDDEN, device=dev, generator=g).to(bf)
+    x_o = torch.randn(1, HIDDEN, device=dev, generator=g).to(bf)
+    x_mlp = torch.randn(1, HIDDEN, device=dev, generator=g).to(bf)
+    x_down = torch.randn(1, INTER, device=dev, generator=g).to(bf)
+    outs = [{n: torch.empty(1, o, device=dev, dtype=bf) for n, o, _ in PROJ} for _ in layers]
+    descs = [{n: mat_desc(m) for n, m in mods.items()} for mods in layers]
+
+    def launch_layer(li, which=None):
+        d, o = descs[li], outs[li]
+        if which in (None, "qkv"):
+            _hxq.gemv_multi(x_attn, [d["q"], d["k"], d["v"]], 128, outs=[o["q"], o["k"], o["v"]])
+        if which in (None, "o"):
+            m = layers[li]["o"]
+            _hxq.gemv(x_o, m.indices, m.codebook, m.group_scale, m.group_offset, 128,
+                      m._sc_row_ptr, m._sc_col, m._sc_delta, m.bias, out=o["o"])
+        if which in (None, "gateup"):
+            _hxq.gemv_multi(x_mlp, [d["gate"], d["up"]], 128, outs=[o["gate"], o["up"]])
+        if which in (None, "down"):
+            m = layers[li]["down"]
+            _hxq.gemv(x_down, m.indices, m.codebook, m.group_scale, m.group_offset, 128,
+                      m._sc_row_ptr, m._sc_col, m._sc_delta, m.bias, out=o["down"])
+
+    def step():
+        for li in range(len(layers)):
+            launch_layer(li)
+
+    # algorithmic bytes: compressed weights + activations read + outputs written
+    def act_bytes(names):
+        k = INTER if names == ["down"] else HIDDEN
+        return 2 * k + sum(2 * layers[0][n].out_features for n in names)
+
+    launch_groups = {"qkv": ["q", "k", "v"], "o": ["o"], "gateup": ["gate", "up"], "down": ["down"]}
+    group_bytes = {}
+    for gname, names in launch_groups.items():
+        group_bytes[gname] = sum(layers[0][n].kernel_bytes() for n in names) + act_bytes(names)
+    step_bytes = sum(group_bytes.values()) * len(layers)
+
+    # warm-up eagerly (fills per-device caches, compiles nothing), then capture
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            step()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    ms_graph = ev0.elapsed_time(ev1) / args.steps
+    print(f"[bench] graph: {ms_graph:.4f} ms/step", file=sys.stderr, flush=True)
+
+    # eager launch (no graph) for reference
+    torch.cuda.synchronize(dev)
+    ev0.record()
+    for _ in range(max(3, args.steps // 5)):
+        step()
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    ms_eager = ev0.elapsed_time(ev1) / max(3, args.steps // 5)
+
+    # per-kernel durations with HIP events on the launch stream: a sleep kernel
+    # keeps the GPU busy while the host enqueues, so each event pair brackets
+    # exactly one kernel.
+    per_group_us = {}
+    cur = torch.cuda.current_stream(dev)
+    for gname in launch_groups:
+        evs = []
+        torch.cuda._sleep(50_000_000)
+        for li in range(len(layers)):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(cur)
+            launch_layer(li, gname)
+            b.record(cur)
+            evs.append((a, b))
+        torch.cuda.synchronize(dev)
+        per_group_us[gname] = 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    dom = "gateup"
+    dom_gbs = group_bytes[dom] / (per_group_us[dom] * 1e-6) / 1e9
+    print(f"[bench] per-launch us: {json.dumps({k: round(v, 2) for k, v in per_group_us.items()})}",
+          file=sys.stderr, flush=True)
+
+    value = step_bytes / (ms_graph * 1e-3) / 1e9
+    result = {
+        "metric": "HXQ gather-GEMV HBM GB/s (% of peak) + decode tok/s, Qwen2.5-3B shape, bs=1",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_graph, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "config1: Qwen2.5-3B-shaped decode, every q/k/v/o/gate/up/down HXQ GEMV "
+                        "of 36 layers per step (token), bs=1",
+            "layers": len(layers),
+            "shapes": {n: [o, i] for n, o, i in PROJ},
+            "activations": "bf16", "weights": "uint8 idx + fp32 cb[256] + group-128 fp32 affine "
+                                              "+ 0.1% CSR sidecar",
+            "launches_per_step": 4 * len(layers),
+            "hip_graph": True,
+        },
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
+        "bytes_per_step": step_bytes,
+        "decode_tok_s_gemv_only": round(1000.0 / ms_graph, 1),
+        "ms_per_step_eager": round(ms_eager, 4),
+        "per_launch_us": {k: round(v, 3) for k, v in per_group_us.items()},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel (gate+up, one launch)",
+            "achieved": round(dom_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": group_bytes[dom],
+            "traffic": None,
+        },
+    }
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(mods, seconds):
+    """Reference CPU path (oracle/cpu_path.forward_naive) on layer 0's seven
+    projections, repeated for about `seconds`; GB/s on the same byte count."""
+    import torch
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import cpu_path
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    cpu = {}
+    for name, m in mods.items():
+        cpu[name] = dict(indices=m.indices.cpu(), codebook=m.codebook.cpu(),
+                         group_scale=m.group_scale.cpu(), group_offset=m.group_offset.cpu(),
+                         sc_rows=m._sidecar_rows.cpu(), sc_cols=m._sidecar_cols.cpu(),
+                         sc_deltas=m._sidecar_deltas.cpu())
+    xs = {n_: torch.randn(1, m.in_features) for n_, m in mods.items()}
+    layer_bytes = sum(m.kernel_bytes() for m in mods.values())
+
+    def one_layer():
+        for name, c in cpu.items():
+            cpu_path.forward_naive(xs[name], c["indices"], c["codebook"], c["group_scale"],
+                                   c["group_offset"], 128, c["sc_rows"], c["sc_cols"],
+                                   c["sc_deltas"])
+
+    one_layer()  # warm-up
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        one_layer()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    per_layer = el / reps
+    return {
+        "value": round(layer_bytes / per_layer / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"layer 0's 7 HXQ projections (fp32 x, bs=1) x {reps} repetitions "
+                  f"({el:.1f} s); torch {torch.__version__} CPU, {n} threads",
+        "ms_per_layer": round(per_layer * 1e3, 2),
+        "decode_tok_s_gemv_only_extrapolated": round(1.0 / (per_layer * N_LAYERS), 3),
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+"""ctypes binding of libhxq.so (the gfx950 HIP kernels behind the C ABI in include/hxq.h).
+
+Tensors cross the boundary as raw device pointers plus sizes; the stream is
+torch's current HIP stream of the tensor's device.  A non-zero status raises
+``RuntimeError`` with the library's message -- there is no silent fallback
+(the reference's fused wrappers fail the same way,
+``triton_vq_matmul.py:627-633``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+_LIB_NAME = "libhxq.so"
+_lib = None
+
+HXQ_F32, HXQ_BF16, HXQ_F16 = 0, 1, 2
+HXQ_MAX_MULTI = 8
+
+_DTYPE_CODE = {torch.float32: HXQ_F32, torch.bfloat16: HXQ_BF16, torch.float16: HXQ_F16}
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+
+
+class HxqMatrix(ctypes.Structure):
+    """Mirror of ``hxq_matrix`` in include/hxq.h."""
+
+    _fields_ = [
+        ("indices", P), ("codebook", P), ("group_scale", P), ("group_offset", P),
+        ("sc_row_ptr", P), ("sc_col", P), ("sc_delta", P), ("bias", P), ("y", P),
+        ("out_features", I64),
+    ]
+
+
+# name -> argtypes; every function returns int (hxq_status)
+SIGNATURES = {
+    "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
+    "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_gemv_multi": [P, I32, P, I32, I32, I32, I64, P],
+}
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("HXQ_LIBRARY", Path(__file__).resolve().parent / _LIB_NAME))
+
+
+def lib():
+    """Load libhxq.so once; raise if it was not built."""
+    global _lib
+    if _lib is None:
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} not found: the HIP extension is not built "
+                "(run __graft_entry__.build() or make -C helix-substrate_amd/csrc). "
+                "No CPU fallback exists for device tensors.")
+        L = ctypes.CDLL(str(path))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        L.hxq_last_error.argtypes = []
+        L.hxq_last_error.restype = ctypes.c_char_p
+        L.hxq_abi_version.argtypes = []
+        L.hxq_abi_version.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _check(name: str, rc: int) -> None:
+    if rc != 0:
+        msg = lib().hxq_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need_device(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("HXQ kernels take device tensors only")
+        if not t.is_contiguous():
+            raise RuntimeError("HXQ kernels take contiguous tensors only")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise RuntimeError(f"unsupported activation dtype {dt}") from None
+
+
+# ---------------------------------------------------------------------------
+# Entry points
+# ---------------------------------------------------------------------------
+
+def dequant_f32(indices, codebook, group_scale, group_offset, group_size,
+                sc_row_ptr, sc_col, sc_val, row_begin=0, row_end=None, out=None):
+    """Reconstruct rows [row_begin, row_end) of W in fp32 (bit-exact)."""
+    out_f, in_f = indices.shape
+    row_end = out_f if row_end is None else row_end
+    if out is None:
+        out = torch.empty(row_end - row_begin, in_f, dtype=torch.float32, device=indices.device)
+    _need_device(indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val, out)
+    rc = lib().hxq_dequant_f32(_ptr(indices), _ptr(codebook), _ptr(group_scale), _ptr(group_offset),
+                               int(group_size), _ptr(sc_row_ptr), _ptr(sc_col), _ptr(sc_val),
+                               out_f, in_f, int(row_begin), int(row_end), _ptr(out),
+                               _stream(indices))
+    _check("hxq_dequant_f32", rc)
+    return out
+
+
+def gemv(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr, sc_col,
+         sc_delta, bias=None, out_dtype=torch.float32, out=None):
+    """y = x @ W^T (+bias) for x [n, K] with 1 <= n <= 4; fp32 accumulation."""
+    n, in_f = x.shape
+    out_f = indices.shape[0]
+    if indices.shape[1] != in_f:
+        raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
+    if out is None:
+        out = torch.empty(n, out_f, dtype=out_dtype, device=x.device)
+    _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_delta,
+                 bias, out)
+    rc = lib().hxq_gemv(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
+                        _ptr(group_scale), _ptr(group_offset), int(group_size), _ptr(sc_row_ptr),
+                        _ptr(sc_col), _ptr(sc_delta), _ptr(bias), _ptr(out),
+                        dtype_code(out.dtype), n, out_f, in_f, _stream(x))
+    _check("hxq_gemv", rc)
+    return out
+
+
+def gemv_multi(x, mats, group_size, out_dtype=torch.float32, outs=None):
+    """One launch for several matrices sharing x [1, K].
+
+    ``mats`` is a list of dicts with keys indices, codebook, group_scale,
+    group_offset, sc_row_ptr, sc_col, sc_delta, bias.
+    """
+    if not 1 <= len(mats) <= HXQ_MAX_MULTI:
+        raise RuntimeError(f"gemv_multi takes 1..{HXQ_MAX_MULTI} matrices")
+    in_f = x.shape[-1]
+    arr = (HxqMatrix * len(mats))()
+    if outs is None:
+        outs = [torch.empty(1, m["indices"].shape[0], dtype=out_dtype, device=x.device)
+                for m in mats]
+    for i, (m, y) in enumerate(zip(mats, outs)):
+        _need_device(x, m["indices"], m["codebook"], m.get("group_scale"), m.get("group_offset"),
+                     m.get("sc_row_ptr"), m.get("sc_col"), m.get("sc_delta"), m.get("bias"), y)
+        arr[i] = HxqMatrix(m["indices"].data_ptr(), m["codebook"].data_ptr(),
+                           *(0 if m.get(k) is None else m[k].data_ptr()
+                             for k in ("group_scale", "group_offset", "sc_row_ptr", "sc_col",
+                                       "sc_delta", "bias")),
+                           y.data_ptr(), m["indices"].shape[0])
+    rc = lib().hxq_gemv_multi(_ptr(x), dtype_code(x.dtype), ctypes.cast(arr, P), len(mats),
+                              int(group_size), dtype_code(outs[0].dtype), in_f, _stream(x))
+    _check("hxq_gemv_multi", rc)
+    return outs

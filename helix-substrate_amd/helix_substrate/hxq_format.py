@@ -1,0 +1,107 @@
+"""Host-side layout of the HXQ tensor format on the device.
+
+The on-disk/state_dict form is the reference's CDNAv3 layout:
+``indices`` uint8 [out, in] row-major, ``codebook`` fp32 [256], and a sidecar
+of flat row-major ``positions`` (int64) with ``values`` (fp16 on disk, fp32 in
+memory) -- ``hxq_writer_v3.py:234-296``, ``generate_sidecars_v3.py:133-185``.
+The benchmark configs add a per-group affine ``group_scale``/``group_offset``
+fp32 [out, in/group_size].
+
+For the kernels the sidecar is re-laid out once, at load time, as CSR over
+output rows (``row_ptr`` int32 [out+1], ``col`` int32, ``val`` fp32 replacement
+values, ``delta`` fp32 corrections) -- the row-owned form lets each GEMV wave
+add its own rows' corrections without atomics.  The reference derives the same
+``rows = pos // in``, ``cols = pos % in``, ``delta = value - vq`` at load
+(``helix_linear.py:184-210, 960-1002``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+
+@dataclass
+class SidecarCSR:
+    row_ptr: torch.Tensor   # int32 [out + 1]
+    col: torch.Tensor       # int32 [nnz]
+    val: torch.Tensor       # fp32 [nnz] replacement values (stored order)
+    delta: torch.Tensor     # fp32 [nnz] val - W_affine[pos]
+    rows: torch.Tensor      # int64 [nnz] (reference _sidecar_rows, CSR order)
+    cols: torch.Tensor      # int64 [nnz] (reference _sidecar_cols, CSR order)
+    vq: torch.Tensor        # fp32 [nnz] W_affine[pos] (reference _sidecar_vq_vals)
+
+
+def affine_values(indices: torch.Tensor, codebook: torch.Tensor,
+                  group_scale: Optional[torch.Tensor], group_offset: Optional[torch.Tensor],
+                  group_size: int, rows: torch.Tensor, cols: torch.Tensor) -> torch.Tensor:
+    """W_affine at (rows, cols): cb[idx], then fl(fl(cb*s) + off) with two roundings.
+
+    Two separate tensor ops keep the two fp32 roundings (no fused multiply-add).
+    """
+    v = codebook[indices[rows, cols].long()]
+    if group_scale is not None:
+        g = cols // group_size
+        v = v * group_scale[rows, g]
+        v = v + group_offset[rows, g]
+    return v.to(torch.float32)
+
+
+def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: torch.Tensor,
+                      codebook: torch.Tensor, group_scale: Optional[torch.Tensor] = None,
+                      group_offset: Optional[torch.Tensor] = None,
+                      group_size: int = 128) -> SidecarCSR:
+    """CSR over output rows from flat sidecar positions.
+
+    Entries keep their stored order inside a row (stable sort), so a repeated
+    position resolves like the reader's ``flat[positions] = values`` (the last
+    one wins) when the dequant kernel replays them in order.
+    Raises ValueError on positions outside the matrix.
+    """
+    out_f, in_f = indices.shape
+    pos = positions.reshape(-1).to(torch.int64)
+    val = values.reshape(-1).to(torch.float32)
+    if pos.numel() != val.numel():
+        raise ValueError("sidecar positions and values differ in length")
+    if pos.numel() and (int(pos.min()) < 0 or int(pos.max()) >= out_f * in_f):
+        raise ValueError("sidecar position outside the weight matrix")
+    if pos.numel() >= 2**31:
+        raise ValueError("sidecar too large for int32 CSR")
+    rows = torch.div(pos, in_f, rounding_mode="floor")
+    order = torch.sort(rows, stable=True).indices
+    rows = rows[order]
+    cols = pos[order] - rows * in_f
+    val = val[order]
+    counts = torch.bincount(rows, minlength=out_f)
+    row_ptr = torch.zeros(out_f + 1, dtype=torch.int64, device=pos.device)
+    row_ptr[1:] = torch.cumsum(counts, 0)
+    vq = affine_values(indices, codebook, group_scale, group_offset, group_size, rows, cols)
+    delta = val - vq
+    return SidecarCSR(row_ptr=row_ptr.to(torch.int32).contiguous(),
+                      col=cols.to(torch.int32).contiguous(), val=val.contiguous(),
+                      delta=delta.contiguous(), rows=rows.contiguous(), cols=cols.contiguous(),
+                      vq=vq.contiguous())
+
+
+def check_kernel_shapes(in_features: int, group_size: int, has_affine: bool) -> None:
+    """Shape rules of the HIP kernels (16-byte index vectors, groups of 16k)."""
+    if in_features % 16 != 0:
+        raise ValueError(f"in_features={in_features} must be a multiple of 16")
+    if has_affine and (group_size <= 0 or group_size % 16 or in_features % group_size):
+        raise ValueError(f"group_size={group_size} must be a multiple of 16 dividing "
+                         f"in_features={in_features}")
+
+
+def compressed_bytes(out_f: int, in_f: int, group_size: Optional[int], nnz: int) -> int:
+    """Bytes one contraction must read from the compressed form (not activations).
+
+    indices 1 B/weight + scale/offset 8 B per group + CSR row_ptr 4 B/row
+    + (col 4 B + delta 4 B) per sidecar entry + codebook 1 KiB.
+    """
+    b = out_f * in_f + 1024
+    if group_size:
+        b += out_f * (in_f // group_size) * 8
+    if nnz:
+        b += (out_f + 1) * 4 + nnz * 8
+    return b

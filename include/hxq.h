@@ -1,0 +1,124 @@
+/*
+ * hxq.h -- C ABI of libhxq.so, the MI355X (gfx950) HXQ compressed-linear
+ * hot path.
+ *
+ * Conventions (all entry points):
+ *   - every pointer is a device pointer, caller-owned, contiguous, row-major;
+ *   - work is enqueued on `stream` (hipStream_t; NULL = default stream) and the
+ *     call returns without synchronising;
+ *   - return value is an hxq_status; on error hxq_last_error() (thread-local)
+ *     says what was wrong.  Nothing is launched when an argument is rejected;
+ *   - no entry point allocates device memory; none keeps state between calls;
+ *   - results are deterministic (no floating-point atomics).
+ *
+ * Tensor format (CDNAv3 + per-group affine extension):
+ *   indices       uint8 [out_features, in_features]     (CDNAv3 indices.bin)
+ *   codebook      fp32  [256]                            (CDNAv3 codebook.npy)
+ *   group_scale   fp32  [out_features, in_features/group_size] or NULL
+ *   group_offset  fp32  [out_features, in_features/group_size] or NULL
+ *   sidecar as CSR over output rows, built from the flat sidecar positions
+ *   (CDNAv3 sidecar.npz: positions int64, values fp16->fp32):
+ *     sc_row_ptr  int32 [out_features + 1]
+ *     sc_col      int32 [nnz]
+ *     sc_val      fp32  [nnz]   replacement value      (dequant)
+ *     sc_delta    fp32  [nnz]   value - W_affine[pos]  (contractions)
+ *   Reconstructed weight:
+ *     W[o,k] = fl(fl(codebook[idx[o,k]] * s[o,k/G]) + off[o,k/G])  (affine)
+ *     W[o,k] = codebook[idx[o,k]]                                   (no affine)
+ *     W[o,k] = sc_val  where (o,k) is a sidecar position (replacement).
+ */
+#ifndef HXQ_H
+#define HXQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum hxq_status {
+    HXQ_OK = 0,
+    HXQ_ERR_INVALID_ARG = 1,
+    HXQ_ERR_UNSUPPORTED = 2,
+    HXQ_ERR_HIP = 3
+} hxq_status;
+
+typedef enum hxq_dtype {
+    HXQ_F32 = 0,
+    HXQ_BF16 = 1,
+    HXQ_F16 = 2
+} hxq_dtype;
+
+/* Message for the last failed call on this thread ("" if none). */
+const char *hxq_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int hxq_abi_version(void);
+
+/*
+ * Reconstruct rows [row_begin, row_end) of W into w_out
+ * (fp32 [row_end-row_begin, in_features]); bit-exact with the reference
+ * reader.
+ * Replaces: CDNAv3Reader.reconstruct / reconstruct_block
+ *   (helix_substrate/hxq_reader_v3.py:102-140, 142-187) and
+ *   HelixLinear.decode_weight / _dequant_tile (helix_linear.py:735-781, 881-888).
+ * Requires in_features % 16 == 0; group_size % 16 == 0 when affine is used.
+ */
+int hxq_dequant_f32(const uint8_t *indices, const float *codebook,
+                    const float *group_scale, const float *group_offset,
+                    int32_t group_size, const int32_t *sc_row_ptr,
+                    const int32_t *sc_col, const float *sc_val,
+                    int64_t out_features, int64_t in_features,
+                    int64_t row_begin, int64_t row_end, float *w_out,
+                    hipStream_t stream);
+
+/*
+ * Decode GEMV: y[n, :] = x[n, :] @ W^T (+ bias) for n < n_rows (1 <= n_rows <= 4).
+ * x is fp32/bf16/fp16 [n_rows, in_features]; arithmetic and accumulation in
+ * fp32; y is written in y_dtype [n_rows, out_features].
+ * Replaces: fused_vq_matmul with N == 1 -> _vq_decode_dotprod_kernel +
+ *   _sidecar_fused_kernel + bias (helix_substrate/triton_vq_matmul.py:521-633,
+ *   670-692, 724-725), called from HelixLinear._forward_fused
+ *   (helix_linear.py:468-502).
+ * Requires in_features % 16 == 0, group_size % 16 == 0 (affine).
+ */
+int hxq_gemv(const void *x, int32_t x_dtype, const uint8_t *indices,
+             const float *codebook, const float *group_scale,
+             const float *group_offset, int32_t group_size,
+             const int32_t *sc_row_ptr, const int32_t *sc_col,
+             const float *sc_delta, const float *bias, void *y,
+             int32_t y_dtype, int64_t n_rows, int64_t out_features,
+             int64_t in_features, hipStream_t stream);
+
+/*
+ * Several HXQ matrices that read the same activation (q/k/v, gate/up) in one
+ * launch.  Each descriptor is one HelixLinear; all share in_features and
+ * group_size.  At most HXQ_MAX_MULTI matrices.
+ * Replaces: consecutive HelixLinear.forward calls on one input
+ *   (helix_linear.py:318-361), one fused_vq_matmul each.
+ */
+#define HXQ_MAX_MULTI 8
+typedef struct hxq_matrix {
+    const uint8_t *indices;
+    const float *codebook;
+    const float *group_scale;
+    const float *group_offset;
+    const int32_t *sc_row_ptr;
+    const int32_t *sc_col;
+    const float *sc_delta;
+    const float *bias;
+    void *y;
+    int64_t out_features;
+} hxq_matrix;
+
+int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats,
+                   int32_t n_mats, int32_t group_size, int32_t y_dtype,
+                   int64_t in_features, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HXQ_H */

@@ -1,0 +1,208 @@
+"""CPU oracle for the HXQ hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this module, and only as the checker (or the timed CPU
+baseline).  The product path (``helix_substrate``) never imports it.
+
+Two independent restatements of every function are kept so that one pins the
+other on inputs where no closed form exists:
+
+* the C restatement in ``hxq_oracle.c`` (loaded through ctypes), and
+* the numpy restatement below.
+
+Reference functions restated (file:line under the reference checkout):
+
+* ``reconstruct``      -- ``CDNAv3Reader.reconstruct`` / ``reconstruct_block``
+  (``helix_substrate/hxq_reader_v3.py:102-140,142-187``): gather, then the
+  sidecar *replaces* values.  The per-group affine extension
+  ``fl(fl(cb[idx]*s) + off)`` has no reference implementation; its op order
+  follows ``triton_affine_group_matmul.py:379`` (value*scale, then +offset).
+* ``linear_f64``       -- ``x @ W^T + bias`` (``helix_linear.py:809-820``) in fp64.
+* ``ssm_scan_f64``     -- ``sequential_scan`` (``mamba_scan_chunked.py:42-86``).
+* ``ssm_scan_chunked_np`` -- the chunked closed form of the same recurrence
+  (the algorithm of ``chunked_scan``, ``mamba_scan_chunked.py:89-213``), written
+  in the segment-sum form exp(cumA_t - cumA_s) that cannot overflow; fp64.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+_LIB_PATH = HERE / "libhxq_oracle.so"
+_lib = None
+
+
+def build(force: bool = False) -> Path:
+    """Compile the C oracle with its Makefile (gcc)."""
+    if force or not _LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(_LIB_PATH))
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        lib.hxq_oracle_reconstruct.argtypes = [P, P, P, P, ctypes.c_int32, P, P, I64,
+                                               I64, I64, I64, I64, P]
+        lib.hxq_oracle_reconstruct.restype = ctypes.c_int
+        lib.hxq_oracle_linear_f64.argtypes = [P, I64, P, I64, I64, P, P]
+        lib.hxq_oracle_linear_f64.restype = ctypes.c_int
+        lib.hxq_oracle_ssm_scan_f64.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, I64,
+                                                I64, I64, P, P]
+        lib.hxq_oracle_ssm_scan_f64.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return None if a is None else np.ascontiguousarray(a, dtype=dtype)
+
+
+# --------------------------------------------------------------------------
+# Reconstruction (hxq_reader_v3.py:102-187 + affine extension)
+# --------------------------------------------------------------------------
+
+def reconstruct(indices, codebook, group_scale=None, group_offset=None, group_size=128,
+                sidecar_positions=None, sidecar_values=None, row_begin=0, row_end=None):
+    """C restatement; returns fp32 [row_end-row_begin, in_features]."""
+    idx = _c(indices, np.uint8)
+    out_f, in_f = idx.shape
+    row_end = out_f if row_end is None else row_end
+    cb = _c(codebook, np.float32)
+    s = _c(group_scale, np.float32)
+    o = _c(group_offset, np.float32)
+    pos = _c(sidecar_positions, np.int64)
+    val = _c(sidecar_values, np.float32)
+    nnz = 0 if pos is None else pos.size
+    w = np.empty((row_end - row_begin, in_f), dtype=np.float32)
+    rc = _load().hxq_oracle_reconstruct(_ptr(idx), _ptr(cb), _ptr(s), _ptr(o), int(group_size),
+                                        _ptr(pos), _ptr(val), nnz, out_f, in_f, row_begin,
+                                        row_end, _ptr(w))
+    if rc != 0:
+        raise ValueError(f"hxq_oracle_reconstruct failed (rc={rc})")
+    return w
+
+
+def reconstruct_np(indices, codebook, group_scale=None, group_offset=None, group_size=128,
+                   sidecar_positions=None, sidecar_values=None):
+    """numpy restatement (float32 arithmetic rounds after every op)."""
+    idx = np.asarray(indices)
+    cb = np.asarray(codebook, dtype=np.float32)
+    w = cb[idx]
+    if group_scale is not None:
+        out_f, in_f = idx.shape
+        g = in_f // group_size
+        s = np.repeat(np.asarray(group_scale, np.float32).reshape(out_f, g), group_size, axis=1)
+        o = np.repeat(np.asarray(group_offset, np.float32).reshape(out_f, g), group_size, axis=1)
+        w = (w * s).astype(np.float32)
+        w = (w + o).astype(np.float32)
+    if sidecar_positions is not None:
+        flat = w.ravel().copy()
+        flat[np.asarray(sidecar_positions, np.int64)] = np.asarray(sidecar_values, np.float32)
+        w = flat.reshape(w.shape)
+    return w
+
+
+# --------------------------------------------------------------------------
+# Contraction (fp64)
+# --------------------------------------------------------------------------
+
+def linear_f64(x, w, bias=None):
+    """C restatement: y = x @ w^T (+bias), fp64 accumulation. x [M,K], w [OUT,K]."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    b = _c(bias, np.float32)
+    m, k = x.shape
+    out_f = w.shape[0]
+    assert w.shape[1] == k
+    y = np.empty((m, out_f), dtype=np.float64)
+    rc = _load().hxq_oracle_linear_f64(_ptr(x), m, _ptr(w), out_f, k, _ptr(b), _ptr(y))
+    if rc != 0:
+        raise ValueError("hxq_oracle_linear_f64 failed")
+    return y
+
+
+def linear_np(x, w, bias=None):
+    y = np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)[None, :]
+    return y
+
+
+# --------------------------------------------------------------------------
+# Selective scan
+# --------------------------------------------------------------------------
+
+def ssm_scan_f64(dt, A, x, B, C, D, h0=None):
+    """C restatement of sequential_scan.  Shapes as in hxq_oracle.c."""
+    dt = _c(dt, np.float32)
+    A = _c(A, np.float32)
+    x = _c(x, np.float32)
+    B = _c(B, np.float32)
+    C = _c(C, np.float32)
+    D = _c(np.asarray(D).reshape(-1), np.float32)
+    batch, seqlen, heads, head_dim = x.shape
+    ngroups, state = B.shape[2], B.shape[3]
+    h0 = _c(h0, np.float32)
+    y = np.empty((batch, seqlen, heads, head_dim), dtype=np.float64)
+    hf = np.empty((batch, heads, head_dim, state), dtype=np.float64)
+    rc = _load().hxq_oracle_ssm_scan_f64(_ptr(h0), _ptr(dt), _ptr(A), _ptr(x), _ptr(B), _ptr(C),
+                                         _ptr(D), batch, seqlen, heads, head_dim, state, ngroups,
+                                         _ptr(y), _ptr(hf))
+    if rc != 0:
+        raise ValueError("hxq_oracle_ssm_scan_f64 failed")
+    return y, hf
+
+
+def ssm_scan_chunked_np(dt, A, x, B, C, D, h0=None, chunk=64):
+    """Chunked closed form in fp64 (segment sums, no 1/cumA division).
+
+    Within a chunk with local cumulative log-decay Lc_t = sum_{j<=t} A*dt_j:
+      h_t = exp(Lc_t) h_init + sum_{s<=t} exp(Lc_t - Lc_s) dt_s x_s B_s^T
+      y_t = <h_t, C_t> + D x_t
+    """
+    dt = np.asarray(dt, np.float64)
+    A = np.asarray(A, np.float64)
+    x = np.asarray(x, np.float64)
+    B = np.asarray(B, np.float64)
+    C = np.asarray(C, np.float64)
+    D = np.asarray(D, np.float64).reshape(-1)
+    batch, seqlen, heads, head_dim = x.shape
+    ngroups, state = B.shape[2], B.shape[3]
+    rep = heads // ngroups
+    Bh = np.repeat(B, rep, axis=2)  # [b, L, H, N]
+    Ch = np.repeat(C, rep, axis=2)
+    h = np.zeros((batch, heads, head_dim, state)) if h0 is None else np.asarray(h0, np.float64).copy()
+    y = np.empty((batch, seqlen, heads, head_dim))
+    for cs in range(0, seqlen, chunk):
+        ce = min(cs + chunk, seqlen)
+        la = A[None, None, :] * dt[:, cs:ce, :]            # [b, T, H]
+        lc = np.cumsum(la, axis=1)                          # [b, T, H]
+        seg = lc[:, :, None, :] - lc[:, None, :, :]         # [b, t, s, H]
+        T = ce - cs
+        causal = np.tril(np.ones((T, T), dtype=bool))
+        decay = np.where(causal[None, :, :, None], np.exp(np.minimum(seg, 0.0)), 0.0)
+        cb = np.einsum("btHn,bsHn->btsH", Ch[:, cs:ce], Bh[:, cs:ce])
+        dtx = dt[:, cs:ce, :, None] * x[:, cs:ce]          # [b, T, H, P]
+        y_intra = np.einsum("btsH,bsHp->btHp", cb * decay, dtx)
+        y_init = np.einsum("btHn,bHpn->btHp", Ch[:, cs:ce], h) * np.exp(lc)[..., None]
+        y[:, cs:ce] = y_intra + y_init + D[None, None, :, None] * x[:, cs:ce]
+        # carry: h_end = exp(Lc_T) h + sum_s exp(Lc_T - Lc_s) dtx_s B_s^T
+        w_end = np.exp(lc[:, -1:, :] - lc)                  # [b, T, H]
+        h = h * np.exp(lc[:, -1, :])[:, :, None, None] + np.einsum(
+            "bsH,bsHp,bsHn->bHpn", w_end, dtx, Bh[:, cs:ce])
+    return y, h

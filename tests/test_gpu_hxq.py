@@ -1,0 +1,173 @@
+"""GPU parity of the HIP dequant and decode GEMV kernels against the CPU oracle.
+
+Bars: reconstructed W bit-exact in fp32; GEMV within 1e-5 max-relative
+(max|y - y_ref| / max|y_ref|, fp32 activations) or 2e-2 (bf16 activations /
+outputs), against the fp64 oracle contraction of the oracle's W.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helix_substrate import _hxq, synth
+from helix_substrate.helix_linear import HelixLinear
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 2e-2
+
+
+def _layer(out_f, in_f, seed, **kw):
+    L = synth.make_layer_np(out_f, in_f, seed=seed, **kw)
+    return L, synth.to_torch(L)
+
+
+def _module(T, dev, bias=None):
+    out_f, in_f = T["indices"].shape
+    return HelixLinear(in_f, out_f, T["codebook"], T["indices"], T["sidecar_positions"],
+                       T["sidecar_values"], bias=bias, group_scale=T["group_scale"],
+                       group_offset=T["group_offset"], group_size=T["group_size"]).to(dev)
+
+
+def _oracle_w(L):
+    return oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
+                              L["group_size"], L["sidecar_positions"], L["sidecar_values"])
+
+
+def _maxrel(y, y_ref):
+    return float(np.abs(np.asarray(y, np.float64) - y_ref).max() / np.abs(y_ref).max())
+
+
+# ------------------------------------------------------------------- dequant
+
+@pytest.mark.parametrize("out_f,in_f,kw", [
+    (2048, 2048, {}),                                  # config 0
+    (37, 11008, {"density": 0.003}),                   # ragged rows, K not a multiple of 1024
+    (5, 16, {"group_size": 16, "density": 0.2}),       # smallest K
+    (64, 256, {"affine": False}),                      # plain CDNAv3 (no affine)
+    (64, 256, {"sidecar": False}),
+])
+def test_dequant_bit_exact(dev, out_f, in_f, kw):
+    L, T = _layer(out_f, in_f, seed=out_f + in_f, **kw)
+    m = _module(T, dev)
+    W = m.decode_weight().cpu().numpy()
+    np.testing.assert_array_equal(W.view(np.uint32), _oracle_w(L).view(np.uint32))
+
+
+def test_dequant_row_blocks_and_duplicates(dev):
+    L, T = _layer(300, 512, seed=21, density=0.01)
+    # repeat some positions with new values: the later entry must win
+    pos = np.concatenate([L["sidecar_positions"], L["sidecar_positions"][:20]])
+    val = np.concatenate([L["sidecar_values"], -L["sidecar_values"][:20] * 2])
+    T["sidecar_positions"] = torch.from_numpy(pos)
+    T["sidecar_values"] = torch.from_numpy(val.astype(np.float32))
+    m = _module(T, dev)
+    W_ref = oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
+                               128, pos, val.astype(np.float32))
+    for r0, r1 in [(0, 300), (0, 1), (17, 133), (299, 300)]:
+        blk = m._dequant_tile(r0, r1).cpu().numpy()
+        np.testing.assert_array_equal(blk.view(np.uint32), W_ref[r0:r1].view(np.uint32))
+
+
+# ---------------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("out_f,in_f", [
+    (2048, 2048),     # config 0 / q, o
+    (256, 2048),      # k, v
+    (11008, 2048),    # gate, up
+    (2048, 11008),    # down
+    (512, 3584),      # Qwen2.5-7B kv
+    (96, 16),
+])
+def test_gemv_f32_matches_oracle(dev, out_f, in_f):
+    L, T = _layer(out_f, in_f, seed=out_f * 3 + in_f)
+    m = _module(T, dev)
+    x = torch.randn(1, in_f, generator=torch.Generator().manual_seed(1))
+    y = m(x.to(dev))
+    assert m._last_dispatch_path == "hip_gemv"
+    assert y.dtype == torch.float32
+    rel = _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L)))
+    assert rel <= TOL_F32, rel
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+def test_gemv_multi_row_inputs(dev, n):
+    L, T = _layer(640, 1536, seed=40 + n)
+    bias = torch.linspace(-0.5, 0.5, 640)
+    m = _module(T, dev, bias=bias)
+    x = torch.randn(n, 1536, generator=torch.Generator().manual_seed(n))
+    y = m(x.to(dev)).cpu().numpy()
+    yr = oracle.linear_f64(x.numpy(), _oracle_w(L), bias.numpy())
+    assert _maxrel(y, yr) <= TOL_F32
+
+
+def test_gemv_bf16_activations(dev):
+    L, T = _layer(2048, 2048, seed=5)
+    m = _module(T, dev)
+    xb = torch.randn(1, 2048, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    W = _oracle_w(L)
+    yr = oracle.linear_f64(xb.float().numpy(), W)
+    y = m(xb.to(dev))
+    assert y.dtype == torch.bfloat16
+    assert _maxrel(y.float().cpu().numpy(), yr) <= TOL_BF16
+    # the input is exact in fp32, so an fp32 output must meet the fp32 bar
+    y32 = _hxq.gemv(xb.to(dev), m.indices, m.codebook, m.group_scale, m.group_offset, 128,
+                    m._sc_row_ptr, m._sc_col, m._sc_delta, None, out_dtype=torch.float32)
+    assert _maxrel(y32.cpu().numpy(), yr) <= TOL_F32
+
+
+def test_gemv_3d_input_and_fp16(dev):
+    L, T = _layer(128, 512, seed=6)
+    m = _module(T, dev)
+    x = torch.randn(2, 3, 512, generator=torch.Generator().manual_seed(7)).to(torch.float16)
+    y = m(x.to(dev))
+    assert y.shape == (2, 3, 128) and y.dtype == torch.float16
+    yr = oracle.linear_f64(x.reshape(-1, 512).float().numpy(), _oracle_w(L))
+    assert _maxrel(y.reshape(-1, 128).float().cpu().numpy(), yr) <= TOL_BF16
+
+
+def test_gemv_without_affine_or_sidecar(dev):
+    for kw in ({"affine": False}, {"sidecar": False}, {"affine": False, "sidecar": False}):
+        L, T = _layer(300, 1024, seed=9, **kw)
+        m = _module(T, dev)
+        x = torch.randn(1, 1024, generator=torch.Generator().manual_seed(3))
+        rel = _maxrel(m(x.to(dev)).cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L)))
+        assert rel <= TOL_F32, (kw, rel)
+
+
+def test_gemv_multi_matrices(dev):
+    # q/k/v shapes in one launch, each with its own codebook/affine/sidecar
+    layers = [_layer(o, 2048, seed=100 + i, sigma=0.02 * (i + 1)) for i, o in enumerate((2048, 256, 256))]
+    mods = [_module(T, dev) for _, T in layers]
+    x = torch.randn(1, 2048, generator=torch.Generator().manual_seed(4))
+    xd = x.to(dev)
+    mats = [dict(indices=m.indices, codebook=m.codebook, group_scale=m.group_scale,
+                 group_offset=m.group_offset, sc_row_ptr=m._sc_row_ptr, sc_col=m._sc_col,
+                 sc_delta=m._sc_delta, bias=None) for m in mods]
+    outs = _hxq.gemv_multi(xd, mats, 128)
+    for (L, _), y in zip(layers, outs):
+        assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= TOL_F32
+
+
+def test_gemv_deterministic(dev):
+    L, T = _layer(2048, 11008, seed=11)
+    m = _module(T, dev)
+    x = torch.randn(1, 11008, device=dev)
+    a = m(x)
+    b = m(x)
+    assert torch.equal(a, b)
+
+
+def test_empty_batch(dev):
+    L, T = _layer(64, 128, seed=12)
+    m = _module(T, dev)
+    y = m(torch.empty(0, 128, device=dev))
+    assert y.shape == (0, 64)
+
+
+def test_device_input_with_cpu_module_fails_loudly(dev):
+    L, T = _layer(64, 128, seed=13)
+    m = _module(T, torch.device("cpu"))
+    with pytest.raises(RuntimeError):
+        m(torch.randn(1, 128, device=dev))
