@@ -91,6 +91,36 @@ __device__ __forceinline__ float affine_exact(float c, float s, float o) {
     return t + o;
 }
 
+// Workgroup barrier that orders LDS only: it waits for this wave's LDS
+// traffic (lgkmcnt) but leaves global loads in flight, so prefetched data
+// can stream in across the barrier.  Use it where no global stores need to
+// become visible to other waves.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Raw buffer resource over [base, base + bytes): loads at or past `bytes`
+// return zero (hardware range check).  bytes must fit in 32 bits.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                             static_cast<int>(static_cast<uint32_t>(bytes)),
+                                             0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float buf_loadf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ int32_t buf_loadi(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 // Full wave64 sum; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -11,20 +11,24 @@
 // 16 weights instead of one per weight).  This changes rounding relative to
 // dequantising first; it stays far inside the 1e-5 relative bound.
 //
-// Work decomposition (wave64, 1024-thread blocks = 16 waves):
+// Work decomposition (wave64, 512-thread blocks = 8 waves, 2 blocks per CU):
 //   * the index matrix is streamed in "chunks" of 1024 columns: lane l of a
 //     wave loads the 16 bytes at columns [16l, 16l+16) with one dwordx4 load,
 //     so one wave load covers 1 KiB of one row, fully coalesced;
-//   * a block tile is RPB = (16/S)*R rows; the 16 waves split as S K-slices x
-//     (16/S) row groups; each wave owns R rows of its K-slice, so every x
-//     value it loads is reused R times from registers;
+//   * block b owns the contiguous rows [T*b/G, T*(b+1)/G) of the concatenated
+//     row space of all matrices in the launch;
+//   * its 8 waves split as S K-slices x (8/S) row lanes; a slice is at most
+//     CPS chunks, whose activations stay in registers for the whole kernel;
+//   * each wave walks its rows in batches of RB rows, issuing every load of a
+//     batch before computing it; two blocks per CU (16 waves) hide the
+//     latency; loads are clamped to valid addresses instead of branched
+//     around, and results of out-of-range rows are not stored;
 //   * the 256-entry codebook lives in LDS replicated NREP times with entry j
 //     of replica r at dword j*NREP + r; lane l reads replica l % NREP, so the
 //     random lookups of one wave hit distinct banks (no bank conflicts);
-//   * the S partial sums of a row are combined in LDS in a fixed order, so the
-//     result is deterministic;
-//   * blocks are persistent over tiles; the codebook table is refilled only
-//     when a block moves on to the next matrix.
+//   * row partials go to LDS; the sidecar corrections of the block's rows are
+//     summed by one thread per row at the end; a final pass adds slices,
+//     sidecar and bias in a fixed order (deterministic, no atomics).
 #include <algorithm>
 
 #include "hxq_common.h"
@@ -42,25 +46,28 @@ struct GemvMat {
     const float *bias;
     void *y;
     int64_t out;
-    int32_t tile_begin;
-    int32_t pad_;
 };
 
-struct GemvParams {
+struct GemvMats {
+    GemvMat m[HXQ_MAX_MULTI];
+};
+
+// Launch header.  It travels as leading scalar kernel arguments so the
+// hardware preloads it into SGPRs (no kernarg memory round trip).
+struct GemvHeader {
     const void *x;
     int64_t K;
     int32_t group;
-    int32_t n_mats;
-    int32_t n_tiles;
     int32_t S;
     int32_t nchunks;
     int32_t x_dtype;
     int32_t y_dtype;
-    int32_t n_x;
-    GemvMat m[HXQ_MAX_MULTI];
+    int32_t n_mats;
+    int32_t red_rows;  // LDS reduction slots per block (rows)
+    int32_t xlds;      // 1: activations staged in LDS for the sidecar gather
+    int32_t bb[HXQ_MAX_MULTI];  // bb[m]: first block after matrix m (cumulative)
 };
 
-constexpr int kMaxWaves = 16;  // waves per block for n_x == 1 (8 for n_x > 1)
 constexpr int kChunk = 1024;  // columns per wave load (64 lanes x 16 bytes)
 
 // Load 16 consecutive activations starting at x + base (fp32/bf16/fp16).
@@ -104,11 +111,11 @@ __device__ __forceinline__ void store_y(void *y, int64_t i, int dt, float v) {
     else static_cast<uint16_t *>(y)[i] = f32_to_f16(v);
 }
 
-// Codebook lookup of byte b (0..3) of the packed index word w.
+// Codebook lookup of byte B (0..3) of the packed index word w.
 //   NREP == 64: entry stride is 256 bytes and the lane's replica offset
 //   (lane*4 < 256) fits in the low byte, so the LDS byte address is
-//   {0, 0, w.byte[b], lane_off} -- one v_perm_b32 builds it.
-//   Other NREP: shift/mask arithmetic.
+//   {0, 0, w.byte[B], lane_off} -- one v_perm_b32 builds it.
+//   NREP == 32: shift/mask arithmetic.
 template <int NREP, int B>
 __device__ __forceinline__ float tbl_lookup(const float *tbl, uint32_t lane_off, uint32_t w) {
     if constexpr (NREP == 64) {
@@ -121,176 +128,326 @@ __device__ __forceinline__ float tbl_lookup(const float *tbl, uint32_t lane_off,
     }
 }
 
-template <int NREP, int R, int NX, int WAVES>
-__global__ __launch_bounds__(WAVES * kWave) void gemv_kernel(const GemvParams p) {
-    constexpr int kGemvThreads = WAVES * kWave;
-    constexpr int kGemvWaves = WAVES;
+// Wave64 sum via DPP; the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+    return v + __int_as_float(s);
+}
+
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);  // row_mirror: every lane holds its row's sum
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;                    // lane 63 holds the wave total
+}
+
+// One pipeline stage: the index words and affine factors of one row x CPS chunks.
+template <int CPS>
+struct GemvItem {
+    u32x4 q[CPS];
+    float sc[CPS];
+    float of[CPS];
+};
+
+constexpr int kEntCap = 512;  // sidecar entries per block staged in LDS
+
+// Kernel phases:
+//   block -> matrix: the host gives each matrix its own contiguous run of
+//             blocks (bb[]); a block owns rows [out*b/nb, out*(b+1)/nb) of it;
+//   prologue  every global load the block needs first is issued before the
+//             first wait: activations, this thread's codebook slots, row_ptr
+//             of the block's rows, and the first batch of index rows;
+//   table     codebook -> LDS (NREP replicas, conflict-free float4 writes);
+//             activations -> LDS (fp32) when they fit, for the sidecar gather;
+//   stream    batches of RB rows per wave, loads of a batch issued together,
+//             double-buffered (batch i+1 in flight while batch i computes);
+//             rows a wave does not own get an out-of-range buffer offset
+//             (no memory traffic) and are not computed;
+//   epilogue  sidecar values x[col]*delta -> LDS; one thread per output row
+//             adds slices, its sidecar entries (CSR order) and bias, and
+//             stores y.  Fixed summation order: deterministic.
+// Barriers order LDS only (lds_barrier), so prefetched loads stay in flight.
+// Occupancy target: 4 waves per SIMD (two 8-wave blocks per CU, <= 128 VGPRs);
+// the long-row variant (4 chunks per slice) accepts 2.
+template <int NREP, int NX, int CPS, int WAVES, bool AFFINE, int RB, int XT>
+__global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
+    const void *__restrict__ x, int32_t K, int32_t group, int32_t S, int32_t nchunks,
+    int32_t flags, int32_t red_rows, int32_t bb1, int32_t bb2, int32_t bb3, int32_t bb4,
+    int32_t bb5, int32_t bb6, int32_t bb7, const GemvMats mats) {
+    constexpr bool XF32 = XT == HXQ_F32;
+    constexpr int NT = WAVES * kWave;
+    constexpr int TPW = 256 * NREP / (4 * NT);  // table float4 writes per thread
+    static_assert(TPW >= 1 && (256 * NREP) % (4 * NT) == 0, "table/thread-count mismatch");
+    constexpr uint32_t kOob = 0x80000000u;      // buffer offset past any range: reads 0
+    const int y_dtype = flags & 0xf;
+    const bool xlds = (flags >> 4) & 1;
+
+    // ---- block -> matrix (scalar compares on preloaded arguments)
+    const int bid = blockIdx.x;
+    const int mi = (bid >= bb1) + (bid >= bb2) + (bid >= bb3) + (bid >= bb4) + (bid >= bb5) +
+                   (bid >= bb6) + (bid >= bb7);
+    const int b_lo = mi == 0 ? 0 : mi == 1 ? bb1 : mi == 2 ? bb2 : mi == 3 ? bb3 : mi == 4 ? bb4
+                   : mi == 5 ? bb5 : mi == 6 ? bb6 : bb7;
+    const GemvMat &M = mats.m[mi];
+
     extern __shared__ float smem[];
-    float *tbl = smem;                 // [256 * NREP]
-    float *red = smem + 256 * NREP;    // [WAVES * R * NX]
+    float *tbl = smem;                                      // [256 * NREP]
+    float *xl = tbl + 256 * NREP;                           // [NX * K] when xlds
+    float *red = xl + (xlds ? NX * K : 0);                  // [red_rows * NX * S]
+    float *ent = red + red_rows * NX * S;                   // [kEntCap * NX]
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int S = p.S;
-    const int RG = kGemvWaves / S;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int RG = WAVES / S;
     const int s_id = wave % S;
     const int rg = wave / S;
-    const int RPB = RG * R;
-    const int64_t K = p.K;
-    const int c_begin = s_id * p.nchunks / S;
-    const int c_end = (s_id + 1) * p.nchunks / S;
+    const int c_lo = s_id * nchunks / S;
+    const int nc = (s_id + 1) * nchunks / S - c_lo;  // chunks of this slice (<= CPS)
     const uint32_t lane_off = static_cast<uint32_t>(lane % NREP) * 4u;
-    const int64_t xstride = K;  // activations are [n_x, K]
+    uint32_t koff[CPS];
+    bool kok[CPS];
+#pragma unroll
+    for (int ci = 0; ci < CPS; ++ci) {
+        const int k0 = (c_lo + ci) * kChunk + lane * 16;
+        kok[ci] = ci < nc && k0 < K;
+        koff[ci] = static_cast<uint32_t>(k0);
+    }
 
-    int cur = -1;
-    for (int tile = blockIdx.x; tile < p.n_tiles; tile += gridDim.x) {
-        int mi = 0;
-        while (mi + 1 < p.n_mats && tile >= p.m[mi + 1].tile_begin) ++mi;
-        const uint8_t *__restrict__ idx = p.m[mi].idx;
-        const float *__restrict__ gs = p.m[mi].gs;
-        const float *__restrict__ go = p.m[mi].go;
-        const int64_t out = p.m[mi].out;
-        if (mi != cur) {
-            const float *cb = p.m[mi].cb;
-            __syncthreads();  // previous matrix's lookups are done
-            for (int e = threadIdx.x; e < 256 * NREP; e += kGemvThreads) tbl[e] = cb[e / NREP];
-            __syncthreads();
-            cur = mi;
+    // rows of this block
+    const int64_t out = M.out;
+    const int32_t b_hi = mi == 0 ? bb1 : mi == 1 ? bb2 : mi == 2 ? bb3 : mi == 3 ? bb4 : mi == 4 ? bb5
+                       : mi == 5 ? bb6 : mi == 6 ? bb7 : static_cast<int32_t>(gridDim.x);
+    const int64_t nblk = b_hi - b_lo, lb = bid - b_lo;
+    const int64_t lo = out * lb / nblk;
+    const int64_t n_rows = out * (lb + 1) / nblk - lo;
+    const int64_t ngroups = AFFINE ? K / group : 0;
+    const int64_t n_mine = n_rows > rg ? (n_rows - rg + RG - 1) / RG : 0;
+    const bool has_sc = M.rp != nullptr;
+
+    // ---- prologue: issue everything, wait later
+    constexpr int XV = XF32 ? 4 : 2;  // 16-byte loads per 16 activations
+    u32x4 xraw[CPS][NX][XV];
+    {
+        const int esz = XF32 ? 4 : 2;
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (int64_t)NX * K * esz);
+#pragma unroll
+        for (int ci = 0; ci < CPS; ++ci)
+#pragma unroll
+            for (int n = 0; n < NX; ++n)
+#pragma unroll
+                for (int v = 0; v < XV; ++v)
+                    xraw[ci][n][v] = buf_load16(xr, (n * K + koff[ci]) * esz + 16u * v);
+    }
+    float cbv[TPW];
+    {
+        const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, 256 * 4);
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) {
+            const uint32_t e = 4u * (threadIdx.x + k * NT);  // first replica slot
+            cbv[k] = buf_loadf(cr, (e / NREP) * 4u);
         }
-        const int64_t row0 = (int64_t)(tile - p.m[mi].tile_begin) * RPB + rg * R;
-        const bool affine = gs != nullptr;
-        const int64_t ngroups = affine ? K / p.group : 0;
+    }
+    const __amdgpu_buffer_rsrc_t rp_r = make_rsrc(M.rp, has_sc ? (out + 1) * 4 : 0);
+    // final-pass outputs: thread t handles (row lo + t / NX, activation t % NX)
+    const int64_t my_rl = threadIdx.x / NX;
+    const int32_t my_j0 = buf_loadi(rp_r, static_cast<uint32_t>((lo + my_rl) * 4));
+    const int32_t my_j1 = buf_loadi(rp_r, static_cast<uint32_t>((lo + my_rl + 1) * 4));
+    const int32_t blk_j0 = buf_loadi(rp_r, static_cast<uint32_t>(lo * 4));
+    const int32_t blk_j1 = buf_loadi(rp_r, static_cast<uint32_t>((lo + n_rows) * 4));
 
-        float acc[R][NX];
+    const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(M.idx, out * K);
+    const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(M.gs, AFFINE ? out * ngroups * 4 : 0);
+    const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(M.go, AFFINE ? out * ngroups * 4 : 0);
+    auto load_item = [&](int64_t i, GemvItem<CPS> &it) {
+        const bool mine = i < n_mine;
+        const uint32_t row = static_cast<uint32_t>(lo + rg + i * RG);
 #pragma unroll
-        for (int i = 0; i < R; ++i)
+        for (int ci = 0; ci < CPS; ++ci) {
+            it.q[ci] = buf_load16(q_rsrc, mine ? row * static_cast<uint32_t>(K) + koff[ci] : kOob);
+            if constexpr (AFFINE) {
+                const uint32_t g4 =
+                    (row * static_cast<uint32_t>(ngroups) + koff[ci] / static_cast<uint32_t>(group)) * 4u;
+                it.sc[ci] = buf_loadf(s_rsrc, mine ? g4 : kOob);
+                it.of[ci] = buf_loadf(o_rsrc, mine ? g4 : kOob);
+            } else {
+                it.sc[ci] = 1.f;
+                it.of[ci] = 0.f;
+            }
+        }
+    };
+    GemvItem<CPS> it[RB];
 #pragma unroll
-            for (int n = 0; n < NX; ++n) acc[i][n] = 0.f;
+    for (int b = 0; b < RB; ++b) load_item(b, it[b]);
+    __builtin_amdgcn_sched_barrier(0);  // all prologue loads are issued before any wait
 
-        for (int c = c_begin; c < c_end; ++c) {
-            const int64_t k0 = (int64_t)c * kChunk + lane * 16;
-            if (k0 >= K) continue;
-            u32x4 q[R];
-            float sc[R], of[R];
-            const int64_t g = affine ? k0 / p.group : 0;
+    // ---- table (+ activations to registers / LDS)
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int64_t row = row0 + i;
-                if (row < out) {
-                    q[i] = __builtin_nontemporal_load(
-                        reinterpret_cast<const u32x4 *>(idx + row * K + k0));
-                    sc[i] = affine ? gs[row * ngroups + g] : 1.f;
-                    of[i] = affine ? go[row * ngroups + g] : 0.f;
-                } else {
-                    q[i] = u32x4{0u, 0u, 0u, 0u};
-                    sc[i] = 0.f;
-                    of[i] = 0.f;
-                }
-            }
-            float xv[NX][16];
-            float xs[NX];
+    for (int k = 0; k < TPW; ++k) {
+        const int e = 4 * (threadIdx.x + k * NT);
+        *reinterpret_cast<float4 *>(tbl + e) = make_float4(cbv[k], cbv[k], cbv[k], cbv[k]);
+    }
+    float xv[CPS][NX][16];
+    float xs[CPS][NX];
 #pragma unroll
-            for (int n = 0; n < NX; ++n) {
-                load_x16(p.x, n * xstride + k0, p.x_dtype, xv[n]);
-                float t = 0.f;
+    for (int ci = 0; ci < CPS; ++ci)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) t += xv[n][j];
-                xs[n] = t;
-            }
+        for (int n = 0; n < NX; ++n) {
+            if constexpr (XF32) {
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const uint32_t w[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
-                float part[NX];
+                for (int v = 0; v < 4; ++v)
 #pragma unroll
-                for (int n = 0; n < NX; ++n) part[n] = 0.f;
+                    for (int j = 0; j < 4; ++j)
+                        xv[ci][n][4 * v + j] = kok[ci] ? __uint_as_float(xraw[ci][n][v][j]) : 0.f;
+            } else {
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const float c0 = tbl_lookup<NREP, 0>(tbl, lane_off, w[d]);
-                    const float c1 = tbl_lookup<NREP, 1>(tbl, lane_off, w[d]);
-                    const float c2 = tbl_lookup<NREP, 2>(tbl, lane_off, w[d]);
-                    const float c3 = tbl_lookup<NREP, 3>(tbl, lane_off, w[d]);
+                for (int v = 0; v < 2; ++v)
 #pragma unroll
-                    for (int n = 0; n < NX; ++n) {
-                        part[n] = fmaf(xv[n][4 * d + 0], c0, part[n]);
-                        part[n] = fmaf(xv[n][4 * d + 1], c1, part[n]);
-                        part[n] = fmaf(xv[n][4 * d + 2], c2, part[n]);
-                        part[n] = fmaf(xv[n][4 * d + 3], c3, part[n]);
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t w = xraw[ci][n][v][j];
+                        float a, b;
+                        if constexpr (XT == HXQ_BF16) {
+                            a = __uint_as_float(w << 16);
+                            b = __uint_as_float(w & 0xffff0000u);
+                        } else {
+                            a = f16_to_f32(static_cast<uint16_t>(w & 0xffffu));
+                            b = f16_to_f32(static_cast<uint16_t>(w >> 16));
+                        }
+                        xv[ci][n][8 * v + 2 * j] = kok[ci] ? a : 0.f;
+                        xv[ci][n][8 * v + 2 * j + 1] = kok[ci] ? b : 0.f;
                     }
-                }
+            }
+            float t = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t += xv[ci][n][j];
+            xs[ci][n] = t;
+            if (xlds && rg == 0 && kok[ci]) {
+                float4 *dst = reinterpret_cast<float4 *>(xl + n * K + koff[ci]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    dst[v] = make_float4(xv[ci][n][4 * v], xv[ci][n][4 * v + 1],
+                                         xv[ci][n][4 * v + 2], xv[ci][n][4 * v + 3]);
+            }
+        }
+    lds_barrier();
+
+    // sidecar entries of this block, first round: col/delta loads now
+    const int32_t nent = has_sc ? blk_j1 - blk_j0 : 0;
+    const __amdgpu_buffer_rsrc_t col_r = make_rsrc(M.col, has_sc ? (int64_t)blk_j1 * 4 : 0);
+    const __amdgpu_buffer_rsrc_t dl_r = make_rsrc(M.delta, has_sc ? (int64_t)blk_j1 * 4 : 0);
+    const uint32_t e0 = (static_cast<uint32_t>(blk_j0) + threadIdx.x) * 4u;
+    const int32_t sc_col0 = buf_loadi(col_r, e0);
+    const float sc_dl0 = buf_loadf(dl_r, e0);
+
+    // ---- stream
+    auto compute_item = [&](int64_t i, const GemvItem<CPS> &itm) {
+        float acc[NX];
+#pragma unroll
+        for (int n = 0; n < NX; ++n) acc[n] = 0.f;
+#pragma unroll
+        for (int ci = 0; ci < CPS; ++ci) {
+            float part[NX];
+#pragma unroll
+            for (int n = 0; n < NX; ++n) part[n] = 0.f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t w = itm.q[ci][d];
+                const float c0 = tbl_lookup<NREP, 0>(tbl, lane_off, w);
+                const float c1 = tbl_lookup<NREP, 1>(tbl, lane_off, w);
+                const float c2 = tbl_lookup<NREP, 2>(tbl, lane_off, w);
+                const float c3 = tbl_lookup<NREP, 3>(tbl, lane_off, w);
 #pragma unroll
                 for (int n = 0; n < NX; ++n) {
-                    acc[i][n] = fmaf(part[n], sc[i], acc[i][n]);
-                    acc[i][n] = fmaf(of[i], xs[n], acc[i][n]);
+                    part[n] = fmaf(xv[ci][n][4 * d + 0], c0, part[n]);
+                    part[n] = fmaf(xv[ci][n][4 * d + 1], c1, part[n]);
+                    part[n] = fmaf(xv[ci][n][4 * d + 2], c2, part[n]);
+                    part[n] = fmaf(xv[ci][n][4 * d + 3], c3, part[n]);
                 }
             }
-        }
-
-        // Sidecar correction: slice 0 adds x[col] * delta for its rows.
-        const int32_t *__restrict__ rp = p.m[mi].rp;
-        if (s_id == 0 && rp != nullptr) {
-            const int32_t *__restrict__ col = p.m[mi].col;
-            const float *__restrict__ delta = p.m[mi].delta;
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int64_t row = row0 + i;
-                if (row >= out) continue;
-                const int32_t jb = rp[row], je = rp[row + 1];
-                for (int32_t j = jb + lane; j < je; j += kWave) {
-                    const int32_t cc = col[j];
-                    const float dv = delta[j];
-#pragma unroll
-                    for (int n = 0; n < NX; ++n)
-                        acc[i][n] = fmaf(load_x1(p.x, n * xstride + cc, p.x_dtype), dv, acc[i][n]);
-                }
-            }
-        }
-
-        const float *__restrict__ bias = p.m[mi].bias;
-        void *y = p.m[mi].y;
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
 #pragma unroll
             for (int n = 0; n < NX; ++n) {
-                const float v = wave_sum(acc[i][n]);
-                const int64_t row = row0 + i;
-                if (S == 1) {
-                    if (lane == 0 && row < out)
-                        store_y(y, n * out + row, p.y_dtype, v + (bias ? bias[row] : 0.f));
-                } else if (lane == 0) {
-                    red[((rg * R + i) * NX + n) * S + s_id] = v;
-                }
+                acc[n] = fmaf(part[n], itm.sc[ci], acc[n]);
+                acc[n] = fmaf(itm.of[ci], xs[ci][n], acc[n]);
             }
         }
-        if (S > 1) {
-            __syncthreads();
-            for (int t = threadIdx.x; t < RPB * NX; t += kGemvThreads) {
-                const int rl = t / NX, n = t % NX;
-                const int64_t row = (int64_t)(tile - p.m[mi].tile_begin) * RPB + rl;
-                if (row < out) {
-                    float v = 0.f;
-                    for (int s = 0; s < S; ++s) v += red[t * S + s];
-                    store_y(y, n * out + row, p.y_dtype, v + (bias ? bias[row] : 0.f));
-                }
-            }
-            __syncthreads();
+        const int64_t rl = rg + i * RG;  // row within the block's range
+#pragma unroll
+        for (int n = 0; n < NX; ++n) {
+            const float v = wave_sum_lane63(acc[n]);
+            if (lane == kWave - 1) red[(rl * NX + n) * S + s_id] = v;
         }
+    };
+    // double-buffered batches: the next batch's loads are issued before the
+    // current batch is computed (it2 is the second buffer)
+    GemvItem<CPS> it2[RB];
+    for (int64_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
+#pragma unroll
+        for (int b = 0; b < RB; ++b) load_item(i0 + RB + b, it2[b]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+            if (i0 + b < n_mine) compute_item(i0 + b, it[b]);
+        if (i0 + RB >= n_mine) break;
+#pragma unroll
+        for (int b = 0; b < RB; ++b) load_item(i0 + 2 * RB + b, it[b]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+            if (i0 + RB + b < n_mine) compute_item(i0 + RB + b, it2[b]);
+    }
+
+    // ---- epilogue
+    auto xval = [&](int n, int32_t c) -> float {
+        return xlds ? xl[n * K + c] : load_x1(x, n * K + c, XT);
+    };
+    lds_barrier();  // red complete
+    if (has_sc) {
+        const int32_t lim = nent < kEntCap ? nent : kEntCap;
+        for (int32_t e = threadIdx.x; e < lim; e += NT) {
+            int32_t c;
+            float dv;
+            if (e == static_cast<int32_t>(threadIdx.x)) {
+                c = sc_col0;
+                dv = sc_dl0;
+            } else {
+                c = M.col[blk_j0 + e];
+                dv = M.delta[blk_j0 + e];
+            }
+#pragma unroll
+            for (int n = 0; n < NX; ++n) ent[e * NX + n] = xval(n, c) * dv;
+        }
+    }
+    lds_barrier();
+    if (threadIdx.x < n_rows * NX) {
+        const int n = static_cast<int>(threadIdx.x % NX);
+        float v = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) v += red[threadIdx.x * S + s2];
+        if (has_sc) {
+            float scs = 0.f;
+            for (int32_t j = my_j0; j < my_j1; ++j) {
+                const int32_t e = j - blk_j0;
+                scs += e < kEntCap ? ent[e * NX + n] : xval(n, M.col[j]) * M.delta[j];
+            }
+            v += scs;
+        }
+        const int64_t row = lo + my_rl;
+        store_y(M.y, n * out + row, y_dtype, v + (M.bias ? M.bias[row] : 0.f));
     }
 }
 
 // ---------------------------------------------------------------------------
-// Host side: validation, launch-shape heuristic, dispatch.
+// Host side: validation, launch-shape choice, dispatch.
 // ---------------------------------------------------------------------------
-struct GemvShape {
-    int R;
-    int S;
-    int waves;
-};
+constexpr int kWaves = 8;  // waves per block (512 threads; two blocks share a CU)
+constexpr int kNrep = 64;  // codebook replicas in LDS (one per lane)
 
 // Launch-shape overrides for tuning sweeps, read once per process:
-// HXQ_GEMV_R (rows per wave), HXQ_GEMV_S (K slices), HXQ_GEMV_BPC (blocks
-// per CU), HXQ_GEMV_NREP (codebook replicas in LDS: 1, 32 or 64).
+// HXQ_GEMV_S (K slices), HXQ_GEMV_BPC (blocks per CU).
 struct GemvTuning {
-    int r, s, bpc, nrep;
+    int s, bpc;
 };
 
 static int env_int(const char *name, int dflt) {
@@ -299,85 +456,104 @@ static int env_int(const char *name, int dflt) {
 }
 
 static const GemvTuning &tuning() {
-    static const GemvTuning t{env_int("HXQ_GEMV_R", 0), env_int("HXQ_GEMV_S", 0),
-                              env_int("HXQ_GEMV_BPC", 2), env_int("HXQ_GEMV_NREP", 64)};
+    static const GemvTuning t{env_int("HXQ_GEMV_S", 0), env_int("HXQ_GEMV_BPC", 2)};
     return t;
 }
 
-static int64_t count_tiles(const GemvParams &p, int rpb) {
-    int64_t tiles = 0;
-    for (int m = 0; m < p.n_mats; ++m) tiles += (p.m[m].out + rpb - 1) / rpb;
-    return tiles;
-}
+struct GemvPlan {
+    int CPS;
+    int grid;
+};
 
-// Pick rows-per-wave R and K-slices S so that there are at least two tiles
-// per CU (persistent blocks stay busy), preferring many rows per wave (more
-// loads in flight, x reused from registers) and few slices (less reduction).
-static GemvShape pick_shape(const GemvParams &p) {
-    const int cus = device_cu_count();
-    const int waves = p.n_x == 1 ? kMaxWaves : kMaxWaves / 2;
-    if (tuning().r > 0 && tuning().s > 0) return {tuning().r, tuning().s, waves};
-    const int max_r = p.n_x == 1 ? 4 : (p.n_x == 2 ? 2 : 1);
-    for (int R = max_r; R >= 1; R /= 2) {
-        for (int S = 1; S <= waves && S <= p.nchunks; S *= 2) {
-            if (count_tiles(p, (waves / S) * R) >= 2 * (int64_t)cus) return {R, S, waves};
-        }
+// Chunks per slice, K slices, and the block partition over matrices.
+static int plan_gemv(GemvHeader &h, const GemvMats &mats, int n_x, GemvPlan &pl) {
+    pl.CPS = 1;
+    if (n_x == 1) {
+        while (pl.CPS < 4 && pl.CPS * kWaves < h.nchunks) pl.CPS *= 2;
     }
+    int64_t total = 0;
+    for (int m = 0; m < h.n_mats; ++m) total += mats.m[m].out;
+    const int cus = device_cu_count();
+    const int64_t target = (int64_t)cus * std::max(1, tuning().bpc);
+    // blocks per matrix proportional to its rows; at most 512/n_x rows a block
+    const int64_t max_rows = (kWaves * kWave) / n_x;
+    int64_t grid = 0;
+    int64_t rows_pb = 1;
+    for (int m = 0; m < h.n_mats; ++m) {
+        const int64_t out = mats.m[m].out;
+        int64_t nb = std::max<int64_t>(1, (target * out + total - 1) / total);
+        nb = std::max<int64_t>(nb, (out + max_rows - 1) / max_rows);
+        nb = std::min<int64_t>(nb, out);
+        grid += nb;
+        HXQ_REQUIRE(grid < (int64_t{1} << 30), "too many GEMV blocks");
+        h.bb[m] = static_cast<int32_t>(grid);
+        rows_pb = std::max<int64_t>(rows_pb, (out + nb - 1) / nb);
+    }
+    for (int m = h.n_mats; m < HXQ_MAX_MULTI; ++m) h.bb[m] = INT32_MAX;
+    pl.grid = static_cast<int>(grid);
     int S = 1;
-    while (S * 2 <= waves && S * 2 <= p.nchunks) S *= 2;
-    return {1, S, waves};
+    while (S * pl.CPS < h.nchunks) S *= 2;
+    // few rows per block: split K further so more waves have rows
+    while (S < kWaves && S < h.nchunks && rows_pb < (int64_t)(kWaves / S)) S *= 2;
+    if (tuning().s > 0) S = tuning().s;
+    HXQ_REQUIRE(S >= 1 && S <= kWaves && (kWaves % S) == 0,
+                "K slices must be a power of two up to the wave count");
+    HXQ_REQUIRE((int64_t)S * pl.CPS >= h.nchunks,
+                n_x == 1 ? "in_features above 32768 is not supported by the GEMV"
+                         : "in_features above 8192 is not supported for 2-4 activation rows");
+    h.S = S;
+    h.red_rows = static_cast<int32_t>(rows_pb);
+    return HXQ_OK;
 }
 
-template <int NREP, int R, int NX, int WAVES>
-static int launch_one(const GemvParams &p, int grid, hipStream_t stream) {
-    const size_t lds = (256 * NREP + WAVES * R * NX) * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<NREP, R, NX, WAVES>), dim3(grid), dim3(WAVES * kWave), lds,
-                       stream, p);
+static size_t gemv_lds_bytes(int nrep, int nx, const GemvHeader &h) {
+    return (256 * (size_t)nrep + (h.xlds ? (size_t)nx * h.K : 0) +
+            (size_t)h.red_rows * nx * h.S + (size_t)kEntCap * nx) * sizeof(float);
+}
+
+template <int NREP, int NX, int CPS, int RB>
+static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipStream_t stream) {
+    const size_t lds = gemv_lds_bytes(NREP, NX, h);
+    const bool aff = mats.m[0].gs != nullptr;
+    const dim3 g(grid), b(kWaves * kWave);
+    const int32_t flags = h.y_dtype | (h.xlds << 4);
+    const int32_t K = static_cast<int32_t>(h.K);
+    // all matrices of one launch either carry the affine factors or none do
+#define HXQ_GEMV_LAUNCH(AFF, XT)                                                               \
+    hipLaunchKernelGGL((gemv_kernel<NREP, NX, CPS, kWaves, AFF, RB, XT>), g, b, lds, stream,   \
+                       h.x, K, h.group, h.S, h.nchunks, flags, h.red_rows, h.bb[0], h.bb[1],   \
+                       h.bb[2], h.bb[3], h.bb[4], h.bb[5], h.bb[6], mats)
+    switch (h.x_dtype) {
+        case HXQ_F32: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32); break;
+        case HXQ_BF16: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_BF16); else HXQ_GEMV_LAUNCH(false, HXQ_BF16); break;
+        default: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F16); else HXQ_GEMV_LAUNCH(false, HXQ_F16); break;
+    }
+#undef HXQ_GEMV_LAUNCH
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }
 
-template <int NREP>
-static int launch_nx1(const GemvParams &p, int R, int grid, hipStream_t stream) {
-    switch (R) {
-        case 4: return launch_one<NREP, 4, 1, kMaxWaves>(p, grid, stream);
-        case 2: return launch_one<NREP, 2, 1, kMaxWaves>(p, grid, stream);
-        default: return launch_one<NREP, 1, 1, kMaxWaves>(p, grid, stream);
-    }
-}
-
-static int gemv_run(GemvParams &p, hipStream_t stream) {
-    const GemvShape sh = pick_shape(p);
-    const int max_r = p.n_x == 1 ? 4 : (p.n_x == 2 ? 2 : 1);
-    HXQ_REQUIRE(sh.R >= 1 && sh.R <= max_r && (sh.R & (sh.R - 1)) == 0,
-                "rows per wave must be 1, 2 or 4 (at most 2 for n_rows 2, 1 above)");
-    HXQ_REQUIRE(sh.S >= 1 && sh.S <= sh.waves && (sh.waves % sh.S) == 0,
-                "K slices must divide the wave count");
-    p.S = sh.S;
-    const int rpb = (sh.waves / sh.S) * sh.R;
-    int64_t tiles = 0;
-    for (int m = 0; m < p.n_mats; ++m) {
-        p.m[m].tile_begin = static_cast<int32_t>(tiles);
-        tiles += (p.m[m].out + rpb - 1) / rpb;
-    }
-    HXQ_REQUIRE(tiles < (1LL << 30), "too many rows");
-    p.n_tiles = static_cast<int32_t>(tiles);
-    const int bpc = std::max(1, tuning().bpc);
-    const int grid = static_cast<int>(std::min<int64_t>(tiles, (int64_t)device_cu_count() * bpc));
-    if (p.n_x == 1) {
-        switch (tuning().nrep) {
-            case 1: return launch_nx1<1>(p, sh.R, grid, stream);
-            case 32: return launch_nx1<32>(p, sh.R, grid, stream);
-            default: return launch_nx1<64>(p, sh.R, grid, stream);
+static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t stream) {
+    GemvPlan pl{};
+    const int rc = plan_gemv(h, mats, n_x, pl);
+    if (rc != HXQ_OK) return rc;
+    // stage activations in LDS (sidecar gather) when two blocks still fit a CU
+    constexpr size_t kLdsBudget = 80 * 1024;
+    h.xlds = 1;
+    if (gemv_lds_bytes(kNrep, n_x, h) > kLdsBudget) h.xlds = 0;
+    HXQ_REQUIRE(gemv_lds_bytes(kNrep, n_x, h) <= 160 * 1024, "GEMV LDS budget exceeded");
+    // rows per batch (two batches in flight): what fits 128 VGPRs
+    if (n_x == 1) {
+        switch (pl.CPS) {
+            case 1: return launch_one<kNrep, 1, 1, 4>(h, mats, pl.grid, stream);
+            case 2: return launch_one<kNrep, 1, 2, 2>(h, mats, pl.grid, stream);
+            default: return launch_one<kNrep, 1, 4, 1>(h, mats, pl.grid, stream);
         }
     }
-    constexpr int W2 = kMaxWaves / 2;
-    switch (p.n_x) {
-        case 2:
-            return sh.R == 2 ? launch_one<64, 2, 2, W2>(p, grid, stream)
-                             : launch_one<64, 1, 2, W2>(p, grid, stream);
-        case 3: return launch_one<64, 1, 3, W2>(p, grid, stream);
-        default: return launch_one<64, 1, 4, W2>(p, grid, stream);
+    switch (n_x) {
+        case 2: return launch_one<kNrep, 2, 1, 2>(h, mats, pl.grid, stream);
+        case 3: return launch_one<kNrep, 3, 1, 1>(h, mats, pl.grid, stream);
+        default: return launch_one<kNrep, 4, 1, 1>(h, mats, pl.grid, stream);
     }
 }
 
@@ -387,6 +563,8 @@ static int check_mat(const hxq_matrix &m, int64_t K, int32_t group) {
     HXQ_REQUIRE(m.indices && m.codebook && m.y, "indices, codebook and y are required");
     HXQ_REQUIRE(aligned16(m.indices), "indices must be 16-byte aligned");
     HXQ_REQUIRE(m.out_features > 0, "out_features must be positive");
+    HXQ_REQUIRE(m.out_features * K + kChunk < (int64_t{1} << 32),
+                "index matrix must be smaller than 4 GiB (32-bit buffer offsets)");
     const bool affine = m.group_scale || m.group_offset;
     HXQ_REQUIRE(!affine || (m.group_scale && m.group_offset),
                 "group_scale and group_offset must be given together");
@@ -400,33 +578,36 @@ static int check_mat(const hxq_matrix &m, int64_t K, int32_t group) {
 
 using namespace hxq;
 
-extern "C" int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats,
+extern "C" int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats_in,
                               int32_t n_mats, int32_t group_size, int32_t y_dtype,
                               int64_t in_features, hipStream_t stream) {
     clear_error();
-    HXQ_REQUIRE(x && mats, "x and mats are required");
+    HXQ_REQUIRE(x && mats_in, "x and mats are required");
     HXQ_REQUIRE(n_mats >= 1 && n_mats <= HXQ_MAX_MULTI, "n_mats must be in [1, HXQ_MAX_MULTI]");
     HXQ_REQUIRE(x_dtype >= HXQ_F32 && x_dtype <= HXQ_F16, "bad x_dtype");
     HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
     HXQ_REQUIRE(in_features > 0 && in_features % 16 == 0, "in_features must be a positive multiple of 16");
     HXQ_REQUIRE(aligned16(x), "x must be 16-byte aligned");
-    GemvParams p{};
-    p.x = x;
-    p.K = in_features;
-    p.group = group_size;
-    p.n_mats = n_mats;
-    p.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
-    p.x_dtype = x_dtype;
-    p.y_dtype = y_dtype;
-    p.n_x = 1;
+    HXQ_REQUIRE(in_features <= INT32_MAX / 4, "in_features too large");
+    GemvHeader h{};
+    h.x = x;
+    h.K = in_features;
+    h.group = group_size;
+    h.n_mats = n_mats;
+    h.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
+    h.x_dtype = x_dtype;
+    h.y_dtype = y_dtype;
+    GemvMats mats{};
     for (int i = 0; i < n_mats; ++i) {
-        const int rc = check_mat(mats[i], in_features, group_size);
+        const int rc = check_mat(mats_in[i], in_features, group_size);
         if (rc != HXQ_OK) return rc;
-        const hxq_matrix &m = mats[i];
-        p.m[i] = GemvMat{m.indices, m.codebook, m.group_scale, m.group_offset, m.sc_row_ptr,
-                         m.sc_col, m.sc_delta, m.bias, m.y, m.out_features, 0, 0};
+        HXQ_REQUIRE((mats_in[i].group_scale != nullptr) == (mats_in[0].group_scale != nullptr),
+                    "all matrices of one launch must agree on having the group affine");
+        const hxq_matrix &m = mats_in[i];
+        mats.m[i] = GemvMat{m.indices, m.codebook, m.group_scale, m.group_offset, m.sc_row_ptr,
+                            m.sc_col, m.sc_delta, m.bias, m.y, m.out_features};
     }
-    return gemv_run(p, stream);
+    return gemv_run(h, mats, 1, stream);
 }
 
 extern "C" int hxq_gemv(const void *x, int32_t x_dtype, const uint8_t *indices,
@@ -447,16 +628,17 @@ extern "C" int hxq_gemv(const void *x, int32_t x_dtype, const uint8_t *indices,
                  bias, y, out_features};
     const int rc = check_mat(m, in_features, group_size);
     if (rc != HXQ_OK) return rc;
-    GemvParams p{};
-    p.x = x;
-    p.K = in_features;
-    p.group = group_size;
-    p.n_mats = 1;
-    p.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
-    p.x_dtype = x_dtype;
-    p.y_dtype = y_dtype;
-    p.n_x = static_cast<int32_t>(n_rows);
-    p.m[0] = GemvMat{indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col,
-                     sc_delta, bias, y, out_features, 0, 0};
-    return gemv_run(p, stream);
+    HXQ_REQUIRE(in_features <= INT32_MAX / 4, "in_features too large");
+    GemvHeader h{};
+    h.x = x;
+    h.K = in_features;
+    h.group = group_size;
+    h.n_mats = 1;
+    h.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
+    h.x_dtype = x_dtype;
+    h.y_dtype = y_dtype;
+    GemvMats mats{};
+    mats.m[0] = GemvMat{indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col,
+                        sc_delta, bias, y, out_features};
+    return gemv_run(h, mats, static_cast<int>(n_rows), stream);
 }

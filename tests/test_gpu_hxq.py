@@ -72,16 +72,17 @@ def test_dequant_row_blocks_and_duplicates(dev):
 
 # ---------------------------------------------------------------------- GEMV
 
-@pytest.mark.parametrize("out_f,in_f", [
-    (2048, 2048),     # config 0 / q, o
-    (256, 2048),      # k, v
-    (11008, 2048),    # gate, up
-    (2048, 11008),    # down
-    (512, 3584),      # Qwen2.5-7B kv
-    (96, 16),
+@pytest.mark.parametrize("out_f,in_f,group", [
+    (2048, 2048, 128),     # config 0 / q, o
+    (256, 2048, 128),      # k, v
+    (11008, 2048, 128),    # gate, up
+    (2048, 11008, 128),    # down
+    (512, 3584, 128),      # Qwen2.5-7B kv
+    (256, 18944, 128),     # Qwen2.5-7B down row length (4 chunks per K slice)
+    (96, 16, 16),          # smallest K
 ])
-def test_gemv_f32_matches_oracle(dev, out_f, in_f):
-    L, T = _layer(out_f, in_f, seed=out_f * 3 + in_f)
+def test_gemv_f32_matches_oracle(dev, out_f, in_f, group):
+    L, T = _layer(out_f, in_f, seed=out_f * 3 + in_f, group_size=group)
     m = _module(T, dev)
     x = torch.randn(1, in_f, generator=torch.Generator().manual_seed(1))
     y = m(x.to(dev))
