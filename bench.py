@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--prefill", type=int, default=1,
+                    help="also time the config-2 prefill GEMMs (Qwen2.5-7B shapes, M=2048)")
     return ap.parse_args()
 
 
@@ -222,9 +224,59 @@ def main():
             "traffic": None,
         },
     }
+    if args.prefill:
+        del graph
+        result["prefill_config2"] = prefill_bench(dev)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def prefill_bench(dev, m_tokens=2048, iters=10):
+    """Config 2: HXQ prefill GEMM (dequant into LDS + bf16 MFMA) at Qwen2.5-7B
+    shapes, M tokens of bf16 activations.  Also times torch.matmul (vendor BLAS)
+    on the same weights pre-dequantised to dense bf16, as a reference point."""
+    import torch
+    from helix_substrate import synth
+    from helix_substrate.helix_linear import HelixLinear
+
+    shapes = {"q": (3584, 3584), "kv": (512, 3584), "gate_up": (18944, 3584),
+              "down": (3584, 18944)}
+    out = {"m_tokens": m_tokens, "peak_tflops_bf16": 2500.0}
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    for k, (name, (o, i)) in enumerate(shapes.items()):
+        L = synth.make_layer_torch(o, i, seed=5000 + k, sigma=0.015, device=dev)
+        m = HelixLinear(i, o, L["codebook"], L["indices"], L["sidecar_positions"],
+                        L["sidecar_values"], group_scale=L["group_scale"],
+                        group_offset=L["group_offset"], group_size=128)
+        x = torch.randn(m_tokens, i, device=dev).to(torch.bfloat16)
+        for _ in range(2):
+            y = m(x)
+        torch.cuda.synchronize(dev)
+        ev0.record()
+        for _ in range(iters):
+            y = m(x)
+        ev1.record()
+        torch.cuda.synchronize(dev)
+        ms = ev0.elapsed_time(ev1) / iters
+        flops = 2.0 * m_tokens * o * i
+        wd = m.decode_weight().to(torch.bfloat16)
+        for _ in range(2):
+            yd = torch.matmul(x, wd.t())
+        torch.cuda.synchronize(dev)
+        ev0.record()
+        for _ in range(iters):
+            yd = torch.matmul(x, wd.t())
+        ev1.record()
+        torch.cuda.synchronize(dev)
+        ms_d = ev0.elapsed_time(ev1) / iters
+        out[name] = {"shape": [o, i], "ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
+                     "frac_of_bf16_peak": round(flops / ms / 1e9 / 2500.0, 4),
+                     "dense_bf16_blas_ms": round(ms_d, 4),
+                     "dense_bf16_blas_tflops": round(flops / ms_d / 1e9, 1)}
+        del m, L, x, y, wd, yd
+    return out
 
 
 def cpu_baseline(mods, seconds):

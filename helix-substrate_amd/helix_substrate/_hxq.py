@@ -42,6 +42,7 @@ SIGNATURES = {
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
     "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemv_multi": [P, I32, P, I32, I32, I32, I64, P],
+    "hxq_gemm": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
 }
 
 
@@ -173,3 +174,22 @@ def gemv_multi(x, mats, group_size, out_dtype=torch.float32, outs=None):
                               int(group_size), dtype_code(outs[0].dtype), in_f, _stream(x))
     _check("hxq_gemv_multi", rc)
     return outs
+
+
+def gemm(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr, sc_col,
+         sc_val, bias=None, out_dtype=None, out=None):
+    """Y = X @ W^T (+bias) on MFMA; X bf16/fp16 [M, K]; W rounded to X's dtype."""
+    m, in_f = x.shape
+    out_f = indices.shape[0]
+    if indices.shape[1] != in_f:
+        raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
+    if out is None:
+        out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
+    _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val,
+                 bias, out)
+    rc = lib().hxq_gemm(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
+                        _ptr(group_scale), _ptr(group_offset), int(group_size), _ptr(sc_row_ptr),
+                        _ptr(sc_col), _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype),
+                        m, out_f, in_f, _stream(x))
+    _check("hxq_gemm", rc)
+    return out

@@ -9,9 +9,11 @@ reference module (``helix_substrate/helix_linear.py:81-239`` constructor,
 ``load_cdna_factors`` / HF-quantizer style loading keep working.
 
 Differences, by design:
-  * device forward is always the fused HIP path (decode GEMV for <= 4 rows,
-    dequant-into-LDS MFMA GEMM above); the reference's "buffered" / "fused"
-    modes both map onto it and there is no silent fallback;
+  * device forward is always the fused HIP path: decode GEMV for <= 4 rows,
+    dequant-into-LDS MFMA GEMM above for bf16/fp16 activations (fp32
+    activations stay in fp32 arithmetic via the GEMV); the reference's
+    "buffered" / "fused" modes both map onto it and there is no silent
+    fallback;
   * optional per-group affine (``group_scale`` / ``group_offset`` fp32
     [out, in/group_size]): W = fl(fl(cb[idx]*s) + off);
   * the sidecar *replaces* reconstructed values (``CDNAv3Reader`` semantics,
@@ -173,6 +175,8 @@ class HelixLinear(nn.Module):
             for name in ("_sc_row_ptr", "_sc_col", "_sc_val", "_sc_delta", "_sidecar_rows",
                          "_sidecar_cols", "_sidecar_deltas", "_sidecar_vq_vals"):
                 self.register_buffer(name, None)
+        # the MFMA GEMM steps K by 64 and reads one affine group per step
+        self._gemm_ok = self.in_features % 64 == 0 and (not has_affine or self.group_size % 64 == 0)
         self.has_svd = self.svd_U is not None
         self.rank = int(self.svd_U.shape[1]) if self.has_svd else 0
         self.has_channel_scales = self.channel_scales is not None
@@ -245,7 +249,13 @@ class HelixLinear(nn.Module):
             self._last_dispatch_path = "hip_gemv"
             _hxq.gemv(x2, self.indices, self.codebook, self.group_scale, self.group_offset,
                       self.group_size, rp, col, delta, self.bias, out=out)
+        elif x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
+            self._last_dispatch_path = "hip_gemm"
+            _hxq.gemm(x2, self.indices, self.codebook, self.group_scale, self.group_offset,
+                      self.group_size, rp, col, None if rp is None else self._sc_val,
+                      self.bias, out=out)
         else:
+            # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
             self._last_dispatch_path = "hip_gemv_rows"
             for r0 in range(0, n, _GEMV_MAX_ROWS):
                 r1 = min(n, r0 + _GEMV_MAX_ROWS)

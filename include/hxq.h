@@ -117,6 +117,25 @@ int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats,
                    int32_t n_mats, int32_t group_size, int32_t y_dtype,
                    int64_t in_features, hipStream_t stream);
 
+/*
+ * Prefill GEMM: Y[m, :] = X[m, :] @ W^T (+ bias), X bf16 or fp16 [m_rows,
+ * in_features], W dequantised tile by tile into LDS (sidecar values replace
+ * their elements, then W is rounded to X's 16-bit type) and multiplied with
+ * MFMA, fp32 accumulation; Y in y_dtype [m_rows, out_features].
+ * Replaces: fused_vq_matmul with N > 1 -> _vq_gather_matmul_tiled_kernel +
+ *   scatter_add sidecar + bias (helix_substrate/triton_vq_matmul.py:634-661,
+ *   693-698, 724-725) and HelixLinear._forward_buffered (helix_linear.py:556-634).
+ * Requires in_features % 64 == 0 and, with affine, group_size % 64 == 0.
+ * sc_val are the replacement values (as for hxq_dequant_f32).
+ */
+int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
+             const float *codebook, const float *group_scale,
+             const float *group_offset, int32_t group_size,
+             const int32_t *sc_row_ptr, const int32_t *sc_col,
+             const float *sc_val, const float *bias, void *y, int32_t y_dtype,
+             int64_t m_rows, int64_t out_features, int64_t in_features,
+             hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,129 @@
+"""GPU parity of the MFMA prefill GEMM against the CPU oracle.
+
+Two bars per case:
+  * the BASELINE bar: max|Y - Y_ref| / max|Y_ref| <= 2e-2 with Y_ref the fp64
+    contraction of the 16-bit activations with the exact fp32 W;
+  * a tight bar pinning layout, sidecar and affine handling: against W
+    rounded to the activation's 16-bit type (what the kernel multiplies),
+    the only error left is fp32 accumulation plus rare one-ulp rounding
+    flips of single weights (fma vs two roundings), so <= 2e-4.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helix_substrate import _hxq, synth
+from helix_substrate.helix_linear import HelixLinear
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(out_f, in_f, seed, **kw):
+    L = synth.make_layer_np(out_f, in_f, seed=seed, **kw)
+    return L, synth.to_torch(L)
+
+
+def _module(T, dev, bias=None):
+    out_f, in_f = T["indices"].shape
+    return HelixLinear(in_f, out_f, T["codebook"], T["indices"], T["sidecar_positions"],
+                       T["sidecar_values"], bias=bias, group_scale=T["group_scale"],
+                       group_offset=T["group_offset"], group_size=T["group_size"]).to(dev)
+
+
+def _oracle_w(L):
+    return oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
+                              L["group_size"], L["sidecar_positions"], L["sidecar_values"])
+
+
+def _maxrel(y, y_ref):
+    return float(np.abs(np.asarray(y, np.float64) - y_ref).max() / np.abs(y_ref).max())
+
+
+def _check(y, x16, W, bias=None):
+    """BASELINE bar for any output dtype; the tight bar for fp32 outputs (a
+    16-bit output adds its own rounding of ~2^-9)."""
+    xf = x16.float().numpy()
+    b = None if bias is None else bias.numpy()
+    is32 = y.dtype == torch.float32
+    y = y.float().cpu().numpy()
+    ref = oracle.linear_np(xf, W, b)
+    assert _maxrel(y, ref) <= 2e-2
+    if is32:
+        W16 = torch.from_numpy(W).to(x16.dtype).float().numpy()
+        rel = _maxrel(y, oracle.linear_np(xf, W16, b))
+        assert rel <= 2e-4, rel
+
+
+def _gemm32(mod, x):
+    return _hxq.gemm(x, mod.indices, mod.codebook, mod.group_scale, mod.group_offset,
+                     mod.group_size, mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias,
+                     out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("m,out_f,in_f", [
+    (5, 128, 128),        # smallest tile, ragged M
+    (64, 256, 512),
+    (300, 640, 1536),     # ragged M and OUT tiles
+    (512, 512, 3584),     # Qwen2.5-7B kv shape
+    (1024, 384, 2048),    # 256-row tiles
+])
+def test_gemm_bf16_matches_oracle(dev, m, out_f, in_f):
+    L, T = _layer(out_f, in_f, seed=m + out_f, sigma=0.015)
+    mod = _module(T, dev)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    y = mod(x.to(dev))
+    assert mod._last_dispatch_path == "hip_gemm"
+    assert y.dtype == torch.bfloat16
+    W = _oracle_w(L)
+    _check(y, x, W)
+    _check(_gemm32(mod, x.to(dev)), x, W)
+
+
+def test_gemm_fp32_output_bias_and_fp16(dev):
+    L, T = _layer(384, 1024, seed=3)
+    bias = torch.linspace(-1, 1, 384)
+    mod = _module(T, dev, bias=bias)
+    W = _oracle_w(L)
+    x = torch.randn(200, 1024, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    y = _hxq.gemm(x.to(dev), mod.indices, mod.codebook, mod.group_scale, mod.group_offset, 128,
+                  mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias, out_dtype=torch.float32)
+    assert y.dtype == torch.float32
+    _check(y, x, W, bias)
+    xh = torch.randn(70, 1024, generator=torch.Generator().manual_seed(2)).to(torch.float16)
+    yh = mod(xh.to(dev))
+    assert yh.dtype == torch.float16 and mod._last_dispatch_path == "hip_gemm"
+    _check(yh, xh, W, bias)
+    _check(_gemm32(mod, xh.to(dev)), xh, W, bias)
+
+
+def test_gemm_without_affine_or_sidecar(dev):
+    for kw in ({"affine": False}, {"sidecar": False}):
+        L, T = _layer(256, 512, seed=9, **kw)
+        mod = _module(T, dev)
+        x = torch.randn(96, 512, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+        _check(_gemm32(mod, x.to(dev)), x, _oracle_w(L))
+
+
+def test_gemm_dense_sidecar_rows(dev):
+    # many entries per row and per K-step exercise the replacement cursors
+    L, T = _layer(128, 512, seed=12, density=0.05)
+    mod = _module(T, dev)
+    x = torch.randn(40, 512, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    _check(_gemm32(mod, x.to(dev)), x, _oracle_w(L))
+
+
+def test_gemm_deterministic(dev):
+    L, T = _layer(512, 1024, seed=13)
+    mod = _module(T, dev)
+    x = torch.randn(300, 1024, device=dev).to(torch.bfloat16)
+    assert torch.equal(mod(x), mod(x))
+
+
+def test_fp32_prefill_stays_fp32(dev):
+    L, T = _layer(256, 512, seed=14)
+    mod = _module(T, dev)
+    x = torch.randn(9, 512, generator=torch.Generator().manual_seed(7))
+    y = mod(x.to(dev))
+    assert mod._last_dispatch_path == "hip_gemv_rows"
+    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= 1e-5
