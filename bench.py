@@ -43,6 +43,8 @@ def parse():
                     help="target CPU time of the cpu_baseline sample (0 = skip)")
     ap.add_argument("--prefill", type=int, default=1,
                     help="also time the config-2 prefill GEMMs (Qwen2.5-7B shapes, M=2048)")
+    ap.add_argument("--scan", type=int, default=1,
+                    help="also time the config-3 Mamba2 selective scan")
     return ap.parse_args()
 
 
@@ -227,6 +229,8 @@ def main():
     if args.prefill:
         del graph
         result["prefill_config2"] = prefill_bench(dev)
+    if args.scan:
+        result["scan_config3"] = scan_bench(dev, cpu=args.cpu_seconds > 0)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -276,6 +280,64 @@ def prefill_bench(dev, m_tokens=2048, iters=10):
                      "dense_bf16_blas_ms": round(ms_d, 4),
                      "dense_bf16_blas_tflops": round(flops / ms_d / 1e9, 1)}
         del m, L, x, y, wd, yd
+    return out
+
+
+def scan_bench(dev, iters=5, cpu=True):
+    """Config 3: Mamba2-1.3B-shaped selective scan, b=8, L=2048, H=64, P=64,
+    N=128, G=1, chunk 256; bf16 x/B/C, fp32 dt/A/D and state, fp32 y."""
+    import math
+
+    import torch
+    from helix_substrate import mamba_scan_chunked as msc
+
+    b, L, H, P, N = 8, 2048, 64, 64, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(b, L, H, P, device=dev, generator=g).to(torch.bfloat16)
+    dt = torch.nn.functional.softplus(torch.randn(b, L, H, device=dev, generator=g) * 0.5 - 2.0)
+    A = -torch.exp(torch.rand(H, device=dev, generator=g) * math.log(16.0))
+    Bm = (torch.randn(b, L, 1, N, device=dev, generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    Cm = (torch.randn(b, L, 1, N, device=dev, generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    D = torch.rand(H, device=dev, generator=g) + 0.5
+    for _ in range(2):
+        y, hf = msc.chunked_scan(None, dt, A, x, Bm, Cm, D, chunk_size=256)
+    torch.cuda.synchronize(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(iters):
+        y, hf = msc.chunked_scan(None, dt, A, x, Bm, Cm, D, chunk_size=256)
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    ms = ev0.elapsed_time(ev1) / iters
+    states = b * L * H * P * N
+    flops = 5.0 * states  # recurrence form: h = a*h + (dt x) B (3), y += h C (2)
+    nbytes = (x.numel() * 2 + dt.numel() * 4 + Bm.numel() * 2 + Cm.numel() * 2 + y.numel() * 4
+              + hf.numel() * 4 + 2 * H * 4)
+    out = {"shape": {"batch": b, "seqlen": L, "heads": H, "head_dim": P, "state": N,
+                     "ngroups": 1, "chunk": 256},
+           "ms": round(ms, 4), "gflop_recurrence": round(flops / 1e9, 2),
+           "tflops": round(flops / ms / 1e9, 2),
+           "frac_of_fp32_peak_157": round(flops / ms / 1e9 / 157.3, 4),
+           "gbs": round(nbytes / ms / 1e6, 1), "bytes": nbytes,
+           "frac_of_hbm_peak": round(nbytes / ms / 1e6 / 8000.0, 4)}
+    if cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import cpu_path
+
+        Ls = 32
+        xc = x[:, :Ls].float().cpu()
+        dtc = dt[:, :Ls].cpu()
+        Bc = Bm[:, :Ls].float().cpu().expand(b, Ls, H, N).contiguous()
+        Cc = Cm[:, :Ls].float().cpu().expand(b, Ls, H, N).contiguous()
+        h0 = torch.zeros(b, H, P, N)
+        t0 = time.perf_counter()
+        cpu_path.sequential_scan(h0, dtc, A.cpu(), xc, Bc, Cc, D.cpu()[:, None])
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"ms_extrapolated_to_L2048": round(el * 1e3 * L / Ls, 1),
+                               "sample": f"reference sequential_scan restated (torch CPU), "
+                                         f"L={Ls} of 2048, {torch.get_num_threads()} threads",
+                               "kind": "port", "cores": torch.get_num_threads()}
     return out
 
 

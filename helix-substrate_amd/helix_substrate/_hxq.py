@@ -43,6 +43,16 @@ SIGNATURES = {
     "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemv_multi": [P, I32, P, I32, I32, I32, I64, P],
     "hxq_gemm": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
+                           I64, I64, I64, P, I64, P],
+    "hxq_ssm_decode_step": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64,
+                            P],
+}
+
+
+# name -> argtypes for entry points returning int64_t (sizes)
+SIGNATURES_I64 = {
+    "hxq_ssm_scan_workspace_bytes": [I64] * 6,
 }
 
 
@@ -69,6 +79,10 @@ def lib():
         L.hxq_last_error.restype = ctypes.c_char_p
         L.hxq_abi_version.argtypes = []
         L.hxq_abi_version.restype = ctypes.c_int
+        for name, argtypes in SIGNATURES_I64.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = I64
         _lib = L
     return _lib
 
@@ -193,3 +207,48 @@ def gemm(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr
                         m, out_f, in_f, _stream(x))
     _check("hxq_gemm", rc)
     return out
+
+
+def ssm_chunk_scan(x, dt, A, B, C, D=None, h0=None, chunk=256, out_dtype=torch.float32,
+                   want_final=True):
+    """Selective scan on the GPU.  x [b, L, H, P], dt [b, L, H], A [H], B/C [b, L, G, N],
+    D [H] (or [H, 1]), h0 [b, H, P, N] fp32 or None.  Returns (y, h_final)."""
+    batch, seqlen, heads, head_dim = x.shape
+    ngroups, state = B.shape[2], B.shape[3]
+    A = A.float().contiguous()
+    D = None if D is None else D.float().reshape(-1).contiguous()
+    h0 = None if h0 is None else h0.float().contiguous()
+    y = torch.empty(batch, seqlen, heads, head_dim, dtype=out_dtype, device=x.device)
+    hf = torch.empty(batch, heads, head_dim, state, dtype=torch.float32, device=x.device) \
+        if want_final else None
+    L = lib()
+    nbytes = L.hxq_ssm_scan_workspace_bytes(batch, seqlen, heads, head_dim, state, chunk)
+    if nbytes < 0:
+        raise RuntimeError("invalid scan sizes")
+    ws = torch.empty(int(nbytes), dtype=torch.uint8, device=x.device)
+    _need_device(x, dt, A, B, C, D, h0, y, hf, ws)
+    rc = L.hxq_ssm_chunk_scan(_ptr(x), dtype_code(x.dtype), _ptr(dt), dtype_code(dt.dtype),
+                              _ptr(A), _ptr(B), _ptr(C), dtype_code(B.dtype), _ptr(D), _ptr(h0),
+                              _ptr(y), dtype_code(y.dtype), _ptr(hf), batch, seqlen, heads,
+                              head_dim, state, ngroups, int(chunk), _ptr(ws), int(nbytes),
+                              _stream(x))
+    _check("hxq_ssm_chunk_scan", rc)
+    if B.dtype != C.dtype:
+        raise RuntimeError("B and C must share a dtype")
+    return y, hf
+
+
+def ssm_decode_step(h, x, dt, A, B, C, D=None, out_dtype=torch.float32):
+    """One token: h [b, H, P, N] fp32 updated in place; returns y [b, H, P]."""
+    batch, heads, head_dim, state = h.shape
+    ngroups = B.shape[1]
+    A = A.float().contiguous()
+    D = None if D is None else D.float().reshape(-1).contiguous()
+    y = torch.empty(batch, heads, head_dim, dtype=out_dtype, device=x.device)
+    _need_device(h, x, dt, A, B, C, D, y)
+    rc = lib().hxq_ssm_decode_step(_ptr(x), dtype_code(x.dtype), _ptr(dt), dtype_code(dt.dtype),
+                                   _ptr(A), _ptr(B), _ptr(C), dtype_code(B.dtype), _ptr(D), _ptr(h),
+                                   _ptr(y), dtype_code(y.dtype), batch, heads, head_dim, state,
+                                   ngroups, _stream(x))
+    _check("hxq_ssm_decode_step", rc)
+    return y

@@ -136,6 +136,42 @@ int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
              int64_t m_rows, int64_t out_features, int64_t in_features,
              hipStream_t stream);
 
+/*
+ * Selective scan (Mamba/Mamba2), fp32 state, chunk-parallel:
+ *   a_t = exp(A[h] dt[b,t,h]);  h_t = a_t h_{t-1} + dt[b,t,h] x[b,t,h,p] B[b,t,g,n]
+ *   y[b,t,h,p] = sum_n h_t C[b,t,g,n] + D[h] x[b,t,h,p],  g = h / (heads/ngroups)
+ * Layouts: x [batch, seqlen, heads, head_dim]; dt [batch, seqlen, heads];
+ * A, D fp32 [heads]; B, C [batch, seqlen, ngroups, state]; h0 / h_final fp32
+ * [batch, heads, head_dim, state] (h0 NULL = zeros, h_final may be NULL);
+ * y [batch, seqlen, heads, head_dim].  x/dt/B/C/y dtypes: HXQ_F32/BF16/F16.
+ * `workspace` (device, >= hxq_ssm_scan_workspace_bytes(...)) holds the chunk
+ * states; state must be 16, 32, 64, 128 or 256.
+ * Replaces: chunked_scan / sequential_scan (helix_substrate/mamba_scan_chunked.py:
+ *   42-86, 89-213) and triton_scan (triton_mamba_scan.py:373-416).
+ */
+int64_t hxq_ssm_scan_workspace_bytes(int64_t batch, int64_t seqlen, int64_t heads,
+                                     int64_t head_dim, int64_t state, int64_t chunk);
+
+int hxq_ssm_chunk_scan(const void *x, int32_t x_dtype, const void *dt, int32_t dt_dtype,
+                       const float *A, const void *B, const void *C, int32_t bc_dtype,
+                       const float *D, const float *h0, void *y, int32_t y_dtype,
+                       float *h_final, int64_t batch, int64_t seqlen, int64_t heads,
+                       int64_t head_dim, int64_t state, int64_t ngroups, int64_t chunk,
+                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * One decode step; h (fp32 [batch, heads, head_dim, state]) is updated in place.
+ * x [batch, heads, head_dim], dt [batch, heads], B/C [batch, ngroups, state],
+ * y [batch, heads, head_dim].
+ * Replaces: triton_mamba_decode_step (triton_mamba_scan.py:312-366) and the
+ *   single-token branch of chunked_scan (mamba_scan_chunked.py:150-159).
+ */
+int hxq_ssm_decode_step(const void *x, int32_t x_dtype, const void *dt, int32_t dt_dtype,
+                        const float *A, const void *B, const void *C, int32_t bc_dtype,
+                        const float *D, float *h, void *y, int32_t y_dtype, int64_t batch,
+                        int64_t heads, int64_t head_dim, int64_t state, int64_t ngroups,
+                        hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,7 +33,9 @@ def lib():
 
 def test_header_declares_entry_points():
     names = _declared_functions()
-    for n in ("hxq_last_error", "hxq_abi_version", "hxq_dequant_f32", "hxq_gemv", "hxq_gemv_multi"):
+    for n in ("hxq_last_error", "hxq_abi_version", "hxq_dequant_f32", "hxq_gemv", "hxq_gemv_multi",
+              "hxq_gemm", "hxq_ssm_chunk_scan", "hxq_ssm_decode_step",
+              "hxq_ssm_scan_workspace_bytes"):
         assert n in names
 
 
@@ -52,7 +54,8 @@ def test_python_signatures_cover_header(lib):
     for name in _declared_functions():
         if name in ("hxq_last_error", "hxq_abi_version"):
             continue
-        assert name in _hxq.SIGNATURES, f"{name} has no ctypes signature"
+        assert name in _hxq.SIGNATURES or name in _hxq.SIGNATURES_I64, \
+            f"{name} has no ctypes signature"
 
 
 def test_rejects_bad_arguments_with_message(lib):
@@ -76,3 +79,9 @@ def test_python_wrapper_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="device tensors"):
         _hxq.gemv(torch.zeros(1, 16), torch.zeros(4, 16, dtype=torch.uint8), torch.zeros(256),
                   None, None, 128, None, None, None)
+
+
+def test_scan_workspace_query(lib):
+    n = lib.hxq_ssm_scan_workspace_bytes(8, 2048, 64, 64, 128, 256)
+    assert n >= 8 * 8 * 64 * 64 * 128 * 4
+    assert lib.hxq_ssm_scan_workspace_bytes(0, 1, 1, 1, 1, 1) == -1
