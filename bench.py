@@ -164,23 +164,29 @@ def main():
     torch.cuda.synchronize(dev)
     ms_eager = ev0.elapsed_time(ev1) / max(3, args.steps // 5)
 
-    # per-kernel durations with HIP events on the launch stream: a sleep kernel
-    # keeps the GPU busy while the host enqueues, so each event pair brackets
-    # exactly one kernel.
+    # Per-launch durations: one HIP graph per launch group holding that group's
+    # launches for every layer, replayed on the launch stream between HIP
+    # events; the average per launch is kernel time plus the graph's
+    # inter-kernel gap (a sub-microsecond bias against us).
     per_group_us = {}
-    cur = torch.cuda.current_stream(dev)
     for gname in launch_groups:
-        evs = []
-        torch.cuda._sleep(50_000_000)
-        for li in range(len(layers)):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(cur)
-            launch_layer(li, gname)
-            b.record(cur)
-            evs.append((a, b))
+        gg = torch.cuda.CUDAGraph()
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(gg, stream=s):
+                for li in range(len(layers)):
+                    launch_layer(li, gname)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        gg.replay()
         torch.cuda.synchronize(dev)
-        per_group_us[gname] = 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        reps = 5
+        ev0.record()
+        for _ in range(reps):
+            gg.replay()
+        ev1.record()
+        torch.cuda.synchronize(dev)
+        per_group_us[gname] = 1000.0 * ev0.elapsed_time(ev1) / (reps * len(layers))
+        del gg
     dom = "gateup"
     dom_gbs = group_bytes[dom] / (per_group_us[dom] * 1e-6) / 1e9
     print(f"[bench] per-launch us: {json.dumps({k: round(v, 2) for k, v in per_group_us.items()})}",
@@ -223,7 +229,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
             "bytes_per_launch": group_bytes[dom],
-            "traffic": None,
+            "traffic": read_traffic(),
         },
     }
     if args.prefill:
@@ -234,6 +240,18 @@ def main():
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def read_traffic():
+    """HBM bytes per gate+up launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size)."""
+    f = ROOT / "profiles" / "gemv_gateup_qwen3b_decode.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
 
 
 def prefill_bench(dev, m_tokens=2048, iters=10):
