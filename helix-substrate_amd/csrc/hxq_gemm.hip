@@ -1,113 +1,251 @@
 // HXQ prefill GEMM: Y[M, OUT] = X[M, K] @ W^T, W dequantised into LDS and fed
-// to bf16/fp16 MFMA (v_mfma_f32_32x32x16_{bf16,f16}) with fp32 accumulation.
+// to bf16/fp16 MFMA (v_mfma_f32_32x32x16_{bf16,f16}) with fp32 accumulation,
+// plus its grouped form for mixture-of-experts FFNs (rows of X gathered per
+// expert, one expert's HXQ matrix per row tile).
 //
 // Replaces fused_vq_matmul's N > 1 path (helix_substrate/triton_vq_matmul.py:
 // 634-661 _vq_gather_matmul_tiled_kernel, 693-698 scatter_add sidecar, 724-725
 // bias) and the default _forward_buffered materialise-then-BLAS path
 // (helix_linear.py:556-634).
 //
-// Block tile BM x BN (M x OUT) with BK = 64 per K-step, 256 threads (4 waves in
-// a 2 x 2 layout, each wave BM/2 x BN/2 = (BM/64) x (BN/64) MFMA 32x32 tiles).
-// Per K-step:
-//   * X tile [BM, 64] (16-bit) -> LDS;
-//   * index tile [BN, 64] (u8) -> codebook lookup (LDS, 16 replicas) ->
-//     fma(cb, scale, offset) -> 16-bit -> LDS; sidecar entries of the tile
-//     then REPLACE their element (each of the 2 threads of a row keeps a
-//     prefetched cursor into its row's CSR entries);
-//   * the next K-step's global loads are issued before this step's MFMAs.
-// LDS rows are padded by 16 bytes so the MFMA operand reads (16 bytes per
-// lane, 32 rows per half-wave) spread over the banks.
+// Block: 512 threads = 8 waves in a 2 (M) x 4 (N) layout; block tile BM x 256
+// (BM = 64/128/256), K-step 64.  Each wave owns a (BM/2) x 64 sub-tile, i.e.
+// (BM/64) x 2 MFMA 32x32 tiles.
+// Per K-step, double-buffered in LDS (one barrier per step):
+//   * X tile [BM, 64] (16-bit) -> LDS, rows XOR-swizzled in 16-byte chunks so
+//     the MFMA operand reads (8 lanes x 16 B per row group) hit all banks;
+//   * index tile [256, 64] (u8) -> codebook lookup (LDS, 32 replicas; 16 in
+//     pair mode) ->
+//     fma(cb, scale, offset) -> v_cvt_pk_bf16_f32 -> LDS; sidecar entries then
+//     REPLACE their element (the block's CSR entries are staged in LDS once;
+//     each of the two threads of a row walks its row's entries);
+//   * global loads run two steps ahead of the LDS writes.
 // Results are written once per output element: deterministic.
+//
+// Grouped mode (MoE): `seg` holds the expert segments [E+1] of a sorted
+// assignment list; row tile y maps to (expert, rows) by a prefix over
+// ceil(count_e / BM); X rows are gathered through `rows` (or taken in order),
+// the weight pointers step by the per-expert strides, and outputs land in
+// sorted order.  Pair mode computes gate rows (tile rows 0..127) and up rows
+// (128..255) of the same 128 features and writes silu(gate) * up.
 #include <algorithm>
+#include <type_traits>
 
 #include "hxq_common.h"
 
 namespace hxq {
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmThreads = 256;
-constexpr int kBK = 64;
-constexpr int kLdsRow = kBK + 8;   // 16-bit elements per padded LDS row
-constexpr int kCbRep = 16;         // codebook replicas (lane % 16)
+constexpr int kGemmThreads = 512;
+constexpr int kBK = 64;        // K per step
+constexpr int kBN = 256;       // tile rows of W (output features) per block
+constexpr int kScCap = 8192;   // sidecar entries staged in LDS per block
 
-struct GemmArgs {
-    const uint16_t *x;    // [M, K] bf16/fp16
-    const uint8_t *idx;   // [OUT, K]
-    const float *cb;      // [256]
-    const float *gs;      // [OUT, K/G] or null
+// One HXQ weight set.  For a bank of experts every array is the per-expert
+// arrays stacked along a leading expert axis.
+struct WSet {
+    const uint8_t *idx;   // [E, OUT, K]
+    const float *cb;      // [E, 256]
+    const float *gs;      // [E, OUT, K/G] or null
     const float *go;
-    const int32_t *rp;    // CSR [OUT+1] or null
+    const int32_t *rp;    // [E, OUT+1] absolute offsets into col/val, or null
     const int32_t *col;
     const float *val;     // replacement values
-    const float *bias;    // [OUT] or null
+};
+
+struct GemmArgs {
+    const uint16_t *x;    // [x_rows, K] bf16/fp16
+    const int32_t *rows;  // grouped: x row of each sorted assignment (null = in order)
+    const int32_t *seg;   // grouped: [E+1] segment offsets (null = dense)
+    WSet w[2];            // w[1]: up matrix of a SwiGLU pair
+    const float *bias;    // [OUT] or null (dense only)
     void *y;              // [M, OUT]
-    int32_t M, OUT, K, group, y_dtype, pad_;
+    int32_t M, OUT, K, group, y_dtype, n_experts, x_rows, pad_;
 };
 
 template <bool BF16>
-__device__ __forceinline__ uint16_t to16(float v) {
-    if constexpr (BF16) return f32_to_bf16(v);
-    else return f32_to_f16(v);
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
-// One K-step worth of global data held in registers between steps.
+template <bool BF16>
+__device__ __forceinline__ uint16_t to16(float v) {
+    return static_cast<uint16_t>(pack2<BF16>(v, 0.f) & 0xffffu);
+}
+
+// Element offset of 16-byte chunk `c` (0..7) of LDS row `r` (64 elements).
+__device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ (r & 7)) << 3); }
+
+// Global data of one K-step, held in registers until written to LDS.
 template <int BM>
 struct GemmStage {
-    u32x4 a[BM / 32];   // X: BM rows x 128 B; a pass of 256 threads x 16 B covers 32 rows
-    u32x4 q[2];         // indices: 32 bytes of one row
+    u32x4 a[BM / 64];   // X: thread t holds chunk t%8 of rows t/8 + 64p
+    u32x4 q[2];         // 32 index bytes of this thread's W row
     float s, o;         // affine factors of that row's group
 };
 
-template <int BM, int BN, bool BF16, bool AFFINE>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(const GemmArgs g) {
-    static_assert(BN == 128, "one index row per thread pair");
-    constexpr int WM = BM / 2, WN = BN / 2;          // wave tile
-    constexpr int TM = WM / 32, TN = WN / 32;        // MFMA tiles per wave
-    __shared__ __attribute__((aligned(16))) uint16_t sA[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[BN * kLdsRow];
-    __shared__ float tbl[256 * kCbRep];
+template <int BM, bool BF16, bool AFFINE, bool GROUPED, bool PAIR>
+__global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g) {
+    static_assert(!PAIR || GROUPED, "pair mode is a grouped-GEMM epilogue");
+    static_assert(!PAIR || BM <= 128, "LDS budget");
+    constexpr int WM = BM / 2;       // wave tile rows (M)
+    constexpr int TM = WM / 32;      // MFMA tiles per wave along M
+    constexpr int TN = 2;            // ... along N (64 columns per wave)
+    constexpr int NT = PAIR ? 2 : 1; // codebook tables
+    // Codebook replicas: 32 per table keep lookups bank-conflict-free (the two
+    // half-waves use the same 32 banks in different cycles); a SwiGLU pair
+    // needs two tables and keeps 16 replicas to fit the 160 KB of LDS.
+    constexpr int NREP = PAIR ? 16 : 32;
+    constexpr int kTblBytes = NT * 256 * NREP * 4;
+    constexpr int kABytes = 2 * BM * kBK * 2;
+    constexpr int kBBytes = 2 * kBN * kBK * 2;
+    // sidecar entries of the block's rows, staged once: {col u16, value u16}
+    constexpr int kScBytes = kScCap * 4;
+    static_assert(kTblBytes + kABytes + kBBytes + kScBytes <= 160 * 1024, "LDS budget");
+    // table first: its LDS offset is 0, so lookups need no base add
+    __shared__ __attribute__((aligned(16))) char smem[kTblBytes + kABytes + kBBytes + kScBytes];
+    float (*tbl)[256 * NREP] = reinterpret_cast<float (*)[256 * NREP]>(smem);
+    uint16_t (*sA)[BM * kBK] = reinterpret_cast<uint16_t (*)[BM * kBK]>(smem + kTblBytes);
+    uint16_t (*sB)[kBN * kBK] = reinterpret_cast<uint16_t (*)[kBN * kBK]>(smem + kTblBytes + kABytes);
+    uint32_t *sSc = reinterpret_cast<uint32_t *>(smem + kTblBytes + kABytes + kBBytes);
+    int *s_tile = reinterpret_cast<int *>(&sA[0][0]);  // read before sA is first written
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int wm = wave / 2, wn = wave % 2;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
+    const int wm = wave / 4, wn = wave % 4;
     const int K = g.K;
     const int nk = K / kBK;
 
-    // codebook replicas: entry j at [j*16 + r]
-    for (int e = tid; e < 256 * kCbRep; e += kGemmThreads) tbl[e] = g.cb[e / kCbRep];
-
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.M * K * 2);
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(g.idx, (int64_t)g.OUT * K);
-    const int ngroups = AFFINE ? K / g.group : 0;
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(g.gs, AFFINE ? (int64_t)g.OUT * ngroups * 4 : 0);
-    const __amdgpu_buffer_rsrc_t orr = make_rsrc(g.go, AFFINE ? (int64_t)g.OUT * ngroups * 4 : 0);
-
-    // X loads: thread t covers row (t / 8) + 32*p, 16-byte column chunk t % 8
-    const int a_row = tid / 8, a_cc = tid % 8;
-    // index loads: thread t covers row t / 2, half t % 2 (32 bytes)
-    const int b_row = tid / 2, b_half = tid % 2;
-    const int grow = n0 + b_row;  // global output row of this thread's index slice
-    const uint32_t kOob = 0x80000000u;
-
-    auto load_stage = [&](int ks, GemmStage<BM> &st) {
-        const int k0 = ks * kBK;
+    // ---- row tile -> (expert, first row, end row) --------------------------
+    int e = 0, r0, r1;
+    if constexpr (GROUPED) {
+        if (wave == 0) {
+            const int by = blockIdx.y;
+            int base = 0, fe = -1, fr0 = 0, fr1 = 0;
+            for (int e0 = 0; e0 < g.n_experts; e0 += 64) {
+                const int ee = e0 + lane;
+                int lo = 0, cnt = 0;
+                if (ee < g.n_experts) {
+                    lo = g.seg[ee];
+                    cnt = g.seg[ee + 1] - lo;
+                }
+                const int t = (cnt + BM - 1) / BM;
+                int incl = t;
 #pragma unroll
-        for (int p = 0; p < BM / 32; ++p) {
-            const int r = m0 + a_row + 32 * p;
-            const uint32_t off = r < g.M ? (uint32_t)((r * K + k0 + a_cc * 8) * 2) : kOob;
-            st.a[p] = buf_load16(xr, off);
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int v = __shfl_up(incl, d, kWave);
+                    if (lane >= d) incl += v;
+                }
+                const int excl = base + incl - t;
+                if (t > 0 && by >= excl && by < excl + t) {
+                    fe = ee;
+                    fr0 = lo + (by - excl) * BM;
+                    fr1 = min(fr0 + BM, lo + cnt);
+                }
+                base += __shfl(incl, 63, kWave);
+            }
+            // at most one lane matched
+            const unsigned long long hit = __ballot(fe >= 0);
+            if (lane == 0) s_tile[0] = -1;
+            if (hit) {
+                const int src = __builtin_ctzll(hit);
+                const int be = __shfl(fe, src, kWave), b0 = __shfl(fr0, src, kWave),
+                          b1 = __shfl(fr1, src, kWave);
+                if (lane == 0) {
+                    s_tile[0] = be;
+                    s_tile[1] = b0;
+                    s_tile[2] = b1;
+                }
+            }
         }
-        const uint32_t qoff = grow < g.OUT ? (uint32_t)(grow * K + k0 + b_half * 32) : kOob;
-        st.q[0] = buf_load16(qr, qoff);
-        st.q[1] = buf_load16(qr, qoff + 16);
+        __syncthreads();
+        e = s_tile[0];
+        if (e < 0) return;  // block-uniform: no tile for this block index
+        r0 = s_tile[1];
+        r1 = s_tile[2];
+    } else {
+        r0 = blockIdx.y * BM;
+        r1 = min(r0 + BM, g.M);
+    }
+
+    // ---- W row of this thread: b_row = tid / 2, half = tid % 2 ------------
+    const int b_row = tid >> 1, b_half = tid & 1;
+    const int part = PAIR ? (b_row >> 7) : 0;
+    const int n0 = blockIdx.x * (PAIR ? kBN / 2 : kBN);
+    const int grow = n0 + (PAIR ? (b_row & 127) : b_row);  // row of matrix `part`
+    const bool row_ok = grow < g.OUT;
+    const int ngroups = AFFINE ? K / g.group : 1;
+    // field-wise select keeps the kernel-argument struct out of scratch
+    WSet ws;
+    ws.idx = part ? g.w[1].idx : g.w[0].idx;
+    ws.gs = part ? g.w[1].gs : g.w[0].gs;
+    ws.go = part ? g.w[1].go : g.w[0].go;
+    ws.rp = part ? g.w[1].rp : g.w[0].rp;
+    ws.col = part ? g.w[1].col : g.w[0].col;
+    ws.val = part ? g.w[1].val : g.w[0].val;
+    const int64_t eo = static_cast<int64_t>(e);
+    const uint8_t *idx_e = ws.idx + eo * g.OUT * K;
+    const float *gs_e = AFFINE ? ws.gs + eo * g.OUT * ngroups : nullptr;
+    const float *go_e = AFFINE ? ws.go + eo * g.OUT * ngroups : nullptr;
+
+    // codebook replicas: entry j at [j * NREP + r]; thread t fills entry t/2
+    // of each table, NREP/2 replicas
+    {
+        const int j = tid >> 1;
+#pragma unroll
+        for (int p = 0; p < NT; ++p) {
+            const float c = g.w[p].cb[eo * 256 + j];
+            float4 *d = reinterpret_cast<float4 *>(&tbl[p][j * NREP + (tid & 1) * (NREP / 2)]);
+#pragma unroll
+            for (int q = 0; q < NREP / 8; ++q) d[q] = make_float4(c, c, c, c);
+        }
+    }
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.x_rows * K * 2);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(idx_e, (int64_t)g.OUT * K);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(gs_e, AFFINE ? (int64_t)g.OUT * ngroups * 4 : 0);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(go_e, AFFINE ? (int64_t)g.OUT * ngroups * 4 : 0);
+    constexpr uint32_t kOob = 0x80000000u;
+
+    // X rows of this thread (fixed for the block)
+    const int a_cc = tid & 7;
+    uint32_t a_off[BM / 64];
+#pragma unroll
+    for (int p = 0; p < BM / 64; ++p) {
+        const int r = r0 + (tid >> 3) + 64 * p;
+        int src = r;
+        if constexpr (GROUPED) {
+            if (r < r1 && g.rows) src = g.rows[r];
+        }
+        a_off[p] = (r < r1 && src >= 0 && src < g.x_rows)
+                       ? (uint32_t)(src * K + a_cc * 8) * 2u : kOob;
+    }
+    const uint32_t q_base = row_ok ? (uint32_t)(grow * K + b_half * 32) : kOob;
+    const uint32_t so_base = row_ok ? (uint32_t)(grow * ngroups) * 4u : kOob;
+
+    // Loads are issued unconditionally (steps past the end read at kOob, which
+    // the buffer range check turns into zeros without memory traffic): a
+    // conditional prefetch would make the compiler's wait counting assume the
+    // prefetch absent and wait for it at the next use of the older stage.
+    auto load_stage = [&](int ks, GemmStage<BM> &st) {
+        const bool live = ks < nk;
+        const uint32_t k0 = (live ? ks : 0) * kBK;
+#pragma unroll
+        for (int p = 0; p < BM / 64; ++p)
+            st.a[p] = buf_load16(xr, (a_off[p] == kOob || !live) ? kOob : a_off[p] + k0 * 2);
+        const uint32_t qo = (q_base == kOob || !live) ? kOob : q_base + k0;
+        st.q[0] = buf_load16(qr, qo);
+        st.q[1] = buf_load16(qr, qo == kOob ? kOob : qo + 16);
         if constexpr (AFFINE) {
-            const uint32_t so = grow < g.OUT ? (uint32_t)((grow * ngroups + k0 / g.group) * 4) : kOob;
+            const uint32_t so = (so_base == kOob || !live) ? kOob : so_base + (k0 / g.group) * 4;
             st.s = buf_loadf(sr, so);
             st.o = buf_loadf(orr, so);
         } else {
@@ -116,19 +254,105 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(const GemmArgs g)
         }
     };
 
-    // sidecar cursor of this thread's row: next entry (col, val) prefetched
-    const bool has_sc = g.rp != nullptr && grow < g.OUT;
-    int32_t sc_j = 0, sc_end = 0;
-    int32_t sc_col = 0x7fffffff;
-    float sc_val = 0.f;
-    if (has_sc) {
-        sc_j = g.rp[grow];
-        sc_end = g.rp[grow + 1];
-        if (sc_j < sc_end) {
-            sc_col = g.col[sc_j];
-            sc_val = g.val[sc_j];
+    // ---- sidecar: the block's CSR entries (per part a contiguous range) ----
+    // Staged into LDS as {col, 16-bit value} so the per-step cursor reads LDS
+    // and never waits on global loads behind the prefetched stages.  A block
+    // with more than kScCap entries (or K > 65535) reads them from global
+    // memory instead (same results, slower).
+    constexpr int RPP = PAIR ? kBN / 2 : kBN;  // rows per part
+    int sc_lo[NT], sc_base[NT], sc_total = 0;
+#pragma unroll
+    for (int p = 0; p < NT; ++p) {
+        sc_base[p] = sc_total;
+        sc_lo[p] = 0;
+        if (g.w[p].rp != nullptr) {
+            const int32_t *rpp = g.w[p].rp + eo * (g.OUT + 1);
+            sc_lo[p] = rpp[n0];
+            sc_total += rpp[min(n0 + RPP, g.OUT)] - sc_lo[p];
         }
     }
+    const bool sc_in_lds = sc_total <= kScCap && K <= 0xffff;
+    int32_t sc_cur = 0, sc_end = 0;
+    if (ws.rp != nullptr && row_ok) {
+        const int32_t *rp = ws.rp + eo * (g.OUT + 1);
+        sc_cur = rp[grow];
+        sc_end = rp[grow + 1];
+        if (sc_in_lds) {
+            const int shift = (part ? sc_base[NT - 1] - sc_lo[NT - 1] : sc_base[0] - sc_lo[0]);
+            sc_cur += shift;
+            sc_end += shift;
+        }
+    }
+    if (sc_in_lds) {
+        for (int i = tid; i < sc_total; i += kGemmThreads) {
+            const int p = (NT == 2 && i >= sc_base[NT - 1]) ? 1 : 0;
+            const int j = sc_lo[p] + (i - sc_base[p]);
+            const int32_t col = p ? g.w[NT - 1].col[j] : g.w[0].col[j];
+            const float v = p ? g.w[NT - 1].val[j] : g.w[0].val[j];
+            sSc[i] = static_cast<uint32_t>(col) | (static_cast<uint32_t>(to16<BF16>(v)) << 16);
+        }
+    }
+
+    // lookup of byte b of index word w in this thread's table
+    const uint32_t lane_off = (lane & (NREP - 1)) * 4u;
+    const char *tb = reinterpret_cast<const char *>(&tbl[part][0]);
+    auto lookup = [&](uint32_t w, int b) -> float {
+        constexpr int kShift = NREP == 32 ? 7 : 6;  // log2(NREP * 4)
+        return *reinterpret_cast<const float *>(tb + lane_off + (((w >> (8 * b)) & 0xffu) << kShift));
+    };
+
+    auto write_stage = [&](int ks, const GemmStage<BM> &st, int buf, auto sc_lds) {
+        constexpr bool SC_LDS = decltype(sc_lds)::value;
+#pragma unroll
+        for (int p = 0; p < BM / 64; ++p)
+            *reinterpret_cast<u32x4 *>(&sA[buf][swz((tid >> 3) + 64 * p, a_cc)]) = st.a[p];
+        // 32 indices -> 4 chunks of 8 16-bit weights (chunks 4*half .. 4*half+3)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                uint32_t pk[4];
+#pragma unroll
+                for (int dd = 0; dd < 2; ++dd) {
+                    const uint32_t w = st.q[h][cc * 2 + dd];
+                    float v[4];
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const float c = lookup(w, b);
+                        v[b] = AFFINE ? fmaf(c, st.s, st.o) : c;
+                    }
+                    pk[dd * 2] = pack2<BF16>(v[0], v[1]);
+                    pk[dd * 2 + 1] = pack2<BF16>(v[2], v[3]);
+                }
+                *reinterpret_cast<u32x4 *>(&sB[buf][swz(b_row, b_half * 4 + h * 2 + cc)]) =
+                    u32x4{pk[0], pk[1], pk[2], pk[3]};
+            }
+        // sidecar: replace entries with column in [lo, lo + 32)
+        const int lo = ks * kBK + b_half * 32, hi = lo + 32;
+        uint16_t *row = &sB[buf][0];
+        if constexpr (SC_LDS) {
+            while (sc_cur < sc_end) {
+                const uint32_t ent = sSc[sc_cur];
+                const int col = static_cast<int>(ent & 0xffffu);
+                if (col >= hi) break;
+                if (col >= lo) {
+                    const int kc = col - ks * kBK;
+                    row[swz(b_row, kc >> 3) + (kc & 7)] = static_cast<uint16_t>(ent >> 16);
+                }
+                ++sc_cur;
+            }
+        } else {
+            while (sc_cur < sc_end) {
+                const int col = ws.col[sc_cur];
+                if (col >= hi) break;
+                if (col >= lo) {
+                    const int kc = col - ks * kBK;
+                    row[swz(b_row, kc >> 3) + (kc & 7)] = to16<BF16>(ws.val[sc_cur]);
+                }
+                ++sc_cur;
+            }
+        }
+    };
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -138,66 +362,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(const GemmArgs g)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    GemmStage<BM> cur;
-    load_stage(0, cur);
-    const uint32_t rep = (lane % kCbRep) * 4u;
-
-    for (int ks = 0; ks < nk; ++ks) {
-        __syncthreads();  // previous MFMAs are done with sA / sB
-        // X -> LDS
-#pragma unroll
-        for (int p = 0; p < BM / 32; ++p)
-            *reinterpret_cast<u32x4 *>(&sA[(a_row + 32 * p) * kLdsRow + a_cc * 8]) = cur.a[p];
-        // indices -> dequantised 16-bit weights -> LDS
-        {
-            uint32_t packed[16];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const uint32_t w = cur.q[h][d];
-                    float v[4];
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const float c = *reinterpret_cast<const float *>(
-                            reinterpret_cast<const char *>(tbl) + ((w >> (8 * b)) & 0xffu) * (kCbRep * 4) + rep);
-                        v[b] = AFFINE ? fmaf(c, cur.s, cur.o) : c;
-                    }
-                    packed[h * 8 + d * 2] = to16<BF16>(v[0]) | (uint32_t(to16<BF16>(v[1])) << 16);
-                    packed[h * 8 + d * 2 + 1] = to16<BF16>(v[2]) | (uint32_t(to16<BF16>(v[3])) << 16);
-                }
-            uint16_t *dst = &sB[b_row * kLdsRow + b_half * 32];
-#pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4)
-                *reinterpret_cast<u32x4 *>(dst + c4 * 8) =
-                    u32x4{packed[4 * c4], packed[4 * c4 + 1], packed[4 * c4 + 2], packed[4 * c4 + 3]};
-            // sidecar: replace entries in [lo, hi) of this row
-            const int lo = ks * kBK + b_half * 32, hi = lo + 32;
-            while (sc_col < hi) {
-                if (sc_col >= lo) sB[b_row * kLdsRow + (sc_col - ks * kBK)] = to16<BF16>(sc_val);
-                ++sc_j;
-                if (sc_j < sc_end) {
-                    sc_col = g.col[sc_j];
-                    sc_val = g.val[sc_j];
-                } else {
-                    sc_col = 0x7fffffff;
-                }
-            }
-        }
-        __syncthreads();
-        if (ks + 1 < nk) load_stage(ks + 1, cur);
-        // MFMAs: 4 k-substeps of 16
+    auto mfma_step = [&](int buf) {
+        const int hsel = lane >> 5;
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
             u32x4 av[TM], bv[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
                 av[i] = *reinterpret_cast<const u32x4 *>(
-                    &sA[(wm * WM + i * 32 + lane % 32) * kLdsRow + kk * 16 + (lane / 32) * 8]);
+                    &sA[buf][swz(wm * WM + i * 32 + (lane & 31), kk * 2 + hsel)]);
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 bv[j] = *reinterpret_cast<const u32x4 *>(
-                    &sB[(wn * WN + j * 32 + lane % 32) * kLdsRow + kk * 16 + (lane / 32) * 8]);
+                    &sB[buf][swz(wn * 64 + j * 32 + (lane & 31), kk * 2 + hsel)]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -212,39 +389,250 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(const GemmArgs g)
                             acc[i][j], 0, 0, 0);
                 }
         }
-    }
+    };
 
-    // epilogue: acc[i][j][r] = C[row = 8*(r/4) + 4*(lane/32) + r%4][col = lane%32]
+    // ---- main loop: loads two steps ahead, LDS double buffer -------------
+    auto main_loop = [&](auto sc_lds) {
+        GemmStage<BM> s0, s1;
+        load_stage(0, s0);
+        load_stage(1, s1);
+        __syncthreads();  // codebook tables and staged sidecar visible
+        write_stage(0, s0, 0, sc_lds);
+        lds_barrier();
+        for (int ks = 0; ks < nk; ks += 2) {
+            load_stage(ks + 2, s0);
+            mfma_step(0);
+            if (ks + 1 < nk) write_stage(ks + 1, s1, 1, sc_lds);
+            lds_barrier();
+            if (ks + 1 >= nk) break;
+            load_stage(ks + 3, s1);
+            mfma_step(1);
+            if (ks + 2 < nk) write_stage(ks + 2, s0, 0, sc_lds);
+            lds_barrier();
+        }
+    };
+    if (sc_in_lds) main_loop(std::true_type{});
+    else main_loop(std::false_type{});
+
+    // ---- epilogue: acc[i][j][r] = C[8*(r/4) + 4*(lane/32) + r%4][lane%32] ----
+    const int nrows = r1 - r0;
+    if constexpr (PAIR) {
+        // waves wn = 2, 3 hold the up rows of the features waves wn = 0, 1 hold
+        // as gate rows, in the same lane/register positions: hand them over
+        // through LDS (the B buffers are free now).
+        float *xch = reinterpret_cast<float *>(&sB[0][0]);
+        constexpr int PER = TM * TN * 16;
+        if (wn >= 2) {
+            float *d = xch + ((wm * 2 + (wn - 2)) * PER) * 64 + lane;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * WN + j * 32 + lane % 32;
-        if (n >= g.OUT) continue;
-        const float bv = g.bias ? g.bias[n] : 0.f;
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                if (m < g.M) {
-                    const float v = acc[i][j][r] + bv;
-                    const int64_t o = (int64_t)m * g.OUT + n;
-                    if (g.y_dtype == HXQ_F32) static_cast<float *>(g.y)[o] = v;
-                    else if (g.y_dtype == HXQ_BF16) static_cast<uint16_t *>(g.y)[o] = f32_to_bf16(v);
-                    else static_cast<uint16_t *>(g.y)[o] = f32_to_f16(v);
-                }
+                    for (int r = 0; r < 16; ++r) d[((i * TN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (wn < 2) {
+            const float *u = xch + ((wm * 2 + wn) * PER) * 64 + lane;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+                if (n >= g.OUT) continue;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int m = wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                        if (m < nrows) {
+                            const float gt = acc[i][j][r];
+                            const float up = u[((i * TN + j) * 16 + r) * 64];
+                            const float hv = gt / (1.f + expf(-gt)) * up;
+                            const int64_t o = (int64_t)(r0 + m) * g.OUT + n;
+                            static_cast<uint16_t *>(g.y)[o] = to16<BF16>(hv);
+                        }
+                    }
             }
+        }
+        return;
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= g.OUT) continue;
+            const float bv = g.bias ? g.bias[n] : 0.f;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                    if (m < nrows) {
+                        const float v = acc[i][j][r] + bv;
+                        const int64_t o = (int64_t)(r0 + m) * g.OUT + n;
+                        if (g.y_dtype == HXQ_F32) static_cast<float *>(g.y)[o] = v;
+                        else static_cast<uint16_t *>(g.y)[o] = g.y_dtype == HXQ_BF16
+                                                                    ? to16<true>(v) : to16<false>(v);
+                    }
+                }
+        }
     }
 }
 
-template <int BM, bool BF16>
-static int gemm_launch(const GemmArgs &a, hipStream_t stream) {
-    const dim3 grid((a.OUT + 127) / 128, (a.M + BM - 1) / BM);
-    if (a.gs)
-        hipLaunchKernelGGL((gemm_kernel<BM, 128, BF16, true>), grid, dim3(kGemmThreads), 0, stream, a);
+// ---------------------------------------------------------------------------
+// MoE routing: softmax over experts, top-k (ties -> lower expert id), and the
+// expert-sorted assignment lists.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int32_t T, int32_t E,
+                                                       int32_t k, int32_t renorm, int32_t *ids,
+                                                       float *wts) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const float *l = logits + (int64_t)t * E;
+    float mx = -INFINITY;
+    for (int i = 0; i < E; ++i) mx = fmaxf(mx, l[i]);
+    float sum = 0.f;
+    for (int i = 0; i < E; ++i) sum += expf(l[i] - mx);
+    uint64_t taken[4] = {0, 0, 0, 0};  // E <= 256
+    float picked = 0.f;
+    for (int s = 0; s < k; ++s) {
+        int best = -1;
+        float bv = -INFINITY;
+        for (int i = 0; i < E; ++i) {
+            if ((taken[i >> 6] >> (i & 63)) & 1ull) continue;
+            const float v = l[i];
+            if (best < 0 || v > bv) { best = i; bv = v; }
+        }
+        taken[best >> 6] |= 1ull << (best & 63);
+        const float p = expf(bv - mx) / sum;
+        ids[(int64_t)t * k + s] = best;
+        wts[(int64_t)t * k + s] = p;
+        picked += p;
+    }
+    if (renorm) {
+        for (int s = 0; s < k; ++s) wts[(int64_t)t * k + s] /= picked;
+    }
+}
+
+// Count (PLACE = false) or place (PLACE = true) the assignments of expert
+// blockIdx.x.  4 waves split the assignment list into contiguous quarters;
+// positions follow assignment order (token-major), so they are deterministic.
+template <bool PLACE>
+__global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64_t n_assign,
+                                                       int32_t E, int32_t k, int32_t *counts,
+                                                       int32_t *offsets, int32_t *sorted_rows,
+                                                       int32_t *assign_pos) {
+    __shared__ int wsum[4];
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t per = ((n_assign + 255) / 256) * 64;  // multiple of 64
+    const int64_t a0 = wave * per, a1 = min(a0 + per, n_assign);
+    int cnt = 0;
+    for (int64_t a = a0; a < a1; a += 64) {
+        const bool hit = a + lane < a1 && ids[a + lane] == e;
+        cnt += __popcll(__ballot(hit));
+    }
+    if (!PLACE) {
+        if (lane == 0) wsum[wave] = cnt;
+        __syncthreads();
+        if (threadIdx.x == 0) counts[e] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        return;
+    }
+    // global offset of this expert: sum of counts of experts before it
+    int pre = 0;
+    for (int i = threadIdx.x; i < e; i += 256) pre += counts[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) pre += __shfl_xor(pre, m, kWave);
+    __shared__ int psum[4];
+    if (lane == 0) {
+        psum[wave] = pre;
+        wsum[wave] = cnt;
+    }
+    __syncthreads();
+    const int off = psum[0] + psum[1] + psum[2] + psum[3];
+    int base = off;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    if (threadIdx.x == 0) {
+        offsets[e] = off;
+        if (e == E - 1) offsets[E] = off + wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int64_t a = a0; a < a1; a += 64) {
+        const bool hit = a + lane < a1 && ids[a + lane] == e;
+        const unsigned long long mask = __ballot(hit);
+        if (hit) {
+            const int pos = base + __popcll(mask & below);
+            sorted_rows[pos] = static_cast<int32_t>((a + lane) / k);
+            assign_pos[a + lane] = pos;
+        }
+        base += __popcll(mask);
+    }
+}
+
+// y[t, :] = sum_s w[t, s] * O[assign_pos[t*k + s], :], slots in order.
+template <int YDT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const float *wts,
+                                                          const int32_t *pos, int32_t k,
+                                                          int32_t hidden, void *y) {
+    const int t = blockIdx.y;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= hidden) return;
+    float acc = 0.f;
+    for (int s = 0; s < k; ++s) {
+        const int64_t a = (int64_t)t * k + s;
+        acc = fmaf(wts[a], O[(int64_t)pos[a] * hidden + c], acc);
+    }
+    store_act<YDT>(y, (int64_t)t * hidden + c, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+template <int BM, bool BF16, bool GROUPED, bool PAIR>
+static int gemm_launch(const GemmArgs &a, int grid_x, int grid_y, hipStream_t stream) {
+    const dim3 grid(grid_x, grid_y);
+    if (a.w[0].gs)
+        hipLaunchKernelGGL((gemm_kernel<BM, BF16, true, GROUPED, PAIR>), grid, dim3(kGemmThreads),
+                           0, stream, a);
     else
-        hipLaunchKernelGGL((gemm_kernel<BM, 128, BF16, false>), grid, dim3(kGemmThreads), 0, stream, a);
+        hipLaunchKernelGGL((gemm_kernel<BM, BF16, false, GROUPED, PAIR>), grid, dim3(kGemmThreads),
+                           0, stream, a);
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
+}
+
+static int check_bank(const hxq_expert_bank *b, const char *what, int64_t out, int64_t in,
+                      int32_t group) {
+    HXQ_REQUIRE(b && b->indices && b->codebook, std::string(what) + ": indices and codebook required");
+    const bool affine = b->group_scale || b->group_offset;
+    HXQ_REQUIRE(!affine || (b->group_scale && b->group_offset),
+                std::string(what) + ": group_scale and group_offset must be given together");
+    HXQ_REQUIRE(!affine || (group >= kBK && group % kBK == 0 && in % group == 0),
+                std::string(what) + ": group_size must be a multiple of 64 dividing in_features");
+    HXQ_REQUIRE(!b->sc_row_ptr || (b->sc_col && b->sc_val),
+                std::string(what) + ": sidecar CSR needs row_ptr, col and val");
+    HXQ_REQUIRE(out * in < (int64_t{1} << 31), std::string(what) + ": matrix too large");
+    return HXQ_OK;
+}
+
+static WSet wset_of(const hxq_expert_bank *b) {
+    return WSet{b->indices, b->codebook, b->group_scale, b->group_offset,
+                b->sc_row_ptr, b->sc_col, b->sc_val};
+}
+
+// Grouped launch over a sorted assignment list: BM 128 when the mean rows per
+// expert exceed 64, else 64.
+template <bool PAIR>
+static int grouped_launch(GemmArgs &a, int64_t n_assign, bool bf16, hipStream_t stream) {
+    const int64_t mean = n_assign / std::max<int32_t>(a.n_experts, 1);
+    const int bn = PAIR ? kBN / 2 : kBN;
+    const int gx = static_cast<int>((a.OUT + bn - 1) / bn);
+    if (mean > 64) {
+        const int gy = static_cast<int>((n_assign + 127) / 128 + a.n_experts);
+        return bf16 ? gemm_launch<128, true, true, PAIR>(a, gx, gy, stream)
+                    : gemm_launch<128, false, true, PAIR>(a, gx, gy, stream);
+    }
+    const int gy = static_cast<int>((n_assign + 63) / 64 + a.n_experts);
+    return bf16 ? gemm_launch<64, true, true, PAIR>(a, gx, gy, stream)
+                : gemm_launch<64, false, true, PAIR>(a, gx, gy, stream);
 }
 
 }  // namespace hxq
@@ -265,23 +653,176 @@ extern "C" int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
     HXQ_REQUIRE(m_rows > 0 && out_features > 0 && in_features > 0, "empty problem");
     HXQ_REQUIRE(in_features % kBK == 0, "in_features must be a multiple of 64");
     HXQ_REQUIRE(m_rows * in_features * 2 < (int64_t{1} << 31) &&
-                    out_features * in_features < (int64_t{1} << 31) &&
-                    m_rows * out_features < (int64_t{1} << 31),
+                    out_features * in_features < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
-    const bool affine = group_scale || group_offset;
-    HXQ_REQUIRE(!affine || (group_scale && group_offset),
-                "group_scale and group_offset must be given together");
-    HXQ_REQUIRE(!affine || (group_size >= kBK && group_size % kBK == 0 &&
-                            in_features % group_size == 0),
-                "the GEMM needs group_size to be a multiple of 64 dividing in_features");
-    HXQ_REQUIRE(!sc_row_ptr || (sc_col && sc_val), "sidecar CSR needs row_ptr, col and val");
-    GemmArgs a{static_cast<const uint16_t *>(x), indices, codebook, group_scale, group_offset,
-               sc_row_ptr, sc_col, sc_val, bias, y,
-               static_cast<int32_t>(m_rows), static_cast<int32_t>(out_features),
-               static_cast<int32_t>(in_features), group_size, y_dtype, 0};
-    const int64_t tiles256 = ((m_rows + 255) / 256) * ((out_features + 127) / 128);
-    const bool big = tiles256 >= device_cu_count();
-    if (x_dtype == HXQ_BF16)
-        return big ? gemm_launch<256, true>(a, stream) : gemm_launch<128, true>(a, stream);
-    return big ? gemm_launch<256, false>(a, stream) : gemm_launch<128, false>(a, stream);
+    const hxq_expert_bank bank{indices, codebook, group_scale, group_offset,
+                               sc_row_ptr, sc_col, sc_val};
+    if (int rc = check_bank(&bank, "weights", out_features, in_features, group_size)) return rc;
+    GemmArgs a{};
+    a.x = static_cast<const uint16_t *>(x);
+    a.w[0] = wset_of(&bank);
+    a.w[1] = a.w[0];
+    a.bias = bias;
+    a.y = y;
+    a.M = static_cast<int32_t>(m_rows);
+    a.OUT = static_cast<int32_t>(out_features);
+    a.K = static_cast<int32_t>(in_features);
+    a.group = group_size > 0 ? group_size : kBK;
+    a.y_dtype = y_dtype;
+    a.n_experts = 1;
+    a.x_rows = a.M;
+    const int gx = static_cast<int>((out_features + kBN - 1) / kBN);
+    const bool bf16 = x_dtype == HXQ_BF16;
+    const int gy = static_cast<int>((m_rows + 127) / 128);
+    return bf16 ? gemm_launch<128, true, false, false>(a, gx, gy, stream)
+                : gemm_launch<128, false, false, false>(a, gx, gy, stream);
+}
+
+extern "C" int hxq_moe_route(const float *logits, int64_t n_tokens, int32_t n_experts,
+                             int32_t top_k, int32_t renormalize, int32_t *topk_ids,
+                             float *topk_weights, int32_t *expert_counts,
+                             int32_t *expert_offsets, int32_t *sorted_rows, int32_t *assign_pos,
+                             hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(logits && topk_ids && topk_weights && expert_counts && expert_offsets &&
+                    sorted_rows && assign_pos, "all pointers are required");
+    HXQ_REQUIRE(n_tokens > 0 && n_tokens * top_k < (int64_t{1} << 31), "bad n_tokens");
+    HXQ_REQUIRE(n_experts >= 1 && n_experts <= 256, "n_experts must be in 1..256");
+    HXQ_REQUIRE(top_k >= 1 && top_k <= n_experts, "top_k must be in 1..n_experts");
+    const int64_t n_assign = n_tokens * top_k;
+    hipLaunchKernelGGL(moe_topk_kernel, dim3((n_tokens + 255) / 256), dim3(256), 0, stream,
+                       logits, static_cast<int32_t>(n_tokens), n_experts, top_k, renormalize,
+                       topk_ids, topk_weights);
+    HXQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(moe_sort_kernel<false>, dim3(n_experts), dim3(256), 0, stream, topk_ids,
+                       n_assign, n_experts, top_k, expert_counts, expert_offsets, sorted_rows,
+                       assign_pos);
+    HXQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(moe_sort_kernel<true>, dim3(n_experts), dim3(256), 0, stream, topk_ids,
+                       n_assign, n_experts, top_k, expert_counts, expert_offsets, sorted_rows,
+                       assign_pos);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
+extern "C" int hxq_moe_grouped_gemm(const void *x, int32_t x_dtype, int64_t x_rows,
+                                    const int32_t *sorted_rows, const int32_t *expert_offsets,
+                                    int64_t n_assign, int32_t n_experts,
+                                    const hxq_expert_bank *bank, int32_t group_size, void *y,
+                                    int32_t y_dtype, int64_t out_features, int64_t in_features,
+                                    hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && expert_offsets && y, "x, expert_offsets and y are required");
+    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16, "x must be bf16 or fp16");
+    HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
+    HXQ_REQUIRE(n_experts >= 1 && n_experts <= 256, "n_experts must be in 1..256");
+    HXQ_REQUIRE(n_assign > 0 && x_rows > 0 && out_features > 0 && in_features > 0, "empty problem");
+    HXQ_REQUIRE(in_features % kBK == 0, "in_features must be a multiple of 64");
+    HXQ_REQUIRE(x_rows * in_features * 2 < (int64_t{1} << 31), "x too large for 32-bit offsets");
+    HXQ_REQUIRE(sorted_rows || x_rows >= n_assign, "without sorted_rows x holds n_assign rows");
+    if (int rc = check_bank(bank, "bank", out_features, in_features, group_size)) return rc;
+    GemmArgs a{};
+    a.x = static_cast<const uint16_t *>(x);
+    a.rows = sorted_rows;
+    a.seg = expert_offsets;
+    a.w[0] = wset_of(bank);
+    a.w[1] = a.w[0];
+    a.y = y;
+    a.M = static_cast<int32_t>(n_assign);
+    a.OUT = static_cast<int32_t>(out_features);
+    a.K = static_cast<int32_t>(in_features);
+    a.group = group_size > 0 ? group_size : kBK;
+    a.y_dtype = y_dtype;
+    a.n_experts = n_experts;
+    a.x_rows = static_cast<int32_t>(x_rows);
+    return grouped_launch<false>(a, n_assign, x_dtype == HXQ_BF16, stream);
+}
+
+extern "C" int64_t hxq_moe_ffn_workspace_bytes(int64_t n_tokens, int64_t hidden,
+                                               int64_t intermediate, int32_t top_k) {
+    if (n_tokens <= 0 || hidden <= 0 || intermediate <= 0 || top_k <= 0) return -1;
+    const int64_t na = n_tokens * top_k;
+    const int64_t h_bytes = ((na * intermediate * 2 + 255) / 256) * 256;
+    return h_bytes + na * hidden * 4 + 256;
+}
+
+extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int64_t hidden,
+                           int64_t intermediate, int32_t n_experts, int32_t top_k,
+                           const float *topk_weights, const int32_t *expert_offsets,
+                           const int32_t *sorted_rows, const int32_t *assign_pos,
+                           const hxq_expert_bank *gate, const hxq_expert_bank *up,
+                           const hxq_expert_bank *down, int32_t group_size, void *workspace,
+                           int64_t workspace_bytes, void *y, int32_t y_dtype,
+                           hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && topk_weights && expert_offsets && sorted_rows && assign_pos && y &&
+                    workspace, "all pointers are required");
+    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16, "x must be bf16 or fp16");
+    HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
+    HXQ_REQUIRE(n_experts >= 1 && n_experts <= 256, "n_experts must be in 1..256");
+    HXQ_REQUIRE(top_k >= 1 && top_k <= n_experts, "top_k must be in 1..n_experts");
+    HXQ_REQUIRE(n_tokens > 0 && hidden > 0 && intermediate > 0, "empty problem");
+    HXQ_REQUIRE(hidden % kBK == 0 && intermediate % kBK == 0,
+                "hidden and intermediate must be multiples of 64");
+    const int64_t na = n_tokens * top_k;
+    HXQ_REQUIRE(na * std::max(hidden, intermediate) * 4 < (int64_t{1} << 31) &&
+                    n_tokens * hidden * 2 < (int64_t{1} << 31),
+                "problem too large for 32-bit offsets");
+    const int64_t need = hxq_moe_ffn_workspace_bytes(n_tokens, hidden, intermediate, top_k);
+    HXQ_REQUIRE(workspace_bytes >= need, "workspace too small (hxq_moe_ffn_workspace_bytes)");
+    HXQ_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-B aligned");
+    if (int rc = check_bank(gate, "gate", intermediate, hidden, group_size)) return rc;
+    if (int rc = check_bank(up, "up", intermediate, hidden, group_size)) return rc;
+    if (int rc = check_bank(down, "down", hidden, intermediate, group_size)) return rc;
+    HXQ_REQUIRE((gate->group_scale != nullptr) == (up->group_scale != nullptr),
+                "gate and up must agree on the affine");
+    const bool bf16 = x_dtype == HXQ_BF16;
+    uint16_t *H = static_cast<uint16_t *>(workspace);
+    float *O = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                         ((na * intermediate * 2 + 255) / 256) * 256);
+    // 1) H = silu(X_e Wg_e^T) * (X_e Wu_e^T), rows in expert-sorted order
+    GemmArgs a{};
+    a.x = static_cast<const uint16_t *>(x);
+    a.rows = sorted_rows;
+    a.seg = expert_offsets;
+    a.w[0] = wset_of(gate);
+    a.w[1] = wset_of(up);
+    a.y = H;
+    a.M = static_cast<int32_t>(na);
+    a.OUT = static_cast<int32_t>(intermediate);
+    a.K = static_cast<int32_t>(hidden);
+    a.group = group_size > 0 ? group_size : kBK;
+    a.y_dtype = x_dtype;
+    a.n_experts = n_experts;
+    a.x_rows = static_cast<int32_t>(n_tokens);
+    if (int rc = grouped_launch<true>(a, na, bf16, stream)) return rc;
+    // 2) O = H_e Wd_e^T (fp32, sorted order)
+    GemmArgs d{};
+    d.x = H;
+    d.rows = nullptr;
+    d.seg = expert_offsets;
+    d.w[0] = wset_of(down);
+    d.w[1] = d.w[0];
+    d.y = O;
+    d.M = static_cast<int32_t>(na);
+    d.OUT = static_cast<int32_t>(hidden);
+    d.K = static_cast<int32_t>(intermediate);
+    d.group = a.group;
+    d.y_dtype = HXQ_F32;
+    d.n_experts = n_experts;
+    d.x_rows = static_cast<int32_t>(na);
+    if (int rc = grouped_launch<false>(d, na, bf16, stream)) return rc;
+    // 3) y[t] = sum_s w[t,s] O[pos(t,s)]
+    const dim3 grid((hidden + 255) / 256, n_tokens);
+    if (y_dtype == HXQ_F32)
+        hipLaunchKernelGGL(moe_combine_kernel<HXQ_F32>, grid, dim3(256), 0, stream, O,
+                           topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y);
+    else if (y_dtype == HXQ_BF16)
+        hipLaunchKernelGGL(moe_combine_kernel<HXQ_BF16>, grid, dim3(256), 0, stream, O,
+                           topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y);
+    else
+        hipLaunchKernelGGL(moe_combine_kernel<HXQ_F16>, grid, dim3(256), 0, stream, O,
+                           topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
 }

@@ -21,7 +21,8 @@
 // mamba_scan_chunked.py:171-183).
 //
 // Layout of a scan block: 8 waves = HPB heads x NSPLIT state splits; lane = p
-// (head_dim <= 64 per p-block); each lane keeps its N/NSPLIT states in VGPRs.
+// (head_dim <= 64 per p-block); each lane keeps its N/NSPLIT (<= 32) states in
+// VGPRs and reads a step's B/C values into registers before using them.
 // Per block of TB = 16 steps, B/C (fp32), x and dt are staged in LDS and B/C
 // are read as LDS broadcasts; per-split y partials are summed through LDS in a
 // fixed order (deterministic).
@@ -60,7 +61,7 @@ __device__ __forceinline__ float ld_any(const void *p, int64_t i, int dt) {
 // Passes 1 and 3.  SL = states per lane, HPB = heads per block; NSPLIT =
 // kScanWaves / HPB state splits, N = SL * NSPLIT.  EMIT_Y selects pass 3.
 template <int SL, int HPB, bool EMIT_Y>
-__global__ __launch_bounds__(kScanThreads, 2) void scan_chunk_kernel(const ScanArgs a) {
+__global__ __launch_bounds__(kScanThreads, 4) void scan_chunk_kernel(const ScanArgs a) {
     constexpr int NSPLIT = kScanWaves / HPB;
     const int N = SL * NSPLIT;
     __shared__ float sB[kTB][SL * NSPLIT];
@@ -127,25 +128,31 @@ __global__ __launch_bounds__(kScanThreads, 2) void scan_chunk_kernel(const ScanA
             const float da = expf(ad);
             const float xv = sX[tt][hl][lane];
             const float dx = dtv * xv;
-            float yp = 0.f;
+            // B (and C) values of a half-slice go to registers before use:
+            // one LDS wait per half, and at most 16+16 live values.
+            constexpr int HS = SL >= 16 ? 16 : SL;
             const float *Bt = &sB[tt][ns * SL];
             const float *Ct = &sC[EMIT_Y ? tt : 0][ns * SL];
+            float yp[4] = {0.f, 0.f, 0.f, 0.f};  // independent partial sums
 #pragma unroll
-            for (int i = 0; i < SL; i += 4) {
-                const float4 b4 = *reinterpret_cast<const float4 *>(Bt + i);
-                st[i + 0] = fmaf(da, st[i + 0], dx * b4.x);
-                st[i + 1] = fmaf(da, st[i + 1], dx * b4.y);
-                st[i + 2] = fmaf(da, st[i + 2], dx * b4.z);
-                st[i + 3] = fmaf(da, st[i + 3], dx * b4.w);
-                if constexpr (EMIT_Y) {
-                    const float4 c4 = *reinterpret_cast<const float4 *>(Ct + i);
-                    yp = fmaf(st[i + 0], c4.x, yp);
-                    yp = fmaf(st[i + 1], c4.y, yp);
-                    yp = fmaf(st[i + 2], c4.z, yp);
-                    yp = fmaf(st[i + 3], c4.w, yp);
+            for (int i0 = 0; i0 < SL; i0 += HS) {
+                float bv[HS], cv[EMIT_Y ? HS : 1];
+#pragma unroll
+                for (int i = 0; i < HS; i += 4) {
+                    const float4 b4 = *reinterpret_cast<const float4 *>(Bt + i0 + i);
+                    bv[i] = b4.x; bv[i + 1] = b4.y; bv[i + 2] = b4.z; bv[i + 3] = b4.w;
+                    if constexpr (EMIT_Y) {
+                        const float4 c4 = *reinterpret_cast<const float4 *>(Ct + i0 + i);
+                        cv[i] = c4.x; cv[i + 1] = c4.y; cv[i + 2] = c4.z; cv[i + 3] = c4.w;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < HS; ++i) {
+                    st[i0 + i] = fmaf(da, st[i0 + i], dx * bv[i]);
+                    if constexpr (EMIT_Y) yp[i & 3] = fmaf(st[i0 + i], cv[i], yp[i & 3]);
                 }
             }
-            if constexpr (EMIT_Y) sY[tt][ns][hl][lane] = yp;
+            if constexpr (EMIT_Y) sY[tt][ns][hl][lane] = (yp[0] + yp[1]) + (yp[2] + yp[3]);
             else lsum += ad;
         }
         if constexpr (EMIT_Y) {
@@ -290,13 +297,12 @@ extern "C" int hxq_ssm_chunk_scan(const void *x, int32_t x_dtype, const void *dt
     const int64_t hpg = heads / ngroups;
     switch (state) {
         case 256:
-            if (hpg % 2 == 0) return launch_chunks<64, 2>(a, stream);
             return launch_chunks<32, 1>(a, stream);
         case 128:
-            if (hpg % 4 == 0) return launch_chunks<64, 4>(a, stream);
+            if (hpg % 2 == 0) return launch_chunks<32, 2>(a, stream);
             return launch_chunks<16, 1>(a, stream);
         case 64:
-            if (hpg % 8 == 0) return launch_chunks<64, 8>(a, stream);
+            if (hpg % 4 == 0) return launch_chunks<32, 4>(a, stream);
             return launch_chunks<8, 1>(a, stream);
         case 32:
             if (hpg % 8 == 0) return launch_chunks<32, 8>(a, stream);

@@ -37,6 +37,15 @@ class HxqMatrix(ctypes.Structure):
     ]
 
 
+class HxqExpertBank(ctypes.Structure):
+    """Mirror of ``hxq_expert_bank`` in include/hxq.h (arrays stacked over experts)."""
+
+    _fields_ = [
+        ("indices", P), ("codebook", P), ("group_scale", P), ("group_offset", P),
+        ("sc_row_ptr", P), ("sc_col", P), ("sc_val", P),
+    ]
+
+
 # name -> argtypes; every function returns int (hxq_status)
 SIGNATURES = {
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
@@ -47,12 +56,16 @@ SIGNATURES = {
                            I64, I64, I64, P, I64, P],
     "hxq_ssm_decode_step": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64,
                             P],
+    "hxq_moe_route": [P, I64, I32, I32, I32, P, P, P, P, P, P, P],
+    "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
+    "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
 }
 
 
 # name -> argtypes for entry points returning int64_t (sizes)
 SIGNATURES_I64 = {
     "hxq_ssm_scan_workspace_bytes": [I64] * 6,
+    "hxq_moe_ffn_workspace_bytes": [I64, I64, I64, I32],
 }
 
 
@@ -251,4 +264,89 @@ def ssm_decode_step(h, x, dt, A, B, C, D=None, out_dtype=torch.float32):
                                    _ptr(y), dtype_code(y.dtype), batch, heads, head_dim, state,
                                    ngroups, _stream(x))
     _check("hxq_ssm_decode_step", rc)
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Mixture of experts
+# ---------------------------------------------------------------------------
+class MoeRouting:
+    """Device routing produced by ``moe_route`` (all int32 except the weights)."""
+
+    __slots__ = ("topk_ids", "topk_weights", "expert_counts", "expert_offsets", "sorted_rows",
+                 "assign_pos", "top_k")
+
+    def __init__(self, **kw):
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+def moe_route(logits, top_k, renormalize=False):
+    """softmax(logits) -> top-k experts per token and the expert-sorted assignment lists."""
+    T, E = logits.shape
+    logits = logits.float().contiguous()
+    dev = logits.device
+    r = MoeRouting(
+        topk_ids=torch.empty(T, top_k, dtype=torch.int32, device=dev),
+        topk_weights=torch.empty(T, top_k, dtype=torch.float32, device=dev),
+        expert_counts=torch.empty(E, dtype=torch.int32, device=dev),
+        expert_offsets=torch.empty(E + 1, dtype=torch.int32, device=dev),
+        sorted_rows=torch.empty(T * top_k, dtype=torch.int32, device=dev),
+        assign_pos=torch.empty(T * top_k, dtype=torch.int32, device=dev),
+        top_k=int(top_k))
+    _need_device(logits)
+    rc = lib().hxq_moe_route(_ptr(logits), T, E, int(top_k), int(bool(renormalize)),
+                             _ptr(r.topk_ids), _ptr(r.topk_weights), _ptr(r.expert_counts),
+                             _ptr(r.expert_offsets), _ptr(r.sorted_rows), _ptr(r.assign_pos),
+                             _stream(logits))
+    _check("hxq_moe_route", rc)
+    return r
+
+
+def _bank(b):
+    _need_device(b["indices"], b["codebook"], b.get("group_scale"), b.get("group_offset"),
+                 b.get("sc_row_ptr"), b.get("sc_col"), b.get("sc_val"))
+    return HxqExpertBank(*(0 if b.get(k) is None else b[k].data_ptr()
+                           for k in ("indices", "codebook", "group_scale", "group_offset",
+                                     "sc_row_ptr", "sc_col", "sc_val")))
+
+
+def moe_grouped_gemm(x, sorted_rows, expert_offsets, bank, n_assign, out_dtype=torch.float32):
+    """Y[pos] = X[sorted_rows[pos]] @ W_e^T for every expert segment (sorted_rows None:
+    X already holds the n_assign rows in sorted order)."""
+    E, out_f, in_f = bank["indices"].shape
+    if x.shape[1] != in_f:
+        raise RuntimeError(f"x has {x.shape[1]} features, experts expect {in_f}")
+    y = torch.empty(int(n_assign), out_f, dtype=out_dtype, device=x.device)
+    _need_device(x, sorted_rows, expert_offsets, y)
+    bk = _bank(bank)
+    rc = lib().hxq_moe_grouped_gemm(_ptr(x), dtype_code(x.dtype), x.shape[0], _ptr(sorted_rows),
+                                    _ptr(expert_offsets), int(n_assign), E, ctypes.byref(bk),
+                                    int(bank.get("group_size") or 0), _ptr(y),
+                                    dtype_code(y.dtype), out_f, in_f, _stream(x))
+    _check("hxq_moe_grouped_gemm", rc)
+    return y
+
+
+def moe_ffn(x, routing, gate, up, down, out_dtype=None):
+    """SwiGLU MoE FFN: sum_s w[t,s] * down_e(silu(gate_e(x_t)) * up_e(x_t))."""
+    T, hidden = x.shape
+    E, inter, in_f = gate["indices"].shape
+    if in_f != hidden or down["indices"].shape[1:] != (hidden, inter):
+        raise RuntimeError("expert bank shapes do not match x")
+    y = torch.empty(T, hidden, dtype=out_dtype or x.dtype, device=x.device)
+    L = lib()
+    nbytes = L.hxq_moe_ffn_workspace_bytes(T, hidden, inter, routing.top_k)
+    if nbytes < 0:
+        raise RuntimeError("invalid MoE sizes")
+    ws = torch.empty(int(nbytes), dtype=torch.uint8, device=x.device)
+    _need_device(x, y, ws, routing.topk_weights, routing.expert_offsets, routing.sorted_rows,
+                 routing.assign_pos)
+    bg, bu, bd = _bank(gate), _bank(up), _bank(down)
+    rc = L.hxq_moe_ffn(_ptr(x), dtype_code(x.dtype), T, hidden, inter, E, routing.top_k,
+                       _ptr(routing.topk_weights), _ptr(routing.expert_offsets),
+                       _ptr(routing.sorted_rows), _ptr(routing.assign_pos), ctypes.byref(bg),
+                       ctypes.byref(bu), ctypes.byref(bd), int(gate.get("group_size") or 0),
+                       _ptr(ws), int(nbytes), _ptr(y), dtype_code(y.dtype), _stream(x))
+    _check("hxq_moe_ffn", rc)
     return y

@@ -137,6 +137,81 @@ int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
              hipStream_t stream);
 
 /*
+ * Mixture-of-experts FFN over HXQ experts (OLMoE-style SwiGLU experts).
+ * The reference has no MoE kernel: HelixLinear replaces per-expert nn.Linear
+ * modules only (helix_substrate/hf_quantizer.py:231-249), so each expert runs
+ * HelixLinear.forward (helix_linear.py:318-361) on its routed tokens.  These
+ * entry points run all experts of a layer in one grouped launch instead.
+ *
+ * An expert bank stacks the per-expert HXQ arrays along a leading expert
+ * axis: indices [E, out, in] u8, codebook [E, 256], group_scale/offset
+ * [E, out, in/G] (both NULL = no affine), sc_row_ptr [E, out+1] holding
+ * ABSOLUTE offsets into sc_col/sc_val (replacement values), columns ascending
+ * within a row.
+ */
+typedef struct hxq_expert_bank {
+    const uint8_t *indices;
+    const float *codebook;
+    const float *group_scale;
+    const float *group_offset;
+    const int32_t *sc_row_ptr;
+    const int32_t *sc_col;
+    const float *sc_val;
+} hxq_expert_bank;
+
+/*
+ * Routing: p = softmax(logits[t, :]) (fp32 [n_tokens, n_experts]); the top_k
+ * experts by logit (ties -> lower id) with weights p (renormalised to sum 1
+ * when `renormalize`); then the expert-sorted assignment list: expert e owns
+ * sorted positions [expert_offsets[e], expert_offsets[e+1]) in token order,
+ * sorted_rows[pos] = token, assign_pos[t*top_k + s] = pos of slot s of t.
+ * Outputs: topk_ids i32 / topk_weights f32 [n_tokens, top_k], expert_counts
+ * [E], expert_offsets [E+1], sorted_rows / assign_pos [n_tokens*top_k].
+ * Replaces: the router of transformers' OlmoeSparseMoeBlock (softmax ->
+ * topk, norm_topk_prob=False), which the reference leaves to the HF model.
+ */
+int hxq_moe_route(const float *logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
+                  int32_t renormalize, int32_t *topk_ids, float *topk_weights,
+                  int32_t *expert_counts, int32_t *expert_offsets, int32_t *sorted_rows,
+                  int32_t *assign_pos, hipStream_t stream);
+
+/*
+ * Grouped GEMM: for each expert e and each sorted position pos in its
+ * segment, Y[pos, :] = X[row(pos), :] @ W_e^T with row(pos) = sorted_rows[pos]
+ * (or pos itself when sorted_rows is NULL, X then holding n_assign rows).
+ * X bf16/fp16 [x_rows, in]; Y y_dtype [n_assign, out].  W_e dequantised into
+ * LDS and multiplied with MFMA as in hxq_gemm.
+ * Replaces: HelixLinear.forward per expert (helix_linear.py:318-361) on that
+ * expert's token rows.
+ */
+int hxq_moe_grouped_gemm(const void *x, int32_t x_dtype, int64_t x_rows,
+                         const int32_t *sorted_rows, const int32_t *expert_offsets,
+                         int64_t n_assign, int32_t n_experts, const hxq_expert_bank *bank,
+                         int32_t group_size, void *y, int32_t y_dtype, int64_t out_features,
+                         int64_t in_features, hipStream_t stream);
+
+/*
+ * Whole SwiGLU MoE FFN from a routing (hxq_moe_route):
+ *   H = silu(X Wg_e^T) * (X Wu_e^T)   (16-bit, x's dtype; one grouped launch)
+ *   O = H Wd_e^T                       (fp32, sorted order)
+ *   y[t] = sum_s topk_weights[t, s] * O[assign_pos[t*top_k + s]]  (slots in order)
+ * x bf16/fp16 [n_tokens, hidden]; y y_dtype [n_tokens, hidden].  `workspace`
+ * (device, 256-B aligned, >= hxq_moe_ffn_workspace_bytes) holds H and O.
+ * Replaces: the expert loop of OlmoeSparseMoeBlock.forward with HelixLinear
+ * experts (helix_linear.py:318-361 per expert projection).
+ */
+int64_t hxq_moe_ffn_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t intermediate,
+                                    int32_t top_k);
+
+int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int64_t hidden,
+                int64_t intermediate, int32_t n_experts, int32_t top_k,
+                const float *topk_weights, const int32_t *expert_offsets,
+                const int32_t *sorted_rows, const int32_t *assign_pos,
+                const hxq_expert_bank *gate, const hxq_expert_bank *up,
+                const hxq_expert_bank *down, int32_t group_size, void *workspace,
+                int64_t workspace_bytes, void *y, int32_t y_dtype, hipStream_t stream);
+
+/*
  * Selective scan (Mamba/Mamba2), fp32 state, chunk-parallel:
  *   a_t = exp(A[h] dt[b,t,h]);  h_t = a_t h_{t-1} + dt[b,t,h] x[b,t,h,p] B[b,t,g,n]
  *   y[b,t,h,p] = sum_n h_t C[b,t,g,n] + D[h] x[b,t,h,p],  g = h / (heads/ngroups)

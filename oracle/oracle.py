@@ -19,6 +19,10 @@ Reference functions restated (file:line under the reference checkout):
   follows ``triton_affine_group_matmul.py:379`` (value*scale, then +offset).
 * ``linear_f64``       -- ``x @ W^T + bias`` (``helix_linear.py:809-820``) in fp64.
 * ``ssm_scan_f64``     -- ``sequential_scan`` (``mamba_scan_chunked.py:42-86``).
+* ``moe_route_np`` / ``moe_sorted_lists_np`` / ``moe_ffn_np`` -- the OLMoE
+  MoE block (no reference kernel; transformers' OlmoeTopKRouter /
+  OlmoeExperts semantics, cited at the functions), composed from
+  ``linear_np``.
 * ``ssm_scan_chunked_np`` -- the chunked closed form of the same recurrence
   (the algorithm of ``chunked_scan``, ``mamba_scan_chunked.py:89-213``), written
   in the segment-sum form exp(cumA_t - cumA_s) that cannot overflow; fp64.
@@ -206,3 +210,61 @@ def ssm_scan_chunked_np(dt, A, x, B, C, D, h0=None, chunk=64):
         h = h * np.exp(lc[:, -1, :])[:, :, None, None] + np.einsum(
             "bsH,bsHp,bsHn->bHpn", w_end, dtx, Bh[:, cs:ce])
     return y, h
+
+
+# ---------------------------------------------------------------------------
+# Mixture of experts (benchmark config 4).  The reference has no MoE kernel;
+# the semantics are those of the HF OLMoE block that HelixLinear experts plug
+# into (transformers 5.15.0, models/olmoe/modeling_olmoe.py): router
+# OlmoeTopKRouter.forward (:337-346: fp32 softmax, topk, optional
+# renormalisation) and OlmoeExperts.forward (:301-325: per expert
+# down(silu(gate(x)) * up(x)) * weight, index_add into the token rows).
+# ---------------------------------------------------------------------------
+def moe_route_np(logits, top_k, renormalize=False):
+    """Softmax over experts in fp64; the top_k experts by logit, ties to the
+    lower expert id; weights = probabilities (renormalised on request)."""
+    lg = np.asarray(logits, np.float64)
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-lg, axis=1, kind="stable")[:, :top_k]
+    w = np.take_along_axis(p, ids, axis=1)
+    if renormalize:
+        w = w / w.sum(axis=1, keepdims=True)
+    return ids, w
+
+
+def moe_sorted_lists_np(ids, n_experts):
+    """Expert-sorted assignment lists: expert-major, then assignment (token-major)
+    order.  Returns counts [E], offsets [E+1], sorted_rows (token of each sorted
+    position) and assign_pos (sorted position of assignment t*k + s)."""
+    ids = np.asarray(ids)
+    k = ids.shape[1]
+    flat = ids.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=n_experts)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    assign_pos = np.empty_like(order)
+    assign_pos[order] = np.arange(order.size)
+    return counts, offsets, order // k, assign_pos
+
+
+def moe_ffn_np(x, ids, w, Wg, Wu, Wd):
+    """fp64 SwiGLU MoE FFN: y[t] = sum_s w[t,s] * Wd_e (silu(Wg_e x_t) * (Wu_e x_t)),
+    e = ids[t, s].  Wg/Wu/Wd: sequences (or callables e -> matrix) of dense
+    per-expert weights."""
+    get = (lambda W, e: W(e)) if callable(Wg) else (lambda W, e: W[e])
+    x = np.asarray(x, np.float64)
+    ids = np.asarray(ids)
+    w = np.asarray(w, np.float64)
+    y = None
+    for e in np.unique(ids):
+        tok, slot = np.nonzero(ids == e)
+        xe = x[tok]
+        g = linear_np(xe, get(Wg, e))
+        u = linear_np(xe, get(Wu, e))
+        h = g / (1.0 + np.exp(-g)) * u
+        o = linear_np(h, get(Wd, e))
+        if y is None:
+            y = np.zeros((x.shape[0], o.shape[1]))
+        np.add.at(y, tok, o * w[tok, slot][:, None])
+    return y
