@@ -25,6 +25,7 @@ _DTYPE_CODE = {torch.float32: HXQ_F32, torch.bfloat16: HXQ_BF16, torch.float16: 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
 I64 = ctypes.c_int64
+F32 = ctypes.c_float
 
 
 class HxqMatrix(ctypes.Structure):
@@ -57,6 +58,11 @@ SIGNATURES = {
     "hxq_ssm_decode_step": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64,
                             P],
     "hxq_moe_route": [P, I64, I32, I32, I32, P, P, P, P, P, P, P],
+    "hxq_mamba2_conv_split": [P, I32, P, P, P, F32, F32, I64, I64, I64, I64, I64, I64, I64, I64,
+                              P, P, P, I32, P, P, P],
+    "hxq_mamba2_conv_step": [P, I32, P, P, P, F32, F32, I64, I64, I64, I64, I64, I64, I64, P, P,
+                             P, P, I32, P, P],
+    "hxq_gated_rmsnorm": [P, I32, P, I32, I64, P, F32, I64, I64, I64, P, I32, P],
     "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
     "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
 }
@@ -350,3 +356,65 @@ def moe_ffn(x, routing, gate, up, down, out_dtype=None):
                        _ptr(ws), int(nbytes), _ptr(y), dtype_code(y.dtype), _stream(x))
     _check("hxq_moe_ffn", rc)
     return y
+
+
+# ---------------------------------------------------------------------------
+# Mamba2 mixer pieces
+# ---------------------------------------------------------------------------
+def mamba2_conv_split(proj, conv_w, conv_b, dt_bias, dt_min, dt_max, d_mlp, d_inner, ngroups,
+                      state, heads, out_dtype=None, conv_state=None):
+    """proj [b, L, proj_width] -> x [b, L, heads, d_inner/heads], B, C [b, L, G, N], dt [b, L, H]."""
+    b, L, pw = proj.shape
+    width = conv_w.shape[1]
+    od = out_dtype or proj.dtype
+    dev = proj.device
+    x = torch.empty(b, L, heads, d_inner // heads, dtype=od, device=dev)
+    B = torch.empty(b, L, ngroups, state, dtype=od, device=dev)
+    C = torch.empty_like(B)
+    dt = torch.empty(b, L, heads, dtype=torch.float32, device=dev)
+    _need_device(proj, conv_w, conv_b, dt_bias, x, B, C, dt, conv_state)
+    rc = lib().hxq_mamba2_conv_split(_ptr(proj), dtype_code(proj.dtype), _ptr(conv_w),
+                                     _ptr(conv_b), _ptr(dt_bias), float(dt_min), float(dt_max),
+                                     b, L, d_mlp, d_inner, ngroups, state, heads, width, _ptr(x),
+                                     _ptr(B), _ptr(C), dtype_code(od), _ptr(dt),
+                                     _ptr(conv_state), _stream(proj))
+    _check("hxq_mamba2_conv_split", rc)
+    return x, B, C, dt
+
+
+def mamba2_conv_step(proj, conv_state, conv_w, conv_b, dt_bias, dt_min, dt_max, d_mlp, d_inner,
+                     ngroups, state, heads, out_dtype=None):
+    """One token: proj [b, proj_width]; conv_state fp32 [b, conv_dim, width] updated in place."""
+    b, pw = proj.shape
+    width = conv_w.shape[1]
+    od = out_dtype or proj.dtype
+    dev = proj.device
+    x = torch.empty(b, heads, d_inner // heads, dtype=od, device=dev)
+    B = torch.empty(b, ngroups, state, dtype=od, device=dev)
+    C = torch.empty_like(B)
+    dt = torch.empty(b, heads, dtype=torch.float32, device=dev)
+    _need_device(proj, conv_state, conv_w, conv_b, dt_bias, x, B, C, dt)
+    rc = lib().hxq_mamba2_conv_step(_ptr(proj), dtype_code(proj.dtype), _ptr(conv_w),
+                                    _ptr(conv_b), _ptr(dt_bias), float(dt_min), float(dt_max), b,
+                                    d_mlp, d_inner, ngroups, state, heads, width,
+                                    _ptr(conv_state), _ptr(x), _ptr(B), _ptr(C), dtype_code(od),
+                                    _ptr(dt), _stream(proj))
+    _check("hxq_mamba2_conv_step", rc)
+    return x, B, C, dt
+
+
+def gated_rmsnorm(y, gate, weight, eps, group_size=0, out_dtype=None):
+    """y [rows, width]; gate a [rows, width] view whose rows may be strided."""
+    rows, width = y.shape
+    if gate.shape != y.shape or gate.stride(1) != 1:
+        raise RuntimeError("gate must be [rows, width] with unit column stride")
+    out = torch.empty(rows, width, dtype=out_dtype or y.dtype, device=y.device)
+    if not gate.is_cuda:
+        raise RuntimeError("HXQ kernels take device tensors only")
+    _need_device(y, weight, out)
+    rc = lib().hxq_gated_rmsnorm(_ptr(y), dtype_code(y.dtype), ctypes.c_void_p(gate.data_ptr()),
+                                 dtype_code(gate.dtype), gate.stride(0), _ptr(weight), float(eps),
+                                 rows, width, int(group_size), _ptr(out), dtype_code(out.dtype),
+                                 _stream(y))
+    _check("hxq_gated_rmsnorm", rc)
+    return out

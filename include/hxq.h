@@ -212,6 +212,54 @@ int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int64_t hidden
                 int64_t workspace_bytes, void *y, int32_t y_dtype, hipStream_t stream);
 
 /*
+ * Mamba2 mixer around the scan.  in_proj's output row is laid out
+ *   [d_mlp | d_mlp | gate (d_inner) | xBC (d_inner + 2*ngroups*state) | dt (heads)]
+ * (proj_width = 2*d_mlp + 2*d_inner + 2*ngroups*state + heads), as split by
+ * the reference mixer (helix_substrate/mamba_scan_chunked.py:256-261).
+ *
+ * hxq_mamba2_conv_split (prefill): causal depthwise conv1d of width `width`
+ * over xBC with left zero padding, + conv_b, SiLU, split into x [b, L, d_inner]
+ * (= [b, L, heads, d_inner/heads]), B and C [b, L, ngroups, state]
+ * (out_dtype); dt[b, L, heads] = clamp(softplus(dt_raw + dt_bias), dt_min,
+ * dt_max) in fp32.  conv_w fp32 [conv_dim, width]; conv_state (optional, fp32
+ * [b, conv_dim, width]) receives the last `width` raw xBC inputs.
+ * Replaces: mamba_scan_chunked.py:296-310 (conv + act + split) and :356-357
+ *   (dt transform) of _chunked_scan_forward.
+ */
+int hxq_mamba2_conv_split(const void *proj, int32_t proj_dtype, const float *conv_w,
+                          const float *conv_b, const float *dt_bias, float dt_min, float dt_max,
+                          int64_t batch, int64_t seqlen, int64_t d_mlp, int64_t d_inner,
+                          int64_t ngroups, int64_t state, int64_t heads, int64_t width,
+                          void *x, void *B, void *C, int32_t out_dtype, float *dt,
+                          float *conv_state, hipStream_t stream);
+
+/*
+ * hxq_mamba2_conv_step (decode, one token per batch row): conv_state rolls
+ * left by one and takes the new raw xBC input, x/B/C = silu(sum(conv_state *
+ * conv_w) + conv_b) and dt as above.  proj [b, proj_width].
+ * Replaces: mamba_scan_chunked.py:269-282 (single-token conv update).
+ */
+int hxq_mamba2_conv_step(const void *proj, int32_t proj_dtype, const float *conv_w,
+                         const float *conv_b, const float *dt_bias, float dt_min, float dt_max,
+                         int64_t batch, int64_t d_mlp, int64_t d_inner, int64_t ngroups,
+                         int64_t state, int64_t heads, int64_t width, float *conv_state,
+                         void *x, void *B, void *C, int32_t out_dtype, float *dt,
+                         hipStream_t stream);
+
+/*
+ * Gated RMSNorm: h = y * silu(gate); out = weight * h * rsqrt(mean(h^2) + eps)
+ * per row, the mean taken over groups of group_size columns (0 = the whole
+ * row).  y [rows, width]; gate rows are gate_row_stride elements apart (a
+ * column slice of in_proj's output); weight fp32 [width].
+ * Replaces: self.norm(y, gate) (mamba_scan_chunked.py:384; transformers
+ *   MambaRMSNormGated.forward, models/mamba2/modeling_mamba2.py:111-120).
+ */
+int hxq_gated_rmsnorm(const void *y, int32_t y_dtype, const void *gate, int32_t gate_dtype,
+                      int64_t gate_row_stride, const float *weight, float eps, int64_t rows,
+                      int64_t width, int64_t group_size, void *out, int32_t out_dtype,
+                      hipStream_t stream);
+
+/*
  * Selective scan (Mamba/Mamba2), fp32 state, chunk-parallel:
  *   a_t = exp(A[h] dt[b,t,h]);  h_t = a_t h_{t-1} + dt[b,t,h] x[b,t,h,p] B[b,t,g,n]
  *   y[b,t,h,p] = sum_n h_t C[b,t,g,n] + D[h] x[b,t,h,p],  g = h / (heads/ngroups)

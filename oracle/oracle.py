@@ -23,6 +23,9 @@ Reference functions restated (file:line under the reference checkout):
   MoE block (no reference kernel; transformers' OlmoeTopKRouter /
   OlmoeExperts semantics, cited at the functions), composed from
   ``linear_np``.
+* ``conv1d_causal_np`` / ``gated_rmsnorm_np`` / ``mamba2_mixer_np`` -- the
+  Mamba2 mixer around the scan (``mamba_scan_chunked.py:239-387``), composed
+  from ``linear_np`` and ``ssm_scan_f64``.
 * ``ssm_scan_chunked_np`` -- the chunked closed form of the same recurrence
   (the algorithm of ``chunked_scan``, ``mamba_scan_chunked.py:89-213``), written
   in the segment-sum form exp(cumA_t - cumA_s) that cannot overflow; fp64.
@@ -268,3 +271,68 @@ def moe_ffn_np(x, ids, w, Wg, Wu, Wd):
             y = np.zeros((x.shape[0], o.shape[1]))
         np.add.at(y, tok, o * w[tok, slot][:, None])
     return y
+
+
+# ---------------------------------------------------------------------------
+# Mamba2 mixer (benchmark config 3) around the scan: the reference's patched
+# mixer forward _chunked_scan_forward (helix_substrate/mamba_scan_chunked.py:
+# 239-387), prefill from zero state, fp64.
+# ---------------------------------------------------------------------------
+def conv1d_causal_np(x, w, b=None):
+    """Depthwise causal conv1d: x [batch, L, C], w [C, W] -> out[t, c] =
+    b[c] + sum_k w[c, k] * x[t - W + 1 + k, c] (zero before t = 0), i.e.
+    conv1d over left-zero-padded input as in mamba_scan_chunked.py:296-303."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    Bt, L, C = x.shape
+    W = w.shape[1]
+    xp = np.concatenate([np.zeros((Bt, W - 1, C)), x], axis=1)
+    out = np.zeros((Bt, L, C)) if b is None else np.broadcast_to(np.asarray(b, np.float64), (Bt, L, C)).copy()
+    for k in range(W):
+        out += w[:, k] * xp[:, k:k + L, :]
+    return out
+
+
+def silu_np(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def softplus_np(v):
+    """torch.nn.functional.softplus (beta 1, threshold 20)."""
+    v = np.asarray(v, np.float64)
+    return np.where(v > 20.0, v, np.log1p(np.exp(np.minimum(v, 20.0))))
+
+
+def gated_rmsnorm_np(y, gate, weight, eps):
+    """weight * h * rsqrt(mean(h^2) + eps), h = y * silu(gate) (mamba_scan_chunked.py:384;
+    transformers MambaRMSNormGated.forward, models/mamba2/modeling_mamba2.py:111-120)."""
+    h = np.asarray(y, np.float64) * silu_np(np.asarray(gate, np.float64))
+    return np.asarray(weight, np.float64) * h / np.sqrt((h * h).mean(-1, keepdims=True) + eps)
+
+
+def mamba2_mixer_np(hs, Win, Wout, conv_w, conv_b, dt_bias, A_log, D, norm_w, eps, heads,
+                    head_dim, state, ngroups, d_mlp=0, dt_min=0.0, dt_max=np.inf):
+    """Prefill of the Mamba2 mixer: returns (out [b, L, d_model], conv_state
+    [b, conv_dim, W] (last W raw xBC inputs), ssm_state [b, H, P, N])."""
+    hs = np.asarray(hs, np.float64)
+    b, L, _ = hs.shape
+    I = heads * head_dim
+    GN = ngroups * state
+    cd = I + 2 * GN
+    proj = linear_np(hs.reshape(b * L, -1), Win).reshape(b, L, -1)
+    gate = proj[..., 2 * d_mlp:2 * d_mlp + I]
+    xbc = proj[..., 2 * d_mlp + I:2 * d_mlp + I + cd]
+    dt = proj[..., 2 * d_mlp + I + cd:]
+    W = np.asarray(conv_w).shape[1]
+    xa = silu_np(conv1d_causal_np(xbc, conv_w, conv_b))
+    xpad = np.concatenate([np.zeros((b, W - 1, cd)), xbc], axis=1)
+    conv_state = np.transpose(xpad[:, -W:, :], (0, 2, 1))
+    x = xa[..., :I].reshape(b, L, heads, head_dim)
+    B = xa[..., I:I + GN].reshape(b, L, ngroups, state)
+    C = xa[..., I + GN:].reshape(b, L, ngroups, state)
+    dtv = np.clip(softplus_np(dt + np.asarray(dt_bias, np.float64)), dt_min, dt_max)
+    A = -np.exp(np.asarray(A_log, np.float64))
+    y, h = ssm_scan_f64(dtv, A, x, B, C, np.asarray(D, np.float64))
+    z = gated_rmsnorm_np(np.asarray(y).reshape(b, L, I), gate, norm_w, eps)
+    out = linear_np(z.reshape(b * L, I), Wout).reshape(b, L, -1)
+    return out, conv_state, h
