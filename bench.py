@@ -44,7 +44,9 @@ def parse():
     ap.add_argument("--prefill", type=int, default=1,
                     help="also time the config-2 prefill GEMMs (Qwen2.5-7B shapes, M=2048)")
     ap.add_argument("--scan", type=int, default=1,
-                    help="also time the config-3 Mamba2 selective scan")
+                    help="also time the config-3 Mamba2 selective scan and mixer layer")
+    ap.add_argument("--moe", type=int, default=1,
+                    help="also time the config-4 OLMoE-shaped MoE FFN (16 layers)")
     return ap.parse_args()
 
 
@@ -237,6 +239,9 @@ def main():
         result["prefill_config2"] = prefill_bench(dev)
     if args.scan:
         result["scan_config3"] = scan_bench(dev, cpu=args.cpu_seconds > 0)
+        result["mixer_config3"] = mixer_bench(dev)
+    if args.moe:
+        result["moe_config4"] = moe_bench(dev, cpu=args.cpu_seconds > 0)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -356,6 +361,140 @@ def scan_bench(dev, iters=5, cpu=True):
                                "sample": f"reference sequential_scan restated (torch CPU), "
                                          f"L={Ls} of 2048, {torch.get_num_threads()} threads",
                                "kind": "port", "cores": torch.get_num_threads()}
+    return out
+
+
+def mixer_bench(dev, iters=5):
+    """Config 3 end to end: one Mamba2-1.3B-shaped mixer layer (HXQ in_proj
+    8512x2048 and out_proj 2048x4096 per the config-0 recipe) on b=8, L=2048
+    bf16 tokens: in_proj GEMM, conv/split, chunked scan, gated RMSNorm,
+    out_proj GEMM.  Reports tokens/s of the layer and a per-stage split."""
+    import torch
+    from helix_substrate import _hxq, synth
+    from helix_substrate.helix_linear import HelixLinear
+    from helix_substrate.mamba2_mixer import HelixMamba2Mixer, mamba2_13b_dims, random_mixer_params
+
+    d = mamba2_13b_dims()
+    H, P, N, G, W, dm = d["num_heads"], d["head_dim"], d["ssm_state_size"], d["n_groups"], \
+        d["conv_width"], d["d_model"]
+    I = H * P
+    pw = 2 * I + 2 * G * N + H
+
+    def hl(o, i, seed):
+        L = synth.make_layer_torch(o, i, seed=seed, device=dev)
+        return HelixLinear(i, o, L["codebook"], L["indices"], L["sidecar_positions"],
+                           L["sidecar_values"], group_scale=L["group_scale"],
+                           group_offset=L["group_offset"], group_size=128)
+
+    p = random_mixer_params(dm, H, P, N, G, W, seed=0, device=dev)
+    m = HelixMamba2Mixer(hl(pw, dm, 7001), hl(dm, I, 7002), p["conv_weight"], p["conv_bias"],
+                         p["dt_bias"], p["A_log"], p["D"], p["norm_weight"], num_heads=H,
+                         head_dim=P, ssm_state_size=N, n_groups=G, eps=1e-5, time_step_min=1e-3)
+    b, L = 8, 2048
+    hs = torch.randn(b, L, dm, device=dev).to(torch.bfloat16)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+    for _ in range(2):
+        out = m(hs)
+    torch.cuda.synchronize(dev)
+    ev[0].record()
+    for _ in range(iters):
+        out = m(hs)
+    ev[1].record()
+    torch.cuda.synchronize(dev)
+    ms = ev[0].elapsed_time(ev[1]) / iters
+    # stage split (one pass, events between stages)
+    ev[0].record()
+    proj = m.in_proj(hs)
+    ev[1].record()
+    x, Bm, Cm, dt = _hxq.mamba2_conv_split(proj, m.conv_weight, m.conv_bias, m.dt_bias, 1e-3,
+                                           float("inf"), 0, I, G, N, H)
+    ev[2].record()
+    y, _ = _hxq.ssm_chunk_scan(x, dt, -torch.exp(m.A_log), Bm, Cm, m.D, None, chunk=256,
+                               want_final=False)
+    ev[3].record()
+    z = _hxq.gated_rmsnorm(y.view(b * L, -1), proj.view(b * L, -1)[:, :I], m.norm_weight, 1e-5,
+                           out_dtype=torch.bfloat16)
+    ev[4].record()
+    m.out_proj(z)
+    ev[5].record()
+    torch.cuda.synchronize(dev)
+    names = ["in_proj_gemm", "conv_split", "scan", "gated_rmsnorm", "out_proj_gemm"]
+    split = {n: round(ev[i].elapsed_time(ev[i + 1]), 4) for i, n in enumerate(names)}
+    flops = 2.0 * b * L * (pw * dm + dm * I)
+    return {"shape": {"batch": b, "seqlen": L, "d_model": dm, "d_inner": I, "heads": H,
+                      "state": N, "in_proj": [pw, dm], "out_proj": [dm, I]},
+            "ms_per_layer": round(ms, 4), "tokens_per_s": round(b * L / ms * 1e3, 1),
+            "stage_ms": split, "proj_gemm_tflops": round(
+                flops / (split["in_proj_gemm"] + split["out_proj_gemm"]) / 1e9, 1)}
+
+
+def moe_bench(dev, n_layers=16, iters=3, cpu=True):
+    """Config 4: OLMoE-shaped MoE FFN, 16 layers of 64 HXQ experts (SwiGLU 1024,
+    hidden 2048), top-8 of softmax(N(0,1) logits), 512 bf16 tokens.  One step =
+    route + grouped FFN for every layer (6.9 GB of expert weights, streamed)."""
+    import torch
+    from helix_substrate import _hxq, moe, synth
+
+    T, E, k, Hd, I = 512, 64, 8, 2048, 1024
+    layers = []
+    for li in range(n_layers):
+        mk = lambda o, i, s: [synth.make_layer_torch(o, i, seed=s + e, device=dev) for e in range(E)]
+        g = moe.stack_bank(mk(I, Hd, 20000 + 1000 * li), dev)
+        u = moe.stack_bank(mk(I, Hd, 40000 + 1000 * li), dev)
+        dn = moe.stack_bank(mk(Hd, I, 60000 + 1000 * li), dev)
+        layers.append((g, u, dn))
+        torch.cuda.empty_cache()
+    x = torch.randn(T, Hd, device=dev).to(torch.bfloat16)
+    logits = [moe.olmoe_router_logits(T, E, seed=li, device=dev) for li in range(n_layers)]
+
+    def step():
+        for li, (g, u, dn) in enumerate(layers):
+            r = _hxq.moe_route(logits[li], k)
+            _hxq.moe_ffn(x, r, g, u, dn)
+        return r
+
+    r = step()
+    torch.cuda.synchronize(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(iters):
+        step()
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    ms = ev0.elapsed_time(ev1) / iters
+    touched = int((r.expert_counts > 0).sum())
+    per_expert = 3 * (I * Hd + I * Hd // 128 * 8 + int(round(0.001 * I * Hd)) * 8) + \
+        4 * (2 * (I + 1) + Hd + 1) + 3 * 1024
+    wbytes = touched * per_expert
+    act_bytes = T * Hd * 2 * 2
+    flops = 2.0 * T * k * 3 * I * Hd
+    counts = r.expert_counts.cpu()
+    out = {"shape": {"tokens": T, "experts": E, "top_k": k, "hidden": Hd, "intermediate": I,
+                     "layers": n_layers},
+           "ms_per_layer": round(ms / n_layers, 4), "ms_all_layers": round(ms, 4),
+           "tokens_per_s_per_layer": round(T / (ms / n_layers) * 1e3, 1),
+           "touched_experts": touched, "bytes_per_layer": wbytes + act_bytes,
+           "gbs": round((wbytes + act_bytes) / (ms / n_layers) / 1e6, 1),
+           "frac_of_hbm_peak": round((wbytes + act_bytes) / (ms / n_layers) / 1e6 / 8000.0, 4),
+           "tflops": round(flops / (ms / n_layers) / 1e9, 1),
+           "expert_load_min_max": [int(counts.min()), int(counts.max())]}
+    if cpu:
+        # reference-style CPU path (per-expert loop of fp32 torch math, the
+        # HelixLinear CPU semantics) on layer 0 with all 512 tokens
+        import time as _t
+
+        g, u, dn = [moe.bank_to(b_, "cpu") for b_ in layers[0]]
+        mm = moe.HelixMoeExperts(g, u, dn, top_k=k)
+        xs, ls = x.float().cpu(), logits[0].cpu()
+        t0 = _t.perf_counter()
+        mm(xs, ls)
+        el = _t.perf_counter() - t0
+        out["cpu_baseline"] = {"ms_per_layer": round(el * 1e3, 1),
+                               "sample": "layer 0, all 512 tokens, per-expert torch CPU loop",
+                               "kind": "port", "cores": torch.get_num_threads()}
+    del layers
+    torch.cuda.empty_cache()
     return out
 
 

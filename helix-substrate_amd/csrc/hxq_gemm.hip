@@ -8,18 +8,22 @@
 // bias) and the default _forward_buffered materialise-then-BLAS path
 // (helix_linear.py:556-634).
 //
-// Block: 512 threads = 8 waves in a 2 (M) x 4 (N) layout; block tile BM x 256
-// (BM = 64/128/256), K-step 64.  Each wave owns a (BM/2) x 64 sub-tile, i.e.
-// (BM/64) x 2 MFMA 32x32 tiles.
-// Per K-step, double-buffered in LDS (one barrier per step):
-//   * X tile [BM, 64] (16-bit) -> LDS, rows XOR-swizzled in 16-byte chunks so
-//     the MFMA operand reads (8 lanes x 16 B per row group) hit all banks;
-//   * index tile [256, 64] (u8) -> codebook lookup (LDS, 32 replicas; 16 in
-//     pair mode) ->
-//     fma(cb, scale, offset) -> v_cvt_pk_bf16_f32 -> LDS; sidecar entries then
-//     REPLACE their element (the block's CSR entries are staged in LDS once;
-//     each of the two threads of a row walks its row's entries);
-//   * global loads run two steps ahead of the LDS writes.
+// Block: 768 threads = 12 waves, block tile BM x 256 (BM = 64 or 128), K-step
+// 64, split by role.  Waves 0-3 consume: each owns BM x 64 outputs
+// ((BM/32) x 2 MFMA 32x32 tiles) and only issues MFMAs on LDS operands.
+// Waves 4-11 produce: per K-step they copy the X tile (16-bit) into LDS, rows
+// XOR-swizzled in 16-byte chunks so the MFMA operand reads (8 lanes x 16 B
+// per row group) hit all banks, and build the W tile: thread t owns 16
+// columns of 2 W rows and
+//   * turns its 64 indices into weights: codebook lookup (LDS, 32 replicas;
+//     16 in pair mode) -> fma(cb, scale, offset) -> v_cvt_pk_bf16_f32 ->
+//     LDS, then REPLACES sidecar entries of the step (the block's CSR
+//     entries are staged in LDS once);
+//   * issues the global loads two steps ahead.
+// The hardware places wave w on SIMD w % 4, so each SIMD runs one consumer
+// and two producers: dequantisation (VALU, LDS lookups, whose latency two
+// producer waves hide) overlaps the MFMAs.  LDS is double-buffered with one
+// barrier per step.
 // Results are written once per output element: deterministic.
 //
 // Grouped mode (MoE): `seg` holds the expert segments [E+1] of a sorted
@@ -42,7 +46,11 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmThreads = 512;
+constexpr int kConsumers = 4;                   // MFMA waves
+constexpr int kProducers = 8;                   // dequantising waves
+constexpr int kGemmThreads = (kConsumers + kProducers) * 64;
+constexpr int kPT = kProducers * 64;            // producer threads
+constexpr int kPRows = 256 / (kPT / 4);         // W rows per producer thread (2)
 constexpr int kBK = 64;        // K per step
 constexpr int kBN = 256;       // tile rows of W (output features) per block
 constexpr int kScCap = 8192;   // sidecar entries staged in LDS per block
@@ -52,8 +60,7 @@ constexpr int kScCap = 8192;   // sidecar entries staged in LDS per block
 struct WSet {
     const uint8_t *idx;   // [E, OUT, K]
     const float *cb;      // [E, 256]
-    const float *gs;      // [E, OUT, K/G] or null
-    const float *go;
+    const float *ga;      // [E, K/G, OUT, 2] {scale, offset} or null
     const int32_t *rp;    // [E, OUT+1] absolute offsets into col/val, or null
     const int32_t *col;
     const float *val;     // replacement values
@@ -83,21 +90,23 @@ __device__ __forceinline__ uint16_t to16(float v) {
 // Element offset of 16-byte chunk `c` (0..7) of LDS row `r` (64 elements).
 __device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ (r & 7)) << 3); }
 
-// Global data of one K-step, held in registers until written to LDS.
+// Global data of one K-step for one producer thread, held in registers until
+// written to LDS.  Producer thread t owns W rows (t/4) + 128i (i = 0, 1), 16
+// indices each (columns 16*(t%4) .. +16 of the step): four lanes cover one
+// row's 64 bytes, so a load instruction touches 16 rows, not 64.
 template <int BM>
 struct GemmStage {
-    u32x4 a[BM / 64];   // X: thread t holds chunk t%8 of rows t/8 + 64p
-    u32x4 q[2];         // 32 index bytes of this thread's W row
-    float s, o;         // affine factors of that row's group
+    u32x4 q[kPRows];              // 16 indices of each of the thread's W rows
+    float2 so[1];                 // {scale, offset} of row qc's group (shared in the quad)
+    u32x4 a[BM * 8 / kPT];        // X: chunk t%8 of rows t/8 + (kPT/8) p
 };
 
 template <int BM, bool BF16, bool AFFINE, bool GROUPED, bool PAIR>
-__global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g) {
     static_assert(!PAIR || GROUPED, "pair mode is a grouped-GEMM epilogue");
-    static_assert(!PAIR || BM <= 128, "LDS budget");
-    constexpr int WM = BM / 2;       // wave tile rows (M)
-    constexpr int TM = WM / 32;      // MFMA tiles per wave along M
-    constexpr int TN = 2;            // ... along N (64 columns per wave)
+    static_assert(BM == 64 || BM == 128, "row tile");
+    constexpr int TM = BM / 32;      // consumer wave tile BM x 64: TM x TN MFMA tiles
+    constexpr int TN = 2;
     constexpr int NT = PAIR ? 2 : 1; // codebook tables
     // Codebook replicas: 32 per table keep lookups bank-conflict-free (the two
     // half-waves use the same 32 banks in different cycles); a SwiGLU pair
@@ -120,7 +129,13 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int wm = wave / 4, wn = wave % 4;
+    // Waves 0-3 consume (MFMA on the staged tiles), waves 4-11 produce (load,
+    // dequantise, write LDS); the hardware places wave w on SIMD w % 4, so
+    // every SIMD runs one consumer next to two producers and their VALU and
+    // MFMA work overlap.
+    const bool producer = wave >= kConsumers;
+    const int cw = wave & 3;               // consumer: 64-column block of the tile
+    const int pt = tid - kConsumers * 64;  // producer thread 0..kPT-1
     const int K = g.K;
     const int nk = K / kBK;
 
@@ -168,37 +183,21 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
         }
         __syncthreads();
         e = s_tile[0];
-        if (e < 0) return;  // block-uniform: no tile for this block index
         r0 = s_tile[1];
         r1 = s_tile[2];
+        __syncthreads();  // s_tile lives in sA: everyone has read it
+        if (e < 0) return;  // block-uniform: no tile for this block index
     } else {
         r0 = blockIdx.y * BM;
         r1 = min(r0 + BM, g.M);
     }
-
-    // ---- W row of this thread: b_row = tid / 2, half = tid % 2 ------------
-    const int b_row = tid >> 1, b_half = tid & 1;
-    const int part = PAIR ? (b_row >> 7) : 0;
-    const int n0 = blockIdx.x * (PAIR ? kBN / 2 : kBN);
-    const int grow = n0 + (PAIR ? (b_row & 127) : b_row);  // row of matrix `part`
-    const bool row_ok = grow < g.OUT;
-    const int ngroups = AFFINE ? K / g.group : 1;
-    // field-wise select keeps the kernel-argument struct out of scratch
-    WSet ws;
-    ws.idx = part ? g.w[1].idx : g.w[0].idx;
-    ws.gs = part ? g.w[1].gs : g.w[0].gs;
-    ws.go = part ? g.w[1].go : g.w[0].go;
-    ws.rp = part ? g.w[1].rp : g.w[0].rp;
-    ws.col = part ? g.w[1].col : g.w[0].col;
-    ws.val = part ? g.w[1].val : g.w[0].val;
     const int64_t eo = static_cast<int64_t>(e);
-    const uint8_t *idx_e = ws.idx + eo * g.OUT * K;
-    const float *gs_e = AFFINE ? ws.gs + eo * g.OUT * ngroups : nullptr;
-    const float *go_e = AFFINE ? ws.go + eo * g.OUT * ngroups : nullptr;
+    const int n0 = blockIdx.x * (PAIR ? kBN / 2 : kBN);
+    const int ngroups = AFFINE ? K / g.group : 1;
 
     // codebook replicas: entry j at [j * NREP + r]; thread t fills entry t/2
     // of each table, NREP/2 replicas
-    {
+    if (tid < 512) {
         const int j = tid >> 1;
 #pragma unroll
         for (int p = 0; p < NT; ++p) {
@@ -209,56 +208,11 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
         }
     }
 
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.x_rows * K * 2);
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(idx_e, (int64_t)g.OUT * K);
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(gs_e, AFFINE ? (int64_t)g.OUT * ngroups * 4 : 0);
-    const __amdgpu_buffer_rsrc_t orr = make_rsrc(go_e, AFFINE ? (int64_t)g.OUT * ngroups * 4 : 0);
-    constexpr uint32_t kOob = 0x80000000u;
-
-    // X rows of this thread (fixed for the block)
-    const int a_cc = tid & 7;
-    uint32_t a_off[BM / 64];
-#pragma unroll
-    for (int p = 0; p < BM / 64; ++p) {
-        const int r = r0 + (tid >> 3) + 64 * p;
-        int src = r;
-        if constexpr (GROUPED) {
-            if (r < r1 && g.rows) src = g.rows[r];
-        }
-        a_off[p] = (r < r1 && src >= 0 && src < g.x_rows)
-                       ? (uint32_t)(src * K + a_cc * 8) * 2u : kOob;
-    }
-    const uint32_t q_base = row_ok ? (uint32_t)(grow * K + b_half * 32) : kOob;
-    const uint32_t so_base = row_ok ? (uint32_t)(grow * ngroups) * 4u : kOob;
-
-    // Loads are issued unconditionally (steps past the end read at kOob, which
-    // the buffer range check turns into zeros without memory traffic): a
-    // conditional prefetch would make the compiler's wait counting assume the
-    // prefetch absent and wait for it at the next use of the older stage.
-    auto load_stage = [&](int ks, GemmStage<BM> &st) {
-        const bool live = ks < nk;
-        const uint32_t k0 = (live ? ks : 0) * kBK;
-#pragma unroll
-        for (int p = 0; p < BM / 64; ++p)
-            st.a[p] = buf_load16(xr, (a_off[p] == kOob || !live) ? kOob : a_off[p] + k0 * 2);
-        const uint32_t qo = (q_base == kOob || !live) ? kOob : q_base + k0;
-        st.q[0] = buf_load16(qr, qo);
-        st.q[1] = buf_load16(qr, qo == kOob ? kOob : qo + 16);
-        if constexpr (AFFINE) {
-            const uint32_t so = (so_base == kOob || !live) ? kOob : so_base + (k0 / g.group) * 4;
-            st.s = buf_loadf(sr, so);
-            st.o = buf_loadf(orr, so);
-        } else {
-            st.s = 1.f;
-            st.o = 0.f;
-        }
-    };
-
     // ---- sidecar: the block's CSR entries (per part a contiguous range) ----
-    // Staged into LDS as {col, 16-bit value} so the per-step cursor reads LDS
-    // and never waits on global loads behind the prefetched stages.  A block
-    // with more than kScCap entries (or K > 65535) reads them from global
-    // memory instead (same results, slower).
+    // Staged into LDS as {col, 16-bit value} so the producers' per-step cursor
+    // reads LDS and never waits on global loads behind the prefetched stages.
+    // A block with more than kScCap entries (or K > 65535) reads them from
+    // global memory instead (same results, slower).
     constexpr int RPP = PAIR ? kBN / 2 : kBN;  // rows per part
     int sc_lo[NT], sc_base[NT], sc_total = 0;
 #pragma unroll
@@ -272,17 +226,6 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
         }
     }
     const bool sc_in_lds = sc_total <= kScCap && K <= 0xffff;
-    int32_t sc_cur = 0, sc_end = 0;
-    if (ws.rp != nullptr && row_ok) {
-        const int32_t *rp = ws.rp + eo * (g.OUT + 1);
-        sc_cur = rp[grow];
-        sc_end = rp[grow + 1];
-        if (sc_in_lds) {
-            const int shift = (part ? sc_base[NT - 1] - sc_lo[NT - 1] : sc_base[0] - sc_lo[0]);
-            sc_cur += shift;
-            sc_end += shift;
-        }
-    }
     if (sc_in_lds) {
         for (int i = tid; i < sc_total; i += kGemmThreads) {
             const int p = (NT == 2 && i >= sc_base[NT - 1]) ? 1 : 0;
@@ -293,66 +236,197 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
         }
     }
 
-    // lookup of byte b of index word w in this thread's table
-    const uint32_t lane_off = (lane & (NREP - 1)) * 4u;
-    const char *tb = reinterpret_cast<const char *>(&tbl[part][0]);
-    auto lookup = [&](uint32_t w, int b) -> float {
-        constexpr int kShift = NREP == 32 ? 7 : 6;  // log2(NREP * 4)
-        return *reinterpret_cast<const float *>(tb + lane_off + (((w >> (8 * b)) & 0xffu) << kShift));
-    };
+    // ---- producers: load two steps ahead, fill the LDS buffer the consumers
+    // read next; one barrier per step (the consumers' loop below hits the
+    // same barriers) -------------------------------------------------------
+    if (producer) {
+        // ---- producer state: W rows (pt/4) + 64i, X chunk pt % 8 ----------------
+        const int qc = pt & 3;                  // 16-index chunk of the step
+        const int qr0 = pt >> 2;                // first W row of this thread (tile row)
+        // rows qr0 + 128i; in pair mode rows 0..127 come from matrix 0 (gate) and
+        // 128..255 from matrix 1 (up): part = i
+        auto tile_row = [&](int i) { return qr0 + 128 * i; };
+        auto mat_row = [&](int i) { return n0 + (PAIR ? (tile_row(i) & 127) : tile_row(i)); };
+        auto part_of = [&](int i) { return PAIR ? i : 0; };
 
-    auto write_stage = [&](int ks, const GemmStage<BM> &st, int buf, auto sc_lds) {
-        constexpr bool SC_LDS = decltype(sc_lds)::value;
-#pragma unroll
-        for (int p = 0; p < BM / 64; ++p)
-            *reinterpret_cast<u32x4 *>(&sA[buf][swz((tid >> 3) + 64 * p, a_cc)]) = st.a[p];
-        // 32 indices -> 4 chunks of 8 16-bit weights (chunks 4*half .. 4*half+3)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                uint32_t pk[4];
-#pragma unroll
-                for (int dd = 0; dd < 2; ++dd) {
-                    const uint32_t w = st.q[h][cc * 2 + dd];
-                    float v[4];
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const float c = lookup(w, b);
-                        v[b] = AFFINE ? fmaf(c, st.s, st.o) : c;
-                    }
-                    pk[dd * 2] = pack2<BF16>(v[0], v[1]);
-                    pk[dd * 2 + 1] = pack2<BF16>(v[2], v[3]);
-                }
-                *reinterpret_cast<u32x4 *>(&sB[buf][swz(b_row, b_half * 4 + h * 2 + cc)]) =
-                    u32x4{pk[0], pk[1], pk[2], pk[3]};
+        constexpr uint32_t kOob = 0x80000000u;
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.x_rows * K * 2);
+        __amdgpu_buffer_rsrc_t qr[NT];
+    #pragma unroll
+        for (int p = 0; p < NT; ++p) qr[p] = make_rsrc(g.w[p].idx + eo * g.OUT * K, (int64_t)g.OUT * K);
+
+        // X: producer thread pt copies chunk pt % 8 of rows pt/8 + (kPT/8) p
+        constexpr int kXP = BM * 8 / kPT;
+        const int a_cc = pt & 7;
+        uint32_t a_off[kXP];
+    #pragma unroll
+        for (int p = 0; p < kXP; ++p) {
+            const int r = r0 + (pt >> 3) + (kPT / 8) * p;
+            int src = r;
+            if constexpr (GROUPED) {
+                if (producer && r < r1 && g.rows) src = g.rows[r];
             }
-        // sidecar: replace entries with column in [lo, lo + 32)
-        const int lo = ks * kBK + b_half * 32, hi = lo + 32;
-        uint16_t *row = &sB[buf][0];
-        if constexpr (SC_LDS) {
-            while (sc_cur < sc_end) {
-                const uint32_t ent = sSc[sc_cur];
-                const int col = static_cast<int>(ent & 0xffffu);
-                if (col >= hi) break;
-                if (col >= lo) {
-                    const int kc = col - ks * kBK;
-                    row[swz(b_row, kc >> 3) + (kc & 7)] = static_cast<uint16_t>(ent >> 16);
+            a_off[p] = (producer && r < r1 && src >= 0 && src < g.x_rows)
+                           ? (uint32_t)(src * K + a_cc * 8) * 2u : kOob;
+        }
+        uint32_t q_off[kPRows];
+    #pragma unroll
+        for (int i = 0; i < kPRows; ++i) {
+            const bool ok = producer && mat_row(i) < g.OUT;
+            q_off[i] = ok ? (uint32_t)(mat_row(i) * K + qc * 16) : kOob;
+        }
+        // affine factors: this lane fetches those of its row qc (see load_stage)
+        const float *ga_mine = nullptr;
+        if constexpr (AFFINE) {
+            const int ri = qc & (kPRows - 1);
+            ga_mine = ((PAIR && ri == 1) ? g.w[NT - 1].ga : g.w[0].ga) + eo * ngroups * g.OUT * 2 +
+                      (int64_t)(mat_row(ri) < g.OUT ? mat_row(ri) : 0) * 2;
+        }
+
+        // sidecar cursors of the thread's 4 rows (each covers its 16 columns);
+        // sc_nc holds the column of the next entry (or a sentinel past any K), so
+        // a step without entries costs one register compare per row
+        int32_t sc_cur[kPRows], sc_end[kPRows], sc_nc[kPRows];
+    #pragma unroll
+        for (int i = 0; i < kPRows; ++i) {
+            sc_cur[i] = 0;
+            sc_end[i] = 0;
+            const int p = part_of(i);
+            const int32_t *rpb = p ? g.w[NT - 1].rp : g.w[0].rp;
+            if (rpb != nullptr && producer && mat_row(i) < g.OUT) {
+                const int32_t *rp = rpb + eo * (g.OUT + 1);
+                sc_cur[i] = rp[mat_row(i)];
+                sc_end[i] = rp[mat_row(i) + 1];
+                if (sc_in_lds) {
+                    const int shift = sc_base[p] - sc_lo[p];
+                    sc_cur[i] += shift;
+                    sc_end[i] += shift;
                 }
-                ++sc_cur;
-            }
-        } else {
-            while (sc_cur < sc_end) {
-                const int col = ws.col[sc_cur];
-                if (col >= hi) break;
-                if (col >= lo) {
-                    const int kc = col - ks * kBK;
-                    row[swz(b_row, kc >> 3) + (kc & 7)] = to16<BF16>(ws.val[sc_cur]);
-                }
-                ++sc_cur;
             }
         }
-    };
+        auto sc_col_of = [&](int i, int j) -> int32_t {
+            if (sc_in_lds) return static_cast<int32_t>(sSc[j] & 0xffffu);
+            return part_of(i) ? g.w[NT - 1].col[j] : g.w[0].col[j];
+        };
+
+        // Loads are issued unconditionally (steps past the end read at kOob, which
+        // the buffer range check turns into zeros without memory traffic): a
+        // conditional prefetch would make the compiler's wait counting assume the
+        // prefetch absent and wait for it at the next use of the older stage.
+        auto load_stage = [&](int ks, GemmStage<BM> &st) {
+            const bool live = ks < nk;
+            const uint32_t k0 = (live ? ks : 0) * kBK;
+    #pragma unroll
+            for (int p = 0; p < kXP; ++p)
+                st.a[p] = buf_load16(xr, (a_off[p] == kOob || !live) ? kOob : a_off[p] + k0 * 2);
+    #pragma unroll
+            for (int i = 0; i < kPRows; ++i)
+                st.q[i] = buf_load16(qr[part_of(i)], (q_off[i] == kOob || !live) ? kOob : q_off[i] + k0);
+            if constexpr (AFFINE) {
+                // the 4 lanes of a quad share their 4 rows: lane qc loads row qc's
+                // factors, a quad broadcast (DPP) hands them to the others
+                // (always a valid address: rows past OUT read row 0, whose value
+                // only reaches outputs the epilogue drops)
+                st.so[0] = *reinterpret_cast<const float2 *>(ga_mine + (int64_t)(k0 / g.group) * g.OUT * 2);
+            } else {
+                st.so[0] = make_float2(1.f, 0.f);
+            }
+        };
+
+        // row i's factors from quad lane i (DPP quad_perm [i,i,i,i])
+        auto quad_bcast = [&](float2 v, float2 (&out)[kPRows]) {
+            if constexpr (AFFINE) {
+                const int x = __float_as_int(v.x), y = __float_as_int(v.y);
+                out[0] = make_float2(__int_as_float(__builtin_amdgcn_mov_dpp(x, 0x00, 0xf, 0xf, false)),
+                                     __int_as_float(__builtin_amdgcn_mov_dpp(y, 0x00, 0xf, 0xf, false)));
+                out[1] = make_float2(__int_as_float(__builtin_amdgcn_mov_dpp(x, 0x55, 0xf, 0xf, false)),
+                                     __int_as_float(__builtin_amdgcn_mov_dpp(y, 0x55, 0xf, 0xf, false)));
+            } else {
+    #pragma unroll
+                for (int i = 0; i < kPRows; ++i) out[i] = make_float2(1.f, 0.f);
+            }
+        };
+        const uint32_t lane_off = (lane & (NREP - 1)) * 4u;
+        auto lookup = [&](int p, uint32_t w, int b) -> float {
+            constexpr int kShift = NREP == 32 ? 7 : 6;  // log2(NREP * 4)
+            const char *tb = reinterpret_cast<const char *>(&tbl[p][0]);
+            return *reinterpret_cast<const float *>(tb + lane_off + (((w >> (8 * b)) & 0xffu) << kShift));
+        };
+
+        auto write_stage = [&](int ks, const GemmStage<BM> &st, int buf, auto sc_lds) {
+            constexpr bool SC_LDS = decltype(sc_lds)::value;
+    #pragma unroll
+            for (int p = 0; p < kXP; ++p)
+                *reinterpret_cast<u32x4 *>(&sA[buf][swz((pt >> 3) + (kPT / 8) * p, a_cc)]) = st.a[p];
+            float2 so[kPRows];
+            quad_bcast(st.so[0], so);
+            // each row: 16 indices -> 2 chunks of 8 16-bit weights
+    #pragma unroll
+            for (int i = 0; i < kPRows; ++i)
+    #pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t pk[4];
+    #pragma unroll
+                    for (int dd = 0; dd < 2; ++dd) {
+                        const uint32_t w = st.q[i][h * 2 + dd];
+                        float v[4];
+    #pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            const float c = lookup(part_of(i), w, b);
+                            v[b] = AFFINE ? fmaf(c, so[i].x, so[i].y) : c;
+                        }
+                        pk[dd * 2] = pack2<BF16>(v[0], v[1]);
+                        pk[dd * 2 + 1] = pack2<BF16>(v[2], v[3]);
+                    }
+                    *reinterpret_cast<u32x4 *>(&sB[buf][swz(tile_row(i), qc * 2 + h)]) =
+                        u32x4{pk[0], pk[1], pk[2], pk[3]};
+                }
+            // sidecar: replace entries with column in this thread's [lo, lo + 16)
+            const int k0 = ks * kBK, lo = k0 + qc * 16, hi = lo + 16;
+            uint16_t *brow = &sB[buf][0];
+    #pragma unroll
+            for (int i = 0; i < kPRows; ++i) {
+                while (sc_nc[i] < hi) {
+                    const int j = sc_cur[i];
+                    if (sc_nc[i] >= lo) {
+                        const int kc = sc_nc[i] - k0;
+                        uint16_t v16;
+                        if constexpr (SC_LDS) v16 = static_cast<uint16_t>(sSc[j] >> 16);
+                        else v16 = to16<BF16>(part_of(i) ? g.w[NT - 1].val[j] : g.w[0].val[j]);
+                        brow[swz(tile_row(i), kc >> 3) + (kc & 7)] = v16;
+                    }
+                    sc_cur[i] = j + 1;
+                    sc_nc[i] = j + 1 < sc_end[i] ? sc_col_of(i, j + 1) : 0x7fffffff;
+                }
+            }
+        };
+
+        auto run = [&](auto sc_lds) {
+            GemmStage<BM> s0, s1;
+            load_stage(0, s0);
+            load_stage(1, s1);
+            __syncthreads();  // codebook tables and staged sidecar visible
+#pragma unroll
+            for (int i = 0; i < kPRows; ++i)
+                sc_nc[i] = sc_cur[i] < sc_end[i] ? sc_col_of(i, sc_cur[i]) : 0x7fffffff;
+            write_stage(0, s0, 0, sc_lds);
+            lds_barrier();
+            int ks = 0;
+            for (; ks + 1 < nk; ks += 2) {
+                load_stage(ks + 2, s0);
+                write_stage(ks + 1, s1, 1, sc_lds);
+                lds_barrier();
+                load_stage(ks + 3, s1);
+                if (ks + 2 < nk) write_stage(ks + 2, s0, 0, sc_lds);
+                lds_barrier();
+            }
+            if (ks < nk) lds_barrier();  // odd step count: the consumers' last step
+        };
+        if (sc_in_lds) run(std::true_type{});
+        else run(std::false_type{});
+        if constexpr (PAIR) __syncthreads();  // the consumers' gate/up hand-over
+        return;
+    }
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -362,68 +436,62 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // consumer: one K-step of MFMAs on LDS buffer `buf` (k permuted within the
+    // step identically for X and W: lane half h takes chunks 2kk + h)
     auto mfma_step = [&](int buf) {
         const int hsel = lane >> 5;
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
-            u32x4 av[TM], bv[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                av[i] = *reinterpret_cast<const u32x4 *>(
-                    &sA[buf][swz(wm * WM + i * 32 + (lane & 31), kk * 2 + hsel)]);
+            u32x4 bv[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 bv[j] = *reinterpret_cast<const u32x4 *>(
-                    &sB[buf][swz(wn * 64 + j * 32 + (lane & 31), kk * 2 + hsel)]);
+                    &sB[buf][swz(cw * 64 + j * 32 + (lane & 31), kk * 2 + hsel)]);
+            // one X operand at a time keeps the live operand registers at 3 x 4
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i) {
+                const u32x4 av = *reinterpret_cast<const u32x4 *>(
+                    &sA[buf][swz(i * 32 + (lane & 31), kk * 2 + hsel)]);
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     if constexpr (BF16)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            __builtin_bit_cast(bf16x8, av[i]), __builtin_bit_cast(bf16x8, bv[j]),
+                            __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv[j]),
                             acc[i][j], 0, 0, 0);
                     else
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            __builtin_bit_cast(f16x8, av[i]), __builtin_bit_cast(f16x8, bv[j]),
+                            __builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv[j]),
                             acc[i][j], 0, 0, 0);
                 }
+            }
         }
     };
 
-    // ---- main loop: loads two steps ahead, LDS double buffer -------------
-    auto main_loop = [&](auto sc_lds) {
-        GemmStage<BM> s0, s1;
-        load_stage(0, s0);
-        load_stage(1, s1);
-        __syncthreads();  // codebook tables and staged sidecar visible
-        write_stage(0, s0, 0, sc_lds);
+    // ---- consumers: MFMAs on the current buffer --------------------------------
+    __syncthreads();
+    lds_barrier();
+    int ks = 0;
+    for (; ks + 1 < nk; ks += 2) {
+        mfma_step(0);
         lds_barrier();
-        for (int ks = 0; ks < nk; ks += 2) {
-            load_stage(ks + 2, s0);
-            mfma_step(0);
-            if (ks + 1 < nk) write_stage(ks + 1, s1, 1, sc_lds);
-            lds_barrier();
-            if (ks + 1 >= nk) break;
-            load_stage(ks + 3, s1);
-            mfma_step(1);
-            if (ks + 2 < nk) write_stage(ks + 2, s0, 0, sc_lds);
-            lds_barrier();
-        }
-    };
-    if (sc_in_lds) main_loop(std::true_type{});
-    else main_loop(std::false_type{});
+        mfma_step(1);
+        lds_barrier();
+    }
+    if (ks < nk) {
+        mfma_step(0);
+        lds_barrier();
+    }
 
-    // ---- epilogue: acc[i][j][r] = C[8*(r/4) + 4*(lane/32) + r%4][lane%32] ----
+    // ---- epilogue (consumers): acc[i][j][r] = C[8*(r/4) + 4*(lane/32) + r%4][lane%32]
     const int nrows = r1 - r0;
     if constexpr (PAIR) {
-        // waves wn = 2, 3 hold the up rows of the features waves wn = 0, 1 hold
+        // consumer waves 2, 3 hold the up rows of the features waves 0, 1 hold
         // as gate rows, in the same lane/register positions: hand them over
         // through LDS (the B buffers are free now).
         float *xch = reinterpret_cast<float *>(&sB[0][0]);
         constexpr int PER = TM * TN * 16;
-        if (wn >= 2) {
-            float *d = xch + ((wm * 2 + (wn - 2)) * PER) * 64 + lane;
+        if (cw >= 2) {
+            float *d = xch + ((cw - 2) * PER) * 64 + lane;
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -432,17 +500,17 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
                     for (int r = 0; r < 16; ++r) d[((i * TN + j) * 16 + r) * 64] = acc[i][j][r];
         }
         __syncthreads();
-        if (wn < 2) {
-            const float *u = xch + ((wm * 2 + wn) * PER) * 64 + lane;
+        if (cw < 2) {
+            const float *u = xch + (cw * PER) * 64 + lane;
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+                const int n = n0 + cw * 64 + j * 32 + (lane & 31);
                 if (n >= g.OUT) continue;
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int m = wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                        const int m = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
                         if (m < nrows) {
                             const float gt = acc[i][j][r];
                             const float up = u[((i * TN + j) * 16 + r) * 64];
@@ -457,14 +525,14 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(const GemmArgs g)
     } else {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            const int n = n0 + cw * 64 + j * 32 + (lane & 31);
             if (n >= g.OUT) continue;
             const float bv = g.bias ? g.bias[n] : 0.f;
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int m = wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                    const int m = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
                     if (m < nrows) {
                         const float v = acc[i][j][r] + bv;
                         const int64_t o = (int64_t)(r0 + m) * g.OUT + n;
@@ -583,13 +651,23 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const 
     store_act<YDT>(y, (int64_t)t * hidden + c, acc);
 }
 
+// ga[g][o] = {scale[o][g], offset[o][g]}: the GEMM's affine layout, so a
+// block's rows for one group are contiguous.
+__global__ __launch_bounds__(256) void affine_pack_kernel(const float *gs, const float *go,
+                                                          int32_t out, int32_t ng, float2 *ga) {
+    const int64_t i = blockIdx.x * 256ll + threadIdx.x;  // = o * ng + g
+    if (i >= (int64_t)out * ng) return;
+    const int o = static_cast<int>(i / ng), gi = static_cast<int>(i % ng);
+    ga[(int64_t)gi * out + o] = make_float2(gs[i], go[i]);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 template <int BM, bool BF16, bool GROUPED, bool PAIR>
 static int gemm_launch(const GemmArgs &a, int grid_x, int grid_y, hipStream_t stream) {
     const dim3 grid(grid_x, grid_y);
-    if (a.w[0].gs)
+    if (a.w[0].ga)
         hipLaunchKernelGGL((gemm_kernel<BM, BF16, true, GROUPED, PAIR>), grid, dim3(kGemmThreads),
                            0, stream, a);
     else
@@ -602,20 +680,18 @@ static int gemm_launch(const GemmArgs &a, int grid_x, int grid_y, hipStream_t st
 static int check_bank(const hxq_expert_bank *b, const char *what, int64_t out, int64_t in,
                       int32_t group) {
     HXQ_REQUIRE(b && b->indices && b->codebook, std::string(what) + ": indices and codebook required");
-    const bool affine = b->group_scale || b->group_offset;
-    HXQ_REQUIRE(!affine || (b->group_scale && b->group_offset),
-                std::string(what) + ": group_scale and group_offset must be given together");
-    HXQ_REQUIRE(!affine || (group >= kBK && group % kBK == 0 && in % group == 0),
+    HXQ_REQUIRE(!b->group_affine || (group >= kBK && group % kBK == 0 && in % group == 0),
                 std::string(what) + ": group_size must be a multiple of 64 dividing in_features");
     HXQ_REQUIRE(!b->sc_row_ptr || (b->sc_col && b->sc_val),
                 std::string(what) + ": sidecar CSR needs row_ptr, col and val");
     HXQ_REQUIRE(out * in < (int64_t{1} << 31), std::string(what) + ": matrix too large");
+    HXQ_REQUIRE(!b->group_affine || (in / group) * out * 8 < (int64_t{1} << 31),
+                std::string(what) + ": affine factors too large for 32-bit offsets");
     return HXQ_OK;
 }
 
 static WSet wset_of(const hxq_expert_bank *b) {
-    return WSet{b->indices, b->codebook, b->group_scale, b->group_offset,
-                b->sc_row_ptr, b->sc_col, b->sc_val};
+    return WSet{b->indices, b->codebook, b->group_affine, b->sc_row_ptr, b->sc_col, b->sc_val};
 }
 
 // Grouped launch over a sorted assignment list: BM 128 when the mean rows per
@@ -640,8 +716,7 @@ static int grouped_launch(GemmArgs &a, int64_t n_assign, bool bf16, hipStream_t 
 using namespace hxq;
 
 extern "C" int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
-                        const float *codebook, const float *group_scale,
-                        const float *group_offset, int32_t group_size,
+                        const float *codebook, const float *group_affine, int32_t group_size,
                         const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
                         const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
                         int64_t out_features, int64_t in_features, hipStream_t stream) {
@@ -655,8 +730,7 @@ extern "C" int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
     HXQ_REQUIRE(m_rows * in_features * 2 < (int64_t{1} << 31) &&
                     out_features * in_features < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
-    const hxq_expert_bank bank{indices, codebook, group_scale, group_offset,
-                               sc_row_ptr, sc_col, sc_val};
+    const hxq_expert_bank bank{indices, codebook, group_affine, sc_row_ptr, sc_col, sc_val};
     if (int rc = check_bank(&bank, "weights", out_features, in_features, group_size)) return rc;
     GemmArgs a{};
     a.x = static_cast<const uint16_t *>(x);
@@ -676,6 +750,21 @@ extern "C" int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
     const int gy = static_cast<int>((m_rows + 127) / 128);
     return bf16 ? gemm_launch<128, true, false, false>(a, gx, gy, stream)
                 : gemm_launch<128, false, false, false>(a, gx, gy, stream);
+}
+
+extern "C" int hxq_affine_pack(const float *group_scale, const float *group_offset,
+                               int64_t out_features, int64_t n_groups, float *group_affine,
+                               hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(group_scale && group_offset && group_affine, "all pointers are required");
+    HXQ_REQUIRE(out_features > 0 && n_groups > 0 && out_features * n_groups < (int64_t{1} << 31),
+                "bad sizes");
+    const int64_t n = out_features * n_groups;
+    hipLaunchKernelGGL(affine_pack_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                       group_scale, group_offset, (int32_t)out_features, (int32_t)n_groups,
+                       reinterpret_cast<float2 *>(group_affine));
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
 }
 
 extern "C" int hxq_moe_route(const float *logits, int64_t n_tokens, int32_t n_experts,
@@ -774,7 +863,7 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     if (int rc = check_bank(gate, "gate", intermediate, hidden, group_size)) return rc;
     if (int rc = check_bank(up, "up", intermediate, hidden, group_size)) return rc;
     if (int rc = check_bank(down, "down", hidden, intermediate, group_size)) return rc;
-    HXQ_REQUIRE((gate->group_scale != nullptr) == (up->group_scale != nullptr),
+    HXQ_REQUIRE((gate->group_affine != nullptr) == (up->group_affine != nullptr),
                 "gate and up must agree on the affine");
     const bool bf16 = x_dtype == HXQ_BF16;
     uint16_t *H = static_cast<uint16_t *>(workspace);

@@ -42,7 +42,7 @@ class HxqExpertBank(ctypes.Structure):
     """Mirror of ``hxq_expert_bank`` in include/hxq.h (arrays stacked over experts)."""
 
     _fields_ = [
-        ("indices", P), ("codebook", P), ("group_scale", P), ("group_offset", P),
+        ("indices", P), ("codebook", P), ("group_affine", P),
         ("sc_row_ptr", P), ("sc_col", P), ("sc_val", P),
     ]
 
@@ -52,7 +52,8 @@ SIGNATURES = {
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
     "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemv_multi": [P, I32, P, I32, I32, I32, I64, P],
-    "hxq_gemm": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_affine_pack": [P, P, I64, I64, P, P],
     "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
                            I64, I64, I64, P, I64, P],
     "hxq_ssm_decode_step": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64,
@@ -209,21 +210,32 @@ def gemv_multi(x, mats, group_size, out_dtype=torch.float32, outs=None):
     return outs
 
 
-def gemm(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr, sc_col,
-         sc_val, bias=None, out_dtype=None, out=None):
-    """Y = X @ W^T (+bias) on MFMA; X bf16/fp16 [M, K]; W rounded to X's dtype."""
+def affine_pack(group_scale, group_offset):
+    """[out, G] scale/offset -> the GEMM layout [G, out, 2] = {scale, offset}."""
+    out_f, ng = group_scale.shape
+    ga = torch.empty(ng, out_f, 2, dtype=torch.float32, device=group_scale.device)
+    gs, go = group_scale.float().contiguous(), group_offset.float().contiguous()
+    _need_device(gs, go, ga)
+    rc = lib().hxq_affine_pack(_ptr(gs), _ptr(go), out_f, ng, _ptr(ga), _stream(gs))
+    _check("hxq_affine_pack", rc)
+    return ga
+
+
+def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_val, bias=None,
+         out_dtype=None, out=None):
+    """Y = X @ W^T (+bias) on MFMA; X bf16/fp16 [M, K]; W rounded to X's dtype.
+    group_affine: [K/G, OUT, 2] (``affine_pack``) or None."""
     m, in_f = x.shape
     out_f = indices.shape[0]
     if indices.shape[1] != in_f:
         raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
     if out is None:
         out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
-    _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val,
-                 bias, out)
+    _need_device(x, indices, codebook, group_affine, sc_row_ptr, sc_col, sc_val, bias, out)
     rc = lib().hxq_gemm(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
-                        _ptr(group_scale), _ptr(group_offset), int(group_size), _ptr(sc_row_ptr),
-                        _ptr(sc_col), _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype),
-                        m, out_f, in_f, _stream(x))
+                        _ptr(group_affine), int(group_size), _ptr(sc_row_ptr), _ptr(sc_col),
+                        _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype), m, out_f, in_f,
+                        _stream(x))
     _check("hxq_gemm", rc)
     return out
 
@@ -310,11 +322,11 @@ def moe_route(logits, top_k, renormalize=False):
 
 
 def _bank(b):
-    _need_device(b["indices"], b["codebook"], b.get("group_scale"), b.get("group_offset"),
-                 b.get("sc_row_ptr"), b.get("sc_col"), b.get("sc_val"))
+    _need_device(b["indices"], b["codebook"], b.get("group_affine"), b.get("sc_row_ptr"),
+                 b.get("sc_col"), b.get("sc_val"))
     return HxqExpertBank(*(0 if b.get(k) is None else b[k].data_ptr()
-                           for k in ("indices", "codebook", "group_scale", "group_offset",
-                                     "sc_row_ptr", "sc_col", "sc_val")))
+                           for k in ("indices", "codebook", "group_affine", "sc_row_ptr",
+                                     "sc_col", "sc_val")))
 
 
 def moe_grouped_gemm(x, sorted_rows, expert_offsets, bank, n_assign, out_dtype=torch.float32):

@@ -175,8 +175,13 @@ class HelixLinear(nn.Module):
             for name in ("_sc_row_ptr", "_sc_col", "_sc_val", "_sc_delta", "_sidecar_rows",
                          "_sidecar_cols", "_sidecar_deltas", "_sidecar_vq_vals"):
                 self.register_buffer(name, None)
-        # the MFMA GEMM steps K by 64 and reads one affine group per step
+        # the MFMA GEMM steps K by 64 and reads one affine group per step, in
+        # the layout [K/G, OUT, 2] = {scale, offset} (derived, not saved)
         self._gemm_ok = self.in_features % 64 == 0 and (not has_affine or self.group_size % 64 == 0)
+        self.register_buffer(
+            "_affine_t",
+            torch.stack([self.group_scale.t(), self.group_offset.t()], dim=-1).contiguous()
+            if has_affine else None, persistent=False)
         self.has_svd = self.svd_U is not None
         self.rank = int(self.svd_U.shape[1]) if self.has_svd else 0
         self.has_channel_scales = self.channel_scales is not None
@@ -251,9 +256,8 @@ class HelixLinear(nn.Module):
                       self.group_size, rp, col, delta, self.bias, out=out)
         elif x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
             self._last_dispatch_path = "hip_gemm"
-            _hxq.gemm(x2, self.indices, self.codebook, self.group_scale, self.group_offset,
-                      self.group_size, rp, col, None if rp is None else self._sc_val,
-                      self.bias, out=out)
+            _hxq.gemm(x2, self.indices, self.codebook, self._affine_t, self.group_size, rp, col,
+                      None if rp is None else self._sc_val, self.bias, out=out)
         else:
             # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
             self._last_dispatch_path = "hip_gemv_rows"

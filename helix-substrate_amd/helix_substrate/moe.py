@@ -16,8 +16,9 @@ experts of a layer as grouped HIP launches over one expert-sorted token list:
           ordered weighted combine                          (hxq_moe_ffn)
 
 Expert weights are stacked into banks (``stack_bank``): indices [E, out, in],
-codebooks [E, 256], affine [E, out, in/G], and one CSR sidecar whose row
-pointers [E, out+1] are absolute offsets into the concatenated entries.
+codebooks [E, 256], affine [E, out, in/G] (and its GEMM layout [E, in/G, out,
+2]), and one CSR sidecar whose row pointers [E, out+1] are absolute offsets
+into the concatenated entries.
 """
 from __future__ import annotations
 
@@ -75,7 +76,10 @@ def stack_bank(layers, device=None):
         base += int(c.numel())
     if base >= 2 ** 31:
         raise ValueError("too many sidecar entries for 32-bit offsets")
+    # the grouped GEMM reads the affine factors as [E, K/G, out, 2]
+    ga = None if gs is None else torch.stack([gs.transpose(1, 2), go.transpose(1, 2)], dim=-1).contiguous()
     return {"indices": idx, "codebook": cb, "group_scale": gs, "group_offset": go,
+            "group_affine": ga,
             "group_size": int(layers[0].get("group_size") or 0) if affine else 0,
             "sc_row_ptr": torch.stack(rps).contiguous(),
             "sc_col": torch.cat(cols).contiguous(), "sc_val": torch.cat(vals).contiguous()}

@@ -122,19 +122,31 @@ int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats,
  * in_features], W dequantised tile by tile into LDS (sidecar values replace
  * their elements, then W is rounded to X's 16-bit type) and multiplied with
  * MFMA, fp32 accumulation; Y in y_dtype [m_rows, out_features].
+ * The affine factors come in the GEMM's layout group_affine fp32
+ * [in/G][out][2] = {scale, offset} (NULL = no affine), built from the
+ * [out, in/G] scale/offset arrays by hxq_affine_pack.
  * Replaces: fused_vq_matmul with N > 1 -> _vq_gather_matmul_tiled_kernel +
  *   scatter_add sidecar + bias (helix_substrate/triton_vq_matmul.py:634-661,
  *   693-698, 724-725) and HelixLinear._forward_buffered (helix_linear.py:556-634).
  * Requires in_features % 64 == 0 and, with affine, group_size % 64 == 0.
- * sc_val are the replacement values (as for hxq_dequant_f32).
+ * sc_val are the replacement values (as for hxq_dequant_f32); columns
+ * ascending within a row.
  */
 int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
-             const float *codebook, const float *group_scale,
-             const float *group_offset, int32_t group_size,
+             const float *codebook, const float *group_affine, int32_t group_size,
              const int32_t *sc_row_ptr, const int32_t *sc_col,
              const float *sc_val, const float *bias, void *y, int32_t y_dtype,
              int64_t m_rows, int64_t out_features, int64_t in_features,
              hipStream_t stream);
+
+/*
+ * group_affine[g][o] = {group_scale[o][g], group_offset[o][g]} (fp32): the
+ * GEMM layout of the per-group affine factors (n_groups = in/G).
+ * No reference counterpart: the affine extension has no reference layout;
+ * HelixLinear builds this once as a derived buffer.
+ */
+int hxq_affine_pack(const float *group_scale, const float *group_offset, int64_t out_features,
+                    int64_t n_groups, float *group_affine, hipStream_t stream);
 
 /*
  * Mixture-of-experts FFN over HXQ experts (OLMoE-style SwiGLU experts).
@@ -144,16 +156,15 @@ int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
  * entry points run all experts of a layer in one grouped launch instead.
  *
  * An expert bank stacks the per-expert HXQ arrays along a leading expert
- * axis: indices [E, out, in] u8, codebook [E, 256], group_scale/offset
- * [E, out, in/G] (both NULL = no affine), sc_row_ptr [E, out+1] holding
- * ABSOLUTE offsets into sc_col/sc_val (replacement values), columns ascending
- * within a row.
+ * axis: indices [E, out, in] u8, codebook [E, 256], group_affine
+ * [E, in/G, out, 2] in the GEMM layout (hxq_affine_pack per expert; NULL = no
+ * affine), sc_row_ptr [E, out+1] holding ABSOLUTE offsets into sc_col/sc_val
+ * (replacement values), columns ascending within a row.
  */
 typedef struct hxq_expert_bank {
     const uint8_t *indices;
     const float *codebook;
-    const float *group_scale;
-    const float *group_offset;
+    const float *group_affine;
     const int32_t *sc_row_ptr;
     const int32_t *sc_col;
     const float *sc_val;

@@ -56,8 +56,8 @@ def _check(y, x16, W, bias=None):
 
 
 def _gemm32(mod, x):
-    return _hxq.gemm(x, mod.indices, mod.codebook, mod.group_scale, mod.group_offset,
-                     mod.group_size, mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias,
+    return _hxq.gemm(x, mod.indices, mod.codebook, mod._affine_t, mod.group_size,
+                     mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias,
                      out_dtype=torch.float32)
 
 
@@ -86,7 +86,7 @@ def test_gemm_fp32_output_bias_and_fp16(dev):
     mod = _module(T, dev, bias=bias)
     W = _oracle_w(L)
     x = torch.randn(200, 1024, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
-    y = _hxq.gemm(x.to(dev), mod.indices, mod.codebook, mod.group_scale, mod.group_offset, 128,
+    y = _hxq.gemm(x.to(dev), mod.indices, mod.codebook, mod._affine_t, 128,
                   mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias, out_dtype=torch.float32)
     assert y.dtype == torch.float32
     _check(y, x, W, bias)
@@ -127,3 +127,10 @@ def test_fp32_prefill_stays_fp32(dev):
     y = mod(x.to(dev))
     assert mod._last_dispatch_path == "hip_gemv_rows"
     assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= 1e-5
+
+
+def test_affine_pack_layout(dev):
+    gs = torch.randn(300, 7, device=dev)
+    go = torch.randn(300, 7, device=dev)
+    ga = _hxq.affine_pack(gs, go)
+    assert torch.equal(ga, torch.stack([gs.t(), go.t()], dim=-1))
