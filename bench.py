@@ -47,6 +47,9 @@ def parse():
                     help="also time the config-3 Mamba2 selective scan and mixer layer")
     ap.add_argument("--moe", type=int, default=1,
                     help="also time the config-4 OLMoE-shaped MoE FFN (16 layers)")
+    ap.add_argument("--decode", type=int, default=1,
+                    help="also run the config-1 greedy decode loop (tok/s, 128-token prompt, "
+                         "256 new tokens)")
     return ap.parse_args()
 
 
@@ -234,8 +237,14 @@ def main():
             "traffic": read_traffic(),
         },
     }
+    del graph
+    layer0 = layers[0]  # the CPU baseline's sample
+    if args.decode:
+        del layers, descs, outs
+        torch.cuda.empty_cache()
+        result["decode_config1"] = decode_bench(dev, args.layers)
+        result["decode_tok_s"] = result["decode_config1"]["tok_s"]
     if args.prefill:
-        del graph
         result["prefill_config2"] = prefill_bench(dev)
     if args.scan:
         result["scan_config3"] = scan_bench(dev, cpu=args.cpu_seconds > 0)
@@ -243,7 +252,7 @@ def main():
     if args.moe:
         result["moe_config4"] = moe_bench(dev, cpu=args.cpu_seconds > 0)
     if args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(layer0, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
@@ -361,6 +370,51 @@ def scan_bench(dev, iters=5, cpu=True):
                                "sample": f"reference sequential_scan restated (torch CPU), "
                                          f"L={Ls} of 2048, {torch.get_num_threads()} threads",
                                "kind": "port", "cores": torch.get_num_threads()}
+    return out
+
+
+def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
+    """Config 1 decode loop: Qwen2.5-3B-shaped (36 layers, hidden 2048, 16/2
+    heads of 128, SwiGLU 11008, vocab 151936, RoPE theta 1e6), random-init,
+    every projection HXQ (config-0 recipe), bf16 tied embedding / LM head.
+    Greedy decode of n_new tokens after a prompt of uniform random ids; each
+    token is one HIP-graph replay (HXQ GEMVs + norm/RoPE/attention/SiLU
+    kernels + bf16 LM head GEMV + argmax), no host sync inside the loop."""
+    import torch
+    from helix_substrate.decoder import QWEN25_3B, DecoderConfig, HelixDecoder
+
+    cfg = DecoderConfig(**{**QWEN25_3B.__dict__, "n_layers": n_layers,
+                           "max_seq": prompt_len + n_new + 8})
+    t0 = time.time()
+    dec = HelixDecoder.synthetic(cfg, seed=0, device=dev)
+    print(f"[bench] decoder built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=g)
+    dec.prefill(prompt)
+    dec.capture()
+    # warm-up replays on a throwaway state, then the measured generation
+    dec.generate(4)
+    torch.cuda.synchronize(dev)
+    dec.reset()
+    dec.prefill(prompt)
+    torch.cuda.synchronize(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    toks = dec.generate(n_new)
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    ms = ev0.elapsed_time(ev1)
+    hxq = dec.hxq_bytes_per_token()
+    lm = dec.embed.numel() * 2
+    per_tok_ms = ms / n_new
+    out = {"layers": n_layers, "prompt": prompt_len, "new_tokens": n_new,
+           "ms_per_token": round(per_tok_ms, 4), "tok_s": round(1000.0 / per_tok_ms, 1),
+           "hxq_bytes_per_token": hxq, "lm_head_bytes_per_token": lm,
+           "gbs_weights": round((hxq + lm) / (per_tok_ms * 1e-3) / 1e9, 1),
+           "first_tokens": toks[:8].cpu().tolist(), "hip_graph": True}
+    del dec
+    torch.cuda.empty_cache()
     return out
 
 

@@ -52,6 +52,19 @@ struct GemvMats {
     GemvMat m[HXQ_MAX_MULTI];
 };
 
+// Fused activation prologue (one fp32 activation row).
+//   XM 1: x_eff = bf16(w * r * rsqrt(mean(r^2) + eps)), r = x + b (b = NULL:
+//         r = x); block 0 also stores r to res_out (the updated residual).
+//   XM 2: x_eff = bf16(silu(x) * b).
+// bf16 rounding matches a separate norm / SiLU kernel writing bf16.
+struct GemvPro {
+    const float *b;
+    const float *w;
+    float *res_out;
+    float eps;
+    int32_t pad_;
+};
+
 // Launch header.  It travels as leading scalar kernel arguments so the
 // hardware preloads it into SGPRs (no kernarg memory round trip).
 struct GemvHeader {
@@ -173,12 +186,13 @@ constexpr int kEntCap = 512;  // sidecar entries per block staged in LDS
 // Barriers order LDS only (lds_barrier), so prefetched loads stay in flight.
 // Occupancy target: 4 waves per SIMD (two 8-wave blocks per CU, <= 128 VGPRs);
 // the long-row variant (4 chunks per slice) accepts 2.
-template <int NREP, int NX, int CPS, int WAVES, bool AFFINE, int RB, int XT>
+template <int NREP, int NX, int CPS, int WAVES, bool AFFINE, int RB, int XT, int XM>
 __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const void *__restrict__ x, int32_t K, int32_t group, int32_t S, int32_t nchunks,
     int32_t flags, int32_t red_rows, int32_t bb1, int32_t bb2, int32_t bb3, int32_t bb4,
-    int32_t bb5, int32_t bb6, int32_t bb7, const GemvMats mats) {
+    int32_t bb5, int32_t bb6, int32_t bb7, const GemvMats mats, const GemvPro pro) {
     constexpr bool XF32 = XT == HXQ_F32;
+    static_assert(XM == 0 || (XF32 && NX == 1), "fused prologues take one fp32 row");
     constexpr int NT = WAVES * kWave;
     constexpr int TPW = 256 * NREP / (4 * NT);  // table float4 writes per thread
     static_assert(TPW >= 1 && (256 * NREP) % (4 * NT) == 0, "table/thread-count mismatch");
@@ -199,6 +213,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     float *xl = tbl + 256 * NREP;                           // [NX * K] when xlds
     float *red = xl + (xlds ? NX * K : 0);                  // [red_rows * NX * S]
     float *ent = red + red_rows * NX * S;                   // [kEntCap * NX]
+    float *sumsq = ent + kEntCap * NX;                      // [S] (XM == 1)
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -241,6 +256,19 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
 #pragma unroll
                 for (int v = 0; v < XV; ++v)
                     xraw[ci][n][v] = buf_load16(xr, (n * K + koff[ci]) * esz + 16u * v);
+    }
+    // fused prologue operands (b: delta or up; w: norm weight), 16 per chunk
+    u32x4 braw[XM != 0 ? CPS : 1][4], wraw[XM == 1 ? CPS : 1][4];
+    if constexpr (XM != 0) {
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(pro.b, pro.b ? (int64_t)K * 4 : 0);
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(pro.w, XM == 1 ? (int64_t)K * 4 : 0);
+#pragma unroll
+        for (int ci = 0; ci < CPS; ++ci)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                braw[ci][v] = buf_load16(br, koff[ci] * 4 + 16u * v);
+                if constexpr (XM == 1) wraw[ci][v] = buf_load16(wr, koff[ci] * 4 + 16u * v);
+            }
     }
     float cbv[TPW];
     {
@@ -320,6 +348,19 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
                         xv[ci][n][8 * v + 2 * j + 1] = kok[ci] ? b : 0.f;
                     }
             }
+            if constexpr (XM != 0) {
+                // r = x + b (norm) / silu(x) * b (SiLU), kept in xv; norm scaling below
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float bv = __uint_as_float(braw[ci][v][j]);
+                        float &e = xv[ci][n][4 * v + j];
+                        if constexpr (XM == 1) e = kok[ci] ? e + bv : 0.f;
+                        else e = kok[ci] ? bf16_to_f32(f32_to_bf16(e / (1.f + expf(-e)) * bv)) : 0.f;
+                    }
+            }
+            if constexpr (XM == 1) continue;  // sums and LDS copy after the norm
             float t = 0.f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) t += xv[ci][n][j];
@@ -332,6 +373,55 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
                                          xv[ci][n][4 * v + 2], xv[ci][n][4 * v + 3]);
             }
         }
+    float norm_inv = 1.f;
+    if constexpr (XM == 1) {
+        // block-wide sum of squares: slice partials of row group 0 -> LDS
+        float ss = 0.f;
+#pragma unroll
+        for (int ci = 0; ci < CPS; ++ci)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ss = fmaf(xv[ci][0][j], xv[ci][0][j], ss);
+        ss = wave_sum(ss);
+        if (rg == 0 && lane == 0) sumsq[s_id] = ss;
+        // the updated residual, once (block 0, row group 0)
+        if (pro.res_out && blockIdx.x == 0 && rg == 0) {
+#pragma unroll
+            for (int ci = 0; ci < CPS; ++ci)
+                if (kok[ci]) {
+                    float4 *dst = reinterpret_cast<float4 *>(pro.res_out + koff[ci]);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        dst[v] = make_float4(xv[ci][0][4 * v], xv[ci][0][4 * v + 1],
+                                             xv[ci][0][4 * v + 2], xv[ci][0][4 * v + 3]);
+                }
+        }
+        lds_barrier();
+        float tot = 0.f;
+        for (int i = 0; i < S; ++i) tot += sumsq[i];
+        norm_inv = rsqrtf(tot / K + pro.eps);
+#pragma unroll
+        for (int ci = 0; ci < CPS; ++ci) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float &e = xv[ci][0][4 * v + j];
+                    e = kok[ci] ? bf16_to_f32(f32_to_bf16(__uint_as_float(wraw[ci][v][j]) * (e * norm_inv)))
+                                : 0.f;
+                }
+            float t = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t += xv[ci][0][j];
+            xs[ci][0] = t;
+            if (xlds && rg == 0 && kok[ci]) {
+                float4 *dst = reinterpret_cast<float4 *>(xl + koff[ci]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    dst[v] = make_float4(xv[ci][0][4 * v], xv[ci][0][4 * v + 1],
+                                         xv[ci][0][4 * v + 2], xv[ci][0][4 * v + 3]);
+            }
+        }
+    }
     lds_barrier();
 
     // sidecar entries of this block, first round: col/delta loads now
@@ -401,7 +491,15 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
 
     // ---- epilogue
     auto xval = [&](int n, int32_t c) -> float {
-        return xlds ? xl[n * K + c] : load_x1(x, n * K + c, XT);
+        if (xlds) return xl[n * K + c];
+        if constexpr (XM == 1) {
+            const float r = static_cast<const float *>(x)[c] + (pro.b ? pro.b[c] : 0.f);
+            return bf16_to_f32(f32_to_bf16(pro.w[c] * (r * norm_inv)));
+        } else if constexpr (XM == 2) {
+            const float g = static_cast<const float *>(x)[c];
+            return bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g)) * pro.b[c]));
+        }
+        return load_x1(x, n * K + c, XT);
     };
     lds_barrier();  // red complete
     if (has_sc) {
@@ -508,11 +606,12 @@ static int plan_gemv(GemvHeader &h, const GemvMats &mats, int n_x, GemvPlan &pl)
 
 static size_t gemv_lds_bytes(int nrep, int nx, const GemvHeader &h) {
     return (256 * (size_t)nrep + (h.xlds ? (size_t)nx * h.K : 0) +
-            (size_t)h.red_rows * nx * h.S + (size_t)kEntCap * nx) * sizeof(float);
+            (size_t)h.red_rows * nx * h.S + (size_t)kEntCap * nx + 64) * sizeof(float);
 }
 
-template <int NREP, int NX, int CPS, int RB>
-static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipStream_t stream) {
+template <int NREP, int NX, int CPS, int RB, int XM = 0>
+static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipStream_t stream,
+                      const GemvPro &pro = GemvPro{}) {
     const size_t lds = gemv_lds_bytes(NREP, NX, h);
     const bool aff = mats.m[0].gs != nullptr;
     const dim3 g(grid), b(kWaves * kWave);
@@ -520,20 +619,26 @@ static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipSt
     const int32_t K = static_cast<int32_t>(h.K);
     // all matrices of one launch either carry the affine factors or none do
 #define HXQ_GEMV_LAUNCH(AFF, XT)                                                               \
-    hipLaunchKernelGGL((gemv_kernel<NREP, NX, CPS, kWaves, AFF, RB, XT>), g, b, lds, stream,   \
+    hipLaunchKernelGGL((gemv_kernel<NREP, NX, CPS, kWaves, AFF, RB, XT, XM>), g, b, lds, stream, \
                        h.x, K, h.group, h.S, h.nchunks, flags, h.red_rows, h.bb[0], h.bb[1],   \
-                       h.bb[2], h.bb[3], h.bb[4], h.bb[5], h.bb[6], mats)
-    switch (h.x_dtype) {
-        case HXQ_F32: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32); break;
-        case HXQ_BF16: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_BF16); else HXQ_GEMV_LAUNCH(false, HXQ_BF16); break;
-        default: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F16); else HXQ_GEMV_LAUNCH(false, HXQ_F16); break;
+                       h.bb[2], h.bb[3], h.bb[4], h.bb[5], h.bb[6], mats, pro)
+    if constexpr (XM != 0) {
+        if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32);
+    } else {
+        switch (h.x_dtype) {
+            case HXQ_F32: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32); break;
+            case HXQ_BF16: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_BF16); else HXQ_GEMV_LAUNCH(false, HXQ_BF16); break;
+            default: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F16); else HXQ_GEMV_LAUNCH(false, HXQ_F16); break;
+        }
     }
 #undef HXQ_GEMV_LAUNCH
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }
 
-static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t stream) {
+template <int XM = 0>
+static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t stream,
+                    const GemvPro &pro = GemvPro{}) {
     GemvPlan pl{};
     const int rc = plan_gemv(h, mats, n_x, pl);
     if (rc != HXQ_OK) return rc;
@@ -545,15 +650,19 @@ static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t st
     // rows per batch (two batches in flight): what fits 128 VGPRs
     if (n_x == 1) {
         switch (pl.CPS) {
-            case 1: return launch_one<kNrep, 1, 1, 4>(h, mats, pl.grid, stream);
-            case 2: return launch_one<kNrep, 1, 2, 2>(h, mats, pl.grid, stream);
-            default: return launch_one<kNrep, 1, 4, 1>(h, mats, pl.grid, stream);
+            case 1: return launch_one<kNrep, 1, 1, 4, XM>(h, mats, pl.grid, stream, pro);
+            case 2: return launch_one<kNrep, 1, 2, 2, XM>(h, mats, pl.grid, stream, pro);
+            default: return launch_one<kNrep, 1, 4, 1, XM>(h, mats, pl.grid, stream, pro);
         }
     }
-    switch (n_x) {
-        case 2: return launch_one<kNrep, 2, 1, 2>(h, mats, pl.grid, stream);
-        case 3: return launch_one<kNrep, 3, 1, 1>(h, mats, pl.grid, stream);
-        default: return launch_one<kNrep, 4, 1, 1>(h, mats, pl.grid, stream);
+    if constexpr (XM != 0) {
+        return HXQ_ERR_INVALID_ARG;
+    } else {
+        switch (n_x) {
+            case 2: return launch_one<kNrep, 2, 1, 2>(h, mats, pl.grid, stream);
+            case 3: return launch_one<kNrep, 3, 1, 1>(h, mats, pl.grid, stream);
+            default: return launch_one<kNrep, 4, 1, 1>(h, mats, pl.grid, stream);
+        }
     }
 }
 
@@ -641,4 +750,56 @@ extern "C" int hxq_gemv(const void *x, int32_t x_dtype, const uint8_t *indices,
     mats.m[0] = GemvMat{indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col,
                         sc_delta, bias, y, out_features};
     return gemv_run(h, mats, static_cast<int>(n_rows), stream);
+}
+
+// Fused-prologue launches: one fp32 activation row, transformed on load.
+static int gemv_fused(int xm, const float *x, const GemvPro &pro, const hxq_matrix *mats_in,
+                      int32_t n_mats, int32_t group_size, int32_t y_dtype, int64_t in_features,
+                      hipStream_t stream) {
+    HXQ_REQUIRE(x && mats_in, "x and mats are required");
+    HXQ_REQUIRE(n_mats >= 1 && n_mats <= HXQ_MAX_MULTI, "n_mats must be in [1, HXQ_MAX_MULTI]");
+    HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
+    HXQ_REQUIRE(in_features > 0 && in_features % 16 == 0, "in_features must be a positive multiple of 16");
+    HXQ_REQUIRE(aligned16(x) && (!pro.b || aligned16(pro.b)) && (!pro.w || aligned16(pro.w)) &&
+                    (!pro.res_out || aligned16(pro.res_out)), "vectors must be 16-byte aligned");
+    HXQ_REQUIRE(in_features <= INT32_MAX / 4, "in_features too large");
+    GemvHeader h{};
+    h.x = x;
+    h.K = in_features;
+    h.group = group_size;
+    h.n_mats = n_mats;
+    h.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
+    h.x_dtype = HXQ_F32;
+    h.y_dtype = y_dtype;
+    GemvMats mats{};
+    for (int i = 0; i < n_mats; ++i) {
+        const int rc = check_mat(mats_in[i], in_features, group_size);
+        if (rc != HXQ_OK) return rc;
+        HXQ_REQUIRE((mats_in[i].group_scale != nullptr) == (mats_in[0].group_scale != nullptr),
+                    "all matrices of one launch must agree on having the group affine");
+        const hxq_matrix &m = mats_in[i];
+        mats.m[i] = GemvMat{m.indices, m.codebook, m.group_scale, m.group_offset, m.sc_row_ptr,
+                            m.sc_col, m.sc_delta, m.bias, m.y, m.out_features};
+    }
+    return xm == 1 ? gemv_run<1>(h, mats, 1, stream, pro) : gemv_run<2>(h, mats, 1, stream, pro);
+}
+
+extern "C" int hxq_gemv_multi_rmsnorm(const float *x, const float *delta, const float *norm_w,
+                                      float eps, float *res_out, const hxq_matrix *mats,
+                                      int32_t n_mats, int32_t group_size, int32_t y_dtype,
+                                      int64_t in_features, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(norm_w, "norm_w is required");
+    HXQ_REQUIRE(!res_out || (res_out != x && res_out != delta), "res_out must not alias x or delta");
+    const GemvPro pro{delta, norm_w, res_out, eps, 0};
+    return gemv_fused(1, x, pro, mats, n_mats, group_size, y_dtype, in_features, stream);
+}
+
+extern "C" int hxq_gemv_multi_silu(const float *gate, const float *up, const hxq_matrix *mats,
+                                   int32_t n_mats, int32_t group_size, int32_t y_dtype,
+                                   int64_t in_features, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(up, "up is required");
+    const GemvPro pro{up, nullptr, nullptr, 0.f, 0};
+    return gemv_fused(2, gate, pro, mats, n_mats, group_size, y_dtype, in_features, stream);
 }

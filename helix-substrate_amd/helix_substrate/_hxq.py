@@ -52,6 +52,8 @@ SIGNATURES = {
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
     "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemv_multi": [P, I32, P, I32, I32, I32, I64, P],
+    "hxq_gemv_multi_rmsnorm": [P, P, P, F32, P, P, I32, I32, I32, I64, P],
+    "hxq_gemv_multi_silu": [P, P, P, I32, I32, I32, I64, P],
     "hxq_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_affine_pack": [P, P, I64, I64, P, P],
     "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
@@ -64,6 +66,13 @@ SIGNATURES = {
     "hxq_mamba2_conv_step": [P, I32, P, P, P, F32, F32, I64, I64, I64, I64, I64, I64, I64, P, P,
                              P, P, I32, P, P],
     "hxq_gated_rmsnorm": [P, I32, P, I32, I64, P, F32, I64, I64, I64, P, I32, P],
+    "hxq_add_rmsnorm": [P, P, I32, P, F32, I64, I64, P, I32, P],
+    "hxq_rope_kv_append": [P, P, I32, I32, I32, F32, P, P, P, I32, I32, P],
+    "hxq_attn_decode": [P, P, P, I32, P, I32, I32, I32, I32, P, I32, P],
+    "hxq_silu_mul": [P, P, I64, P, I32, P],
+    "hxq_attn_rope_decode": [P, P, I32, I32, I32, F32, P, P, I32, I32, P, I32, P],
+    "hxq_dense_gemv_bf16": [P, P, I32, I64, I64, P, P],
+    "hxq_argmax": [P, I64, P, P, P, P],
     "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
     "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
 }
@@ -183,15 +192,9 @@ def gemv(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr
     return out
 
 
-def gemv_multi(x, mats, group_size, out_dtype=torch.float32, outs=None):
-    """One launch for several matrices sharing x [1, K].
-
-    ``mats`` is a list of dicts with keys indices, codebook, group_scale,
-    group_offset, sc_row_ptr, sc_col, sc_delta, bias.
-    """
+def _mat_array(x, mats, outs, out_dtype):
     if not 1 <= len(mats) <= HXQ_MAX_MULTI:
         raise RuntimeError(f"gemv_multi takes 1..{HXQ_MAX_MULTI} matrices")
-    in_f = x.shape[-1]
     arr = (HxqMatrix * len(mats))()
     if outs is None:
         outs = [torch.empty(1, m["indices"].shape[0], dtype=out_dtype, device=x.device)
@@ -204,9 +207,47 @@ def gemv_multi(x, mats, group_size, out_dtype=torch.float32, outs=None):
                              for k in ("group_scale", "group_offset", "sc_row_ptr", "sc_col",
                                        "sc_delta", "bias")),
                            y.data_ptr(), m["indices"].shape[0])
+    return arr, outs
+
+
+def gemv_multi(x, mats, group_size, out_dtype=torch.float32, outs=None):
+    """One launch for several matrices sharing x [1, K].
+
+    ``mats`` is a list of dicts with keys indices, codebook, group_scale,
+    group_offset, sc_row_ptr, sc_col, sc_delta, bias.
+    """
+    in_f = x.shape[-1]
+    arr, outs = _mat_array(x, mats, outs, out_dtype)
     rc = lib().hxq_gemv_multi(_ptr(x), dtype_code(x.dtype), ctypes.cast(arr, P), len(mats),
                               int(group_size), dtype_code(outs[0].dtype), in_f, _stream(x))
     _check("hxq_gemv_multi", rc)
+    return outs
+
+
+def gemv_multi_rmsnorm(x, delta, norm_w, eps, res_out, mats, group_size, out_dtype=torch.float32,
+                       outs=None):
+    """y_m = W_m h, h = bf16(norm_w * r * rsqrt(mean(r^2) + eps)), r = x + delta
+    (fp32 [1, K]); res_out (optional) receives r.  One launch."""
+    in_f = x.shape[-1]
+    arr, outs = _mat_array(x, mats, outs, out_dtype)
+    _need_device(delta, norm_w, res_out)
+    rc = lib().hxq_gemv_multi_rmsnorm(_ptr(x), _ptr(delta), _ptr(norm_w), float(eps),
+                                      _ptr(res_out), ctypes.cast(arr, P), len(mats),
+                                      int(group_size), dtype_code(outs[0].dtype), in_f,
+                                      _stream(x))
+    _check("hxq_gemv_multi_rmsnorm", rc)
+    return outs
+
+
+def gemv_multi_silu(gate, up, mats, group_size, out_dtype=torch.float32, outs=None):
+    """y_m = W_m bf16(silu(gate) * up) (fp32 [1, K] inputs).  One launch."""
+    in_f = gate.shape[-1]
+    arr, outs = _mat_array(gate, mats, outs, out_dtype)
+    _need_device(up)
+    rc = lib().hxq_gemv_multi_silu(_ptr(gate), _ptr(up), ctypes.cast(arr, P), len(mats),
+                                   int(group_size), dtype_code(outs[0].dtype), in_f,
+                                   _stream(gate))
+    _check("hxq_gemv_multi_silu", rc)
     return outs
 
 
@@ -430,3 +471,73 @@ def gated_rmsnorm(y, gate, weight, eps, group_size=0, out_dtype=None):
                                  _stream(y))
     _check("hxq_gated_rmsnorm", rc)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Decoder-step pieces (batch-1 greedy decoding)
+# ---------------------------------------------------------------------------
+def add_rmsnorm(x, delta, weight, eps, out):
+    """x fp32 [rows, H] += delta (optional); out = weight * rmsnorm(x)."""
+    rows, H = x.shape
+    _need_device(x, delta, weight, out)
+    rc = lib().hxq_add_rmsnorm(_ptr(x), _ptr(delta), 0 if delta is None else dtype_code(delta.dtype),
+                               _ptr(weight), float(eps), rows, H, _ptr(out),
+                               dtype_code(out.dtype), _stream(x))
+    _check("hxq_add_rmsnorm", rc)
+    return out
+
+
+def rope_kv_append(qkv, pos, n_heads, n_kv, head_dim, theta, q_out, k_cache, v_cache):
+    _need_device(qkv, pos, q_out, k_cache, v_cache)
+    rc = lib().hxq_rope_kv_append(_ptr(qkv), _ptr(pos), n_heads, n_kv, head_dim, float(theta),
+                                  _ptr(q_out), _ptr(k_cache), _ptr(v_cache),
+                                  dtype_code(k_cache.dtype), k_cache.shape[0], _stream(qkv))
+    _check("hxq_rope_kv_append", rc)
+
+
+def attn_decode(q, k_cache, v_cache, pos, n_heads, n_kv, head_dim, out):
+    _need_device(q, k_cache, v_cache, pos, out)
+    rc = lib().hxq_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache.dtype),
+                               _ptr(pos), n_heads, n_kv, head_dim, k_cache.shape[0], _ptr(out),
+                               dtype_code(out.dtype), _stream(q))
+    _check("hxq_attn_decode", rc)
+    return out
+
+
+def attn_rope_decode(qkv, pos, n_heads, n_kv, head_dim, theta, k_cache, v_cache, out):
+    """RoPE + KV append + decode attention in one launch (qkv fp32 row of the token)."""
+    _need_device(qkv, pos, k_cache, v_cache, out)
+    rc = lib().hxq_attn_rope_decode(_ptr(qkv), _ptr(pos), n_heads, n_kv, head_dim, float(theta),
+                                    _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache.dtype),
+                                    k_cache.shape[0], _ptr(out), dtype_code(out.dtype),
+                                    _stream(qkv))
+    _check("hxq_attn_rope_decode", rc)
+    return out
+
+
+def silu_mul(gate, up, out):
+    _need_device(gate, up, out)
+    rc = lib().hxq_silu_mul(_ptr(gate), _ptr(up), gate.numel(), _ptr(out), dtype_code(out.dtype),
+                            _stream(gate))
+    _check("hxq_silu_mul", rc)
+    return out
+
+
+def dense_gemv_bf16(weight, x, out):
+    rows, K = weight.shape
+    _need_device(weight, x, out)
+    rc = lib().hxq_dense_gemv_bf16(_ptr(weight), _ptr(x), dtype_code(x.dtype), rows, K,
+                                   _ptr(out), _stream(weight))
+    _check("hxq_dense_gemv_bf16", rc)
+    return out
+
+
+def argmax(logits, out_id, pos=None, workspace=None):
+    """Greedy argmax; workspace: >= 2048 device bytes (allocated here if None)."""
+    if workspace is None:
+        workspace = torch.empty(2048, dtype=torch.uint8, device=logits.device)
+    _need_device(logits, out_id, pos, workspace)
+    rc = lib().hxq_argmax(_ptr(logits), logits.numel(), _ptr(out_id), _ptr(pos), _ptr(workspace),
+                          _stream(logits))
+    _check("hxq_argmax", rc)
+    return out_id

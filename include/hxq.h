@@ -118,6 +118,25 @@ int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats,
                    int64_t in_features, hipStream_t stream);
 
 /*
+ * hxq_gemv_multi with the activation built on load (one fp32 row, K =
+ * in_features), so a decoder step needs no separate norm / SiLU launch:
+ *   _rmsnorm: r = x + delta (delta NULL: r = x); h = bf16(norm_w * r *
+ *     rsqrt(mean(r^2) + eps)); y_m = W_m h.  res_out (optional, must not alias
+ *     x or delta) receives r, written once.
+ *   _silu:    h = bf16(silu(gate) * up); y_m = W_m h.
+ * No reference counterparts: they fuse transformers' Qwen2RMSNorm
+ * (models/qwen2/modeling_qwen2.py:247-253) / Qwen2MLP act(gate) * up into the
+ * HelixLinear.forward GEMV that follows them.
+ */
+int hxq_gemv_multi_rmsnorm(const float *x, const float *delta, const float *norm_w, float eps,
+                           float *res_out, const hxq_matrix *mats, int32_t n_mats,
+                           int32_t group_size, int32_t y_dtype, int64_t in_features,
+                           hipStream_t stream);
+int hxq_gemv_multi_silu(const float *gate, const float *up, const hxq_matrix *mats,
+                        int32_t n_mats, int32_t group_size, int32_t y_dtype, int64_t in_features,
+                        hipStream_t stream);
+
+/*
  * Prefill GEMM: Y[m, :] = X[m, :] @ W^T (+ bias), X bf16 or fp16 [m_rows,
  * in_features], W dequantised tile by tile into LDS (sidecar values replace
  * their elements, then W is rounded to X's 16-bit type) and multiplied with
@@ -269,6 +288,51 @@ int hxq_gated_rmsnorm(const void *y, int32_t y_dtype, const void *gate, int32_t 
                       int64_t gate_row_stride, const float *weight, float eps, int64_t rows,
                       int64_t width, int64_t group_size, void *out, int32_t out_dtype,
                       hipStream_t stream);
+
+/*
+ * Batch-1 decoder step pieces around the HXQ GEMVs (Qwen2-shaped greedy
+ * decoding).  The position `pos` is a device int so one captured HIP graph
+ * replays every step; hxq_argmax advances it.  No reference counterparts:
+ * the reference runs these parts in transformers' Qwen2 model (models/qwen2/
+ * modeling_qwen2.py: Qwen2RMSNorm :247-253, apply_rotary_pos_emb :113-135,
+ * eager attention :150-170, Qwen2MLP) around HelixLinear projections.
+ *
+ * hxq_add_rmsnorm: x fp32 [rows, hidden] += delta (optional, delta_dtype);
+ *   out = weight * x * rsqrt(mean(x^2) + eps) in out_dtype.
+ * hxq_rope_kv_append: qkv fp32 [(n_heads + 2 n_kv) * D] of one token; rotates
+ *   q and k at *pos (rotate_half, inv_freq = theta^(-2i/D)), writes q_out fp32
+ *   [n_heads*D] and k/v rows *pos of the caches [max_seq, n_kv, D].
+ * hxq_attn_decode: per query head softmax(q.k_t / sqrt(D), t <= *pos) . v_t,
+ *   GQA (head h reads kv head h / (n_heads/n_kv)); out [n_heads*D]; D = 128.
+ * hxq_silu_mul: out = silu(gate) * up (fp32 inputs).
+ * hxq_dense_gemv_bf16: y fp32 [rows] = W bf16 [rows, in] . x (the
+ *   uncompressed LM head).
+ * hxq_argmax: *out_id = argmax(logits) (ties -> lowest index); ++*pos when
+ *   pos is not NULL; workspace: device scratch of >= 2048 bytes (partials).
+ * hxq_dense_gemv_bf16 needs in_features % 8 == 0 and a 16-byte aligned weight.
+ */
+int hxq_add_rmsnorm(float *x, const void *delta, int32_t delta_dtype, const float *weight,
+                    float eps, int64_t rows, int64_t hidden, void *out, int32_t out_dtype,
+                    hipStream_t stream);
+int hxq_rope_kv_append(const float *qkv, const int32_t *pos, int32_t n_heads, int32_t n_kv_heads,
+                       int32_t head_dim, float theta, float *q_out, void *k_cache, void *v_cache,
+                       int32_t cache_dtype, int32_t max_seq, hipStream_t stream);
+int hxq_attn_decode(const float *q, const void *k_cache, const void *v_cache,
+                    int32_t cache_dtype, const int32_t *pos, int32_t n_heads,
+                    int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, void *out,
+                    int32_t out_dtype, hipStream_t stream);
+int hxq_silu_mul(const float *gate, const float *up, int64_t n, void *out, int32_t out_dtype,
+                 hipStream_t stream);
+/* hxq_attn_rope_decode: hxq_rope_kv_append + hxq_attn_decode in one launch
+ * (qkv fp32 row in; k/v of position *pos stored into the caches). */
+int hxq_attn_rope_decode(const float *qkv, const int32_t *pos, int32_t n_heads,
+                         int32_t n_kv_heads, int32_t head_dim, float theta, void *k_cache,
+                         void *v_cache, int32_t cache_dtype, int32_t max_seq, void *out,
+                         int32_t out_dtype, hipStream_t stream);
+int hxq_dense_gemv_bf16(const uint16_t *weight, const void *x, int32_t x_dtype, int64_t rows,
+                        int64_t in_features, float *y, hipStream_t stream);
+int hxq_argmax(const float *logits, int64_t n, int32_t *out_id, int32_t *pos,
+               void *workspace, hipStream_t stream);
 
 /*
  * Selective scan (Mamba/Mamba2), fp32 state, chunk-parallel:

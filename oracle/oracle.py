@@ -26,6 +26,9 @@ Reference functions restated (file:line under the reference checkout):
 * ``conv1d_causal_np`` / ``gated_rmsnorm_np`` / ``mamba2_mixer_np`` -- the
   Mamba2 mixer around the scan (``mamba_scan_chunked.py:239-387``), composed
   from ``linear_np`` and ``ssm_scan_f64``.
+* ``rmsnorm_np`` / ``rope_np`` / ``causal_gqa_attention_np`` /
+  ``qwen2_logits_np`` -- the Qwen2-shaped decoder around the HXQ projections
+  (transformers' Qwen2, cited at the functions), composed from ``linear_np``.
 * ``ssm_scan_chunked_np`` -- the chunked closed form of the same recurrence
   (the algorithm of ``chunked_scan``, ``mamba_scan_chunked.py:89-213``), written
   in the segment-sum form exp(cumA_t - cumA_s) that cannot overflow; fp64.
@@ -336,3 +339,63 @@ def mamba2_mixer_np(hs, Win, Wout, conv_w, conv_b, dt_bias, A_log, D, norm_w, ep
     z = gated_rmsnorm_np(np.asarray(y).reshape(b, L, I), gate, norm_w, eps)
     out = linear_np(z.reshape(b * L, I), Wout).reshape(b, L, -1)
     return out, conv_state, h
+
+
+# ---------------------------------------------------------------------------
+# Qwen2-shaped decoder (benchmark config 1 decode loop).  The reference runs
+# HelixLinear projections inside transformers' Qwen2 model; restated from
+# transformers 5.15.0 models/qwen2/modeling_qwen2.py: Qwen2RMSNorm (:247-253),
+# rotary inv_freq (:86) and apply_rotary_pos_emb/rotate_half (:105-135),
+# eager attention with repeat_kv and scaling D^-1/2 (:138-170), decoder layer
+# residual structure (:269-300), Qwen2MLP down(silu(gate) * up).  fp64.
+# ---------------------------------------------------------------------------
+def rmsnorm_np(x, w, eps):
+    x = np.asarray(x, np.float64)
+    return np.asarray(w, np.float64) * x / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+
+
+def rope_np(x, pos, theta):
+    """x [..., T, D] rotated at positions pos [T] (rotate_half convention)."""
+    x = np.asarray(x, np.float64)
+    D = x.shape[-1]
+    inv = theta ** (-np.arange(0, D, 2, dtype=np.float64) / D)
+    ang = np.asarray(pos, np.float64)[:, None] * inv[None, :]
+    cos = np.concatenate([np.cos(ang)] * 2, -1)
+    sin = np.concatenate([np.sin(ang)] * 2, -1)
+    rot = np.concatenate([-x[..., D // 2:], x[..., :D // 2]], -1)
+    return x * cos + rot * sin
+
+
+def causal_gqa_attention_np(q, k, v):
+    """q [nh, T, D], k/v [nkv, T, D]: softmax(q k^T / sqrt(D) + causal) v."""
+    nh, T, D = q.shape
+    rep = nh // k.shape[0]
+    out = np.empty_like(q)
+    mask = np.triu(np.ones((T, T), bool), 1)
+    for h in range(nh):
+        s = q[h] @ k[h // rep].T / np.sqrt(D)
+        s[mask] = -np.inf
+        s = np.exp(s - s.max(-1, keepdims=True))
+        out[h] = (s / s.sum(-1, keepdims=True)) @ v[h // rep]
+    return out
+
+
+def qwen2_logits_np(tokens, embed, layers, final_norm, n_heads, n_kv, head_dim, theta, eps):
+    """Logits [T, vocab] of a token sequence.  layers: dicts of dense fp64
+    weights q/k/v/o/gate/up/down ([out, in]), biases bq/bk/bv, in_norm,
+    post_norm; the embedding is tied to the LM head."""
+    E = np.asarray(embed, np.float64)
+    x = E[np.asarray(tokens)]
+    T = x.shape[0]
+    pos = np.arange(T)
+    for L in layers:
+        h = rmsnorm_np(x, L["in_norm"], eps)
+        q = (linear_np(h, L["q"], L.get("bq"))).reshape(T, n_heads, head_dim).transpose(1, 0, 2)
+        k = (linear_np(h, L["k"], L.get("bk"))).reshape(T, n_kv, head_dim).transpose(1, 0, 2)
+        v = (linear_np(h, L["v"], L.get("bv"))).reshape(T, n_kv, head_dim).transpose(1, 0, 2)
+        a = causal_gqa_attention_np(rope_np(q, pos, theta), rope_np(k, pos, theta), v)
+        x = x + linear_np(a.transpose(1, 0, 2).reshape(T, -1), L["o"])
+        h = rmsnorm_np(x, L["post_norm"], eps)
+        g = linear_np(h, L["gate"])
+        x = x + linear_np(silu_np(g) * linear_np(h, L["up"]), L["down"])
+    return linear_np(rmsnorm_np(x, final_norm, eps), E)
