@@ -549,34 +549,59 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
 // MoE routing: softmax over experts, top-k (ties -> lower expert id), and the
 // expert-sorted assignment lists.
 // ---------------------------------------------------------------------------
+// One wave per token; lane l holds logits l, l + 64, ... (E <= 256).  The
+// softmax denominator and each of the k picks are wave reductions.
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int32_t T, int32_t E,
                                                        int32_t k, int32_t renorm, int32_t *ids,
                                                        float *wts) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + threadIdx.x / 64;
+    if (t >= T) return;  // wave-uniform
     const float *l = logits + (int64_t)t * E;
+    float v[4];
     float mx = -INFINITY;
-    for (int i = 0; i < E; ++i) mx = fmaxf(mx, l[i]);
-    float sum = 0.f;
-    for (int i = 0; i < E; ++i) sum += expf(l[i] - mx);
-    uint64_t taken[4] = {0, 0, 0, 0};  // E <= 256
-    float picked = 0.f;
-    for (int s = 0; s < k; ++s) {
-        int best = -1;
-        float bv = -INFINITY;
-        for (int i = 0; i < E; ++i) {
-            if ((taken[i >> 6] >> (i & 63)) & 1ull) continue;
-            const float v = l[i];
-            if (best < 0 || v > bv) { best = i; bv = v; }
-        }
-        taken[best >> 6] |= 1ull << (best & 63);
-        const float p = expf(bv - mx) / sum;
-        ids[(int64_t)t * k + s] = best;
-        wts[(int64_t)t * k + s] = p;
-        picked += p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? l[e] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
     }
-    if (renorm) {
-        for (int s = 0; s < k; ++s) wts[(int64_t)t * k + s] /= picked;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, kWave));
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < E) sum += expf(v[j] - mx);
+    sum = wave_sum(sum);
+    float picked = 0.f, my_w = 0.f;
+    int my_id = 0;
+    for (int s = 0; s < k; ++s) {
+        // best (value, id) of this lane, then across the wave; ties -> lower id
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            if (e < E && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = __shfl_xor(bv, m, kWave);
+            const int oi = __shfl_xor(bi, m, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        // remove the pick from its owner lane
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j == bi) v[j] = -INFINITY;
+        const float p = expf(bv - mx) / sum;
+        picked += p;
+        if (lane == s) { my_id = bi; my_w = p; }
+    }
+    // lanes 0..k-1 hold the picks in order (k <= 64)
+    if (lane < k) {
+        ids[(int64_t)t * k + lane] = my_id;
+        wts[(int64_t)t * k + lane] = renorm ? my_w / picked : my_w;
     }
 }
 
@@ -777,9 +802,9 @@ extern "C" int hxq_moe_route(const float *logits, int64_t n_tokens, int32_t n_ex
                     sorted_rows && assign_pos, "all pointers are required");
     HXQ_REQUIRE(n_tokens > 0 && n_tokens * top_k < (int64_t{1} << 31), "bad n_tokens");
     HXQ_REQUIRE(n_experts >= 1 && n_experts <= 256, "n_experts must be in 1..256");
-    HXQ_REQUIRE(top_k >= 1 && top_k <= n_experts, "top_k must be in 1..n_experts");
+    HXQ_REQUIRE(top_k >= 1 && top_k <= n_experts && top_k <= 64, "top_k must be in 1..min(n_experts, 64)");
     const int64_t n_assign = n_tokens * top_k;
-    hipLaunchKernelGGL(moe_topk_kernel, dim3((n_tokens + 255) / 256), dim3(256), 0, stream,
+    hipLaunchKernelGGL(moe_topk_kernel, dim3((n_tokens + 3) / 4), dim3(256), 0, stream,
                        logits, static_cast<int32_t>(n_tokens), n_experts, top_k, renormalize,
                        topk_ids, topk_weights);
     HXQ_LAUNCH_CHECK();

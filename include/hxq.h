@@ -190,7 +190,8 @@ typedef struct hxq_expert_bank {
 } hxq_expert_bank;
 
 /*
- * Routing: p = softmax(logits[t, :]) (fp32 [n_tokens, n_experts]); the top_k
+ * Routing: p = softmax(logits[t, :]) (fp32 [n_tokens, n_experts], n_experts <=
+ * 256, top_k <= 64); the top_k
  * experts by logit (ties -> lower id) with weights p (renormalised to sum 1
  * when `renormalize`); then the expert-sorted assignment list: expert e owns
  * sorted positions [expert_offsets[e], expert_offsets[e+1]) in token order,
