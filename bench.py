@@ -47,13 +47,17 @@ def parse():
                     help="also time the config-3 Mamba2 selective scan and mixer layer")
     ap.add_argument("--moe", type=int, default=1,
                     help="also time the config-4 OLMoE-shaped MoE FFN (16 layers)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant kernel for counter runs (rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE): the gate+up GEMV of 12 layers twice, then "
+                         "a 256 MiB copy as the counter calibration; prints no JSON")
     ap.add_argument("--decode", type=int, default=1,
                     help="also run the config-1 greedy decode loop (tok/s, 128-token prompt, "
                          "256 new tokens)")
     return ap.parse_args()
 
 
-def build_layers(n_layers, dev):
+def build_layers(n_layers, dev, names=None):
     import torch
     from helix_substrate import synth
     from helix_substrate.helix_linear import HelixLinear
@@ -62,6 +66,8 @@ def build_layers(n_layers, dev):
     for li in range(n_layers):
         mods = {}
         for pi, (name, out_f, in_f) in enumerate(PROJ):
+            if names is not None and name not in names:
+                continue
             L = synth.make_layer_torch(out_f, in_f, seed=1000 + 16 * li + pi, device=dev)
             mods[name] = HelixLinear(in_f, out_f, L["codebook"], L["indices"],
                                      L["sidecar_positions"], L["sidecar_values"],
@@ -91,6 +97,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.traffic_probe:
+        traffic_probe(dev)
+        return
     t0 = time.time()
     layers = build_layers(args.layers, dev)
     print(f"[bench] built {args.layers} layers in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
@@ -254,6 +263,27 @@ def main():
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layer0, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def traffic_probe(dev):
+    """Counter-run workload: 12 layers of the gate+up GEMV launch, twice, then a
+    256 MiB device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    import torch
+    from helix_substrate import _hxq
+
+    layers = build_layers(12, dev, names=("gate", "up"))
+    x = torch.randn(1, HIDDEN, device=dev).to(torch.bfloat16)
+    outs = [torch.empty(1, INTER, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    for _ in range(2):
+        for mods in layers:
+            _hxq.gemv_multi(x, [mat_desc(mods["gate"]), mat_desc(mods["up"])], 128, outs=outs)
+    torch.cuda.synchronize(dev)
+    a = torch.empty(64 * 1024 * 1024, device=dev)
+    b = torch.randn(64 * 1024 * 1024, device=dev)
+    for _ in range(3):
+        a.copy_(b)
+    torch.cuda.synchronize(dev)
+    print("[bench] traffic probe done", file=sys.stderr, flush=True)
 
 
 def read_traffic():
