@@ -407,9 +407,14 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
     """Config 1 decode loop: Qwen2.5-3B-shaped (36 layers, hidden 2048, 16/2
     heads of 128, SwiGLU 11008, vocab 151936, RoPE theta 1e6), random-init,
     every projection HXQ (config-0 recipe), bf16 tied embedding / LM head.
-    Greedy decode of n_new tokens after a prompt of uniform random ids; each
-    token is one HIP-graph replay (HXQ GEMVs + norm/RoPE/attention/SiLU
-    kernels + bf16 LM head GEMV + argmax), no host sync inside the loop."""
+    Greedy decode of n_new tokens after a prompt of uniform random ids, two
+    ways, no host sync inside either loop:
+      persistent: one cooperative launch per token (hxq_decoder_step: every
+                  layer, LM head and argmax with grid barriers in between);
+      graph:      one HIP-graph replay per token of the per-kernel sequence
+                  (HXQ GEMVs + norm/RoPE/attention/SiLU kernels + bf16 LM
+                  head GEMV + argmax).
+    tok_s is the faster of the two."""
     import torch
     from helix_substrate.decoder import QWEN25_3B, DecoderConfig, HelixDecoder
 
@@ -420,29 +425,47 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
     print(f"[bench] decoder built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=g)
+
+    def timed(fn):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        toks = fn()
+        ev1.record()
+        torch.cuda.synchronize(dev)
+        return ev0.elapsed_time(ev1) / n_new, toks
+
+    # graph path: warm-up replays on a throwaway state, then the measured run
     dec.prefill(prompt)
     dec.capture()
-    # warm-up replays on a throwaway state, then the measured generation
     dec.generate(4)
     torch.cuda.synchronize(dev)
     dec.reset()
     dec.prefill(prompt)
     torch.cuda.synchronize(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    toks = dec.generate(n_new)
-    ev1.record()
+    ms_graph, toks_graph = timed(lambda: dec.generate(n_new))
+    # persistent path: same prompt fed token by token, then the measured run
+    dec.reset()
+    dec.persistent_init()
+    for t in prompt.tolist():
+        dec.tok.fill_(t)
+        dec.step_persistent(1)
     torch.cuda.synchronize(dev)
-    ms = ev0.elapsed_time(ev1)
+    ms_pers, toks_pers = timed(lambda: dec.generate_persistent(n_new))
+    err = dec.persistent_error()
+    if err:
+        raise RuntimeError(f"persistent decode reported error {err}")
     hxq = dec.hxq_bytes_per_token()
     lm = dec.embed.numel() * 2
-    per_tok_ms = ms / n_new
+    per_tok_ms = min(ms_graph, ms_pers)
     out = {"layers": n_layers, "prompt": prompt_len, "new_tokens": n_new,
            "ms_per_token": round(per_tok_ms, 4), "tok_s": round(1000.0 / per_tok_ms, 1),
+           "ms_per_token_persistent": round(ms_pers, 4),
+           "ms_per_token_graph": round(ms_graph, 4),
            "hxq_bytes_per_token": hxq, "lm_head_bytes_per_token": lm,
            "gbs_weights": round((hxq + lm) / (per_tok_ms * 1e-3) / 1e9, 1),
-           "first_tokens": toks[:8].cpu().tolist(), "hip_graph": True}
+           "first_tokens_persistent": toks_pers[:8].cpu().tolist(),
+           "first_tokens_graph": toks_graph[:8].cpu().tolist()}
     del dec
     torch.cuda.empty_cache()
     return out

@@ -124,40 +124,6 @@ __device__ __forceinline__ void store_y(void *y, int64_t i, int dt, float v) {
     else static_cast<uint16_t *>(y)[i] = f32_to_f16(v);
 }
 
-// Codebook lookup of byte B (0..3) of the packed index word w.
-//   NREP == 64: entry stride is 256 bytes and the lane's replica offset
-//   (lane*4 < 256) fits in the low byte, so the LDS byte address is
-//   {0, 0, w.byte[B], lane_off} -- one v_perm_b32 builds it.
-//   NREP == 32: shift/mask arithmetic.
-template <int NREP, int B>
-__device__ __forceinline__ float tbl_lookup(const float *tbl, uint32_t lane_off, uint32_t w) {
-    if constexpr (NREP == 64) {
-        constexpr uint32_t sel = (12u << 24) | (12u << 16) | (static_cast<uint32_t>(B) << 8) | 4u;
-        const uint32_t addr = __builtin_amdgcn_perm(lane_off, w, sel);
-        return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(tbl) + addr);
-    } else {
-        const uint32_t addr = ((w >> (8 * B)) & 0xffu) * (NREP * 4) + lane_off;
-        return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(tbl) + addr);
-    }
-}
-
-// Wave64 sum via DPP; the total lands in lane 63.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add(float v) {
-    const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
-    return v + __int_as_float(s);
-}
-
-__device__ __forceinline__ float wave_sum_lane63(float v) {
-    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
-    v = dpp_add<0x140, 0xf>(v);  // row_mirror: every lane holds its row's sum
-    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-    return v;                    // lane 63 holds the wave total
-}
-
 // One pipeline stage: the index words and affine factors of one row x CPS chunks.
 template <int CPS>
 struct GemvItem {

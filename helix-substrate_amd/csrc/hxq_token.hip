@@ -1,0 +1,1453 @@
+// Persistent batch-1 decode step: ONE cooperative launch runs a whole token of
+// a Qwen2-shaped decoder whose q/k/v/o/gate/up/down projections are HXQ
+// matrices -- every layer's norm + q/k/v GEMV, RoPE + KV append + GQA
+// attention, o GEMV, norm + gate/up GEMV with the SiLU product, down GEMV,
+// then the final norm, the tied bf16 LM head and the greedy argmax.
+//
+// Why: at batch 1 the multi-launch step pays a fixed cost per launch (launch
+// gap, first-data round trip, tail) that is larger than the data time of most
+// projections.  Here the grid stays resident (one 16-wave block per CU) and
+// the stages are separated by grid barriers; the compressed weights of the
+// NEXT stage do not depend on the barrier, so every block issues their loads
+// (index rows, affine factors, codebook, CSR row pointers) right after
+// arriving and before waiting: HBM streams while the grid synchronises.
+//
+// Grid barrier (per-block arrival flags + one release word):
+//   arrive: each wave waits for its own stores (s_waitcnt 0), workgroup
+//           barrier, thread 0 stores flag[block] = target (coherent store);
+//   wait:   block 0's wave 0 polls all flags until every one reached target,
+//           then stores release = target; the other blocks' wave 0 polls the
+//           release word.  Every wait gives up after 1 s of wall clock or when
+//           the error word is set, and the kernel then returns, so every wave
+//           ends even if the grid cannot synchronise.
+// Data that crosses blocks inside a launch (residual stream, q/k/v, attention
+// output, o, SiLU product, down output, argmax partials) is written with
+// coherent stores (sc1) and read with coherent loads (sc1), so no L2
+// write-back or invalidate is needed at the barriers (each XCD has its own
+// L2).  Weights, norms and the KV cache rows of earlier positions are read
+// with ordinary loads (written before the launch).
+//
+// GEMV stages follow hxq_gemv.hip's scheme (16-byte index loads per lane, the
+// 256-entry codebook replicated 64x in LDS, affine factored out of the sum,
+// sidecar as an epilogue in CSR order, fixed summation order): rows of a
+// stage are split over the blocks, the 16 waves of a block split into S
+// K-slices x row lanes.  Gate and up rows j are computed by the same block
+// (waves 0-7 gate, 8-15 up, each with its own LDS codebook) so the block
+// writes act[j] = bf16(silu(g) * u) directly.
+//
+// Math: transformers' Qwen2 (models/qwen2/modeling_qwen2.py): RMSNorm
+// (:247-253), rotate_half RoPE (:105-135), eager GQA attention (:138-170),
+// residuals (:269-300), MLP down(act(gate) * up).  Residual stream fp32,
+// activations entering the projections bf16, KV cache bf16.
+#include <cfloat>
+#include <cstring>
+#include <vector>
+
+#include "hxq_common.h"
+
+namespace hxq {
+namespace tok {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / kWave;      // 16
+constexpr int CPS = 1;                        // 1024-column chunks per wave slice
+constexpr int RB = 4;                         // rows per load batch
+constexpr int NREP = 64;                      // codebook replicas in LDS
+constexpr int kTbl = 256 * NREP;              // floats per codebook table (64 KB)
+constexpr int kTPW = kTbl / (4 * kThreads);   // float4 table writes per thread (4)
+constexpr int kChunk = 1024;
+constexpr int kRedCap = 512;                  // row x slice partials per segment
+constexpr int kEnt = 512;                     // sidecar entries per segment staged in LDS
+constexpr int kRps = 1028;                    // CSR row pointers per segment staged in LDS
+constexpr int kHeadDim = 128;
+constexpr int kMaxSeq = 1024;
+constexpr int kLmRB = 1;                      // LM-head rows per load batch
+constexpr uint32_t kOob = 0x80000000u;        // buffer offset past any range: reads 0
+constexpr int kCoh = 16;                      // cache policy sc1: coherent across XCDs
+constexpr uint64_t kTimeoutTicks = 100000000ull;  // 1 s of the 100 MHz wall clock
+
+enum { kQ = 0, kK = 1, kV = 2, kO = 3, kG = 4, kU = 5, kD = 6 };
+
+// wave-uniform values forced into scalar registers
+__device__ __forceinline__ uint64_t ufl64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+template <typename T>
+__device__ __forceinline__ T *uptr(T *p) {
+    return reinterpret_cast<T *>(ufl64(reinterpret_cast<uint64_t>(p)));
+}
+
+
+struct Mat {
+    const uint8_t *idx;
+    const float *cb;
+    const float *gs;
+    const float *go;
+    const int32_t *rp;
+    const int32_t *col;
+    const float *delta;
+    const float *bias;
+    int64_t out;
+};
+
+// A matrix descriptor read from the layer table into scalar registers (the
+// table lives in ordinary device memory, which the compiler cannot prove
+// read-only, so it would otherwise keep every field in vector registers).
+__device__ __forceinline__ Mat umat(const Mat &m) {
+    Mat r;
+    r.idx = uptr(m.idx);
+    r.cb = uptr(m.cb);
+    r.gs = uptr(m.gs);
+    r.go = uptr(m.go);
+    r.rp = uptr(m.rp);
+    r.col = uptr(m.col);
+    r.delta = uptr(m.delta);
+    r.bias = uptr(m.bias);
+    r.out = static_cast<int64_t>(ufl64(static_cast<uint64_t>(m.out)));
+    return r;
+}
+
+struct Layer {
+    Mat m[7];
+    const float *in_norm;
+    const float *post_norm;
+    uint16_t *kc;
+    uint16_t *vc;
+};
+
+struct Plan {
+    int32_t hidden, n_layers, n_heads, n_kv, inter, vocab, max_seq, group, nblocks;
+    float eps, theta;
+    int32_t qkv_b1, qkv_b2;            // blocks [0,b1) q, [b1,b2) k, [b2,nb) v
+    int32_t s_qkv, s_o, s_gu, s_down;  // K slices per wave group
+    int32_t lds_red;                   // float offset of the red/ent area in LDS
+    int32_t pad_;
+    const uint16_t *embed;
+    const float *final_norm;
+    int32_t *tok;
+    int32_t *pos;
+    float *logits;
+    const Layer *layers;
+    // Data that crosses blocks: one slot per layer, so every address is
+    // written once per launch before any block reads it -- no L2 can hold a
+    // stale copy, and readers use ordinary cached loads (8 L2 fills per
+    // line instead of one memory read per block).  Producers store with sc1
+    // (write-through) so the data is at the coherence point before their
+    // barrier flag.
+    //   res[l]  residual entering layer l (l = 1..L; layer 0 embeds)
+    //   ra[l]   residual after layer l's attention block input add
+    //   qkv[l], attn[l], o[l], act[l], dn[l]
+    float *res, *ra, *qkv, *o, *dn, *part_v;
+    uint16_t *attn, *act;
+    int32_t ls_hid, ls_qkv, ls_attn, ls_act;  // slot strides (elements)
+    int32_t *part_i;
+    uint32_t *flags, *release;
+    int32_t *err;
+};
+
+// Buffer resource with base and size forced into scalar registers (the
+// values are wave-uniform; without this the compiler may not prove it and
+// wraps every load in a per-lane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t urs(const void *base, int64_t bytes) {
+    const uint64_t v = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    const uint32_t n = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bytes));
+    return make_rsrc(reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo), n);
+}
+
+// ---------------------------------------------------------------------------
+// coherent accesses
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 coh_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoh);
+}
+__device__ __forceinline__ void coh_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCoh);
+}
+__device__ __forceinline__ float coh_loadf(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t coh_loadi(const int32_t *p) {
+    return __hip_atomic_load(const_cast<int32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_storef(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_storei(int32_t *p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_store_u32(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_store_bf16(uint16_t *base, int64_t n, int64_t i, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), urs(base, n * 2),
+                                          static_cast<uint32_t>(i * 2), 0, kCoh);
+}
+__device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// Wave64 reductions via DPP (no lane-address registers); the result is
+// read from lane 63 into a scalar register, i.e. every lane gets it.
+__device__ __forceinline__ float wave_sum_all(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_lane63(v)), 63));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+    const int s = __builtin_amdgcn_update_dpp(__float_as_int(-FLT_MAX), __float_as_int(v), CTRL,
+                                              ROW_MASK, 0xf, false);
+    return fmaxf(v, __int_as_float(s));
+}
+
+__device__ __forceinline__ float wave_max_all(float v) {
+    v = dpp_max<0xb1, 0xf>(v);
+    v = dpp_max<0x4e, 0xf>(v);
+    v = dpp_max<0x141, 0xf>(v);
+    v = dpp_max<0x140, 0xf>(v);
+    v = dpp_max<0x142, 0xa>(v);
+    v = dpp_max<0x143, 0xc>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Redefines a value with an empty asm so the compiler recomputes whatever
+// derives from it instead of keeping it live from an earlier stage.
+__device__ __forceinline__ int fresh_s(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+__device__ __forceinline__ int fresh_v(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// grid barrier
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void arrive(const Plan &P, uint32_t target) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_store(P.flags + blockIdx.x, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool gave_up(const Plan &P, uint64_t t0) {
+    const int32_t e = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (e != 0 || wall_clock64() - t0 > kTimeoutTicks) {
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_store(P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
+    return false;
+}
+
+// Returns false when the grid could not synchronise (the caller returns).
+__device__ __forceinline__ bool wait_all(const Plan &P, uint32_t target, int *sh) {
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        int ok = 1;
+        const uint64_t t0 = wall_clock64();
+        if (blockIdx.x == 0) {
+            const int nb = P.nblocks;
+            const __amdgpu_buffer_rsrc_t fr = urs(P.flags, static_cast<int64_t>(nb) * 4);
+            while (true) {
+                int done = 1;
+                for (int i0 = 0; i0 < nb; i0 += 4 * kWave) {
+                    const u32x4 f = coh_load16(fr, static_cast<uint32_t>(i0 + 4 * lane) * 4u);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int i = i0 + 4 * lane + j;
+                        done &= (i >= nb) || static_cast<int32_t>(f[j] - target) >= 0;
+                    }
+                }
+                if (__all(done)) break;
+                if (gave_up(P, t0)) { ok = 0; break; }
+            }
+            if (ok && lane == 0)
+                __hip_atomic_store(P.release, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            while (true) {
+                const uint32_t r = __builtin_amdgcn_readfirstlane(
+                    __hip_atomic_load(P.release, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                if (static_cast<int32_t>(r - target) >= 0) break;
+                if (gave_up(P, t0)) { ok = 0; break; }
+            }
+        }
+        if (lane == 0) *sh = ok;
+    }
+    __syncthreads();
+    return *sh != 0;
+}
+
+// Waits until the producer blocks of this block's input reached `target`:
+// the blocks in up to three ranges [a, b) (one hop: no release word).
+// Wave 0 polls; returns false when it gave up.
+__device__ __forceinline__ bool wait_blocks(const Plan &P, uint32_t target, int *sh, int a0,
+                                            int b0, int a1, int b1, int a2, int b2) {
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        const int n0 = b0 - a0, n1 = b1 - a1, n = n0 + n1 + (b2 - a2);
+        int ok = 1;
+        const uint64_t t0 = wall_clock64();
+        while (true) {
+            int done = 1;
+            for (int i = lane; i < n; i += kWave) {
+                const int blk = i < n0 ? a0 + i : i < n0 + n1 ? a1 + i - n0 : a2 + i - n0 - n1;
+                const uint32_t f = __hip_atomic_load(P.flags + blk, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                done &= static_cast<int32_t>(f - target) >= 0;
+            }
+            if (__all(done)) break;
+            if (gave_up(P, t0)) { ok = 0; break; }
+        }
+        if (lane == 0) *sh = ok;
+    }
+    __syncthreads();
+    return *sh != 0;
+}
+
+// Block (of nbm, rows split as out*b/nbm) holding row r.
+__device__ __forceinline__ int block_of_row(uint32_t out, uint32_t nbm, uint32_t r) {
+    uint32_t b = r * nbm / out;
+    while (b + 1 < nbm && out * (b + 1) / nbm <= r) ++b;
+    while (b > 0 && out * b / nbm > r) --b;
+    return static_cast<int>(b);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV stages
+// ---------------------------------------------------------------------------
+struct Batch {
+    u32x4 q[RB][CPS];
+    float sc[RB][CPS];
+    float of[RB][CPS];
+};
+
+// Loads issued before a stage's barrier: the codebook values this thread
+// writes into the LDS tables, the block's CSR range (per segment) and the
+// first batch of this wave's rows.  One batch (about 16 MB over the GPU)
+// covers the barrier and activation latency; a deeper prefetch fills the
+// HBM queues and delays the barrier's own flag traffic behind it.  The
+// second batch is issued right after the stage's activation loads.
+struct Pre {
+    Batch bt[2];
+    float cbv[2][kTPW];
+    int32_t b0[2], b1[2];
+};
+
+// One wave's share of a matrix segment: rows [lo, lo+n) of the block, waves
+// split into S K-slices x RG row lanes.
+struct Seg {
+    int64_t lo, n, n_mine;
+    int s_id, rg, RG, S, c_lo, nc;
+};
+
+// A stage as seen by one block: one matrix (q/k/v by block, o, down) or the
+// gate/up pair (segment = wave / 8).
+struct Geo {
+    Mat m0, m1;
+    int nseg;
+    int seg;       // this wave's segment
+    int64_t lo, n;
+    int32_t K;
+    int64_t y_off; // output offset of the block's matrix (q/k/v rows in qkv)
+    Seg g;
+};
+
+__device__ __forceinline__ Seg make_seg(int64_t lo, int64_t n, int w, int nw, int S, int nchunks) {
+    Seg g;
+    g.lo = lo;
+    g.n = n;
+    g.S = S;
+    g.RG = nw / S;
+    g.s_id = w % S;
+    g.rg = w / S;
+    g.c_lo = g.s_id * nchunks / S;
+    g.nc = (g.s_id + 1) * nchunks / S - g.c_lo;
+    g.n_mine = (g.rg < g.RG && n > g.rg) ? (n - g.rg + g.RG - 1) / g.RG : 0;
+    return g;
+}
+
+__device__ __forceinline__ int nchunks_of(int32_t K) { return (K + kChunk - 1) / kChunk; }
+
+__device__ __forceinline__ Geo geo_qkv(const Plan &P, const Layer &L, int wave) {
+    Geo G;
+    const int b = blockIdx.x, nb = P.nblocks;
+    const int mi = b < P.qkv_b1 ? 0 : b < P.qkv_b2 ? 1 : 2;
+    const int bs = mi == 0 ? 0 : mi == 1 ? P.qkv_b1 : P.qkv_b2;
+    const int be = mi == 0 ? P.qkv_b1 : mi == 1 ? P.qkv_b2 : nb;
+    G.m0 = G.m1 = umat(L.m[mi]);
+    G.nseg = 1;
+    G.seg = 0;
+    const int64_t out = G.m0.out;
+    G.lo = static_cast<uint32_t>(out) * static_cast<uint32_t>(b - bs) / static_cast<uint32_t>(be - bs);
+    G.n = static_cast<uint32_t>(out) * static_cast<uint32_t>(b - bs + 1) / static_cast<uint32_t>(be - bs) - G.lo;
+    G.K = P.hidden;
+    G.y_off = mi == 0 ? 0 : mi == 1 ? int64_t{P.n_heads} * kHeadDim
+                                    : int64_t{P.n_heads + P.n_kv} * kHeadDim;
+    G.g = make_seg(G.lo, G.n, wave, kWaves, P.s_qkv, nchunks_of(G.K));
+    return G;
+}
+
+__device__ __forceinline__ Geo geo_plain(const Plan &P, const Layer &L, int mi, int32_t K, int S,
+                                         int wave) {
+    Geo G;
+    const int b = blockIdx.x, nb = P.nblocks;
+    G.m0 = G.m1 = umat(L.m[mi]);
+    G.nseg = 1;
+    G.seg = 0;
+    const int64_t out = G.m0.out;
+    G.lo = static_cast<uint32_t>(out) * static_cast<uint32_t>(b) / static_cast<uint32_t>(nb);
+    G.n = static_cast<uint32_t>(out) * static_cast<uint32_t>(b + 1) / static_cast<uint32_t>(nb) - G.lo;
+    G.K = K;
+    G.y_off = 0;
+    G.g = make_seg(G.lo, G.n, wave, kWaves, S, nchunks_of(K));
+    return G;
+}
+
+__device__ __forceinline__ Geo geo_pair(const Plan &P, const Layer &L, int wave) {
+    Geo G;
+    const int b = blockIdx.x, nb = P.nblocks;
+    G.m0 = umat(L.m[kG]);
+    G.m1 = umat(L.m[kU]);
+    G.nseg = 2;
+    G.seg = wave / (kWaves / 2);
+    const int64_t out = P.inter;
+    G.lo = static_cast<uint32_t>(out) * static_cast<uint32_t>(b) / static_cast<uint32_t>(nb);
+    G.n = static_cast<uint32_t>(out) * static_cast<uint32_t>(b + 1) / static_cast<uint32_t>(nb) - G.lo;
+    G.K = P.hidden;
+    G.y_off = 0;
+    G.g = make_seg(G.lo, G.n, wave % (kWaves / 2), kWaves / 2, P.s_gu, nchunks_of(G.K));
+    return G;
+}
+
+__device__ __forceinline__ void load_batch(const Mat &M, const Seg &g, int32_t K, int32_t group,
+                                           int64_t t0, int lane, Batch &b) {
+    const bool affine = M.gs != nullptr;
+    const int64_t ngroups = affine ? K / group : 0;
+    const __amdgpu_buffer_rsrc_t qr = urs(M.idx, M.out * K);
+    const __amdgpu_buffer_rsrc_t sr = urs(M.gs, affine ? M.out * ngroups * 4 : 0);
+    const __amdgpu_buffer_rsrc_t orr = urs(M.go, affine ? M.out * ngroups * 4 : 0);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int64_t t = t0 + r;
+        const bool mine = t < g.n_mine;
+        const uint32_t row = static_cast<uint32_t>(g.lo + g.rg + t * g.RG);
+#pragma unroll
+        for (int ci = 0; ci < CPS; ++ci) {
+            const int k0 = (g.c_lo + ci) * kChunk + lane * 16;
+            const bool ok = mine && ci < g.nc && k0 < K;
+            b.q[r][ci] = buf_load16(qr, ok ? row * static_cast<uint32_t>(K) + k0 : kOob);
+            if (affine) {
+                const uint32_t g4 = (row * static_cast<uint32_t>(ngroups) +
+                                     static_cast<uint32_t>(k0) / static_cast<uint32_t>(group)) * 4u;
+                b.sc[r][ci] = buf_loadf(sr, ok ? g4 : kOob);
+                b.of[r][ci] = buf_loadf(orr, ok ? g4 : kOob);
+            } else {
+                b.sc[r][ci] = 1.f;
+                b.of[r][ci] = 0.f;
+            }
+        }
+    }
+}
+
+// Everything a stage needs that does not depend on the barrier.
+__device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, Pre &p) {
+    const int lane = tid & 63;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (s >= G.nseg) break;
+        const Mat &M = s ? G.m1 : G.m0;
+        const __amdgpu_buffer_rsrc_t cr = urs(M.cb, 256 * 4);
+#pragma unroll
+        for (int k = 0; k < kTPW; ++k) {
+            const uint32_t f = tid + k * kThreads;  // float4 slot of the table
+            p.cbv[s][k] = buf_loadf(cr, (f * 4u / NREP) * 4u);
+        }
+        const bool has_sc = M.rp != nullptr;
+        const __amdgpu_buffer_rsrc_t rr = urs(M.rp, has_sc ? (M.out + 1) * 4 : 0);
+        p.b0[s] = buf_loadi(rr, static_cast<uint32_t>(G.lo * 4));
+        p.b1[s] = buf_loadi(rr, static_cast<uint32_t>((G.lo + G.n) * 4));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // small loads first: they return first
+    const Mat &Mw = G.seg ? G.m1 : G.m0;
+    load_batch(Mw, G.g, G.K, group, 0, lane, p.bt[0]);
+}
+
+__device__ __forceinline__ float row_dot(const float *tb, uint32_t lane_off, const Batch &b, int r,
+                                         const float (&xv)[CPS][16], const float (&xs)[CPS]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int ci = 0; ci < CPS; ++ci) {
+        float part = 0.f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t w = b.q[r][ci][d];
+            const float c0 = tbl_lookup<NREP, 0>(tb, lane_off, w);
+            const float c1 = tbl_lookup<NREP, 1>(tb, lane_off, w);
+            const float c2 = tbl_lookup<NREP, 2>(tb, lane_off, w);
+            const float c3 = tbl_lookup<NREP, 3>(tb, lane_off, w);
+            part = fmaf(xv[ci][4 * d + 0], c0, part);
+            part = fmaf(xv[ci][4 * d + 1], c1, part);
+            part = fmaf(xv[ci][4 * d + 2], c2, part);
+            part = fmaf(xv[ci][4 * d + 3], c3, part);
+        }
+        acc = fmaf(part, b.sc[r][ci], acc);
+        acc = fmaf(b.of[r][ci], xs[ci], acc);
+    }
+    return acc;
+}
+
+// Activation sources of a GEMV stage.
+//   XNORM: r = base + delta (fp32, coherent; delta may be null) or the bf16
+//          embedding row emb; x = bf16(w * r * rsqrt(mean(r^2) + eps)); block
+//          0 stores r to res_out.
+//   XBF16: x = bf16 vector (coherent).
+enum { XNORM = 0, XBF16 = 1 };
+
+struct XSrc {
+    const float *base;
+    const float *delta;
+    const uint16_t *emb;
+    const float *w;
+    float *res_out;
+    const uint16_t *xb;
+};
+
+// Builds the stage's activation vector in LDS xl (fp32 [K]) block-wide --
+// each thread handles 4 (XNORM) or 8 (XBF16) consecutive elements, so few
+// registers are live next to the prefetched batches -- then loads the wave's
+// slice into xv / xs (zeros outside it).  `part` is 16 floats of LDS scratch.
+template <int HC, int XM, typename After>
+__device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &G, int tid,
+                                       int lane, float *xl, float *part, float (&xv)[CPS][16],
+                                       float (&xs)[CPS], After after) {
+    const int32_t K = G.K;
+    const int t = tid;
+    if constexpr (XM == XNORM) {
+        // K <= 4096: one float4 per thread
+        const bool mine = t * 4 < K;
+        const uint32_t o4 = mine ? static_cast<uint32_t>(t) * 16u : kOob;
+        float r[4];
+        if (X.emb) {
+            const __amdgpu_buffer_rsrc_t er = urs(X.emb, static_cast<int64_t>(K) * 2);
+            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(er, mine ? t * 8u : kOob, 0, 0);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(er, mine ? t * 8u + 4u : kOob, 0, 0);
+            r[0] = __uint_as_float(lo << 16);
+            r[1] = __uint_as_float(lo & 0xffff0000u);
+            r[2] = __uint_as_float(hi << 16);
+            r[3] = __uint_as_float(hi & 0xffff0000u);
+        } else {
+            const u32x4 a = buf_load16(urs(X.base, static_cast<int64_t>(K) * 4), o4);
+            const u32x4 d = buf_load16(urs(X.delta, X.delta ? static_cast<int64_t>(K) * 4 : 0), o4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[j] = __uint_as_float(a[j]) + __uint_as_float(d[j]);
+        }
+        const u32x4 w = buf_load16(urs(X.w, static_cast<int64_t>(K) * 4), o4);
+        __builtin_amdgcn_sched_barrier(0);
+        after();  // loads that may return after the activations
+        __builtin_amdgcn_sched_barrier(0);
+        if (X.res_out && blockIdx.x == 0 && mine) {
+            u32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = __float_as_uint(r[j]);
+            coh_store16(urs(X.res_out, static_cast<int64_t>(K) * 4), o4, v);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss = fmaf(r[j], r[j], ss);
+        ss = wave_sum_all(ss);
+        if (lane == 0) part[t / kWave] = ss;
+        lds_barrier();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) tot += part[i];
+        const float inv = rsqrtf(tot / K + P.eps);
+        if (mine)
+            *reinterpret_cast<float4 *>(xl + 4 * t) =
+                make_float4(bf16r(__uint_as_float(w[0]) * (r[0] * inv)),
+                            bf16r(__uint_as_float(w[1]) * (r[1] * inv)),
+                            bf16r(__uint_as_float(w[2]) * (r[2] * inv)),
+                            bf16r(__uint_as_float(w[3]) * (r[3] * inv)));
+    } else {
+        // K <= 16384: at most two 16-byte pieces per thread
+        const __amdgpu_buffer_rsrc_t xr = urs(X.xb, static_cast<int64_t>(K) * 2);
+        u32x4 w[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = t + j * kThreads;
+            w[j] = buf_load16(xr, i * 8 < K ? static_cast<uint32_t>(i) * 16u : kOob);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        after();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = t + j * kThreads;
+            if (i * 8 < K) {
+                float4 *dst = reinterpret_cast<float4 *>(xl + 8 * i);
+                dst[0] = make_float4(__uint_as_float(w[j][0] << 16), __uint_as_float(w[j][0] & 0xffff0000u),
+                                     __uint_as_float(w[j][1] << 16), __uint_as_float(w[j][1] & 0xffff0000u));
+                dst[1] = make_float4(__uint_as_float(w[j][2] << 16), __uint_as_float(w[j][2] & 0xffff0000u),
+                                     __uint_as_float(w[j][3] << 16), __uint_as_float(w[j][3] & 0xffff0000u));
+            }
+        }
+    }
+    lds_barrier();  // xl complete
+    const Seg &g = G.g;
+#pragma unroll
+    for (int ci = 0; ci < CPS; ++ci) {
+        const int k0 = (g.c_lo + ci) * kChunk + lane * 16;
+        const bool ok = ci < g.nc && k0 < K;
+        float t2 = 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float4 f = ok ? reinterpret_cast<const float4 *>(xl + k0)[v] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[ci][4 * v] = f.x;
+            xv[ci][4 * v + 1] = f.y;
+            xv[ci][4 * v + 2] = f.z;
+            xv[ci][4 * v + 3] = f.w;
+            t2 += (f.x + f.y) + (f.z + f.w);
+        }
+        xs[ci] = t2;
+    }
+}
+
+// Outputs of a GEMV stage.
+//   YF32: y[y_off + row] fp32 (coherent) for the block's matrix;
+//   YACT: pair stage, act[row] = bf16(silu(gate) * up) (coherent).
+enum { YF32 = 0, YACT = 1 };
+
+// Sum of one row: slices, then sidecar entries in CSR order (the caller
+// adds the bias).
+__device__ __forceinline__ float row_total(const Mat &M, int r, int S, const float *red,
+                                           int32_t j0, int32_t j1, int32_t b0, const float *ent,
+                                           const float *xl) {
+    float v = 0.f;
+    for (int s = 0; s < S; ++s) v += red[r * S + s];
+    if (M.rp) {
+        for (int32_t j = j0; j < j1; ++j) {
+            const int32_t e = j - b0;
+            v += e < kEnt ? ent[e] : xl[M.col[j]] * M.delta[j];
+        }
+    }
+    return v;
+}
+
+template <int HC, int XM, int YM>
+__device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, const XSrc &X,
+                                         void *y, float *smem, int tid, int lane) {
+    const int32_t K = G.K, group = P.group;
+    float *xl = smem + (G.nseg == 2 ? 2 * kTbl : kTbl);
+    float *red = smem + P.lds_red;                           // [2][kRedCap]
+    float *ent = red + 2 * kRedCap;                          // [2][kEnt]
+    int32_t *rps = reinterpret_cast<int32_t *>(ent + 2 * kEnt);  // [2][kRps]
+    float *misc = reinterpret_cast<float *>(rps + 2 * kRps);
+    const int t = tid;
+    // Issue every other load the stage needs before its stream: the CSR row
+    // pointers and biases of the block's rows and its sidecar entries.  They
+    // queue behind the prefetched batches (which the stream needs first
+    // anyway); row pointers and sidecar products go to LDS, so few registers
+    // stay live during the stream.
+    int32_t rpv[2] = {0, 0}, ecol[2] = {0, 0}, nent[2] = {0, 0};
+    float edl[2] = {0.f, 0.f}, bias[2] = {0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (s >= G.nseg) break;
+        const Mat &M = s ? G.m1 : G.m0;
+        const __amdgpu_buffer_rsrc_t rr = urs(M.rp, M.rp ? (M.out + 1) * 4 : 0);
+        rpv[s] = buf_loadi(rr, t <= G.n ? static_cast<uint32_t>((G.lo + t) * 4) : kOob);
+        const __amdgpu_buffer_rsrc_t br = urs(M.bias, M.bias ? M.out * 4 : 0);
+        bias[s] = buf_loadf(br, t < G.n ? static_cast<uint32_t>((G.lo + t) * 4) : kOob);
+        const int32_t b0 = __builtin_amdgcn_readfirstlane(pf.b0[s]);
+        const int32_t b1 = __builtin_amdgcn_readfirstlane(pf.b1[s]);
+        nent[s] = M.rp ? b1 - b0 : 0;
+        const bool mine = t < min(nent[s], kEnt);
+        const __amdgpu_buffer_rsrc_t colr = urs(M.col, M.rp ? static_cast<int64_t>(b1) * 4 : 0);
+        const __amdgpu_buffer_rsrc_t dlr = urs(M.delta, M.rp ? static_cast<int64_t>(b1) * 4 : 0);
+        const uint32_t e4 = mine ? (static_cast<uint32_t>(b0) + t) * 4u : kOob;
+        ecol[s] = buf_loadi(colr, e4);
+        edl[s] = buf_loadf(dlr, e4);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (s >= G.nseg) break;
+        float *tb = smem + s * kTbl;
+#pragma unroll
+        for (int k = 0; k < kTPW; ++k)
+            reinterpret_cast<float4 *>(tb)[t + k * kThreads] =
+                make_float4(pf.cbv[s][k], pf.cbv[s][k], pf.cbv[s][k], pf.cbv[s][k]);
+    }
+    float xv[CPS][16], xs[CPS];
+    const Mat &Mw = G.seg ? G.m1 : G.m0;
+    load_x<HC, XM>(P, X, G, t, lane, xl, misc + 16, xv, xs,  // ends with a barrier: xl ready
+                   [&] { load_batch(Mw, G.g, K, group, RB, lane, pf.bt[1]); });
+    // the loads above have landed by now (they were issued before x's)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (s >= G.nseg) break;
+        if (t <= G.n) rps[s * kRps + t] = rpv[s];
+        if (t < min(nent[s], kEnt)) ent[s * kEnt + t] = xl[ecol[s]] * edl[s];
+    }
+
+    // stream the wave's rows (two batches already in flight)
+    const Seg &g = G.g;
+    const float *tb = smem + G.seg * kTbl;
+    float *redw = red + G.seg * kRedCap;
+    const uint32_t lane_off = static_cast<uint32_t>(lane) * 4u;
+    auto compute = [&](int64_t t0, const Batch &b) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int64_t tt = t0 + r;
+            if (tt < g.n_mine) {
+                const float v = wave_sum_lane63(row_dot(tb, lane_off, b, r, xv, xs));
+                if (lane == kWave - 1) redw[(g.rg + tt * g.RG) * g.S + g.s_id] = v;
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one row's lookups in flight at a time
+        }
+    };
+    for (int64_t i0 = 0; i0 < g.n_mine; i0 += 2 * RB) {
+        compute(i0, pf.bt[0]);
+        if (i0 + RB >= g.n_mine) break;
+        load_batch(Mw, g, K, group, i0 + 2 * RB, lane, pf.bt[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(i0 + RB, pf.bt[1]);
+        if (i0 + 2 * RB >= g.n_mine) break;
+        load_batch(Mw, g, K, group, i0 + 3 * RB, lane, pf.bt[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();  // red and ent complete
+
+    // final pass: one thread per row of the block
+    if (t < G.n) {
+        const int64_t row = G.lo + t;
+        const int S = g.S;
+        const float v0 = row_total(G.m0, t, S, red, rps[t], rps[t + 1], rps[0], ent, xl) + bias[0];
+        if constexpr (YM == YF32) {
+            coh_storef(static_cast<float *>(y) + G.y_off + row, v0);
+        } else {
+            const float v1 = row_total(G.m1, t, S, red + kRedCap, rps[kRps + t],
+                                       rps[kRps + t + 1], rps[kRps], ent + kEnt, xl) + bias[1];
+            coh_store_bf16(static_cast<uint16_t *>(y), P.inter, row, v0 / (1.f + expf(-v0)) * v1);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// attention (one block per query head)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = wave_max_all(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = -FLT_MAX;
+    for (int i = 0; i < kWaves; ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum_all(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < kWaves; ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ void rope_pair(float x1, float x2, int i, int pos, float theta,
+                                          float &o1, float &o2) {
+    const float inv_freq = powf(theta, -2.f * i / kHeadDim);
+    float sn, cs;
+    sincosf(static_cast<float>(pos) * inv_freq, &sn, &cs);
+    o1 = x1 * cs - x2 * sn;
+    o2 = x2 * cs + x1 * sn;
+}
+
+__device__ void attention(const Plan &P, const Layer &L, const float *qkv, uint16_t *attn, int h,
+                          int pos, float *smem) {
+    constexpr int D = kHeadDim;
+    float *sc = smem;                     // [kMaxSeq]
+    float *qs = sc + kMaxSeq;             // [D]
+    float *kn = qs + D;                   // [D]
+    float *vn = kn + D;                   // [D]
+    float *part = vn + D;                 // [kWaves][D]
+    float *red = part + kWaves * D;       // [kWaves]
+    const int grp = P.n_heads / P.n_kv;
+    const int kvh = h / grp;
+    const int n = pos + 1;
+    const float scale = rsqrtf(static_cast<float>(D));
+    const int64_t row = static_cast<int64_t>(P.n_kv) * D;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x / kWave;
+    const float *qh = qkv + static_cast<int64_t>(h) * D;
+    const float *kh = qkv + static_cast<int64_t>(P.n_heads + kvh) * D;
+    const float *vh = qkv + static_cast<int64_t>(P.n_heads + P.n_kv + kvh) * D;
+    const bool writer = h % grp == 0;
+    if (threadIdx.x < D / 2) {
+        const int i = threadIdx.x;
+        float a, b;
+        rope_pair(qh[i], qh[i + D / 2], i, pos, P.theta, a, b);
+        qs[i] = a * scale;
+        qs[i + D / 2] = b * scale;
+        rope_pair(kh[i], kh[i + D / 2], i, pos, P.theta, a, b);
+        const int64_t base = static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D;
+        if (writer) {
+            L.kc[base + i] = f32_to_bf16(a);
+            L.kc[base + i + D / 2] = f32_to_bf16(b);
+        }
+        kn[i] = bf16r(a);
+        kn[i + D / 2] = bf16r(b);
+    } else if (threadIdx.x < D / 2 + D) {
+        const int j = threadIdx.x - D / 2;
+        const float v = vh[j];
+        if (writer) L.vc[static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D + j] = f32_to_bf16(v);
+        vn[j] = bf16r(v);
+    }
+    __syncthreads();
+    float mx = -FLT_MAX;
+    for (int t = threadIdx.x; t < n; t += kThreads) {
+        float s0 = 0.f, s1 = 0.f;
+        if (t == pos) {
+            for (int d = 0; d < D; d += 2) {
+                s0 = fmaf(qs[d], kn[d], s0);
+                s1 = fmaf(qs[d + 1], kn[d + 1], s1);
+            }
+        } else {
+            const u32x4 *kr = reinterpret_cast<const u32x4 *>(
+                L.kc + static_cast<int64_t>(t) * row + static_cast<int64_t>(kvh) * D);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                u32x4 w[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) w[c] = kr[half * 8 + c];
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int d = (half * 8 + c) * 8 + 2 * e;
+                        s0 = fmaf(qs[d], __uint_as_float(w[c][e] << 16), s0);
+                        s1 = fmaf(qs[d + 1], __uint_as_float(w[c][e] & 0xffff0000u), s1);
+                    }
+            }
+        }
+        sc[t] = s0 + s1;
+        mx = fmaxf(mx, s0 + s1);
+    }
+    mx = block_max(mx, red);
+    float sum = 0.f;
+    for (int t = threadIdx.x; t < n; t += kThreads) {
+        const float p = expf(sc[t] - mx);
+        sc[t] = p;
+        sum += p;
+    }
+    sum = block_sum(sum, red);
+    const float inv = 1.f / sum;
+    float a0 = 0.f, a1 = 0.f;
+    const int64_t voff = static_cast<int64_t>(kvh) * D + 2 * lane;
+    for (int t0 = wave; t0 < n; t0 += 8 * kWaves) {
+        float v0[8], v1[8], p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int t = t0 + u * kWaves;
+            const bool ok = t < n && t != pos;
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(
+                L.vc + static_cast<int64_t>(ok ? t : 0) * row + voff);
+            v0[u] = __uint_as_float(w << 16);
+            v1[u] = __uint_as_float(w & 0xffff0000u);
+            p[u] = ok ? sc[t] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a0 = fmaf(p[u], v0[u], a0);
+            a1 = fmaf(p[u], v1[u], a1);
+        }
+    }
+    if (wave == pos % kWaves) {
+        a0 = fmaf(sc[pos], vn[2 * lane], a0);
+        a1 = fmaf(sc[pos], vn[2 * lane + 1], a1);
+    }
+    part[wave * D + 2 * lane] = a0;
+    part[wave * D + 2 * lane + 1] = a1;
+    __syncthreads();
+    if (threadIdx.x < D / 2) {
+        const int d = 2 * threadIdx.x;
+        float v0 = 0.f, v1 = 0.f;
+        for (int w = 0; w < kWaves; ++w) {
+            v0 += part[w * D + d];
+            v1 += part[w * D + d + 1];
+        }
+        const uint32_t packed = static_cast<uint32_t>(f32_to_bf16(v0 * inv)) |
+                                (static_cast<uint32_t>(f32_to_bf16(v1 * inv)) << 16);
+        coh_store_u32(reinterpret_cast<uint32_t *>(attn + static_cast<int64_t>(h) * D + d), packed);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LM head: final norm, tied bf16 embedding rows, per-block argmax
+// ---------------------------------------------------------------------------
+template <int HC>
+struct LmPre {
+    u32x4 w[2][kLmRB][2 * HC];  // 16-byte loads (8 weights) per lane and row
+};
+
+template <int HC>
+__device__ __forceinline__ void lm_load(const Plan &P, int64_t lo, int64_t n, int wave, int lane,
+                                        int64_t t0, u32x4 (&w)[kLmRB][2 * HC]) {
+    const int32_t K = P.hidden;
+    const __amdgpu_buffer_rsrc_t er = urs(P.embed, static_cast<int64_t>(P.vocab) * K * 2);
+#pragma unroll
+    for (int r = 0; r < kLmRB; ++r) {
+        const int64_t rl = wave + (t0 + r) * kWaves;
+        const bool mine = rl < n;
+        const uint32_t rowb = static_cast<uint32_t>((lo + rl) * K * 2);
+#pragma unroll
+        for (int c = 0; c < 2 * HC; ++c) {
+            const uint32_t col = c * 512 + lane * 8;
+            w[r][c] = buf_load16(er, mine && col < static_cast<uint32_t>(K) ? rowb + col * 2 : kOob);
+        }
+    }
+}
+
+template <int HC>
+__device__ void lm_head(const Plan &P, LmPre<HC> &pf, float *smem, int wave, int lane) {
+    const int32_t K = P.hidden;
+    const int b = blockIdx.x, nb = P.nblocks;
+    const int64_t lo = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b) / static_cast<uint32_t>(nb);
+    const int64_t n = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b + 1) / static_cast<uint32_t>(nb) - lo;
+    // h = bf16(final_norm * r * inv), r = xa + dn; lane holds columns c*512 + lane*8 + j
+    float hx[2 * HC][8];
+    float ss = 0.f;
+    const int64_t lL = P.n_layers;
+    const __amdgpu_buffer_rsrc_t ar = urs(P.res + lL * P.ls_hid, static_cast<int64_t>(K) * 4);
+    const __amdgpu_buffer_rsrc_t dr = urs(P.dn + (lL - 1) * P.ls_hid, static_cast<int64_t>(K) * 4);
+    const __amdgpu_buffer_rsrc_t wr = urs(P.final_norm, static_cast<int64_t>(K) * 4);
+#pragma unroll
+    for (int c = 0; c < 2 * HC; ++c) {
+        const uint32_t col = c * 512 + lane * 8;
+        const bool ok = col < static_cast<uint32_t>(K);
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const u32x4 a = buf_load16(ar, ok ? col * 4 + 16u * v : kOob);
+            const u32x4 d = buf_load16(dr, ok ? col * 4 + 16u * v : kOob);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hx[c][4 * v + j] = __uint_as_float(a[j]) + __uint_as_float(d[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(hx[c][j], hx[c][j], ss);
+    }
+    ss = wave_sum_all(ss);
+    const float inv = rsqrtf(ss / K + P.eps);
+#pragma unroll
+    for (int c = 0; c < 2 * HC; ++c) {
+        const uint32_t col = c * 512 + lane * 8;
+        const bool ok = col < static_cast<uint32_t>(K);
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const u32x4 w = buf_load16(wr, ok ? col * 4 + 16u * v : kOob);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                hx[c][4 * v + j] = ok ? bf16r(__uint_as_float(w[j]) * (hx[c][4 * v + j] * inv)) : 0.f;
+        }
+    }
+    float best = -FLT_MAX;
+    int bi = 0x7fffffff;
+    const int64_t n_mine = n > wave ? (n - wave + kWaves - 1) / kWaves : 0;
+    auto compute = [&](int64_t t0, const u32x4 (&w)[kLmRB][2 * HC]) {
+#pragma unroll
+        for (int r = 0; r < kLmRB; ++r) {
+            const int64_t t = t0 + r;
+            if (t < n_mine) {
+                float acc = 0.f;
+#pragma unroll
+                for (int c = 0; c < 2 * HC; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc = fmaf(__uint_as_float(w[r][c][e] << 16), hx[c][2 * e], acc);
+                        acc = fmaf(__uint_as_float(w[r][c][e] & 0xffff0000u), hx[c][2 * e + 1], acc);
+                    }
+                const float v = wave_sum_lane63(acc);
+                const int64_t row = lo + wave + t * kWaves;
+                if (lane == kWave - 1) {
+                    P.logits[row] = v;
+                    if (v > best) { best = v; bi = static_cast<int>(row); }
+                }
+            }
+        }
+    };
+    for (int64_t i0 = 0; i0 < n_mine; i0 += 2 * kLmRB) {
+        compute(i0, pf.w[0]);
+        if (i0 + kLmRB >= n_mine) break;
+        lm_load<HC>(P, lo, n, wave, lane, i0 + 2 * kLmRB, pf.w[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(i0 + kLmRB, pf.w[1]);
+        if (i0 + 2 * kLmRB >= n_mine) break;
+        lm_load<HC>(P, lo, n, wave, lane, i0 + 3 * kLmRB, pf.w[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    float *bv = smem;
+    int *bix = reinterpret_cast<int *>(smem + kWaves);
+    if (lane == kWave - 1) {
+        bv[wave] = best;
+        bix[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = -FLT_MAX;
+        int i = 0x7fffffff;
+        for (int w = 0; w < kWaves; ++w)
+            if (bv[w] > v || (bv[w] == v && bix[w] < i)) { v = bv[w]; i = bix[w]; }
+        coh_storef(P.part_v + b, v);
+        coh_storei(P.part_i + b, i);
+    }
+}
+
+__device__ void final_argmax(const Plan &P, float *smem) {
+    float v = -FLT_MAX;
+    int i = 0x7fffffff;
+    if (static_cast<int>(threadIdx.x) < P.nblocks) {
+        v = P.part_v[threadIdx.x];
+        i = P.part_i[threadIdx.x];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(v, m, kWave);
+        const int oi = __shfl_xor(i, m, kWave);
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+    float *bv = smem;
+    int *bix = reinterpret_cast<int *>(smem + kWaves);
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x / kWave] = v;
+        bix[threadIdx.x / kWave] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 0; w < kWaves; ++w)
+            if (bv[w] > v || (bv[w] == v && bix[w] < i)) { v = bv[w]; i = bix[w]; }
+        *P.tok = i;
+        *P.pos += 1;  // next decode position
+    }
+}
+
+// ---------------------------------------------------------------------------
+// the token kernel
+// ---------------------------------------------------------------------------
+// One layer.  On entry the previous stage has arrived at barrier `target`
+// (layer 0: nothing to wait for); on exit this layer's last stage has arrived.
+template <int HC>
+__device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t &target,
+                                         float *smem, int *sh, int wave0, int tok) {
+    const Layer &L = P.layers[l];
+    Pre pf;
+    // Each stage starts from fresh copies of the thread / wave ids, so values
+    // derived from them are recomputed per stage rather than kept live.
+    int tid = fresh_v(static_cast<int>(threadIdx.x)), wave = fresh_s(wave0), lane = tid & 63;
+    // 1. r = x + delta -> xb; q/k/v = W norm(r)
+    {
+        const Geo G = geo_qkv(P, L, wave);
+        prefetch(G, P.group, tid, pf);
+        if (l > 0 && !wait_all(P, target, sh)) return false;
+        XSrc X{};
+        X.base = P.res + static_cast<int64_t>(l) * P.ls_hid;
+        X.delta = l == 0 ? nullptr : P.dn + static_cast<int64_t>(l - 1) * P.ls_hid;
+        X.emb = l == 0 ? P.embed + static_cast<int64_t>(tok) * P.hidden : nullptr;
+        X.w = uptr(L.in_norm);
+        X.res_out = P.ra + static_cast<int64_t>(l) * P.ls_hid;
+        run_gemv<HC, XNORM, YF32>(P, G, pf, X, P.qkv + static_cast<int64_t>(l) * P.ls_qkv, smem, tid,
+                                  lane);
+    }
+    arrive(P, ++target);
+    tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
+    const Geo Go = geo_plain(P, L, kO, P.n_heads * kHeadDim, P.s_o, wave);
+    prefetch(Go, P.group, tid, pf);
+    // 2. attention: block h waits only for the blocks that computed its q rows
+    // and its kv head's k and v rows; the other blocks go on to wait for the
+    // attention blocks
+    if (static_cast<int>(blockIdx.x) < P.n_heads) {
+        const int h = blockIdx.x, kvh = h / (P.n_heads / P.n_kv);
+        const uint32_t rq = P.n_heads * kHeadDim, rk = P.n_kv * kHeadDim;
+        const uint32_t nq = P.qkv_b1, nk = P.qkv_b2 - P.qkv_b1, nv = P.nblocks - P.qkv_b2;
+        const int q0 = block_of_row(rq, nq, h * kHeadDim);
+        const int q1 = block_of_row(rq, nq, (h + 1) * kHeadDim - 1) + 1;
+        const int k0 = P.qkv_b1 + block_of_row(rk, nk, kvh * kHeadDim);
+        const int k1 = P.qkv_b1 + block_of_row(rk, nk, (kvh + 1) * kHeadDim - 1) + 1;
+        const int v0 = P.qkv_b2 + block_of_row(rk, nv, kvh * kHeadDim);
+        const int v1 = P.qkv_b2 + block_of_row(rk, nv, (kvh + 1) * kHeadDim - 1) + 1;
+        if (!wait_blocks(P, target, sh, q0, q1, k0, k1, v0, v1)) return false;
+        attention(P, L, P.qkv + static_cast<int64_t>(l) * P.ls_qkv,
+                  P.attn + static_cast<int64_t>(l) * P.ls_attn, h, pos, smem);
+    }
+    arrive(P, ++target);
+    if (!wait_blocks(P, target, sh, 0, P.n_heads, 0, 0, 0, 0)) return false;
+    // 3. o = W_o attn
+    {
+        tid = fresh_v(tid), lane = tid & 63;
+        XSrc X{};
+        X.xb = P.attn + static_cast<int64_t>(l) * P.ls_attn;
+        run_gemv<HC, XBF16, YF32>(P, Go, pf, X, P.o + static_cast<int64_t>(l) * P.ls_hid, smem, tid,
+                                  lane);
+    }
+    arrive(P, ++target);
+    {
+        tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
+        const Geo Gp = geo_pair(P, L, wave);
+        prefetch(Gp, P.group, tid, pf);
+        if (!wait_all(P, target, sh)) return false;
+        // 4. r = xb + o -> xa; act = silu(W_g norm(r)) * (W_u norm(r))
+        XSrc X{};
+        X.base = P.ra + static_cast<int64_t>(l) * P.ls_hid;
+        X.delta = P.o + static_cast<int64_t>(l) * P.ls_hid;
+        X.w = uptr(L.post_norm);
+        X.res_out = P.res + static_cast<int64_t>(l + 1) * P.ls_hid;
+        run_gemv<HC, XNORM, YACT>(P, Gp, pf, X, P.act + static_cast<int64_t>(l) * P.ls_act, smem,
+                                  tid, lane);
+    }
+    arrive(P, ++target);
+    {
+        tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
+        const Geo Gd = geo_plain(P, L, kD, P.inter, P.s_down, wave);
+        prefetch(Gd, P.group, tid, pf);
+        if (!wait_all(P, target, sh)) return false;
+        // 5. dn = W_d act
+        XSrc X{};
+        X.xb = P.act + static_cast<int64_t>(l) * P.ls_act;
+        run_gemv<HC, XBF16, YF32>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid, smem, tid,
+                                  lane);
+    }
+    arrive(P, ++target);
+    return true;
+}
+
+template <int HC>
+__global__ __launch_bounds__(kThreads, 1) void token_kernel(const Plan *__restrict__ plan,
+                                                             int32_t step, int32_t *out_ids) {
+    extern __shared__ float smem[];
+    const Plan &P = *plan;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int *sh = reinterpret_cast<int *>(smem + P.lds_red + 2 * kRedCap + 2 * kEnt + 2 * kRps);
+    uint32_t target = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(P.flags + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int pos = __builtin_amdgcn_readfirstlane(*P.pos);
+    const int tok = __builtin_amdgcn_readfirstlane(*P.tok);
+    if (pos < 0 || pos >= P.max_seq || tok < 0 || tok >= P.vocab) {
+        // the host keeps pos < max_seq; a bad state ends the launch everywhere
+        if (threadIdx.x == 0) __hip_atomic_store(P.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0 && out_ids) out_ids[step] = tok;
+#pragma clang loop unroll(disable)
+    for (int l = 0; l < P.n_layers; ++l)
+        if (!do_layer<HC>(P, l, pos, target, smem, sh, wave, tok)) return;
+    {
+        LmPre<HC> lpf;
+        const int b = blockIdx.x, nb = P.nblocks;
+        const int64_t lo = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b) / static_cast<uint32_t>(nb);
+        const int64_t n = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b + 1) / static_cast<uint32_t>(nb) - lo;
+        lm_load<HC>(P, lo, n, wave, lane, 0, lpf.w[0]);
+        lm_load<HC>(P, lo, n, wave, lane, kLmRB, lpf.w[1]);
+        if (!wait_all(P, target, sh)) return;
+        lm_head<HC>(P, lpf, smem, wave, lane);
+    }
+    arrive(P, ++target);
+    if (!wait_all(P, target, sh)) return;
+    if (blockIdx.x == 0) final_argmax(P, smem);
+}
+
+__global__ void clear_sync_kernel(uint32_t *flags, int32_t n, uint32_t *release, int32_t *err) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) flags[i] = 0;
+    if (threadIdx.x == 0) {
+        *release = 0;
+        *err = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct Layout {
+    int64_t plan, layers, res, ra, qkv, o, dn, part_v, part_i, attn, act, flags, release, err, total;
+    int32_t s_hid, s_qkv, s_attn, s_act;  // slot strides in elements (256-byte multiples)
+};
+
+static int64_t align256(int64_t v) { return (v + 255) & ~int64_t{255}; }
+
+static Layout layout_of(const hxq_decoder *d, int nb) {
+    Layout L{};
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) { const int64_t o = off; off = align256(off + bytes); return o; };
+    const int64_t nl = d->n_layers;
+    L.s_hid = static_cast<int32_t>(align256(4LL * d->hidden) / 4);
+    L.s_qkv = static_cast<int32_t>(align256(4LL * (d->n_heads + 2 * d->n_kv_heads) * kHeadDim) / 4);
+    L.s_attn = static_cast<int32_t>(align256(2LL * d->n_heads * kHeadDim) / 2);
+    L.s_act = static_cast<int32_t>(align256(2LL * d->intermediate) / 2);
+    L.plan = take(sizeof(Plan));
+    L.layers = take(static_cast<int64_t>(sizeof(Layer)) * nl);
+    L.res = take(4LL * L.s_hid * (nl + 1));
+    L.ra = take(4LL * L.s_hid * nl);
+    L.qkv = take(4LL * L.s_qkv * nl);
+    L.o = take(4LL * L.s_hid * nl);
+    L.dn = take(4LL * L.s_hid * nl);
+    L.part_v = take(4LL * nb);
+    L.part_i = take(4LL * nb);
+    L.attn = take(2LL * L.s_attn * nl);
+    L.act = take(2LL * L.s_act * nl);
+    L.flags = take(4LL * nb);
+    L.release = take(256);
+    L.err = take(256);
+    L.total = off;
+    return L;
+}
+
+// Slices for a segment of nw waves: every slice at most CPS chunks; fewest
+// chunk-rows per wave, then fewest slices.
+static int choose_slices(int64_t rows, int nw, int nchunks) {
+    int best = -1;
+    int64_t best_cost = INT64_MAX;
+    for (int S = 1; S <= nw && S <= nchunks; ++S) {
+        if ((nchunks + S - 1) / S > CPS) continue;
+        const int RG = nw / S;
+        const int64_t cost = ((rows + RG - 1) / RG) * ((nchunks + S - 1) / S);
+        if (cost < best_cost) { best_cost = cost; best = S; }
+    }
+    return best;
+}
+
+static int lds_red_offset(const hxq_decoder *d) {
+    const int kmax = std::max({d->hidden, d->n_heads * kHeadDim, d->intermediate});
+    const int a = 2 * kTbl + ((d->hidden + 3) & ~3);
+    const int b = kTbl + ((kmax + 3) & ~3);
+    return std::max(a, b);
+}
+
+static size_t lds_bytes(const hxq_decoder *d) {
+    return sizeof(float) * (static_cast<size_t>(lds_red_offset(d)) + 2 * kRedCap + 2 * kEnt + 2 * kRps + 64);
+}
+
+static int hc_of(const hxq_decoder *d) { return d->hidden <= 1024 ? 1 : 2; }
+
+}  // namespace tok
+}  // namespace hxq
+
+using namespace hxq;
+using namespace hxq::tok;
+
+static int check_mat(const hxq_matrix &m, int64_t out, int64_t in, int32_t group, const char *name) {
+    if (!m.indices || !m.codebook) {
+        set_error(std::string("hxq_decoder_init: ") + name + ": indices and codebook are required");
+        return HXQ_ERR_INVALID_ARG;
+    }
+    if (m.out_features != out) {
+        set_error(std::string("hxq_decoder_init: ") + name + ": out_features " +
+                  std::to_string(m.out_features) + ", expected " + std::to_string(out));
+        return HXQ_ERR_INVALID_ARG;
+    }
+    if ((m.group_scale == nullptr) != (m.group_offset == nullptr) ||
+        (m.group_scale && (group <= 0 || group % 16 != 0 || in % group != 0))) {
+        set_error(std::string("hxq_decoder_init: ") + name + ": bad affine / group_size");
+        return HXQ_ERR_INVALID_ARG;
+    }
+    if ((m.sc_row_ptr == nullptr) != (m.sc_col == nullptr) ||
+        (m.sc_row_ptr == nullptr) != (m.sc_delta == nullptr)) {
+        set_error(std::string("hxq_decoder_init: ") + name + ": sidecar arrays must be all set or all NULL");
+        return HXQ_ERR_INVALID_ARG;
+    }
+    if (out * in >= (int64_t{1} << 31)) {
+        set_error(std::string("hxq_decoder_init: ") + name + ": matrix too large");
+        return HXQ_ERR_INVALID_ARG;
+    }
+    return HXQ_OK;
+}
+
+static int validate(const hxq_decoder *d, int nb) {
+    HXQ_REQUIRE(d && d->layers && d->embed && d->final_norm && d->token && d->pos && d->logits,
+                "descriptor pointers are required");
+    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 2048 && d->hidden % 512 == 0,
+                "hidden must be 512..2048, a multiple of 512");
+    HXQ_REQUIRE(d->head_dim == kHeadDim, "head_dim must be 128");
+    HXQ_REQUIRE(d->n_layers >= 1 && d->n_heads >= 1 && d->n_kv_heads >= 1 &&
+                    d->n_heads % d->n_kv_heads == 0 && d->n_heads <= nb,
+                "bad head counts");
+    HXQ_REQUIRE(d->n_heads * kHeadDim <= CPS * kChunk * kWaves, "too many heads");
+    HXQ_REQUIRE(d->intermediate >= 16 && d->intermediate % 16 == 0 &&
+                    d->intermediate <= CPS * kChunk * kWaves,
+                "intermediate must be a multiple of 16, at most 16384");
+    HXQ_REQUIRE(d->max_seq >= 1 && d->max_seq <= kMaxSeq, "max_seq must be 1..1024");
+    HXQ_REQUIRE(d->vocab >= 1 && static_cast<int64_t>(d->vocab) * d->hidden * 2 < (int64_t{1} << 32),
+                "vocab too large");
+    HXQ_REQUIRE(lds_bytes(d) <= 160 * 1024, "LDS budget exceeded (intermediate too large)");
+    const int64_t H = d->hidden, I = d->intermediate, QD = int64_t{d->n_heads} * kHeadDim,
+                  KD = int64_t{d->n_kv_heads} * kHeadDim;
+    for (int l = 0; l < d->n_layers; ++l) {
+        const hxq_decoder_layer &L = d->layers[l];
+        HXQ_REQUIRE(L.in_norm && L.post_norm && L.k_cache && L.v_cache, "layer norms and caches are required");
+        HXQ_REQUIRE(reinterpret_cast<uintptr_t>(L.k_cache) % 16 == 0, "k_cache must be 16-byte aligned");
+        if (int rc = check_mat(L.q, QD, H, d->group_size, "q")) return rc;
+        if (int rc = check_mat(L.k, KD, H, d->group_size, "k")) return rc;
+        if (int rc = check_mat(L.v, KD, H, d->group_size, "v")) return rc;
+        if (int rc = check_mat(L.o, H, QD, d->group_size, "o")) return rc;
+        if (int rc = check_mat(L.gate, I, H, d->group_size, "gate")) return rc;
+        if (int rc = check_mat(L.up, I, H, d->group_size, "up")) return rc;
+        if (int rc = check_mat(L.down, H, I, d->group_size, "down")) return rc;
+    }
+    return HXQ_OK;
+}
+
+static Mat mat_of(const hxq_matrix &m) {
+    Mat r;
+    r.idx = m.indices;
+    r.cb = m.codebook;
+    r.gs = m.group_scale;
+    r.go = m.group_offset;
+    r.rp = m.sc_row_ptr;
+    r.col = m.sc_col;
+    r.delta = m.sc_delta;
+    r.bias = m.bias;
+    r.out = m.out_features;
+    return r;
+}
+
+extern "C" int64_t hxq_decoder_workspace_bytes(const hxq_decoder *d) {
+    clear_error();
+    if (!d) return -1;
+    return layout_of(d, device_cu_count()).total;
+}
+
+extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t workspace_bytes,
+                                hipStream_t stream) {
+    clear_error();
+    const int nb = device_cu_count();
+    if (int rc = validate(d, nb)) return rc;
+    const Layout lay = layout_of(d, nb);
+    HXQ_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small");
+    HXQ_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+    char *ws = static_cast<char *>(workspace);
+
+    // q/k/v block split in proportion to rows (every matrix at least one block)
+    const int64_t rq = int64_t{d->n_heads} * kHeadDim, rk = int64_t{d->n_kv_heads} * kHeadDim;
+    const int64_t rt = rq + 2 * rk;
+    int bq = static_cast<int>((nb * rq + rt / 2) / rt);
+    int bk = static_cast<int>((nb * rk + rt / 2) / rt);
+    bq = std::max(1, std::min(bq, nb - 2));
+    bk = std::max(1, std::min(bk, nb - bq - 1));
+    const int bv = nb - bq - bk;
+    const int nch_h = (d->hidden + kChunk - 1) / kChunk;
+    const int nch_o = (d->n_heads * kHeadDim + kChunk - 1) / kChunk;
+    const int nch_i = (d->intermediate + kChunk - 1) / kChunk;
+    const int64_t rows_qkv = std::max({(rq + bq - 1) / bq, (rk + bk - 1) / bk, (rk + bv - 1) / bv});
+    const int64_t rows_o = (d->hidden + nb - 1) / nb;
+    const int64_t rows_gu = (d->intermediate + nb - 1) / nb;
+    const int64_t rows_d = (d->hidden + nb - 1) / nb;
+    Plan P{};
+    P.hidden = d->hidden;
+    P.n_layers = d->n_layers;
+    P.n_heads = d->n_heads;
+    P.n_kv = d->n_kv_heads;
+    P.inter = d->intermediate;
+    P.vocab = d->vocab;
+    P.max_seq = d->max_seq;
+    P.group = d->group_size > 0 ? d->group_size : 16;
+    P.nblocks = nb;
+    P.eps = d->rms_eps;
+    P.theta = d->rope_theta;
+    P.qkv_b1 = bq;
+    P.qkv_b2 = bq + bk;
+    P.s_qkv = choose_slices(rows_qkv, kWaves, nch_h);
+    P.s_o = choose_slices(rows_o, kWaves, nch_o);
+    P.s_gu = choose_slices(rows_gu, kWaves / 2, nch_h);
+    P.s_down = choose_slices(rows_d, kWaves, nch_i);
+    HXQ_REQUIRE(P.s_qkv > 0 && P.s_o > 0 && P.s_gu > 0 && P.s_down > 0, "no slice split fits");
+    HXQ_REQUIRE(rows_qkv <= kThreads && rows_o <= kThreads && rows_gu <= kThreads &&
+                    rows_qkv * P.s_qkv <= kRedCap && rows_o * P.s_o <= kRedCap &&
+                    rows_gu * P.s_gu <= kRedCap && rows_d * P.s_down <= kRedCap,
+                "too many rows per block for this GPU");
+    P.lds_red = lds_red_offset(d);
+    P.embed = d->embed;
+    P.final_norm = d->final_norm;
+    P.tok = d->token;
+    P.pos = d->pos;
+    P.logits = d->logits;
+    P.layers = reinterpret_cast<const Layer *>(ws + lay.layers);
+    P.res = reinterpret_cast<float *>(ws + lay.res);
+    P.ra = reinterpret_cast<float *>(ws + lay.ra);
+    P.qkv = reinterpret_cast<float *>(ws + lay.qkv);
+    P.o = reinterpret_cast<float *>(ws + lay.o);
+    P.dn = reinterpret_cast<float *>(ws + lay.dn);
+    P.part_v = reinterpret_cast<float *>(ws + lay.part_v);
+    P.part_i = reinterpret_cast<int32_t *>(ws + lay.part_i);
+    P.attn = reinterpret_cast<uint16_t *>(ws + lay.attn);
+    P.act = reinterpret_cast<uint16_t *>(ws + lay.act);
+    P.ls_hid = lay.s_hid;
+    P.ls_qkv = lay.s_qkv;
+    P.ls_attn = lay.s_attn;
+    P.ls_act = lay.s_act;
+    P.flags = reinterpret_cast<uint32_t *>(ws + lay.flags);
+    P.release = reinterpret_cast<uint32_t *>(ws + lay.release);
+    P.err = reinterpret_cast<int32_t *>(ws + lay.err);
+
+    std::vector<Layer> layers(d->n_layers);
+    for (int l = 0; l < d->n_layers; ++l) {
+        const hxq_decoder_layer &s = d->layers[l];
+        Layer &L = layers[l];
+        L.m[kQ] = mat_of(s.q);
+        L.m[kK] = mat_of(s.k);
+        L.m[kV] = mat_of(s.v);
+        L.m[kO] = mat_of(s.o);
+        L.m[kG] = mat_of(s.gate);
+        L.m[kU] = mat_of(s.up);
+        L.m[kD] = mat_of(s.down);
+        L.in_norm = s.in_norm;
+        L.post_norm = s.post_norm;
+        L.kc = s.k_cache;
+        L.vc = s.v_cache;
+    }
+    HXQ_HIP_TRY(hipMemcpyAsync(ws + lay.plan, &P, sizeof(Plan), hipMemcpyHostToDevice, stream));
+    HXQ_HIP_TRY(hipMemcpyAsync(ws + lay.layers, layers.data(), sizeof(Layer) * layers.size(),
+                               hipMemcpyHostToDevice, stream));
+    hipLaunchKernelGGL(clear_sync_kernel, dim3(1), dim3(256), 0, stream, P.flags, nb, P.release, P.err);
+    HXQ_LAUNCH_CHECK();
+    HXQ_HIP_TRY(hipStreamSynchronize(stream));  // host staging buffers go out of scope
+    return HXQ_OK;
+}
+
+template <int HC>
+static int launch_steps(const hxq_decoder *d, void *workspace, int32_t n_steps, int32_t *out_ids,
+                        hipStream_t stream) {
+    const size_t lds = lds_bytes(d);
+    const void *fn = reinterpret_cast<const void *>(&token_kernel<HC>);
+    HXQ_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    int occ = 0;
+    HXQ_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, token_kernel<HC>, kThreads, lds));
+    HXQ_REQUIRE(occ >= 1, "the token kernel does not fit on a compute unit");
+    const Plan *plan = reinterpret_cast<const Plan *>(workspace);
+    const int nb = device_cu_count();
+    for (int32_t s = 0; s < n_steps; ++s) {
+        int32_t step = s;
+        void *args[] = {&plan, &step, &out_ids};
+        HXQ_HIP_TRY(hipLaunchCooperativeKernel(fn, dim3(nb), dim3(kThreads), args, lds, stream));
+    }
+    return HXQ_OK;
+}
+
+extern "C" int hxq_decoder_step(const hxq_decoder *d, void *workspace, int32_t n_steps,
+                                int32_t *out_ids, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(d && workspace && n_steps >= 0, "bad arguments");
+    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 2048, "hidden must be 512..2048");
+    if (hc_of(d) == 1) return launch_steps<1>(d, workspace, n_steps, out_ids, stream);
+    return launch_steps<2>(d, workspace, n_steps, out_ids, stream);
+}
+
+extern "C" int hxq_decoder_error(const void *workspace, const hxq_decoder *d, int32_t *err_out,
+                                 hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(workspace && d && err_out, "bad arguments");
+    const Layout lay = layout_of(d, device_cu_count());
+    HXQ_HIP_TRY(hipMemcpyAsync(err_out, static_cast<const char *>(workspace) + lay.err, 4,
+                               hipMemcpyDeviceToHost, stream));
+    HXQ_HIP_TRY(hipStreamSynchronize(stream));
+    return HXQ_OK;
+}

@@ -47,6 +47,27 @@ class HxqExpertBank(ctypes.Structure):
     ]
 
 
+class HxqDecoderLayer(ctypes.Structure):
+    """Mirror of ``hxq_decoder_layer`` in include/hxq.h."""
+
+    _fields_ = [
+        ("q", HxqMatrix), ("k", HxqMatrix), ("v", HxqMatrix), ("o", HxqMatrix),
+        ("gate", HxqMatrix), ("up", HxqMatrix), ("down", HxqMatrix),
+        ("in_norm", P), ("post_norm", P), ("k_cache", P), ("v_cache", P),
+    ]
+
+
+class HxqDecoder(ctypes.Structure):
+    """Mirror of ``hxq_decoder`` in include/hxq.h (``layers`` is a host array)."""
+
+    _fields_ = [
+        ("hidden", I32), ("n_layers", I32), ("n_heads", I32), ("n_kv_heads", I32),
+        ("head_dim", I32), ("intermediate", I32), ("vocab", I32), ("max_seq", I32),
+        ("group_size", I32), ("rms_eps", F32), ("rope_theta", F32),
+        ("layers", P), ("embed", P), ("final_norm", P), ("token", P), ("pos", P), ("logits", P),
+    ]
+
+
 # name -> argtypes; every function returns int (hxq_status)
 SIGNATURES = {
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
@@ -75,6 +96,9 @@ SIGNATURES = {
     "hxq_argmax": [P, I64, P, P, P, P],
     "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
     "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
+    "hxq_decoder_init": [P, P, I64, P],
+    "hxq_decoder_step": [P, P, I32, P, P],
+    "hxq_decoder_error": [P, P, P, P],
 }
 
 
@@ -82,6 +106,7 @@ SIGNATURES = {
 SIGNATURES_I64 = {
     "hxq_ssm_scan_workspace_bytes": [I64] * 6,
     "hxq_moe_ffn_workspace_bytes": [I64, I64, I64, I32],
+    "hxq_decoder_workspace_bytes": [P],
 }
 
 
@@ -541,3 +566,44 @@ def argmax(logits, out_id, pos=None, workspace=None):
                           _stream(logits))
     _check("hxq_argmax", rc)
     return out_id
+
+
+# -- whole decode step in one launch per token ---------------------------------
+def hxq_matrix_of(m):
+    """hxq_matrix of a HelixLinear (y unused)."""
+    def p(t):
+        return 0 if t is None else t.data_ptr()
+    _need_device(m.indices, m.codebook, m.group_scale, m.group_offset, m._sc_row_ptr, m._sc_col,
+                 m._sc_delta, m.bias)
+    return HxqMatrix(m.indices.data_ptr(), m.codebook.data_ptr(), p(m.group_scale),
+                     p(m.group_offset), p(m._sc_row_ptr), p(m._sc_col), p(m._sc_delta), p(m.bias),
+                     0, m.out_features)
+
+
+def decoder_workspace_bytes(desc: HxqDecoder) -> int:
+    return int(lib().hxq_decoder_workspace_bytes(ctypes.addressof(desc)))
+
+
+def decoder_init(desc: HxqDecoder, workspace: torch.Tensor) -> None:
+    _need_device(workspace)
+    rc = lib().hxq_decoder_init(ctypes.addressof(desc), _ptr(workspace), workspace.numel(),
+                                _stream(workspace))
+    _check("hxq_decoder_init", rc)
+
+
+def decoder_step(desc: HxqDecoder, workspace: torch.Tensor, n_steps: int = 1, out_ids=None) -> None:
+    if out_ids is not None:
+        _need_device(workspace, out_ids)
+        if out_ids.dtype != torch.int32 or out_ids.numel() < n_steps:
+            raise RuntimeError("out_ids must be int32 with at least n_steps elements")
+    rc = lib().hxq_decoder_step(ctypes.addressof(desc), _ptr(workspace), int(n_steps),
+                                _ptr(out_ids), _stream(workspace))
+    _check("hxq_decoder_step", rc)
+
+
+def decoder_error(desc: HxqDecoder, workspace: torch.Tensor) -> int:
+    err = ctypes.c_int32(0)
+    rc = lib().hxq_decoder_error(_ptr(workspace), ctypes.addressof(desc), ctypes.addressof(err),
+                                 _stream(workspace))
+    _check("hxq_decoder_error", rc)
+    return int(err.value)

@@ -15,6 +15,7 @@ stream is kept in fp32, activations entering the GEMVs are bf16.
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -231,6 +232,49 @@ class HelixDecoder:
                 self._graph.replay()
             else:
                 self._step_launches()
+        return out
+
+    # -- one launch per token (persistent kernel) ---------------------------------
+    def persistent_init(self):
+        """Prepare hxq_decoder_step: one cooperative launch runs a whole token
+        (every layer, LM head and argmax) with grid barriers between stages;
+        same math as _step_launches.  Shares this decoder's buffers (token,
+        position, caches, logits)."""
+        c = self.cfg
+        n = len(self.layers)
+        arr = (_hxq.HxqDecoderLayer * n)()
+        for i, L in enumerate(self.layers):
+            arr[i] = _hxq.HxqDecoderLayer(
+                *(_hxq.hxq_matrix_of(L[name]) for name in _PROJ),
+                L["in_norm"].data_ptr(), L["post_norm"].data_ptr(), self.kc[i].data_ptr(),
+                self.vc[i].data_ptr())
+        desc = _hxq.HxqDecoder(c.hidden, n, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate,
+                               c.vocab, c.max_seq, self._group, c.rms_eps, c.rope_theta,
+                               ctypes.addressof(arr), self.embed.data_ptr(),
+                               self.final_norm.data_ptr(), self.tok.data_ptr(),
+                               self.pos.data_ptr(), self.logits.data_ptr())
+        ws = torch.empty(_hxq.decoder_workspace_bytes(desc), dtype=torch.uint8, device=self.device)
+        _hxq.decoder_init(desc, ws)
+        self._p_layers, self._p_desc, self._p_ws = arr, desc, ws
+        return self
+
+    def step_persistent(self, n_steps=1, out_ids=None):
+        """n_steps greedy steps, one launch each (no host synchronisation)."""
+        if getattr(self, "_p_desc", None) is None:
+            self.persistent_init()
+        _hxq.decoder_step(self._p_desc, self._p_ws, n_steps, out_ids)
+
+    def persistent_error(self):
+        """0 when every step completed; 1 = a grid barrier timed out; 2 = bad
+        token / position.  Synchronises the stream."""
+        return _hxq.decoder_error(self._p_desc, self._p_ws)
+
+    def generate_persistent(self, n_new):
+        """generate() through the one-launch-per-token kernel."""
+        if int(self.pos.item()) + n_new > self.cfg.max_seq:
+            raise ValueError("generation would exceed max_seq")
+        out = torch.empty(n_new, dtype=torch.int32, device=self.device)
+        self.step_persistent(n_new, out)
         return out
 
     def hxq_bytes_per_token(self):

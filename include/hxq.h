@@ -336,6 +336,61 @@ int hxq_argmax(const float *logits, int64_t n, int32_t *out_id, int32_t *pos,
                void *workspace, hipStream_t stream);
 
 /*
+ * Whole greedy decode step in ONE launch per token (persistent kernel, one
+ * 16-wave block per compute unit, grid barriers between the stages; the
+ * next stage's compressed weights are fetched while the grid synchronises).
+ * Per layer: r = x + delta, q/k/v = W norm(r) (+bias); RoPE, KV append and
+ * GQA attention; o = W_o attn; r' = r + o, act = silu(W_g norm(r')) *
+ * (W_u norm(r')); delta = W_d act.  Then logits = E norm(x + delta) (tied
+ * bf16 embedding E), *token = argmax (ties -> lowest id), ++*pos.  The step
+ * embeds *token at position *pos; out_ids[i] (optional) receives the token
+ * fed into step i.  Same math as the per-kernel sequence above.
+ * No reference counterpart: it replaces the HF decoder-layer loop around
+ * HelixLinear.forward (helix_linear.py:318-361) for benchmark config 1.
+ *
+ * hxq_decoder_layer holds one layer's seven HXQ matrices (the y fields are
+ * ignored), fp32 norm weights and bf16 caches [max_seq, n_kv_heads, 128].
+ * hxq_decoder: sizes, a HOST array of layers, device embedding / final norm,
+ * device token and position words, device fp32 logits [vocab].
+ * Limits: hidden 512..2048 (multiple of 512), head_dim 128, max_seq <= 1024,
+ * n_heads <= number of compute units.
+ * hxq_decoder_init copies the layer table into `workspace` (device, 256-byte
+ * aligned, >= hxq_decoder_workspace_bytes) and clears the barrier state;
+ * hxq_decoder_step runs n_steps tokens (n_steps launches, no host sync);
+ * hxq_decoder_error copies the barrier error word (0 = fine; 1 = a grid
+ * barrier timed out; 2 = token/position out of range) to *err_out and
+ * synchronises the stream.  A workspace serves one stream at a time.
+ */
+typedef struct hxq_decoder_layer {
+    hxq_matrix q, k, v, o, gate, up, down;
+    const float *in_norm;
+    const float *post_norm;
+    uint16_t *k_cache;
+    uint16_t *v_cache;
+} hxq_decoder_layer;
+
+typedef struct hxq_decoder {
+    int32_t hidden, n_layers, n_heads, n_kv_heads, head_dim, intermediate, vocab, max_seq;
+    int32_t group_size;
+    float rms_eps;
+    float rope_theta;
+    const hxq_decoder_layer *layers;
+    const uint16_t *embed;
+    const float *final_norm;
+    int32_t *token;
+    int32_t *pos;
+    float *logits;
+} hxq_decoder;
+
+int64_t hxq_decoder_workspace_bytes(const hxq_decoder *d);
+int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t workspace_bytes,
+                     hipStream_t stream);
+int hxq_decoder_step(const hxq_decoder *d, void *workspace, int32_t n_steps, int32_t *out_ids,
+                     hipStream_t stream);
+int hxq_decoder_error(const void *workspace, const hxq_decoder *d, int32_t *err_out,
+                      hipStream_t stream);
+
+/*
  * Selective scan (Mamba/Mamba2), fp32 state, chunk-parallel:
  *   a_t = exp(A[h] dt[b,t,h]);  h_t = a_t h_{t-1} + dt[b,t,h] x[b,t,h,p] B[b,t,g,n]
  *   y[b,t,h,p] = sum_n h_t C[b,t,g,n] + D[h] x[b,t,h,p],  g = h / (heads/ngroups)

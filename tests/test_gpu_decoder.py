@@ -109,3 +109,88 @@ def test_fused_prologue_gemv_matches_separate_kernels(dev):
         _hxq.silu_mul(x, up, act)
         ys_ref = _hxq.gemv_multi(act, mats, 128)[0]
         assert torch.equal(ys, ys_ref)
+
+
+CFG2 = DecoderConfig(hidden=2048, n_layers=2, n_heads=16, n_kv_heads=2, head_dim=128,
+                     intermediate=1408, vocab=4096, rope_theta=1e6, rms_eps=1e-6, max_seq=96)
+
+
+@pytest.mark.parametrize("cfg", [CFG, CFG2], ids=["hidden512", "hidden2048"])
+def test_persistent_step_matches_launch_sequence_and_oracle(dev, cfg):
+    """hxq_decoder_step (one launch per token) against the per-kernel launch
+    sequence on the same weights (5e-3 of max|logit|: the two paths sum the
+    norms in different orders, so a bf16 rounding of the GEMV input may
+    differ) and against the fp64 oracle at the bf16 bar."""
+    global CFG
+    saved, CFG = CFG, cfg
+    try:
+        mk = lambda o, i, s: synth.make_layer_np(o, i, seed=s, group_size=64)
+        a = HelixDecoder.synthetic(cfg, seed=3, device=dev, layer_fn=mk)
+        b = HelixDecoder.synthetic(cfg, seed=3, device=dev, layer_fn=mk)
+        b.persistent_init()
+        prompt = [7, 0, cfg.vocab - 1, 100, 55, 3]
+        ref = _oracle_logits(a, prompt)
+        for t, tok in enumerate(prompt):
+            a.tok.fill_(tok)
+            b.tok.fill_(tok)
+            a._step_launches()
+            b.step_persistent(1)
+            la, lb = a.logits.cpu().numpy(), b.logits.cpu().numpy()
+            scale = np.abs(la).max()
+            assert np.abs(la - lb).max() <= 5e-3 * scale, (t, np.abs(la - lb).max() / scale)
+            assert np.abs(lb - ref[t]).max() <= 2e-2 * np.abs(ref[t]).max(), t
+            assert int(b.pos.item()) == t + 1
+            assert int(b.tok.item()) == int(np.argmax(lb))
+        assert b.persistent_error() == 0
+        # the KV caches the two paths wrote agree
+        for kc_a, kc_b in zip(a.kc, b.kc):
+            d = (kc_a[:len(prompt)].float() - kc_b[:len(prompt)].float()).abs().max().item()
+            assert d <= 2e-2 * kc_a[:len(prompt)].float().abs().max().item()
+    finally:
+        CFG = saved
+
+
+def test_persistent_generate_matches_launch_sequence(dev):
+    """Greedy tokens from n_steps back-to-back launches (no host sync) equal the
+    graph path's while the top-2 margin of the graph path's logits is clear."""
+    a, b = _build(dev, seed=4), _build(dev, seed=4)
+    prompt = [2, 7, 1, 8, 2, 8]
+    a.prefill(prompt)
+    a.capture()
+    b.persistent_init()
+    for tok in prompt:
+        b.tok.fill_(tok)
+        b.step_persistent(1)
+    assert int(a.tok.item()) == int(b.tok.item())
+    n = 8
+    out_b = b.generate_persistent(n).cpu().numpy()
+    margins = []
+    out_a = []
+    for _ in range(n):
+        out_a.append(int(a.tok.item()))
+        a._graph.replay()
+        top2 = np.sort(a.logits.cpu().numpy())[-2:]
+        margins.append(top2[1] - top2[0])
+    assert b.persistent_error() == 0
+    assert int(b.pos.item()) == len(prompt) + n
+    for t in range(n):
+        assert out_b[t] == out_a[t], t
+        if margins[t] < 1e-2 * np.abs(a.logits.cpu().numpy()).max():
+            break
+
+
+def test_persistent_rejects_position_out_of_range(dev):
+    """A position at max_seq ends the launch in every block before any barrier
+    and reports error 2; a fresh init clears it."""
+    b = _build(dev, seed=5)
+    b.persistent_init()
+    b.pos.fill_(CFG.max_seq)
+    b.step_persistent(1)
+    assert b.persistent_error() == 2
+    assert int(b.pos.item()) == CFG.max_seq
+    b.pos.zero_()
+    b.persistent_init()
+    b.tok.fill_(1)
+    b.step_persistent(1)
+    assert b.persistent_error() == 0
+    assert int(b.pos.item()) == 1
