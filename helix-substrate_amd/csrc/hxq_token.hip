@@ -476,7 +476,26 @@ __device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, P
     load_batch(Mw, G.g, G.K, group, 0, lane, p.bt[0]);
 }
 
-__device__ __forceinline__ float row_dot(const float *tb, uint32_t lane_off, const Batch &b, int r,
+// Codebook lookup of byte B of the packed index word w.  Tables start at LDS
+// address 0 (the kernel has no static LDS; checked at launch start), table t
+// at t * 65536 bytes, entry j replica r at byte 256 j + 4 r.  One v_perm
+// builds the whole byte address {0, t, w.byte[B], 4 * lane} from
+// lane_seg = (t << 16) | (4 * lane).
+typedef __attribute__((address_space(3))) const float lds_cfloat;
+
+template <int B>
+__device__ __forceinline__ float tok_lookup(uint32_t lane_seg, uint32_t w) {
+    constexpr uint32_t sel = (12u << 24) | (6u << 16) | (static_cast<uint32_t>(B) << 8) | 4u;
+    const uint32_t addr = __builtin_amdgcn_perm(lane_seg, w, sel);
+    return *reinterpret_cast<lds_cfloat *>(static_cast<uintptr_t>(addr));
+}
+
+__device__ __forceinline__ uint32_t lds_offset_of(const float *p) {
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const float *)p));
+}
+
+__device__ __forceinline__ float row_dot(uint32_t lane_seg, const Batch &b, int r,
                                          const float (&xv)[CPS][16], const float (&xs)[CPS]) {
     float acc = 0.f;
 #pragma unroll
@@ -485,10 +504,10 @@ __device__ __forceinline__ float row_dot(const float *tb, uint32_t lane_off, con
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t w = b.q[r][ci][d];
-            const float c0 = tbl_lookup<NREP, 0>(tb, lane_off, w);
-            const float c1 = tbl_lookup<NREP, 1>(tb, lane_off, w);
-            const float c2 = tbl_lookup<NREP, 2>(tb, lane_off, w);
-            const float c3 = tbl_lookup<NREP, 3>(tb, lane_off, w);
+            const float c0 = tok_lookup<0>(lane_seg, w);
+            const float c1 = tok_lookup<1>(lane_seg, w);
+            const float c2 = tok_lookup<2>(lane_seg, w);
+            const float c3 = tok_lookup<3>(lane_seg, w);
             part = fmaf(xv[ci][4 * d + 0], c0, part);
             part = fmaf(xv[ci][4 * d + 1], c1, part);
             part = fmaf(xv[ci][4 * d + 2], c2, part);
@@ -694,15 +713,14 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
 
     // stream the wave's rows (two batches already in flight)
     const Seg &g = G.g;
-    const float *tb = smem + G.seg * kTbl;
     float *redw = red + G.seg * kRedCap;
-    const uint32_t lane_off = static_cast<uint32_t>(lane) * 4u;
+    const uint32_t lane_seg = (static_cast<uint32_t>(G.seg) << 16) | (static_cast<uint32_t>(lane) * 4u);
     auto compute = [&](int64_t t0, const Batch &b) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
             const int64_t tt = t0 + r;
             if (tt < g.n_mine) {
-                const float v = wave_sum_lane63(row_dot(tb, lane_off, b, r, xv, xs));
+                const float v = wave_sum_lane63(row_dot(lane_seg, b, r, xv, xs));
                 if (lane == kWave - 1) redw[(g.rg + tt * g.RG) * g.S + g.s_id] = v;
             }
             __builtin_amdgcn_sched_barrier(0);  // one row's lookups in flight at a time
@@ -758,17 +776,38 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return t;
 }
 
-__device__ __forceinline__ void rope_pair(float x1, float x2, int i, int pos, float theta,
-                                          float &o1, float &o2) {
-    const float inv_freq = powf(theta, -2.f * i / kHeadDim);
-    float sn, cs;
-    sincosf(static_cast<float>(pos) * inv_freq, &sn, &cs);
-    o1 = x1 * cs - x2 * sn;
-    o2 = x2 * cs + x1 * sn;
+
+// Rotation of element pair (i, i + D/2) by the angle table entry cs = (cos, sin).
+__device__ __forceinline__ void rope_rot(float x1, float x2, float2 cs, float &o1, float &o2) {
+    o1 = x1 * cs.x - x2 * cs.y;
+    o2 = x2 * cs.x + x1 * cs.y;
 }
 
-__device__ void attention(const Plan &P, const Layer &L, const float *qkv, uint16_t *attn, int h,
-                          int pos, float *smem) {
+// cos / sin of pos * theta^(-2i/D), i < D/2: the same for every layer of a
+// token, so attention blocks compute them once per launch into LDS.
+__device__ __forceinline__ void rope_table(const Plan &P, int pos, float2 *tab) {
+    if (threadIdx.x < kHeadDim / 2) {
+        const int i = threadIdx.x;
+        const float inv_freq = powf(P.theta, -2.f * i / kHeadDim);
+        float sn, cs;
+        sincosf(static_cast<float>(pos) * inv_freq, &sn, &cs);
+        tab[i] = make_float2(cs, sn);
+    }
+}
+
+// One block per query head: softmax(q . k_t * D^-1/2, t <= pos) . v_t over
+// the head's KV group (head h reads kv head h / (n_heads / n_kv)).
+//   The cache rows of earlier positions do not depend on this token: each
+//   thread's key row (position = thread) and each wave's first eight value
+//   rows are loaded BEFORE waiting for the q/k/v producers (`wait`), so they
+//   arrive while the block waits.  Then q and the new key are rotated
+//   (angle table in LDS), the new key/value are stored into the caches by
+//   the first head of each group, scores are one position per thread,
+//   softmax by block reductions, and the output is summed by wave over
+//   positions (lane = 2 dims) and across waves in LDS.
+template <typename Wait>
+__device__ bool attention(const Plan &P, const Layer &L, const float *qkv, uint16_t *attn, int h,
+                          int pos, float *smem, const float2 *rope, Wait wait) {
     constexpr int D = kHeadDim;
     float *sc = smem;                     // [kMaxSeq]
     float *qs = sc + kMaxSeq;             // [D]
@@ -779,36 +818,58 @@ __device__ void attention(const Plan &P, const Layer &L, const float *qkv, uint1
     const int grp = P.n_heads / P.n_kv;
     const int kvh = h / grp;
     const int n = pos + 1;
-    const float scale = rsqrtf(static_cast<float>(D));
-    const int64_t row = static_cast<int64_t>(P.n_kv) * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x / kWave;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t / kWave;
+    const int64_t row = static_cast<int64_t>(P.n_kv) * D;  // cache elements between positions
+    const uint16_t *kc = uptr(L.kc), *vcache = uptr(L.vc);
+    // earlier positions' cache rows
+    const __amdgpu_buffer_rsrc_t kr = urs(kc, static_cast<int64_t>(P.max_seq) * row * 2);
+    const __amdgpu_buffer_rsrc_t vr = urs(vcache, static_cast<int64_t>(P.max_seq) * row * 2);
+    u32x4 kw[D / 8];
+    {
+        const bool mine = t < pos;
+        const uint32_t base = static_cast<uint32_t>((t * row + static_cast<int64_t>(kvh) * D) * 2);
+#pragma unroll
+        for (int c = 0; c < D / 8; ++c) kw[c] = buf_load16(kr, mine ? base + 16u * c : kOob);
+    }
+    uint32_t vw[8];
+    const uint32_t voff = static_cast<uint32_t>((static_cast<int64_t>(kvh) * D + 2 * lane) * 2);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int tt = wave + u * kWaves;
+        vw[u] = __builtin_amdgcn_raw_buffer_load_b32(
+            vr, tt < pos ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
+    }
+    if (!wait()) return false;
+    // this token's q, k, v
     const float *qh = qkv + static_cast<int64_t>(h) * D;
     const float *kh = qkv + static_cast<int64_t>(P.n_heads + kvh) * D;
     const float *vh = qkv + static_cast<int64_t>(P.n_heads + P.n_kv + kvh) * D;
     const bool writer = h % grp == 0;
-    if (threadIdx.x < D / 2) {
-        const int i = threadIdx.x;
+    const float scale = rsqrtf(static_cast<float>(D));
+    if (t < D / 2) {
+        const float2 cs = rope[t];
         float a, b;
-        rope_pair(qh[i], qh[i + D / 2], i, pos, P.theta, a, b);
-        qs[i] = a * scale;
-        qs[i + D / 2] = b * scale;
-        rope_pair(kh[i], kh[i + D / 2], i, pos, P.theta, a, b);
+        rope_rot(qh[t], qh[t + D / 2], cs, a, b);
+        qs[t] = a * scale;
+        qs[t + D / 2] = b * scale;
+        rope_rot(kh[t], kh[t + D / 2], cs, a, b);
         const int64_t base = static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D;
         if (writer) {
-            L.kc[base + i] = f32_to_bf16(a);
-            L.kc[base + i + D / 2] = f32_to_bf16(b);
+            L.kc[base + t] = f32_to_bf16(a);
+            L.kc[base + t + D / 2] = f32_to_bf16(b);
         }
-        kn[i] = bf16r(a);
-        kn[i + D / 2] = bf16r(b);
-    } else if (threadIdx.x < D / 2 + D) {
-        const int j = threadIdx.x - D / 2;
+        kn[t] = bf16r(a);
+        kn[t + D / 2] = bf16r(b);
+    } else if (t < D / 2 + D) {
+        const int j = t - D / 2;
         const float v = vh[j];
         if (writer) L.vc[static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D + j] = f32_to_bf16(v);
         vn[j] = bf16r(v);
     }
     __syncthreads();
     float mx = -FLT_MAX;
-    for (int t = threadIdx.x; t < n; t += kThreads) {
+    if (t < n) {  // n <= max_seq <= kThreads: one position per thread
         float s0 = 0.f, s1 = 0.f;
         if (t == pos) {
             for (int d = 0; d < D; d += 2) {
@@ -816,64 +877,61 @@ __device__ void attention(const Plan &P, const Layer &L, const float *qkv, uint1
                 s1 = fmaf(qs[d + 1], kn[d + 1], s1);
             }
         } else {
-            const u32x4 *kr = reinterpret_cast<const u32x4 *>(
-                L.kc + static_cast<int64_t>(t) * row + static_cast<int64_t>(kvh) * D);
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                u32x4 w[8];
+            for (int c = 0; c < D / 8; ++c)
 #pragma unroll
-                for (int c = 0; c < 8; ++c) w[c] = kr[half * 8 + c];
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int d = (half * 8 + c) * 8 + 2 * e;
-                        s0 = fmaf(qs[d], __uint_as_float(w[c][e] << 16), s0);
-                        s1 = fmaf(qs[d + 1], __uint_as_float(w[c][e] & 0xffff0000u), s1);
-                    }
-            }
+                for (int e = 0; e < 4; ++e) {
+                    const int d = c * 8 + 2 * e;
+                    s0 = fmaf(qs[d], __uint_as_float(kw[c][e] << 16), s0);
+                    s1 = fmaf(qs[d + 1], __uint_as_float(kw[c][e] & 0xffff0000u), s1);
+                }
         }
         sc[t] = s0 + s1;
-        mx = fmaxf(mx, s0 + s1);
+        mx = s0 + s1;
     }
     mx = block_max(mx, red);
     float sum = 0.f;
-    for (int t = threadIdx.x; t < n; t += kThreads) {
+    if (t < n) {
         const float p = expf(sc[t] - mx);
         sc[t] = p;
-        sum += p;
+        sum = p;
     }
     sum = block_sum(sum, red);
     const float inv = 1.f / sum;
     float a0 = 0.f, a1 = 0.f;
-    const int64_t voff = static_cast<int64_t>(kvh) * D + 2 * lane;
-    for (int t0 = wave; t0 < n; t0 += 8 * kWaves) {
-        float v0[8], v1[8], p[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {  // first eight positions of the wave: preloaded
+        const int tt = wave + u * kWaves;
+        const float p = tt < pos ? sc[tt] : 0.f;
+        a0 = fmaf(p, __uint_as_float(vw[u] << 16), a0);
+        a1 = fmaf(p, __uint_as_float(vw[u] & 0xffff0000u), a1);
+    }
+    for (int t0 = wave + 8 * kWaves; t0 < pos; t0 += 8 * kWaves) {
+        uint32_t w[8];
+        float p[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int t = t0 + u * kWaves;
-            const bool ok = t < n && t != pos;
-            const uint32_t w = *reinterpret_cast<const uint32_t *>(
-                L.vc + static_cast<int64_t>(ok ? t : 0) * row + voff);
-            v0[u] = __uint_as_float(w << 16);
-            v1[u] = __uint_as_float(w & 0xffff0000u);
-            p[u] = ok ? sc[t] : 0.f;
+            const int tt = t0 + u * kWaves;
+            const bool ok = tt < pos;
+            w[u] = __builtin_amdgcn_raw_buffer_load_b32(
+                vr, ok ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
+            p[u] = ok ? sc[tt] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            a0 = fmaf(p[u], v0[u], a0);
-            a1 = fmaf(p[u], v1[u], a1);
+            a0 = fmaf(p[u], __uint_as_float(w[u] << 16), a0);
+            a1 = fmaf(p[u], __uint_as_float(w[u] & 0xffff0000u), a1);
         }
     }
-    if (wave == pos % kWaves) {
+    if (wave == pos % kWaves) {  // position pos: value from LDS
         a0 = fmaf(sc[pos], vn[2 * lane], a0);
         a1 = fmaf(sc[pos], vn[2 * lane + 1], a1);
     }
     part[wave * D + 2 * lane] = a0;
     part[wave * D + 2 * lane + 1] = a1;
     __syncthreads();
-    if (threadIdx.x < D / 2) {
-        const int d = 2 * threadIdx.x;
+    if (t < D / 2) {
+        const int d = 2 * t;
         float v0 = 0.f, v1 = 0.f;
         for (int w = 0; w < kWaves; ++w) {
             v0 += part[w * D + d];
@@ -883,6 +941,7 @@ __device__ void attention(const Plan &P, const Layer &L, const float *qkv, uint1
                                 (static_cast<uint32_t>(f32_to_bf16(v1 * inv)) << 16);
         coh_store_u32(reinterpret_cast<uint32_t *>(attn + static_cast<int64_t>(h) * D + d), packed);
     }
+    return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -1039,7 +1098,8 @@ __device__ void final_argmax(const Plan &P, float *smem) {
 // (layer 0: nothing to wait for); on exit this layer's last stage has arrived.
 template <int HC>
 __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t &target,
-                                         float *smem, int *sh, int wave0, int tok) {
+                                         float *smem, int *sh, const float2 *rope, int wave0,
+                                         int tok) {
     const Layer &L = P.layers[l];
     Pre pf;
     // Each stage starts from fresh copies of the thread / wave ids, so values
@@ -1062,10 +1122,10 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
     arrive(P, ++target);
     tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
     const Geo Go = geo_plain(P, L, kO, P.n_heads * kHeadDim, P.s_o, wave);
-    prefetch(Go, P.group, tid, pf);
     // 2. attention: block h waits only for the blocks that computed its q rows
-    // and its kv head's k and v rows; the other blocks go on to wait for the
-    // attention blocks
+    // and its kv head's k and v rows.  Every block arrives before it issues
+    // its o-stage prefetch: arriving waits for all of the block's memory
+    // operations, and the o blocks wait for the attention blocks' flags.
     if (static_cast<int>(blockIdx.x) < P.n_heads) {
         const int h = blockIdx.x, kvh = h / (P.n_heads / P.n_kv);
         const uint32_t rq = P.n_heads * kHeadDim, rk = P.n_kv * kHeadDim;
@@ -1076,11 +1136,13 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         const int k1 = P.qkv_b1 + block_of_row(rk, nk, (kvh + 1) * kHeadDim - 1) + 1;
         const int v0 = P.qkv_b2 + block_of_row(rk, nv, kvh * kHeadDim);
         const int v1 = P.qkv_b2 + block_of_row(rk, nv, (kvh + 1) * kHeadDim - 1) + 1;
-        if (!wait_blocks(P, target, sh, q0, q1, k0, k1, v0, v1)) return false;
-        attention(P, L, P.qkv + static_cast<int64_t>(l) * P.ls_qkv,
-                  P.attn + static_cast<int64_t>(l) * P.ls_attn, h, pos, smem);
+        if (!attention(P, L, P.qkv + static_cast<int64_t>(l) * P.ls_qkv,
+                       P.attn + static_cast<int64_t>(l) * P.ls_attn, h, pos, smem, rope,
+                       [&] { return wait_blocks(P, target, sh, q0, q1, k0, k1, v0, v1); }))
+            return false;
     }
     arrive(P, ++target);
+    prefetch(Go, P.group, tid, pf);
     if (!wait_blocks(P, target, sh, 0, P.n_heads, 0, 0, 0, 0)) return false;
     // 3. o = W_o attn
     {
@@ -1133,15 +1195,21 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(const Plan *__restri
         __hip_atomic_load(P.flags + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     const int pos = __builtin_amdgcn_readfirstlane(*P.pos);
     const int tok = __builtin_amdgcn_readfirstlane(*P.tok);
+    if (lds_offset_of(smem) != 0) {  // the table lookups address LDS from 0
+        if (threadIdx.x == 0) __hip_atomic_store(P.err, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     if (pos < 0 || pos >= P.max_seq || tok < 0 || tok >= P.vocab) {
         // the host keeps pos < max_seq; a bad state ends the launch everywhere
         if (threadIdx.x == 0) __hip_atomic_store(P.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0 && out_ids) out_ids[step] = tok;
+    float2 *rope = reinterpret_cast<float2 *>(smem + P.lds_red + 2 * kRedCap + 2 * kEnt + 2 * kRps + 64);
+    if (static_cast<int>(blockIdx.x) < P.n_heads) rope_table(P, pos, rope);  // read after barriers
 #pragma clang loop unroll(disable)
     for (int l = 0; l < P.n_layers; ++l)
-        if (!do_layer<HC>(P, l, pos, target, smem, sh, wave, tok)) return;
+        if (!do_layer<HC>(P, l, pos, target, smem, sh, rope, wave, tok)) return;
     {
         LmPre<HC> lpf;
         const int b = blockIdx.x, nb = P.nblocks;
@@ -1224,7 +1292,8 @@ static int lds_red_offset(const hxq_decoder *d) {
 }
 
 static size_t lds_bytes(const hxq_decoder *d) {
-    return sizeof(float) * (static_cast<size_t>(lds_red_offset(d)) + 2 * kRedCap + 2 * kEnt + 2 * kRps + 64);
+    return sizeof(float) * (static_cast<size_t>(lds_red_offset(d)) + 2 * kRedCap + 2 * kEnt + 2 * kRps +
+                             64 + kHeadDim);
 }
 
 static int hc_of(const hxq_decoder *d) { return d->hidden <= 1024 ? 1 : 2; }
