@@ -1,0 +1,716 @@
+// CDNAv3 encoder on the GPU: 1-D k-means codebook, nearest-codebook
+// assignment and percentile outliers (the sidecar), with the reference's
+// CPU results reproduced bit for bit.
+//
+// Reference (helix_substrate/hxq_encoder.py:107-177 _simple_kmeans,
+// hxq_writer_v3.py:427-470 _build_kmeans_codebook / _chunked_assign,
+// generate_sidecars_v3.py:18-40 find_outliers_percentile) computes with
+// numpy; the arithmetic restated here is numpy's:
+//   * assignment: argmin_j |fl(x - c_j)| in fp32, first index on ties, NaN
+//     distances win (numpy argmin returns the first NaN);
+//   * cluster mean: np.mean of the members in index order = fp32 sum over
+//     consecutive 8192-element blocks, each block summed pairwise (blocks of
+//     <= 128 with eight running sums, larger ones split at n/2 rounded down
+//     to a multiple of 8), divided by the count in fp32;
+//   * percentiles: numpy's 'linear' method on the sorted data (virtual index
+//     (n-1) q, lerp a + (b-a) t for t < 1/2 else b - (b-a)(1-t)); fp64 for
+//     the k-means initialisation (an array of percentiles), fp32 for the
+//     sidecar thresholds (a scalar percentile of fp32 data);
+//   * convergence: max |new - old| (fp32) < rtol * (c_last - c_first).
+// Every reduction is integer or follows that fixed order: results are
+// deterministic and independent of the launch shape.
+#include <cfloat>
+#include <cmath>
+
+#include "hxq_common.h"
+
+namespace hxq {
+namespace enc {
+
+constexpr int kThreads = 256;
+constexpr int kMaxK = 256;
+
+// fp32 -> uint32 whose unsigned order is numpy's sort order (NaN last).
+__device__ __forceinline__ uint32_t sort_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+    if (k == 0xffffffffu) return __uint_as_float(0x7fc00000u);
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// ---------------------------------------------------------------------------
+// nearest codebook entry
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float absdiff(float x, float c) {
+#pragma clang fp contract(off)
+    return fabsf(x - c);
+}
+
+// General scan: first index of the minimum; a NaN distance is a minimum.
+__device__ __forceinline__ int nearest_scan(float x, const float *cb, int k) {
+    int best = 0;
+    float bd = absdiff(x, cb[0]);
+    if (bd != bd) return 0;
+    for (int j = 1; j < k; ++j) {
+        const float d = absdiff(x, cb[j]);
+        if (d != d) return j;
+        if (d < bd) { bd = d; best = j; }
+    }
+    return best;
+}
+
+// Sorted (non-decreasing, no NaN) codebook: the distances fall then rise
+// with j, so the minimum is at the last entry <= x or the first entry > x,
+// and the first index holding the minimum value is found by a second
+// binary search over the falling part.
+__device__ __forceinline__ int nearest_sorted(float x, const float *cb, int k) {
+    if (x != x) return 0;
+    // hi = first j with cb[j] > x (k if none)
+    int lo = 0, hi = k;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (cb[mid] > x) hi = mid; else lo = mid + 1;
+    }
+    const int jr = hi;           // first entry > x
+    const int jl = hi - 1;       // last entry <= x
+    float dmin;
+    if (jl < 0) return 0;        // every entry > x: distances rise from j = 0
+    dmin = absdiff(x, cb[jl]);
+    const bool right_wins = jr < k && absdiff(x, cb[jr]) < dmin;
+    if (right_wins) return jr;
+    // first j <= jl with |x - cb[j]| == dmin (distances non-increasing on [0, jl])
+    int a = 0, b = jl;
+    while (a < b) {
+        const int mid = (a + b) >> 1;
+        if (absdiff(x, cb[mid]) <= dmin) b = mid; else a = mid + 1;
+    }
+    return a;
+}
+
+// Codebook staged in LDS; `sorted` decided by the block (uniform).
+__device__ __forceinline__ bool stage_codebook(const float *cb, int k, float *s_cb, int *s_flag) {
+    if (threadIdx.x == 0) *s_flag = 1;
+    __syncthreads();
+    for (int j = threadIdx.x; j < k; j += blockDim.x) {
+        const float v = cb[j];
+        s_cb[j] = v;
+        // finite and non-decreasing: the binary-search path applies
+        if (!isfinite(v) || (j + 1 < k && !(v <= cb[j + 1]))) *s_flag = 0;
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+
+__global__ __launch_bounds__(kThreads) void assign_kernel(const float *x, int64_t n, const float *cb,
+                                                          int k, uint8_t *idx) {
+    __shared__ float s_cb[kMaxK];
+    __shared__ int s_flag;
+    const bool sorted = stage_codebook(cb, k, s_cb, &s_flag);
+    for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const float v = x[i];
+        idx[i] = static_cast<uint8_t>(sorted ? nearest_sorted(v, s_cb, k) : nearest_scan(v, s_cb, k));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bitonic sort of keys (n padded to a power of two with 0xffffffff)
+// ---------------------------------------------------------------------------
+constexpr int kSortBlock = 2048;  // elements per block in the LDS stages
+
+__global__ __launch_bounds__(kThreads) void keys_kernel(const float *x, int64_t n, int64_t np2,
+                                                        uint32_t *keys) {
+    for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < np2;
+         i += (int64_t)gridDim.x * kThreads)
+        keys[i] = i < n ? sort_key(x[i]) : 0xffffffffu;
+}
+
+// one global compare-exchange step (k, j >= kSortBlock / 2)
+__global__ __launch_bounds__(kThreads) void bitonic_global(uint32_t *keys, int64_t np2, int64_t k,
+                                                           int64_t j) {
+    for (int64_t t = blockIdx.x * (int64_t)kThreads + threadIdx.x; t < np2 / 2;
+         t += (int64_t)gridDim.x * kThreads) {
+        const int64_t i = ((t / j) * 2 * j) + (t % j);
+        const int64_t p = i + j;
+        const bool up = (i & k) == 0;
+        const uint32_t a = keys[i], b = keys[p];
+        if ((a > b) == up) { keys[i] = b; keys[p] = a; }
+    }
+}
+
+// all steps j < kSortBlock of stage k (or stages 2..kSortBlock when k == 0), in LDS
+__global__ __launch_bounds__(kThreads) void bitonic_local(uint32_t *keys, int64_t k_stage) {
+    __shared__ uint32_t s[kSortBlock];
+    const int64_t base = blockIdx.x * (int64_t)kSortBlock;
+    for (int i = threadIdx.x; i < kSortBlock; i += kThreads) s[i] = keys[base + i];
+    __syncthreads();
+    const int64_t k_lo = k_stage == 0 ? 2 : k_stage;
+    const int64_t k_hi = k_stage == 0 ? kSortBlock : k_stage;
+    for (int64_t k = k_lo; k <= k_hi; k <<= 1) {
+        for (int j = static_cast<int>(min<int64_t>(k >> 1, kSortBlock >> 1)); j > 0; j >>= 1) {
+            for (int t = threadIdx.x; t < kSortBlock / 2; t += kThreads) {
+                const int i = ((t / j) * 2 * j) + (t % j);
+                const int p = i + j;
+                const bool up = ((base + i) & k) == 0;
+                const uint32_t a = s[i], b = s[p];
+                if ((a > b) == up) { s[i] = b; s[p] = a; }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < kSortBlock; i += kThreads) keys[base + i] = s[i];
+}
+
+// ---------------------------------------------------------------------------
+// k-means initialisation and bookkeeping
+// ---------------------------------------------------------------------------
+// distinct values of the sorted keys (NaNs count once, as np.unique)
+__global__ void zero_i32_kernel(int32_t *p) { *p = 0; }
+
+__global__ __launch_bounds__(kThreads) void count_unique_kernel(const uint32_t *keys, int64_t n,
+                                                                int32_t *count) {
+    __shared__ int32_t s;
+    if (threadIdx.x == 0) s = 0;
+    __syncthreads();
+    int32_t c = 0;
+    for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        if (i == 0) { ++c; continue; }
+        const uint32_t a = keys[i - 1], b = keys[i];
+        // +0.0 and -0.0 are equal values
+        const bool same = a == b || (key_float(a) == key_float(b));
+        c += !same;
+    }
+    atomicAdd(&s, c);
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(count, s);
+}
+
+// centroid j = percentile(data, q_j) with numpy's fp64 'linear' lerp, as fp32
+__global__ __launch_bounds__(kMaxK) void kmeans_init_kernel(const uint32_t *keys, int64_t n, const double *q, int k,
+                                   float *cb, double rtol, double *abs_tol, int32_t *done,
+                                   int32_t *iters) {
+#pragma clang fp contract(off)
+    // numpy's percentile is NaN for every q once the data holds a NaN
+    // (sorted last)
+    const bool has_nan = keys[n - 1] == 0xffffffffu;
+    for (int j = threadIdx.x; j < k; j += blockDim.x) {
+        const double v = static_cast<double>(n - 1) * q[j];
+        double r;
+        if (has_nan) {
+            r = static_cast<double>(key_float(0xffffffffu));
+        } else if (v >= static_cast<double>(n - 1)) {
+            r = static_cast<double>(key_float(keys[n - 1]));
+        } else {
+            const int64_t i = static_cast<int64_t>(floor(v));
+            const double t = v - static_cast<double>(i);
+            const float a = key_float(keys[i]), b = key_float(keys[i + 1]);
+            const double d = static_cast<double>(b - a);  // fp32 difference
+            r = t >= 0.5 ? static_cast<double>(b) - d * (1.0 - t) : static_cast<double>(a) + d * t;
+        }
+        cb[j] = static_cast<float>(r);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double range = static_cast<double>(cb[k - 1] - cb[0]);
+        if (range < 1e-30) range = 1.0;
+        *abs_tol = rtol * range;
+        *done = 0;
+        *iters = 0;
+    }
+}
+
+// Lloyd step 1: assignment + per-block cluster counts.  Block b owns the
+// contiguous elements [b * per, (b + 1) * per).
+__global__ __launch_bounds__(kThreads) void km_assign_kernel(const float *x, int64_t n, int64_t per,
+                                                             const float *cb, int k, uint8_t *idx,
+                                                             int32_t *blk_counts, const int32_t *done) {
+    if (*done) return;
+    __shared__ float s_cb[kMaxK];
+    __shared__ int s_flag;
+    __shared__ int32_t s_cnt[kMaxK];
+    for (int j = threadIdx.x; j < kMaxK; j += kThreads) s_cnt[j] = 0;
+    const bool sorted = stage_codebook(cb, k, s_cb, &s_flag);
+    const int64_t lo = blockIdx.x * per, hi = min(n, lo + per);
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) {
+        const float v = x[i];
+        const int c = sorted ? nearest_sorted(v, s_cb, k) : nearest_scan(v, s_cb, k);
+        idx[i] = static_cast<uint8_t>(c);
+        atomicAdd(&s_cnt[c], 1);
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < k; j += kThreads) blk_counts[blockIdx.x * (int64_t)k + j] = s_cnt[j];
+}
+
+// Lloyd step 2: exclusive offsets, cluster-major then block order (stable)
+__global__ __launch_bounds__(kMaxK) void km_offsets_kernel(int32_t *blk_counts, int nblk, int k, int32_t *starts,
+                                  int32_t *counts, const int32_t *done) {
+    if (*done) return;
+    __shared__ int32_t tot[kMaxK];
+    const int j = threadIdx.x;
+    if (j < k) {
+        int32_t s = 0;
+        for (int b = 0; b < nblk; ++b) {
+            const int32_t c = blk_counts[(int64_t)b * k + j];
+            blk_counts[(int64_t)b * k + j] = s;  // offset within cluster j
+            s += c;
+        }
+        tot[j] = s;
+        counts[j] = s;
+    }
+    __syncthreads();
+    if (j == 0) {
+        int32_t s = 0;
+        for (int c = 0; c < k; ++c) { starts[c] = s; s += tot[c]; }
+    }
+}
+
+// Lloyd step 3: stable scatter of the values into cluster-contiguous order
+// (within a cluster, elements keep their index order)
+__global__ __launch_bounds__(kThreads) void km_scatter_kernel(const float *x, int64_t n, int64_t per,
+                                                              const uint8_t *idx, const int32_t *blk_offs,
+                                                              const int32_t *starts, int k, float *out,
+                                                              const int32_t *done) {
+    if (*done) return;
+    constexpr int W = kThreads / kWave;
+    __shared__ int32_t base[kMaxK];
+    __shared__ int32_t wcnt[W][kMaxK];
+    for (int j = threadIdx.x; j < k; j += kThreads)
+        base[j] = starts[j] + blk_offs[blockIdx.x * (int64_t)k + j];
+    const int lane = threadIdx.x & 63, w = threadIdx.x / kWave;
+    const int64_t lo = blockIdx.x * per, hi = min(n, lo + per);
+    for (int64_t c0 = lo; c0 < hi; c0 += kThreads) {
+        for (int j = threadIdx.x; j < W * kMaxK; j += kThreads) (&wcnt[0][0])[j] = 0;
+        __syncthreads();
+        const int64_t i = c0 + threadIdx.x;
+        const bool ok = i < hi;
+        const int c = ok ? idx[i] : -1;
+        // rank among earlier lanes of this wave with the same cluster
+        int r = 0;
+        for (int l = 0; l < kWave; ++l) {
+            const int cl = __shfl(c, l, kWave);
+            r += (l < lane && cl == c);
+        }
+        if (ok) atomicAdd(&wcnt[w][c], 1);
+        __syncthreads();
+        if (ok) {
+            int32_t pos = base[c] + r;
+            for (int ww = 0; ww < w; ++ww) pos += wcnt[ww][c];
+            out[pos] = x[i];
+        }
+        __syncthreads();
+        for (int j = threadIdx.x; j < k; j += kThreads) {
+            int32_t s = 0;
+            for (int ww = 0; ww < W; ++ww) s += wcnt[ww][j];
+            base[j] += s;
+        }
+        __syncthreads();
+    }
+}
+
+// numpy's pairwise sum of fp32 (blocks of <= 128: eight running sums)
+__device__ float pairwise_leaf(const float *a, int n) {
+#pragma clang fp contract(off)
+    if (n < 8) {
+        float r = 0.f;
+        for (int i = 0; i < n; ++i) r += a[i];
+        return r;
+    }
+    float r[8];
+    for (int j = 0; j < 8; ++j) r[j] = a[j];
+    int i = 8;
+    for (; i < n - (n % 8); i += 8)
+        for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+    float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += a[i];
+    return res;
+}
+
+// pairwise sum of n <= 8192 elements (split at n/2 rounded down to a
+// multiple of 8 until <= 128), evaluated with an explicit stack
+__device__ float pairwise_sum(const float *a, int n) {
+#pragma clang fp contract(off)
+    if (n <= 128) return pairwise_leaf(a, n);
+    // frames: offset, length, state (0: visit left, 1: visit right, 2: combine)
+    int off[16], len[16], st[16];
+    float left[16];
+    int sp = 0;
+    off[0] = 0; len[0] = n; st[0] = 0;
+    float ret = 0.f;
+    while (sp >= 0) {
+        const int m = len[sp];
+        if (m <= 128) {
+            ret = pairwise_leaf(a + off[sp], m);
+            --sp;
+            continue;
+        }
+        int m2 = m / 2;
+        m2 -= m2 % 8;
+        if (st[sp] == 0) {
+            st[sp] = 1;
+            ++sp; off[sp] = off[sp - 1]; len[sp] = m2; st[sp] = 0;
+        } else if (st[sp] == 1) {
+            left[sp] = ret;
+            st[sp] = 2;
+            ++sp; off[sp] = off[sp - 1] + m2; len[sp] = m - m2; st[sp] = 0;
+        } else {
+            ret = left[sp] + ret;
+            --sp;
+        }
+    }
+    return ret;
+}
+
+// Lloyd step 4: means, movement, convergence.  One thread per cluster.
+__global__ __launch_bounds__(kMaxK) void km_update_kernel(const float *sorted_vals, const int32_t *starts,
+                                 const int32_t *counts, int k, float *cb, const double *abs_tol,
+                                 int32_t *done, int32_t *iters) {
+#pragma clang fp contract(off)
+    if (*done) return;
+    __shared__ float s_new[kMaxK];
+    __shared__ float s_delta[kMaxK];
+    const int j = threadIdx.x;
+    if (j < k) {
+        const int32_t c = counts[j];
+        float v = cb[j];
+        if (c > 0) {
+            const float *a = sorted_vals + starts[j];
+            float sum = 0.f;
+            bool first = true;
+            for (int32_t s = 0; s < c; s += 8192) {
+                const float p = pairwise_sum(a + s, min(8192, c - s));
+                sum = first ? p : sum + p;
+                first = false;
+            }
+            v = sum / static_cast<float>(c);
+        }
+        s_new[j] = v;
+        s_delta[j] = fabsf(v - cb[j]);
+    }
+    __syncthreads();
+    if (j == 0) {
+        float m = 0.f;
+        bool nan = false;
+        for (int c = 0; c < k; ++c) {
+            nan |= s_delta[c] != s_delta[c];
+            m = fmaxf(m, s_delta[c]);
+        }
+        // numpy's max propagates NaN; NaN < tol is false: no convergence
+        const bool conv = !nan && static_cast<double>(m) < *abs_tol;
+        s_delta[0] = conv ? 1.f : 0.f;
+        *iters += 1;
+        if (conv) *done = 1;
+    }
+    __syncthreads();
+    if (j < k && s_delta[0] == 0.f) cb[j] = s_new[j];
+}
+
+// ---------------------------------------------------------------------------
+// radix select (exact order statistics of up to 4 ranks) and outliers
+// ---------------------------------------------------------------------------
+constexpr int kSelMax = 4;
+
+struct SelState {
+    uint32_t prefix[kSelMax];  // key bits fixed so far
+    uint32_t rank[kSelMax];    // rank within the keys matching prefix
+    uint32_t hist[kSelMax][256];
+    int32_t nan_count;
+    int32_t pad_;
+};
+
+__global__ __launch_bounds__(kThreads) void select_hist_kernel(const float *x, int64_t n, int m,
+                                                               int shift, SelState *st) {
+    __shared__ uint32_t h[kSelMax][256];
+    for (int i = threadIdx.x; i < kSelMax * 256; i += kThreads) (&h[0][0])[i] = 0;
+    __syncthreads();
+    uint32_t pre[kSelMax];
+    for (int r = 0; r < m; ++r) pre[r] = st->prefix[r];
+    const uint32_t hi_mask = shift >= 24 ? 0u : (0xffffffffu << (shift + 8));
+    int32_t nans = 0;
+    for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads) {
+        const uint32_t key = sort_key(x[i]);
+        if (shift == 24 && key == 0xffffffffu) ++nans;
+        const uint32_t d = (key >> shift) & 0xffu;
+        for (int r = 0; r < m; ++r)
+            if ((key & hi_mask) == (pre[r] & hi_mask)) atomicAdd(&h[r][d], 1u);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < m * 256; i += kThreads) {
+        const uint32_t v = (&h[0][0])[i];
+        if (v) atomicAdd(&st->hist[i / 256][i % 256], v);
+    }
+    if (shift == 24 && nans) atomicAdd(&st->nan_count, nans);
+}
+
+__global__ void select_pick_kernel(int m, int shift, SelState *st, float *out) {
+    const int r = threadIdx.x;
+    if (r < m) {
+        uint32_t rank = st->rank[r];
+        int d = 0;
+        for (; d < 255; ++d) {
+            const uint32_t c = st->hist[r][d];
+            if (rank < c) break;
+            rank -= c;
+        }
+        st->prefix[r] |= static_cast<uint32_t>(d) << shift;
+        st->rank[r] = rank;
+        for (int i = 0; i < 256; ++i) st->hist[r][i] = 0;
+        if (shift == 0) out[r] = key_float(st->prefix[r]);
+    }
+}
+
+__global__ void select_init_kernel(const int64_t *ranks, int m, SelState *st) {
+    for (int i = threadIdx.x; i < kSelMax * 256; i += blockDim.x) (&st->hist[0][0])[i] = 0;
+    if (threadIdx.x < kSelMax) {
+        st->prefix[threadIdx.x] = 0;
+        st->rank[threadIdx.x] = threadIdx.x < m ? static_cast<uint32_t>(ranks[threadIdx.x]) : 0;
+    }
+    if (threadIdx.x == 0) st->nan_count = 0;
+}
+
+// outliers: x < lo or x > hi, positions ascending (two passes)
+__global__ __launch_bounds__(kThreads) void outlier_count_kernel(const float *x, int64_t n, int64_t per,
+                                                                 const float *lohi, int32_t *blk) {
+    __shared__ int32_t s;
+    if (threadIdx.x == 0) s = 0;
+    __syncthreads();
+    const float lo = lohi[0], hi = lohi[1];
+    const int64_t a = blockIdx.x * per, b = min(n, a + per);
+    int32_t c = 0;
+    for (int64_t i = a + threadIdx.x; i < b; i += kThreads) {
+        const float v = x[i];
+        c += (v < lo) | (v > hi);
+    }
+    atomicAdd(&s, c);
+    __syncthreads();
+    if (threadIdx.x == 0) blk[blockIdx.x] = s;
+}
+
+__global__ void outlier_scan_kernel(int32_t *blk, int nblk, int64_t *total) {
+    if (threadIdx.x == 0) {
+        int64_t s = 0;
+        for (int b = 0; b < nblk; ++b) { const int32_t c = blk[b]; blk[b] = static_cast<int32_t>(s); s += c; }
+        *total = s;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void outlier_write_kernel(const float *x, int64_t n, int64_t per,
+                                                                 const float *lohi, const int32_t *blk,
+                                                                 int64_t cap, int64_t *pos, float *val) {
+    constexpr int W = kThreads / kWave;
+    __shared__ int32_t wsum[W];
+    __shared__ int32_t base;
+    if (threadIdx.x == 0) base = blk[blockIdx.x];
+    const float lo = lohi[0], hi = lohi[1];
+    const int lane = threadIdx.x & 63, w = threadIdx.x / kWave;
+    const int64_t a = blockIdx.x * per, b = min(n, a + per);
+    for (int64_t c0 = a; c0 < b; c0 += kThreads) {
+        const int64_t i = c0 + threadIdx.x;
+        const float v = i < b ? x[i] : 0.f;
+        const bool hit = i < b && ((v < lo) | (v > hi));
+        const uint64_t mask = __ballot(hit);
+        const int r = __popcll(mask & ((1ull << lane) - 1ull));
+        if (lane == 0) wsum[w] = __popcll(mask);
+        __syncthreads();
+        if (hit) {
+            int64_t p = base + r;
+            for (int ww = 0; ww < w; ++ww) p += wsum[ww];
+            if (p < cap) { pos[p] = i; val[p] = v; }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int32_t s = 0;
+            for (int ww = 0; ww < W; ++ww) s += wsum[ww];
+            base += s;
+        }
+        __syncthreads();
+    }
+}
+
+static int grid_for(int64_t n) {
+    const int64_t g = (n + kThreads - 1) / kThreads;
+    return static_cast<int>(std::min<int64_t>(std::max<int64_t>(g, 1), 8192));
+}
+
+static int64_t next_pow2(int64_t n) {
+    int64_t p = kSortBlock;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+}  // namespace enc
+}  // namespace hxq
+
+using namespace hxq;
+using namespace hxq::enc;
+
+extern "C" int hxq_assign_nearest(const float *x, int64_t n, const float *codebook, int32_t k,
+                                  uint8_t *indices, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && codebook && indices, "x, codebook and indices are required");
+    HXQ_REQUIRE(n >= 0 && k >= 1 && k <= kMaxK, "k must be 1..256");
+    if (n == 0) return HXQ_OK;
+    hipLaunchKernelGGL(assign_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream, x, n, codebook,
+                       k, indices);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
+extern "C" int64_t hxq_sort_workspace_bytes(int64_t n) {
+    return n <= 0 ? 0 : 4 * next_pow2(n);
+}
+
+static int sort_keys(const float *x, int64_t n, uint32_t *keys, hipStream_t stream) {
+    const int64_t np2 = next_pow2(n);
+    hipLaunchKernelGGL(keys_kernel, dim3(grid_for(np2)), dim3(kThreads), 0, stream, x, n, np2, keys);
+    HXQ_LAUNCH_CHECK();
+    const dim3 lgrid(static_cast<uint32_t>(np2 / kSortBlock));
+    hipLaunchKernelGGL(bitonic_local, lgrid, dim3(kThreads), 0, stream, keys, int64_t{0});
+    HXQ_LAUNCH_CHECK();
+    for (int64_t k = 2 * kSortBlock; k <= np2; k <<= 1) {
+        for (int64_t j = k >> 1; j >= kSortBlock; j >>= 1) {
+            hipLaunchKernelGGL(bitonic_global, dim3(grid_for(np2 / 2)), dim3(kThreads), 0, stream, keys,
+                               np2, k, j);
+            HXQ_LAUNCH_CHECK();
+        }
+        hipLaunchKernelGGL(bitonic_local, lgrid, dim3(kThreads), 0, stream, keys, k);
+        HXQ_LAUNCH_CHECK();
+    }
+    return HXQ_OK;
+}
+
+static int64_t align256(int64_t b) { return (b + 255) & ~int64_t{255}; }
+
+// k-means workspace regions, each 256-byte aligned: sort keys, cluster-ordered
+// values, per-block counts / offsets, then starts, counts and the fp64
+// tolerance + done flag
+struct KmLayout {
+    int64_t vals, blk, starts, counts, tol, done, total;
+    explicit KmLayout(int64_t n) {
+        const int64_t nblk = (n + 4095) / 4096;
+        vals = align256(4 * next_pow2(n));
+        blk = vals + align256(4 * n);
+        starts = blk + align256(4 * nblk * kMaxK);
+        counts = starts + 4 * kMaxK;
+        tol = counts + 4 * kMaxK;
+        done = tol + 8;
+        total = align256(done + 8);
+    }
+};
+
+extern "C" int64_t hxq_kmeans_workspace_bytes(int64_t n) {
+    return n <= 0 ? 0 : KmLayout(n).total;
+}
+
+extern "C" int hxq_kmeans_init(const float *x, int64_t n, void *workspace, int64_t workspace_bytes,
+                               int32_t *n_unique, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && workspace && n_unique && n >= 1, "bad arguments");
+    HXQ_REQUIRE(n < (int64_t{1} << 31), "n too large");
+    HXQ_REQUIRE(workspace_bytes >= hxq_kmeans_workspace_bytes(n), "workspace too small");
+    uint32_t *keys = static_cast<uint32_t *>(workspace);
+    if (int rc = sort_keys(x, n, keys, stream)) return rc;
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(1), 0, stream, n_unique);
+    HXQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(count_unique_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream, keys, n,
+                       n_unique);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
+extern "C" int hxq_kmeans_run(const float *x, int64_t n, const double *percentiles01, int32_t k,
+                              int32_t max_iters, double rtol, void *workspace,
+                              int64_t workspace_bytes, float *codebook, uint8_t *assignments,
+                              int32_t *iters, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && percentiles01 && workspace && codebook && assignments && iters, "bad arguments");
+    // max_iters == 0 leaves the reference's assignments unbound (an error there)
+    HXQ_REQUIRE(n >= 1 && n < (int64_t{1} << 31) && k >= 1 && k <= kMaxK && max_iters >= 1,
+                "bad sizes (n 1..2^31-1, k 1..256, max_iters >= 1)");
+    HXQ_REQUIRE(workspace_bytes >= hxq_kmeans_workspace_bytes(n), "workspace too small");
+    char *ws = static_cast<char *>(workspace);
+    const int64_t nblk = (n + 4095) / 4096;
+    const KmLayout lay(n);
+    uint32_t *keys = reinterpret_cast<uint32_t *>(ws);              // sorted by hxq_kmeans_init
+    float *vals = reinterpret_cast<float *>(ws + lay.vals);
+    int32_t *blk = reinterpret_cast<int32_t *>(ws + lay.blk);
+    int32_t *starts = reinterpret_cast<int32_t *>(ws + lay.starts);
+    int32_t *counts = reinterpret_cast<int32_t *>(ws + lay.counts);
+    double *abs_tol = reinterpret_cast<double *>(ws + lay.tol);
+    int32_t *done = reinterpret_cast<int32_t *>(ws + lay.done);
+    hipLaunchKernelGGL(kmeans_init_kernel, dim3(1), dim3(kMaxK), 0, stream, keys, n, percentiles01,
+                       k, codebook, rtol, abs_tol, done, iters);
+    HXQ_LAUNCH_CHECK();
+    const int64_t per = 4096;
+    for (int it = 0; it < max_iters; ++it) {
+        hipLaunchKernelGGL(km_assign_kernel, dim3(static_cast<uint32_t>(nblk)), dim3(kThreads), 0,
+                           stream, x, n, per, codebook, k, assignments, blk, done);
+        HXQ_LAUNCH_CHECK();
+        hipLaunchKernelGGL(km_offsets_kernel, dim3(1), dim3(kMaxK), 0, stream, blk,
+                           static_cast<int>(nblk), k, starts, counts, done);
+        HXQ_LAUNCH_CHECK();
+        hipLaunchKernelGGL(km_scatter_kernel, dim3(static_cast<uint32_t>(nblk)), dim3(kThreads), 0,
+                           stream, x, n, per, assignments, blk, starts, k, vals, done);
+        HXQ_LAUNCH_CHECK();
+        hipLaunchKernelGGL(km_update_kernel, dim3(1), dim3(kMaxK), 0, stream, vals, starts, counts,
+                           k, codebook, abs_tol, done, iters);
+        HXQ_LAUNCH_CHECK();
+    }
+    return HXQ_OK;
+}
+
+extern "C" int64_t hxq_select_workspace_bytes(void) { return sizeof(SelState); }
+
+extern "C" int hxq_select_f32(const float *x, int64_t n, const int64_t *ranks, int32_t m,
+                              float *values, int32_t *nan_count, void *workspace,
+                              int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && ranks && values && workspace, "bad arguments");
+    HXQ_REQUIRE(m >= 1 && m <= kSelMax && n >= 1 && n < (int64_t{1} << 32), "bad sizes");
+    HXQ_REQUIRE(workspace_bytes >= static_cast<int64_t>(sizeof(SelState)), "workspace too small");
+    SelState *st = static_cast<SelState *>(workspace);
+    hipLaunchKernelGGL(select_init_kernel, dim3(1), dim3(256), 0, stream, ranks, m, st);
+    HXQ_LAUNCH_CHECK();
+    const int g = std::min(grid_for(n), 2048);
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hipLaunchKernelGGL(select_hist_kernel, dim3(g), dim3(kThreads), 0, stream, x, n, m, shift, st);
+        HXQ_LAUNCH_CHECK();
+        hipLaunchKernelGGL(select_pick_kernel, dim3(1), dim3(64), 0, stream, m, shift, st, values);
+        HXQ_LAUNCH_CHECK();
+    }
+    if (nan_count)
+        HXQ_HIP_TRY(hipMemcpyAsync(nan_count, &st->nan_count, 4, hipMemcpyDeviceToDevice, stream));
+    return HXQ_OK;
+}
+
+extern "C" int64_t hxq_outliers_workspace_bytes(int64_t n) {
+    const int64_t nblk = (n + 65535) / 65536;
+    return 4 * std::max<int64_t>(nblk, 1) + 64;
+}
+
+extern "C" int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capacity,
+                                int64_t *positions, float *values, int64_t *count, void *workspace,
+                                int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && lohi && count && workspace && (capacity == 0 || (positions && values)),
+                "bad arguments");
+    HXQ_REQUIRE(n >= 1 && capacity >= 0, "bad sizes");
+    HXQ_REQUIRE(workspace_bytes >= hxq_outliers_workspace_bytes(n), "workspace too small");
+    const int64_t per = 65536;
+    const int nblk = static_cast<int>((n + per - 1) / per);
+    int32_t *blk = static_cast<int32_t *>(workspace);
+    hipLaunchKernelGGL(outlier_count_kernel, dim3(nblk), dim3(kThreads), 0, stream, x, n, per, lohi, blk);
+    HXQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(outlier_scan_kernel, dim3(1), dim3(64), 0, stream, blk, nblk, count);
+    HXQ_LAUNCH_CHECK();
+    if (capacity > 0) {
+        hipLaunchKernelGGL(outlier_write_kernel, dim3(nblk), dim3(kThreads), 0, stream, x, n, per, lohi,
+                           blk, capacity, positions, values);
+        HXQ_LAUNCH_CHECK();
+    }
+    return HXQ_OK;
+}

@@ -96,6 +96,11 @@ SIGNATURES = {
     "hxq_argmax": [P, I64, P, P, P, P],
     "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
     "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
+    "hxq_assign_nearest": [P, I64, P, I32, P, P],
+    "hxq_kmeans_init": [P, I64, P, I64, P, P],
+    "hxq_kmeans_run": [P, I64, P, I32, I32, ctypes.c_double, P, I64, P, P, P, P],
+    "hxq_select_f32": [P, I64, P, I32, P, P, P, I64, P],
+    "hxq_outliers_f32": [P, I64, P, I64, P, P, P, P, I64, P],
     "hxq_decoder_init": [P, P, I64, P],
     "hxq_decoder_step": [P, P, I32, P, P],
     "hxq_decoder_error": [P, P, P, P],
@@ -107,6 +112,10 @@ SIGNATURES_I64 = {
     "hxq_ssm_scan_workspace_bytes": [I64] * 6,
     "hxq_moe_ffn_workspace_bytes": [I64, I64, I64, I32],
     "hxq_decoder_workspace_bytes": [P],
+    "hxq_sort_workspace_bytes": [I64],
+    "hxq_kmeans_workspace_bytes": [I64],
+    "hxq_select_workspace_bytes": [],
+    "hxq_outliers_workspace_bytes": [I64],
 }
 
 
@@ -607,3 +616,115 @@ def decoder_error(desc: HxqDecoder, workspace: torch.Tensor) -> int:
                                  _stream(workspace))
     _check("hxq_decoder_error", rc)
     return int(err.value)
+
+
+# -- encoder ---------------------------------------------------------------------
+def assign_nearest(x, codebook, out=None):
+    """indices (uint8, shape of x) = argmin_j |x - codebook[j]| (first on ties)."""
+    xf = x.reshape(-1)
+    _need_device(xf, codebook)
+    if xf.dtype != torch.float32 or codebook.dtype != torch.float32:
+        raise RuntimeError("assign_nearest takes fp32 data and codebook")
+    xf = xf.contiguous()
+    cb = codebook.contiguous()
+    if out is None:
+        out = torch.empty(xf.numel(), dtype=torch.uint8, device=xf.device)
+    rc = lib().hxq_assign_nearest(_ptr(xf), xf.numel(), _ptr(cb), cb.numel(), _ptr(out), _stream(xf))
+    _check("hxq_assign_nearest", rc)
+    return out.view(x.shape)
+
+
+def kmeans_1d(sample, n_clusters=256, max_iters=10, rtol=0.001):
+    """The reference's _simple_kmeans on a device fp32 vector: returns
+    (codebook fp32 [k], assignments uint8 [n], iterations run)."""
+    import numpy as np
+    x = sample.reshape(-1).contiguous()
+    _need_device(x)
+    if x.dtype != torch.float32:
+        raise RuntimeError("kmeans_1d takes fp32 data")
+    n = x.numel()
+    L = lib()
+    ws = torch.empty(int(L.hxq_kmeans_workspace_bytes(n)), dtype=torch.uint8, device=x.device)
+    n_unique = torch.empty(1, dtype=torch.int32, device=x.device)
+    _check("hxq_kmeans_init", L.hxq_kmeans_init(_ptr(x), n, _ptr(ws), ws.numel(), _ptr(n_unique),
+                                                _stream(x)))
+    k = min(int(n_clusters), int(n_unique.item()))
+    q01 = torch.from_numpy(np.linspace(0, 100, k) / np.float32(100)).to(x.device)
+    cb = torch.empty(k, dtype=torch.float32, device=x.device)
+    asg = torch.empty(n, dtype=torch.uint8, device=x.device)
+    iters = torch.empty(1, dtype=torch.int32, device=x.device)
+    _check("hxq_kmeans_run", L.hxq_kmeans_run(_ptr(x), n, _ptr(q01), k, int(max_iters), float(rtol),
+                                              _ptr(ws), ws.numel(), _ptr(cb), _ptr(asg), _ptr(iters),
+                                              _stream(x)))
+    return cb, asg, int(iters.item())
+
+
+def select_f32(x, ranks):
+    """Exact order statistics (0-based ranks, numpy sort order) of a device fp32
+    tensor: returns (values fp32 [m], nan_count int)."""
+    xf = x.reshape(-1).contiguous()
+    _need_device(xf)
+    r = torch.as_tensor(ranks, dtype=torch.int64).to(xf.device)
+    vals = torch.empty(r.numel(), dtype=torch.float32, device=xf.device)
+    nans = torch.empty(1, dtype=torch.int32, device=xf.device)
+    L = lib()
+    ws = torch.empty(int(L.hxq_select_workspace_bytes()), dtype=torch.uint8, device=xf.device)
+    rc = L.hxq_select_f32(_ptr(xf), xf.numel(), _ptr(r), r.numel(), _ptr(vals), _ptr(nans), _ptr(ws),
+                          ws.numel(), _stream(xf))
+    _check("hxq_select_f32", rc)
+    return vals, int(nans.item())
+
+
+def percentile_f32(x, qs):
+    """numpy.percentile(x, q) (method 'linear', fp32 data, scalar q) for each
+    q in qs: order statistics on the GPU, numpy's fp32 interpolation on the
+    host.  Returns a list of numpy float32 scalars."""
+    import numpy as np
+    f32 = np.float32
+    n = x.numel()
+    plan = []
+    ranks = []
+    for q in qs:
+        v = f32(n - 1) * (f32(q) / f32(100))
+        i = int(np.floor(v))
+        if v >= n - 1:
+            plan.append((len(ranks), None, None))
+            ranks.append(n - 1)
+        else:
+            plan.append((len(ranks), len(ranks) + 1, f32(v - f32(i))))
+            ranks += [i, i + 1]
+    parts = [select_f32(x, ranks[i:i + 4]) for i in range(0, len(ranks), 4)]  # <= 4 ranks a call
+    vals = np.concatenate([v.cpu().numpy() for v, _ in parts])
+    nans = parts[0][1]
+    out = []
+    for a_i, b_i, t in plan:
+        if nans:
+            out.append(f32(np.nan))
+        elif b_i is None:
+            out.append(vals[a_i])
+        else:
+            a, b = vals[a_i], vals[b_i]
+            d = f32(b - a)
+            out.append(f32(b - d * (f32(1) - t)) if t >= 0.5 else f32(a + d * t))
+    return out
+
+
+def outliers_f32(x, lo, hi):
+    """Positions (int64, ascending) and values of x < lo or x > hi."""
+    xf = x.reshape(-1).contiguous()
+    _need_device(xf)
+    lohi = torch.tensor([float(lo), float(hi)], dtype=torch.float32, device=xf.device)
+    L = lib()
+    ws = torch.empty(int(L.hxq_outliers_workspace_bytes(xf.numel())), dtype=torch.uint8,
+                     device=xf.device)
+    cnt = torch.empty(1, dtype=torch.int64, device=xf.device)
+    _check("hxq_outliers_f32", L.hxq_outliers_f32(_ptr(xf), xf.numel(), _ptr(lohi), 0, None, None,
+                                                  _ptr(cnt), _ptr(ws), ws.numel(), _stream(xf)))
+    n = int(cnt.item())
+    pos = torch.empty(n, dtype=torch.int64, device=xf.device)
+    val = torch.empty(n, dtype=torch.float32, device=xf.device)
+    if n:
+        _check("hxq_outliers_f32", L.hxq_outliers_f32(_ptr(xf), xf.numel(), _ptr(lohi), n, _ptr(pos),
+                                                      _ptr(val), _ptr(cnt), _ptr(ws), ws.numel(),
+                                                      _stream(xf)))
+    return pos, val

@@ -11,12 +11,25 @@ from pathlib import Path
 import numpy as np
 
 
-def find_outliers_percentile(tensor: np.ndarray, percentile: float = 99.9):
-    """Positions (flat, sorted) and values of entries with |w| above the percentile
-    of |w| (reference generate_sidecars_v3.py:18-40)."""
+def find_outliers_percentile(tensor, percentile: float = 99.9):
+    """Positions (flat, ascending) and values of entries below the
+    (100 - percentile)-th or above the percentile-th percentile of the
+    tensor (both tails; reference generate_sidecars_v3.py:18-40).
+
+    Device tensors: thresholds from exact GPU order statistics with numpy's
+    fp32 'linear' interpolation, positions by an ordered GPU compaction;
+    returns device tensors.  numpy input: numpy."""
+    import torch
+
+    if isinstance(tensor, torch.Tensor) and tensor.is_cuda:
+        from . import _hxq
+        flat = tensor.reshape(-1).float()
+        lo, hi = _hxq.percentile_f32(flat, [100.0 - percentile, percentile])
+        return _hxq.outliers_f32(flat, lo, hi)
     flat = np.asarray(tensor, dtype=np.float32).ravel()
-    thr = np.percentile(np.abs(flat), percentile)
-    positions = np.nonzero(np.abs(flat) > thr)[0].astype(np.int64)
+    lo = np.percentile(flat, 100.0 - percentile)
+    hi = np.percentile(flat, percentile)
+    positions = np.where((flat < lo) | (flat > hi))[0].astype(np.int64)
     return positions, flat[positions].astype(np.float32)
 
 

@@ -1,0 +1,96 @@
+"""CDNAv3 scalar encoder: 1-D k-means codebook and nearest-entry assignment.
+
+Mirrors the reference's ``_simple_kmeans`` (``helix_substrate/hxq_encoder.py:
+107-177``) and ``CDNAv3Writer._chunked_assign`` / ``_build_kmeans_codebook``
+(``hxq_writer_v3.py:427-470``).  numpy inputs run the reference's CPU
+algorithm (numpy percentile init, argmin assignment, np.mean updates,
+relative convergence test); device tensors run the HIP kernels of
+``hxq_encode.hip``, which reproduce that CPU algorithm bit for bit (same
+init, same first-index argmin, cluster means summed in numpy's order).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _hxq
+
+KMEANS_MAX_SAMPLES = 500_000   # reference hxq_writer_v3.py:37
+ASSIGN_CHUNK = 1 << 20         # reference hxq_writer_v3.py:39
+
+
+def _is_device(x) -> bool:
+    return isinstance(x, torch.Tensor) and x.is_cuda
+
+
+def chunked_assign(flat, codebook):
+    """indices[i] = argmin_j |flat[i] - codebook[j]| (first index on ties),
+    uint8.  Device tensors: one HIP launch; numpy: chunked argmin."""
+    if _is_device(flat):
+        cb = codebook if _is_device(codebook) else torch.as_tensor(
+            np.asarray(codebook, dtype=np.float32)).to(flat.device)
+        return _hxq.assign_nearest(flat.reshape(-1).float(), cb.float())
+    flat = np.asarray(flat, dtype=np.float32).ravel()
+    codebook = np.asarray(codebook, dtype=np.float32)
+    out = np.empty(flat.size, dtype=np.uint8 if codebook.size <= 256 else np.uint16)
+    for s in range(0, flat.size, ASSIGN_CHUNK):
+        chunk = flat[s:s + ASSIGN_CHUNK]
+        out[s:s + chunk.size] = np.argmin(np.abs(chunk[:, None] - codebook), axis=1)
+    return out
+
+
+def _simple_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
+    """(centroids fp32 [k], assignments uint8 [n]) with k = min(n_clusters,
+    distinct values); device tensors return device tensors."""
+    if _is_device(data):
+        cb, asg, _ = _hxq.kmeans_1d(data.reshape(-1).float(), n_clusters, max_iters, rtol)
+        return cb, asg
+    data = np.asarray(data, dtype=np.float32).ravel()
+    k = min(int(n_clusters), len(np.unique(data)))
+    centroids = np.percentile(data, np.linspace(0, 100, k)).astype(np.float32)
+    cb_range = float(centroids[-1] - centroids[0])
+    if cb_range < 1e-30:
+        cb_range = 1.0
+    abs_tol = rtol * cb_range
+    assignments = np.zeros(data.size, dtype=np.uint8)
+    for _ in range(max_iters):
+        assignments = chunked_assign(data, centroids).astype(np.uint8)
+        # members of each cluster in index order, contiguous (stable sort)
+        order = np.argsort(assignments, kind="stable")
+        vals = data[order]
+        counts = np.bincount(assignments, minlength=k)
+        starts = np.concatenate(([0], np.cumsum(counts)[:-1]))
+        new = np.zeros_like(centroids)
+        for j in range(k):
+            new[j] = np.mean(vals[starts[j]:starts[j] + counts[j]]) if counts[j] else centroids[j]
+        if float(np.max(np.abs(new - centroids))) < abs_tol:
+            break
+        centroids = new
+    return centroids, assignments
+
+
+def kmeans_sample(flat, max_samples=KMEANS_MAX_SAMPLES):
+    """The reference's k-means subsample: all of flat, or RandomState(42)
+    .choice(n, max_samples, replace=False) of it (hxq_writer_v3.py:427-433)."""
+    n = flat.numel() if isinstance(flat, torch.Tensor) else np.asarray(flat).size
+    if n <= max_samples:
+        return flat
+    idx = np.random.RandomState(42).choice(n, max_samples, replace=False)
+    if isinstance(flat, torch.Tensor):
+        return flat.reshape(-1)[torch.from_numpy(idx).to(flat.device)]
+    return np.asarray(flat).ravel()[idx]
+
+
+def build_kmeans_codebook(flat, n_clusters=256):
+    """_build_kmeans_codebook: k-means on the subsample, fp32 codebook."""
+    cb, _ = _simple_kmeans(kmeans_sample(flat), n_clusters, max_iters=10)
+    return cb if isinstance(cb, torch.Tensor) else cb.astype(np.float32)
+
+
+def build_uniform_codebook(flat, n_clusters=256):
+    """_build_uniform_codebook: linspace(min, max, n_clusters) in fp32."""
+    if isinstance(flat, torch.Tensor):
+        vmin, vmax = float(flat.min()), float(flat.max())
+        return torch.from_numpy(np.linspace(vmin, vmax, n_clusters).astype(np.float32)).to(flat.device)
+    flat = np.asarray(flat)
+    return np.linspace(float(flat.min()), float(flat.max()), n_clusters).astype(np.float32)

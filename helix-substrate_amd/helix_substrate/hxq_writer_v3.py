@@ -2,9 +2,13 @@
 
 Writes the directory layout of the reference ``CDNAv3Writer``
 (``helix_substrate/hxq_writer_v3.py:234-296``: meta.json keys, codebook.npy,
-indices.bin, sidecar.npz with fp16 values, codebook SHA-256) for tensors that
-are already quantised, plus the affine extension files group_scale.npy /
-group_offset.npy with meta "group_size".
+indices.bin, sidecar.npz with fp16 values, codebook SHA-256), plus the affine
+extension files group_scale.npy / group_offset.npy with meta "group_size".
+``write_quantized`` takes an already quantised tensor; ``write_tensor``
+quantises one (the reference's scalar ``_write_quantized`` path,
+``hxq_writer_v3.py:162-336``): k-means (or uniform) codebook, nearest-entry
+indices, percentile sidecar trimmed to ``max_corrections`` -- on the GPU for
+device tensors.
 """
 from __future__ import annotations
 
@@ -29,7 +33,7 @@ class CDNAv3Writer:
 
     def write_quantized(self, tensor_name: str, codebook: np.ndarray, indices: np.ndarray,
                         sidecar_positions=None, sidecar_values=None, group_scale=None,
-                        group_offset=None, group_size: int = 128) -> Path:
+                        group_offset=None, group_size: int = 128, extra_meta=None) -> Path:
         codebook = np.ascontiguousarray(codebook, dtype=np.float32)
         indices = np.ascontiguousarray(indices, dtype=np.uint8)
         rows, cols = indices.shape
@@ -54,5 +58,72 @@ class CDNAv3Writer:
         }
         if group_scale is not None:
             meta["group_size"] = int(group_size)
+        if extra_meta:
+            meta.update(extra_meta)
         (out / "meta.json").write_text(json.dumps(meta, indent=2))
         return out
+
+    def write_tensor(self, tensor, tensor_name: str, n_clusters: int = 256,
+                     percentile: float = 99.9, use_kmeans: bool = True,
+                     sidecar_enabled: bool = True, max_corrections: int = 512,
+                     storage_mode: str = "codebook+sidecar", tensor_class: str = "unknown",
+                     source_artifact: str = "") -> dict:
+        """Quantise a 2-D fp32 tensor (numpy, or a device tensor for the GPU
+        path) and write its directory; returns the stats the reference writes
+        to stats.json."""
+        import torch
+
+        from .generate_sidecars_v3 import find_outliers_percentile
+        from .hxq_encoder import build_kmeans_codebook, build_uniform_codebook, chunked_assign
+
+        dev = isinstance(tensor, torch.Tensor) and tensor.is_cuda
+        if not dev:
+            tensor = np.asarray(tensor, dtype=np.float32)
+        rows, cols = tensor.shape
+        flat = tensor.reshape(-1).float() if dev else tensor.ravel()
+        codebook = (build_kmeans_codebook(flat, n_clusters) if use_kmeans
+                    else build_uniform_codebook(flat, n_clusters))
+        indices = chunked_assign(flat, codebook)
+        recon = codebook[indices.long()] if dev else codebook[indices]
+        positions = values = None
+        if sidecar_enabled:
+            positions, values = find_outliers_percentile(tensor, percentile)
+            if dev:
+                positions, values = positions.cpu().numpy(), values.cpu().numpy()
+            if max_corrections > 0 and len(positions) > max_corrections:
+                # keep the largest |value| entries (same numpy calls as the reference)
+                top = np.argsort(np.abs(values))[::-1][:max_corrections]
+                positions = np.sort(positions[top])
+                values = (flat[torch.from_numpy(positions).to(flat.device)].cpu().numpy() if dev
+                          else flat[positions])
+            if len(positions) == 0:
+                positions = values = None
+
+        def cosine(a, b):
+            a = torch.as_tensor(a).double().reshape(-1)
+            b = torch.as_tensor(b).double().reshape(-1).to(a.device)
+            na, nb = a.norm(), b.norm()
+            return 0.0 if na == 0 or nb == 0 else float((a @ b) / (na * nb))
+
+        cos_no = cosine(flat, recon)
+        cos_sc = cos_no
+        if positions is not None:
+            patched = torch.as_tensor(recon).clone().reshape(-1)
+            pos_t = torch.from_numpy(positions).to(patched.device)
+            patched[pos_t] = torch.as_tensor(values).to(patched.device).to(patched.dtype)
+            cos_sc = cosine(flat, patched)
+        cb_np = codebook.cpu().numpy() if dev else codebook
+        idx_np = (indices.cpu().numpy() if dev else indices).reshape(rows, cols)
+        out = self.write_quantized(
+            tensor_name, cb_np, idx_np, positions, values,
+            extra_meta={"storage_mode": storage_mode, "tensor_class": tensor_class,
+                        "n_clusters": int(n_clusters), "percentile": percentile,
+                        "use_kmeans": use_kmeans, "sidecar_enabled": sidecar_enabled,
+                        "source_artifact": source_artifact})
+        stats = {"tensor_name": tensor_name, "shape": [rows, cols],
+                 "original_bytes": rows * cols * 4,
+                 "cosine_no_sidecar": round(cos_no, 6), "cosine_with_sidecar": round(cos_sc, 6),
+                 "num_outliers": 0 if positions is None else int(len(positions)),
+                 "n_clusters": int(len(cb_np)), "codec_decision": storage_mode}
+        (out / "stats.json").write_text(json.dumps(stats, indent=2))
+        return stats

@@ -336,6 +336,53 @@ int hxq_argmax(const float *logits, int64_t n, int32_t *out_id, int32_t *pos,
                void *workspace, hipStream_t stream);
 
 /*
+ * CDNAv3 encoder (k-means codebook, assignment, percentile sidecar), with the
+ * reference's numpy results reproduced bit for bit (fp32 argmin with first
+ * index on ties; cluster means as numpy's fp32 pairwise sums over 8192-element
+ * blocks; numpy's 'linear' percentiles).
+ *
+ * hxq_assign_nearest: indices[i] = argmin_j |x[i] - codebook[j]| (k <= 256).
+ *   Replaces: CDNAv3Writer._chunked_assign / _gpu_assign
+ *   (helix_substrate/hxq_writer_v3.py:449-487).
+ * hxq_kmeans_init: sorts x (keys in the workspace, kept for hxq_kmeans_run)
+ *   and counts its distinct values into *n_unique (device int32).
+ * hxq_kmeans_run: k centroids initialised at the percentiles
+ *   percentiles01[j] (fp64, the reference's np.linspace(0, 100, k) / 100) of
+ *   the sorted sample, then up to max_iters Lloyd steps on the device, stopping
+ *   when the largest centroid move is below rtol * (c[k-1] - c[0]); writes
+ *   codebook fp32 [k], assignments u8 [n] (of the last assignment step) and
+ *   *iters (device int32).  Same workspace as hxq_kmeans_init, called before
+ *   on the same x.  max_iters >= 1 (with none the reference has no
+ *   assignments).
+ *   Replaces: _simple_kmeans (helix_substrate/hxq_encoder.py:107-177).
+ * hxq_select_f32: values[r] = the ranks[r]-th smallest element (0-based,
+ *   numpy sort order, NaN last) for m <= 4 ranks (device int64 ranks);
+ *   *nan_count (optional, device) = number of NaNs.
+ * hxq_outliers_f32: positions (ascending) and values of x < lohi[0] or
+ *   x > lohi[1] (device fp32 thresholds); *count (device int64) = total, at
+ *   most `capacity` written.
+ *   With hxq_select_f32 these replace find_outliers_percentile
+ *   (helix_substrate/generate_sidecars_v3.py:18-40).
+ */
+int hxq_assign_nearest(const float *x, int64_t n, const float *codebook, int32_t k,
+                       uint8_t *indices, hipStream_t stream);
+int64_t hxq_sort_workspace_bytes(int64_t n);
+int64_t hxq_kmeans_workspace_bytes(int64_t n);
+int hxq_kmeans_init(const float *x, int64_t n, void *workspace, int64_t workspace_bytes,
+                    int32_t *n_unique, hipStream_t stream);
+int hxq_kmeans_run(const float *x, int64_t n, const double *percentiles01, int32_t k,
+                   int32_t max_iters, double rtol, void *workspace, int64_t workspace_bytes,
+                   float *codebook, uint8_t *assignments, int32_t *iters, hipStream_t stream);
+int64_t hxq_select_workspace_bytes(void);
+int hxq_select_f32(const float *x, int64_t n, const int64_t *ranks, int32_t m, float *values,
+                   int32_t *nan_count, void *workspace, int64_t workspace_bytes,
+                   hipStream_t stream);
+int64_t hxq_outliers_workspace_bytes(int64_t n);
+int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capacity,
+                     int64_t *positions, float *values, int64_t *count, void *workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * Whole greedy decode step in ONE launch per token (persistent kernel, one
  * 16-wave block per compute unit, grid barriers between the stages; the
  * next stage's compressed weights are fetched while the grid synchronises).

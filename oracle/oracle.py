@@ -29,6 +29,11 @@ Reference functions restated (file:line under the reference checkout):
 * ``rmsnorm_np`` / ``rope_np`` / ``causal_gqa_attention_np`` /
   ``qwen2_logits_np`` -- the Qwen2-shaped decoder around the HXQ projections
   (transformers' Qwen2, cited at the functions), composed from ``linear_np``.
+* ``assign_nearest_np`` / ``kmeans_np`` / ``find_outliers_percentile_np`` /
+  ``write_tensor_np`` -- the CDNAv3 encoder's CPU algorithm
+  (``hxq_encoder.py:107-177``, ``hxq_writer_v3.py:162-226, 427-467``,
+  ``generate_sidecars_v3.py:18-40``), and ``mean_f32`` / ``percentile_f32``
+  / ``percentiles_f64`` -- exact restatements of the numpy arithmetic it uses.
 * ``ssm_scan_chunked_np`` -- the chunked closed form of the same recurrence
   (the algorithm of ``chunked_scan``, ``mamba_scan_chunked.py:89-213``), written
   in the segment-sum form exp(cumA_t - cumA_s) that cannot overflow; fp64.
@@ -399,3 +404,154 @@ def qwen2_logits_np(tokens, embed, layers, final_norm, n_heads, n_kv, head_dim, 
         g = linear_np(h, L["gate"])
         x = x + linear_np(silu_np(g) * linear_np(h, L["up"]), L["down"])
     return linear_np(rmsnorm_np(x, final_norm, eps), E)
+
+
+# ---------------------------------------------------------------------------
+# CDNAv3 encoder: the reference's CPU algorithm (hxq_encoder.py:107-177
+# _simple_kmeans, hxq_writer_v3.py:427-470 subsample / assignment,
+# generate_sidecars_v3.py:18-40 percentile outliers), restated with the same
+# numpy calls, plus exact restatements of the numpy arithmetic the GPU
+# kernels reproduce (fp32 mean, 'linear' percentiles).
+# ---------------------------------------------------------------------------
+def assign_nearest_np(x, codebook, chunk=1 << 16):
+    """argmin_j |x - c_j| in fp32, first index on ties (reference
+    _chunked_assign, hxq_writer_v3.py:449-467)."""
+    x = np.asarray(x, np.float32).ravel()
+    c = np.asarray(codebook, np.float32)
+    out = np.empty(x.size, np.int64)
+    for s in range(0, x.size, chunk):
+        out[s:s + chunk] = np.argmin(np.abs(x[s:s + chunk, None] - c), axis=1)
+    return out.astype(np.uint8 if c.size <= 256 else np.uint16)
+
+
+def kmeans_np(data, n_clusters, max_iters=10, rtol=0.001):
+    """_simple_kmeans CPU branch (hxq_encoder.py:132-177): percentile init,
+    argmin assignment, per-cluster np.mean over a boolean mask, stop when the
+    largest move is below rtol * codebook range (returning the centroids
+    before that last update).  Returns (centroids, assignments, iterations)."""
+    data = np.asarray(data, np.float32).ravel()
+    n_clusters = min(n_clusters, len(np.unique(data)))
+    centroids = np.percentile(data, np.linspace(0, 100, n_clusters)).astype(np.float32)
+    cb_range = float(centroids[-1] - centroids[0])
+    if cb_range < 1e-30:
+        cb_range = 1.0
+    abs_tol = rtol * cb_range
+    assignments = None
+    it = 0
+    for _ in range(max_iters):
+        it += 1
+        assignments = assign_nearest_np(data, centroids)
+        new = np.zeros_like(centroids)
+        for i in range(n_clusters):
+            mask = assignments == i
+            new[i] = np.mean(data[mask]) if np.any(mask) else centroids[i]
+        if float(np.max(np.abs(new - centroids))) < abs_tol:
+            break
+        centroids = new
+    return centroids, assignments, it
+
+
+def kmeans_sample_np(flat, max_samples=500_000):
+    """The writer's k-means subsample (hxq_writer_v3.py:427-433)."""
+    flat = np.asarray(flat).ravel()
+    if flat.size <= max_samples:
+        return flat
+    return flat[np.random.RandomState(42).choice(flat.size, max_samples, replace=False)]
+
+
+def find_outliers_percentile_np(tensor, percentile=99.9):
+    """generate_sidecars_v3.py:18-40: both tails beyond the percentile."""
+    flat = np.asarray(tensor, np.float32).ravel()
+    lo = np.percentile(flat, 100.0 - percentile)
+    hi = np.percentile(flat, percentile)
+    pos = np.where((flat < lo) | (flat > hi))[0].astype(np.int64)
+    return pos, flat[pos].astype(np.float32)
+
+
+def write_tensor_np(tensor, n_clusters=256, percentile=99.9, max_corrections=512):
+    """The scalar _write_quantized pipeline (hxq_writer_v3.py:162-226):
+    (codebook, indices [rows, cols], sidecar positions, sidecar values)."""
+    tensor = np.asarray(tensor, np.float32)
+    flat = tensor.ravel()
+    codebook, _, _ = kmeans_np(kmeans_sample_np(flat), n_clusters, max_iters=10)
+    codebook = codebook.astype(np.float32)
+    indices = assign_nearest_np(flat, codebook).reshape(tensor.shape)
+    pos, val = find_outliers_percentile_np(tensor, percentile)
+    if max_corrections > 0 and len(pos) > max_corrections:
+        top = np.argsort(np.abs(val))[::-1][:max_corrections]
+        pos = np.sort(pos[top])
+        val = flat[pos]
+    return codebook, indices, pos, val
+
+
+def pairwise_sum_f32(a):
+    """numpy's fp32 pairwise summation of one buffer (<= 8192 elements):
+    below 8 a plain loop, up to 128 eight running sums combined as
+    ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) plus the tail, above that split at
+    n/2 rounded down to a multiple of 8."""
+    f32 = np.float32
+    a = np.asarray(a, np.float32)
+    n = a.size
+    if n < 8:
+        r = f32(0)
+        for v in a:
+            r = f32(r + v)
+        return r
+    if n <= 128:
+        m = n - n % 8
+        r = a[:8].copy()
+        for row in a[8:m].reshape(-1, 8):
+            r = (r + row).astype(np.float32)
+        res = f32(f32(f32(r[0] + r[1]) + f32(r[2] + r[3])) + f32(f32(r[4] + r[5]) + f32(r[6] + r[7])))
+        for v in a[m:]:
+            res = f32(res + v)
+        return res
+    n2 = n // 2
+    n2 -= n2 % 8
+    return f32(pairwise_sum_f32(a[:n2]) + pairwise_sum_f32(a[n2:]))
+
+
+def mean_f32(a):
+    """np.mean of fp32 data: fp32 sum of the pairwise sums of consecutive
+    8192-element buffers, divided by the count in fp32."""
+    a = np.asarray(a, np.float32)
+    s = None
+    for i in range(0, a.size, 8192):
+        p = pairwise_sum_f32(a[i:i + 8192])
+        s = p if s is None else np.float32(s + p)
+    return np.float32(s / np.float32(a.size))
+
+
+def percentile_f32(x, q):
+    """np.percentile(x, q) for fp32 x and a scalar q: virtual index and
+    interpolation in fp32 (numpy divides q by the data's dtype)."""
+    f32 = np.float32
+    s = np.sort(np.asarray(x, np.float32).ravel())
+    n = s.size
+    v = f32(n - 1) * (f32(q) / f32(100))
+    if v >= n - 1:
+        return s[-1]
+    i = int(np.floor(v))
+    t = f32(v - f32(i))
+    a, b = s[i], s[i + 1]
+    d = f32(b - a)
+    return f32(b - d * (f32(1) - t)) if t >= 0.5 else f32(a + d * t)
+
+
+def percentiles_f64(x, qs):
+    """np.percentile(x, qs) for fp32 x and an array qs: fp64 virtual index
+    and interpolation over fp32 order statistics (their difference in fp32)."""
+    s = np.sort(np.asarray(x, np.float32).ravel())
+    n = s.size
+    out = []
+    for q in np.asarray(qs, np.float64) / np.float32(100):
+        v = (n - 1) * q
+        if v >= n - 1:
+            out.append(np.float64(s[-1]))
+            continue
+        i = int(np.floor(v))
+        t = v - i
+        a, b = s[i], s[i + 1]
+        d = np.float64(np.float32(b - a))
+        out.append(np.float64(b) - d * (1 - t) if t >= 0.5 else np.float64(a) + d * t)
+    return np.array(out)

@@ -1,0 +1,162 @@
+"""GPU CDNAv3 encoder against the oracle, bit for bit: nearest-codebook
+assignment (ties, NaN, infinities, unsorted and duplicated codebooks),
+1-D k-means (codebook, assignments and the iteration at which the
+reference's convergence test stops), exact order statistics / numpy
+percentiles, two-tailed percentile outliers, and the whole write_tensor
+pipeline's files."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helix_substrate import _hxq, hxq_encoder
+from helix_substrate.generate_sidecars_v3 import find_outliers_percentile
+from helix_substrate.hxq_writer_v3 import CDNAv3Writer
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(rs, n, scale=0.02):
+    w = (rs.standard_t(5, n) * scale).astype(np.float32)
+    return w
+
+
+def _bf16(x):
+    return torch.from_numpy(x).bfloat16().float().numpy()
+
+
+@pytest.mark.parametrize("case", ["sorted256", "unsorted37", "dups", "specials", "ragged"])
+def test_assign_matches_oracle(dev, case):
+    rs = np.random.RandomState(11)
+    x = _weights(rs, 1 << 20)
+    if case == "sorted256":
+        cb = np.sort(_weights(rs, 256))
+    elif case == "unsorted37":
+        cb = _weights(rs, 37)
+    elif case == "dups":
+        cb = np.sort(np.repeat(_weights(rs, 40), 3))[:100]
+        x = np.concatenate([x, cb, (cb[1:] + cb[:-1]) / 2])  # exact hits and midpoints
+    elif case == "specials":
+        cb = np.sort(_weights(rs, 64))
+        x[:8] = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30, cb[5]]
+        mids = (cb[:-1] + np.diff(cb) / 2).astype(np.float32)  # near-ties
+        x[8:8 + mids.size] = mids
+    else:
+        x = x[:1000003]
+        cb = np.sort(_weights(rs, 255))
+        cb[10] = np.nan  # unsorted path (NaN in the codebook)
+    print(f"assign case={case} n={x.size} k={cb.size}", flush=True)
+    got = _hxq.assign_nearest(torch.from_numpy(x).to(dev), torch.from_numpy(cb).to(dev))
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle.assign_nearest_np(x, cb))
+
+
+def _kmeans_cases():
+    rs = np.random.RandomState(12)
+    return {
+        "t5_20k": _weights(rs, 20000),
+        "bf16_ties_100k": _bf16(_weights(rs, 100000)),
+        "few_unique": rs.choice(_weights(rs, 50), 30000).astype(np.float32),
+        # 16 wide clusters of ~12K members: means over several 8192-element blocks
+        "big_clusters_k16": (rs.randint(0, 16, 200000) + rs.randn(200000) * 0.05).astype(np.float32),
+        "tiny": np.float32([3.0, -1.0, 3.0, 2.5]),
+        "constant": np.full(1000, 0.25, np.float32),
+        "with_nan": np.concatenate([_weights(rs, 999), np.float32([np.nan])]),
+    }
+
+
+@pytest.mark.parametrize("name", list(_kmeans_cases().keys()))
+def test_kmeans_matches_oracle(dev, name):
+    data = _kmeans_cases()[name]
+    k = 16 if name == "big_clusters_k16" else 256
+    print(f"kmeans case={name} n={data.size} k={k}", flush=True)
+    cb, asg, it = _hxq.kmeans_1d(torch.from_numpy(data).to(dev), k, 10, 0.001)
+    cb_o, asg_o, it_o = oracle.kmeans_np(data, k)
+    np.testing.assert_array_equal(cb.cpu().numpy(), cb_o)
+    np.testing.assert_array_equal(asg.cpu().numpy(), asg_o)
+    assert it == it_o
+
+
+def test_kmeans_iteration_limits(dev):
+    data = _weights(np.random.RandomState(13), 5000)
+    x = torch.from_numpy(data).to(dev)
+    for max_iters, rtol in [(1, 0.001), (3, 0.0), (10, 10.0)]:
+        cb, asg, it = _hxq.kmeans_1d(x, 64, max_iters, rtol)
+        cb_o, asg_o, it_o = oracle.kmeans_np(data, 64, max_iters=max_iters, rtol=rtol)
+        np.testing.assert_array_equal(cb.cpu().numpy(), cb_o)
+        np.testing.assert_array_equal(asg.cpu().numpy(), asg_o)
+        assert it == it_o
+    with pytest.raises(RuntimeError):
+        _hxq.kmeans_1d(x, 64, 0, 0.001)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 1000, 65537, 1 << 22])
+def test_percentiles_match_numpy(dev, n):
+    rs = np.random.RandomState(n)
+    x = _weights(rs, n)
+    if n > 3:
+        x[: n // 3] = _bf16(x[: n // 3])  # duplicated values
+        x[5] = -0.0
+    print(f"percentile n={n}", flush=True)
+    qs = [99.9, 0.1, 50.0, 0.0, 100.0, 37.5]
+    got = _hxq.percentile_f32(torch.from_numpy(x).to(dev), qs)
+    for q, g in zip(qs, got):
+        assert g == np.percentile(x, q), q
+    ranks = sorted(set(int(r) for r in rs.randint(0, n, 4)))
+    vals, nans = _hxq.select_f32(torch.from_numpy(x).to(dev), ranks)
+    np.testing.assert_array_equal(vals.cpu().numpy(), np.sort(x)[ranks])
+    assert nans == 0
+
+
+def test_select_nan_last(dev):
+    x = np.float32([2.0, np.nan, -1.0, np.inf, np.nan, -np.inf, 0.5])
+    vals, nans = _hxq.select_f32(torch.from_numpy(x).to(dev), [0, 1, 4, 5])
+    assert nans == 2
+    np.testing.assert_array_equal(vals.cpu().numpy(), np.sort(x)[[0, 1, 4, 5]])
+    assert np.isnan(_hxq.percentile_f32(torch.from_numpy(x).to(dev), [50.0])[0])
+
+
+@pytest.mark.parametrize("shape,pct", [((2048, 2048), 99.9), ((11008, 256), 99.0), ((7, 13), 90.0),
+                                       ((1, 1), 99.9)])
+def test_outliers_match_oracle(dev, shape, pct):
+    rs = np.random.RandomState(14)
+    t = _weights(rs, shape[0] * shape[1]).reshape(shape)
+    print(f"outliers shape={shape} pct={pct}", flush=True)
+    pos, val = find_outliers_percentile(torch.from_numpy(t).to(dev), pct)
+    pos_o, val_o = oracle.find_outliers_percentile_np(t, pct)
+    np.testing.assert_array_equal(pos.cpu().numpy(), pos_o)
+    np.testing.assert_array_equal(val.cpu().numpy(), val_o)
+
+
+@pytest.mark.parametrize("shape", [(256, 1024), (1024, 768)])
+def test_write_tensor_files_match_oracle(dev, tmp_path, shape):
+    rs = np.random.RandomState(15)
+    t = _weights(rs, shape[0] * shape[1]).reshape(shape)
+    print(f"write_tensor shape={shape}", flush=True)
+    w = CDNAv3Writer(tmp_path / "gpu")
+    stats = w.write_tensor(torch.from_numpy(t).to(dev), "blk.0.ffn_up.weight")
+    w_cpu = CDNAv3Writer(tmp_path / "cpu")
+    stats_cpu = w_cpu.write_tensor(t, "blk.0.ffn_up.weight")
+    cb_o, idx_o, pos_o, val_o = oracle.write_tensor_np(t)
+    d = tmp_path / "gpu" / "blk_0_ffn_up_weight.cdnav3"
+    np.testing.assert_array_equal(np.load(d / "codebook.npy"), cb_o)
+    np.testing.assert_array_equal(np.fromfile(d / "indices.bin", np.uint8).reshape(shape), idx_o)
+    with np.load(d / "sidecar.npz") as z:
+        np.testing.assert_array_equal(z["positions"], pos_o)
+        np.testing.assert_array_equal(z["values"], val_o.astype(np.float16))
+    dc = tmp_path / "cpu" / "blk_0_ffn_up_weight.cdnav3"
+    for f in ("codebook.npy", "indices.bin"):
+        assert (d / f).read_bytes() == (dc / f).read_bytes(), f
+    for key in ("shape", "num_outliers", "n_clusters"):
+        assert stats[key] == stats_cpu[key]
+    for key in ("cosine_no_sidecar", "cosine_with_sidecar"):  # fp64 dot products, any order
+        assert abs(stats[key] - stats_cpu[key]) <= 2e-6
+
+
+def test_large_sample_codebook(dev):
+    """The writer's 500K-sample k-means on a 2048 x 1024 tensor."""
+    rs = np.random.RandomState(16)
+    flat = _weights(rs, 2048 * 1024)
+    print("kmeans 500K sample", flush=True)
+    cb = hxq_encoder.build_kmeans_codebook(torch.from_numpy(flat).to(dev), 256)
+    cb_o, _, _ = oracle.kmeans_np(oracle.kmeans_sample_np(flat), 256)
+    np.testing.assert_array_equal(cb.cpu().numpy(), cb_o)
