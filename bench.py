@@ -51,6 +51,9 @@ def parse():
                     help="only launch the dominant kernel for counter runs (rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE): the gate+up GEMV of 12 layers twice, then "
                          "a 256 MiB copy as the counter calibration; prints no JSON")
+    ap.add_argument("--encode", type=int, default=1,
+                    help="also time the CDNAv3 encoder on one Qwen2.5-3B gate_proj "
+                         "(k-means codebook, assignment, percentile sidecar)")
     ap.add_argument("--decode", type=int, default=1,
                     help="also run the config-1 greedy decode loop (tok/s, 128-token prompt, "
                          "256 new tokens)")
@@ -260,6 +263,8 @@ def main():
         result["mixer_config3"] = mixer_bench(dev)
     if args.moe:
         result["moe_config4"] = moe_bench(dev, cpu=args.cpu_seconds > 0)
+    if args.encode:
+        result["encode_cdnav3"] = encode_bench(dev, cpu=args.cpu_seconds > 0)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layer0, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -601,6 +606,74 @@ def moe_bench(dev, n_layers=16, iters=3, cpu=True):
                                "sample": "layer 0, all 512 tokens, per-expert torch CPU loop",
                                "kind": "port", "cores": torch.get_num_threads()}
     del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+def encode_bench(dev, iters=3, cpu=True):
+    """CDNAv3 encode of one Qwen2.5-3B gate_proj (11008 x 2048 fp32, N(0, 0.02)):
+    the writer's 500K-sample k-means codebook (256 entries, up to 10 Lloyd
+    steps), nearest-entry assignment of all 22.5M weights, and the two-tailed
+    99.9th-percentile sidecar cut to the 512 largest |value|.  Timed end to
+    end (host syncs included: the distinct-value count, the iteration count
+    and the top-512 cut run on the host, as in the writer)."""
+    import numpy as np
+    import torch
+    from helix_substrate import hxq_encoder
+    from helix_substrate.generate_sidecars_v3 import find_outliers_percentile
+
+    rows, cols = INTER, HIDDEN
+    g = torch.Generator(device=dev).manual_seed(7)
+    w = torch.randn(rows, cols, device=dev, generator=g) * 0.02
+    flat = w.reshape(-1)
+    stages = {"kmeans_ms": 0.0, "assign_ms": 0.0, "sidecar_ms": 0.0}
+
+    def encode(timed):
+        t0 = time.perf_counter()
+        cb = hxq_encoder.build_kmeans_codebook(flat, 256)
+        torch.cuda.synchronize(dev)
+        t1 = time.perf_counter()
+        idx = hxq_encoder.chunked_assign(flat, cb)
+        torch.cuda.synchronize(dev)
+        t2 = time.perf_counter()
+        pos, val = find_outliers_percentile(w, 99.9)
+        pos, val = pos.cpu().numpy(), val.cpu().numpy()
+        if len(pos) > 512:
+            pos = np.sort(pos[np.argsort(np.abs(val))[::-1][:512]])
+        t3 = time.perf_counter()
+        if timed:
+            stages["kmeans_ms"] += (t1 - t0) * 1e3 / iters
+            stages["assign_ms"] += (t2 - t1) * 1e3 / iters
+            stages["sidecar_ms"] += (t3 - t2) * 1e3 / iters
+        return cb, idx, pos
+
+    encode(False)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        encode(True)
+    ms = (time.perf_counter() - t0) * 1e3 / iters
+    n = rows * cols
+    out = {"tensor": [rows, cols], "ms_per_tensor": round(ms, 2),
+           "mweights_per_s": round(n / ms / 1e3, 1),
+           **{k: round(v, 2) for k, v in stages.items()},
+           "assign_gbs": round(n * 5 / (stages["assign_ms"] * 1e6), 1)}
+    if cpu:
+        # the reference's numpy pipeline (oracle restatement) on a 2048 x 2048
+        # sample of the same distribution: 500K-sample k-means, argmin
+        # assignment of all 4.2M weights, percentile sidecar
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle
+
+        sample = w[:2048].cpu().numpy()
+        t0 = time.perf_counter()
+        oracle.write_tensor_np(sample)
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"mweights_per_s": round(sample.size / el / 1e6, 3),
+                               "s_per_sample": round(el, 2),
+                               "sample": "2048 x 2048 rows of the same tensor, numpy pipeline "
+                                         "(oracle.write_tensor_np)",
+                               "kind": "port", "cores": 1}
+    del w, flat
     torch.cuda.empty_cache()
     return out
 

@@ -10,6 +10,8 @@ init, same first-index argmin, cluster means summed in numpy's order).
 """
 from __future__ import annotations
 
+import functools
+
 import numpy as np
 import torch
 
@@ -69,13 +71,19 @@ def _simple_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
     return centroids, assignments
 
 
+@functools.lru_cache(maxsize=16)
+def _sample_index(n, max_samples):
+    # depends on (n, max_samples) only: RandomState(42) is reseeded per call
+    return np.random.RandomState(42).choice(n, max_samples, replace=False)
+
+
 def kmeans_sample(flat, max_samples=KMEANS_MAX_SAMPLES):
     """The reference's k-means subsample: all of flat, or RandomState(42)
     .choice(n, max_samples, replace=False) of it (hxq_writer_v3.py:427-433)."""
     n = flat.numel() if isinstance(flat, torch.Tensor) else np.asarray(flat).size
     if n <= max_samples:
         return flat
-    idx = np.random.RandomState(42).choice(n, max_samples, replace=False)
+    idx = _sample_index(int(n), int(max_samples))
     if isinstance(flat, torch.Tensor):
         return flat.reshape(-1)[torch.from_numpy(idx).to(flat.device)]
     return np.asarray(flat).ravel()[idx]
