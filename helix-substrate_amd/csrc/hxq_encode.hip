@@ -531,6 +531,82 @@ __global__ __launch_bounds__(kThreads) void outlier_write_kernel(const float *x,
     }
 }
 
+// ---------------------------------------------------------------------------
+// per-group affine fit: (s, o) = argmin sum_j (s c_j + o - w_j)^2 over the
+// group's elements not in the sidecar, c_j = codebook[idx_j]; fp64 sums in a
+// fixed order (lane l of the group's wave adds elements l, l+64, ... in turn,
+// then a xor butterfly 32, 16, ..., 1), closed-form solution in fp64, fp32
+// results.  Degenerate groups (n < 2 or a zero determinant) keep s = 1 and
+// take o = mean(w - c) (0 for an empty group).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void mark_kernel(const int64_t *pos, int64_t m, uint32_t *bits) {
+    for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < m;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t p = pos[i];
+        atomicOr(&bits[p >> 5], 1u << (p & 31));
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void zero_u32_kernel(uint32_t *p, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kThreads)
+        p[i] = 0u;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma clang fp contract(off)
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, kWave);
+    return v;
+}
+
+__global__ __launch_bounds__(kThreads) void affine_fit_kernel(const float *w, const uint8_t *idx,
+                                                              const float *cb, int k, int64_t rows,
+                                                              int64_t cols, int group,
+                                                              const uint32_t *bits, float *scale,
+                                                              float *offset) {
+#pragma clang fp contract(off)
+    __shared__ float s_cb[kMaxK];
+    for (int j = threadIdx.x; j < kMaxK; j += kThreads) s_cb[j] = j < k ? cb[j] : 0.f;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t ngroups = cols / group;
+    const int64_t unit = blockIdx.x * (int64_t)(kThreads / kWave) + threadIdx.x / kWave;
+    if (unit >= rows * ngroups) return;
+    const int64_t r = unit / ngroups, g = unit % ngroups;
+    const int64_t base = r * cols + g * group;
+    double sc = 0.0, sw = 0.0, scc = 0.0, scw = 0.0, sn = 0.0;
+    for (int t = lane; t < group; t += kWave) {
+        const int64_t e = base + t;
+        const bool skip = bits && ((bits[e >> 5] >> (e & 31)) & 1u);
+        if (!skip) {
+            const double c = static_cast<double>(s_cb[idx[e]]);
+            const double x = static_cast<double>(w[e]);
+            sc = sc + c;
+            sw = sw + x;
+            scc = scc + c * c;
+            scw = scw + c * x;
+            sn = sn + 1.0;
+        }
+    }
+    sc = wave_sum_f64(sc);
+    sw = wave_sum_f64(sw);
+    scc = wave_sum_f64(scc);
+    scw = wave_sum_f64(scw);
+    sn = wave_sum_f64(sn);
+    if (lane == 0) {
+        double s = 1.0, o = 0.0;
+        const double det = sn * scc - sc * sc;
+        if (sn >= 2.0 && det > 0.0) {
+            s = (sn * scw - sc * sw) / det;
+            o = (sw - s * sc) / sn;
+        } else if (sn > 0.0) {
+            o = (sw - sc) / sn;
+        }
+        scale[r * ngroups + g] = static_cast<float>(s);
+        offset[r * ngroups + g] = static_cast<float>(o);
+    }
+}
+
 static int grid_for(int64_t n) {
     const int64_t g = (n + kThreads - 1) / kThreads;
     return static_cast<int>(std::min<int64_t>(std::max<int64_t>(g, 1), 8192));
@@ -712,5 +788,42 @@ extern "C" int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, in
                            blk, capacity, positions, values);
         HXQ_LAUNCH_CHECK();
     }
+    return HXQ_OK;
+}
+
+extern "C" int64_t hxq_affine_fit_workspace_bytes(int64_t rows, int64_t cols) {
+    return rows <= 0 || cols <= 0 ? 0 : 4 * ((rows * cols + 31) / 32);
+}
+
+extern "C" int hxq_affine_fit(const float *w, const uint8_t *indices, const float *codebook,
+                              int32_t k, int64_t rows, int64_t cols, int32_t group_size,
+                              const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
+                              int64_t workspace_bytes, float *scale, float *offset,
+                              hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(w && indices && codebook && scale && offset, "bad arguments");
+    HXQ_REQUIRE(k >= 1 && k <= kMaxK && rows >= 1 && cols >= 1, "bad sizes (k 1..256)");
+    HXQ_REQUIRE(group_size >= 1 && cols % group_size == 0, "cols must be a multiple of group_size");
+    HXQ_REQUIRE(n_exclude >= 0 && (n_exclude == 0 || exclude_positions), "bad exclusion list");
+    uint32_t *bits = nullptr;
+    if (n_exclude > 0) {
+        HXQ_REQUIRE(workspace && workspace_bytes >= hxq_affine_fit_workspace_bytes(rows, cols),
+                    "workspace too small");
+        bits = static_cast<uint32_t *>(workspace);
+        const int64_t words = (rows * cols + 31) / 32;
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(grid_for(words)), dim3(kThreads), 0, stream, bits,
+                           words);
+        HXQ_LAUNCH_CHECK();
+        hipLaunchKernelGGL(mark_kernel, dim3(grid_for(n_exclude)), dim3(kThreads), 0, stream,
+                           exclude_positions, n_exclude, bits);
+        HXQ_LAUNCH_CHECK();
+    }
+    const int64_t units = rows * (cols / group_size);
+    const int64_t per_block = kThreads / kWave;
+    const int64_t blocks = (units + per_block - 1) / per_block;
+    HXQ_REQUIRE(blocks < (int64_t{1} << 31), "too many groups");
+    hipLaunchKernelGGL(affine_fit_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                       stream, w, indices, codebook, k, rows, cols, group_size, bits, scale, offset);
+    HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }

@@ -101,6 +101,7 @@ SIGNATURES = {
     "hxq_kmeans_run": [P, I64, P, I32, I32, ctypes.c_double, P, I64, P, P, P, P],
     "hxq_select_f32": [P, I64, P, I32, P, P, P, I64, P],
     "hxq_outliers_f32": [P, I64, P, I64, P, P, P, P, I64, P],
+    "hxq_affine_fit": [P, P, P, I32, I64, I64, I32, P, I64, P, I64, P, P, P],
     "hxq_decoder_init": [P, P, I64, P],
     "hxq_decoder_step": [P, P, I32, P, P],
     "hxq_decoder_error": [P, P, P, P],
@@ -112,6 +113,7 @@ SIGNATURES_I64 = {
     "hxq_ssm_scan_workspace_bytes": [I64] * 6,
     "hxq_moe_ffn_workspace_bytes": [I64, I64, I64, I32],
     "hxq_decoder_workspace_bytes": [P],
+    "hxq_affine_fit_workspace_bytes": [I64, I64],
     "hxq_sort_workspace_bytes": [I64],
     "hxq_kmeans_workspace_bytes": [I64],
     "hxq_select_workspace_bytes": [],
@@ -728,3 +730,37 @@ def outliers_f32(x, lo, hi):
                                                       _ptr(val), _ptr(cnt), _ptr(ws), ws.numel(),
                                                       _stream(xf)))
     return pos, val
+
+
+def affine_fit(w, indices, codebook, group_size, exclude_positions=None):
+    """Per-group (scale, offset) fp32 [rows, cols / group_size] minimising the
+    squared error of scale * codebook[idx] + offset against w (fp32 [rows,
+    cols]) over the elements not at exclude_positions (flat int64)."""
+    _need_device(w, indices, codebook)
+    if w.dim() != 2 or tuple(indices.shape) != tuple(w.shape):
+        raise RuntimeError("affine_fit takes w [rows, cols] and indices of the same shape")
+    rows, cols = w.shape
+    if cols % group_size:
+        raise RuntimeError("cols must be a multiple of group_size")
+    wf = w.float().contiguous()
+    idx = indices.to(torch.uint8).contiguous()
+    cb = codebook.float().contiguous()
+    ng = cols // group_size
+    scale = torch.empty(rows, ng, dtype=torch.float32, device=w.device)
+    offset = torch.empty(rows, ng, dtype=torch.float32, device=w.device)
+    L = lib()
+    ex = None
+    ws = None
+    n_ex = 0
+    if exclude_positions is not None and exclude_positions.numel():
+        ex = exclude_positions.to(device=w.device, dtype=torch.int64).contiguous()
+        n_ex = ex.numel()
+        if int(ex.min()) < 0 or int(ex.max()) >= rows * cols:
+            raise RuntimeError("exclude_positions out of range")
+        ws = torch.empty(int(L.hxq_affine_fit_workspace_bytes(rows, cols)), dtype=torch.uint8,
+                         device=w.device)
+    _check("hxq_affine_fit", L.hxq_affine_fit(_ptr(wf), _ptr(idx), _ptr(cb), cb.numel(), rows, cols,
+                                              int(group_size), _ptr(ex), n_ex, _ptr(ws),
+                                              0 if ws is None else ws.numel(), _ptr(scale),
+                                              _ptr(offset), _stream(wf)))
+    return scale, offset

@@ -102,3 +102,57 @@ def build_uniform_codebook(flat, n_clusters=256):
         return torch.from_numpy(np.linspace(vmin, vmax, n_clusters).astype(np.float32)).to(flat.device)
     flat = np.asarray(flat)
     return np.linspace(float(flat.min()), float(flat.max()), n_clusters).astype(np.float32)
+
+
+def fit_group_affine(w, indices, codebook, group_size=128, exclude_positions=None):
+    """Per-group affine (scale, offset) fp32 [rows, cols / group_size] of the
+    format extension: the least-squares fit of scale * codebook[idx] + offset
+    to w over each group's elements outside the sidecar (exclude_positions,
+    flat).  fp64 sums in one fixed order (element l, l+64, ... per lane of a
+    64-lane group, then halves added pairwise), so the device kernel and this
+    numpy path give identical bits.  Degenerate groups: scale 1, offset
+    mean(w - c) (0 when every element is excluded)."""
+    if _is_device(w):
+        ex = None
+        if exclude_positions is not None and len(exclude_positions):
+            ex = torch.as_tensor(exclude_positions, dtype=torch.int64).to(w.device)
+        cb = codebook if _is_device(codebook) else torch.as_tensor(
+            np.asarray(codebook, np.float32)).to(w.device)
+        return _hxq.affine_fit(w, indices, cb, group_size, ex)
+    w = np.asarray(w, np.float32)
+    rows, cols = w.shape
+    G = int(group_size)
+    if cols % G:
+        raise ValueError("cols must be a multiple of group_size")
+    ng = cols // G
+    keep = np.ones(rows * cols, bool)
+    if exclude_positions is not None and len(exclude_positions):
+        keep[np.asarray(exclude_positions, np.int64)] = False
+    keep = keep.reshape(rows, ng, G)
+    c = np.asarray(codebook, np.float32)[np.asarray(indices, np.int64)].astype(np.float64)
+    c = c.reshape(rows, ng, G)
+    x = w.astype(np.float64).reshape(rows, ng, G)
+    lanes = -(-G // 64) * 64
+
+    def group_sum(t):
+        t = np.where(keep, t, 0.0)
+        if lanes != G:
+            t = np.concatenate([t, np.zeros((rows, ng, lanes - G))], axis=2)
+        t = t.reshape(rows, ng, lanes // 64, 64)
+        acc = t[:, :, 0, :] + 0.0
+        for j in range(1, lanes // 64):
+            acc = acc + t[:, :, j, :]
+        width = 64
+        while width > 1:
+            width //= 2
+            acc = acc[..., :width] + acc[..., width:]
+        return acc[..., 0]
+
+    sc, sw, scc, scw = group_sum(c), group_sum(x), group_sum(c * c), group_sum(c * x)
+    n = group_sum(np.ones_like(c))
+    det = n * scc - sc * sc
+    fit = (n >= 2) & (det > 0)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scale = np.where(fit, (n * scw - sc * sw) / det, 1.0)
+        offset = np.where(n > 0, (sw - scale * sc) / np.maximum(n, 1.0), 0.0)
+    return scale.astype(np.float32), offset.astype(np.float32)

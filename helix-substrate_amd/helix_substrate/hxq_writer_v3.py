@@ -63,18 +63,37 @@ class CDNAv3Writer:
         (out / "meta.json").write_text(json.dumps(meta, indent=2))
         return out
 
+    def write_exact(self, tensor, tensor_name: str) -> dict:
+        """1-D / exact tensors as fp16 ``{safe}.npy`` plus ``{safe}.npy.meta.json``
+        (reference ``_write_exact``, hxq_writer_v3.py:91-111)."""
+        import torch
+
+        if isinstance(tensor, torch.Tensor):
+            tensor = tensor.detach().float().cpu().numpy()
+        arr = np.asarray(tensor).astype(np.float16)
+        safe = _safe_name(tensor_name)
+        out = self.base_dir / f"{safe}.npy"
+        np.save(out, arr)
+        (self.base_dir / f"{safe}.npy.meta.json").write_text(json.dumps(
+            {"tensor_name": tensor_name, "shape": list(arr.shape), "storage_mode": "exact"}))
+        return {"tensor_name": tensor_name, "storage_mode": "exact", "shape": list(arr.shape),
+                "original_bytes": arr.nbytes, "compressed_bytes": out.stat().st_size}
+
     def write_tensor(self, tensor, tensor_name: str, n_clusters: int = 256,
                      percentile: float = 99.9, use_kmeans: bool = True,
                      sidecar_enabled: bool = True, max_corrections: int = 512,
                      storage_mode: str = "codebook+sidecar", tensor_class: str = "unknown",
-                     source_artifact: str = "") -> dict:
+                     source_artifact: str = "", group_size=None) -> dict:
         """Quantise a 2-D fp32 tensor (numpy, or a device tensor for the GPU
         path) and write its directory; returns the stats the reference writes
-        to stats.json."""
+        to stats.json.  group_size (extension): also fit the per-group affine
+        (least squares per row and group, sidecar positions excluded) and
+        write group_scale / group_offset."""
         import torch
 
         from .generate_sidecars_v3 import find_outliers_percentile
-        from .hxq_encoder import build_kmeans_codebook, build_uniform_codebook, chunked_assign
+        from .hxq_encoder import (build_kmeans_codebook, build_uniform_codebook, chunked_assign,
+                                  fit_group_affine)
 
         dev = isinstance(tensor, torch.Tensor) and tensor.is_cuda
         if not dev:
@@ -98,6 +117,18 @@ class CDNAv3Writer:
                           else flat[positions])
             if len(positions) == 0:
                 positions = values = None
+        gscale = goffset = None
+        if group_size:
+            idx2 = indices.reshape(rows, cols)
+            gscale, goffset = fit_group_affine(tensor, idx2, codebook, int(group_size), positions)
+            G = int(group_size)
+            if dev:
+                rs = torch.repeat_interleave(gscale, G, dim=1).reshape(-1)
+                ro = torch.repeat_interleave(goffset, G, dim=1).reshape(-1)
+            else:
+                rs = np.repeat(gscale, G, axis=1).ravel()
+                ro = np.repeat(goffset, G, axis=1).ravel()
+            recon = recon.reshape(-1) * rs + ro  # fl(fl(c * s) + o): two roundings
 
         def cosine(a, b):
             a = torch.as_tensor(a).double().reshape(-1)
@@ -114,8 +145,11 @@ class CDNAv3Writer:
             cos_sc = cosine(flat, patched)
         cb_np = codebook.cpu().numpy() if dev else codebook
         idx_np = (indices.cpu().numpy() if dev else indices).reshape(rows, cols)
+        if gscale is not None and dev:
+            gscale, goffset = gscale.cpu().numpy(), goffset.cpu().numpy()
         out = self.write_quantized(
-            tensor_name, cb_np, idx_np, positions, values,
+            tensor_name, cb_np, idx_np, positions, values, gscale, goffset,
+            int(group_size) if group_size else 128,
             extra_meta={"storage_mode": storage_mode, "tensor_class": tensor_class,
                         "n_clusters": int(n_clusters), "percentile": percentile,
                         "use_kmeans": use_kmeans, "sidecar_enabled": sidecar_enabled,

@@ -377,6 +377,24 @@ int64_t hxq_select_workspace_bytes(void);
 int hxq_select_f32(const float *x, int64_t n, const int64_t *ranks, int32_t m, float *values,
                    int32_t *nan_count, void *workspace, int64_t workspace_bytes,
                    hipStream_t stream);
+/*
+ * hxq_affine_fit: per-group affine of the encoder (an extension with no
+ * reference counterpart: the benchmark configs' group_scale / group_offset,
+ * fp32 [rows, cols / group_size]).  For each row and group of group_size
+ * columns, (s, o) minimise sum (s * codebook[idx] + o - w)^2 over the group's
+ * elements whose flat position is not in exclude_positions (the sidecar,
+ * which replaces them); fp64 sums in a fixed order (lane l of a 64-lane wave
+ * adds elements l, l + 64, ... in turn, then a xor butterfly 32 ... 1),
+ * closed form in fp64, rounded to fp32.  Groups with fewer than two elements
+ * or a zero determinant keep s = 1 and o = mean(w - c) (0 if empty).
+ * workspace: hxq_affine_fit_workspace_bytes(rows, cols) bytes (an exclusion
+ * bitmap), needed only when n_exclude > 0; positions must be < rows * cols.
+ */
+int64_t hxq_affine_fit_workspace_bytes(int64_t rows, int64_t cols);
+int hxq_affine_fit(const float *w, const uint8_t *indices, const float *codebook, int32_t k,
+                   int64_t rows, int64_t cols, int32_t group_size,
+                   const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
+                   int64_t workspace_bytes, float *scale, float *offset, hipStream_t stream);
 int64_t hxq_outliers_workspace_bytes(int64_t n);
 int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capacity,
                      int64_t *positions, float *values, int64_t *count, void *workspace,

@@ -555,3 +555,51 @@ def percentiles_f64(x, qs):
         d = np.float64(np.float32(b - a))
         out.append(np.float64(b) - d * (1 - t) if t >= 0.5 else np.float64(a) + d * t)
     return np.array(out)
+
+
+def affine_fit_np(w, indices, codebook, group_size, exclude_positions=None):
+    """Per-group affine fit of the encoder (an extension of the format with no
+    reference counterpart; the benchmark configs' group_scale/group_offset):
+    for each row and group of `group_size` columns, (s, o) minimising
+    sum (s*c + o - w)^2 with c = codebook[idx] over the group's elements not
+    in `exclude_positions` (flat positions: the sidecar).  fp64 sums in the
+    kernel's fixed order: lane l (of 64) adds elements l, l+64, ... in turn
+    starting from 0, then halves are added pairwise (32, 16, ..., 1); closed
+    form (n*Scw - Sc*Sw)/(n*Scc - Sc^2), o = (Sw - s*Sc)/n in fp64, rounded
+    to fp32; n < 2 or a non-positive determinant: s = 1, o = mean(w - c)
+    (0 if empty).  Returns (scale, offset) fp32 [rows, cols/group_size]."""
+    w = np.asarray(w, np.float32)
+    rows, cols = w.shape
+    G = int(group_size)
+    ng = cols // G
+    c = np.asarray(codebook, np.float32)[np.asarray(indices).astype(np.int64)].astype(np.float64)
+    x = w.astype(np.float64)
+    keep = np.ones(rows * cols, bool)
+    if exclude_positions is not None and len(exclude_positions):
+        keep[np.asarray(exclude_positions, np.int64)] = False
+    keep = keep.reshape(rows, cols)
+    # excluded elements add nothing (where, not a multiply: w may hold inf/NaN there)
+    z = lambda a: np.where(keep, a, 0.0)
+    terms = [z(c), z(x), z(c * c), z(c * x), keep.astype(np.float64)]
+    pad = (-G) % 64
+    sums = []
+    for t in terms:
+        t = t.reshape(rows, ng, G)
+        if pad:
+            t = np.concatenate([t, np.zeros((rows, ng, pad))], axis=2)
+        t = t.reshape(rows, ng, -1, 64)
+        acc = np.zeros((rows, ng, 64))
+        for j in range(t.shape[2]):
+            acc = acc + t[:, :, j, :]
+        while acc.shape[-1] > 1:
+            h = acc.shape[-1] // 2
+            acc = acc[..., :h] + acc[..., h:]
+        sums.append(acc[..., 0])
+    sc, sw, scc, scw, n = sums
+    det = n * scc - sc * sc
+    ok = (n >= 2) & (det > 0)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        s_fit = (n * scw - sc * sw) / det
+        s = np.where(ok, s_fit, 1.0)
+        o = np.where(n > 0, (sw - s * sc) / np.where(n > 0, n, 1.0), 0.0)
+    return s.astype(np.float32), o.astype(np.float32)

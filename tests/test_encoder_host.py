@@ -126,3 +126,105 @@ def test_write_tensor_cpu_matches_reference_pipeline(tmp_path):
         np.testing.assert_array_equal(z["positions"], pos_o)
         np.testing.assert_array_equal(z["values"], val_o.astype(np.float16))
     assert stats["num_outliers"] == 20 and stats["cosine_with_sidecar"] >= stats["cosine_no_sidecar"]
+
+
+def _lstsq_fit(c, w):
+    A = np.stack([c.astype(np.float64), np.ones(c.size)], axis=1)
+    (s, o), *_ = np.linalg.lstsq(A, w.astype(np.float64), rcond=None)
+    return s, o
+
+
+def test_affine_fit_exact_recovery():
+    # w = 1.25 * c + 0.5 with c on a 2^-8 grid: every fp64 sum is exact, so
+    # the closed form returns the generating pair exactly
+    rs = np.random.RandomState(20)
+    cb = (np.arange(256, dtype=np.float32) - 128) / 256
+    idx = rs.randint(0, 256, (4, 256)).astype(np.uint8)
+    w = (1.25 * cb[idx] + 0.5).astype(np.float32)
+    s, o = oracle.affine_fit_np(w, idx, cb, 128)
+    assert np.all(s == 1.25) and np.all(o == 0.5)
+
+
+@pytest.mark.parametrize("G", [32, 64, 128, 256])
+def test_affine_fit_matches_lstsq(G):
+    rs = np.random.RandomState(21)
+    cb = np.sort(rs.randn(256).astype(np.float32) * 0.02)
+    idx = rs.randint(0, 256, (6, 512)).astype(np.uint8)
+    w = (cb[idx] * rs.uniform(0.9, 1.1) + rs.randn(6, 512).astype(np.float32) * 0.003).astype(np.float32)
+    s, o = oracle.affine_fit_np(w, idx, cb, G)
+    for r in range(6):
+        for g in range(512 // G):
+            sl = slice(g * G, (g + 1) * G)
+            s_ref, o_ref = _lstsq_fit(cb[idx[r, sl]], w[r, sl])
+            assert abs(s[r, g] - s_ref) <= 2e-6 * abs(s_ref)
+            assert abs(o[r, g] - o_ref) <= 1e-6 * abs(o_ref) + 1e-9
+    # least squares: no worse than the identity affine or a perturbed one
+    sse = lambda s_, o_: float(((np.repeat(s_, G, 1) * cb[idx] + np.repeat(o_, G, 1) - w) ** 2).sum())
+    assert sse(s, o) <= sse(np.ones_like(s), np.zeros_like(o))
+    assert sse(s, o) <= sse(s * 1.001, o) and sse(s, o) <= sse(s, o + 1e-5)
+
+
+def test_affine_fit_exclusions_and_degenerate_groups():
+    rs = np.random.RandomState(22)
+    cb = np.sort(rs.randn(256).astype(np.float32) * 0.02)
+    idx = rs.randint(0, 256, (3, 256)).astype(np.uint8)
+    w = (cb[idx] * 1.02 + 0.001).astype(np.float32) + rs.randn(3, 256).astype(np.float32) * 1e-3
+    ex = np.array([0, 5, 300, 511, 700], np.int64)
+    w_bad = w.copy().ravel()
+    w_bad[ex] = [np.nan, np.inf, 1e30, -1e30, np.nan]
+    s, o = oracle.affine_fit_np(w_bad.reshape(3, 256), idx, cb, 128, ex)
+    keep = np.ones(w.size, bool)
+    keep[ex] = False
+    for r in range(3):
+        for g in range(2):
+            sel = np.zeros(w.size, bool)
+            sel[r * 256 + g * 128: r * 256 + (g + 1) * 128] = True
+            sel &= keep
+            s_ref, o_ref = _lstsq_fit(cb[idx.ravel()[sel]], w.ravel()[sel])
+            assert abs(s[r, g] - s_ref) <= 2e-6 * abs(s_ref)
+    # one index everywhere: zero determinant -> s = 1, o = mean(w - c)
+    idx1 = np.full((1, 128), 7, np.uint8)
+    w1 = rs.randn(1, 128).astype(np.float32)
+    s1, o1 = oracle.affine_fit_np(w1, idx1, cb, 128)
+    assert s1[0, 0] == 1.0
+    assert abs(o1[0, 0] - np.mean(w1.astype(np.float64) - cb[7])) <= 1e-7
+    # a group with one kept element -> s = 1, o = w - c; all excluded -> (1, 0)
+    s2, o2 = oracle.affine_fit_np(w1, idx1 * 0 + 3, cb, 64, np.arange(1, 64))
+    assert s2[0, 0] == 1.0 and o2[0, 0] == np.float32(np.float64(w1[0, 0]) - np.float64(cb[3]))
+    s3, o3 = oracle.affine_fit_np(w1, idx1, cb, 64, np.arange(64, 128))
+    assert s3[0, 1] == 1.0 and o3[0, 1] == 0.0
+
+
+def test_module_affine_fit_matches_oracle():
+    rs = np.random.RandomState(23)
+    cb = np.sort(rs.randn(256).astype(np.float32) * 0.02)
+    for G, shape in [(128, (5, 384)), (32, (3, 96)), (256, (2, 512))]:
+        idx = rs.randint(0, 256, shape).astype(np.uint8)
+        w = (cb[idx] * 0.97 + rs.randn(*shape).astype(np.float32) * 0.002).astype(np.float32)
+        ex = np.unique(rs.randint(0, w.size, 9)).astype(np.int64)
+        s, o = hxq_encoder.fit_group_affine(w, idx, cb, G, ex)
+        s_o, o_o = oracle.affine_fit_np(w, idx, cb, G, ex)
+        np.testing.assert_array_equal(s, s_o)
+        np.testing.assert_array_equal(o, o_o)
+
+
+def test_write_tensor_with_affine(tmp_path):
+    from helix_substrate.hxq_reader_v3 import CDNAv3Reader
+
+    rs = np.random.RandomState(24)
+    t = (rs.randn(64, 256) * 0.02 * rs.uniform(0.5, 2.0, (64, 1))).astype(np.float32)
+    w = CDNAv3Writer(tmp_path)
+    st_plain = w.write_tensor(t, "a.weight", max_corrections=16)
+    st_aff = w.write_tensor(t, "b.weight", max_corrections=16, group_size=128)
+    cb_o, idx_o, pos_o, val_o = oracle.write_tensor_np(t, max_corrections=16)
+    s_o, o_o = oracle.affine_fit_np(t, idx_o, cb_o, 128, pos_o)
+    d = tmp_path / "b_weight.cdnav3"
+    np.testing.assert_array_equal(np.load(d / "group_scale.npy"), s_o)
+    np.testing.assert_array_equal(np.load(d / "group_offset.npy"), o_o)
+    r = CDNAv3Reader(d)
+    assert r.meta["group_size"] == 128
+    W = r.reconstruct()
+    np.testing.assert_array_equal(
+        W, oracle.reconstruct(idx_o, cb_o, s_o, o_o, 128, pos_o, val_o.astype(np.float16).astype(np.float32)))
+    # the fit can only lower the squared error of the codebook reconstruction
+    assert st_aff["cosine_no_sidecar"] >= st_plain["cosine_no_sidecar"]

@@ -160,3 +160,37 @@ def test_large_sample_codebook(dev):
     cb = hxq_encoder.build_kmeans_codebook(torch.from_numpy(flat).to(dev), 256)
     cb_o, _, _ = oracle.kmeans_np(oracle.kmeans_sample_np(flat), 256)
     np.testing.assert_array_equal(cb.cpu().numpy(), cb_o)
+
+
+@pytest.mark.parametrize("rows,cols,G,n_ex,poison", [(2048, 2048, 128, 4194, False),
+                                                      (512, 1024, 64, 0, False),
+                                                      (256, 96, 32, 50, False),
+                                                      (128, 512, 256, 300, True)])
+def test_affine_fit_matches_oracle(dev, rows, cols, G, n_ex, poison):
+    rs = np.random.RandomState(17)
+    cb = np.sort(_weights(rs, 256))
+    idx = rs.randint(0, 256, (rows, cols)).astype(np.uint8)
+    w = (cb[idx] * rs.uniform(0.9, 1.1, (rows, 1)) + _weights(rs, rows * cols, 0.003)
+         .reshape(rows, cols)).astype(np.float32)
+    ex = np.sort(rs.choice(rows * cols, n_ex, replace=False)).astype(np.int64) if n_ex else None
+    if poison:
+        w.ravel()[ex[::2]] = np.nan
+        w.ravel()[ex[1::2]] = np.inf
+    print(f"affine_fit rows={rows} cols={cols} G={G} n_ex={n_ex}", flush=True)
+    s, o = _hxq.affine_fit(torch.from_numpy(w).to(dev), torch.from_numpy(idx).to(dev),
+                           torch.from_numpy(cb).to(dev), G,
+                           None if ex is None else torch.from_numpy(ex).to(dev))
+    s_o, o_o = oracle.affine_fit_np(w, idx, cb, G, ex)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_o)
+    np.testing.assert_array_equal(o.cpu().numpy(), o_o)
+
+
+def test_write_tensor_affine_gpu_matches_cpu(dev, tmp_path):
+    rs = np.random.RandomState(18)
+    t = (_weights(rs, 512 * 1024).reshape(512, 1024) * rs.uniform(0.5, 2, (512, 1))).astype(np.float32)
+    print("write_tensor affine", flush=True)
+    CDNAv3Writer(tmp_path / "gpu").write_tensor(torch.from_numpy(t).to(dev), "m.weight", group_size=128)
+    CDNAv3Writer(tmp_path / "cpu").write_tensor(t, "m.weight", group_size=128)
+    for f in ("codebook.npy", "indices.bin", "group_scale.npy", "group_offset.npy"):
+        assert (tmp_path / "gpu" / "m_weight.cdnav3" / f).read_bytes() == \
+            (tmp_path / "cpu" / "m_weight.cdnav3" / f).read_bytes(), f
