@@ -161,3 +161,49 @@ class CDNAv3Writer:
                  "n_clusters": int(len(cb_np)), "codec_decision": storage_mode}
         (out / "stats.json").write_text(json.dumps(stats, indent=2))
         return stats
+
+
+def compress_model(model, out_dir, device=None, group_size=None, n_clusters: int = 256,
+                   percentile: float = 99.9, max_corrections: int = 512,
+                   skip_modules=("embed_tokens", "lm_head")) -> dict:
+    """Encode every nn.Linear weight of `model` into ``{name}.cdnav3`` under
+    out_dir (on `device` when given: the GPU encoder) and every other tensor
+    (norms, embeddings, biases) as an exact fp16 ``.npy``; writes
+    manifest.json.  Modules whose name contains an entry of `skip_modules`
+    stay exact (config 1 keeps the embedding / LM head uncompressed).
+    Returns the manifest."""
+    import torch
+    import torch.nn as nn
+
+    w = CDNAv3Writer(out_dir)
+    linear_weights = {f"{n}.weight" for n, m in model.named_modules()
+                      if isinstance(m, nn.Linear) and not any(s in n for s in skip_modules)}
+    entries, orig, comp = [], 0, 0
+    seen = set()
+    for name, t in model.state_dict().items():
+        if t.data_ptr() in seen and t.numel():
+            continue  # tied copy
+        seen.add(t.data_ptr())
+        if name in linear_weights and t.dim() == 2:
+            src = t.detach().float()
+            src = src.to(device) if device is not None else src.cpu().numpy()
+            st = w.write_tensor(src, name, n_clusters=n_clusters, percentile=percentile,
+                                max_corrections=max_corrections, group_size=group_size,
+                                tensor_class="linear")
+            d = w.base_dir / f"{_safe_name(name)}.cdnav3"
+            st["compressed_bytes"] = sum(f.stat().st_size for f in d.iterdir()
+                                         if f.name not in ("meta.json", "stats.json"))
+        elif torch.is_floating_point(t):
+            st = w.write_exact(t, name)
+        else:
+            continue
+        orig += st["original_bytes"]
+        comp += st["compressed_bytes"]
+        entries.append(st)
+    manifest = {"format_version": "cdna_v3", "n_tensors": len(entries),
+                "n_compressed": sum(1 for e in entries if e.get("storage_mode") != "exact"),
+                "original_bytes": orig, "compressed_bytes": comp,
+                "compression_ratio": round(orig / max(comp, 1), 3), "n_svd_routed": 0,
+                "group_size": group_size, "tensors": entries}
+    (w.base_dir / "manifest.json").write_text(json.dumps(manifest, indent=2))
+    return manifest
