@@ -41,6 +41,7 @@ void clear_error();
 int device_cu_count();
 
 constexpr int kWave = 64;
+constexpr int kPairCodes = 4096;  // largest pair (2-D) codebook
 
 // ---------------------------------------------------------------------------
 // Numeric conversions (device)

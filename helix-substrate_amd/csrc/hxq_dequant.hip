@@ -64,9 +64,114 @@ __global__ __launch_bounds__(256) void dequant_sidecar_kernel(
         w[r * K + col[j]] = val[j];
 }
 
+// Reconstruction for the packed / pair formats: one thread per 16 weights.
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_fmt_kernel(
+    const uint8_t *__restrict__ idx, const float *__restrict__ cb, int32_t n_codes,
+    const float *__restrict__ gs, const float *__restrict__ go, int32_t group, int64_t K,
+    int64_t row_begin, int64_t n_vec16, float *__restrict__ w) {
+    constexpr bool PAIR = FMT != HXQ_FMT_AF6;
+    constexpr int QB = FMT == HXQ_FMT_VQ2_U16 ? 16 : 12;
+    __shared__ float2 tbl[PAIR ? kPairCodes : 1];
+    if constexpr (PAIR) {
+        for (int j = threadIdx.x; j < kPairCodes; j += blockDim.x)
+            tbl[j] = j < n_codes ? make_float2(cb[2 * j], cb[2 * j + 1]) : make_float2(0.f, 0.f);
+        __syncthreads();
+    }
+    const int64_t vec_per_row = K / 16;
+    const int64_t row_bytes = vec_per_row * QB;
+    for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < n_vec16;
+         v += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = v / vec_per_row;
+        const int64_t c16 = v - r * vec_per_row;
+        const int64_t row = row_begin + r;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(idx + row * row_bytes + c16 * QB);
+        const uint32_t q[4] = {src[0], src[1], src[2], QB == 16 ? src[3] : 0u};
+        auto field = [&](int bit, int width) -> uint32_t {
+            const int d = bit >> 5, sh = bit & 31;
+            const uint32_t x = sh + width <= 32 ? q[d] >> sh : __builtin_amdgcn_alignbit(q[d + 1], q[d], sh);
+            return x & ((1u << width) - 1u);
+        };
+        float out[16];
+        if constexpr (FMT == HXQ_FMT_AF6) {
+            const int64_t g = row * (K / group) + c16 * 16 / group;
+            const float s = gs[g], o = go[g];
+#pragma unroll
+            for (int f = 0; f < 16; ++f) out[f] = affine_exact(static_cast<float>(field(6 * f, 6)), s, o);
+        } else {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const uint32_t id = FMT == HXQ_FMT_VQ2_U16 ? (q[p >> 1] >> (16 * (p & 1))) & (kPairCodes - 1u)
+                                                           : field(12 * p, 12);
+                const float2 c = tbl[id];
+                out[2 * p] = c.x;
+                out[2 * p + 1] = c.y;
+            }
+        }
+        float4 *dst = reinterpret_cast<float4 *>(w + r * K + c16 * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dst[j] = make_float4(out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]);
+    }
+}
+
 }  // namespace hxq
 
 using namespace hxq;
+
+extern "C" int hxq_dequant_fmt(int32_t format, const uint8_t *indices, const float *codebook,
+                               int32_t n_codes, const float *group_scale,
+                               const float *group_offset, int32_t group_size,
+                               const int32_t *sc_row_ptr, const int32_t *sc_col,
+                               const float *sc_val, int64_t out_features, int64_t in_features,
+                               int64_t row_begin, int64_t row_end, float *w_out,
+                               hipStream_t stream) {
+    clear_error();
+    if (format == HXQ_FMT_SCALAR)
+        return hxq_dequant_f32(indices, codebook, group_scale, group_offset, group_size,
+                               sc_row_ptr, sc_col, sc_val, out_features, in_features, row_begin,
+                               row_end, w_out, stream);
+    HXQ_REQUIRE(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12 || format == HXQ_FMT_AF6,
+                "unknown index format");
+    HXQ_REQUIRE(indices && w_out, "indices and w_out are required");
+    HXQ_REQUIRE((reinterpret_cast<uintptr_t>(indices) & 3u) == 0, "indices must be 4-byte aligned");
+    HXQ_REQUIRE((reinterpret_cast<uintptr_t>(w_out) & 15u) == 0, "w_out must be 16-byte aligned");
+    HXQ_REQUIRE(out_features > 0 && in_features > 0 && in_features % 16 == 0,
+                "in_features must be a positive multiple of 16");
+    HXQ_REQUIRE(0 <= row_begin && row_begin <= row_end && row_end <= out_features,
+                "row range out of bounds");
+    if (format == HXQ_FMT_AF6)
+        HXQ_REQUIRE(group_scale && group_offset && group_size > 0 && group_size % 16 == 0 &&
+                        in_features % group_size == 0,
+                    "6-bit levels need the group affine (group_size a multiple of 16)");
+    else
+        HXQ_REQUIRE(codebook && n_codes >= 1 && n_codes <= kPairCodes,
+                    "pair codebooks need 1..4096 entries");
+    HXQ_REQUIRE(!sc_row_ptr || (sc_col && sc_val), "sidecar CSR needs row_ptr, col and val");
+    const int64_t rows = row_end - row_begin;
+    if (rows == 0) return HXQ_OK;
+    const int64_t n_vec16 = rows * (in_features / 16);
+    const int grid = static_cast<int>(
+        std::min<int64_t>((n_vec16 + 255) / 256, (int64_t)device_cu_count() * 16));
+#define HXQ_DQ(F)                                                                                \
+    hipLaunchKernelGGL(dequant_fmt_kernel<F>, dim3(grid), dim3(256), 0, stream, indices, codebook, \
+                       n_codes, group_scale, group_offset, group_size, in_features, row_begin,   \
+                       n_vec16, w_out)
+    switch (format) {
+        case HXQ_FMT_VQ2_U16: HXQ_DQ(HXQ_FMT_VQ2_U16); break;
+        case HXQ_FMT_VQ2_P12: HXQ_DQ(HXQ_FMT_VQ2_P12); break;
+        default: HXQ_DQ(HXQ_FMT_AF6); break;
+    }
+#undef HXQ_DQ
+    HXQ_LAUNCH_CHECK();
+    if (sc_row_ptr) {
+        hipLaunchKernelGGL(dequant_sidecar_kernel, dim3(static_cast<int>((rows + 255) / 256)),
+                           dim3(256), 0, stream, sc_row_ptr, sc_col, sc_val, in_features,
+                           row_begin, rows, w_out);
+        HXQ_LAUNCH_CHECK();
+    }
+    return HXQ_OK;
+}
 
 extern "C" int hxq_dequant_f32(const uint8_t *indices, const float *codebook,
                                const float *group_scale, const float *group_offset,

@@ -46,6 +46,7 @@ struct GemvMat {
     const float *bias;
     void *y;
     int64_t out;
+    int64_t ncodes;  // codebook entries (formats with a pair codebook)
 };
 
 struct GemvMats {
@@ -78,6 +79,7 @@ struct GemvHeader {
     int32_t n_mats;
     int32_t red_rows;  // LDS reduction slots per block (rows)
     int32_t xlds;      // 1: activations staged in LDS for the sidecar gather
+    int32_t fmt;       // HXQ_FMT_*
     int32_t bb[HXQ_MAX_MULTI];  // bb[m]: first block after matrix m (cumulative)
 };
 
@@ -125,6 +127,30 @@ __device__ __forceinline__ void store_y(void *y, int64_t i, int dt, float v) {
 }
 
 // One pipeline stage: the index words and affine factors of one row x CPS chunks.
+// Index formats (HXQ_FMT_*): bytes of index data per 16 weights, and LDS
+// table floats per block.
+__host__ __device__ constexpr int fmt_bytes16(int f) {
+    return (f == HXQ_FMT_VQ2_P12 || f == HXQ_FMT_AF6) ? 12 : 16;
+}
+__host__ __device__ constexpr int fmt_table_floats(int f, int nrep) {
+    return f == HXQ_FMT_SCALAR ? 256 * nrep : f == HXQ_FMT_AF6 ? 0 : 2 * kPairCodes;
+}
+
+// Bits [bit, bit + width) of the little-endian 96/128-bit stream q (bit and
+// width are constants after unrolling, so this folds to a shift/mask or one
+// v_alignbit_b32).
+__device__ __forceinline__ uint32_t bitfield(const u32x4 &q, int bit, int width) {
+    const int d = bit >> 5, sh = bit & 31;
+    const uint32_t v = sh + width <= 32 ? q[d] >> sh : __builtin_amdgcn_alignbit(q[d + 1], q[d], sh);
+    return v & ((1u << width) - 1u);
+}
+
+__device__ __forceinline__ u32x4 buf_load12(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+    return u32x4{v[0], v[1], v[2], 0u};
+}
+
 template <int CPS>
 struct GemvItem {
     u32x4 q[CPS];
@@ -152,7 +178,7 @@ constexpr int kEntCap = 512;  // sidecar entries per block staged in LDS
 // Barriers order LDS only (lds_barrier), so prefetched loads stay in flight.
 // Occupancy target: 4 waves per SIMD (two 8-wave blocks per CU, <= 128 VGPRs);
 // the long-row variant (4 chunks per slice) accepts 2.
-template <int NREP, int NX, int CPS, int WAVES, bool AFFINE, int RB, int XT, int XM>
+template <int NREP, int NX, int CPS, int WAVES, bool AFFINE, int RB, int XT, int XM, int FMT>
 __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const void *__restrict__ x, int32_t K, int32_t group, int32_t S, int32_t nchunks,
     int32_t flags, int32_t red_rows, int32_t bb1, int32_t bb2, int32_t bb3, int32_t bb4,
@@ -160,8 +186,14 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     constexpr bool XF32 = XT == HXQ_F32;
     static_assert(XM == 0 || (XF32 && NX == 1), "fused prologues take one fp32 row");
     constexpr int NT = WAVES * kWave;
-    constexpr int TPW = 256 * NREP / (4 * NT);  // table float4 writes per thread
-    static_assert(TPW >= 1 && (256 * NREP) % (4 * NT) == 0, "table/thread-count mismatch");
+    constexpr int TBLF = fmt_table_floats(FMT, NREP);
+    constexpr int TPW = TBLF / (4 * NT);  // table float4 writes per thread
+    static_assert(FMT == HXQ_FMT_AF6 || (TPW >= 1 && TBLF % (4 * NT) == 0),
+                  "table/thread-count mismatch");
+    static_assert(XM == 0 || FMT == HXQ_FMT_SCALAR, "fused prologues take scalar codebooks");
+    static_assert((FMT == HXQ_FMT_AF6) == AFFINE || FMT == HXQ_FMT_SCALAR,
+                  "6-bit levels carry the affine; pair codebooks have none");
+    constexpr int QB = fmt_bytes16(FMT);  // index bytes per 16 weights
     constexpr uint32_t kOob = 0x80000000u;      // buffer offset past any range: reads 0
     const int y_dtype = flags & 0xf;
     const bool xlds = (flags >> 4) & 1;
@@ -175,8 +207,8 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const GemvMat &M = mats.m[mi];
 
     extern __shared__ float smem[];
-    float *tbl = smem;                                      // [256 * NREP]
-    float *xl = tbl + 256 * NREP;                           // [NX * K] when xlds
+    float *tbl = smem;                                      // [TBLF]
+    float *xl = tbl + TBLF;                                 // [NX * K] when xlds
     float *red = xl + (xlds ? NX * K : 0);                  // [red_rows * NX * S]
     float *ent = red + red_rows * NX * S;                   // [kEntCap * NX]
     float *sumsq = ent + kEntCap * NX;                      // [S] (XM == 1)
@@ -236,14 +268,20 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
                 if constexpr (XM == 1) wraw[ci][v] = buf_load16(wr, koff[ci] * 4 + 16u * v);
             }
     }
-    float cbv[TPW];
-    {
+    float cbv[FMT == HXQ_FMT_SCALAR ? TPW : 1];
+    u32x4 cbq[(FMT == HXQ_FMT_VQ2_U16 || FMT == HXQ_FMT_VQ2_P12) ? TPW : 1];
+    if constexpr (FMT == HXQ_FMT_SCALAR) {
         const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, 256 * 4);
 #pragma unroll
         for (int k = 0; k < TPW; ++k) {
             const uint32_t e = 4u * (threadIdx.x + k * NT);  // first replica slot
             cbv[k] = buf_loadf(cr, (e / NREP) * 4u);
         }
+    } else if constexpr (FMT != HXQ_FMT_AF6) {
+        // pair codebook [ncodes, 2] fp32 as is; entries past ncodes read 0
+        const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, M.ncodes * 8);
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) cbq[k] = buf_load16(cr, 16u * (threadIdx.x + k * NT));
     }
     const __amdgpu_buffer_rsrc_t rp_r = make_rsrc(M.rp, has_sc ? (out + 1) * 4 : 0);
     // final-pass outputs: thread t handles (row lo + t / NX, activation t % NX)
@@ -253,7 +291,8 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const int32_t blk_j0 = buf_loadi(rp_r, static_cast<uint32_t>(lo * 4));
     const int32_t blk_j1 = buf_loadi(rp_r, static_cast<uint32_t>((lo + n_rows) * 4));
 
-    const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(M.idx, out * K);
+    const uint32_t row_bytes = static_cast<uint32_t>(K) / 16u * QB;
+    const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(M.idx, out * row_bytes);
     const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(M.gs, AFFINE ? out * ngroups * 4 : 0);
     const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(M.go, AFFINE ? out * ngroups * 4 : 0);
     auto load_item = [&](int64_t i, GemvItem<CPS> &it) {
@@ -261,7 +300,9 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
         const uint32_t row = static_cast<uint32_t>(lo + rg + i * RG);
 #pragma unroll
         for (int ci = 0; ci < CPS; ++ci) {
-            it.q[ci] = buf_load16(q_rsrc, mine ? row * static_cast<uint32_t>(K) + koff[ci] : kOob);
+            const uint32_t qo = mine ? row * row_bytes + koff[ci] / 16u * QB : kOob;
+            if constexpr (QB == 16) it.q[ci] = buf_load16(q_rsrc, qo);
+            else it.q[ci] = buf_load12(q_rsrc, qo);
             if constexpr (AFFINE) {
                 const uint32_t g4 =
                     (row * static_cast<uint32_t>(ngroups) + koff[ci] / static_cast<uint32_t>(group)) * 4u;
@@ -279,10 +320,16 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     __builtin_amdgcn_sched_barrier(0);  // all prologue loads are issued before any wait
 
     // ---- table (+ activations to registers / LDS)
+    if constexpr (FMT == HXQ_FMT_SCALAR) {
 #pragma unroll
-    for (int k = 0; k < TPW; ++k) {
-        const int e = 4 * (threadIdx.x + k * NT);
-        *reinterpret_cast<float4 *>(tbl + e) = make_float4(cbv[k], cbv[k], cbv[k], cbv[k]);
+        for (int k = 0; k < TPW; ++k) {
+            const int e = 4 * (threadIdx.x + k * NT);
+            *reinterpret_cast<float4 *>(tbl + e) = make_float4(cbv[k], cbv[k], cbv[k], cbv[k]);
+        }
+    } else if constexpr (FMT != HXQ_FMT_AF6) {
+#pragma unroll
+        for (int k = 0; k < TPW; ++k)
+            *reinterpret_cast<u32x4 *>(tbl + 4 * (threadIdx.x + k * NT)) = cbq[k];
     }
     float xv[CPS][NX][16];
     float xs[CPS][NX];
@@ -408,19 +455,44 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             float part[NX];
 #pragma unroll
             for (int n = 0; n < NX; ++n) part[n] = 0.f;
+            if constexpr (FMT == HXQ_FMT_SCALAR) {
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t w = itm.q[ci][d];
-                const float c0 = tbl_lookup<NREP, 0>(tbl, lane_off, w);
-                const float c1 = tbl_lookup<NREP, 1>(tbl, lane_off, w);
-                const float c2 = tbl_lookup<NREP, 2>(tbl, lane_off, w);
-                const float c3 = tbl_lookup<NREP, 3>(tbl, lane_off, w);
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t w = itm.q[ci][d];
+                    const float c0 = tbl_lookup<NREP, 0>(tbl, lane_off, w);
+                    const float c1 = tbl_lookup<NREP, 1>(tbl, lane_off, w);
+                    const float c2 = tbl_lookup<NREP, 2>(tbl, lane_off, w);
+                    const float c3 = tbl_lookup<NREP, 3>(tbl, lane_off, w);
 #pragma unroll
-                for (int n = 0; n < NX; ++n) {
-                    part[n] = fmaf(xv[ci][n][4 * d + 0], c0, part[n]);
-                    part[n] = fmaf(xv[ci][n][4 * d + 1], c1, part[n]);
-                    part[n] = fmaf(xv[ci][n][4 * d + 2], c2, part[n]);
-                    part[n] = fmaf(xv[ci][n][4 * d + 3], c3, part[n]);
+                    for (int n = 0; n < NX; ++n) {
+                        part[n] = fmaf(xv[ci][n][4 * d + 0], c0, part[n]);
+                        part[n] = fmaf(xv[ci][n][4 * d + 1], c1, part[n]);
+                        part[n] = fmaf(xv[ci][n][4 * d + 2], c2, part[n]);
+                        part[n] = fmaf(xv[ci][n][4 * d + 3], c3, part[n]);
+                    }
+                }
+            } else if constexpr (FMT == HXQ_FMT_AF6) {
+                // 16 six-bit levels, little-endian bit stream
+#pragma unroll
+                for (int f = 0; f < 16; ++f) {
+                    const float c = static_cast<float>(bitfield(itm.q[ci], 6 * f, 6));
+#pragma unroll
+                    for (int n = 0; n < NX; ++n) part[n] = fmaf(xv[ci][n][f], c, part[n]);
+                }
+            } else {
+                // 8 pair indices (uint16 in the low 12 bits, or packed 12-bit)
+                const float2 *tbl2 = reinterpret_cast<const float2 *>(tbl);
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    const uint32_t id = FMT == HXQ_FMT_VQ2_U16
+                                            ? (itm.q[ci][p >> 1] >> (16 * (p & 1))) & (kPairCodes - 1u)
+                                            : bitfield(itm.q[ci], 12 * p, 12);
+                    const float2 c = tbl2[id];
+#pragma unroll
+                    for (int n = 0; n < NX; ++n) {
+                        part[n] = fmaf(xv[ci][n][2 * p], c.x, part[n]);
+                        part[n] = fmaf(xv[ci][n][2 * p + 1], c.y, part[n]);
+                    }
                 }
             }
 #pragma unroll
@@ -571,11 +643,11 @@ static int plan_gemv(GemvHeader &h, const GemvMats &mats, int n_x, GemvPlan &pl)
 }
 
 static size_t gemv_lds_bytes(int nrep, int nx, const GemvHeader &h) {
-    return (256 * (size_t)nrep + (h.xlds ? (size_t)nx * h.K : 0) +
+    return ((size_t)fmt_table_floats(h.fmt, nrep) + (h.xlds ? (size_t)nx * h.K : 0) +
             (size_t)h.red_rows * nx * h.S + (size_t)kEntCap * nx + 64) * sizeof(float);
 }
 
-template <int NREP, int NX, int CPS, int RB, int XM = 0>
+template <int NREP, int NX, int CPS, int RB, int XM = 0, int FMT = HXQ_FMT_SCALAR>
 static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipStream_t stream,
                       const GemvPro &pro = GemvPro{}) {
     const size_t lds = gemv_lds_bytes(NREP, NX, h);
@@ -585,11 +657,18 @@ static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipSt
     const int32_t K = static_cast<int32_t>(h.K);
     // all matrices of one launch either carry the affine factors or none do
 #define HXQ_GEMV_LAUNCH(AFF, XT)                                                               \
-    hipLaunchKernelGGL((gemv_kernel<NREP, NX, CPS, kWaves, AFF, RB, XT, XM>), g, b, lds, stream, \
+    hipLaunchKernelGGL((gemv_kernel<NREP, NX, CPS, kWaves, AFF, RB, XT, XM, FMT>), g, b, lds, stream, \
                        h.x, K, h.group, h.S, h.nchunks, flags, h.red_rows, h.bb[0], h.bb[1],   \
                        h.bb[2], h.bb[3], h.bb[4], h.bb[5], h.bb[6], mats, pro)
     if constexpr (XM != 0) {
         if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32);
+    } else if constexpr (FMT != HXQ_FMT_SCALAR) {
+        constexpr bool A = FMT == HXQ_FMT_AF6;
+        switch (h.x_dtype) {
+            case HXQ_F32: HXQ_GEMV_LAUNCH(A, HXQ_F32); break;
+            case HXQ_BF16: HXQ_GEMV_LAUNCH(A, HXQ_BF16); break;
+            default: HXQ_GEMV_LAUNCH(A, HXQ_F16); break;
+        }
     } else {
         switch (h.x_dtype) {
             case HXQ_F32: if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32); break;
@@ -602,9 +681,10 @@ static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipSt
     return HXQ_OK;
 }
 
-template <int XM = 0>
+template <int XM = 0, int FMT = HXQ_FMT_SCALAR>
 static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t stream,
                     const GemvPro &pro = GemvPro{}) {
+    h.fmt = FMT;
     GemvPlan pl{};
     const int rc = plan_gemv(h, mats, n_x, pl);
     if (rc != HXQ_OK) return rc;
@@ -616,18 +696,18 @@ static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t st
     // rows per batch (two batches in flight): what fits 128 VGPRs
     if (n_x == 1) {
         switch (pl.CPS) {
-            case 1: return launch_one<kNrep, 1, 1, 4, XM>(h, mats, pl.grid, stream, pro);
-            case 2: return launch_one<kNrep, 1, 2, 2, XM>(h, mats, pl.grid, stream, pro);
-            default: return launch_one<kNrep, 1, 4, 1, XM>(h, mats, pl.grid, stream, pro);
+            case 1: return launch_one<kNrep, 1, 1, 4, XM, FMT>(h, mats, pl.grid, stream, pro);
+            case 2: return launch_one<kNrep, 1, 2, 2, XM, FMT>(h, mats, pl.grid, stream, pro);
+            default: return launch_one<kNrep, 1, 4, 1, XM, FMT>(h, mats, pl.grid, stream, pro);
         }
     }
     if constexpr (XM != 0) {
         return HXQ_ERR_INVALID_ARG;
     } else {
         switch (n_x) {
-            case 2: return launch_one<kNrep, 2, 1, 2>(h, mats, pl.grid, stream);
-            case 3: return launch_one<kNrep, 3, 1, 1>(h, mats, pl.grid, stream);
-            default: return launch_one<kNrep, 4, 1, 1>(h, mats, pl.grid, stream);
+            case 2: return launch_one<kNrep, 2, 1, 2, 0, FMT>(h, mats, pl.grid, stream);
+            case 3: return launch_one<kNrep, 3, 1, 1, 0, FMT>(h, mats, pl.grid, stream);
+            default: return launch_one<kNrep, 4, 1, 1, 0, FMT>(h, mats, pl.grid, stream);
         }
     }
 }
@@ -768,4 +848,60 @@ extern "C" int hxq_gemv_multi_silu(const float *gate, const float *up, const hxq
     HXQ_REQUIRE(up, "up is required");
     const GemvPro pro{up, nullptr, nullptr, 0.f, 0};
     return gemv_fused(2, gate, pro, mats, n_mats, group_size, y_dtype, in_features, stream);
+}
+
+extern "C" int hxq_gemv_fmt(const void *x, int32_t x_dtype, int32_t format, const uint8_t *indices,
+                            const float *codebook, int32_t n_codes, const float *group_scale,
+                            const float *group_offset, int32_t group_size,
+                            const int32_t *sc_row_ptr, const int32_t *sc_col,
+                            const float *sc_delta, const float *bias, void *y, int32_t y_dtype,
+                            int64_t n_rows, int64_t out_features, int64_t in_features,
+                            hipStream_t stream) {
+    clear_error();
+    if (format == HXQ_FMT_SCALAR)
+        return hxq_gemv(x, x_dtype, indices, codebook, group_scale, group_offset, group_size,
+                        sc_row_ptr, sc_col, sc_delta, bias, y, y_dtype, n_rows, out_features,
+                        in_features, stream);
+    HXQ_REQUIRE(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12 || format == HXQ_FMT_AF6,
+                "unknown index format");
+    HXQ_REQUIRE(n_rows >= 1 && n_rows <= 4, "n_rows must be in [1, 4]");
+    HXQ_REQUIRE(x && indices && y, "x, indices and y are required");
+    HXQ_REQUIRE(x_dtype >= HXQ_F32 && x_dtype <= HXQ_F16, "bad x_dtype");
+    HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
+    HXQ_REQUIRE(in_features > 0 && in_features % 16 == 0 && in_features <= INT32_MAX / 4,
+                "in_features must be a positive multiple of 16");
+    HXQ_REQUIRE(out_features > 0, "out_features must be positive");
+    HXQ_REQUIRE(aligned16(x), "x must be 16-byte aligned");
+    HXQ_REQUIRE(aligned16(indices) || fmt_bytes16(format) == 12, "indices must be 16-byte aligned");
+    HXQ_REQUIRE((reinterpret_cast<uintptr_t>(indices) & 3u) == 0, "indices must be 4-byte aligned");
+    HXQ_REQUIRE(out_features * (in_features / 16 * fmt_bytes16(format)) + kChunk <
+                    (int64_t{1} << 32), "index data must be smaller than 4 GiB");
+    HXQ_REQUIRE(!sc_row_ptr || (sc_col && sc_delta), "sidecar CSR needs row_ptr, col, delta");
+    if (format == HXQ_FMT_AF6) {
+        HXQ_REQUIRE(group_scale && group_offset, "6-bit levels need group_scale and group_offset");
+        HXQ_REQUIRE(group_size > 0 && group_size % 16 == 0 && in_features % group_size == 0,
+                    "group_size must be a positive multiple of 16 dividing in_features");
+    } else {
+        HXQ_REQUIRE(codebook && n_codes >= 1 && n_codes <= kPairCodes,
+                    "pair codebooks need 1..4096 entries");
+        HXQ_REQUIRE(!group_scale && !group_offset, "pair codebooks take no group affine");
+        HXQ_REQUIRE(aligned16(codebook), "codebook must be 16-byte aligned");
+    }
+    GemvHeader h{};
+    h.x = x;
+    h.K = in_features;
+    h.group = format == HXQ_FMT_AF6 ? group_size : 0;
+    h.n_mats = 1;
+    h.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
+    h.x_dtype = x_dtype;
+    h.y_dtype = y_dtype;
+    GemvMats mats{};
+    mats.m[0] = GemvMat{indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_delta,
+                        bias, y, out_features, n_codes};
+    const int nx = static_cast<int>(n_rows);
+    switch (format) {
+        case HXQ_FMT_VQ2_U16: return gemv_run<0, HXQ_FMT_VQ2_U16>(h, mats, nx, stream);
+        case HXQ_FMT_VQ2_P12: return gemv_run<0, HXQ_FMT_VQ2_P12>(h, mats, nx, stream);
+        default: return gemv_run<0, HXQ_FMT_AF6>(h, mats, nx, stream);
+    }
 }

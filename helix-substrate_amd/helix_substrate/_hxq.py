@@ -72,6 +72,8 @@ class HxqDecoder(ctypes.Structure):
 SIGNATURES = {
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
     "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_gemv_fmt": [P, I32, I32, P, P, I32, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_dequant_fmt": [I32, P, P, I32, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
     "hxq_gemv_multi": [P, I32, P, I32, I32, I32, I64, P],
     "hxq_gemv_multi_rmsnorm": [P, P, P, F32, P, P, I32, I32, I32, I64, P],
     "hxq_gemv_multi_silu": [P, P, P, I32, I32, I32, I64, P],
@@ -225,6 +227,48 @@ def gemv(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr
                         _ptr(sc_col), _ptr(sc_delta), _ptr(bias), _ptr(out),
                         dtype_code(out.dtype), n, out_f, in_f, _stream(x))
     _check("hxq_gemv", rc)
+    return out
+
+
+# index formats (include/hxq.h hxq_format)
+FMT_SCALAR, FMT_VQ2_U16, FMT_VQ2_P12, FMT_AF6 = 0, 1, 2, 3
+
+
+def gemv_fmt(x, fmt, indices, out_features, codebook=None, group_scale=None, group_offset=None,
+             group_size=0, sc_row_ptr=None, sc_col=None, sc_delta=None, bias=None,
+             out_dtype=torch.float32, out=None):
+    """y = x @ W^T (+bias) for any index format (FMT_*); x [n, K], 1 <= n <= 4.
+    `indices` holds the raw index bytes (uint16 pairs as int16, packed streams
+    as uint8)."""
+    n, in_f = x.shape
+    if out is None:
+        out = torch.empty(n, out_features, dtype=out_dtype, device=x.device)
+    _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_delta,
+                 bias, out)
+    n_codes = 0 if codebook is None else int(codebook.shape[0])
+    rc = lib().hxq_gemv_fmt(_ptr(x), dtype_code(x.dtype), int(fmt), _ptr(indices), _ptr(codebook),
+                            n_codes, _ptr(group_scale), _ptr(group_offset), int(group_size),
+                            _ptr(sc_row_ptr), _ptr(sc_col), _ptr(sc_delta), _ptr(bias), _ptr(out),
+                            dtype_code(out.dtype), n, int(out_features), in_f, _stream(x))
+    _check("hxq_gemv_fmt", rc)
+    return out
+
+
+def dequant_fmt(fmt, indices, out_features, in_features, codebook=None, group_scale=None,
+                group_offset=None, group_size=0, sc_row_ptr=None, sc_col=None, sc_val=None,
+                row_begin=0, row_end=None, out=None):
+    """Reconstruct rows [row_begin, row_end) of W in fp32 for any index format."""
+    row_end = out_features if row_end is None else row_end
+    if out is None:
+        out = torch.empty(row_end - row_begin, in_features, dtype=torch.float32,
+                          device=indices.device)
+    _need_device(indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val, out)
+    n_codes = 0 if codebook is None else int(codebook.shape[0])
+    rc = lib().hxq_dequant_fmt(int(fmt), _ptr(indices), _ptr(codebook), n_codes, _ptr(group_scale),
+                               _ptr(group_offset), int(group_size), _ptr(sc_row_ptr), _ptr(sc_col),
+                               _ptr(sc_val), int(out_features), int(in_features), int(row_begin),
+                               int(row_end), _ptr(out), _stream(indices))
+    _check("hxq_dequant_fmt", rc)
     return out
 
 

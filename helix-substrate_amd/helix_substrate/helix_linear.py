@@ -21,7 +21,13 @@ Differences, by design:
     the reconstruction is bit-exact; contractions add ``x[col]*delta`` with
     delta = value - W_affine[pos] (the reference's delta form,
     ``helix_linear.py:188-203``);
-  * scalar codebooks of at most 256 entries (uint8 indices) only.
+  * scalar codebooks of at most 256 entries (uint8 indices), or pair
+    codebooks (``vector_dim=2``, [k <= 4096, 2], reference
+    ``triton_vq2d_matmul.py``) with int16 indices [out, in/2] or the
+    reference's 12-bit packing (``index_packing="12bit"``, uint8 1-D,
+    ``index_packing.py``); the pair formats run the same GEMV kernel with a
+    pair-table decode, and above 4 rows dequantise row tiles with the HIP
+    kernel into a library GEMM (the reference's buffered mode).
 """
 from __future__ import annotations
 
@@ -39,6 +45,7 @@ from .hxq_format import build_sidecar_csr, check_kernel_shapes, compressed_bytes
 
 _CPU_TILE_ROWS = 256
 _GEMV_MAX_ROWS = 4
+_DEQUANT_TILE_ELEMS = 1 << 24  # fp32 elements per dequantised row tile (64 MiB)
 
 
 class HelixLinear(nn.Module):
@@ -63,14 +70,26 @@ class HelixLinear(nn.Module):
         super().__init__()
         self._init_attrs(in_features, out_features, tensor_name, compute_dtype, vector_dim,
                          group_size)
-        if vector_dim != 1:
-            raise NotImplementedError("vector_dim > 1 (2-D VQ) is not supported by the HIP path")
-        if codebook.numel() > 256:
-            raise NotImplementedError("codebooks above 256 entries (uint16 indices) are not supported")
-        if tuple(indices.shape) != (out_features, in_features):
-            raise ValueError(f"indices shape {tuple(indices.shape)} != ({out_features}, {in_features})")
+        if vector_dim not in (1, 2):
+            raise NotImplementedError("vector_dim must be 1 (scalar) or 2 (pair codebook)")
+        if vector_dim == 1:
+            if codebook.numel() > 256:
+                raise NotImplementedError("scalar codebooks above 256 entries are not supported")
+            if tuple(indices.shape) != (out_features, in_features):
+                raise ValueError(f"indices shape {tuple(indices.shape)} != ({out_features}, {in_features})")
+            indices = indices.to(torch.uint8)
+        else:
+            if codebook.dim() != 2 or codebook.shape[1] != 2 or codebook.shape[0] > 4096:
+                raise NotImplementedError("pair codebooks are [k <= 4096, 2]")
+            if group_scale is not None or group_offset is not None:
+                raise NotImplementedError("pair codebooks take no group affine")
+            if not (indices.dtype == torch.uint8 and indices.dim() == 1):  # not 12-bit packed
+                if tuple(indices.shape) != (out_features, in_features // 2):
+                    raise ValueError(f"indices shape {tuple(indices.shape)} != "
+                                     f"({out_features}, {in_features // 2})")
+                indices = indices.to(torch.int32).to(torch.int16)
         self.register_buffer("codebook", codebook.to(torch.float32).contiguous())
-        self.register_buffer("indices", indices.to(torch.uint8).contiguous())
+        self.register_buffer("indices", indices.contiguous())
         self.register_buffer("sidecar_positions",
                              None if sidecar_positions is None else sidecar_positions.to(torch.int64).contiguous())
         self.register_buffer("sidecar_values",
@@ -141,8 +160,13 @@ class HelixLinear(nn.Module):
             buf = getattr(self, name, None)
             if buf is not None and buf.numel() == 0:
                 self.register_buffer(name, None)
-        if self.codebook.dim() != 1:
-            raise NotImplementedError("only scalar (1-D) codebooks are supported")
+        # [k] = scalar, [k, d] = vector codebook (reference helix_linear.py:929-933)
+        self.vector_dim = int(self.codebook.shape[1]) if self.codebook.dim() == 2 else 1
+        if self.vector_dim != 1:
+            self._recompute_derived_pairs()
+            return
+        self._fmt = _hxq.FMT_SCALAR
+        self.index_packing = None
         if self.indices.dtype != torch.uint8:
             if self.codebook.numel() > 256:
                 raise NotImplementedError("uint16 indices are not supported")
@@ -189,6 +213,73 @@ class HelixLinear(nn.Module):
             self.register_buffer("codebook_f16", self.codebook.half().contiguous())
         else:
             self.register_buffer("codebook_f16", None)
+
+    def _recompute_derived_pairs(self) -> None:
+        """Derived state of a pair-codebook layer (vector_dim 2)."""
+        if self.vector_dim != 2 or self.codebook.shape[0] > 4096:
+            raise NotImplementedError("pair codebooks are [k <= 4096, 2]")
+        if self.group_scale is not None or self.group_offset is not None:
+            raise NotImplementedError("pair codebooks take no group affine")
+        if self.in_features % 16:
+            raise ValueError(f"in_features={self.in_features} must be a multiple of 16")
+        if self.codebook.dtype != torch.float32:
+            self.register_buffer("codebook", self.codebook.float().contiguous())
+        n_pairs = self.out_features * (self.in_features // 2)
+        # uint8 1-D indices with k > 256 are the 12-bit packing (reference helix_linear.py:936-942)
+        packed = self.indices.dtype == torch.uint8 and self.indices.dim() == 1
+        if packed:
+            if self.indices.numel() != n_pairs * 3 // 2:
+                raise ValueError(f"packed indices hold {self.indices.numel()} bytes, expected "
+                                 f"{n_pairs * 3 // 2}")
+        else:
+            if tuple(self.indices.shape) != (self.out_features, self.in_features // 2):
+                raise ValueError("pair indices must be [out_features, in_features // 2]")
+            if self.indices.dtype != torch.int16:
+                self.register_buffer("indices", self.indices.to(torch.int32).to(torch.int16).contiguous())
+        self.index_packing = "12bit" if packed else None
+        self._idx_rows, self._idx_cols = self.out_features, self.in_features // 2
+        self._fmt = _hxq.FMT_VQ2_P12 if packed else _hxq.FMT_VQ2_U16
+        if self.sidecar_positions is not None and self.sidecar_values is not None:
+            csr = build_sidecar_csr(self.sidecar_positions, self.sidecar_values, self.indices,
+                                    self.codebook, shape=(self.out_features, self.in_features),
+                                    recon_at=self._pair_recon_at)
+            for name, t in (("_sc_row_ptr", csr.row_ptr), ("_sc_col", csr.col), ("_sc_val", csr.val),
+                            ("_sc_delta", csr.delta), ("_sidecar_rows", csr.rows),
+                            ("_sidecar_cols", csr.cols), ("_sidecar_deltas", csr.delta),
+                            ("_sidecar_vq_vals", csr.vq)):
+                self.register_buffer(name, t)
+        else:
+            for name in ("_sc_row_ptr", "_sc_col", "_sc_val", "_sc_delta", "_sidecar_rows",
+                         "_sidecar_cols", "_sidecar_deltas", "_sidecar_vq_vals"):
+                self.register_buffer(name, None)
+        self._gemm_ok = False
+        self.register_buffer("_affine_t", None, persistent=False)
+        self.has_svd = self.svd_U is not None
+        self.rank = int(self.svd_U.shape[1]) if self.has_svd else 0
+        self.has_channel_scales = self.channel_scales is not None
+        self.register_buffer("codebook_f16", self.codebook.half().contiguous()
+                             if self.compute_dtype == torch.float16 else None)
+
+    def _pair_index_at(self, rows: torch.Tensor, pairs: torch.Tensor) -> torch.Tensor:
+        """Pair index at (row, pair column), from int16 or 12-bit packed storage."""
+        if self.index_packing != "12bit":
+            return self.indices[rows, pairs].long()
+        flat = rows * (self.in_features // 2) + pairs
+        b = torch.div(flat, 2, rounding_mode="floor") * 3
+        t = self.indices
+        b0, b1, b2 = t[b].long(), t[b + 1].long(), t[b + 2].long()
+        return torch.where(flat % 2 == 0, b0 | ((b1 & 15) << 8), (b1 >> 4) | (b2 << 4))
+
+    def _pair_recon_at(self, rows: torch.Tensor, cols: torch.Tensor) -> torch.Tensor:
+        idx = self._pair_index_at(rows, torch.div(cols, 2, rounding_mode="floor"))
+        return self.codebook[idx, cols % 2]
+
+    def _pair_rows(self, start_row: int, end_row: int) -> torch.Tensor:
+        if self.index_packing == "12bit":
+            from .index_packing import unpack_12bit_rows
+
+            return unpack_12bit_rows(self.indices, start_row, end_row, self.in_features // 2).long()
+        return self.indices[start_row:end_row].long()
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):
@@ -250,6 +341,8 @@ class HelixLinear(nn.Module):
         out = torch.empty(n, self.out_features, dtype=out_dtype, device=x2.device)
         if n == 0:
             pass
+        elif self.vector_dim != 1:
+            self._forward_hip_pairs(x2, rp, col, delta, out)
         elif n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv"
             _hxq.gemv(x2, self.indices, self.codebook, self.group_scale, self.group_offset,
@@ -270,6 +363,27 @@ class HelixLinear(nn.Module):
             xf = x2.float()
             out += ((xf @ self.svd_Vt.t()) * self.svd_s.unsqueeze(0)) @ self.svd_U.t()
         return out.reshape(*orig_shape[:-1], self.out_features)
+
+    def _forward_hip_pairs(self, x2, rp, col, delta, out) -> None:
+        n = x2.shape[0]
+        if n <= _GEMV_MAX_ROWS:
+            self._last_dispatch_path = "hip_gemv_fmt"
+            _hxq.gemv_fmt(x2, self._fmt, self.indices, self.out_features, codebook=self.codebook,
+                          sc_row_ptr=rp, sc_col=col, sc_delta=delta, bias=self.bias, out=out)
+            return
+        # many rows: HIP dequant of row tiles, then the library GEMM on them
+        self._last_dispatch_path = "hip_dequant_gemm"
+        step = max(1, _DEQUANT_TILE_ELEMS // self.in_features)
+        for r0 in range(0, self.out_features, step):
+            r1 = min(self.out_features, r0 + step)
+            w = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features, self.in_features,
+                                 codebook=self.codebook, sc_row_ptr=rp, sc_col=col,
+                                 sc_val=None if rp is None else self._sc_val, row_begin=r0,
+                                 row_end=r1)
+            y = x2 @ w.to(x2.dtype).t()
+            if self.bias is not None:
+                y = y + self.bias[r0:r1].to(y.dtype)
+            out[:, r0:r1] = y
 
     def _forward_naive(self, x: torch.Tensor) -> torch.Tensor:
         """CPU tensors: 256-row tiles, fp32 (reference helix_linear.py:783-822)."""
@@ -295,6 +409,21 @@ class HelixLinear(nn.Module):
         On the GPU this is the bit-exact HIP dequant kernel.
         """
         apply_sc = getattr(self, "_apply_sidecar_this_call", True)
+        if self.vector_dim != 1:
+            if self.indices.is_cuda:
+                tile = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features,
+                                        self.in_features, codebook=self.codebook,
+                                        sc_row_ptr=self._sc_row_ptr if apply_sc else None,
+                                        sc_col=self._sc_col if apply_sc else None,
+                                        sc_val=self._sc_val if apply_sc else None,
+                                        row_begin=start_row, row_end=end_row)
+            else:
+                tile = self.codebook[self._pair_rows(start_row, end_row)].reshape(
+                    end_row - start_row, self.in_features)
+                tile = self._replace_sidecar(tile, start_row, end_row, apply_sc)
+            if self.has_svd and not self._cell_skip_svd:
+                tile = tile + (self.svd_U[start_row:end_row] * self.svd_s.unsqueeze(0)) @ self.svd_Vt
+            return tile
         if self.indices.is_cuda:
             tile = _hxq.dequant_f32(self.indices, self.codebook, self.group_scale,
                                     self.group_offset, self.group_size,
@@ -308,17 +437,21 @@ class HelixLinear(nn.Module):
                 o = self.group_offset[start_row:end_row].repeat_interleave(self.group_size, dim=1)
                 tile = tile * s
                 tile = tile + o
-            if self._sc_row_ptr is not None and apply_sc:
-                lo = int(self._sc_row_ptr[start_row])
-                hi = int(self._sc_row_ptr[end_row])
-                if hi > lo:
-                    tile = tile.clone()
-                    # CSR keeps stored order within a row, so the last of a
-                    # repeated position wins, like numpy fancy assignment.
-                    tile[self._sidecar_rows[lo:hi] - start_row,
-                         self._sidecar_cols[lo:hi]] = self._sc_val[lo:hi]
+            tile = self._replace_sidecar(tile, start_row, end_row, apply_sc)
         if self.has_svd and not self._cell_skip_svd:
             tile = tile + (self.svd_U[start_row:end_row] * self.svd_s.unsqueeze(0)) @ self.svd_Vt
+        return tile
+
+    def _replace_sidecar(self, tile, start_row, end_row, apply_sc):
+        if self._sc_row_ptr is not None and apply_sc:
+            lo = int(self._sc_row_ptr[start_row])
+            hi = int(self._sc_row_ptr[end_row])
+            if hi > lo:
+                tile = tile.clone()
+                # CSR keeps stored order within a row, so the last of a
+                # repeated position wins, like numpy fancy assignment.
+                tile[self._sidecar_rows[lo:hi] - start_row,
+                     self._sidecar_cols[lo:hi]] = self._sc_val[lo:hi]
         return tile
 
     def decode_weight(self) -> torch.Tensor:
@@ -382,7 +515,7 @@ class HelixLinear(nn.Module):
 
     def memory_savings(self) -> dict:
         dense = self.out_features * self.in_features * 4
-        comp = self.codebook.numel() * 4 + self.indices.numel()
+        comp = self.codebook.numel() * 4 + self.indices.numel() * self.indices.element_size()
         for t in (self.sidecar_positions, self._sidecar_rows, self._sidecar_cols):
             comp += 0 if t is None else t.numel() * 8
         for t in (self.sidecar_values, self._sidecar_deltas, self.svd_U, self.svd_s, self.svd_Vt,
@@ -397,6 +530,9 @@ class HelixLinear(nn.Module):
     def kernel_bytes(self) -> int:
         """Bytes of compressed state one contraction streams (roofline accounting)."""
         nnz = 0 if self._sc_col is None else self._sc_col.numel()
+        if self.vector_dim != 1:
+            b = self.indices.numel() * self.indices.element_size() + self.codebook.numel() * 4
+            return b + ((self.out_features + 1) * 4 + nnz * 8 if nnz else 0)
         return compressed_bytes(self.out_features, self.in_features,
                                 self.group_size if self.group_scale is not None else None, nnz)
 
@@ -421,14 +557,24 @@ class HelixLinear(nn.Module):
                               group_size: int = 128) -> "HelixLinear":
         """Empty shell whose buffers a safetensors load fills; then call
         ``_recompute_derived()`` (reference helix_linear.py:1020-1119)."""
-        if vector_dim != 1 or n_clusters > 256 or index_packing is not None:
-            raise NotImplementedError("only scalar k<=256 uint8 HXQ tensors are supported")
+        if vector_dim not in (1, 2) or (vector_dim == 1 and n_clusters > 256):
+            raise NotImplementedError("scalar codebooks take k <= 256, vector codebooks d = 2")
         inst = cls.__new__(cls)
         nn.Module.__init__(inst)
         inst._init_attrs(in_features, out_features, tensor_name, compute_dtype, vector_dim,
                          group_size)
-        inst.register_buffer("codebook", torch.zeros(n_clusters, dtype=torch.float32))
-        inst.register_buffer("indices", torch.zeros(out_features, in_features, dtype=torch.uint8))
+        if vector_dim == 1:
+            inst.register_buffer("codebook", torch.zeros(n_clusters, dtype=torch.float32))
+            inst.register_buffer("indices", torch.zeros(out_features, in_features, dtype=torch.uint8))
+        else:
+            inst.register_buffer("codebook", torch.zeros(n_clusters, 2, dtype=torch.float32))
+            n_pairs = out_features * (in_features // 2)
+            if index_packing == "12bit" and n_clusters > 256:
+                inst.register_buffer("indices", torch.zeros(n_pairs * 3 // 2, dtype=torch.uint8))
+                inst.index_packing = "12bit"
+            else:
+                inst.register_buffer("indices", torch.zeros(out_features, in_features // 2,
+                                                            dtype=torch.int16))
         inst.register_buffer("sidecar_positions", torch.zeros(0, dtype=torch.int64))
         for name in ("sidecar_values", "svd_U", "svd_s", "svd_Vt", "bias", "channel_scales",
                      "group_scale", "group_offset"):
@@ -463,9 +609,12 @@ def load_helix_linear_from_cdnav3(tensor_dir, bias: Optional[torch.Tensor] = Non
     def t(a):
         return None if a is None else torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
 
+    idx = r._load_indices()
+    if idx.dtype == np.uint16:  # pair indices < 4096 (int16 in memory, as the reference)
+        idx = idx.astype(np.int16)
     return HelixLinear(
         in_features=cols, out_features=rows, codebook=t(r._load_codebook()),
-        indices=torch.from_numpy(r._load_indices().copy()), sidecar_positions=pos,
+        indices=torch.from_numpy(idx.copy()), sidecar_positions=pos,
         sidecar_values=val, svd_U=t(svd[0]), svd_s=t(svd[1]), svd_Vt=t(svd[2]), bias=bias,
         tensor_name=r.meta.get("tensor_name", ""), compute_dtype=compute_dtype,
         channel_scales=t(cs), vector_dim=r.vector_dim, group_scale=t(gs), group_offset=t(go),

@@ -51,7 +51,7 @@ def affine_values(indices: torch.Tensor, codebook: torch.Tensor,
 def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: torch.Tensor,
                       codebook: torch.Tensor, group_scale: Optional[torch.Tensor] = None,
                       group_offset: Optional[torch.Tensor] = None,
-                      group_size: int = 128) -> SidecarCSR:
+                      group_size: int = 128, shape=None, recon_at=None) -> SidecarCSR:
     """CSR over output rows from flat sidecar positions.
 
     Entries keep their stored order inside a row (stable sort), so a repeated
@@ -59,7 +59,7 @@ def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: to
     one wins) when the dequant kernel replays them in order.
     Raises ValueError on positions outside the matrix.
     """
-    out_f, in_f = indices.shape
+    out_f, in_f = indices.shape if shape is None else shape
     pos = positions.reshape(-1).to(torch.int64)
     val = values.reshape(-1).to(torch.float32)
     if pos.numel() != val.numel():
@@ -76,7 +76,9 @@ def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: to
     counts = torch.bincount(rows, minlength=out_f)
     row_ptr = torch.zeros(out_f + 1, dtype=torch.int64, device=pos.device)
     row_ptr[1:] = torch.cumsum(counts, 0)
-    vq = affine_values(indices, codebook, group_scale, group_offset, group_size, rows, cols)
+    # reconstruction at the positions (recon_at(rows, cols) for other index formats)
+    vq = (recon_at(rows, cols) if recon_at is not None else
+          affine_values(indices, codebook, group_scale, group_offset, group_size, rows, cols))
     delta = val - vq
     return SidecarCSR(row_ptr=row_ptr.to(torch.int32).contiguous(),
                       col=cols.to(torch.int32).contiguous(), val=val.contiguous(),

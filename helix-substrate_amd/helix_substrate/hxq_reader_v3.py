@@ -79,12 +79,13 @@ class CDNAv3Reader:
     def _load_indices(self) -> np.ndarray:
         if self._indices is None:
             rows, cols = self.shape
-            if self._meta.get("index_dtype", "uint8") != "uint8" or self.vector_dim != 1:
-                raise NotImplementedError("only scalar uint8 CDNAv3 tensors are supported")
-            raw = np.fromfile(self.tensor_dir / "indices.bin", dtype=np.uint8)
-            if raw.size != rows * cols:
-                raise ValueError(f"indices.bin has {raw.size} entries, expected {rows * cols}")
-            self._indices = raw.reshape(rows, cols)
+            d = self.vector_dim
+            dt = np.uint16 if self._meta.get("index_dtype", "uint8") == "uint16" else np.uint8
+            raw = np.fromfile(self.tensor_dir / "indices.bin", dtype=dt)
+            n_cols = cols // d
+            if raw.size != rows * n_cols:
+                raise ValueError(f"indices.bin has {raw.size} entries, expected {rows * n_cols}")
+            self._indices = raw.reshape(rows, n_cols)
         return self._indices
 
     def _load_sidecar(self):
@@ -120,7 +121,9 @@ class CDNAv3Reader:
 
     def reconstruct_block(self, start_row: int, end_row: int) -> np.ndarray:
         rows, cols = self.shape
+        # vector VQ: codebook [k, d], indices [rows, cols / d] -> [rows, cols]
         block = self._load_codebook()[self._load_indices()[start_row:end_row]].astype(np.float32)
+        block = block.reshape(end_row - start_row, cols)
         block = self._affine_rows(block, start_row, end_row)
         sc = self._load_sidecar()
         if sc is not None:

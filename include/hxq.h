@@ -51,6 +51,33 @@ typedef enum hxq_dtype {
     HXQ_F16 = 2
 } hxq_dtype;
 
+/* Index formats (the packed index data per weight):
+ *   HXQ_FMT_SCALAR   uint8 index into a <= 256-entry fp32 codebook, optional
+ *                    per-group affine: W = fl(fl(cb[q] * s) + o) (1 B/weight).
+ *   HXQ_FMT_VQ2_U16  2-D VQ: one uint16 index per weight pair into a
+ *                    [n_codes <= 4096, 2] fp32 codebook, W[o, 2j + d] =
+ *                    cb[q[o, j]][d] (1 B/weight; reference
+ *                    triton_vq2d_matmul.py:1-24).
+ *   HXQ_FMT_VQ2_P12  the same with the pair indices packed 12-bit, two per
+ *                    3 bytes (a = byte0 | (byte1 & 15) << 8, b = byte1 >> 4 |
+ *                    byte2 << 4; reference index_packing.py:1-13), rows of
+ *                    in/2 indices (in % 4 == 0) (0.75 B/weight).
+ *   HXQ_FMT_AF6      6-bit levels packed four per 3 bytes (q0 = b0 & 63,
+ *                    q1 = b0 >> 6 | (b1 & 15) << 2, q2 = b1 >> 4 | (b2 & 3) << 4,
+ *                    q3 = b2 >> 2), no codebook: W = fl(fl(q * s) + o) with
+ *                    the per-group fp32 scale/offset (reference
+ *                    triton_affine_group_matmul.py:181-259, 366-383)
+ *                    (0.75 B/weight).
+ * Both packed forms are little-endian bit streams (field i at bit 12i / 6i of
+ * the row's bytes).  The uint8 affine-group format of the same reference file
+ * is HXQ_FMT_SCALAR with the identity codebook cb[j] = j. */
+typedef enum hxq_format {
+    HXQ_FMT_SCALAR = 0,
+    HXQ_FMT_VQ2_U16 = 1,
+    HXQ_FMT_VQ2_P12 = 2,
+    HXQ_FMT_AF6 = 3
+} hxq_format;
+
 /* Message for the last failed call on this thread ("" if none). */
 const char *hxq_last_error(void);
 
@@ -112,6 +139,33 @@ typedef struct hxq_matrix {
     void *y;
     int64_t out_features;
 } hxq_matrix;
+
+/*
+ * hxq_gemv_fmt: hxq_gemv for any index format (HXQ_FMT_*); y = x W^T (+ bias),
+ * 1-4 activation rows, fp32 accumulation, sidecar CSR in weight coordinates
+ * (sc_delta = value - reconstruction).  Pair formats take `codebook`
+ * [n_codes, 2] and no affine; HXQ_FMT_AF6 takes the affine and no codebook.
+ * Indices must lie below n_codes.
+ * Replaces: the decode branches of fused_vq2d_matmul
+ * (triton_vq2d_matmul.py:171-280, with the 12-bit gather of
+ * triton_gather_12bit.py:43-157) and fused_affine_group_matmul_packed6
+ * (triton_affine_group_matmul.py:181-259, 262-363).
+ * hxq_dequant_fmt: the reconstruction W (fp32 rows [row_begin, row_end)),
+ * sidecar values replacing (as hxq_dequant_f32); replaces naive_vq2d_matmul's
+ * W / dequant_vq2d_tile (triton_vq2d_matmul.py:283-336) and
+ * unpack_12bit_rows (index_packing.py:75-95).
+ */
+int hxq_gemv_fmt(const void *x, int32_t x_dtype, int32_t format, const uint8_t *indices,
+                 const float *codebook, int32_t n_codes, const float *group_scale,
+                 const float *group_offset, int32_t group_size, const int32_t *sc_row_ptr,
+                 const int32_t *sc_col, const float *sc_delta, const float *bias, void *y,
+                 int32_t y_dtype, int64_t n_rows, int64_t out_features, int64_t in_features,
+                 hipStream_t stream);
+int hxq_dequant_fmt(int32_t format, const uint8_t *indices, const float *codebook,
+                    int32_t n_codes, const float *group_scale, const float *group_offset,
+                    int32_t group_size, const int32_t *sc_row_ptr, const int32_t *sc_col,
+                    const float *sc_val, int64_t out_features, int64_t in_features,
+                    int64_t row_begin, int64_t row_end, float *w_out, hipStream_t stream);
 
 int hxq_gemv_multi(const void *x, int32_t x_dtype, const hxq_matrix *mats,
                    int32_t n_mats, int32_t group_size, int32_t y_dtype,

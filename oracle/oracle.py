@@ -34,6 +34,12 @@ Reference functions restated (file:line under the reference checkout):
   (``hxq_encoder.py:107-177``, ``hxq_writer_v3.py:162-226, 427-467``,
   ``generate_sidecars_v3.py:18-40``), and ``mean_f32`` / ``percentile_f32``
   / ``percentiles_f64`` -- exact restatements of the numpy arithmetic it uses.
+* ``affine_fit_np`` -- the encoder's per-group affine fit (an extension of
+  the format; fixed-order fp64 least squares, stated at the function).
+* ``pack_12bit_np`` / ``unpack_12bit_np`` / ``unpack_6bit_np`` /
+  ``reconstruct_vq2_np`` / ``reconstruct_af6_np`` -- the variant index
+  formats (``index_packing.py:21-95``, ``triton_vq2d_matmul.py:283-308``,
+  ``triton_affine_group_matmul.py:223-233, 366-383``).
 * ``ssm_scan_chunked_np`` -- the chunked closed form of the same recurrence
   (the algorithm of ``chunked_scan``, ``mamba_scan_chunked.py:89-213``), written
   in the segment-sum form exp(cumA_t - cumA_s) that cannot overflow; fp64.
@@ -603,3 +609,62 @@ def affine_fit_np(w, indices, codebook, group_size, exclude_positions=None):
         s = np.where(ok, s_fit, 1.0)
         o = np.where(n > 0, (sw - s * sc) / np.where(n > 0, n, 1.0), 0.0)
     return s.astype(np.float32), o.astype(np.float32)
+
+
+def pack_12bit_np(values):
+    """Reference pack_12bit (index_packing.py:21-48): pairs (a, b) ->
+    [a & 0xff, (a >> 8) & 0xf | (b & 0xf) << 4, (b >> 4) & 0xff]."""
+    v = np.asarray(values).reshape(-1).astype(np.int64)
+    a, b = v[0::2], v[1::2]
+    out = np.empty((a.size, 3), np.uint8)
+    out[:, 0] = a & 0xFF
+    out[:, 1] = ((a >> 8) & 0x0F) | ((b & 0x0F) << 4)
+    out[:, 2] = (b >> 4) & 0xFF
+    return out.reshape(-1)
+
+
+def unpack_12bit_np(packed, n_values):
+    """Reference unpack_12bit (index_packing.py:51-72)."""
+    t = np.asarray(packed, np.uint8)[: n_values * 3 // 2].reshape(-1, 3).astype(np.int64)
+    a = t[:, 0] | ((t[:, 1] & 0x0F) << 8)
+    b = ((t[:, 1] >> 4) & 0x0F) | (t[:, 2] << 4)
+    return np.stack([a, b], 1).reshape(-1).astype(np.int16)
+
+
+def unpack_6bit_np(packed, n_values):
+    """The reference's 6-bit unpack (triton_affine_group_matmul.py:228-233;
+    codec spec: byte0 = q0 | q1 << 6, byte1 = q1 >> 2 | q2 << 4,
+    byte2 = q2 >> 4 | q3 << 2)."""
+    t = np.asarray(packed, np.uint8)[: n_values * 3 // 4].reshape(-1, 3).astype(np.int64)
+    b0, b1, b2 = t[:, 0], t[:, 1], t[:, 2]
+    q = np.stack([b0 & 0x3F, ((b0 >> 6) | (b1 << 2)) & 0x3F, ((b1 >> 4) | (b2 << 4)) & 0x3F,
+                  (b2 >> 2) & 0x3F], 1)
+    return q.reshape(-1).astype(np.uint8)
+
+
+def reconstruct_vq2_np(pair_indices, codebook, positions=None, values=None):
+    """2-D VQ reconstruction (reference hxq_reader_v3.py:118-133 with d = 2,
+    naive_vq2d_matmul's W, triton_vq2d_matmul.py:283-308): W[o, 2j + d] =
+    codebook[idx[o, j], d]; sidecar values replace (the reader's rule)."""
+    idx = np.asarray(pair_indices).astype(np.int64)
+    rows = idx.shape[0]
+    w = np.asarray(codebook, np.float32)[idx].reshape(rows, -1).copy()
+    if positions is not None and len(positions):
+        flat = w.reshape(-1)
+        flat[np.asarray(positions, np.int64)] = np.asarray(values, np.float32)
+    return w
+
+
+def reconstruct_af6_np(levels, scale, offset, group_size, positions=None, values=None):
+    """Per-group affine of integer levels (reference
+    affine_group_matmul_reference, triton_affine_group_matmul.py:366-383):
+    W = idx * scale + offset as two fp32 operations; sidecar values replace."""
+    q = np.asarray(levels).astype(np.float32)
+    rows, cols = q.shape
+    s = np.repeat(np.asarray(scale, np.float32), group_size, axis=1)
+    o = np.repeat(np.asarray(offset, np.float32), group_size, axis=1)
+    w = ((q * s).astype(np.float32) + o).astype(np.float32)
+    if positions is not None and len(positions):
+        flat = w.reshape(-1)
+        flat[np.asarray(positions, np.int64)] = np.asarray(values, np.float32)
+    return w

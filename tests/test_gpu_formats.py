@@ -1,0 +1,153 @@
+"""Variant index formats on the GPU against the oracle: reconstruction
+bit-exact (pair codebooks with uint16 and 12-bit packed indices, 6-bit affine
+levels, with sidecar replacement and row ranges); GEMV within 1e-5
+max-relative for fp32 activations and 2e-2 for bf16 (1-4 rows, ragged row
+counts, long rows, bias, sidecar); HelixLinear with pair codebooks (decode
+and many-row paths); the affine-group entry points against the reference
+formula."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helix_substrate import _hxq
+from helix_substrate.affine_group import (affine_group_matmul_reference, fused_affine_group_matmul,
+                                          fused_affine_group_matmul_packed6)
+from helix_substrate.helix_linear import HelixLinear
+from helix_substrate.hxq_format import build_sidecar_csr
+from helix_substrate.index_packing import pack_6bit, pack_12bit
+
+pytestmark = pytest.mark.gpu
+
+
+def _maxrel(y, ref):
+    return float(np.abs(np.asarray(y, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _case(fmt, out, inp, k=4096, G=128, nsc=0.001, seed=0):
+    """(raw index tensor, codebook, scale, offset, positions, values, W, W
+    without the sidecar) -- the oracle's reconstructions."""
+    rs = np.random.RandomState(seed)
+    if fmt == _hxq.FMT_AF6:
+        q = rs.randint(0, 64, (out, inp))
+        s = rs.uniform(0.5, 1.5, (out, inp // G)).astype(np.float16).astype(np.float32) * 1e-3
+        o = (rs.randn(out, inp // G) * 1e-2).astype(np.float16).astype(np.float32)
+        raw, cb = pack_6bit(torch.from_numpy(q)), None
+        rec = lambda p, v: oracle.reconstruct_af6_np(q, s, o, G, p, v)
+    else:
+        cb = (rs.randn(k, 2) * 0.02).astype(np.float32)
+        idx = rs.randint(0, k, (out, inp // 2))
+        raw = (pack_12bit(torch.from_numpy(idx)) if fmt == _hxq.FMT_VQ2_P12
+               else torch.from_numpy(idx.astype(np.int16)))
+        s = o = None
+        rec = lambda p, v: oracle.reconstruct_vq2_np(idx, cb, p, v)
+    rs2 = np.random.RandomState(seed + 1)
+    pos = np.sort(rs2.choice(out * inp, int(out * inp * nsc), replace=False)).astype(np.int64)
+    val = (rs2.randn(pos.size) * 0.1).astype(np.float32)
+    return raw, cb, s, o, pos, val, rec(pos, val), rec(None, None)
+
+
+def _dev(dev, *arrs):
+    return [None if a is None else (a.to(dev) if isinstance(a, torch.Tensor)
+                                    else torch.from_numpy(np.ascontiguousarray(a)).to(dev))
+            for a in arrs]
+
+
+def _csr(dev, pos, val, W_nosc, out, inp):
+    t = torch.from_numpy
+    csr = build_sidecar_csr(t(pos), t(val), torch.zeros(out, inp, dtype=torch.uint8), None,
+                            shape=(out, inp),
+                            recon_at=lambda r, c: t(W_nosc)[r, c])
+    return csr.row_ptr.to(dev), csr.col.to(dev), csr.val.to(dev), csr.delta.to(dev)
+
+
+FMTS = [_hxq.FMT_VQ2_U16, _hxq.FMT_VQ2_P12, _hxq.FMT_AF6]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape,k", [((512, 1024), 4096), ((300, 256), 1000)])
+def test_dequant_fmt_bit_exact(dev, fmt, shape, k):
+    out, inp = shape
+    G = 64 if inp == 256 else 128
+    raw, cb, s, o, pos, val, W, W0 = _case(fmt, out, inp, k=k, G=G)
+    print(f"dequant fmt={fmt} shape={shape} k={k}", flush=True)
+    rp, col, sval, _ = _csr(dev, pos, val, W0, out, inp)
+    raw_d, cb_d, s_d, o_d = _dev(dev, raw, cb, s, o)
+    got = _hxq.dequant_fmt(fmt, raw_d, out, inp, codebook=cb_d, group_scale=s_d, group_offset=o_d,
+                           group_size=G, sc_row_ptr=rp, sc_col=col, sc_val=sval)
+    np.testing.assert_array_equal(got.cpu().numpy(), W)
+    part = _hxq.dequant_fmt(fmt, raw_d, out, inp, codebook=cb_d, group_scale=s_d, group_offset=o_d,
+                            group_size=G, row_begin=7, row_end=45)
+    np.testing.assert_array_equal(part.cpu().numpy(), W0[7:45])
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("out,inp,n", [(2048, 2048, 1), (2048, 2048, 4), (1000, 512, 3),
+                                       (2048, 11008, 1), (22016, 2048, 1)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_gemv_fmt_matches_oracle(dev, fmt, out, inp, n, xdt):
+    raw, cb, s, o, pos, val, W, W0 = _case(fmt, out, inp, seed=out + inp)
+    rp, col, _, delta = _csr(dev, pos, val, W0, out, inp)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(n, inp, generator=g).to(xdt)
+    bias = torch.randn(out, generator=g) * 0.1
+    raw_d, cb_d, s_d, o_d, x_d, b_d = _dev(dev, raw, cb, s, o, x, bias)
+    print(f"gemv fmt={fmt} out={out} in={inp} n={n} x={xdt}", flush=True)
+    y = _hxq.gemv_fmt(x_d, fmt, raw_d, out, codebook=cb_d, group_scale=s_d, group_offset=o_d,
+                      group_size=128, sc_row_ptr=rp, sc_col=col, sc_delta=delta, bias=b_d)
+    ref = oracle.linear_f64(x.float().numpy(), W, bias.numpy())
+    assert _maxrel(y.cpu().numpy(), ref) <= (1e-5 if xdt == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_pair_helix_linear_device(dev, packed):
+    rs = np.random.RandomState(6)
+    out, inp = 768, 1024
+    cb = torch.from_numpy((rs.randn(4096, 2) * 0.02).astype(np.float32))
+    idx = torch.from_numpy(rs.randint(0, 4096, (out, inp // 2)).astype(np.int16))
+    pos = torch.from_numpy(np.sort(rs.choice(out * inp, 700, replace=False)).astype(np.int64))
+    val = torch.from_numpy(rs.randn(700).astype(np.float32) * 0.1)
+    bias = torch.from_numpy(rs.randn(out).astype(np.float32))
+    m = HelixLinear(inp, out, cb, pack_12bit(idx) if packed else idx, sidecar_positions=pos,
+                    sidecar_values=val, bias=bias, vector_dim=2).to(dev)
+    W = oracle.reconstruct_vq2_np(idx.numpy(), cb.numpy(), pos.numpy(), val.numpy())
+    np.testing.assert_array_equal(m.decode_weight().cpu().numpy(), W)
+    print(f"pair HelixLinear packed={packed}", flush=True)
+    for n, dt, tol, path in [(1, torch.float32, 1e-5, "hip_gemv_fmt"),
+                             (4, torch.bfloat16, 2e-2, "hip_gemv_fmt"),
+                             (37, torch.float32, 1e-5, "hip_dequant_gemm"),
+                             (64, torch.bfloat16, 2e-2, "hip_dequant_gemm")]:
+        x = torch.from_numpy(rs.randn(n, inp).astype(np.float32)).to(dt)
+        y = m(x.to(dev))
+        assert m._last_dispatch_path == path and y.dtype == dt
+        ref = oracle.linear_f64(x.float().numpy(), W, bias.numpy())
+        assert _maxrel(y.float().cpu().numpy(), ref) <= tol, (n, dt)
+
+
+def test_affine_group_entry_points(dev):
+    rs = np.random.RandomState(7)
+    out, inp, G = 1024, 2048, 128
+    q = torch.from_numpy(rs.randint(0, 256, (out, inp)).astype(np.uint8))
+    s = torch.from_numpy(rs.uniform(1e-4, 2e-4, (out, inp // G)).astype(np.float16))
+    o = torch.from_numpy((rs.randn(out, inp // G) * 1e-2).astype(np.float16))
+    b = torch.from_numpy(rs.randn(out).astype(np.float32))
+    W8 = oracle.reconstruct_af6_np(q.numpy(), s.float().numpy(), o.float().numpy(), G)
+    print("affine group uint8", flush=True)
+    for n, dt, tol in [(1, torch.float32, 1e-5), (3, torch.float32, 1e-5), (64, torch.bfloat16, 2e-2)]:
+        x = torch.from_numpy(rs.randn(n, inp).astype(np.float32)).to(dt)
+        y = fused_affine_group_matmul(x.to(dev), q.to(dev), s.to(dev), o.to(dev), G, b.to(dev))
+        assert y.dtype == torch.float32
+        assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.float().numpy(), W8, b.numpy())) <= tol
+    q6 = torch.from_numpy(rs.randint(0, 64, (out, inp)).astype(np.uint8))
+    W6 = oracle.reconstruct_af6_np(q6.numpy(), s.float().numpy(), o.float().numpy(), G)
+    p6 = pack_6bit(q6).to(dev)
+    print("affine group 6-bit", flush=True)
+    for n, dt, tol in [(1, torch.float32, 1e-5), (4, torch.bfloat16, 2e-2), (20, torch.float32, 1e-5)]:
+        x = torch.from_numpy(rs.randn(n, inp).astype(np.float32)).to(dt)
+        y = fused_affine_group_matmul_packed6(x.to(dev), p6, s.to(dev), o.to(dev), out, inp, G,
+                                              b.to(dev))
+        assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.float().numpy(), W6, b.numpy())) <= tol
+    # the torch formula agrees with the oracle as well
+    x = torch.from_numpy(rs.randn(2, inp).astype(np.float32))
+    yr = affine_group_matmul_reference(x, q6, s, o, G, b)
+    assert _maxrel(yr.numpy(), oracle.linear_f64(x.numpy(), W6, b.numpy())) <= 1e-5
