@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--encode", type=int, default=1,
                     help="also time the CDNAv3 encoder on one Qwen2.5-3B gate_proj "
                          "(k-means codebook, assignment, percentile sidecar)")
+    ap.add_argument("--formats", type=int, default=1,
+                    help="also time the GEMV on the variant index formats (pair codebook with "
+                         "uint16 / 12-bit indices, 6-bit affine) at the gate+up shape")
     ap.add_argument("--decode", type=int, default=1,
                     help="also run the config-1 greedy decode loop (tok/s, 128-token prompt, "
                          "256 new tokens)")
@@ -265,6 +268,8 @@ def main():
         result["moe_config4"] = moe_bench(dev, cpu=args.cpu_seconds > 0)
     if args.encode:
         result["encode_cdnav3"] = encode_bench(dev, cpu=args.cpu_seconds > 0)
+    if args.formats:
+        result["formats_gateup"] = formats_bench(dev)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layer0, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -608,6 +613,86 @@ def moe_bench(dev, n_layers=16, iters=3, cpu=True):
     del layers
     torch.cuda.empty_cache()
     return out
+
+
+def formats_bench(dev, copies=12, reps=5):
+    """GEMV on each index format at the gate+up shape (22016 x 2048, one bf16
+    row, 0.1% sidecar as CSR, bias-free): `copies` distinct matrices (well past
+    the 256 MB Infinity Cache) launched back to back in one HIP graph; per
+    launch: algorithmic bytes (index data + codebook + affine + CSR + x + y)
+    / average launch time between HIP events on the launch stream."""
+    import torch
+    from helix_substrate import _hxq
+
+    out_f, in_f, G = 2 * INTER, HIDDEN, 128
+    g = torch.Generator(device=dev).manual_seed(11)
+    nnz = out_f * 2  # 2 entries per row ~ 0.1% of 2048 columns
+    csr = (torch.arange(out_f + 1, device=dev, dtype=torch.int32) * 2,
+           torch.randint(0, in_f, (nnz,), device=dev, generator=g, dtype=torch.int32),
+           torch.randn(nnz, device=dev, generator=g) * 0.05)
+    csr_bytes = (out_f + 1) * 4 + nnz * 8
+    x = torch.randn(1, in_f, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(1, out_f, device=dev, dtype=torch.bfloat16)
+    specs = {
+        "scalar_u8_affine": (_hxq.FMT_SCALAR, out_f * in_f, 256, True),
+        "vq2_u16": (_hxq.FMT_VQ2_U16, out_f * in_f, 4096, False),
+        "vq2_p12": (_hxq.FMT_VQ2_P12, out_f * in_f * 3 // 4, 4096, False),
+        "af6": (_hxq.FMT_AF6, out_f * in_f * 3 // 4, 0, True),
+    }
+    res = {}
+    for name, (fmt, nbytes, k, aff) in specs.items():
+        mats = []
+        for _ in range(copies):
+            raw = torch.randint(0, 256, (nbytes,), device=dev, generator=g, dtype=torch.int32)
+            raw = raw.to(torch.uint8)
+            if fmt == _hxq.FMT_VQ2_U16:
+                raw = (raw.view(-1, 2)[:, 0].to(torch.int16) |
+                       ((raw.view(-1, 2)[:, 1].to(torch.int16) & 15) << 8))
+            cb = (None if k == 0 else torch.randn(*((k,) if fmt == _hxq.FMT_SCALAR else (k, 2)),
+                                                   device=dev, generator=g) * 0.02)
+            gs = go = None
+            if aff:
+                gs = torch.rand(out_f, in_f // G, device=dev, generator=g) * 1e-3
+                go = torch.randn(out_f, in_f // G, device=dev, generator=g) * 1e-3
+            mats.append((raw, cb, gs, go))
+        torch.cuda.synchronize(dev)
+
+        def launch(m):
+            raw, cb, gs, go = m
+            _hxq.gemv_fmt(x, fmt, raw if fmt != _hxq.FMT_SCALAR else raw.view(out_f, in_f), out_f,
+                          codebook=cb, group_scale=gs, group_offset=go, group_size=G,
+                          sc_row_ptr=csr[0], sc_col=csr[1], sc_delta=csr[2], out=y)
+
+        for m in mats:
+            launch(m)
+        gg = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream(dev)
+        st.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(gg, stream=st):
+                for m in mats:
+                    launch(m)
+        torch.cuda.current_stream(dev).wait_stream(st)
+        gg.replay()
+        torch.cuda.synchronize(dev)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            gg.replay()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        us = 1000.0 * e0.elapsed_time(e1) / (reps * copies)
+        extra = (0 if k == 0 else (k * 4 if fmt == _hxq.FMT_SCALAR else k * 8))
+        extra += out_f * (in_f // G) * 8 if aff else 0
+        b = nbytes + extra + csr_bytes + in_f * 2 + out_f * 2
+        res[name] = {"us_per_launch": round(us, 2), "bytes_per_launch": b,
+                     "bytes_per_weight": round(b / (out_f * in_f), 4),
+                     "gbs": round(b / (us * 1e-6) / 1e9, 1),
+                     "frac_of_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del mats, gg
+        torch.cuda.empty_cache()
+    return res
 
 
 def encode_bench(dev, iters=3, cpu=True):
