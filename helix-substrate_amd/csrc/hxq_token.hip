@@ -12,14 +12,15 @@
 // (index rows, affine factors, codebook, CSR row pointers) right after
 // arriving and before waiting: HBM streams while the grid synchronises.
 //
-// Grid barrier (per-block arrival flags + one release word):
+// Grid barrier (per-block arrival flags):
 //   arrive: each wave waits for its own stores (s_waitcnt 0), workgroup
 //           barrier, thread 0 stores flag[block] = target (coherent store);
-//   wait:   block 0's wave 0 polls all flags until every one reached target,
-//           then stores release = target; the other blocks' wave 0 polls the
-//           release word.  Every wait gives up after 1 s of wall clock or when
-//           the error word is set, and the kernel then returns, so every wave
-//           ends even if the grid cannot synchronise.
+//   wait:   wave 0 of every block polls all flags (or only its producers'
+//           flags) until each reached target -- one cross-XCD hop.  Every
+//           wait gives up after 1 s of wall clock or when the error word is
+//           set, and the kernel then returns, so every wave ends even if the
+//           grid cannot synchronise.  (The release word in the workspace is
+//           cleared but no longer used.)
 // Data that crosses blocks inside a launch (residual stream, q/k/v, attention
 // output, o, SiLU product, down output, argmax partials) is written with
 // coherent stores (sc1) and read with coherent loads (sc1), so no L2
@@ -130,18 +131,19 @@ struct Plan {
     int32_t *pos;
     float *logits;
     const Layer *layers;
-    // Data that crosses blocks: one slot per layer, so every address is
-    // written once per launch before any block reads it -- no L2 can hold a
-    // stale copy, and readers use ordinary cached loads (8 L2 fills per
-    // line instead of one memory read per block).  Producers store with sc1
-    // (write-through) so the data is at the coherence point before their
-    // barrier flag.
+    // Data that crosses blocks: one slot per layer (every address written
+    // once per launch), in flag-in-data words (ll_* below): fp32 values as
+    // two words, bf16 values as one, each word tagged with the producing
+    // stage's epoch.  Producers store with sc1 (write-through); consumers
+    // poll with sc1 loads until every word they need carries the epoch, so
+    // no grid barrier separates the stages of a layer.
     //   res[l]  residual entering layer l (l = 1..L; layer 0 embeds)
     //   ra[l]   residual after layer l's attention block input add
     //   qkv[l], attn[l], o[l], act[l], dn[l]
-    float *res, *ra, *qkv, *o, *dn, *part_v;
-    uint16_t *attn, *act;
-    int32_t ls_hid, ls_qkv, ls_attn, ls_act;  // slot strides (elements)
+    uint32_t *res, *ra, *qkv, *o, *dn;
+    float *part_v;
+    uint32_t *attn, *act;
+    int32_t ls_hid, ls_qkv, ls_attn, ls_act;  // slot strides (32-bit words)
     int32_t *part_i;
     uint32_t *flags, *release;
     int32_t *err;
@@ -187,6 +189,36 @@ __device__ __forceinline__ void coh_store_bf16(uint16_t *base, int64_t n, int64_
                                           static_cast<uint32_t>(i * 2), 0, kCoh);
 }
 __device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// ---------------------------------------------------------------------------
+// flag-in-data words
+// ---------------------------------------------------------------------------
+// A word holds 16 data bits in its high half and the producing stage's epoch
+// (never 0: zeroed memory is never valid) in its low half.  fp32 values are
+// two words (high, low 16 bits), bf16 values one.  Each word is validated on
+// its own, so no store wider than 32 bits needs to be single-copy atomic.
+__device__ __forceinline__ uint32_t ll_epoch(uint32_t target) { return (target & 0x7fffu) | 0x8000u; }
+__device__ __forceinline__ bool ll_ok(uint32_t w, uint32_t e) { return (w & 0xffffu) == e; }
+__device__ __forceinline__ float ll_f32(uint32_t hi, uint32_t lo) {
+    return __uint_as_float((hi & 0xffff0000u) | (lo >> 16));
+}
+__device__ __forceinline__ float ll_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t ll_hi(float v, uint32_t e) { return (__float_as_uint(v) & 0xffff0000u) | e; }
+__device__ __forceinline__ uint32_t ll_lo(float v, uint32_t e) { return (__float_as_uint(v) << 16) | e; }
+__device__ __forceinline__ uint32_t ll_bf16w(float v, uint32_t e) {
+    return (static_cast<uint32_t>(f32_to_bf16(v)) << 16) | e;
+}
+// two words at p (8-byte aligned), one coherent store
+__device__ __forceinline__ void ll_store2(uint32_t *p, uint32_t a, uint32_t b) {
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p),
+                       static_cast<uint64_t>(a) | (static_cast<uint64_t>(b) << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint2 coh_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoh);
+    return make_uint2(v[0], v[1]);
+}
 
 // Wave64 reductions via DPP (no lane-address registers); the result is
 // read from lane 63 into a scalar register, i.e. every lane gets it.
@@ -243,37 +275,29 @@ __device__ __forceinline__ bool gave_up(const Plan &P, uint64_t t0) {
     return false;
 }
 
-// Returns false when the grid could not synchronise (the caller returns).
+// Grid barrier, one hop: wave 0 of every block polls all blocks' flags
+// (one coherent 16-byte load per lane per 256 blocks) until each reached
+// `target`.  Returns false when the grid could not synchronise (the caller
+// returns).
 __device__ __forceinline__ bool wait_all(const Plan &P, uint32_t target, int *sh) {
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
         int ok = 1;
         const uint64_t t0 = wall_clock64();
-        if (blockIdx.x == 0) {
-            const int nb = P.nblocks;
-            const __amdgpu_buffer_rsrc_t fr = urs(P.flags, static_cast<int64_t>(nb) * 4);
-            while (true) {
-                int done = 1;
-                for (int i0 = 0; i0 < nb; i0 += 4 * kWave) {
-                    const u32x4 f = coh_load16(fr, static_cast<uint32_t>(i0 + 4 * lane) * 4u);
+        const int nb = P.nblocks;
+        const __amdgpu_buffer_rsrc_t fr = urs(P.flags, static_cast<int64_t>(nb) * 4);
+        while (true) {
+            int done = 1;
+            for (int i0 = 0; i0 < nb; i0 += 4 * kWave) {
+                const u32x4 f = coh_load16(fr, static_cast<uint32_t>(i0 + 4 * lane) * 4u);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int i = i0 + 4 * lane + j;
-                        done &= (i >= nb) || static_cast<int32_t>(f[j] - target) >= 0;
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    const int i = i0 + 4 * lane + j;
+                    done &= (i >= nb) || static_cast<int32_t>(f[j] - target) >= 0;
                 }
-                if (__all(done)) break;
-                if (gave_up(P, t0)) { ok = 0; break; }
             }
-            if (ok && lane == 0)
-                __hip_atomic_store(P.release, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            while (true) {
-                const uint32_t r = __builtin_amdgcn_readfirstlane(
-                    __hip_atomic_load(P.release, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-                if (static_cast<int32_t>(r - target) >= 0) break;
-                if (gave_up(P, t0)) { ok = 0; break; }
-            }
+            if (__all(done)) break;
+            if (gave_up(P, t0)) { ok = 0; break; }
         }
         if (lane == 0) *sh = ok;
     }
@@ -519,21 +543,26 @@ __device__ __forceinline__ float row_dot(uint32_t lane_seg, const Batch &b, int 
     return acc;
 }
 
-// Activation sources of a GEMV stage.
-//   XNORM: r = base + delta (fp32, coherent; delta may be null) or the bf16
-//          embedding row emb; x = bf16(w * r * rsqrt(mean(r^2) + eps)); block
-//          0 stores r to res_out.
-//   XBF16: x = bf16 vector (coherent).
+// Activation sources of a GEMV stage (flag-in-data slots, polled until
+// every word carries its producer's epoch: eb for base / xb, ed for delta).
+//   XNORM: r = base + delta (fp32 words; delta may be null) or the bf16
+//          embedding row emb (plain); x = bf16(w * r * rsqrt(mean(r^2) +
+//          eps)); block 0 stores r to res_out with epoch eo.
+//   XBF16: x = bf16 words.
 enum { XNORM = 0, XBF16 = 1 };
 
 struct XSrc {
-    const float *base;
-    const float *delta;
+    const uint32_t *base;
+    const uint32_t *delta;
     const uint16_t *emb;
     const float *w;
-    float *res_out;
-    const uint16_t *xb;
+    uint32_t *res_out;
+    const uint32_t *xb;
+    uint32_t eb, ed, eo;
 };
+
+// Poll iterations between checks of the error word / clock.
+constexpr int kPollCheck = 16;
 
 // Builds the stage's activation vector in LDS xl (fp32 [K]) block-wide --
 // each thread handles 4 (XNORM) or 8 (XBF16) consecutive elements, so few
@@ -559,20 +588,41 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             r[2] = __uint_as_float(hi << 16);
             r[3] = __uint_as_float(hi & 0xffff0000u);
         } else {
-            const u32x4 a = buf_load16(urs(X.base, static_cast<int64_t>(K) * 4), o4);
-            const u32x4 d = buf_load16(urs(X.delta, X.delta ? static_cast<int64_t>(K) * 4 : 0), o4);
+            // 4 values = 8 words = two 16-byte pieces per buffer
+            const __amdgpu_buffer_rsrc_t br = urs(X.base, static_cast<int64_t>(K) * 8);
+            const __amdgpu_buffer_rsrc_t dr = urs(X.delta, X.delta ? static_cast<int64_t>(K) * 8 : 0);
+            const uint32_t o8 = mine ? static_cast<uint32_t>(t) * 32u : kOob;
+            const bool has_d = X.delta != nullptr;
+            u32x4 a0, a1, d0, d1;
+            const uint64_t t0 = wall_clock64();
+            for (int it = 1;; ++it) {
+                a0 = coh_load16(br, o8);
+                a1 = coh_load16(br, o8 + 16u);
+                d0 = coh_load16(dr, o8);
+                d1 = coh_load16(dr, o8 + 16u);
+                bool ok = true;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) r[j] = __uint_as_float(a[j]) + __uint_as_float(d[j]);
+                for (int j = 0; j < 4; ++j)
+                    ok = ok && ll_ok(a0[j], X.eb) && ll_ok(a1[j], X.eb) &&
+                         (!has_d || (ll_ok(d0[j], X.ed) && ll_ok(d1[j], X.ed)));
+                if (__all(ok || !mine)) break;
+                if (it % kPollCheck == 0 && gave_up(P, t0)) break;
+            }
+            r[0] = ll_f32(a0[0], a0[1]) + ll_f32(d0[0], d0[1]);
+            r[1] = ll_f32(a0[2], a0[3]) + ll_f32(d0[2], d0[3]);
+            r[2] = ll_f32(a1[0], a1[1]) + ll_f32(d1[0], d1[1]);
+            r[3] = ll_f32(a1[2], a1[3]) + ll_f32(d1[2], d1[3]);
         }
         const u32x4 w = buf_load16(urs(X.w, static_cast<int64_t>(K) * 4), o4);
         __builtin_amdgcn_sched_barrier(0);
         after();  // loads that may return after the activations
         __builtin_amdgcn_sched_barrier(0);
         if (X.res_out && blockIdx.x == 0 && mine) {
-            u32x4 v;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = __float_as_uint(r[j]);
-            coh_store16(urs(X.res_out, static_cast<int64_t>(K) * 4), o4, v);
+            const __amdgpu_buffer_rsrc_t rr = urs(X.res_out, static_cast<int64_t>(K) * 8);
+            const u32x4 v0{ll_hi(r[0], X.eo), ll_lo(r[0], X.eo), ll_hi(r[1], X.eo), ll_lo(r[1], X.eo)};
+            const u32x4 v1{ll_hi(r[2], X.eo), ll_lo(r[2], X.eo), ll_hi(r[3], X.eo), ll_lo(r[3], X.eo)};
+            coh_store16(rr, static_cast<uint32_t>(t) * 32u, v0);
+            coh_store16(rr, static_cast<uint32_t>(t) * 32u + 16u, v1);
         }
         float ss = 0.f;
 #pragma unroll
@@ -591,13 +641,26 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
                             bf16r(__uint_as_float(w[2]) * (r[2] * inv)),
                             bf16r(__uint_as_float(w[3]) * (r[3] * inv)));
     } else {
-        // K <= 16384: at most two 16-byte pieces per thread
-        const __amdgpu_buffer_rsrc_t xr = urs(X.xb, static_cast<int64_t>(K) * 2);
-        u32x4 w[2];
+        // K <= 16384: at most two pieces of 8 values (8 words, 32 bytes) per thread
+        const __amdgpu_buffer_rsrc_t xr = urs(X.xb, static_cast<int64_t>(K) * 4);
+        u32x4 w[2][2];
+        bool have[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int i = t + j * kThreads;
-            w[j] = buf_load16(xr, i * 8 < K ? static_cast<uint32_t>(i) * 16u : kOob);
+        for (int j = 0; j < 2; ++j) have[j] = (t + j * kThreads) * 8 < K;
+        const uint64_t t0 = wall_clock64();
+        for (int it = 1;; ++it) {
+            bool ok = true;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t off = have[j] ? static_cast<uint32_t>(t + j * kThreads) * 32u : kOob;
+                w[j][0] = coh_load16(xr, off);
+                w[j][1] = coh_load16(xr, off + 16u);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ok = ok && (!have[j] || (ll_ok(w[j][0][e], X.eb) && ll_ok(w[j][1][e], X.eb)));
+            }
+            if (__all(ok)) break;
+            if (it % kPollCheck == 0 && gave_up(P, t0)) break;
         }
         __builtin_amdgcn_sched_barrier(0);
         after();
@@ -605,12 +668,12 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int i = t + j * kThreads;
-            if (i * 8 < K) {
+            if (have[j]) {
                 float4 *dst = reinterpret_cast<float4 *>(xl + 8 * i);
-                dst[0] = make_float4(__uint_as_float(w[j][0] << 16), __uint_as_float(w[j][0] & 0xffff0000u),
-                                     __uint_as_float(w[j][1] << 16), __uint_as_float(w[j][1] & 0xffff0000u));
-                dst[1] = make_float4(__uint_as_float(w[j][2] << 16), __uint_as_float(w[j][2] & 0xffff0000u),
-                                     __uint_as_float(w[j][3] << 16), __uint_as_float(w[j][3] & 0xffff0000u));
+                dst[0] = make_float4(ll_bf16(w[j][0][0]), ll_bf16(w[j][0][1]), ll_bf16(w[j][0][2]),
+                                     ll_bf16(w[j][0][3]));
+                dst[1] = make_float4(ll_bf16(w[j][1][0]), ll_bf16(w[j][1][1]), ll_bf16(w[j][1][2]),
+                                     ll_bf16(w[j][1][3]));
             }
         }
     }
@@ -634,9 +697,9 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
     }
 }
 
-// Outputs of a GEMV stage.
-//   YF32: y[y_off + row] fp32 (coherent) for the block's matrix;
-//   YACT: pair stage, act[row] = bf16(silu(gate) * up) (coherent).
+// Outputs of a GEMV stage (flag-in-data words with epoch ey, coherent):
+//   YF32: fp32 y[y_off + row] for the block's matrix;
+//   YACT: pair stage, bf16 act[row] = silu(gate) * up.
 enum { YF32 = 0, YACT = 1 };
 
 // Sum of one row: slices, then sidecar entries in CSR order (the caller
@@ -657,7 +720,7 @@ __device__ __forceinline__ float row_total(const Mat &M, int r, int S, const flo
 
 template <int HC, int XM, int YM>
 __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, const XSrc &X,
-                                         void *y, float *smem, int tid, int lane) {
+                                         uint32_t *y, uint32_t ey, float *smem, int tid, int lane) {
     const int32_t K = G.K, group = P.group;
     float *xl = smem + (G.nseg == 2 ? 2 * kTbl : kTbl);
     float *red = smem + P.lds_red;                           // [2][kRedCap]
@@ -744,13 +807,16 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
         const int S = g.S;
         const float v0 = row_total(G.m0, t, S, red, rps[t], rps[t + 1], rps[0], ent, xl) + bias[0];
         if constexpr (YM == YF32) {
-            coh_storef(static_cast<float *>(y) + G.y_off + row, v0);
+            ll_store2(y + 2 * (G.y_off + row), ll_hi(v0, ey), ll_lo(v0, ey));
         } else {
             const float v1 = row_total(G.m1, t, S, red + kRedCap, rps[kRps + t],
                                        rps[kRps + t + 1], rps[kRps], ent + kEnt, xl) + bias[1];
-            coh_store_bf16(static_cast<uint16_t *>(y), P.inter, row, v0 / (1.f + expf(-v0)) * v1);
+            coh_store_u32(y + row, ll_bf16w(v0 / (1.f + expf(-v0)) * v1, ey));
         }
     }
+    // the next stage rebuilds the tables and xl in LDS: every thread is past
+    // this stage's reads first (stores stay in flight: LDS-only barrier)
+    lds_barrier();
 }
 
 // ---------------------------------------------------------------------------
@@ -805,9 +871,9 @@ __device__ __forceinline__ void rope_table(const Plan &P, int pos, float2 *tab) 
 //   the first head of each group, scores are one position per thread,
 //   softmax by block reductions, and the output is summed by wave over
 //   positions (lane = 2 dims) and across waves in LDS.
-template <typename Wait>
-__device__ bool attention(const Plan &P, const Layer &L, const float *qkv, uint16_t *attn, int h,
-                          int pos, float *smem, const float2 *rope, Wait wait) {
+__device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const uint32_t *qkv, uint32_t eq,
+                          uint32_t *attn, uint32_t ea, int h,
+                          int pos, float *smem, const float2 *rope) {
     constexpr int D = kHeadDim;
     float *sc = smem;                     // [kMaxSeq]
     float *qs = sc + kMaxSeq;             // [D]
@@ -840,20 +906,52 @@ __device__ bool attention(const Plan &P, const Layer &L, const float *qkv, uint1
         vw[u] = __builtin_amdgcn_raw_buffer_load_b32(
             vr, tt < pos ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
     }
-    if (!wait()) return false;
-    // this token's q, k, v
-    const float *qh = qkv + static_cast<int64_t>(h) * D;
-    const float *kh = qkv + static_cast<int64_t>(P.n_heads + kvh) * D;
-    const float *vh = qkv + static_cast<int64_t>(P.n_heads + P.n_kv + kvh) * D;
+    // this token's q, k, v (flag-in-data words of the q/k/v stage, epoch eq):
+    // threads [0, D/2) take q[t], q[t + D/2], k[t], k[t + D/2]; threads
+    // [D/2, D/2 + D) take v[t - D/2]
+    const int64_t qe = static_cast<int64_t>(h) * D, ke = static_cast<int64_t>(P.n_heads + kvh) * D;
+    const int64_t ve = static_cast<int64_t>(P.n_heads + P.n_kv + kvh) * D;
+    float qv0 = 0.f, qv1 = 0.f, kv0 = 0.f, kv1 = 0.f, vv = 0.f;
+    {
+        const __amdgpu_buffer_rsrc_t qr =
+            urs(qkv, static_cast<int64_t>(P.n_heads + 2 * P.n_kv) * D * 8);
+        const bool qk = t < D / 2, vt = t >= D / 2 && t < D / 2 + D;
+        const uint32_t o0 = qk ? static_cast<uint32_t>(qe + t) * 8u : vt ? static_cast<uint32_t>(ve + t - D / 2) * 8u : kOob;
+        const uint32_t o1 = qk ? static_cast<uint32_t>(qe + t + D / 2) * 8u : kOob;
+        const uint32_t o2 = qk ? static_cast<uint32_t>(ke + t) * 8u : kOob;
+        const uint32_t o3 = qk ? static_cast<uint32_t>(ke + t + D / 2) * 8u : kOob;
+        uint2 w0, w1, w2, w3;
+        const uint64_t t0 = wall_clock64();
+        for (int it = 1;; ++it) {
+            w0 = coh_load8(qr, o0);
+            w1 = coh_load8(qr, o1);
+            w2 = coh_load8(qr, o2);
+            w3 = coh_load8(qr, o3);
+            const bool ok = !(qk || vt) ||
+                            (ll_ok(w0.x, eq) && ll_ok(w0.y, eq) &&
+                             (vt || (ll_ok(w1.x, eq) && ll_ok(w1.y, eq) && ll_ok(w2.x, eq) &&
+                                     ll_ok(w2.y, eq) && ll_ok(w3.x, eq) && ll_ok(w3.y, eq))));
+            if (__all(ok)) break;
+            if (it % kPollCheck == 0 && gave_up(P, t0)) break;
+        }
+        if (qk) {
+            qv0 = ll_f32(w0.x, w0.y);
+            qv1 = ll_f32(w1.x, w1.y);
+            kv0 = ll_f32(w2.x, w2.y);
+            kv1 = ll_f32(w3.x, w3.y);
+        } else {
+            vv = ll_f32(w0.x, w0.y);
+        }
+    }
     const bool writer = h % grp == 0;
     const float scale = rsqrtf(static_cast<float>(D));
     if (t < D / 2) {
         const float2 cs = rope[t];
         float a, b;
-        rope_rot(qh[t], qh[t + D / 2], cs, a, b);
+        rope_rot(qv0, qv1, cs, a, b);
         qs[t] = a * scale;
         qs[t + D / 2] = b * scale;
-        rope_rot(kh[t], kh[t + D / 2], cs, a, b);
+        rope_rot(kv0, kv1, cs, a, b);
         const int64_t base = static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D;
         if (writer) {
             L.kc[base + t] = f32_to_bf16(a);
@@ -863,7 +961,7 @@ __device__ bool attention(const Plan &P, const Layer &L, const float *qkv, uint1
         kn[t + D / 2] = bf16r(b);
     } else if (t < D / 2 + D) {
         const int j = t - D / 2;
-        const float v = vh[j];
+        const float v = vv;
         if (writer) L.vc[static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D + j] = f32_to_bf16(v);
         vn[j] = bf16r(v);
     }
@@ -937,9 +1035,7 @@ __device__ bool attention(const Plan &P, const Layer &L, const float *qkv, uint1
             v0 += part[w * D + d];
             v1 += part[w * D + d + 1];
         }
-        const uint32_t packed = static_cast<uint32_t>(f32_to_bf16(v0 * inv)) |
-                                (static_cast<uint32_t>(f32_to_bf16(v1 * inv)) << 16);
-        coh_store_u32(reinterpret_cast<uint32_t *>(attn + static_cast<int64_t>(h) * D + d), packed);
+        ll_store2(attn + static_cast<int64_t>(h) * D + d, ll_bf16w(v0 * inv, ea), ll_bf16w(v1 * inv, ea));
     }
     return true;
 }
@@ -980,19 +1076,20 @@ __device__ void lm_head(const Plan &P, LmPre<HC> &pf, float *smem, int wave, int
     float hx[2 * HC][8];
     float ss = 0.f;
     const int64_t lL = P.n_layers;
-    const __amdgpu_buffer_rsrc_t ar = urs(P.res + lL * P.ls_hid, static_cast<int64_t>(K) * 4);
-    const __amdgpu_buffer_rsrc_t dr = urs(P.dn + (lL - 1) * P.ls_hid, static_cast<int64_t>(K) * 4);
+    // flag-in-data words (complete: every block arrived after its last stage)
+    const __amdgpu_buffer_rsrc_t ar = urs(P.res + lL * P.ls_hid, static_cast<int64_t>(K) * 8);
+    const __amdgpu_buffer_rsrc_t dr = urs(P.dn + (lL - 1) * P.ls_hid, static_cast<int64_t>(K) * 8);
     const __amdgpu_buffer_rsrc_t wr = urs(P.final_norm, static_cast<int64_t>(K) * 4);
 #pragma unroll
     for (int c = 0; c < 2 * HC; ++c) {
         const uint32_t col = c * 512 + lane * 8;
         const bool ok = col < static_cast<uint32_t>(K);
 #pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const u32x4 a = buf_load16(ar, ok ? col * 4 + 16u * v : kOob);
-            const u32x4 d = buf_load16(dr, ok ? col * 4 + 16u * v : kOob);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) hx[c][4 * v + j] = __uint_as_float(a[j]) + __uint_as_float(d[j]);
+        for (int v = 0; v < 4; ++v) {
+            const u32x4 a = coh_load16(ar, ok ? col * 8 + 16u * v : kOob);
+            const u32x4 d = coh_load16(dr, ok ? col * 8 + 16u * v : kOob);
+            hx[c][2 * v] = ll_f32(a[0], a[1]) + ll_f32(d[0], d[1]);
+            hx[c][2 * v + 1] = ll_f32(a[2], a[3]) + ll_f32(d[2], d[3]);
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss = fmaf(hx[c][j], hx[c][j], ss);
@@ -1094,92 +1191,84 @@ __device__ void final_argmax(const Plan &P, float *smem) {
 // ---------------------------------------------------------------------------
 // the token kernel
 // ---------------------------------------------------------------------------
-// One layer.  On entry the previous stage has arrived at barrier `target`
-// (layer 0: nothing to wait for); on exit this layer's last stage has arrived.
+// One layer: five stages whose outputs are flag-in-data words tagged with
+// the stage's epoch (ll_epoch of the running stage count `target`); each
+// stage's readers poll for their producers' epochs, so no grid barrier runs
+// inside the layer.  Every stage issues its compressed-weight loads first.
 template <int HC>
 __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t &target,
-                                         float *smem, int *sh, const float2 *rope, int wave0,
-                                         int tok) {
+                                         float *smem, const float2 *rope, int wave0, int tok) {
     const Layer &L = P.layers[l];
     Pre pf;
+    const uint32_t t0 = target;  // the previous layer's last stage (its down output)
+    const uint32_t e1 = ll_epoch(t0 + 1), e2 = ll_epoch(t0 + 2), e3 = ll_epoch(t0 + 3);
+    const uint32_t e4 = ll_epoch(t0 + 4), e5 = ll_epoch(t0 + 5);
+    target = t0 + 5;
     // Each stage starts from fresh copies of the thread / wave ids, so values
     // derived from them are recomputed per stage rather than kept live.
     int tid = fresh_v(static_cast<int>(threadIdx.x)), wave = fresh_s(wave0), lane = tid & 63;
-    // 1. r = x + delta -> xb; q/k/v = W norm(r)
+    // 1. r = x + delta -> ra; q/k/v = W norm(r)
     {
         const Geo G = geo_qkv(P, L, wave);
         prefetch(G, P.group, tid, pf);
-        if (l > 0 && !wait_all(P, target, sh)) return false;
         XSrc X{};
         X.base = P.res + static_cast<int64_t>(l) * P.ls_hid;
         X.delta = l == 0 ? nullptr : P.dn + static_cast<int64_t>(l - 1) * P.ls_hid;
         X.emb = l == 0 ? P.embed + static_cast<int64_t>(tok) * P.hidden : nullptr;
         X.w = uptr(L.in_norm);
         X.res_out = P.ra + static_cast<int64_t>(l) * P.ls_hid;
-        run_gemv<HC, XNORM, YF32>(P, G, pf, X, P.qkv + static_cast<int64_t>(l) * P.ls_qkv, smem, tid,
-                                  lane);
+        X.eb = ll_epoch(t0 - 1);  // res[l]: the previous layer's stage 4
+        X.ed = ll_epoch(t0);      // dn[l-1]: the previous layer's stage 5
+        X.eo = e1;
+        run_gemv<HC, XNORM, YF32>(P, G, pf, X, P.qkv + static_cast<int64_t>(l) * P.ls_qkv, e1, smem,
+                                  tid, lane);
     }
-    arrive(P, ++target);
     tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
     const Geo Go = geo_plain(P, L, kO, P.n_heads * kHeadDim, P.s_o, wave);
-    // 2. attention: block h waits only for the blocks that computed its q rows
-    // and its kv head's k and v rows.  Every block arrives before it issues
-    // its o-stage prefetch: arriving waits for all of the block's memory
-    // operations, and the o blocks wait for the attention blocks' flags.
+    // 2. attention (block h = query head h); the other blocks go straight on
+    // to the o stage's prefetch
     if (static_cast<int>(blockIdx.x) < P.n_heads) {
-        const int h = blockIdx.x, kvh = h / (P.n_heads / P.n_kv);
-        const uint32_t rq = P.n_heads * kHeadDim, rk = P.n_kv * kHeadDim;
-        const uint32_t nq = P.qkv_b1, nk = P.qkv_b2 - P.qkv_b1, nv = P.nblocks - P.qkv_b2;
-        const int q0 = block_of_row(rq, nq, h * kHeadDim);
-        const int q1 = block_of_row(rq, nq, (h + 1) * kHeadDim - 1) + 1;
-        const int k0 = P.qkv_b1 + block_of_row(rk, nk, kvh * kHeadDim);
-        const int k1 = P.qkv_b1 + block_of_row(rk, nk, (kvh + 1) * kHeadDim - 1) + 1;
-        const int v0 = P.qkv_b2 + block_of_row(rk, nv, kvh * kHeadDim);
-        const int v1 = P.qkv_b2 + block_of_row(rk, nv, (kvh + 1) * kHeadDim - 1) + 1;
-        if (!attention(P, L, P.qkv + static_cast<int64_t>(l) * P.ls_qkv,
-                       P.attn + static_cast<int64_t>(l) * P.ls_attn, h, pos, smem, rope,
-                       [&] { return wait_blocks(P, target, sh, q0, q1, k0, k1, v0, v1); }))
-            return false;
+        attention(P, L, P.qkv + static_cast<int64_t>(l) * P.ls_qkv, e1,
+                  P.attn + static_cast<int64_t>(l) * P.ls_attn, e2, blockIdx.x, pos, smem, rope);
+        lds_barrier();  // attention's LDS is reused by the o stage
     }
-    arrive(P, ++target);
     prefetch(Go, P.group, tid, pf);
-    if (!wait_blocks(P, target, sh, 0, P.n_heads, 0, 0, 0, 0)) return false;
     // 3. o = W_o attn
     {
         tid = fresh_v(tid), lane = tid & 63;
         XSrc X{};
         X.xb = P.attn + static_cast<int64_t>(l) * P.ls_attn;
-        run_gemv<HC, XBF16, YF32>(P, Go, pf, X, P.o + static_cast<int64_t>(l) * P.ls_hid, smem, tid,
-                                  lane);
+        X.eb = e2;
+        run_gemv<HC, XBF16, YF32>(P, Go, pf, X, P.o + static_cast<int64_t>(l) * P.ls_hid, e3, smem,
+                                  tid, lane);
     }
-    arrive(P, ++target);
     {
         tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
         const Geo Gp = geo_pair(P, L, wave);
         prefetch(Gp, P.group, tid, pf);
-        if (!wait_all(P, target, sh)) return false;
-        // 4. r = xb + o -> xa; act = silu(W_g norm(r)) * (W_u norm(r))
+        // 4. r = ra + o -> res[l+1]; act = silu(W_g norm(r)) * (W_u norm(r))
         XSrc X{};
         X.base = P.ra + static_cast<int64_t>(l) * P.ls_hid;
         X.delta = P.o + static_cast<int64_t>(l) * P.ls_hid;
         X.w = uptr(L.post_norm);
         X.res_out = P.res + static_cast<int64_t>(l + 1) * P.ls_hid;
-        run_gemv<HC, XNORM, YACT>(P, Gp, pf, X, P.act + static_cast<int64_t>(l) * P.ls_act, smem,
+        X.eb = e1;
+        X.ed = e3;
+        X.eo = e4;
+        run_gemv<HC, XNORM, YACT>(P, Gp, pf, X, P.act + static_cast<int64_t>(l) * P.ls_act, e4, smem,
                                   tid, lane);
     }
-    arrive(P, ++target);
     {
         tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
         const Geo Gd = geo_plain(P, L, kD, P.inter, P.s_down, wave);
         prefetch(Gd, P.group, tid, pf);
-        if (!wait_all(P, target, sh)) return false;
         // 5. dn = W_d act
         XSrc X{};
         X.xb = P.act + static_cast<int64_t>(l) * P.ls_act;
-        run_gemv<HC, XBF16, YF32>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid, smem, tid,
-                                  lane);
+        X.eb = e4;
+        run_gemv<HC, XBF16, YF32>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid, e5, smem,
+                                  tid, lane);
     }
-    arrive(P, ++target);
     return true;
 }
 
@@ -1209,7 +1298,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(const Plan *__restri
     if (static_cast<int>(blockIdx.x) < P.n_heads) rope_table(P, pos, rope);  // read after barriers
 #pragma clang loop unroll(disable)
     for (int l = 0; l < P.n_layers; ++l)
-        if (!do_layer<HC>(P, l, pos, target, smem, sh, rope, wave, tok)) return;
+        if (!do_layer<HC>(P, l, pos, target, smem, rope, wave, tok)) return;
+    // the last layer's outputs are complete everywhere once every block has
+    // arrived (arriving waits for the block's stores)
+    arrive(P, target);
     {
         LmPre<HC> lpf;
         const int b = blockIdx.x, nb = P.nblocks;
@@ -1238,7 +1330,7 @@ __global__ void clear_sync_kernel(uint32_t *flags, int32_t n, uint32_t *release,
 // ---------------------------------------------------------------------------
 struct Layout {
     int64_t plan, layers, res, ra, qkv, o, dn, part_v, part_i, attn, act, flags, release, err, total;
-    int32_t s_hid, s_qkv, s_attn, s_act;  // slot strides in elements (256-byte multiples)
+    int32_t s_hid, s_qkv, s_attn, s_act;  // slot strides in 32-bit words (256-byte multiples)
 };
 
 static int64_t align256(int64_t v) { return (v + 255) & ~int64_t{255}; }
@@ -1248,10 +1340,11 @@ static Layout layout_of(const hxq_decoder *d, int nb) {
     int64_t off = 0;
     auto take = [&](int64_t bytes) { const int64_t o = off; off = align256(off + bytes); return o; };
     const int64_t nl = d->n_layers;
-    L.s_hid = static_cast<int32_t>(align256(4LL * d->hidden) / 4);
-    L.s_qkv = static_cast<int32_t>(align256(4LL * (d->n_heads + 2 * d->n_kv_heads) * kHeadDim) / 4);
-    L.s_attn = static_cast<int32_t>(align256(2LL * d->n_heads * kHeadDim) / 2);
-    L.s_act = static_cast<int32_t>(align256(2LL * d->intermediate) / 2);
+    // slots in flag-in-data words: fp32 values two words, bf16 values one
+    L.s_hid = static_cast<int32_t>(align256(8LL * d->hidden) / 4);
+    L.s_qkv = static_cast<int32_t>(align256(8LL * (d->n_heads + 2 * d->n_kv_heads) * kHeadDim) / 4);
+    L.s_attn = static_cast<int32_t>(align256(4LL * d->n_heads * kHeadDim) / 4);
+    L.s_act = static_cast<int32_t>(align256(4LL * d->intermediate) / 4);
     L.plan = take(sizeof(Plan));
     L.layers = take(static_cast<int64_t>(sizeof(Layer)) * nl);
     L.res = take(4LL * L.s_hid * (nl + 1));
@@ -1261,8 +1354,8 @@ static Layout layout_of(const hxq_decoder *d, int nb) {
     L.dn = take(4LL * L.s_hid * nl);
     L.part_v = take(4LL * nb);
     L.part_i = take(4LL * nb);
-    L.attn = take(2LL * L.s_attn * nl);
-    L.act = take(2LL * L.s_act * nl);
+    L.attn = take(4LL * L.s_attn * nl);
+    L.act = take(4LL * L.s_act * nl);
     L.flags = take(4LL * nb);
     L.release = take(256);
     L.err = take(256);
@@ -1440,15 +1533,15 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     P.pos = d->pos;
     P.logits = d->logits;
     P.layers = reinterpret_cast<const Layer *>(ws + lay.layers);
-    P.res = reinterpret_cast<float *>(ws + lay.res);
-    P.ra = reinterpret_cast<float *>(ws + lay.ra);
-    P.qkv = reinterpret_cast<float *>(ws + lay.qkv);
-    P.o = reinterpret_cast<float *>(ws + lay.o);
-    P.dn = reinterpret_cast<float *>(ws + lay.dn);
+    P.res = reinterpret_cast<uint32_t *>(ws + lay.res);
+    P.ra = reinterpret_cast<uint32_t *>(ws + lay.ra);
+    P.qkv = reinterpret_cast<uint32_t *>(ws + lay.qkv);
+    P.o = reinterpret_cast<uint32_t *>(ws + lay.o);
+    P.dn = reinterpret_cast<uint32_t *>(ws + lay.dn);
     P.part_v = reinterpret_cast<float *>(ws + lay.part_v);
     P.part_i = reinterpret_cast<int32_t *>(ws + lay.part_i);
-    P.attn = reinterpret_cast<uint16_t *>(ws + lay.attn);
-    P.act = reinterpret_cast<uint16_t *>(ws + lay.act);
+    P.attn = reinterpret_cast<uint32_t *>(ws + lay.attn);
+    P.act = reinterpret_cast<uint32_t *>(ws + lay.act);
     P.ls_hid = lay.s_hid;
     P.ls_qkv = lay.s_qkv;
     P.ls_attn = lay.s_attn;
