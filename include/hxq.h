@@ -456,8 +456,10 @@ int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capac
 
 /*
  * Whole greedy decode step in ONE launch per token (persistent kernel, one
- * 16-wave block per compute unit, grid barriers between the stages; the
- * next stage's compressed weights are fetched while the grid synchronises).
+ * 16-wave block per compute unit; inside a layer the stages exchange
+ * activations as epoch-tagged words that consumers poll, with each stage's
+ * compressed weights fetched before it waits; a grid barrier only before the
+ * LM head and the argmax).
  * Per layer: r = x + delta, q/k/v = W norm(r) (+bias); RoPE, KV append and
  * GQA attention; o = W_o attn; r' = r + o, act = silu(W_g norm(r')) *
  * (W_u norm(r')); delta = W_d act.  Then logits = E norm(x + delta) (tied
@@ -476,8 +478,8 @@ int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capac
  * hxq_decoder_init copies the layer table into `workspace` (device, 256-byte
  * aligned, >= hxq_decoder_workspace_bytes) and clears the barrier state;
  * hxq_decoder_step runs n_steps tokens (n_steps launches, no host sync);
- * hxq_decoder_error copies the barrier error word (0 = fine; 1 = a grid
- * barrier timed out; 2 = token/position out of range) to *err_out and
+ * hxq_decoder_error copies the barrier error word (0 = fine; 1 = a wait
+ * for other blocks timed out; 2 = token/position out of range) to *err_out and
  * synchronises the stream.  A workspace serves one stream at a time.
  */
 typedef struct hxq_decoder_layer {
