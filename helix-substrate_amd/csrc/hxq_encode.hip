@@ -329,21 +329,50 @@ __device__ float pairwise_leaf(const float *a, int n) {
     return res;
 }
 
-// pairwise sum of n <= 8192 elements (split at n/2 rounded down to a
-// multiple of 8 until <= 128), evaluated with an explicit stack
-__device__ float pairwise_sum(const float *a, int n) {
+// Leaves of numpy's pairwise tree over n <= 8192 elements, left to right:
+// ranges of <= 128 elements (nodes above 128 split at n/2 rounded down to a
+// multiple of 8, so every leaf has at least 64 elements: at most 128 leaves).
+__device__ int pairwise_leaves(int n, int *loff, int *llen) {
+    int so[16], sl[16];
+    int sp = 1, nl = 0;
+    so[0] = 0;
+    sl[0] = n;
+    while (sp > 0) {
+        --sp;
+        const int o = so[sp], m = sl[sp];
+        if (m <= 128) {
+            loff[nl] = o;
+            llen[nl] = m;
+            ++nl;
+            continue;
+        }
+        int m2 = m / 2;
+        m2 -= m2 % 8;
+        so[sp] = o + m2;  // right, visited after the left subtree
+        sl[sp] = m - m2;
+        ++sp;
+        so[sp] = o;
+        sl[sp] = m2;
+        ++sp;
+    }
+    return nl;
+}
+
+// pairwise_sum with the leaf sums given (in leaf order): the same tree and
+// the same additions
+__device__ float pairwise_combine(int n, const float *lsum) {
 #pragma clang fp contract(off)
-    if (n <= 128) return pairwise_leaf(a, n);
-    // frames: offset, length, state (0: visit left, 1: visit right, 2: combine)
-    int off[16], len[16], st[16];
+    if (n <= 128) return lsum[0];
+    int len[16], st[16];
     float left[16];
-    int sp = 0;
-    off[0] = 0; len[0] = n; st[0] = 0;
+    int sp = 0, li = 0;
+    len[0] = n;
+    st[0] = 0;
     float ret = 0.f;
     while (sp >= 0) {
         const int m = len[sp];
         if (m <= 128) {
-            ret = pairwise_leaf(a + off[sp], m);
+            ret = lsum[li++];
             --sp;
             continue;
         }
@@ -351,11 +380,11 @@ __device__ float pairwise_sum(const float *a, int n) {
         m2 -= m2 % 8;
         if (st[sp] == 0) {
             st[sp] = 1;
-            ++sp; off[sp] = off[sp - 1]; len[sp] = m2; st[sp] = 0;
+            ++sp; len[sp] = m2; st[sp] = 0;
         } else if (st[sp] == 1) {
             left[sp] = ret;
             st[sp] = 2;
-            ++sp; off[sp] = off[sp - 1] + m2; len[sp] = m - m2; st[sp] = 0;
+            ++sp; len[sp] = m - m2; st[sp] = 0;
         } else {
             ret = left[sp] + ret;
             --sp;
@@ -364,29 +393,54 @@ __device__ float pairwise_sum(const float *a, int n) {
     return ret;
 }
 
-// Lloyd step 4: means, movement, convergence.  One thread per cluster.
-__global__ __launch_bounds__(kMaxK) void km_update_kernel(const float *sorted_vals, const int32_t *starts,
-                                 const int32_t *counts, int k, float *cb, const double *abs_tol,
-                                 int32_t *done, int32_t *iters) {
+// Lloyd step 4a: cluster means, one block per cluster: per 8192-element
+// block of the cluster's members, thread 0 lists the pairwise leaves, the
+// threads sum one leaf each, thread 0 combines them in tree order; block sums
+// are added in order and divided by the count (numpy's np.mean, bit for bit).
+// Empty clusters keep their centroid.
+__global__ __launch_bounds__(kThreads) void km_sum_kernel(const float *sorted_vals, const int32_t *starts,
+                                                          const int32_t *counts, const float *cb,
+                                                          float *means, const int32_t *done) {
+#pragma clang fp contract(off)
+    if (*done) return;
+    __shared__ int loff[128], llen[128];
+    __shared__ float lsum[128];
+    __shared__ int s_nl;
+    const int j = blockIdx.x;
+    const int32_t c = counts[j];
+    if (c == 0) {
+        if (threadIdx.x == 0) means[j] = cb[j];
+        return;
+    }
+    const float *a = sorted_vals + starts[j];
+    float sum = 0.f;
+    for (int32_t s = 0; s < c; s += 8192) {
+        const int m = min(8192, c - s);
+        if (threadIdx.x == 0) s_nl = pairwise_leaves(m, loff, llen);
+        __syncthreads();
+        const int nl = s_nl;
+        for (int i = threadIdx.x; i < nl; i += kThreads) lsum[i] = pairwise_leaf(a + s + loff[i], llen[i]);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const float p = pairwise_combine(m, lsum);
+            sum = s == 0 ? p : sum + p;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) means[j] = sum / static_cast<float>(c);
+}
+
+// Lloyd step 4b: movement and convergence over the k new means.
+__global__ __launch_bounds__(kMaxK) void km_update_kernel(const float *means, int k, float *cb,
+                                                          const double *abs_tol, int32_t *done,
+                                                          int32_t *iters) {
 #pragma clang fp contract(off)
     if (*done) return;
     __shared__ float s_new[kMaxK];
     __shared__ float s_delta[kMaxK];
     const int j = threadIdx.x;
     if (j < k) {
-        const int32_t c = counts[j];
-        float v = cb[j];
-        if (c > 0) {
-            const float *a = sorted_vals + starts[j];
-            float sum = 0.f;
-            bool first = true;
-            for (int32_t s = 0; s < c; s += 8192) {
-                const float p = pairwise_sum(a + s, min(8192, c - s));
-                sum = first ? p : sum + p;
-                first = false;
-            }
-            v = sum / static_cast<float>(c);
-        }
+        const float v = means[j];
         s_new[j] = v;
         s_delta[j] = fabsf(v - cb[j]);
     }
@@ -665,14 +719,15 @@ static int64_t align256(int64_t b) { return (b + 255) & ~int64_t{255}; }
 // values, per-block counts / offsets, then starts, counts and the fp64
 // tolerance + done flag
 struct KmLayout {
-    int64_t vals, blk, starts, counts, tol, done, total;
+    int64_t vals, blk, starts, counts, means, tol, done, total;
     explicit KmLayout(int64_t n) {
         const int64_t nblk = (n + 4095) / 4096;
         vals = align256(4 * next_pow2(n));
         blk = vals + align256(4 * n);
         starts = blk + align256(4 * nblk * kMaxK);
         counts = starts + 4 * kMaxK;
-        tol = counts + 4 * kMaxK;
+        means = counts + 4 * kMaxK;
+        tol = means + 4 * kMaxK;
         done = tol + 8;
         total = align256(done + 8);
     }
@@ -716,6 +771,7 @@ extern "C" int hxq_kmeans_run(const float *x, int64_t n, const double *percentil
     int32_t *blk = reinterpret_cast<int32_t *>(ws + lay.blk);
     int32_t *starts = reinterpret_cast<int32_t *>(ws + lay.starts);
     int32_t *counts = reinterpret_cast<int32_t *>(ws + lay.counts);
+    float *means = reinterpret_cast<float *>(ws + lay.means);
     double *abs_tol = reinterpret_cast<double *>(ws + lay.tol);
     int32_t *done = reinterpret_cast<int32_t *>(ws + lay.done);
     hipLaunchKernelGGL(kmeans_init_kernel, dim3(1), dim3(kMaxK), 0, stream, keys, n, percentiles01,
@@ -732,8 +788,11 @@ extern "C" int hxq_kmeans_run(const float *x, int64_t n, const double *percentil
         hipLaunchKernelGGL(km_scatter_kernel, dim3(static_cast<uint32_t>(nblk)), dim3(kThreads), 0,
                            stream, x, n, per, assignments, blk, starts, k, vals, done);
         HXQ_LAUNCH_CHECK();
-        hipLaunchKernelGGL(km_update_kernel, dim3(1), dim3(kMaxK), 0, stream, vals, starts, counts,
-                           k, codebook, abs_tol, done, iters);
+        hipLaunchKernelGGL(km_sum_kernel, dim3(k), dim3(kThreads), 0, stream, vals, starts, counts,
+                           codebook, means, done);
+        HXQ_LAUNCH_CHECK();
+        hipLaunchKernelGGL(km_update_kernel, dim3(1), dim3(kMaxK), 0, stream, means, k, codebook,
+                           abs_tol, done, iters);
         HXQ_LAUNCH_CHECK();
     }
     return HXQ_OK;

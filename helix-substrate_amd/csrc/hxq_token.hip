@@ -61,7 +61,10 @@ constexpr int kRedCap = 512;                  // row x slice partials per segmen
 constexpr int kEnt = 512;                     // sidecar entries per segment staged in LDS
 constexpr int kRps = 1028;                    // CSR row pointers per segment staged in LDS
 constexpr int kHeadDim = 128;
+constexpr int kVStage = 3584;                  // float offset of attention's staged V rows in LDS
 constexpr int kMaxSeq = 1024;
+static_assert(kMaxSeq + 3 * kHeadDim + kWaves * kHeadDim + kWaves + 1 <= kVStage,
+              "attention scratch overlaps the staged V rows");
 constexpr int kLmRB = 1;                      // LM-head rows per load batch
 constexpr uint32_t kOob = 0x80000000u;        // buffer offset past any range: reads 0
 constexpr int kCoh = 16;                      // cache policy sc1: coherent across XCDs
@@ -824,9 +827,9 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float block_max(float v, float *red) {
     v = wave_max_all(v);
-    __syncthreads();
+    lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
-    __syncthreads();
+    lds_barrier();
     float t = -FLT_MAX;
     for (int i = 0; i < kWaves; ++i) t = fmaxf(t, red[i]);
     return t;
@@ -834,9 +837,9 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum_all(v);
-    __syncthreads();
+    lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
-    __syncthreads();
+    lds_barrier();
     float t = 0.f;
     for (int i = 0; i < kWaves; ++i) t += red[i];
     return t;
@@ -881,6 +884,7 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     float *vn = kn + D;                   // [D]
     float *part = vn + D;                 // [kWaves][D]
     float *red = part + kWaves * D;       // [kWaves]
+    float *spos = red + kWaves;           // [1] score of position pos
     const int grp = P.n_heads / P.n_kv;
     const int kvh = h / grp;
     const int n = pos + 1;
@@ -905,6 +909,24 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         const int tt = wave + u * kWaves;
         vw[u] = __builtin_amdgcn_raw_buffer_load_b32(
             vr, tt < pos ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
+    }
+    // V rows of positions [8 * kWaves, vend) go straight to LDS (buffer loads
+    // into LDS: no registers), four 256-byte rows per wave instruction, into
+    // the LDS the GEMV stages use for tables (free during attention); later
+    // positions are read from memory in the accumulation loop.
+    uint32_t *vst = reinterpret_cast<uint32_t *>(smem + kVStage);
+    const int vcap = ((P.lds_red - kVStage) / (D / 2)) & ~3;  // whole 4-row instructions fit
+    const int vbeg = 8 * kWaves;
+    const int vend = pos > vbeg ? min(pos, vbeg + vcap) : vbeg;
+    for (int q = wave; 4 * q < vend - vbeg; q += kWaves) {
+        const int r = vbeg + 4 * q + lane / 16;
+        const uint32_t go = r < vend ? static_cast<uint32_t>((static_cast<int64_t>(r) * row +
+                                                               static_cast<int64_t>(kvh) * D) * 2) +
+                                           16u * static_cast<uint32_t>(lane % 16)
+                                     : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            vr, (__attribute__((address_space(3))) void *)(vst + 4 * q * (D / 2)), 16,
+            go, 0, 0, 0);
     }
     // this token's q, k, v (flag-in-data words of the q/k/v stage, epoch eq):
     // threads [0, D/2) take q[t], q[t + D/2], k[t], k[t + D/2]; threads
@@ -945,12 +967,13 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     }
     const bool writer = h % grp == 0;
     const float scale = rsqrtf(static_cast<float>(D));
-    if (t < D / 2) {
+    if (t < D / 2) {  // wave 0
         const float2 cs = rope[t];
         float a, b;
         rope_rot(qv0, qv1, cs, a, b);
-        qs[t] = a * scale;
-        qs[t + D / 2] = b * scale;
+        const float q0 = a * scale, q1 = b * scale;
+        qs[t] = q0;
+        qs[t + D / 2] = q1;
         rope_rot(kv0, kv1, cs, a, b);
         const int64_t base = static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D;
         if (writer) {
@@ -959,21 +982,21 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         }
         kn[t] = bf16r(a);
         kn[t + D / 2] = bf16r(b);
+        // this position's score, reduced across the wave
+        const float sp = wave_sum_all(fmaf(q0, bf16r(a), q1 * bf16r(b)));
+        if (t == 0) *spos = sp;
     } else if (t < D / 2 + D) {
         const int j = t - D / 2;
         const float v = vv;
         if (writer) L.vc[static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D + j] = f32_to_bf16(v);
         vn[j] = bf16r(v);
     }
-    __syncthreads();
+    lds_barrier();  // LDS only: the cache stores are read by later launches
     float mx = -FLT_MAX;
     if (t < n) {  // n <= max_seq <= kThreads: one position per thread
         float s0 = 0.f, s1 = 0.f;
         if (t == pos) {
-            for (int d = 0; d < D; d += 2) {
-                s0 = fmaf(qs[d], kn[d], s0);
-                s1 = fmaf(qs[d + 1], kn[d + 1], s1);
-            }
+            s0 = *spos;
         } else {
 #pragma unroll
             for (int c = 0; c < D / 8; ++c)
@@ -1011,8 +1034,12 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         for (int u = 0; u < 8; ++u) {
             const int tt = t0 + u * kWaves;
             const bool ok = tt < pos;
-            w[u] = __builtin_amdgcn_raw_buffer_load_b32(
-                vr, ok ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
+            if (tt < vend) {
+                w[u] = vst[(tt - vbeg) * (D / 2) + lane];
+            } else {
+                w[u] = __builtin_amdgcn_raw_buffer_load_b32(
+                    vr, ok ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
+            }
             p[u] = ok ? sc[tt] : 0.f;
         }
 #pragma unroll
@@ -1027,7 +1054,7 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     }
     part[wave * D + 2 * lane] = a0;
     part[wave * D + 2 * lane + 1] = a1;
-    __syncthreads();
+    lds_barrier();
     if (t < D / 2) {
         const int d = 2 * t;
         float v0 = 0.f, v1 = 0.f;
