@@ -68,6 +68,7 @@ static_assert(kMaxSeq + 3 * kHeadDim + kWaves * kHeadDim + kWaves + 1 <= kVStage
 constexpr int kLmRB = 1;                      // LM-head rows per load batch
 constexpr uint32_t kOob = 0x80000000u;        // buffer offset past any range: reads 0
 constexpr int kCoh = 16;                      // cache policy sc1: coherent across XCDs
+constexpr int kVmcnt0 = 0x0F70;               // s_waitcnt vmcnt(0) (expcnt, lgkmcnt untouched)
 constexpr uint64_t kTimeoutTicks = 100000000ull;  // 1 s of the 100 MHz wall clock
 
 enum { kQ = 0, kK = 1, kV = 2, kO = 3, kG = 4, kU = 5, kD = 6 };
@@ -597,6 +598,10 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             const uint32_t o8 = mine ? static_cast<uint32_t>(t) * 32u : kOob;
             const bool has_d = X.delta != nullptr;
             u32x4 a0, a1, d0, d1;
+            // loads return in order: a poll issued now would come back only
+            // after the prefetched batch, with data sampled now -- so wait
+            // for the batch first and sample later
+            __builtin_amdgcn_s_waitcnt(kVmcnt0);
             const uint64_t t0 = wall_clock64();
             for (int it = 1;; ++it) {
                 a0 = coh_load16(br, o8);
@@ -650,6 +655,7 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
         bool have[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) have[j] = (t + j * kThreads) * 8 < K;
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);  // sample after the prefetched batch (see above)
         const uint64_t t0 = wall_clock64();
         for (int it = 1;; ++it) {
             bool ok = true;
@@ -943,6 +949,7 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         const uint32_t o2 = qk ? static_cast<uint32_t>(ke + t) * 8u : kOob;
         const uint32_t o3 = qk ? static_cast<uint32_t>(ke + t + D / 2) * 8u : kOob;
         uint2 w0, w1, w2, w3;
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);  // sample after the K/V preloads land
         const uint64_t t0 = wall_clock64();
         for (int it = 1;; ++it) {
             w0 = coh_load8(qr, o0);
