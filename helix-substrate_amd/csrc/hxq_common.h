@@ -129,21 +129,30 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Codebook lookup of byte B (0..3) of the packed index word w.
+typedef __attribute__((address_space(3))) const float lds_cfloat;
+
+// LDS byte address of a pointer into LDS.
+__device__ __forceinline__ uint32_t lds_offset_of(const float *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cfloat *)p));
+}
+
+// Codebook lookup of byte B (0..3) of the packed index word w in a table
+// that starts at LDS address 0 (the caller checks lds_offset_of(table) == 0).
 //   NREP == 64: entry stride is 256 bytes and the lane's replica offset
 //   (lane*4 < 256) fits in the low byte, so the LDS byte address is
-//   {0, 0, w.byte[B], lane_off} -- one v_perm_b32 builds it.
+//   {0, 0, w.byte[B], lane_off} -- one v_perm_b32 builds it, and the load
+//   goes straight to that address (no base add).
 //   NREP == 32: shift/mask arithmetic.
 template <int NREP, int B>
-__device__ __forceinline__ float tbl_lookup(const float *tbl, uint32_t lane_off, uint32_t w) {
+__device__ __forceinline__ float tbl_lookup0(uint32_t lane_off, uint32_t w) {
+    uint32_t addr;
     if constexpr (NREP == 64) {
         constexpr uint32_t sel = (12u << 24) | (12u << 16) | (static_cast<uint32_t>(B) << 8) | 4u;
-        const uint32_t addr = __builtin_amdgcn_perm(lane_off, w, sel);
-        return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(tbl) + addr);
+        addr = __builtin_amdgcn_perm(lane_off, w, sel);
     } else {
-        const uint32_t addr = ((w >> (8 * B)) & 0xffu) * (NREP * 4) + lane_off;
-        return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(tbl) + addr);
+        addr = ((w >> (8 * B)) & 0xffu) * (NREP * 4) + lane_off;
     }
+    return *reinterpret_cast<lds_cfloat *>(static_cast<uintptr_t>(addr));
 }
 
 // Wave64 sum via DPP; the total lands in lane 63.

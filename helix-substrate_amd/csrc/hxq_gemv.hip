@@ -47,6 +47,8 @@ struct GemvMat {
     void *y;
     int64_t out;
     int64_t ncodes;  // codebook entries (formats with a pair codebook)
+    int32_t rpb;     // rows per block (set by the launch plan)
+    int32_t pad_;
 };
 
 struct GemvMats {
@@ -215,11 +217,14 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int RG = WAVES / S;
-    const int s_id = wave % S;
-    const int rg = wave / S;
-    const int c_lo = s_id * nchunks / S;
-    const int nc = (s_id + 1) * nchunks / S - c_lo;  // chunks of this slice (<= CPS)
+    // S and RG = WAVES / S are powers of two: shifts, not divisions
+    const int lg_s = __builtin_ctz(static_cast<uint32_t>(S));
+    const int RG = WAVES >> lg_s;
+    const int lg_rg = __builtin_ctz(static_cast<uint32_t>(RG));
+    const int s_id = wave & (S - 1);
+    const int rg = wave >> lg_s;
+    const int c_lo = (s_id * nchunks) >> lg_s;
+    const int nc = (((s_id + 1) * nchunks) >> lg_s) - c_lo;  // chunks of this slice (<= CPS)
     const uint32_t lane_off = static_cast<uint32_t>(lane % NREP) * 4u;
     uint32_t koff[CPS];
     bool kok[CPS];
@@ -230,16 +235,21 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
         koff[ci] = static_cast<uint32_t>(k0);
     }
 
-    // rows of this block
+    // rows of this block: [lo, lo + n_rows), rpb rows per block (the last may have fewer)
     const int64_t out = M.out;
-    const int32_t b_hi = mi == 0 ? bb1 : mi == 1 ? bb2 : mi == 2 ? bb3 : mi == 3 ? bb4 : mi == 4 ? bb5
-                       : mi == 5 ? bb6 : mi == 6 ? bb7 : static_cast<int32_t>(gridDim.x);
-    const int64_t nblk = b_hi - b_lo, lb = bid - b_lo;
-    const int64_t lo = out * lb / nblk;
-    const int64_t n_rows = out * (lb + 1) / nblk - lo;
+    const int32_t rpb = M.rpb;
+    const int64_t lo = static_cast<int64_t>(bid - b_lo) * rpb;
+    const int32_t n_rows = static_cast<int32_t>(min(static_cast<int64_t>(rpb), out - lo));
     const int64_t ngroups = AFFINE ? K / group : 0;
-    const int64_t n_mine = n_rows > rg ? (n_rows - rg + RG - 1) / RG : 0;
+    const int32_t n_mine = n_rows > rg ? (n_rows - rg + RG - 1) >> lg_rg : 0;
     const bool has_sc = M.rp != nullptr;
+    if (lds_offset_of(smem) != 0) {
+        // the lookups address the table from LDS 0 (no static LDS in this kernel):
+        // never taken, but poison the outputs rather than read a wrong table
+        if (threadIdx.x < n_rows * NX)
+            store_y(M.y, (threadIdx.x % NX) * out + lo + threadIdx.x / NX, y_dtype, __builtin_nanf(""));
+        return;
+    }
 
     // ---- prologue: issue everything, wait later
     constexpr int XV = XF32 ? 4 : 2;  // 16-byte loads per 16 activations
@@ -295,7 +305,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(M.idx, out * row_bytes);
     const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(M.gs, AFFINE ? out * ngroups * 4 : 0);
     const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(M.go, AFFINE ? out * ngroups * 4 : 0);
-    auto load_item = [&](int64_t i, GemvItem<CPS> &it) {
+    auto load_item = [&](int32_t i, GemvItem<CPS> &it) {
         const bool mine = i < n_mine;
         const uint32_t row = static_cast<uint32_t>(lo + rg + i * RG);
 #pragma unroll
@@ -446,7 +456,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const float sc_dl0 = buf_loadf(dl_r, e0);
 
     // ---- stream
-    auto compute_item = [&](int64_t i, const GemvItem<CPS> &itm) {
+    auto compute_item = [&](int32_t i, const GemvItem<CPS> &itm) {
         float acc[NX];
 #pragma unroll
         for (int n = 0; n < NX; ++n) acc[n] = 0.f;
@@ -459,10 +469,10 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
                     const uint32_t w = itm.q[ci][d];
-                    const float c0 = tbl_lookup<NREP, 0>(tbl, lane_off, w);
-                    const float c1 = tbl_lookup<NREP, 1>(tbl, lane_off, w);
-                    const float c2 = tbl_lookup<NREP, 2>(tbl, lane_off, w);
-                    const float c3 = tbl_lookup<NREP, 3>(tbl, lane_off, w);
+                    const float c0 = tbl_lookup0<NREP, 0>(lane_off, w);
+                    const float c1 = tbl_lookup0<NREP, 1>(lane_off, w);
+                    const float c2 = tbl_lookup0<NREP, 2>(lane_off, w);
+                    const float c3 = tbl_lookup0<NREP, 3>(lane_off, w);
 #pragma unroll
                     for (int n = 0; n < NX; ++n) {
                         part[n] = fmaf(xv[ci][n][4 * d + 0], c0, part[n]);
@@ -501,7 +511,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
                 acc[n] = fmaf(itm.of[ci], xs[ci][n], acc[n]);
             }
         }
-        const int64_t rl = rg + i * RG;  // row within the block's range
+        const int32_t rl = rg + i * RG;  // row within the block's range
 #pragma unroll
         for (int n = 0; n < NX; ++n) {
             const float v = wave_sum_lane63(acc[n]);
@@ -511,7 +521,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     // double-buffered batches: the next batch's loads are issued before the
     // current batch is computed (it2 is the second buffer)
     GemvItem<CPS> it2[RB];
-    for (int64_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
+    for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
 #pragma unroll
         for (int b = 0; b < RB; ++b) load_item(i0 + RB + b, it2[b]);
         __builtin_amdgcn_sched_barrier(0);
@@ -602,7 +612,7 @@ struct GemvPlan {
 };
 
 // Chunks per slice, K slices, and the block partition over matrices.
-static int plan_gemv(GemvHeader &h, const GemvMats &mats, int n_x, GemvPlan &pl) {
+static int plan_gemv(GemvHeader &h, GemvMats &mats, int n_x, GemvPlan &pl) {
     pl.CPS = 1;
     if (n_x == 1) {
         while (pl.CPS < 4 && pl.CPS * kWaves < h.nchunks) pl.CPS *= 2;
@@ -620,10 +630,14 @@ static int plan_gemv(GemvHeader &h, const GemvMats &mats, int n_x, GemvPlan &pl)
         int64_t nb = std::max<int64_t>(1, (target * out + total - 1) / total);
         nb = std::max<int64_t>(nb, (out + max_rows - 1) / max_rows);
         nb = std::min<int64_t>(nb, out);
+        // equal runs of rpb rows; the last block of the matrix takes the rest
+        const int64_t rpb = (out + nb - 1) / nb;
+        nb = (out + rpb - 1) / rpb;
+        mats.m[m].rpb = static_cast<int32_t>(rpb);
         grid += nb;
         HXQ_REQUIRE(grid < (int64_t{1} << 30), "too many GEMV blocks");
         h.bb[m] = static_cast<int32_t>(grid);
-        rows_pb = std::max<int64_t>(rows_pb, (out + nb - 1) / nb);
+        rows_pb = std::max<int64_t>(rows_pb, rpb);
     }
     for (int m = h.n_mats; m < HXQ_MAX_MULTI; ++m) h.bb[m] = INT32_MAX;
     pl.grid = static_cast<int>(grid);
@@ -682,7 +696,7 @@ static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipSt
 }
 
 template <int XM = 0, int FMT = HXQ_FMT_SCALAR>
-static int gemv_run(GemvHeader &h, const GemvMats &mats, int n_x, hipStream_t stream,
+static int gemv_run(GemvHeader &h, GemvMats &mats, int n_x, hipStream_t stream,
                     const GemvPro &pro = GemvPro{}) {
     h.fmt = FMT;
     GemvPlan pl{};

@@ -509,18 +509,11 @@ __device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, P
 // at t * 65536 bytes, entry j replica r at byte 256 j + 4 r.  One v_perm
 // builds the whole byte address {0, t, w.byte[B], 4 * lane} from
 // lane_seg = (t << 16) | (4 * lane).
-typedef __attribute__((address_space(3))) const float lds_cfloat;
-
 template <int B>
 __device__ __forceinline__ float tok_lookup(uint32_t lane_seg, uint32_t w) {
     constexpr uint32_t sel = (12u << 24) | (6u << 16) | (static_cast<uint32_t>(B) << 8) | 4u;
     const uint32_t addr = __builtin_amdgcn_perm(lane_seg, w, sel);
     return *reinterpret_cast<lds_cfloat *>(static_cast<uintptr_t>(addr));
-}
-
-__device__ __forceinline__ uint32_t lds_offset_of(const float *p) {
-    return static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const float *)p));
 }
 
 __device__ __forceinline__ float row_dot(uint32_t lane_seg, const Batch &b, int r,
