@@ -86,7 +86,7 @@ def build_layers(n_layers, dev, names=None):
 
 
 def mat_desc(m):
-    return dict(indices=m.indices, codebook=m.codebook, group_scale=m.group_scale,
+    return dict(indices=m.indices, codebook=m._kcb, group_scale=m.group_scale,
                 group_offset=m.group_offset, sc_row_ptr=m._sc_row_ptr, sc_col=m._sc_col,
                 sc_delta=m._sc_delta, bias=m.bias)
 
@@ -125,13 +125,13 @@ def main():
             _hxq.gemv_multi(x_attn, [d["q"], d["k"], d["v"]], 128, outs=[o["q"], o["k"], o["v"]])
         if which in (None, "o"):
             m = layers[li]["o"]
-            _hxq.gemv(x_o, m.indices, m.codebook, m.group_scale, m.group_offset, 128,
+            _hxq.gemv(x_o, m.indices, m._kcb, m.group_scale, m.group_offset, 128,
                       m._sc_row_ptr, m._sc_col, m._sc_delta, m.bias, out=o["o"])
         if which in (None, "gateup"):
             _hxq.gemv_multi(x_mlp, [d["gate"], d["up"]], 128, outs=[o["gate"], o["up"]])
         if which in (None, "down"):
             m = layers[li]["down"]
-            _hxq.gemv(x_down, m.indices, m.codebook, m.group_scale, m.group_offset, 128,
+            _hxq.gemv(x_down, m.indices, m._kcb, m.group_scale, m.group_offset, 128,
                       m._sc_row_ptr, m._sc_col, m._sc_delta, m.bias, out=o["down"])
 
     def step():

@@ -184,6 +184,14 @@ def _need_device(*ts):
     return dev
 
 
+def _need_cb256(cb):
+    """Scalar-codebook kernels read all 256 entries (uint8 indices): shorter
+    codebooks must be padded by the caller (HelixLinear keeps a padded copy)."""
+    if cb is None or cb.dtype != torch.float32 or cb.numel() < 256:
+        raise ValueError("scalar-codebook kernels take an fp32 codebook of 256 entries "
+                         "(pad shorter codebooks; HelixLinear._kcb is the padded copy)")
+
+
 def dtype_code(dt: torch.dtype) -> int:
     try:
         return _DTYPE_CODE[dt]
@@ -203,6 +211,7 @@ def dequant_f32(indices, codebook, group_scale, group_offset, group_size,
     if out is None:
         out = torch.empty(row_end - row_begin, in_f, dtype=torch.float32, device=indices.device)
     _need_device(indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val, out)
+    _need_cb256(codebook)
     rc = lib().hxq_dequant_f32(_ptr(indices), _ptr(codebook), _ptr(group_scale), _ptr(group_offset),
                                int(group_size), _ptr(sc_row_ptr), _ptr(sc_col), _ptr(sc_val),
                                out_f, in_f, int(row_begin), int(row_end), _ptr(out),
@@ -222,6 +231,7 @@ def gemv(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr
         out = torch.empty(n, out_f, dtype=out_dtype, device=x.device)
     _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_delta,
                  bias, out)
+    _need_cb256(codebook)
     rc = lib().hxq_gemv(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
                         _ptr(group_scale), _ptr(group_offset), int(group_size), _ptr(sc_row_ptr),
                         _ptr(sc_col), _ptr(sc_delta), _ptr(bias), _ptr(out),
@@ -282,6 +292,7 @@ def _mat_array(x, mats, outs, out_dtype):
     for i, (m, y) in enumerate(zip(mats, outs)):
         _need_device(x, m["indices"], m["codebook"], m.get("group_scale"), m.get("group_offset"),
                      m.get("sc_row_ptr"), m.get("sc_col"), m.get("sc_delta"), m.get("bias"), y)
+        _need_cb256(m["codebook"])
         arr[i] = HxqMatrix(m["indices"].data_ptr(), m["codebook"].data_ptr(),
                            *(0 if m.get(k) is None else m[k].data_ptr()
                              for k in ("group_scale", "group_offset", "sc_row_ptr", "sc_col",
@@ -353,6 +364,7 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
     if out is None:
         out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
     _need_device(x, indices, codebook, group_affine, sc_row_ptr, sc_col, sc_val, bias, out)
+    _need_cb256(codebook)
     rc = lib().hxq_gemm(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
                         _ptr(group_affine), int(group_size), _ptr(sc_row_ptr), _ptr(sc_col),
                         _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype), m, out_f, in_f,
@@ -445,6 +457,8 @@ def moe_route(logits, top_k, renormalize=False):
 def _bank(b):
     _need_device(b["indices"], b["codebook"], b.get("group_affine"), b.get("sc_row_ptr"),
                  b.get("sc_col"), b.get("sc_val"))
+    if b["codebook"].dtype != torch.float32 or b["codebook"].shape[-1] != 256:
+        raise ValueError("expert banks take fp32 codebooks [E, 256]")
     return HxqExpertBank(*(0 if b.get(k) is None else b[k].data_ptr()
                            for k in ("indices", "codebook", "group_affine", "sc_row_ptr",
                                      "sc_col", "sc_val")))
@@ -628,9 +642,10 @@ def hxq_matrix_of(m):
     """hxq_matrix of a HelixLinear (y unused)."""
     def p(t):
         return 0 if t is None else t.data_ptr()
-    _need_device(m.indices, m.codebook, m.group_scale, m.group_offset, m._sc_row_ptr, m._sc_col,
+    _need_device(m.indices, m._kcb, m.group_scale, m.group_offset, m._sc_row_ptr, m._sc_col,
                  m._sc_delta, m.bias)
-    return HxqMatrix(m.indices.data_ptr(), m.codebook.data_ptr(), p(m.group_scale),
+    _need_cb256(m._kcb)
+    return HxqMatrix(m.indices.data_ptr(), m._kcb.data_ptr(), p(m.group_scale),
                      p(m.group_offset), p(m._sc_row_ptr), p(m._sc_col), p(m._sc_delta), p(m.bias),
                      0, m.out_features)
 

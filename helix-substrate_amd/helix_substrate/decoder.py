@@ -45,7 +45,7 @@ _PROJ = ("q", "k", "v", "o", "gate", "up", "down")
 
 
 def _mats(mods):
-    return [{"indices": m.indices, "codebook": m.codebook, "group_scale": m.group_scale,
+    return [{"indices": m.indices, "codebook": m._kcb, "group_scale": m.group_scale,
              "group_offset": m.group_offset, "sc_row_ptr": m._sc_row_ptr, "sc_col": m._sc_col,
              "sc_delta": m._sc_delta, "bias": m.bias} for m in mods]
 
@@ -148,7 +148,7 @@ class HelixDecoder:
             _hxq.attn_rope_decode(self.qkv, self.pos, c.n_heads, c.n_kv_heads, c.head_dim,
                                   c.rope_theta, self.kc[li], self.vc[li], self.attn)
             Lo = L["o"]
-            _hxq.gemv(self.attn, Lo.indices, Lo.codebook, Lo.group_scale, Lo.group_offset,
+            _hxq.gemv(self.attn, Lo.indices, Lo._kcb, Lo.group_scale, Lo.group_offset,
                       Lo.group_size, Lo._sc_row_ptr, Lo._sc_col, Lo._sc_delta, Lo.bias,
                       out=self.o)
             # r = xb + o -> xa; h = norm(r) -> gate/up
@@ -158,7 +158,7 @@ class HelixDecoder:
             # far cheaper than fp32 gate and up in every block
             _hxq.silu_mul(self.g, self.u, self.act)
             Ld = L["down"]
-            _hxq.gemv(self.act, Ld.indices, Ld.codebook, Ld.group_scale, Ld.group_offset,
+            _hxq.gemv(self.act, Ld.indices, Ld._kcb, Ld.group_scale, Ld.group_offset,
                       Ld.group_size, Ld._sc_row_ptr, Ld._sc_col, Ld._sc_delta, Ld.bias,
                       out=self.dn)
             delta = self.dn
@@ -178,14 +178,14 @@ class HelixDecoder:
             _hxq.attn_decode(self.q, self.kc[li], self.vc[li], self.pos, c.n_heads, c.n_kv_heads,
                              c.head_dim, self.attn)
             Lo = L["o"]
-            _hxq.gemv(self.attn, Lo.indices, Lo.codebook, Lo.group_scale, Lo.group_offset,
+            _hxq.gemv(self.attn, Lo.indices, Lo._kcb, Lo.group_scale, Lo.group_offset,
                       Lo.group_size, Lo._sc_row_ptr, Lo._sc_col, Lo._sc_delta, Lo.bias,
                       out=self.o)
             _hxq.add_rmsnorm(self.x, self.o, L["post_norm"], c.rms_eps, self.h)
             _hxq.gemv_multi(self.h, self._gu_mats[li], self._group, outs=[self.g, self.u])
             _hxq.silu_mul(self.g, self.u, self.act)
             Ld = L["down"]
-            _hxq.gemv(self.act, Ld.indices, Ld.codebook, Ld.group_scale, Ld.group_offset,
+            _hxq.gemv(self.act, Ld.indices, Ld._kcb, Ld.group_scale, Ld.group_offset,
                       Ld.group_size, Ld._sc_row_ptr, Ld._sc_col, Ld._sc_delta, Ld.bias,
                       out=self.dn)
             delta = self.dn

@@ -183,6 +183,12 @@ class HelixLinear(nn.Module):
                 if tuple(t.shape) != (self.out_features, ng):
                     raise ValueError(f"{name} shape {tuple(t.shape)} != ({self.out_features}, {ng})")
         check_kernel_shapes(self.in_features, self.group_size, has_affine)
+        # the kernels read 256 codebook entries (uint8 indices): a shorter
+        # codebook is zero-padded in a derived copy
+        cb = self.codebook.float().contiguous()
+        self.register_buffer(
+            "_kcb", cb if cb.numel() == 256 else torch.cat([cb, cb.new_zeros(256 - cb.numel())]),
+            persistent=False)
         if self.sidecar_positions is not None and self.sidecar_values is not None:
             csr = build_sidecar_csr(self.sidecar_positions, self.sidecar_values, self.indices,
                                     self.codebook, self.group_scale, self.group_offset,
@@ -216,6 +222,7 @@ class HelixLinear(nn.Module):
 
     def _recompute_derived_pairs(self) -> None:
         """Derived state of a pair-codebook layer (vector_dim 2)."""
+        self.register_buffer("_kcb", None, persistent=False)
         if self.vector_dim != 2 or self.codebook.shape[0] > 4096:
             raise NotImplementedError("pair codebooks are [k <= 4096, 2]")
         if self.group_scale is not None or self.group_offset is not None:
@@ -345,18 +352,18 @@ class HelixLinear(nn.Module):
             self._forward_hip_pairs(x2, rp, col, delta, out)
         elif n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv"
-            _hxq.gemv(x2, self.indices, self.codebook, self.group_scale, self.group_offset,
+            _hxq.gemv(x2, self.indices, self._kcb, self.group_scale, self.group_offset,
                       self.group_size, rp, col, delta, self.bias, out=out)
         elif x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
             self._last_dispatch_path = "hip_gemm"
-            _hxq.gemm(x2, self.indices, self.codebook, self._affine_t, self.group_size, rp, col,
+            _hxq.gemm(x2, self.indices, self._kcb, self._affine_t, self.group_size, rp, col,
                       None if rp is None else self._sc_val, self.bias, out=out)
         else:
             # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
             self._last_dispatch_path = "hip_gemv_rows"
             for r0 in range(0, n, _GEMV_MAX_ROWS):
                 r1 = min(n, r0 + _GEMV_MAX_ROWS)
-                _hxq.gemv(x2[r0:r1], self.indices, self.codebook, self.group_scale,
+                _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
                           self.group_offset, self.group_size, rp, col, delta, self.bias,
                           out=out[r0:r1])
         if svd_on:
@@ -425,7 +432,7 @@ class HelixLinear(nn.Module):
                 tile = tile + (self.svd_U[start_row:end_row] * self.svd_s.unsqueeze(0)) @ self.svd_Vt
             return tile
         if self.indices.is_cuda:
-            tile = _hxq.dequant_f32(self.indices, self.codebook, self.group_scale,
+            tile = _hxq.dequant_f32(self.indices, self._kcb, self.group_scale,
                                     self.group_offset, self.group_size,
                                     self._sc_row_ptr if apply_sc else None,
                                     self._sc_col if apply_sc else None,

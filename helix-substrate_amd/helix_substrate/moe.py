@@ -147,7 +147,7 @@ class HelixMoeExperts(nn.Module):
         def layers(mods):
             out = []
             for m in mods:
-                out.append({"indices": m.indices, "codebook": m.codebook,
+                out.append({"indices": m.indices, "codebook": m._kcb,
                             "group_scale": getattr(m, "group_scale", None),
                             "group_offset": getattr(m, "group_offset", None),
                             "group_size": getattr(m, "group_size", 0),

@@ -151,6 +151,28 @@ def test_gemv_multi_matrices(dev):
         assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= TOL_F32
 
 
+@pytest.mark.parametrize("k", [1, 37, 255])
+def test_short_codebook_is_padded(dev, k):
+    """A k < 256 codebook (indices < k): the kernels read a zero-padded
+    256-entry copy; GEMV, GEMM and dequant match the oracle of the original."""
+    L, _ = _layer(96, 512, seed=30 + k)
+    rs = np.random.RandomState(k)
+    L["codebook"] = np.sort(rs.standard_normal(k).astype(np.float32) * 0.02)
+    L["indices"] = rs.randint(0, k, L["indices"].shape).astype(np.uint8)
+    # sidecar values replace the reconstruction at their positions (any k)
+    m = _module(synth.to_torch(L), dev)
+    assert m._kcb.numel() == 256 and m.codebook.numel() == k
+    W = _oracle_w(L)
+    np.testing.assert_array_equal(m.decode_weight().cpu().numpy().view(np.uint32), W.view(np.uint32))
+    for rows in (1, 64):
+        x = torch.randn(rows, 512, generator=torch.Generator().manual_seed(k + rows))
+        rel = _maxrel(m(x.to(dev)).float().cpu().numpy(), oracle.linear_f64(x.numpy(), W))
+        assert rel <= (TOL_F32 if rows == 1 else TOL_BF16), (rows, rel)
+    with pytest.raises(ValueError):
+        _hxq.gemv(torch.randn(1, 512, device=dev), m.indices, m.codebook.contiguous(), m.group_scale,
+                  m.group_offset, 128, None, None, None)
+
+
 def test_gemv_deterministic(dev):
     L, T = _layer(2048, 11008, seed=11)
     m = _module(T, dev)

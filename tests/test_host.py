@@ -82,6 +82,25 @@ def test_decode_weight_bit_exact_cpu():
     np.testing.assert_array_equal(torch.cat(tiles).numpy(), W)
 
 
+def test_short_codebook_kernel_copy_is_padded():
+    """Scalar-codebook kernels read 256 entries: a k < 256 codebook gets a
+    zero-padded kernel copy (_kcb); the saved codebook keeps k entries, and
+    the kernel wrappers refuse a short codebook."""
+    from helix_substrate import _hxq
+    L = synth.make_layer_np(40, 128, seed=5, sidecar=False)
+    L["codebook"] = np.sort(np.random.RandomState(1).standard_normal(37).astype(np.float32))
+    L["indices"] = np.random.RandomState(2).randint(0, 37, (40, 128)).astype(np.uint8)
+    m = _module(L)
+    assert m.codebook.numel() == 37 and m.state_dict()["codebook"].numel() == 37
+    assert "_kcb" not in m.state_dict()
+    assert m._kcb.numel() == 256
+    assert torch.equal(m._kcb[:37], m.codebook) and not m._kcb[37:].any()
+    np.testing.assert_array_equal(m.decode_weight().numpy(), _oracle_w(L))
+    with pytest.raises(ValueError):
+        _hxq._need_cb256(m.codebook)
+    _hxq._need_cb256(m._kcb)
+
+
 @pytest.mark.parametrize("shape", [(256,), (3, 256), (2, 3, 256)])
 def test_forward_cpu_matches_oracle(shape):
     L = synth.make_layer_np(96, 256, seed=4)
