@@ -74,7 +74,30 @@ struct GemmArgs {
     const float *bias;    // [OUT] or null (dense only)
     void *y;              // [M, OUT]
     int32_t M, OUT, K, group, y_dtype, n_experts, x_rows, pad_;
+    int32_t tiles_x, tiles_y, tiles_per_xcd, pad2_;  // dense: tile grid, XCD share
 };
+
+// Dense tile order.  Blocks are dealt round-robin to the XCDs (block b runs on
+// XCD b % kXcds), each with its own L2.  Tile t = (b % kXcds) * per + b / kXcds
+// gives every XCD a contiguous run of the order, and the order walks groups of
+// kGroupRows row tiles column by column, so the ~32 blocks one XCD runs at a
+// time cover about 8 X row tiles x 4 W column tiles: each tile is fetched into
+// that L2 once and reused by the blocks beside it, instead of every block
+// fetching a W tile no other block on its XCD reads.  Returns false for the
+// padding blocks past the last tile.
+constexpr int kXcds = 8;
+constexpr int kGroupRows = 8;
+__device__ __forceinline__ bool dense_tile(const GemmArgs &g, int b, int &tx, int &ty) {
+    const int t = (b % kXcds) * g.tiles_per_xcd + b / kXcds;
+    if (t >= g.tiles_x * g.tiles_y) return false;
+    const int grp = t / (kGroupRows * g.tiles_x);
+    const int r0 = grp * kGroupRows;
+    const int gr = min(kGroupRows, g.tiles_y - r0);  // rows in this group
+    const int w = t - grp * kGroupRows * g.tiles_x;
+    tx = w / gr;
+    ty = r0 + w % gr;
+    return true;
+}
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -187,12 +210,16 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
         r1 = s_tile[2];
         __syncthreads();  // s_tile lives in sA: everyone has read it
         if (e < 0) return;  // block-uniform: no tile for this block index
-    } else {
-        r0 = blockIdx.y * BM;
+    }
+    int tile_x = blockIdx.x;
+    if constexpr (!GROUPED) {
+        int ty;
+        if (!dense_tile(g, blockIdx.x, tile_x, ty)) return;  // block-uniform
+        r0 = ty * BM;
         r1 = min(r0 + BM, g.M);
     }
     const int64_t eo = static_cast<int64_t>(e);
-    const int n0 = blockIdx.x * (PAIR ? kBN / 2 : kBN);
+    const int n0 = tile_x * (PAIR ? kBN / 2 : kBN);
     const int ngroups = AFFINE ? K / g.group : 1;
 
     // codebook replicas: entry j at [j * NREP + r]; thread t fills entry t/2
@@ -690,8 +717,15 @@ __global__ __launch_bounds__(256) void affine_pack_kernel(const float *gs, const
 // Host side
 // ---------------------------------------------------------------------------
 template <int BM, bool BF16, bool GROUPED, bool PAIR>
-static int gemm_launch(const GemmArgs &a, int grid_x, int grid_y, hipStream_t stream) {
-    const dim3 grid(grid_x, grid_y);
+static int gemm_launch(GemmArgs &a, int grid_x, int grid_y, hipStream_t stream) {
+    dim3 grid(grid_x, grid_y);
+    if constexpr (!GROUPED) {
+        // one dimension: the kernel maps blocks to tiles XCD by XCD
+        a.tiles_x = grid_x;
+        a.tiles_y = grid_y;
+        a.tiles_per_xcd = (grid_x * grid_y + kXcds - 1) / kXcds;
+        grid = dim3(a.tiles_per_xcd * kXcds, 1);
+    }
     if (a.w[0].ga)
         hipLaunchKernelGGL((gemm_kernel<BM, BF16, true, GROUPED, PAIR>), grid, dim3(kGemmThreads),
                            0, stream, a);

@@ -641,6 +641,10 @@ static int plan_gemv(GemvHeader &h, GemvMats &mats, int n_x, GemvPlan &pl) {
     }
     for (int m = h.n_mats; m < HXQ_MAX_MULTI; ++m) h.bb[m] = INT32_MAX;
     pl.grid = static_cast<int>(grid);
+    // Enough rows per block for every wave: two chunks per slice, so one
+    // cross-lane reduction covers 32 weights per lane instead of 16 (with few
+    // rows per block the K split keeps more waves busy instead).
+    if (n_x == 1 && pl.CPS == 1 && h.nchunks >= 2 && rows_pb >= 2 * kWaves) pl.CPS = 2;
     int S = 1;
     while (S * pl.CPS < h.nchunks) S *= 2;
     // few rows per block: split K further so more waves have rows
