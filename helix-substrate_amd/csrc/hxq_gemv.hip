@@ -612,7 +612,7 @@ struct GemvPlan {
 };
 
 // Chunks per slice, K slices, and the block partition over matrices.
-static int plan_gemv(GemvHeader &h, GemvMats &mats, int n_x, GemvPlan &pl) {
+static int plan_gemv(GemvHeader &h, GemvMats &mats, int n_x, GemvPlan &pl, bool fused_prologue) {
     pl.CPS = 1;
     if (n_x == 1) {
         while (pl.CPS < 4 && pl.CPS * kWaves < h.nchunks) pl.CPS *= 2;
@@ -644,7 +644,9 @@ static int plan_gemv(GemvHeader &h, GemvMats &mats, int n_x, GemvPlan &pl) {
     // Enough rows per block for every wave: two chunks per slice, so one
     // cross-lane reduction covers 32 weights per lane instead of 16 (with few
     // rows per block the K split keeps more waves busy instead).
-    if (n_x == 1 && pl.CPS == 1 && h.nchunks >= 2 && rows_pb >= 2 * kWaves) pl.CPS = 2;
+    // (Not with a fused prologue: its extra operand registers would spill.)
+    if (n_x == 1 && !fused_prologue && pl.CPS == 1 && h.nchunks >= 2 && rows_pb >= 2 * kWaves)
+        pl.CPS = 2;
     int S = 1;
     while (S * pl.CPS < h.nchunks) S *= 2;
     // few rows per block: split K further so more waves have rows
@@ -704,7 +706,7 @@ static int gemv_run(GemvHeader &h, GemvMats &mats, int n_x, hipStream_t stream,
                     const GemvPro &pro = GemvPro{}) {
     h.fmt = FMT;
     GemvPlan pl{};
-    const int rc = plan_gemv(h, mats, n_x, pl);
+    const int rc = plan_gemv(h, mats, n_x, pl, XM != 0);
     if (rc != HXQ_OK) return rc;
     // stage activations in LDS (sidecar gather) when two blocks still fit a CU
     constexpr size_t kLdsBudget = 80 * 1024;
