@@ -183,12 +183,8 @@ class HelixLinear(nn.Module):
                 if tuple(t.shape) != (self.out_features, ng):
                     raise ValueError(f"{name} shape {tuple(t.shape)} != ({self.out_features}, {ng})")
         check_kernel_shapes(self.in_features, self.group_size, has_affine)
-        # the kernels read 256 codebook entries (uint8 indices): a shorter
-        # codebook is zero-padded in a derived copy
-        cb = self.codebook.float().contiguous()
-        self.register_buffer(
-            "_kcb", cb if cb.numel() == 256 else torch.cat([cb, cb.new_zeros(256 - cb.numel())]),
-            persistent=False)
+        self._kcb_cache = None
+        _ = self._kcb  # build the padded kernel codebook now (not inside a graph capture)
         if self.sidecar_positions is not None and self.sidecar_values is not None:
             csr = build_sidecar_csr(self.sidecar_positions, self.sidecar_values, self.indices,
                                     self.codebook, self.group_scale, self.group_offset,
@@ -222,7 +218,7 @@ class HelixLinear(nn.Module):
 
     def _recompute_derived_pairs(self) -> None:
         """Derived state of a pair-codebook layer (vector_dim 2)."""
-        self.register_buffer("_kcb", None, persistent=False)
+        self._kcb_cache = None
         if self.vector_dim != 2 or self.codebook.shape[0] > 4096:
             raise NotImplementedError("pair codebooks are [k <= 4096, 2]")
         if self.group_scale is not None or self.group_offset is not None:
@@ -287,6 +283,25 @@ class HelixLinear(nn.Module):
 
             return unpack_12bit_rows(self.indices, start_row, end_row, self.in_features // 2).long()
         return self.indices[start_row:end_row].long()
+
+    @property
+    def _kcb(self) -> torch.Tensor:
+        """The codebook as the scalar kernels read it: fp32 [256] (uint8 indices reach every
+        entry).  A 256-entry fp32 codebook is used as is; a shorter one gets a zero-padded
+        copy, rebuilt whenever the codebook tensor, its contents version or its device
+        changes (e.g. after load_state_dict or .to())."""
+        cb = self.codebook
+        if cb.dtype == torch.float32 and cb.numel() == 256 and cb.is_contiguous():
+            return cb
+        key = (cb.data_ptr(), cb._version, cb.device, cb.numel(), cb.dtype)
+        cache = getattr(self, "_kcb_cache", None)
+        if cache is None or cache[0] != key:
+            c = cb.reshape(-1).float()
+            if c.numel() > 256:
+                raise NotImplementedError("scalar codebooks above 256 entries are not supported")
+            cache = (key, torch.cat([c, c.new_zeros(256 - c.numel())]).contiguous())
+            self._kcb_cache = cache
+        return cache[1]
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):

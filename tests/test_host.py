@@ -92,13 +92,23 @@ def test_short_codebook_kernel_copy_is_padded():
     L["indices"] = np.random.RandomState(2).randint(0, 37, (40, 128)).astype(np.uint8)
     m = _module(L)
     assert m.codebook.numel() == 37 and m.state_dict()["codebook"].numel() == 37
-    assert "_kcb" not in m.state_dict()
+    assert not any("kcb" in k for k in m.state_dict())
     assert m._kcb.numel() == 256
     assert torch.equal(m._kcb[:37], m.codebook) and not m._kcb[37:].any()
     np.testing.assert_array_equal(m.decode_weight().numpy(), _oracle_w(L))
     with pytest.raises(ValueError):
         _hxq._need_cb256(m.codebook)
     _hxq._need_cb256(m._kcb)
+    # the padded copy follows the codebook: in-place edits, load_state_dict
+    m.codebook.mul_(2.0)
+    assert torch.equal(m._kcb[:37], m.codebook)
+    sd = {k: v.clone() for k, v in m.state_dict().items()}
+    sd["codebook"] = sd["codebook"] + 1.0
+    m.load_state_dict(sd, strict=False)
+    assert torch.equal(m._kcb[:37], sd["codebook"]) and not m._kcb[37:].any()
+    # a full 256-entry codebook is used as is (no copy to go stale)
+    m2 = _module(synth.make_layer_np(8, 128, seed=6, sidecar=False))
+    assert m2._kcb is m2.codebook
 
 
 @pytest.mark.parametrize("shape", [(256,), (3, 256), (2, 3, 256)])
