@@ -194,3 +194,49 @@ def test_persistent_rejects_position_out_of_range(dev):
     b.step_persistent(1)
     assert b.persistent_error() == 0
     assert int(b.pos.item()) == 1
+
+
+@pytest.mark.parametrize("hidden", [512, 2048])
+def test_persistent_long_context_matches_launch_sequence(dev, hidden):
+    """Teacher-forced decode to position ~680: the persistent kernel's attention
+    preloads the first 128 value rows into registers, stages the next ones in
+    LDS (buffer-to-LDS loads) and reads the rest from memory; every range is
+    crossed here.  Logits against the per-kernel launch sequence (5e-3 of
+    max|logit|) at sampled positions, and the KV caches written by both."""
+    global CFG
+    cfg = DecoderConfig(hidden=hidden, n_layers=2, n_heads=hidden // 128, n_kv_heads=2,
+                        head_dim=128, intermediate=768, vocab=1000, rope_theta=1e6,
+                        rms_eps=1e-6, max_seq=704)
+    saved, CFG = CFG, cfg
+    try:
+        mk = lambda o, i, s: synth.make_layer_np(o, i, seed=s, group_size=64)
+        a = HelixDecoder.synthetic(cfg, seed=6, device=dev, layer_fn=mk)
+        b = HelixDecoder.synthetic(cfg, seed=6, device=dev, layer_fn=mk)
+        b.persistent_init()
+        rng = np.random.default_rng(7)
+        prompt = rng.integers(0, cfg.vocab, 690).tolist()
+        checks = {0, 1, 127, 128, 129, 200, 400, 600, 640, 689}
+        # the fp64 oracle of the same math at the bf16 bar (hidden 512: cheap in numpy)
+        ref = _oracle_logits(a, prompt) if hidden == 512 else None
+        print(f"long context hidden={hidden} tokens={len(prompt)}", flush=True)
+        for t, tok in enumerate(prompt):
+            a.tok.fill_(tok)
+            b.tok.fill_(tok)
+            a._step_launches()
+            b.step_persistent(1)
+            if t in checks:
+                la, lb = a.logits.cpu().numpy(), b.logits.cpu().numpy()
+                scale = np.abs(la).max()
+                assert np.abs(la - lb).max() <= 5e-3 * scale, (t, np.abs(la - lb).max() / scale)
+                if ref is not None:
+                    assert np.abs(lb - ref[t]).max() <= 2e-2 * np.abs(ref[t]).max(), t
+        assert b.persistent_error() == 0
+        assert int(b.pos.item()) == len(prompt)
+        for kc_a, kc_b in zip(a.kc, b.kc):
+            d = (kc_a[:len(prompt)].float() - kc_b[:len(prompt)].float()).abs().max().item()
+            assert d <= 2e-2 * kc_a[:len(prompt)].float().abs().max().item()
+        for vc_a, vc_b in zip(a.vc, b.vc):
+            d = (vc_a[:len(prompt)].float() - vc_b[:len(prompt)].float()).abs().max().item()
+            assert d <= 2e-2 * vc_a[:len(prompt)].float().abs().max().item()
+    finally:
+        CFG = saved
