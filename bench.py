@@ -53,7 +53,8 @@ def parse():
                          "a 256 MiB copy as the counter calibration; prints no JSON")
     ap.add_argument("--encode", type=int, default=1,
                     help="also time the CDNAv3 encoder on one Qwen2.5-3B gate_proj "
-                         "(k-means codebook, assignment, percentile sidecar)")
+                         "(k-means codebook, assignment, percentile sidecar; and the "
+                         "4096-entry pair-codebook k-means and assignment)")
     ap.add_argument("--formats", type=int, default=1,
                     help="also time the GEMV on the variant index formats (pair codebook with "
                          "uint16 / 12-bit indices, 6-bit affine) at the gate+up shape")
@@ -268,6 +269,7 @@ def main():
         result["moe_config4"] = moe_bench(dev, cpu=args.cpu_seconds > 0)
     if args.encode:
         result["encode_cdnav3"] = encode_bench(dev, cpu=args.cpu_seconds > 0)
+        result["encode_cdnav3_pairs"] = encode_pairs_bench(dev, cpu=args.cpu_seconds > 0)
     if args.formats:
         result["formats_gateup"] = formats_bench(dev)
     if args.cpu_seconds > 0:
@@ -761,6 +763,87 @@ def encode_bench(dev, iters=3, cpu=True):
     del w, flat
     torch.cuda.empty_cache()
     return out
+
+
+def encode_pairs_bench(dev, iters=2, cpu=True):
+    """Pair-codebook (vector_dim 2) encode of the same gate_proj: 11.27M column
+    pairs, 4096-entry codebook fitted on the writer's 500K-pair subsample
+    (k-means++ seeding on the host, up to 10 Lloyd steps on the device), then
+    every pair assigned.  The assignment kernel is VALU-bound: 7 fp32 vector
+    instructions per (pair, entry) (mul, fma, add, fma, compare, two selects),
+    so 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz / 7 = 5.62e12 pair-entry
+    distances/s is its roof."""
+    import numpy as np
+    import torch
+    from helix_substrate import _hxq, hxq_encoder
+
+    rows, cols, k = INTER, HIDDEN, 4096
+    g = torch.Generator(device=dev).manual_seed(7)
+    w = torch.randn(rows, cols, device=dev, generator=g) * 0.02
+    stages = {"fit_ms": 0.0, "assign_ms": 0.0}
+    steps = [0]
+
+    def encode(timed):
+        vec = w.reshape(-1, 2)
+        t0 = time.perf_counter()
+        sel = hxq_encoder._sample_index(int(vec.shape[0]), hxq_encoder.KMEANS_MAX_SAMPLES)
+        fit = vec[torch.from_numpy(sel).to(dev)].contiguous()
+        cb, _, steps[0] = hxq_encoder.vector_kmeans(fit, k)
+        torch.cuda.synchronize(dev)
+        t1 = time.perf_counter()
+        idx = _hxq.vq2_assign(vec, cb)
+        torch.cuda.synchronize(dev)
+        t2 = time.perf_counter()
+        if timed:
+            stages["fit_ms"] += (t1 - t0) * 1e3 / iters
+            stages["assign_ms"] += (t2 - t1) * 1e3 / iters
+        return cb, idx
+
+    cb, _ = encode(False)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        encode(True)
+    ms = (time.perf_counter() - t0) * 1e3 / iters
+    # the assignment launch alone, HIP events on the launch stream
+    vec = w.reshape(-1, 2)
+    out = torch.empty(vec.shape[0], dtype=torch.int16, device=dev)
+    ws = torch.empty(16 * k, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _hxq.vq2_assign(vec, cb, out=out, workspace=ws)
+    e0.record(st)
+    for _ in range(5):
+        _hxq.vq2_assign(vec, cb, out=out, workspace=ws)
+    e1.record(st)
+    torch.cuda.synchronize(dev)
+    launch_ms = e0.elapsed_time(e1) / 5
+    dist = vec.shape[0] * k
+    roof = 256 * 4 * 16 * 2.4e9 / 7
+    res = {"tensor": [rows, cols], "pairs": int(vec.shape[0]), "codebook": [k, 2],
+           "fit_sample": hxq_encoder.KMEANS_MAX_SAMPLES, "lloyd_steps": int(steps[0]),
+           "ms_per_tensor": round(ms, 2), **{kk: round(v, 2) for kk, v in stages.items()},
+           "assign_launch_ms": round(launch_ms, 3),
+           "assign_gdist_per_s": round(dist / launch_ms / 1e6, 1),
+           "assign_valu_frac": round(dist / (launch_ms * 1e-3) / roof, 3)}
+    if cpu:
+        # the reference's numpy/CPU algorithm (oracle restatement, C distance
+        # and update steps) on 64 rows of the same tensor: 65536 pairs, all
+        # fitted (below the 500K subsample), 4096 entries
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle
+
+        sample = w[:64].cpu().numpy()
+        t0 = time.perf_counter()
+        oracle.build_vector_codebook_np(sample, k)
+        el = time.perf_counter() - t0
+        res["cpu_baseline"] = {"s_per_sample": round(el, 2),
+                               "kpairs_per_s": round(sample.size / 2 / el / 1e3, 2),
+                               "sample": "64 x 2048 rows of the same tensor (65536 pairs), "
+                                         "oracle.build_vector_codebook_np",
+                               "kind": "port", "cores": 1}
+    del w
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(mods, seconds):

@@ -1,6 +1,7 @@
 // CDNAv3 encoder on the GPU: 1-D k-means codebook, nearest-codebook
-// assignment and percentile outliers (the sidecar), with the reference's
-// CPU results reproduced bit for bit.
+// assignment and percentile outliers (the sidecar), and the pair-codebook
+// (vector_dim 2) k-means steps, with the reference's CPU results reproduced
+// bit for bit.
 //
 // Reference (helix_substrate/hxq_encoder.py:107-177 _simple_kmeans,
 // hxq_writer_v3.py:427-470 _build_kmeans_codebook / _chunked_assign,
@@ -672,6 +673,200 @@ static int64_t next_pow2(int64_t n) {
     return p;
 }
 
+
+// ---------------------------------------------------------------------------
+// pair (vector_dim 2) codebook: nearest centroid and centroid update
+// ---------------------------------------------------------------------------
+// The reference's numpy arithmetic (hxq_encoder.py:280-300):
+//   d_j = fl(fl(|x|^2 + |c_j|^2) - 2 x.c_j), |v|^2 = fl(fl(v0*v0) + fl(v1*v1)),
+//   x.c = fma(x1, c1, fl(x0*c0)) (what numpy's sgemm gives a K = 2 product),
+//   first index of the minimum;  new c_j = fp32(fp64 sum / fp32 count).
+// 2 x.c is exact, so fl(t - fl(2 x.c)) is the single rounding fma(-2, x.c, t).
+constexpr int kPairMaxK = 4096;
+constexpr int kPairThreads = 512;
+constexpr int kUpdThreads = 1024;     // one owner thread per cluster id mod 1024
+constexpr int kUpdChunk = 1024;       // ids staged in LDS per pass
+constexpr int kUpdMaxBlocks = 512;
+constexpr int kUpdSlots = kPairMaxK / kUpdThreads;
+
+// {c0, c1, |c|^2, 0} per centroid.
+__global__ __launch_bounds__(256) void pair_table_kernel(const float *__restrict__ cb, int k,
+                                                         float4 *__restrict__ tab) {
+#pragma clang fp contract(off)
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j < k) {
+        const float c0 = cb[2 * j], c1 = cb[2 * j + 1];
+        tab[j] = make_float4(c0, c1, c0 * c0 + c1 * c1, 0.0f);
+    }
+}
+
+// V pairs per thread (pair i = block base + threadIdx.x + v * kPairThreads);
+// the table is staged once per block in LDS and read as a broadcast.
+template <int V>
+__global__ __launch_bounds__(kPairThreads) void pair_assign_kernel(
+    const float2 *__restrict__ x, int64_t n, const float4 *__restrict__ tab, int k,
+    uint16_t *__restrict__ idx) {
+#pragma clang fp contract(off)
+    extern __shared__ float4 stab[];
+    for (int j = threadIdx.x; j < k; j += kPairThreads) stab[j] = tab[j];
+    __syncthreads();
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kPairThreads * V) + threadIdx.x;
+    float x0[V], x1[V], xsq[V], best[V];
+    int bj[V];
+    const float4 c = stab[0];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int64_t i = base + static_cast<int64_t>(v) * kPairThreads;
+        const float2 p = i < n ? x[i] : make_float2(0.0f, 0.0f);
+        x0[v] = p.x;
+        x1[v] = p.y;
+        xsq[v] = p.x * p.x + p.y * p.y;
+        best[v] = fmaf(-2.0f, fmaf(x1[v], c.y, x0[v] * c.x), xsq[v] + c.z);
+        bj[v] = 0;
+    }
+    for (int j = 1; j < k; ++j) {
+        const float4 cj = stab[j];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const float d = fmaf(-2.0f, fmaf(x1[v], cj.y, x0[v] * cj.x), xsq[v] + cj.z);
+            if (d < best[v]) {
+                best[v] = d;
+                bj[v] = j;
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int64_t i = base + static_cast<int64_t>(v) * kPairThreads;
+        if (i < n) idx[i] = static_cast<uint16_t>(bj[v]);
+    }
+}
+
+// fp64 sums and counts per cluster over one block's range of pairs.  Thread
+// t = 64 * wave + lane owns the ids with id % 1024 == t and adds their pairs
+// in index order, so the partials do not depend on timing.  The ids are
+// wave-uniform (read from LDS, made scalar), so the owner test is a scalar
+// branch and only the owning lane does vector work.  Block 0 clears
+// *max_delta for the finish kernel that follows on the stream.
+__global__ __launch_bounds__(kUpdThreads) void pair_partial_kernel(
+    const float2 *__restrict__ x, int64_t n, const uint16_t *__restrict__ idx, int k,
+    int64_t per_block, double *__restrict__ psum, uint32_t *__restrict__ pcnt,
+    float *__restrict__ max_delta) {
+    __shared__ uint16_t sidx[kUpdChunk];
+    __shared__ float2 sx[kUpdChunk];
+    const int t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
+    if (blockIdx.x == 0 && t == 0) *max_delta = 0.0f;
+    double s0[kUpdSlots], s1[kUpdSlots];
+    uint32_t cnt[kUpdSlots];
+#pragma unroll
+    for (int s = 0; s < kUpdSlots; ++s) {
+        s0[s] = 0.0;
+        s1[s] = 0.0;
+        cnt[s] = 0;
+    }
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * per_block;
+    const int64_t hi = lo + per_block < n ? lo + per_block : n;
+    for (int64_t b = lo; b < hi; b += kUpdChunk) {
+        const int m = static_cast<int>(hi - b < kUpdChunk ? hi - b : kUpdChunk);
+        __syncthreads();
+        if (t < m) {
+            sidx[t] = idx[b + t];
+            sx[t] = x[b + t];
+        }
+        __syncthreads();
+        for (int i = 0; i < m; ++i) {
+            const int id = __builtin_amdgcn_readfirstlane(static_cast<int>(sidx[i]));
+            if (((id >> 6) & 15) != wave) continue;
+            if (lane != (id & 63)) continue;
+            const float2 v = sx[i];
+            const int slot = id >> 10;
+#pragma unroll
+            for (int s = 0; s < kUpdSlots; ++s) {
+                if (slot == s) {
+                    s0[s] += static_cast<double>(v.x);
+                    s1[s] += static_cast<double>(v.y);
+                    cnt[s] += 1;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kUpdSlots; ++s) {
+        const int j = s * kUpdThreads + t;
+        if (j < k) {
+            psum[(2 * static_cast<int64_t>(blockIdx.x)) * k + j] = s0[s];
+            psum[(2 * static_cast<int64_t>(blockIdx.x) + 1) * k + j] = s1[s];
+            pcnt[static_cast<int64_t>(blockIdx.x) * k + j] = cnt[s];
+        }
+    }
+}
+
+// Adds the block partials in a fixed order (wave w of 16 takes blocks w,
+// w + 16, ... in turn; the 16 wave totals are then added in wave order),
+// writes the new centroids (empty clusters keep the old one) and raises
+// *max_delta to max |new - old| (non-negative floats order as their bits).
+__global__ __launch_bounds__(1024) void pair_finish_kernel(
+    const double *__restrict__ psum, const uint32_t *__restrict__ pcnt, int nparts, int k,
+    const float *__restrict__ old, float *__restrict__ out, float *__restrict__ max_delta) {
+    __shared__ double l0[16][64], l1[16][64];
+    __shared__ uint32_t lc[16][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
+    double a0 = 0.0, a1 = 0.0;
+    uint32_t c = 0;
+    if (j < k) {
+        for (int p = w; p < nparts; p += 16) {
+            a0 += psum[(2 * static_cast<int64_t>(p)) * k + j];
+            a1 += psum[(2 * static_cast<int64_t>(p) + 1) * k + j];
+            c += pcnt[static_cast<int64_t>(p) * k + j];
+        }
+    }
+    l0[w][lane] = a0;
+    l1[w][lane] = a1;
+    lc[w][lane] = c;
+    __syncthreads();
+    if (w != 0) return;
+    float dmax = 0.0f;
+    if (j < k) {
+        double t0 = 0.0, t1 = 0.0;
+        uint32_t tc = 0;
+        for (int q = 0; q < 16; ++q) {
+            t0 += l0[q][lane];
+            t1 += l1[q][lane];
+            tc += lc[q][lane];
+        }
+        const float o0 = old[2 * j], o1 = old[2 * j + 1];
+        float n0 = o0, n1 = o1;
+        if (tc > 0) {
+            const double fc = static_cast<double>(static_cast<float>(tc));
+            n0 = static_cast<float>(t0 / fc);
+            n1 = static_cast<float>(t1 / fc);
+        }
+        out[2 * j] = n0;
+        out[2 * j + 1] = n1;
+        dmax = fmaxf(fabsf(n0 - o0), fabsf(n1 - o1));
+    }
+    for (int off = 32; off > 0; off >>= 1) dmax = fmaxf(dmax, __shfl_xor(dmax, off));
+    if (lane == 0 && dmax > 0.0f)
+        atomicMax(reinterpret_cast<unsigned int *>(max_delta), __float_as_uint(dmax));
+}
+
+struct PairPlan {
+    int64_t per_block;
+    int64_t nparts;
+};
+
+static PairPlan pair_plan(int64_t n) {
+    PairPlan p;
+    int64_t per = (n + kUpdMaxBlocks - 1) / kUpdMaxBlocks;
+    per = (per + kUpdChunk - 1) / kUpdChunk * kUpdChunk;
+    p.per_block = per < kUpdChunk ? kUpdChunk : per;
+    p.nparts = n <= 0 ? 1 : (n + p.per_block - 1) / p.per_block;
+    return p;
+}
+
+
 }  // namespace enc
 }  // namespace hxq
 
@@ -883,6 +1078,69 @@ extern "C" int hxq_affine_fit(const float *w, const uint8_t *indices, const floa
     HXQ_REQUIRE(blocks < (int64_t{1} << 31), "too many groups");
     hipLaunchKernelGGL(affine_fit_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
                        stream, w, indices, codebook, k, rows, cols, group_size, bits, scale, offset);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
+extern "C" int64_t hxq_vq2_workspace_bytes(int64_t n, int32_t k) {
+    if (n < 0 || k < 1 || k > kPairMaxK) return -1;
+    const PairPlan p = pair_plan(n);
+    return align256(int64_t{16} * k) + align256(p.nparts * 16 * k) + align256(p.nparts * 4 * k);
+}
+
+static int pair_table(const float *codebook, int32_t k, float4 *tab, hipStream_t stream) {
+    hipLaunchKernelGGL(pair_table_kernel, dim3((k + 255) / 256), dim3(256), 0, stream, codebook, k,
+                       tab);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
+extern "C" int hxq_vq2_assign(const float *x, int64_t n, const float *codebook, int32_t k,
+                              uint16_t *indices, void *workspace, int64_t workspace_bytes,
+                              hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && codebook && indices && workspace, "x, codebook, indices and workspace are required");
+    HXQ_REQUIRE(n >= 0 && k >= 1 && k <= kPairMaxK, "k must be 1..4096");
+    HXQ_REQUIRE(workspace_bytes >= int64_t{16} * k, "workspace too small");
+    if (n == 0) return HXQ_OK;
+    float4 *tab = static_cast<float4 *>(workspace);
+    const int rc = pair_table(codebook, k, tab, stream);
+    if (rc != HXQ_OK) return rc;
+    const size_t lds = static_cast<size_t>(k) * sizeof(float4);
+    const auto *xv = reinterpret_cast<const float2 *>(x);
+    const int64_t big = (n + kPairThreads * 8 - 1) / (kPairThreads * 8);
+    if (big >= 1024) {
+        HXQ_REQUIRE(big < (int64_t{1} << 31), "too many pairs");
+        hipLaunchKernelGGL(pair_assign_kernel<8>, dim3(static_cast<uint32_t>(big)),
+                           dim3(kPairThreads), lds, stream, xv, n, tab, k, indices);
+    } else {
+        const int64_t g = (n + kPairThreads * 2 - 1) / (kPairThreads * 2);
+        hipLaunchKernelGGL(pair_assign_kernel<2>, dim3(static_cast<uint32_t>(g)),
+                           dim3(kPairThreads), lds, stream, xv, n, tab, k, indices);
+    }
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
+extern "C" int hxq_vq2_update(const float *x, int64_t n, const uint16_t *indices, int32_t k,
+                              const float *centroids, float *new_centroids, float *max_delta,
+                              void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && indices && centroids && new_centroids && max_delta && workspace,
+                "x, indices, centroids, new_centroids, max_delta and workspace are required");
+    HXQ_REQUIRE(n >= 0 && k >= 1 && k <= kPairMaxK, "k must be 1..4096");
+    HXQ_REQUIRE(workspace_bytes >= hxq_vq2_workspace_bytes(n, k), "workspace too small");
+    HXQ_REQUIRE(new_centroids != centroids, "new_centroids must not alias centroids");
+    const PairPlan p = pair_plan(n);
+    char *ws = static_cast<char *>(workspace) + align256(int64_t{16} * k);
+    double *psum = reinterpret_cast<double *>(ws);
+    uint32_t *pcnt = reinterpret_cast<uint32_t *>(ws + align256(p.nparts * 16 * k));
+    hipLaunchKernelGGL(pair_partial_kernel, dim3(static_cast<uint32_t>(p.nparts)),
+                       dim3(kUpdThreads), 0, stream, reinterpret_cast<const float2 *>(x), n,
+                       indices, k, p.per_block, psum, pcnt, max_delta);
+    HXQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(pair_finish_kernel, dim3((k + 63) / 64), dim3(1024), 0, stream, psum, pcnt,
+                       static_cast<int>(p.nparts), k, centroids, new_centroids, max_delta);
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }

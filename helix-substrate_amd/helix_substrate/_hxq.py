@@ -99,6 +99,8 @@ SIGNATURES = {
     "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
     "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
     "hxq_assign_nearest": [P, I64, P, I32, P, P],
+    "hxq_vq2_assign": [P, I64, P, I32, P, P, I64, P],
+    "hxq_vq2_update": [P, I64, P, I32, P, P, P, P, I64, P],
     "hxq_kmeans_init": [P, I64, P, I64, P, P],
     "hxq_kmeans_run": [P, I64, P, I32, I32, ctypes.c_double, P, I64, P, P, P, P],
     "hxq_select_f32": [P, I64, P, I32, P, P, P, I64, P],
@@ -120,6 +122,7 @@ SIGNATURES_I64 = {
     "hxq_kmeans_workspace_bytes": [I64],
     "hxq_select_workspace_bytes": [],
     "hxq_outliers_workspace_bytes": [I64],
+    "hxq_vq2_workspace_bytes": [I64, I32],
 }
 
 
@@ -680,6 +683,58 @@ def decoder_error(desc: HxqDecoder, workspace: torch.Tensor) -> int:
 
 
 # -- encoder ---------------------------------------------------------------------
+def _pair_args(x, codebook):
+    _need_device(x, codebook)
+    if x.dtype != torch.float32 or codebook.dtype != torch.float32:
+        raise RuntimeError("pair encoder steps take fp32 pairs and codebook")
+    if x.dim() != 2 or x.shape[1] != 2 or codebook.dim() != 2 or codebook.shape[1] != 2:
+        raise ValueError("x must be [n, 2] and codebook [k, 2]")
+    if not 1 <= codebook.shape[0] <= 4096:
+        raise ValueError("pair codebooks hold 1..4096 entries")
+
+
+def vq2_workspace(n, k, device):
+    nbytes = lib().hxq_vq2_workspace_bytes(int(n), int(k))
+    if nbytes < 0:
+        raise ValueError("pair codebooks hold 1..4096 entries")
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def vq2_assign(x, codebook, out=None, workspace=None):
+    """int16 [n] = nearest pair-codebook entry of each row of x (fp32 [n, 2]),
+    the reference's matmul-form fp32 distances, first index on ties."""
+    _pair_args(x, codebook)
+    n, k = x.shape[0], codebook.shape[0]
+    if out is None:
+        out = torch.empty(n, dtype=torch.int16, device=x.device)
+    if workspace is None:
+        workspace = torch.empty(16 * k, dtype=torch.uint8, device=x.device)
+    rc = lib().hxq_vq2_assign(_ptr(x), n, _ptr(codebook), k, _ptr(out), _ptr(workspace),
+                              workspace.numel(), _stream(x))
+    _check("hxq_vq2_assign", rc)
+    return out
+
+
+def vq2_update(x, indices, centroids, out=None, max_delta=None, workspace=None):
+    """(new centroids fp32 [k, 2], max |new - old| as a device fp32 [1]):
+    fp64 cluster sums of x over indices (int16 [n], < k)."""
+    _pair_args(x, centroids)
+    _need_device(indices)
+    if indices.dtype != torch.int16 or indices.numel() != x.shape[0]:
+        raise ValueError("indices must be int16 [n]")
+    n, k = x.shape[0], centroids.shape[0]
+    if out is None:
+        out = torch.empty_like(centroids)
+    if max_delta is None:
+        max_delta = torch.empty(1, dtype=torch.float32, device=x.device)
+    if workspace is None:
+        workspace = vq2_workspace(n, k, x.device)
+    rc = lib().hxq_vq2_update(_ptr(x), n, _ptr(indices), k, _ptr(centroids), _ptr(out),
+                              _ptr(max_delta), _ptr(workspace), workspace.numel(), _stream(x))
+    _check("hxq_vq2_update", rc)
+    return out, max_delta
+
+
 def assign_nearest(x, codebook, out=None):
     """indices (uint8, shape of x) = argmin_j |x - codebook[j]| (first on ties)."""
     xf = x.reshape(-1)

@@ -1,4 +1,5 @@
-"""CDNAv3 scalar encoder: 1-D k-means codebook and nearest-entry assignment.
+"""CDNAv3 encoder: 1-D k-means codebook and nearest-entry assignment, and the
+pair-codebook (vector_dim 2) k-means.
 
 Mirrors the reference's ``_simple_kmeans`` (``helix_substrate/hxq_encoder.py:
 107-177``) and ``CDNAv3Writer._chunked_assign`` / ``_build_kmeans_codebook``
@@ -7,6 +8,14 @@ algorithm (numpy percentile init, argmin assignment, np.mean updates,
 relative convergence test); device tensors run the HIP kernels of
 ``hxq_encode.hip``, which reproduce that CPU algorithm bit for bit (same
 init, same first-index argmin, cluster means summed in numpy's order).
+
+The pair encoder (``vector_kmeans`` / ``build_vector_codebook_and_assign``,
+reference ``_vector_kmeans``, ``hxq_encoder.py:210-315``, and
+``CDNAv3Writer._build_vector_codebook_and_assign``, ``hxq_writer_v3.py:
+338-420``) takes device tensors: the k-means++ seeding draws from the
+reference's RandomState(42) stream on the host (sequential, at most 64 draws),
+the Lloyd steps and the assignment of every pair run as HIP kernels that
+reproduce the reference's numpy CPU arithmetic.
 """
 from __future__ import annotations
 
@@ -156,3 +165,86 @@ def fit_group_affine(w, indices, codebook, group_size=128, exclude_positions=Non
         scale = np.where(fit, (n * scw - sc * sw) / det, 1.0)
         offset = np.where(n > 0, (sw - scale * sc) / np.maximum(n, 1.0), 0.0)
     return scale.astype(np.float32), offset.astype(np.float32)
+
+
+def kmeanspp_init(data, n_clusters):
+    """k-means++ seeding of _vector_kmeans (hxq_encoder.py:235-256) on host
+    rows data (fp32 [n, d]): a RandomState(42) stream, the first seed a
+    uniform row, then up to 63 rows drawn with probability proportional to
+    the squared distance (matmul form, clipped at 0) to the nearest seed so
+    far -- on a fresh 100000-row subsample each draw when n > 100000 -- and
+    any further seeds uniform rows without replacement."""
+    data = np.asarray(data, dtype=np.float32)
+    n, d = data.shape
+    rs = np.random.RandomState(42)
+    seeds = np.zeros((n_clusters, d), dtype=np.float32)
+    seeds[0] = data[rs.randint(n)]
+    for i in range(1, min(n_clusters, 64)):
+        have = seeds[:i]
+        pool = data[rs.choice(n, 100000, replace=False)] if n > 100000 else data
+        d2 = (np.sum(pool ** 2, axis=1, keepdims=True) + np.sum(have ** 2, axis=1, keepdims=True).T
+              - 2.0 * (pool @ have.T))
+        np.maximum(d2, 0, out=d2)
+        nearest = d2.min(axis=1)
+        seeds[i] = pool[rs.choice(len(pool), p=nearest / max(nearest.sum(), 1e-30))]
+    if n_clusters > 64:
+        seeds[64:] = data[rs.choice(n, n_clusters - 64, replace=False)]
+    return seeds
+
+
+def vector_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
+    """Pair k-means on device rows data (fp32 [n, 2]): (centroids fp32
+    [k, 2], assignments int16 [n] of the final pass, update steps taken),
+    k = min(n_clusters, n).  Stops when the largest centroid move is below
+    rtol * (max - min over the seeds), keeping the centroids of before that
+    update, as the reference does."""
+    if not _is_device(data):
+        raise RuntimeError("vector_kmeans takes a device tensor")
+    if data.dim() != 2 or data.shape[1] != 2:
+        raise NotImplementedError("the pair encoder handles vector_dim 2")
+    data = data.float().contiguous()
+    n = data.shape[0]
+    k = min(int(n_clusters), n)
+    if k < 1 or k > 4096:
+        raise ValueError("pair codebooks hold 1..4096 entries")
+    seeds = kmeanspp_init(data.cpu().numpy(), k)
+    rng = float(seeds.max() - seeds.min())
+    abs_tol = rtol * (rng if rng >= 1e-30 else 1.0)
+    cent = torch.from_numpy(seeds).to(data.device)
+    nxt = torch.empty_like(cent)
+    md = torch.empty(1, dtype=torch.float32, device=data.device)
+    ws = _hxq.vq2_workspace(n, k, data.device)
+    idx = torch.empty(n, dtype=torch.int16, device=data.device)
+    steps = 0
+    for _ in range(max_iters):
+        steps += 1
+        _hxq.vq2_assign(data, cent, out=idx, workspace=ws)
+        _hxq.vq2_update(data, idx, cent, out=nxt, max_delta=md, workspace=ws)
+        if float(md.item()) < abs_tol:
+            break
+        cent, nxt = nxt, cent
+    _hxq.vq2_assign(data, cent, out=idx, workspace=ws)
+    return cent, idx, steps
+
+
+def build_vector_codebook_and_assign(tensor, n_clusters, vector_dim=2, max_iters=10):
+    """CDNAv3Writer._build_vector_codebook_and_assign for vector_dim 2:
+    adjacent column pairs of the device tensor [rows, cols], k-means fitted on
+    a RandomState(42) subsample of at most KMEANS_MAX_SAMPLES pairs, every
+    pair assigned with the fitted codebook.  Returns (codebook fp32 [k, 2],
+    indices int16 [rows, cols / 2])."""
+    if vector_dim != 2:
+        raise NotImplementedError("the pair encoder handles vector_dim 2")
+    if not _is_device(tensor):
+        raise RuntimeError("build_vector_codebook_and_assign takes a device tensor")
+    rows, cols = tensor.shape
+    if cols % 2:
+        raise ValueError(f"in_features ({cols}) must be divisible by vector_dim (2)")
+    vec = tensor.float().contiguous().reshape(-1, 2)
+    fit = vec
+    if vec.shape[0] > KMEANS_MAX_SAMPLES:
+        sel = _sample_index(int(vec.shape[0]), KMEANS_MAX_SAMPLES)
+        fit = vec[torch.from_numpy(sel).to(vec.device)].contiguous()
+    cb, _, _ = vector_kmeans(fit, n_clusters, max_iters=max_iters)
+    idx = _hxq.vq2_assign(vec, cb)
+    return cb, idx.reshape(rows, cols // 2)

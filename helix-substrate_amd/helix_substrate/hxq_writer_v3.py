@@ -35,8 +35,10 @@ class CDNAv3Writer:
                         sidecar_positions=None, sidecar_values=None, group_scale=None,
                         group_offset=None, group_size: int = 128, extra_meta=None) -> Path:
         codebook = np.ascontiguousarray(codebook, dtype=np.float32)
-        indices = np.ascontiguousarray(indices, dtype=np.uint8)
-        rows, cols = indices.shape
+        vdim = int(codebook.shape[1]) if codebook.ndim == 2 else 1
+        wide = vdim > 1 or codebook.shape[0] > 256
+        indices = np.ascontiguousarray(indices, dtype=np.uint16 if wide else np.uint8)
+        rows, cols = indices.shape[0], indices.shape[1] * vdim
         out = self.base_dir / f"{_safe_name(tensor_name)}.cdnav3"
         out.mkdir(parents=True, exist_ok=True)
         np.save(out / "codebook.npy", codebook)
@@ -50,8 +52,8 @@ class CDNAv3Writer:
             np.save(out / "group_offset.npy", np.ascontiguousarray(group_offset, dtype=np.float32))
         meta = {
             "format_version": "cdna_v3", "tensor_name": tensor_name, "shape": [rows, cols],
-            "dtype": "float32", "index_dtype": "uint8", "storage_mode": "codebook",
-            "n_clusters": int(codebook.shape[0]), "vector_dim": 1,
+            "dtype": "float32", "index_dtype": "uint16" if wide else "uint8",
+            "storage_mode": "codebook", "n_clusters": int(codebook.shape[0]), "vector_dim": vdim,
             "codebook_sha256": hashlib.sha256(codebook.tobytes()).hexdigest(),
             "svd_residual_rank": 0, "num_outliers": n_out,
             "created_utc": datetime.now(timezone.utc).isoformat(),
@@ -83,16 +85,20 @@ class CDNAv3Writer:
                      percentile: float = 99.9, use_kmeans: bool = True,
                      sidecar_enabled: bool = True, max_corrections: int = 512,
                      storage_mode: str = "codebook+sidecar", tensor_class: str = "unknown",
-                     source_artifact: str = "", group_size=None) -> dict:
+                     source_artifact: str = "", group_size=None, vector_dim: int = 1) -> dict:
         """Quantise a 2-D fp32 tensor (numpy, or a device tensor for the GPU
         path) and write its directory; returns the stats the reference writes
         to stats.json.  group_size (extension): also fit the per-group affine
         (least squares per row and group, sidecar positions excluded) and
-        write group_scale / group_offset."""
+        write group_scale / group_offset.  vector_dim 2: pair codebook
+        [n_clusters <= 4096, 2] over adjacent columns and uint16 indices
+        [rows, cols / 2] (reference hxq_writer_v3.py:174-212; device tensors
+        only, no affine)."""
         import torch
 
         from .generate_sidecars_v3 import find_outliers_percentile
-        from .hxq_encoder import (build_kmeans_codebook, build_uniform_codebook, chunked_assign,
+        from .hxq_encoder import (build_kmeans_codebook, build_uniform_codebook,
+                                  build_vector_codebook_and_assign, chunked_assign,
                                   fit_group_affine)
 
         dev = isinstance(tensor, torch.Tensor) and tensor.is_cuda
@@ -100,10 +106,18 @@ class CDNAv3Writer:
             tensor = np.asarray(tensor, dtype=np.float32)
         rows, cols = tensor.shape
         flat = tensor.reshape(-1).float() if dev else tensor.ravel()
-        codebook = (build_kmeans_codebook(flat, n_clusters) if use_kmeans
-                    else build_uniform_codebook(flat, n_clusters))
-        indices = chunked_assign(flat, codebook)
-        recon = codebook[indices.long()] if dev else codebook[indices]
+        if vector_dim > 1:
+            if group_size:
+                raise NotImplementedError("the per-group affine is fitted for scalar codebooks")
+            if not dev:
+                raise RuntimeError("the pair encoder takes a device tensor")
+            codebook, indices = build_vector_codebook_and_assign(tensor, n_clusters, vector_dim)
+            recon = codebook[indices.reshape(-1).long()].reshape(-1)
+        else:
+            codebook = (build_kmeans_codebook(flat, n_clusters) if use_kmeans
+                        else build_uniform_codebook(flat, n_clusters))
+            indices = chunked_assign(flat, codebook)
+            recon = codebook[indices.long()] if dev else codebook[indices]
         positions = values = None
         if sidecar_enabled:
             positions, values = find_outliers_percentile(tensor, percentile)
@@ -144,7 +158,7 @@ class CDNAv3Writer:
             patched[pos_t] = torch.as_tensor(values).to(patched.device).to(patched.dtype)
             cos_sc = cosine(flat, patched)
         cb_np = codebook.cpu().numpy() if dev else codebook
-        idx_np = (indices.cpu().numpy() if dev else indices).reshape(rows, cols)
+        idx_np = (indices.cpu().numpy() if dev else indices).reshape(rows, cols // max(1, vector_dim))
         if gscale is not None and dev:
             gscale, goffset = gscale.cpu().numpy(), goffset.cpu().numpy()
         out = self.write_quantized(

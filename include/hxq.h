@@ -432,6 +432,34 @@ int hxq_select_f32(const float *x, int64_t n, const int64_t *ranks, int32_t m, f
                    int32_t *nan_count, void *workspace, int64_t workspace_bytes,
                    hipStream_t stream);
 /*
+ * Pair-codebook (vector_dim 2) encoder steps, with the reference's numpy CPU
+ * arithmetic reproduced bit for bit.  x is fp32 [n, 2] (adjacent column
+ * pairs of the weight), the codebook fp32 [k, 2], 1 <= k <= 4096.
+ *
+ * hxq_vq2_assign: indices[i] = argmin_j fl(fl(|x_i|^2 + |c_j|^2) - 2 x_i.c_j)
+ *   with |v|^2 = fl(fl(v0 v0) + fl(v1 v1)), x.c = fma(x1, c1, fl(x0 c0)),
+ *   first index on ties.  workspace >= 16 * k bytes.
+ *   Replaces: the assignment of _vector_kmeans (helix_substrate/
+ *   hxq_encoder.py:280-289, 305-313) and CDNAv3Writer._chunked_vector_assign
+ *   (helix_substrate/hxq_writer_v3.py:373-420).
+ * hxq_vq2_update: new_centroids[j] = fp32(sum of the pairs assigned to j /
+ *   fp32 count) with fp64 sums (a fixed-order two-level sum), or centroids[j]
+ *   if none is; *max_delta (device fp32) = max |new - old|.  indices < k.
+ *   workspace >= hxq_vq2_workspace_bytes(n, k) (at most about 42 MB at
+ *   k = 4096).  new_centroids must not alias centroids.
+ *   Replaces: the bincount update of _vector_kmeans
+ *   (helix_substrate/hxq_encoder.py:291-303).
+ * The k-means++ seeding (a sequential RandomState(42) stream) stays on the
+ * host, as in the reference.
+ */
+int64_t hxq_vq2_workspace_bytes(int64_t n, int32_t k);
+int hxq_vq2_assign(const float *x, int64_t n, const float *codebook, int32_t k,
+                   uint16_t *indices, void *workspace, int64_t workspace_bytes,
+                   hipStream_t stream);
+int hxq_vq2_update(const float *x, int64_t n, const uint16_t *indices, int32_t k,
+                   const float *centroids, float *new_centroids, float *max_delta,
+                   void *workspace, int64_t workspace_bytes, hipStream_t stream);
+/*
  * hxq_affine_fit: per-group affine of the encoder (an extension with no
  * reference counterpart: the benchmark configs' group_scale / group_offset,
  * fp32 [rows, cols / group_size]).  For each row and group of group_size

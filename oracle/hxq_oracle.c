@@ -20,6 +20,19 @@
  *                            (helix_linear.py:809-820, triton_vq_matmul.py:521).
  *   hxq_oracle_ssm_scan_f64  sequential_scan (mamba_scan_chunked.py:42-86),
  *                            evaluated in fp64 from fp32 inputs.
+ *   hxq_oracle_vq2_assign    the pair (vector_dim 2) nearest-centroid step of
+ *                            _vector_kmeans / _chunked_vector_assign
+ *                            (hxq_encoder.py:280-289, hxq_writer_v3.py:409-418):
+ *                            argmin_j fl(fl(|x|^2 + |c_j|^2) - 2 x.c_j) in fp32,
+ *                            |v|^2 = fl(fl(v0*v0) + fl(v1*v1)) (np.sum of the
+ *                            squares) and x.c = fma(x1, c1, fl(x0*c0)) (the
+ *                            rounding numpy's sgemm gives a K = 2 product);
+ *                            first index on ties (np.argmin).
+ *   hxq_oracle_vq2_update    the centroid update of the same loop
+ *                            (hxq_encoder.py:291-298): fp64 sums in index order
+ *                            (np.bincount with weights), counts as fp32, new =
+ *                            fp32(sum / count), empty clusters keep the old
+ *                            centroid; also max |new - old| (fp32).
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; contraction must stay off
  * so the affine step keeps its two roundings).
@@ -28,6 +41,7 @@
 #include <stddef.h>
 #include <math.h>
 #include <string.h>
+#include <stdlib.h>
 
 int hxq_oracle_version(void) { return 1; }
 
@@ -147,5 +161,71 @@ int hxq_oracle_ssm_scan_f64(const float *h0, const float *dt, const float *A,
             }
         }
     }
+    return 0;
+}
+
+int hxq_oracle_vq2_assign(const float *x, int64_t n, const float *cb, int32_t k, int32_t *out)
+{
+    if (n < 0 || k < 1)
+        return 1;
+    for (int64_t i = 0; i < n; ++i) {
+        const float x0 = x[2 * i], x1 = x[2 * i + 1];
+        const float xsq = x0 * x0 + x1 * x1;
+        float best = 0.0f;
+        int32_t bj = 0;
+        for (int32_t j = 0; j < k; ++j) {
+            const float c0 = cb[2 * j], c1 = cb[2 * j + 1];
+            const float csq = c0 * c0 + c1 * c1;
+            const float dot = fmaf(x1, c1, x0 * c0);
+            const float d = (xsq + csq) - 2.0f * dot;
+            if (j == 0 || d < best) {
+                best = d;
+                bj = j;
+            }
+        }
+        out[i] = bj;
+    }
+    return 0;
+}
+
+int hxq_oracle_vq2_update(const float *x, int64_t n, const int32_t *idx, int32_t k,
+                          const float *old, float *out, float *max_delta)
+{
+    if (n < 0 || k < 1)
+        return 1;
+    double *sum = (double *)calloc((size_t)k * 2, sizeof(double));
+    int64_t *cnt = (int64_t *)calloc((size_t)k, sizeof(int64_t));
+    if (!sum || !cnt) {
+        free(sum);
+        free(cnt);
+        return 2;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t j = idx[i];
+        if (j < 0 || j >= k) {
+            free(sum);
+            free(cnt);
+            return 3;
+        }
+        sum[2 * j] += (double)x[2 * i];
+        sum[2 * j + 1] += (double)x[2 * i + 1];
+        cnt[j] += 1;
+    }
+    float md = 0.0f;
+    for (int32_t j = 0; j < k; ++j) {
+        for (int dd = 0; dd < 2; ++dd) {
+            const float o = old[2 * j + dd];
+            float v = o;
+            if (cnt[j] > 0)
+                v = (float)(sum[2 * j + dd] / (double)(float)cnt[j]);
+            out[2 * j + dd] = v;
+            const float dlt = fabsf(v - o);
+            if (dlt > md)
+                md = dlt;
+        }
+    }
+    *max_delta = md;
+    free(sum);
+    free(cnt);
     return 0;
 }

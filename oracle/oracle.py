@@ -34,6 +34,12 @@ Reference functions restated (file:line under the reference checkout):
   (``hxq_encoder.py:107-177``, ``hxq_writer_v3.py:162-226, 427-467``,
   ``generate_sidecars_v3.py:18-40``), and ``mean_f32`` / ``percentile_f32``
   / ``percentiles_f64`` -- exact restatements of the numpy arithmetic it uses.
+* ``vq2_assign`` / ``vq2_update`` (C) / ``kmeanspp_init_np`` /
+  ``vector_kmeans_np`` / ``build_vector_codebook_np`` -- the pair-codebook
+  (vector_dim 2) encoder's CPU algorithm (``hxq_encoder.py:210-315``,
+  ``hxq_writer_v3.py:338-420``); ``vq2_assign_expr_np`` /
+  ``vq2_update_expr_np`` run the reference's own numpy expressions and pin
+  the C steps.
 * ``affine_fit_np`` -- the encoder's per-group affine fit (an extension of
   the format; fixed-order fp64 least squares, stated at the function).
 * ``pack_12bit_np`` / ``unpack_12bit_np`` / ``unpack_6bit_np`` /
@@ -81,6 +87,10 @@ def _load():
         lib.hxq_oracle_ssm_scan_f64.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, I64,
                                                 I64, I64, P, P]
         lib.hxq_oracle_ssm_scan_f64.restype = ctypes.c_int
+        lib.hxq_oracle_vq2_assign.argtypes = [P, I64, P, ctypes.c_int32, P]
+        lib.hxq_oracle_vq2_assign.restype = ctypes.c_int
+        lib.hxq_oracle_vq2_update.argtypes = [P, I64, P, ctypes.c_int32, P, P, P]
+        lib.hxq_oracle_vq2_update.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -463,6 +473,118 @@ def kmeans_sample_np(flat, max_samples=500_000):
     if flat.size <= max_samples:
         return flat
     return flat[np.random.RandomState(42).choice(flat.size, max_samples, replace=False)]
+
+
+def vq2_assign(x, codebook):
+    """C restatement of the pair nearest-centroid step (hxq_oracle.c):
+    x fp32 [n, 2], codebook fp32 [k, 2] -> int32 [n]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, 2)
+    cb = np.ascontiguousarray(codebook, np.float32).reshape(-1, 2)
+    out = np.empty(len(x), np.int32)
+    rc = _load().hxq_oracle_vq2_assign(_ptr(x), len(x), _ptr(cb), len(cb), _ptr(out))
+    if rc:
+        raise ValueError(f"hxq_oracle_vq2_assign: {rc}")
+    return out
+
+
+def vq2_assign_expr_np(x, codebook, chunk=50_000):
+    """The reference's numpy expression for the same step, as written at
+    hxq_encoder.py:282-289 (matmul trick, np.argmin); runs numpy's BLAS."""
+    x = np.asarray(x, np.float32).reshape(-1, 2)
+    cb = np.asarray(codebook, np.float32).reshape(-1, 2)
+    c_sq = np.sum(cb ** 2, axis=1, keepdims=True).T
+    out = np.empty(len(x), np.int32)
+    for s in range(0, len(x), chunk):
+        xc = x[s:s + chunk]
+        x_sq = np.sum(xc ** 2, axis=1, keepdims=True)
+        out[s:s + chunk] = np.argmin(x_sq + c_sq - 2.0 * (xc @ cb.T), axis=1)
+    return out
+
+
+def vq2_update(x, assignments, centroids):
+    """C restatement of the centroid update (hxq_encoder.py:291-300):
+    returns (new centroids fp32 [k, 2], max |new - old| as a float)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, 2)
+    a = np.ascontiguousarray(assignments, np.int32)
+    old = np.ascontiguousarray(centroids, np.float32).reshape(-1, 2)
+    new = np.empty_like(old)
+    md = np.zeros(1, np.float32)
+    rc = _load().hxq_oracle_vq2_update(_ptr(x), len(x), _ptr(a), len(old), _ptr(old), _ptr(new),
+                                       _ptr(md))
+    if rc:
+        raise ValueError(f"hxq_oracle_vq2_update: {rc}")
+    return new, float(md[0])
+
+
+def vq2_update_expr_np(x, assignments, centroids):
+    """The reference's numpy expression for the update (np.bincount)."""
+    x = np.asarray(x, np.float32).reshape(-1, 2)
+    old = np.asarray(centroids, np.float32).reshape(-1, 2)
+    k = len(old)
+    counts = np.bincount(assignments, minlength=k).astype(np.float32)
+    new = np.zeros_like(old)
+    for dim in range(2):
+        sums = np.bincount(assignments, weights=x[:, dim], minlength=k)
+        new[:, dim] = np.where(counts > 0, sums / np.maximum(counts, 1), old[:, dim])
+    return new, float(np.max(np.abs(new - old)))
+
+
+def kmeanspp_init_np(data, n_clusters):
+    """k-means++ seeding of _vector_kmeans (hxq_encoder.py:235-256): the
+    RandomState(42) stream, at most 64 distance-weighted draws (on a 100000
+    subsample above that many rows), the rest uniform rows."""
+    data = np.asarray(data, np.float32)
+    n, d = data.shape
+    rs = np.random.RandomState(42)
+    cent = np.zeros((n_clusters, d), np.float32)
+    cent[0] = data[rs.randint(n)]
+    for i in range(1, min(n_clusters, 64)):
+        c = cent[:i]
+        sub = data[rs.choice(n, 100000, replace=False)] if n > 100000 else data
+        dist = (np.sum(sub ** 2, axis=1, keepdims=True) + np.sum(c ** 2, axis=1, keepdims=True).T
+                - 2.0 * (sub @ c.T))
+        np.maximum(dist, 0, out=dist)
+        m = dist.min(axis=1)
+        cent[i] = sub[rs.choice(len(sub), p=m / max(m.sum(), 1e-30))]
+    if n_clusters > 64:
+        cent[64:] = data[rs.choice(n, n_clusters - 64, replace=False)]
+    return cent
+
+
+def vector_kmeans_np(data, n_clusters, max_iters=10, rtol=0.001):
+    """_vector_kmeans, CPU branch (hxq_encoder.py:210-315) for d = 2, with
+    the assignment and update steps of the C restatement.  Stops when the
+    largest move is below rtol * (max - min of the seeds), keeping the
+    centroids of before that update.  Returns (centroids, assignments of the
+    final pass, update steps taken)."""
+    data = np.asarray(data, np.float32).reshape(-1, 2)
+    k = min(n_clusters, len(data))
+    cent = kmeanspp_init_np(data, k)
+    cb_range = float(cent.max() - cent.min())
+    abs_tol = rtol * (cb_range if cb_range >= 1e-30 else 1.0)
+    steps = 0
+    for _ in range(max_iters):
+        steps += 1
+        new, md = vq2_update(data, vq2_assign(data, cent), cent)
+        if md < abs_tol:
+            break
+        cent = new
+    return cent, vq2_assign(data, cent), steps
+
+
+def build_vector_codebook_np(tensor, n_clusters, max_samples=500_000, max_iters=10):
+    """CDNAv3Writer._build_vector_codebook_and_assign for vector_dim 2
+    (hxq_writer_v3.py:338-371): fit on a RandomState(42) subsample of at most
+    max_samples pairs, then assign every pair.  Returns (codebook [k, 2],
+    indices uint16 [rows, cols / 2])."""
+    tensor = np.asarray(tensor, np.float32)
+    rows, cols = tensor.shape
+    vec = tensor.reshape(-1, 2)
+    fit = vec
+    if len(vec) > max_samples:
+        fit = vec[np.random.RandomState(42).choice(len(vec), max_samples, replace=False)]
+    cb, _, _ = vector_kmeans_np(fit, n_clusters, max_iters=max_iters)
+    return cb, vq2_assign(vec, cb).astype(np.uint16).reshape(rows, cols // 2)
 
 
 def find_outliers_percentile_np(tensor, percentile=99.9):

@@ -228,3 +228,110 @@ def test_write_tensor_with_affine(tmp_path):
         W, oracle.reconstruct(idx_o, cb_o, s_o, o_o, 128, pos_o, val_o.astype(np.float16).astype(np.float32)))
     # the fit can only lower the squared error of the codebook reconstruction
     assert st_aff["cosine_no_sidecar"] >= st_plain["cosine_no_sidecar"]
+
+
+# ---------------------------------------------------------------------------
+# pair codebook (vector_dim 2)
+# ---------------------------------------------------------------------------
+
+def _pairs(rs, n, scale=0.02):
+    return (rs.standard_t(5, (n, 2)) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("k", [1, 7, 256, 1000])
+def test_vq2_steps_match_reference_numpy_expressions(k):
+    # The C steps against the reference's own numpy expressions (BLAS matmul
+    # form of the distances, np.argmin, np.bincount update), bit for bit.
+    rs = np.random.RandomState(5 + k)
+    x = _pairs(rs, 40000)
+    cb = _pairs(rs, k)
+    if k >= 7:
+        cb[3] = cb[1]                     # duplicated entry: ties go to the lower index
+        x[:50] = cb[1]
+    a = oracle.vq2_assign(x, cb)
+    np.testing.assert_array_equal(a, oracle.vq2_assign_expr_np(x, cb))
+    if k >= 7:
+        assert not np.any(a == 3)
+    empty = np.where(np.bincount(a, minlength=k) == 0)[0]
+    new, md = oracle.vq2_update(x, a, cb)
+    new2, md2 = oracle.vq2_update_expr_np(x, a, cb)
+    np.testing.assert_array_equal(new, new2)
+    assert md == md2
+    np.testing.assert_array_equal(new[empty], cb[empty])   # empty clusters stay
+
+
+def test_vq2_assign_is_nearest_within_rounding():
+    # Brute force in fp64: the pick is the exact nearest entry up to the fp32
+    # rounding of the matmul-form distance (|x|^2 + |c|^2 ~ 1e-3 here).
+    rs = np.random.RandomState(9)
+    x = _pairs(rs, 5000)
+    cb = _pairs(rs, 300)
+    a = oracle.vq2_assign(x, cb)
+    d = ((x[:, None, :].astype(np.float64) - cb[None].astype(np.float64)) ** 2).sum(-1)
+    gap = d[np.arange(len(x)), a] - d.min(1)
+    assert gap.max() <= 4e-9
+    assert np.mean(a == d.argmin(1)) > 0.99
+
+
+def test_vq2_update_known_answer():
+    x = np.array([[1, 2], [3, 4], [10, 10], [5, 6]], np.float32)
+    a = np.array([0, 0, 2, 0], np.int32)
+    old = np.array([[0, 0], [7, 7], [9, 9]], np.float32)
+    new, md = oracle.vq2_update(x, a, old)
+    np.testing.assert_array_equal(new, np.array([[3, 4], [7, 7], [10, 10]], np.float32))
+    assert md == 4.0
+
+
+def test_vector_kmeans_oracle_recovers_separated_clusters():
+    # 24 tight clusters far apart: k-means++ seeds one point per cluster (the
+    # draws are proportional to squared distance).  The first update moves
+    # each seed to its cluster mean by ~1e-3 < rtol * range (5e-3), so the
+    # loop stops after one update and keeps the seeds (the reference's
+    # convergence test discards that last update).
+    rs = np.random.RandomState(3)
+    centers = np.stack(np.meshgrid(np.arange(6), np.arange(4)), -1).reshape(-1, 2).astype(np.float32)
+    lab = rs.randint(0, 24, 4800)
+    x = (centers[lab] + rs.standard_normal((4800, 2)).astype(np.float32) * 1e-3).astype(np.float32)
+    cb, a, steps = oracle.vector_kmeans_np(x, 24)
+    assert steps == 1
+    np.testing.assert_array_equal(cb, oracle.kmeanspp_init_np(x, 24))
+    for j in range(24):
+        members = lab[a == j]              # one true center per cluster
+        assert members.size > 0 and np.all(members == members[0])
+        assert np.any(np.all(x[a == j] == cb[j], axis=1))   # the seed is a member
+        np.testing.assert_allclose(cb[j], centers[members[0]], atol=5e-3)
+    # with a tighter tolerance the loop runs on and lands on the means
+    cb2, a2, steps2 = oracle.vector_kmeans_np(x, 24, rtol=1e-9)
+    assert steps2 >= 2
+    np.testing.assert_array_equal(a2, a)
+    for j in range(24):
+        np.testing.assert_allclose(cb2[j], x[a == j].astype(np.float64).mean(0), atol=1e-6)
+
+
+def test_vector_kmeans_oracle_seeding():
+    # seeding: the first seed is RandomState(42).randint(n)'s row; more than 64
+    # clusters: seeds 64.. are distinct rows (no replacement)
+    rs = np.random.RandomState(4)
+    x = _pairs(rs, 3000)
+    seeds = oracle.kmeanspp_init_np(x, 200)
+    np.testing.assert_array_equal(seeds[0], x[np.random.RandomState(42).randint(3000)])
+    rows = {tuple(r) for r in x.tolist()}
+    assert all(tuple(s) in rows for s in seeds.tolist())
+    assert len({tuple(s) for s in seeds[64:].tolist()}) == 136
+
+
+def test_vector_seeding_product_matches_oracle():
+    from helix_substrate.hxq_encoder import kmeanspp_init
+
+    rs = np.random.RandomState(6)
+    for n, k in [(5000, 40), (120000, 100)]:
+        x = _pairs(rs, n)
+        np.testing.assert_array_equal(kmeanspp_init(x, k), oracle.kmeanspp_init_np(x, k))
+
+
+def test_pair_writer_takes_device_tensors(tmp_path):
+    from helix_substrate.hxq_writer_v3 import CDNAv3Writer
+
+    with pytest.raises(RuntimeError):
+        CDNAv3Writer(tmp_path).write_tensor(np.zeros((4, 8), np.float32), "w", n_clusters=16,
+                                            vector_dim=2)

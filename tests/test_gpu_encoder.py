@@ -194,3 +194,100 @@ def test_write_tensor_affine_gpu_matches_cpu(dev, tmp_path):
     for f in ("codebook.npy", "indices.bin", "group_scale.npy", "group_offset.npy"):
         assert (tmp_path / "gpu" / "m_weight.cdnav3" / f).read_bytes() == \
             (tmp_path / "cpu" / "m_weight.cdnav3" / f).read_bytes(), f
+
+
+# ---------------------------------------------------------------------------
+# pair codebook (vector_dim 2)
+# ---------------------------------------------------------------------------
+
+def _pairs(rs, n, scale=0.02):
+    return (rs.standard_t(5, (n, 2)) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (1000, 37), (300_001, 256), (4_300_000, 64), (70_000, 4096)])
+def test_vq2_assign_matches_oracle(dev, n, k):
+    print(f"vq2_assign n={n} k={k}", flush=True)
+    rs = np.random.RandomState(n % 1000 + k)
+    x = _pairs(rs, n)
+    cb = _pairs(rs, k)
+    if k >= 37:
+        cb[5] = cb[2]                                   # tie: the lower index wins
+        x[: min(n, 100)] = cb[2]
+    got = _hxq.vq2_assign(torch.from_numpy(x).to(dev), torch.from_numpy(cb).to(dev))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy().astype(np.int32), oracle.vq2_assign(x, cb))
+
+
+@pytest.mark.parametrize("n,k", [(5, 3), (4000, 37), (500_000, 4096), (1_300_000, 1000)])
+def test_vq2_update_matches_oracle(dev, n, k):
+    print(f"vq2_update n={n} k={k}", flush=True)
+    rs = np.random.RandomState(k)
+    x = _pairs(rs, n)
+    old = _pairs(rs, k)
+    a = rs.randint(0, max(1, k - 2), n).astype(np.int32)   # the last clusters stay empty
+    new, md = _hxq.vq2_update(torch.from_numpy(x).to(dev), torch.from_numpy(a.astype(np.int16)).to(dev),
+                              torch.from_numpy(old).to(dev))
+    torch.cuda.synchronize()
+    want, wmd = oracle.vq2_update(x, a, old)
+    np.testing.assert_array_equal(new.cpu().numpy(), want)
+    assert float(md.item()) == wmd
+    # a second call on the same workspace-free path clears max_delta itself
+    new2, md2 = _hxq.vq2_update(torch.from_numpy(x).to(dev),
+                                torch.from_numpy(a.astype(np.int16)).to(dev),
+                                torch.from_numpy(want).to(dev))
+    torch.cuda.synchronize()
+    assert float(md2.item()) == 0.0
+    np.testing.assert_array_equal(new2.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("n,k", [(20_000, 4096), (150_000, 256), (3_000, 100)])
+def test_vector_kmeans_matches_oracle(dev, n, k):
+    print(f"vector_kmeans n={n} k={k}", flush=True)
+    rs = np.random.RandomState(n + k)
+    x = _pairs(rs, n)
+    cb, a, steps = hxq_encoder.vector_kmeans(torch.from_numpy(x).to(dev), k)
+    torch.cuda.synchronize()
+    wcb, wa, wsteps = oracle.vector_kmeans_np(x, k)
+    assert steps == wsteps
+    np.testing.assert_array_equal(cb.cpu().numpy(), wcb)
+    np.testing.assert_array_equal(a.cpu().numpy().astype(np.int32), wa)
+
+
+def test_vector_codebook_subsample_matches_oracle(dev):
+    # 614400 pairs > 500000: the fit runs on the RandomState(42) subsample
+    print("build_vector_codebook_and_assign 1024x1200 k=256", flush=True)
+    rs = np.random.RandomState(21)
+    w = (rs.standard_t(5, (1024, 1200)) * 0.02).astype(np.float32)
+    cb, idx = hxq_encoder.build_vector_codebook_and_assign(torch.from_numpy(w).to(dev), 256)
+    torch.cuda.synchronize()
+    wcb, widx = oracle.build_vector_codebook_np(w, 256)
+    np.testing.assert_array_equal(cb.cpu().numpy(), wcb)
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.uint16), widx)
+
+
+def test_write_tensor_pairs_round_trip(dev, tmp_path):
+    # writer (vector_dim 2) -> files -> reader -> pair HelixLinear on the GPU
+    print("write_tensor vector_dim=2 128x512 k=4096", flush=True)
+    from helix_substrate.helix_linear import load_helix_linear_from_cdnav3
+    from helix_substrate.hxq_reader_v3 import CDNAv3Reader
+
+    rs = np.random.RandomState(8)
+    w = (rs.standard_t(5, (128, 512)) * 0.02).astype(np.float32)
+    st = CDNAv3Writer(tmp_path).write_tensor(torch.from_numpy(w).to(dev), "layer.w",
+                                             n_clusters=4096, vector_dim=2)
+    d = tmp_path / "layer_w.cdnav3"
+    wcb, widx = oracle.build_vector_codebook_np(w, 4096)
+    np.testing.assert_array_equal(np.load(d / "codebook.npy"), wcb)
+    np.testing.assert_array_equal(np.fromfile(d / "indices.bin", np.uint16).reshape(128, 256), widx)
+    pos, val = oracle.find_outliers_percentile_np(w, 99.9)
+    assert st["num_outliers"] == len(pos) and st["cosine_with_sidecar"] >= st["cosine_no_sidecar"]
+    want = wcb[widx].reshape(128, 512).copy()
+    want.reshape(-1)[pos] = val.astype(np.float16).astype(np.float32)   # fp16 on disk
+    r = CDNAv3Reader(d)
+    assert r.vector_dim == 2
+    np.testing.assert_array_equal(r.reconstruct(), want)
+    layer = load_helix_linear_from_cdnav3(d).to(dev)
+    x = rs.standard_normal((3, 512)).astype(np.float32)
+    y = layer(torch.from_numpy(x).to(dev)).float().cpu().numpy()
+    ref = oracle.linear_f64(x, want)
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref)) + 1e-6
