@@ -770,9 +770,9 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
     pairs, 4096-entry codebook fitted on the writer's 500K-pair subsample
     (k-means++ seeding on the host, up to 10 Lloyd steps on the device), then
     every pair assigned.  The assignment kernel is VALU-bound: 7 fp32 vector
-    instructions per (pair, entry) (mul, fma, add, fma, compare, two selects),
-    so 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz / 7 = 5.62e12 pair-entry
-    distances/s is its roof."""
+    instructions per (pair, entry) (mul, fma, add, fma, compare, two selects)
+    against MI355X's 157.3 TFLOP/s fp32 vector peak = 78.6e12 lane operations/s,
+    so 11.2e12 pair-entry distances/s is its roof."""
     import numpy as np
     import torch
     from helix_substrate import _hxq, hxq_encoder
@@ -818,7 +818,7 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
     torch.cuda.synchronize(dev)
     launch_ms = e0.elapsed_time(e1) / 5
     dist = vec.shape[0] * k
-    roof = 256 * 4 * 16 * 2.4e9 / 7
+    roof = 157.3e12 / 2 / 7
     res = {"tensor": [rows, cols], "pairs": int(vec.shape[0]), "codebook": [k, 2],
            "fit_sample": hxq_encoder.KMEANS_MAX_SAMPLES, "lloyd_steps": int(steps[0]),
            "ms_per_tensor": round(ms, 2), **{kk: round(v, 2) for kk, v in stages.items()},

@@ -702,10 +702,13 @@ __global__ __launch_bounds__(256) void pair_table_kernel(const float *__restrict
 
 // V pairs per thread (pair i = block base + threadIdx.x + v * kPairThreads);
 // the table is staged once per block in LDS and read as a broadcast.
-template <int V>
+// MIN: writes dmin[i] = max(min_j d_j, 0) instead of the index (the k-means++
+// seeding distance, np.maximum(d, 0).min(axis=1)), for the rows rows[i] of x
+// when rows is given (an out-of-range row gives NaN).
+template <int V, bool MIN>
 __global__ __launch_bounds__(kPairThreads) void pair_assign_kernel(
-    const float2 *__restrict__ x, int64_t n, const float4 *__restrict__ tab, int k,
-    uint16_t *__restrict__ idx) {
+    const float2 *__restrict__ x, int64_t n, const int64_t *__restrict__ rows, int64_t m,
+    const float4 *__restrict__ tab, int k, uint16_t *__restrict__ idx, float *__restrict__ dmin) {
 #pragma clang fp contract(off)
     extern __shared__ float4 stab[];
     for (int j = threadIdx.x; j < k; j += kPairThreads) stab[j] = tab[j];
@@ -717,7 +720,10 @@ __global__ __launch_bounds__(kPairThreads) void pair_assign_kernel(
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         const int64_t i = base + static_cast<int64_t>(v) * kPairThreads;
-        const float2 p = i < n ? x[i] : make_float2(0.0f, 0.0f);
+        int64_t r = i;
+        if (MIN && rows != nullptr && i < m) r = rows[i];
+        float2 p = make_float2(0.0f, 0.0f);
+        if (i < m) p = (r >= 0 && r < n) ? x[r] : make_float2(NAN, NAN);
         x0[v] = p.x;
         x1[v] = p.y;
         xsq[v] = p.x * p.x + p.y * p.y;
@@ -738,7 +744,12 @@ __global__ __launch_bounds__(kPairThreads) void pair_assign_kernel(
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         const int64_t i = base + static_cast<int64_t>(v) * kPairThreads;
-        if (i < n) idx[i] = static_cast<uint16_t>(bj[v]);
+        if (i < m) {
+            if (MIN)
+                dmin[i] = best[v] >= 0.0f || best[v] != best[v] ? best[v] : 0.0f;
+            else
+                idx[i] = static_cast<uint16_t>(bj[v]);
+        }
     }
 }
 
@@ -1095,6 +1106,25 @@ static int pair_table(const float *codebook, int32_t k, float4 *tab, hipStream_t
     return HXQ_OK;
 }
 
+template <bool MIN>
+static int pair_launch(const float2 *x, int64_t n, const int64_t *rows, int64_t m,
+                       const float4 *tab, int32_t k, uint16_t *indices, float *dmin,
+                       hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(k) * sizeof(float4);
+    const int64_t big = (m + kPairThreads * 8 - 1) / (kPairThreads * 8);
+    if (big >= 1024) {
+        HXQ_REQUIRE(big < (int64_t{1} << 31), "too many pairs");
+        hipLaunchKernelGGL((pair_assign_kernel<8, MIN>), dim3(static_cast<uint32_t>(big)),
+                           dim3(kPairThreads), lds, stream, x, n, rows, m, tab, k, indices, dmin);
+    } else {
+        const int64_t g = (m + kPairThreads * 2 - 1) / (kPairThreads * 2);
+        hipLaunchKernelGGL((pair_assign_kernel<2, MIN>), dim3(static_cast<uint32_t>(g)),
+                           dim3(kPairThreads), lds, stream, x, n, rows, m, tab, k, indices, dmin);
+    }
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
 extern "C" int hxq_vq2_assign(const float *x, int64_t n, const float *codebook, int32_t k,
                               uint16_t *indices, void *workspace, int64_t workspace_bytes,
                               hipStream_t stream) {
@@ -1106,20 +1136,24 @@ extern "C" int hxq_vq2_assign(const float *x, int64_t n, const float *codebook, 
     float4 *tab = static_cast<float4 *>(workspace);
     const int rc = pair_table(codebook, k, tab, stream);
     if (rc != HXQ_OK) return rc;
-    const size_t lds = static_cast<size_t>(k) * sizeof(float4);
-    const auto *xv = reinterpret_cast<const float2 *>(x);
-    const int64_t big = (n + kPairThreads * 8 - 1) / (kPairThreads * 8);
-    if (big >= 1024) {
-        HXQ_REQUIRE(big < (int64_t{1} << 31), "too many pairs");
-        hipLaunchKernelGGL(pair_assign_kernel<8>, dim3(static_cast<uint32_t>(big)),
-                           dim3(kPairThreads), lds, stream, xv, n, tab, k, indices);
-    } else {
-        const int64_t g = (n + kPairThreads * 2 - 1) / (kPairThreads * 2);
-        hipLaunchKernelGGL(pair_assign_kernel<2>, dim3(static_cast<uint32_t>(g)),
-                           dim3(kPairThreads), lds, stream, xv, n, tab, k, indices);
-    }
-    HXQ_LAUNCH_CHECK();
-    return HXQ_OK;
+    return pair_launch<false>(reinterpret_cast<const float2 *>(x), n, nullptr, n, tab, k, indices,
+                              nullptr, stream);
+}
+
+extern "C" int hxq_vq2_min_dist(const float *x, int64_t n, const int64_t *rows, int64_t m,
+                                const float *codebook, int32_t k, float *dmin, void *workspace,
+                                int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && codebook && dmin && workspace, "x, codebook, dmin and workspace are required");
+    HXQ_REQUIRE(n >= 0 && m >= 0 && k >= 1 && k <= kPairMaxK, "k must be 1..4096");
+    HXQ_REQUIRE(rows != nullptr || m <= n, "without rows, m must be <= n");
+    HXQ_REQUIRE(workspace_bytes >= int64_t{16} * k, "workspace too small");
+    if (m == 0) return HXQ_OK;
+    float4 *tab = static_cast<float4 *>(workspace);
+    const int rc = pair_table(codebook, k, tab, stream);
+    if (rc != HXQ_OK) return rc;
+    return pair_launch<true>(reinterpret_cast<const float2 *>(x), n, rows, m, tab, k, nullptr, dmin,
+                             stream);
 }
 
 extern "C" int hxq_vq2_update(const float *x, int64_t n, const uint16_t *indices, int32_t k,

@@ -101,6 +101,7 @@ SIGNATURES = {
     "hxq_assign_nearest": [P, I64, P, I32, P, P],
     "hxq_vq2_assign": [P, I64, P, I32, P, P, I64, P],
     "hxq_vq2_update": [P, I64, P, I32, P, P, P, P, I64, P],
+    "hxq_vq2_min_dist": [P, I64, P, I64, P, I32, P, P, I64, P],
     "hxq_kmeans_init": [P, I64, P, I64, P, P],
     "hxq_kmeans_run": [P, I64, P, I32, I32, ctypes.c_double, P, I64, P, P, P, P],
     "hxq_select_f32": [P, I64, P, I32, P, P, P, I64, P],
@@ -712,6 +713,26 @@ def vq2_assign(x, codebook, out=None, workspace=None):
     rc = lib().hxq_vq2_assign(_ptr(x), n, _ptr(codebook), k, _ptr(out), _ptr(workspace),
                               workspace.numel(), _stream(x))
     _check("hxq_vq2_assign", rc)
+    return out
+
+
+def vq2_min_dist(x, codebook, rows=None, out=None, workspace=None):
+    """fp32 [m] = max(0, smallest distance from x[rows[i]] (all rows when rows
+    is None) to the codebook entries), the seeding distance of k-means++."""
+    _pair_args(x, codebook)
+    if rows is not None:
+        _need_device(rows)
+        if rows.dtype != torch.int64 or rows.dim() != 1:
+            raise ValueError("rows must be int64 [m]")
+    m = x.shape[0] if rows is None else rows.numel()
+    k = codebook.shape[0]
+    if out is None:
+        out = torch.empty(m, dtype=torch.float32, device=x.device)
+    if workspace is None:
+        workspace = torch.empty(16 * k, dtype=torch.uint8, device=x.device)
+    rc = lib().hxq_vq2_min_dist(_ptr(x), x.shape[0], _ptr(rows), m, _ptr(codebook), k, _ptr(out),
+                                _ptr(workspace), workspace.numel(), _stream(x))
+    _check("hxq_vq2_min_dist", rc)
     return out
 
 

@@ -13,9 +13,10 @@ The pair encoder (``vector_kmeans`` / ``build_vector_codebook_and_assign``,
 reference ``_vector_kmeans``, ``hxq_encoder.py:210-315``, and
 ``CDNAv3Writer._build_vector_codebook_and_assign``, ``hxq_writer_v3.py:
 338-420``) takes device tensors: the k-means++ seeding draws from the
-reference's RandomState(42) stream on the host (sequential, at most 64 draws),
-the Lloyd steps and the assignment of every pair run as HIP kernels that
-reproduce the reference's numpy CPU arithmetic.
+reference's RandomState(42) stream on the host (sequential, at most 64 draws)
+with its distances computed on the device; the Lloyd steps and the assignment
+of every pair run as HIP kernels; all reproduce the reference's numpy CPU
+arithmetic.
 """
 from __future__ import annotations
 
@@ -168,27 +169,35 @@ def fit_group_affine(w, indices, codebook, group_size=128, exclude_positions=Non
 
 
 def kmeanspp_init(data, n_clusters):
-    """k-means++ seeding of _vector_kmeans (hxq_encoder.py:235-256) on host
-    rows data (fp32 [n, d]): a RandomState(42) stream, the first seed a
-    uniform row, then up to 63 rows drawn with probability proportional to
-    the squared distance (matmul form, clipped at 0) to the nearest seed so
-    far -- on a fresh 100000-row subsample each draw when n > 100000 -- and
-    any further seeds uniform rows without replacement."""
-    data = np.asarray(data, dtype=np.float32)
-    n, d = data.shape
+    """k-means++ seeding of _vector_kmeans (hxq_encoder.py:235-256) for device
+    rows data (fp32 [n, 2]): a RandomState(42) stream, the first seed a
+    uniform row, then up to 63 rows drawn with probability proportional to the
+    squared distance (matmul form, clipped at 0) to the nearest seed so far --
+    on a fresh 100000-row subsample each draw when n > 100000 -- and any
+    further seeds uniform rows without replacement.  The draws run on the host
+    (the reference's sequential stream); the distances run on the device
+    (hxq_vq2_min_dist, the same fp32 arithmetic), the host sums them as numpy
+    does.  Returns the seeds as a host fp32 [n_clusters, 2] array."""
+    host = data.cpu().numpy()
+    n = host.shape[0]
     rs = np.random.RandomState(42)
-    seeds = np.zeros((n_clusters, d), dtype=np.float32)
-    seeds[0] = data[rs.randint(n)]
-    for i in range(1, min(n_clusters, 64)):
-        have = seeds[:i]
-        pool = data[rs.choice(n, 100000, replace=False)] if n > 100000 else data
-        d2 = (np.sum(pool ** 2, axis=1, keepdims=True) + np.sum(have ** 2, axis=1, keepdims=True).T
-              - 2.0 * (pool @ have.T))
-        np.maximum(d2, 0, out=d2)
-        nearest = d2.min(axis=1)
-        seeds[i] = pool[rs.choice(len(pool), p=nearest / max(nearest.sum(), 1e-30))]
+    seeds = np.zeros((n_clusters, 2), dtype=np.float32)
+    seeds[0] = host[rs.randint(n)]
+    n_draw = min(n_clusters, 64)
+    if n_draw > 1:
+        have = torch.empty(64, 2, dtype=torch.float32, device=data.device)
+        ws = torch.empty(16 * 64, dtype=torch.uint8, device=data.device)
+        dmin = torch.empty(min(n, 100000), dtype=torch.float32, device=data.device)
+        for i in range(1, n_draw):
+            have[:i].copy_(torch.from_numpy(seeds[:i]))
+            sel = rs.choice(n, 100000, replace=False) if n > 100000 else None
+            rows = None if sel is None else torch.from_numpy(sel).to(data.device)
+            _hxq.vq2_min_dist(data, have[:i], rows=rows, out=dmin, workspace=ws)
+            nearest = dmin.cpu().numpy()
+            pick = rs.choice(len(nearest), p=nearest / max(nearest.sum(), 1e-30))
+            seeds[i] = host[pick if sel is None else sel[pick]]
     if n_clusters > 64:
-        seeds[64:] = data[rs.choice(n, n_clusters - 64, replace=False)]
+        seeds[64:] = host[rs.choice(n, n_clusters - 64, replace=False)]
     return seeds
 
 
@@ -207,7 +216,7 @@ def vector_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
     k = min(int(n_clusters), n)
     if k < 1 or k > 4096:
         raise ValueError("pair codebooks hold 1..4096 entries")
-    seeds = kmeanspp_init(data.cpu().numpy(), k)
+    seeds = kmeanspp_init(data, k)
     rng = float(seeds.max() - seeds.min())
     abs_tol = rtol * (rng if rng >= 1e-30 else 1.0)
     cent = torch.from_numpy(seeds).to(data.device)

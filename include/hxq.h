@@ -449,13 +449,21 @@ int hxq_select_f32(const float *x, int64_t n, const int64_t *ranks, int32_t m, f
  *   k = 4096).  new_centroids must not alias centroids.
  *   Replaces: the bincount update of _vector_kmeans
  *   (helix_substrate/hxq_encoder.py:291-303).
- * The k-means++ seeding (a sequential RandomState(42) stream) stays on the
+ * hxq_vq2_min_dist: dmin[i] = max(0, min_j d(x[rows[i]], c_j)) (the same
+ *   fp32 distance; rows NULL: row i, m <= n) -- the seeding distances of the
+ *   k-means++ initialisation (helix_substrate/hxq_encoder.py:241-251,
+ *   np.maximum(dists, 0) then min over the seeds).  An out-of-range row gives
+ *   NaN.  workspace >= 16 * k bytes.
+ * The seeding's draws (a sequential RandomState(42) stream) stay on the
  * host, as in the reference.
  */
 int64_t hxq_vq2_workspace_bytes(int64_t n, int32_t k);
 int hxq_vq2_assign(const float *x, int64_t n, const float *codebook, int32_t k,
                    uint16_t *indices, void *workspace, int64_t workspace_bytes,
                    hipStream_t stream);
+int hxq_vq2_min_dist(const float *x, int64_t n, const int64_t *rows, int64_t m,
+                     const float *codebook, int32_t k, float *dmin, void *workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
 int hxq_vq2_update(const float *x, int64_t n, const uint16_t *indices, int32_t k,
                    const float *centroids, float *new_centroids, float *max_delta,
                    void *workspace, int64_t workspace_bytes, hipStream_t stream);

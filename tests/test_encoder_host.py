@@ -320,15 +320,6 @@ def test_vector_kmeans_oracle_seeding():
     assert len({tuple(s) for s in seeds[64:].tolist()}) == 136
 
 
-def test_vector_seeding_product_matches_oracle():
-    from helix_substrate.hxq_encoder import kmeanspp_init
-
-    rs = np.random.RandomState(6)
-    for n, k in [(5000, 40), (120000, 100)]:
-        x = _pairs(rs, n)
-        np.testing.assert_array_equal(kmeanspp_init(x, k), oracle.kmeanspp_init_np(x, k))
-
-
 def test_pair_writer_takes_device_tensors(tmp_path):
     from helix_substrate.hxq_writer_v3 import CDNAv3Writer
 

@@ -240,6 +240,46 @@ def test_vq2_update_matches_oracle(dev, n, k):
     np.testing.assert_array_equal(new2.cpu().numpy(), want)
 
 
+def test_seeding_distance_expression_on_this_host():
+    # the device seeding distance equals the reference's numpy expression as
+    # this host's BLAS evaluates it (the C step is that arithmetic)
+    rs = np.random.RandomState(12)
+    x = _pairs(rs, 30000)
+    for i in (1, 2, 17, 63):
+        c = _pairs(rs, i)
+        d = np.sum(x ** 2, axis=1, keepdims=True) + np.sum(c ** 2, axis=1, keepdims=True).T \
+            - 2.0 * (x @ c.T)
+        np.maximum(d, 0, out=d)
+        want = d.min(axis=1)
+        got = oracle.vq2_assign(x, c)
+        np.testing.assert_array_equal(d[np.arange(len(x)), got], want)
+
+
+@pytest.mark.parametrize("n,m,k", [(5000, None, 63), (400_000, 100_000, 17), (777, 3, 1)])
+def test_vq2_min_dist_matches_numpy(dev, n, m, k):
+    print(f"vq2_min_dist n={n} m={m} k={k}", flush=True)
+    rs = np.random.RandomState(n + k)
+    x = _pairs(rs, n)
+    c = _pairs(rs, k)
+    sel = None if m is None else rs.choice(n, m, replace=False)
+    sub = x if sel is None else x[sel]
+    d = np.sum(sub ** 2, axis=1, keepdims=True) + np.sum(c ** 2, axis=1, keepdims=True).T \
+        - 2.0 * (sub @ c.T)
+    np.maximum(d, 0, out=d)
+    rows = None if sel is None else torch.from_numpy(sel).to(dev)
+    got = _hxq.vq2_min_dist(torch.from_numpy(x).to(dev), torch.from_numpy(c).to(dev), rows=rows)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), d.min(axis=1))
+
+
+@pytest.mark.parametrize("n,k", [(5000, 40), (120_000, 100), (3, 7)])
+def test_vector_seeding_matches_oracle(dev, n, k):
+    print(f"kmeanspp_init n={n} k={k}", flush=True)
+    x = _pairs(np.random.RandomState(6 + n), n)
+    got = hxq_encoder.kmeanspp_init(torch.from_numpy(x).to(dev), min(k, n))
+    np.testing.assert_array_equal(got, oracle.kmeanspp_init_np(x, min(k, n)))
+
+
 @pytest.mark.parametrize("n,k", [(20_000, 4096), (150_000, 256), (3_000, 100)])
 def test_vector_kmeans_matches_oracle(dev, n, k):
     print(f"vector_kmeans n={n} k={k}", flush=True)
