@@ -769,7 +769,10 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
     """Pair-codebook (vector_dim 2) encode of the same gate_proj: 11.27M column
     pairs, 4096-entry codebook fitted on the writer's 500K-pair subsample
     (k-means++ seeding on the host, up to 10 Lloyd steps on the device), then
-    every pair assigned.  The assignment kernel is VALU-bound: 7 fp32 vector
+    every pair assigned.  ms_per_tensor is the steady state of a model's
+    tensors of one shape (the seeding's RandomState draws, which depend only
+    on the shape, are replayed once per shape; first_tensor_of_shape_ms
+    includes that replay).  The assignment kernel is VALU-bound: 7 fp32 vector
     instructions per (pair, entry) (mul, fma, add, fma, compare, two selects)
     against MI355X's 157.3 TFLOP/s fp32 vector peak = 78.6e12 lane operations/s,
     so 11.2e12 pair-entry distances/s is its roof."""
@@ -799,7 +802,10 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
             stages["assign_ms"] += (t2 - t1) * 1e3 / iters
         return cb, idx
 
+    hxq_encoder._seeding_stream.cache_clear()
+    t0 = time.perf_counter()
     cb, _ = encode(False)
+    first_ms = (time.perf_counter() - t0) * 1e3
     t0 = time.perf_counter()
     for _ in range(iters):
         encode(True)
@@ -822,6 +828,7 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
     res = {"tensor": [rows, cols], "pairs": int(vec.shape[0]), "codebook": [k, 2],
            "fit_sample": hxq_encoder.KMEANS_MAX_SAMPLES, "lloyd_steps": int(steps[0]),
            "ms_per_tensor": round(ms, 2), **{kk: round(v, 2) for kk, v in stages.items()},
+           "first_tensor_of_shape_ms": round(first_ms, 1),
            "assign_launch_ms": round(launch_ms, 3),
            "assign_gdist_per_s": round(dist / launch_ms / 1e6, 1),
            "assign_valu_frac": round(dist / (launch_ms * 1e-3) / roof, 3)}

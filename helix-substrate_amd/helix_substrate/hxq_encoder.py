@@ -168,21 +168,57 @@ def fit_group_affine(w, indices, codebook, group_size=128, exclude_positions=Non
     return scale.astype(np.float32), offset.astype(np.float32)
 
 
+@functools.lru_cache(maxsize=2)
+def _seeding_stream(n, n_clusters, device):
+    """The RandomState(42) draws of the k-means++ seeding for n rows.  They do
+    not depend on the data: randint(n), then per weighted draw a 100000-row
+    choice without replacement (n > 100000) and the one uniform double that
+    choice(len, p=...) consumes, then the uniform rows past 64.  Replayed once
+    per (n, n_clusters) and kept (host and device copies of the row sets)."""
+    rs = np.random.RandomState(42)
+    first = int(rs.randint(n))
+    n_draw = min(n_clusters, 64)
+    rows_h, us = [], []
+    for _ in range(1, n_draw):
+        rows_h.append(rs.choice(n, 100000, replace=False) if n > 100000 else None)
+        us.append(float(rs.random_sample()))
+    tail = rs.choice(n, n_clusters - 64, replace=False) if n_clusters > 64 else None
+    rows_d = None
+    if n > 100000 and rows_h:
+        rows_d = torch.from_numpy(np.stack(rows_h)).to(device)
+    return first, rows_h, rows_d, us, tail
+
+
+def _weighted_draw(p, u):
+    """RandomState.choice(len(p), p=p) given the uniform double u it draws:
+    the same checks, the fp64 cumulative sum normalised by its last value,
+    searchsorted to the right (numpy's mtrand choice)."""
+    atol = max(np.sqrt(np.finfo(np.float64).eps), np.sqrt(np.finfo(p.dtype).eps))
+    p64 = np.asarray(p, dtype=np.float64)
+    if np.any(p64 < 0):
+        raise ValueError("probabilities are not non-negative")
+    if abs(p64.sum() - 1.0) > atol:
+        raise ValueError("probabilities do not sum to 1")
+    cdf = p64.cumsum()
+    cdf /= cdf[-1]
+    return int(cdf.searchsorted(u, side="right"))
+
+
 def kmeanspp_init(data, n_clusters):
     """k-means++ seeding of _vector_kmeans (hxq_encoder.py:235-256) for device
     rows data (fp32 [n, 2]): a RandomState(42) stream, the first seed a
     uniform row, then up to 63 rows drawn with probability proportional to the
     squared distance (matmul form, clipped at 0) to the nearest seed so far --
     on a fresh 100000-row subsample each draw when n > 100000 -- and any
-    further seeds uniform rows without replacement.  The draws run on the host
-    (the reference's sequential stream); the distances run on the device
-    (hxq_vq2_min_dist, the same fp32 arithmetic), the host sums them as numpy
-    does.  Returns the seeds as a host fp32 [n_clusters, 2] array."""
+    further seeds uniform rows without replacement.  The stream's draws are
+    replayed on the host (cached per shape), the distances run on the device
+    (hxq_vq2_min_dist, the same fp32 arithmetic) and the host sums them as
+    numpy does.  Returns the seeds as a host fp32 [n_clusters, 2] array."""
     host = data.cpu().numpy()
     n = host.shape[0]
-    rs = np.random.RandomState(42)
+    first, rows_h, rows_d, us, tail = _seeding_stream(n, n_clusters, str(data.device))
     seeds = np.zeros((n_clusters, 2), dtype=np.float32)
-    seeds[0] = host[rs.randint(n)]
+    seeds[0] = host[first]
     n_draw = min(n_clusters, 64)
     if n_draw > 1:
         have = torch.empty(64, 2, dtype=torch.float32, device=data.device)
@@ -190,14 +226,13 @@ def kmeanspp_init(data, n_clusters):
         dmin = torch.empty(min(n, 100000), dtype=torch.float32, device=data.device)
         for i in range(1, n_draw):
             have[:i].copy_(torch.from_numpy(seeds[:i]))
-            sel = rs.choice(n, 100000, replace=False) if n > 100000 else None
-            rows = None if sel is None else torch.from_numpy(sel).to(data.device)
+            rows = None if rows_d is None else rows_d[i - 1]
             _hxq.vq2_min_dist(data, have[:i], rows=rows, out=dmin, workspace=ws)
             nearest = dmin.cpu().numpy()
-            pick = rs.choice(len(nearest), p=nearest / max(nearest.sum(), 1e-30))
-            seeds[i] = host[pick if sel is None else sel[pick]]
-    if n_clusters > 64:
-        seeds[64:] = host[rs.choice(n, n_clusters - 64, replace=False)]
+            pick = _weighted_draw(nearest / max(nearest.sum(), 1e-30), us[i - 1])
+            seeds[i] = host[pick if rows_h[i - 1] is None else rows_h[i - 1][pick]]
+    if tail is not None:
+        seeds[64:] = host[tail]
     return seeds
 
 

@@ -326,3 +326,28 @@ def test_pair_writer_takes_device_tensors(tmp_path):
     with pytest.raises(RuntimeError):
         CDNAv3Writer(tmp_path).write_tensor(np.zeros((4, 8), np.float32), "w", n_clusters=16,
                                             vector_dim=2)
+
+
+def test_seeding_stream_replay_matches_randomstate():
+    # the cached replay of the k-means++ draws equals RandomState(42) used the
+    # way the seeding uses it, with data-dependent probabilities in between
+    from helix_substrate.hxq_encoder import _seeding_stream, _weighted_draw
+
+    rs_p = np.random.RandomState(0)
+    for n, k in [(150_000, 70), (5000, 40)]:
+        first, rows_h, rows_d, us, tail = _seeding_stream(n, k, "cpu")
+        rs = np.random.RandomState(42)
+        assert rs.randint(n) == first
+        for i in range(1, min(k, 64)):
+            if n > 100000:
+                np.testing.assert_array_equal(rs.choice(n, 100000, replace=False), rows_h[i - 1])
+                np.testing.assert_array_equal(rows_d[i - 1].numpy(), rows_h[i - 1])
+            m = min(n, 100000)
+            w = (rs_p.random_sample(m) ** 8).astype(np.float32)
+            w[rs_p.randint(0, m, 50)] = 0
+            p = w / max(w.sum(), 1e-30)
+            assert rs.choice(m, p=p) == _weighted_draw(p, us[i - 1])
+        if k > 64:
+            np.testing.assert_array_equal(rs.choice(n, k - 64, replace=False), tail)
+    with pytest.raises(ValueError):
+        _weighted_draw(np.zeros(10, np.float32), 0.5)
