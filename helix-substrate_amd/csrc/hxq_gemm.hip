@@ -75,6 +75,8 @@ struct GemmArgs {
     void *y;              // [M, OUT]
     int32_t M, OUT, K, group, y_dtype, n_experts, x_rows, pad_;
     int32_t tiles_x, tiles_y, tiles_per_xcd, pad2_;  // dense: tile grid, XCD share
+    float *part;          // dense split-K: fp32 partials [ksplit, M, OUT] (ksplit > 1)
+    int32_t ksplit, ks_per;  // dense: K-step ranges (blockIdx.y = range), steps per range
 };
 
 // Dense tile order.  Blocks are dealt round-robin to the XCDs (block b runs on
@@ -160,7 +162,9 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
     const int cw = wave & 3;               // consumer: 64-column block of the tile
     const int pt = tid - kConsumers * 64;  // producer thread 0..kPT-1
     const int K = g.K;
-    const int nk = K / kBK;
+    // dense split-K: this block runs K-steps [kb, kb + nk) of the tile
+    const int kb = GROUPED ? 0 : static_cast<int>(blockIdx.y) * g.ks_per;
+    const int nk = GROUPED ? K / kBK : min(K / kBK - kb, g.ks_per);
 
     // ---- row tile -> (expert, first row, end row) --------------------------
     int e = 0, r0, r1;
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
         // prefetch absent and wait for it at the next use of the older stage.
         auto load_stage = [&](int ks, GemmStage<BM> &st) {
             const bool live = ks < nk;
-            const uint32_t k0 = (live ? ks : 0) * kBK;
+            const uint32_t k0 = (kb + (live ? ks : 0)) * kBK;
     #pragma unroll
             for (int p = 0; p < kXP; ++p)
                 st.a[p] = buf_load16(xr, (a_off[p] == kOob || !live) ? kOob : a_off[p] + k0 * 2);
@@ -409,7 +413,7 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
                         u32x4{pk[0], pk[1], pk[2], pk[3]};
                 }
             // sidecar: replace entries with column in this thread's [lo, lo + 16)
-            const int k0 = ks * kBK, lo = k0 + qc * 16, hi = lo + 16;
+            const int k0 = (kb + ks) * kBK, lo = k0 + qc * 16, hi = lo + 16;
             uint16_t *brow = &sB[buf][0];
     #pragma unroll
             for (int i = 0; i < kPRows; ++i) {
@@ -549,6 +553,22 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
             }
         }
         return;
+    } else if (!GROUPED && g.ksplit > 1) {
+        // split-K: this range's fp32 partial; the reduce kernel adds the
+        // ranges in order, then the bias
+        float *part = g.part + static_cast<int64_t>(blockIdx.y) * g.M * g.OUT;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + cw * 64 + j * 32 + (lane & 31);
+            if (n >= g.OUT) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                    if (m < nrows) part[(int64_t)(r0 + m) * g.OUT + n] = acc[i][j][r];
+                }
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -703,6 +723,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const 
     store_act<YDT>(y, (int64_t)t * hidden + c, acc);
 }
 
+// y = sum over the split-K ranges in range order (+ bias), in y's dtype.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part,
+                                                            int32_t ksplit, int64_t mn,
+                                                            int32_t out, const float *bias,
+                                                            void *y, int32_t y_dtype) {
+    const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+    if (i >= mn) return;
+    float v = part[i];
+    for (int s = 1; s < ksplit; ++s) v += part[s * mn + i];
+    if (bias) v += bias[i % out];
+    if (y_dtype == HXQ_F32) static_cast<float *>(y)[i] = v;
+    else static_cast<uint16_t *>(y)[i] = y_dtype == HXQ_BF16 ? to16<true>(v) : to16<false>(v);
+}
+
 // ga[g][o] = {scale[o][g], offset[o][g]}: the GEMM's affine layout, so a
 // block's rows for one group are contiguous.
 __global__ __launch_bounds__(256) void affine_pack_kernel(const float *gs, const float *go,
@@ -724,7 +758,7 @@ static int gemm_launch(GemmArgs &a, int grid_x, int grid_y, hipStream_t stream) 
         a.tiles_x = grid_x;
         a.tiles_y = grid_y;
         a.tiles_per_xcd = (grid_x * grid_y + kXcds - 1) / kXcds;
-        grid = dim3(a.tiles_per_xcd * kXcds, 1);
+        grid = dim3(a.tiles_per_xcd * kXcds, a.ksplit > 1 ? a.ksplit : 1);
     }
     if (a.w[0].ga)
         hipLaunchKernelGGL((gemm_kernel<BM, BF16, true, GROUPED, PAIR>), grid, dim3(kGemmThreads),
@@ -774,11 +808,47 @@ static int grouped_launch(GemmArgs &a, int64_t n_assign, bool bf16, hipStream_t 
 
 using namespace hxq;
 
+namespace {
+// Dense split-K plan: when the output tiles fill under half of the 256 CUs,
+// split K into up to 8 ranges of at least 4 steps (fp32 partials + an ordered
+// reduce); otherwise one range.
+struct SplitPlan {
+    int ksplit, ks_per;
+};
+SplitPlan split_plan(int64_t m_rows, int64_t out_features, int64_t in_features) {
+    const int64_t tiles = ((out_features + kBN - 1) / kBN) * ((m_rows + 127) / 128);
+    const int nk = static_cast<int>(in_features / kBK);
+    int ks = 1;
+    if (tiles < 128) ks = static_cast<int>(std::min<int64_t>({8, 256 / tiles, nk / 4}));
+    if (ks < 2) return {1, nk};
+    const int per = (nk + ks - 1) / ks;
+    return {(nk + per - 1) / per, per};
+}
+}  // namespace
+
+extern "C" int64_t hxq_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
+                                            int64_t in_features) {
+    if (m_rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % kBK) return 0;
+    const SplitPlan sp = split_plan(m_rows, out_features, in_features);
+    return sp.ksplit > 1 ? int64_t{4} * sp.ksplit * m_rows * out_features : 0;
+}
+
 extern "C" int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
                         const float *codebook, const float *group_affine, int32_t group_size,
                         const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
                         const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
                         int64_t out_features, int64_t in_features, hipStream_t stream) {
+    return hxq_gemm_ws(x, x_dtype, indices, codebook, group_affine, group_size, sc_row_ptr,
+                       sc_col, sc_val, bias, y, y_dtype, m_rows, out_features, in_features,
+                       nullptr, 0, stream);
+}
+
+extern "C" int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
+                           const float *codebook, const float *group_affine, int32_t group_size,
+                           const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
+                           const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
+                           int64_t out_features, int64_t in_features, void *workspace,
+                           int64_t workspace_bytes, hipStream_t stream) {
     clear_error();
     HXQ_REQUIRE(x && indices && codebook && y, "x, indices, codebook and y are required");
     HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16,
@@ -804,11 +874,27 @@ extern "C" int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
     a.y_dtype = y_dtype;
     a.n_experts = 1;
     a.x_rows = a.M;
+    a.ksplit = 1;
+    a.ks_per = a.K / kBK;
+    const int64_t need = hxq_gemm_workspace_bytes(m_rows, out_features, in_features);
+    if (workspace != nullptr && need > 0) {
+        HXQ_REQUIRE(workspace_bytes >= need, "workspace too small (hxq_gemm_workspace_bytes)");
+        const SplitPlan sp = split_plan(m_rows, out_features, in_features);
+        a.ksplit = sp.ksplit;
+        a.ks_per = sp.ks_per;
+        a.part = static_cast<float *>(workspace);
+    }
     const int gx = static_cast<int>((out_features + kBN - 1) / kBN);
     const bool bf16 = x_dtype == HXQ_BF16;
     const int gy = static_cast<int>((m_rows + 127) / 128);
-    return bf16 ? gemm_launch<128, true, false, false>(a, gx, gy, stream)
-                : gemm_launch<128, false, false, false>(a, gx, gy, stream);
+    const int rc = bf16 ? gemm_launch<128, true, false, false>(a, gx, gy, stream)
+                        : gemm_launch<128, false, false, false>(a, gx, gy, stream);
+    if (rc != HXQ_OK || a.ksplit == 1) return rc;
+    const int64_t mn = m_rows * out_features;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<uint32_t>((mn + 255) / 256)),
+                       dim3(256), 0, stream, a.part, a.ksplit, mn, a.OUT, bias, y, y_dtype);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
 }
 
 extern "C" int hxq_affine_pack(const float *group_scale, const float *group_offset,

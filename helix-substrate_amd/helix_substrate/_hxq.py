@@ -78,6 +78,7 @@ SIGNATURES = {
     "hxq_gemv_multi_rmsnorm": [P, P, P, F32, P, P, I32, I32, I32, I64, P],
     "hxq_gemv_multi_silu": [P, P, P, I32, I32, I32, I64, P],
     "hxq_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_gemm_ws": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64, P],
     "hxq_affine_pack": [P, P, I64, I64, P, P],
     "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
                            I64, I64, I64, P, I64, P],
@@ -124,6 +125,7 @@ SIGNATURES_I64 = {
     "hxq_select_workspace_bytes": [],
     "hxq_outliers_workspace_bytes": [I64],
     "hxq_vq2_workspace_bytes": [I64, I32],
+    "hxq_gemm_workspace_bytes": [I64, I64, I64],
 }
 
 
@@ -358,9 +360,10 @@ def affine_pack(group_scale, group_offset):
 
 
 def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_val, bias=None,
-         out_dtype=None, out=None):
+         out_dtype=None, out=None, split_k=True):
     """Y = X @ W^T (+bias) on MFMA; X bf16/fp16 [M, K]; W rounded to X's dtype.
-    group_affine: [K/G, OUT, 2] (``affine_pack``) or None."""
+    group_affine: [K/G, OUT, 2] (``affine_pack``) or None.  split_k: let
+    shapes with few output tiles split K (fp32 partials in a workspace)."""
     m, in_f = x.shape
     out_f = indices.shape[0]
     if indices.shape[1] != in_f:
@@ -369,11 +372,13 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
         out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
     _need_device(x, indices, codebook, group_affine, sc_row_ptr, sc_col, sc_val, bias, out)
     _need_cb256(codebook)
-    rc = lib().hxq_gemm(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
-                        _ptr(group_affine), int(group_size), _ptr(sc_row_ptr), _ptr(sc_col),
-                        _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype), m, out_f, in_f,
-                        _stream(x))
-    _check("hxq_gemm", rc)
+    nbytes = lib().hxq_gemm_workspace_bytes(m, out_f, in_f) if split_k else 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+    rc = lib().hxq_gemm_ws(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
+                           _ptr(group_affine), int(group_size), _ptr(sc_row_ptr), _ptr(sc_col),
+                           _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype), m, out_f,
+                           in_f, _ptr(ws), nbytes, _stream(x))
+    _check("hxq_gemm_ws", rc)
     return out
 
 

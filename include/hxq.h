@@ -211,6 +211,23 @@ int hxq_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
              const float *sc_val, const float *bias, void *y, int32_t y_dtype,
              int64_t m_rows, int64_t out_features, int64_t in_features,
              hipStream_t stream);
+/*
+ * hxq_gemm_ws: hxq_gemm with a workspace.  When the output tiles
+ * (128 x 256) cover under half of the compute units, K is split into up to 8
+ * ranges run in parallel, each writing fp32 partials to the workspace, and a
+ * second launch adds the ranges in order (then the bias) into y; results are
+ * deterministic.  workspace_bytes >= hxq_gemm_workspace_bytes(m_rows,
+ * out_features, in_features) (0 when no split is planned; a NULL workspace
+ * runs unsplit, as hxq_gemm does).
+ * Replaces: the same reference paths as hxq_gemm.
+ */
+int64_t hxq_gemm_workspace_bytes(int64_t m_rows, int64_t out_features, int64_t in_features);
+int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
+                const float *codebook, const float *group_affine, int32_t group_size,
+                const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
+                const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
+                int64_t out_features, int64_t in_features, void *workspace,
+                int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * group_affine[g][o] = {group_scale[o][g], group_offset[o][g]} (fp32): the

@@ -134,3 +134,30 @@ def test_affine_pack_layout(dev):
     go = torch.randn(300, 7, device=dev)
     ga = _hxq.affine_pack(gs, go)
     assert torch.equal(ga, torch.stack([gs.t(), go.t()], dim=-1))
+
+
+@pytest.mark.parametrize("m,out_f,in_f,density", [
+    (130, 512, 3584, 0.001),   # kv-like: 2 x 2 tiles, K split 8 ways
+    (40, 128, 512, 0.05),      # 8 K-steps split 2 ways, dense sidecar rows
+    (2048, 512, 3584, 0.001),  # the benchmark's kv shape
+])
+def test_gemm_split_k_matches_unsplit_and_oracle(dev, m, out_f, in_f, density):
+    print(f"split-K gemm m={m} out={out_f} in={in_f}", flush=True)
+    assert _hxq.lib().hxq_gemm_workspace_bytes(m, out_f, in_f) > 0   # a split is planned
+    L, T = _layer(out_f, in_f, seed=m + 7, sigma=0.015, density=density)
+    bias = torch.linspace(-1, 1, out_f)
+    mod = _module(T, dev, bias=bias)
+    W = _oracle_w(L)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    args = (x.to(dev), mod.indices, mod.codebook, mod._affine_t, mod.group_size,
+            mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias)
+    ys = _hxq.gemm(*args, out_dtype=torch.float32)
+    yu = _hxq.gemm(*args, out_dtype=torch.float32, split_k=False)
+    _check(ys, x, W, bias)
+    _check(yu, x, W, bias)
+    assert _maxrel(ys.cpu().numpy(), yu.cpu().numpy().astype(np.float64)) <= 1e-5
+    assert torch.equal(_hxq.gemm(*args, out_dtype=torch.float32), ys)   # ordered reduce
+    yb = _hxq.gemm(*args)
+    assert yb.dtype == torch.bfloat16
+    _check(yb, x, W, bias)
+    assert torch.equal(mod(x.to(dev)), yb)                              # module path
