@@ -179,13 +179,16 @@ class CDNAv3Writer:
 
 def compress_model(model, out_dir, device=None, group_size=None, n_clusters: int = 256,
                    percentile: float = 99.9, max_corrections: int = 512,
-                   skip_modules=("embed_tokens", "lm_head")) -> dict:
+                   skip_modules=("embed_tokens", "lm_head"), vector_dim: int = 1,
+                   module_vector_dim_map=None) -> dict:
     """Encode every nn.Linear weight of `model` into ``{name}.cdnav3`` under
     out_dir (on `device` when given: the GPU encoder) and every other tensor
     (norms, embeddings, biases) as an exact fp16 ``.npy``; writes
     manifest.json.  Modules whose name contains an entry of `skip_modules`
     stay exact (config 1 keeps the embedding / LM head uncompressed).
-    Returns the manifest."""
+    vector_dim 2 (or a module-name substring -> vector_dim map, first match
+    wins) encodes those weights with a pair codebook of n_clusters entries
+    (device required, no affine).  Returns the manifest."""
     import torch
     import torch.nn as nn
 
@@ -201,9 +204,15 @@ def compress_model(model, out_dir, device=None, group_size=None, n_clusters: int
         if name in linear_weights and t.dim() == 2:
             src = t.detach().float()
             src = src.to(device) if device is not None else src.cpu().numpy()
+            vd = vector_dim
+            for key, v in (module_vector_dim_map or {}).items():
+                if key in name:
+                    vd = int(v)
+                    break
             st = w.write_tensor(src, name, n_clusters=n_clusters, percentile=percentile,
-                                max_corrections=max_corrections, group_size=group_size,
-                                tensor_class="linear")
+                                max_corrections=max_corrections,
+                                group_size=None if vd > 1 else group_size,
+                                tensor_class="linear", vector_dim=vd)
             d = w.base_dir / f"{_safe_name(name)}.cdnav3"
             st["compressed_bytes"] = sum(f.stat().st_size for f in d.iterdir()
                                          if f.name not in ("meta.json", "stats.json"))

@@ -59,3 +59,31 @@ def test_gpu_bf16_model(dev, hf_dir):
         ref = cpu(ids).logits
         out = gpu(ids.to(dev)).logits.float().cpu()
     assert float((out - ref).abs().max()) <= 3e-2 * float(ref.abs().max())
+
+
+def test_compress_model_pair_modules(dev, tmp_path):
+    # module_vector_dim_map: the MLP weights get pair codebooks, the rest scalar
+    import numpy as np
+
+    from helix_substrate.helix_linear import load_cdna_factors
+    from helix_substrate.hxq_reader_v3 import CDNAv3Reader
+
+    torch.manual_seed(1)
+    model = Qwen2ForCausalLM(Qwen2Config(**CFG)).eval()
+    print("compress_model with pair MLPs", flush=True)
+    compress_model(model, tmp_path / "cdna", device=dev, group_size=128,
+                   module_vector_dim_map={"mlp": 2})
+    mods = load_cdna_factors(tmp_path / "cdna")
+    pair = {k: m for k, m in mods.items() if m.vector_dim == 2}
+    assert len(pair) == 3 * CFG["num_hidden_layers"] and all("mlp" in k for k in pair)
+    assert all(m.vector_dim == 1 for k, m in mods.items() if "mlp" not in k)
+    for k, m in pair.items():
+        d = tmp_path / "cdna" / (k.replace(".", "_") + "_weight.cdnav3")
+        w = CDNAv3Reader(d).reconstruct().astype(np.float64)
+        dense = dict(model.named_parameters())[k + ".weight"].detach().double().numpy()
+        cos = (w * dense).sum() / np.sqrt((w * w).sum() * (dense * dense).sum())
+        assert cos > 0.9, (k, cos)
+        x = torch.randn(3, m.in_features, generator=torch.Generator().manual_seed(4))
+        y = m.to(dev)(x.to(dev)).float().cpu().double().numpy()
+        ref = x.double().numpy() @ w.T
+        assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max() + 1e-7
