@@ -331,3 +331,24 @@ def test_write_tensor_pairs_round_trip(dev, tmp_path):
     y = layer(torch.from_numpy(x).to(dev)).float().cpu().numpy()
     ref = oracle.linear_f64(x, want)
     assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref)) + 1e-6
+
+
+def test_vector_kmeans_edge_cases(dev):
+    # fewer rows than entries: k = n; constant data: every seeding distance is
+    # 0, so the weighted draw has no valid probabilities and both raise, as
+    # RandomState.choice does in the reference
+    print("vector_kmeans edge cases", flush=True)
+    x = _pairs(np.random.RandomState(31), 5)
+    cb, a, steps = hxq_encoder.vector_kmeans(torch.from_numpy(x).to(dev), 16)
+    wcb, wa, wsteps = oracle.vector_kmeans_np(x, 16)
+    assert cb.shape == (5, 2) and steps == wsteps
+    np.testing.assert_array_equal(cb.cpu().numpy(), wcb)
+    np.testing.assert_array_equal(a.cpu().numpy().astype(np.int32), wa)
+    const = np.full((1000, 2), 0.25, np.float32)
+    with pytest.raises(ValueError):
+        oracle.vector_kmeans_np(const, 8)
+    with pytest.raises(ValueError):
+        hxq_encoder.vector_kmeans(torch.from_numpy(const).to(dev), 8)
+    one, a1, _ = hxq_encoder.vector_kmeans(torch.from_numpy(const).to(dev), 1)
+    np.testing.assert_array_equal(one.cpu().numpy(), const[:1])
+    assert int(a1.abs().sum()) == 0
