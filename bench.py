@@ -772,10 +772,10 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
     every pair assigned.  ms_per_tensor is the steady state of a model's
     tensors of one shape (the seeding's RandomState draws, which depend only
     on the shape, are replayed once per shape; first_tensor_of_shape_ms
-    includes that replay).  The assignment kernel is VALU-bound: 7 fp32 vector
-    instructions per (pair, entry) (mul, fma, add, fma, compare, two selects)
-    against MI355X's 157.3 TFLOP/s fp32 vector peak = 78.6e12 lane operations/s,
-    so 11.2e12 pair-entry distances/s is its roof."""
+    includes that replay).  The assignment kernel is VALU-bound: a (pair, entry)
+    distance needs 5 fp32 vector operations (mul, fma, add, fma, and a min to
+    keep the nearest) against MI355X's 157.3 TFLOP/s fp32 vector peak =
+    78.6e12 lane operations/s, so 15.7e12 pair-entry distances/s is its roof."""
     import numpy as np
     import torch
     from helix_substrate import _hxq, hxq_encoder
@@ -824,7 +824,7 @@ def encode_pairs_bench(dev, iters=2, cpu=True):
     torch.cuda.synchronize(dev)
     launch_ms = e0.elapsed_time(e1) / 5
     dist = vec.shape[0] * k
-    roof = 157.3e12 / 2 / 7
+    roof = 157.3e12 / 2 / 5
     res = {"tensor": [rows, cols], "pairs": int(vec.shape[0]), "codebook": [k, 2],
            "fit_sample": hxq_encoder.KMEANS_MAX_SAMPLES, "lloyd_steps": int(steps[0]),
            "ms_per_tensor": round(ms, 2), **{kk: round(v, 2) for kk, v in stages.items()},

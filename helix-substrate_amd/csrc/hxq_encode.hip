@@ -730,14 +730,41 @@ __global__ __launch_bounds__(kPairThreads) void pair_assign_kernel(
         best[v] = fmaf(-2.0f, fmaf(x1[v], c.y, x0[v] * c.x), xsq[v] + c.z);
         bj[v] = 0;
     }
-    for (int j = 1; j < k; ++j) {
-        const float4 cj = stab[j];
+    if constexpr (MIN) {
+        for (int j = 1; j < k; ++j) {
+            const float4 cj = stab[j];
 #pragma unroll
-        for (int v = 0; v < V; ++v) {
-            const float d = fmaf(-2.0f, fmaf(x1[v], cj.y, x0[v] * cj.x), xsq[v] + cj.z);
-            if (d < best[v]) {
-                best[v] = d;
-                bj[v] = j;
+            for (int v = 0; v < V; ++v) {
+                const float d = fmaf(-2.0f, fmaf(x1[v], cj.y, x0[v] * cj.x), xsq[v] + cj.z);
+                if (d < best[v]) best[v] = d;
+            }
+        }
+    } else {
+        // Entries in groups of 8: the group's minimum (fminf skips NaN, as the
+        // strict compare does) replaces the best only if strictly smaller, and
+        // only then is its first index looked up -- the same (value, first
+        // index) as a strict-compare scan, with the index work done on the
+        // few groups that improve.  Entries past k read entry k - 1 again; it
+        // sits earlier in the same group, so a tie never picks the copy.
+        for (int j0 = 1; j0 < k; j0 += 8) {
+            float4 cg[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) cg[t] = stab[min(j0 + t, k - 1)];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                float d[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    d[t] = fmaf(-2.0f, fmaf(x1[v], cg[t].y, x0[v] * cg[t].x), xsq[v] + cg[t].z);
+                const float g = fminf(fminf(fminf(d[0], d[1]), fminf(d[2], d[3])),
+                                      fminf(fminf(d[4], d[5]), fminf(d[6], d[7])));
+                if (g < best[v]) {
+                    int at = j0 + 7;
+#pragma unroll
+                    for (int t = 6; t >= 0; --t) at = d[t] == g ? j0 + t : at;
+                    best[v] = g;
+                    bj[v] = at;
+                }
             }
         }
     }
