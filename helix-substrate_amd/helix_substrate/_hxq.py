@@ -198,6 +198,21 @@ def _need_cb256(cb):
                          "(pad shorter codebooks; HelixLinear._kcb is the padded copy)")
 
 
+def _need_f32(**named):
+    """The kernels read codebooks, affine factors, sidecar values/deltas and bias as
+    fp32; a 16-bit tensor here would be read past its end (e.g. a module cast
+    with .bfloat16() by code that bypasses HelixLinear._apply).  Raise instead."""
+    for name, t in named.items():
+        if t is not None and t.dtype != torch.float32:
+            raise RuntimeError(f"{name} must be float32 (got {t.dtype})")
+
+
+def _need_i32(**named):
+    for name, t in named.items():
+        if t is not None and t.dtype != torch.int32:
+            raise RuntimeError(f"{name} must be int32 (got {t.dtype})")
+
+
 def dtype_code(dt: torch.dtype) -> int:
     try:
         return _DTYPE_CODE[dt]
@@ -218,6 +233,8 @@ def dequant_f32(indices, codebook, group_scale, group_offset, group_size,
         out = torch.empty(row_end - row_begin, in_f, dtype=torch.float32, device=indices.device)
     _need_device(indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val, out)
     _need_cb256(codebook)
+    _need_f32(group_scale=group_scale, group_offset=group_offset, sc_val=sc_val, out=out)
+    _need_i32(sc_row_ptr=sc_row_ptr, sc_col=sc_col)
     rc = lib().hxq_dequant_f32(_ptr(indices), _ptr(codebook), _ptr(group_scale), _ptr(group_offset),
                                int(group_size), _ptr(sc_row_ptr), _ptr(sc_col), _ptr(sc_val),
                                out_f, in_f, int(row_begin), int(row_end), _ptr(out),
@@ -238,6 +255,8 @@ def gemv(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr
     _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_delta,
                  bias, out)
     _need_cb256(codebook)
+    _need_f32(group_scale=group_scale, group_offset=group_offset, sc_delta=sc_delta, bias=bias)
+    _need_i32(sc_row_ptr=sc_row_ptr, sc_col=sc_col)
     rc = lib().hxq_gemv(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
                         _ptr(group_scale), _ptr(group_offset), int(group_size), _ptr(sc_row_ptr),
                         _ptr(sc_col), _ptr(sc_delta), _ptr(bias), _ptr(out),
@@ -261,6 +280,9 @@ def gemv_fmt(x, fmt, indices, out_features, codebook=None, group_scale=None, gro
         out = torch.empty(n, out_features, dtype=out_dtype, device=x.device)
     _need_device(x, indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_delta,
                  bias, out)
+    _need_f32(codebook=codebook, group_scale=group_scale, group_offset=group_offset,
+              sc_delta=sc_delta, bias=bias)
+    _need_i32(sc_row_ptr=sc_row_ptr, sc_col=sc_col)
     n_codes = 0 if codebook is None else int(codebook.shape[0])
     rc = lib().hxq_gemv_fmt(_ptr(x), dtype_code(x.dtype), int(fmt), _ptr(indices), _ptr(codebook),
                             n_codes, _ptr(group_scale), _ptr(group_offset), int(group_size),
@@ -279,6 +301,9 @@ def dequant_fmt(fmt, indices, out_features, in_features, codebook=None, group_sc
         out = torch.empty(row_end - row_begin, in_features, dtype=torch.float32,
                           device=indices.device)
     _need_device(indices, codebook, group_scale, group_offset, sc_row_ptr, sc_col, sc_val, out)
+    _need_f32(codebook=codebook, group_scale=group_scale, group_offset=group_offset,
+              sc_val=sc_val, out=out)
+    _need_i32(sc_row_ptr=sc_row_ptr, sc_col=sc_col)
     n_codes = 0 if codebook is None else int(codebook.shape[0])
     rc = lib().hxq_dequant_fmt(int(fmt), _ptr(indices), _ptr(codebook), n_codes, _ptr(group_scale),
                                _ptr(group_offset), int(group_size), _ptr(sc_row_ptr), _ptr(sc_col),
@@ -299,6 +324,9 @@ def _mat_array(x, mats, outs, out_dtype):
         _need_device(x, m["indices"], m["codebook"], m.get("group_scale"), m.get("group_offset"),
                      m.get("sc_row_ptr"), m.get("sc_col"), m.get("sc_delta"), m.get("bias"), y)
         _need_cb256(m["codebook"])
+        _need_f32(group_scale=m.get("group_scale"), group_offset=m.get("group_offset"),
+                  sc_delta=m.get("sc_delta"), bias=m.get("bias"))
+        _need_i32(sc_row_ptr=m.get("sc_row_ptr"), sc_col=m.get("sc_col"))
         arr[i] = HxqMatrix(m["indices"].data_ptr(), m["codebook"].data_ptr(),
                            *(0 if m.get(k) is None else m[k].data_ptr()
                              for k in ("group_scale", "group_offset", "sc_row_ptr", "sc_col",
@@ -372,6 +400,8 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
         out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
     _need_device(x, indices, codebook, group_affine, sc_row_ptr, sc_col, sc_val, bias, out)
     _need_cb256(codebook)
+    _need_f32(group_affine=group_affine, sc_val=sc_val, bias=bias)
+    _need_i32(sc_row_ptr=sc_row_ptr, sc_col=sc_col)
     nbytes = lib().hxq_gemm_workspace_bytes(m, out_f, in_f) if split_k else 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
     rc = lib().hxq_gemm_ws(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),

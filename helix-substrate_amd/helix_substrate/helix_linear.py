@@ -323,6 +323,26 @@ class HelixLinear(nn.Module):
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
                                       unexpected_keys, error_msgs)
 
+    # Floating-point HXQ state the kernels read as fp32, whatever the module's dtype.
+    _FP32_STATE = ("codebook", "sidecar_values", "svd_U", "svd_s", "svd_Vt", "bias",
+                   "channel_scales", "group_scale", "group_offset", "_sc_val", "_sc_delta",
+                   "_sidecar_deltas", "_sidecar_vq_vals", "_affine_t")
+
+    def _apply(self, fn, recurse=True):
+        """``.to()/.cuda()/.half()/.bfloat16()``: move the HXQ state with the module but
+        keep it fp32 (reference helix_linear.py:275-283 refreshes its dispatch state
+        here).  A dtype cast would round the codebook, affine, sidecar and bias; the
+        original fp32 tensor is moved to the new device instead."""
+        keep = {n: t for n, t in self._buffers.items()
+                if n in self._FP32_STATE and t is not None and t.dtype == torch.float32}
+        super()._apply(fn, recurse)
+        for name, t in keep.items():
+            new = self._buffers.get(name)
+            if new is not None and new.dtype != torch.float32:
+                self._buffers[name] = t.to(device=new.device)
+        self._kcb_cache = None
+        return self
+
     def set_compute_dtype(self, dtype: torch.dtype) -> None:
         self.compute_dtype = dtype
         self.register_buffer("codebook_f16",

@@ -161,3 +161,63 @@ def test_gemm_split_k_matches_unsplit_and_oracle(dev, m, out_f, in_f, density):
     assert yb.dtype == torch.bfloat16
     _check(yb, x, W, bias)
     assert torch.equal(mod(x.to(dev)), yb)                              # module path
+
+
+def _row_slice(m):
+    """Rows compared against the fp64 oracle: the first, a middle and the last 32."""
+    mid = (m // 2) & ~31
+    return torch.from_numpy(np.unique(np.r_[0:32, mid:mid + 32, m - 32:m]))
+
+
+@pytest.mark.parametrize("out_f,in_f", [
+    (3584, 3584),     # q (and o)
+    (18944, 3584),    # gate / up
+    (3584, 18944),    # down: K = 18944 walks the long-K sidecar cursor
+])
+def test_gemm_config2_shapes_m512(dev, out_f, in_f):
+    """Benchmark config 2 (Qwen2.5-7B prefill) at M = 512, sigma 0.015: a row
+    slice of Y against the fp64 oracle of the full reconstructed W (bf16
+    output at the 2e-2 bar; fp32 output also at the tight 2e-4 bar)."""
+    m = 512
+    print(f"config-2 gemm m={m} out={out_f} in={in_f}", flush=True)
+    L, T = _layer(out_f, in_f, seed=out_f + 3 * in_f, sigma=0.015)
+    mod = _module(T, dev)
+    W = _oracle_w(L)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(out_f)).to(torch.bfloat16)
+    xd = x.to(dev)
+    rows = _row_slice(m)
+    y = mod(xd)
+    assert mod._last_dispatch_path == "hip_gemm" and y.dtype == torch.bfloat16
+    _check(y[rows], x[rows], W)
+    _check(_gemm32(mod, xd)[rows], x[rows], W)
+
+
+def test_gemm_config2_gate_up_m8192(dev):
+    """Config 2's largest M (8192) on the gate/up shape: row subset against the
+    oracle, plus bitwise determinism of the whole output."""
+    m, out_f, in_f = 8192, 18944, 3584
+    print(f"config-2 gemm m={m} out={out_f} in={in_f}", flush=True)
+    L, T = _layer(out_f, in_f, seed=77, sigma=0.015)
+    mod = _module(T, dev)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    xd = x.to(dev)
+    y = mod(xd)
+    rows = _row_slice(m)
+    _check(y[rows], x[rows], _oracle_w(L))
+    assert torch.equal(mod(xd), y)
+
+
+@pytest.mark.parametrize("out_f,in_f", [(8512, 2048), (2048, 4096)])
+def test_gemm_config3_mixer_projections(dev, out_f, in_f):
+    """Config 3's Mamba2 in_proj (8512 x 2048) and out_proj (2048 x 4096) at
+    M = batch 8 x seqlen 2048 = 16384 tokens, on a row slice."""
+    m = 16384
+    print(f"config-3 gemm m={m} out={out_f} in={in_f}", flush=True)
+    L, T = _layer(out_f, in_f, seed=out_f + in_f)
+    mod = _module(T, dev)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(in_f)).to(torch.bfloat16)
+    xd = x.to(dev)
+    rows = _row_slice(m)
+    W = _oracle_w(L)
+    _check(mod(xd)[rows], x[rows], W)
+    _check(_gemm32(mod, xd)[rows], x[rows], W)

@@ -194,3 +194,55 @@ def test_device_input_with_cpu_module_fails_loudly(dev):
     m = _module(T, torch.device("cpu"))
     with pytest.raises(RuntimeError):
         m(torch.randn(1, 128, device=dev))
+
+
+@pytest.mark.parametrize("rows", [1, 64])
+def test_bfloat16_cast_module_matches_oracle(dev, rows):
+    """model.to(torch.bfloat16) after loading: the HXQ state stays fp32 (the kernels
+    read it as fp32), so the GEMV/GEMM and the dequant still match the oracle."""
+    L, T = _layer(512, 1024, seed=14, density=0.01)
+    bias = torch.linspace(-0.5, 0.5, 512)
+    m = _module(T, dev, bias=bias).bfloat16()
+    for name in HelixLinear._FP32_STATE:
+        t = getattr(m, name, None)
+        assert t is None or (t.dtype == torch.float32 and t.is_cuda), name
+    W = _oracle_w(L)
+    np.testing.assert_array_equal(m.decode_weight().cpu().numpy().view(np.uint32), W.view(np.uint32))
+    xb = torch.randn(rows, 1024, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+    y = m(xb.to(dev))
+    assert y.dtype == torch.bfloat16
+    assert m._last_dispatch_path == ("hip_gemv" if rows == 1 else "hip_gemm")
+    yr = oracle.linear_f64(xb.float().numpy(), W, bias.numpy())
+    assert _maxrel(y.float().cpu().numpy(), yr) <= TOL_BF16
+
+
+def test_headline_gate_up_gemv_multi_bf16(dev):
+    """The bench's dominant launch: gate+up (2 x 11008 x 2048) in one gemv_multi
+    with bf16 activations, each matrix with its own codebook/affine/sidecar;
+    bf16 outputs at the 2e-2 bar and fp32 outputs at 1e-5 (x is exact in fp32)."""
+    layers = [_layer(11008, 2048, seed=200 + i, sigma=0.02) for i in range(2)]
+    mods = [_module(T, dev) for _, T in layers]
+    xb = torch.randn(1, 2048, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    mats = [dict(indices=m.indices, codebook=m.codebook, group_scale=m.group_scale,
+                 group_offset=m.group_offset, sc_row_ptr=m._sc_row_ptr, sc_col=m._sc_col,
+                 sc_delta=m._sc_delta, bias=None) for m in mods]
+    refs = [oracle.linear_f64(xb.float().numpy(), _oracle_w(L)) for L, _ in layers]
+    for out_dtype, tol in ((torch.bfloat16, TOL_BF16), (torch.float32, TOL_F32)):
+        outs = _hxq.gemv_multi(xb.to(dev), mats, 128, out_dtype=out_dtype)
+        for y, yr in zip(outs, refs):
+            assert y.dtype == out_dtype
+            assert _maxrel(y.float().cpu().numpy(), yr) <= tol, (out_dtype, tol)
+
+
+def test_headline_down_gemv_bf16(dev):
+    """Config-1 down projection (2048 x 11008) with bf16 activations."""
+    L, T = _layer(2048, 11008, seed=210)
+    m = _module(T, dev)
+    xb = torch.randn(1, 11008, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
+    yr = oracle.linear_f64(xb.float().numpy(), _oracle_w(L))
+    y = m(xb.to(dev))
+    assert y.dtype == torch.bfloat16 and m._last_dispatch_path == "hip_gemv"
+    assert _maxrel(y.float().cpu().numpy(), yr) <= TOL_BF16
+    y32 = _hxq.gemv(xb.to(dev), m.indices, m.codebook, m.group_scale, m.group_offset, 128,
+                    m._sc_row_ptr, m._sc_col, m._sc_delta, None, out_dtype=torch.float32)
+    assert _maxrel(y32.cpu().numpy(), yr) <= TOL_F32

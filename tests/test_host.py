@@ -111,6 +111,35 @@ def test_short_codebook_kernel_copy_is_padded():
     assert m2._kcb is m2.codebook
 
 
+@pytest.mark.parametrize("cast", ["bfloat16", "half", "double"])
+def test_dtype_cast_keeps_hxq_state_fp32(cast):
+    """module.bfloat16() / .half() / .double() (e.g. model.to(dtype) after loading)
+    must not round the codebook, affine, sidecar or bias the kernels read as fp32."""
+    L = synth.make_layer_np(96, 256, seed=12, density=0.01)
+    b = torch.linspace(-1, 1, 96)
+    m = getattr(_module(L, bias=b), cast)()
+    for name in HelixLinear._FP32_STATE:
+        t = getattr(m, name, None)
+        assert t is None or t.dtype == torch.float32, (name, t.dtype)
+    assert m.indices.dtype == torch.uint8
+    np.testing.assert_array_equal(m.decode_weight().numpy().view(np.uint32),
+                                  _oracle_w(L).view(np.uint32))
+    x = torch.randn(3, 256, generator=torch.Generator().manual_seed(1))
+    yr = oracle.linear_f64(x.numpy(), _oracle_w(L), b.numpy())
+    y = m(x)
+    assert y.dtype == torch.float32
+    assert np.abs(y.numpy() - yr).max() / np.abs(yr).max() < 1e-5
+
+
+def test_kernel_wrappers_refuse_16bit_state():
+    from helix_substrate import _hxq
+    with pytest.raises(RuntimeError, match="float32"):
+        _hxq._need_f32(bias=torch.zeros(4, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="int32"):
+        _hxq._need_i32(sc_col=torch.zeros(4, dtype=torch.int64))
+    _hxq._need_f32(bias=None, group_scale=torch.zeros(2))
+
+
 @pytest.mark.parametrize("shape", [(256,), (3, 256), (2, 3, 256)])
 def test_forward_cpu_matches_oracle(shape):
     L = synth.make_layer_np(96, 256, seed=4)
