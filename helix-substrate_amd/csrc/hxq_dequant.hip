@@ -64,18 +64,25 @@ __global__ __launch_bounds__(256) void dequant_sidecar_kernel(
         w[r * K + col[j]] = val[j];
 }
 
-// Reconstruction for the packed / pair formats: one thread per 16 weights.
+// Reconstruction for the packed / pair / uint16-index formats: one thread per
+// 16 weights.
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_fmt_kernel(
     const uint8_t *__restrict__ idx, const float *__restrict__ cb, int32_t n_codes,
     const float *__restrict__ gs, const float *__restrict__ go, int32_t group, int64_t K,
     int64_t row_begin, int64_t n_vec16, float *__restrict__ w) {
-    constexpr bool PAIR = FMT != HXQ_FMT_AF6;
-    constexpr int QB = FMT == HXQ_FMT_VQ2_U16 ? 16 : 12;
+    constexpr bool PAIR = FMT == HXQ_FMT_VQ2_U16 || FMT == HXQ_FMT_VQ2_P12;
+    constexpr bool U16 = FMT == HXQ_FMT_SCALAR_U16;
+    constexpr int QB = U16 ? 32 : FMT == HXQ_FMT_VQ2_U16 ? 16 : 12;
     __shared__ float2 tbl[PAIR ? kPairCodes : 1];
+    __shared__ float tbl1[U16 ? kPairCodes : 1];
     if constexpr (PAIR) {
         for (int j = threadIdx.x; j < kPairCodes; j += blockDim.x)
             tbl[j] = j < n_codes ? make_float2(cb[2 * j], cb[2 * j + 1]) : make_float2(0.f, 0.f);
+        __syncthreads();
+    }
+    if constexpr (U16) {
+        for (int j = threadIdx.x; j < kPairCodes; j += blockDim.x) tbl1[j] = j < n_codes ? cb[j] : 0.f;
         __syncthreads();
     }
     const int64_t vec_per_row = K / 16;
@@ -86,14 +93,28 @@ __global__ __launch_bounds__(256) void dequant_fmt_kernel(
         const int64_t c16 = v - r * vec_per_row;
         const int64_t row = row_begin + r;
         const uint32_t *src = reinterpret_cast<const uint32_t *>(idx + row * row_bytes + c16 * QB);
-        const uint32_t q[4] = {src[0], src[1], src[2], QB == 16 ? src[3] : 0u};
+        const uint32_t q[4] = {src[0], src[1], src[2], QB >= 16 ? src[3] : 0u};
         auto field = [&](int bit, int width) -> uint32_t {
             const int d = bit >> 5, sh = bit & 31;
             const uint32_t x = sh + width <= 32 ? q[d] >> sh : __builtin_amdgcn_alignbit(q[d + 1], q[d], sh);
             return x & ((1u << width) - 1u);
         };
         float out[16];
-        if constexpr (FMT == HXQ_FMT_AF6) {
+        if constexpr (U16) {
+            const uint4 hi = *reinterpret_cast<const uint4 *>(src + 4);
+            const uint32_t q2[8] = {q[0], q[1], q[2], q[3], hi.x, hi.y, hi.z, hi.w};
+            float s = 1.f, o = 0.f;
+            if (gs != nullptr) {
+                const int64_t g = row * (K / group) + c16 * 16 / group;
+                s = gs[g];
+                o = go[g];
+            }
+#pragma unroll
+            for (int f = 0; f < 16; ++f) {
+                const float c = tbl1[(q2[f >> 1] >> (16 * (f & 1))) & (kPairCodes - 1u)];
+                out[f] = gs != nullptr ? affine_exact(c, s, o) : c;
+            }
+        } else if constexpr (FMT == HXQ_FMT_AF6) {
             const int64_t g = row * (K / group) + c16 * 16 / group;
             const float s = gs[g], o = go[g];
 #pragma unroll
@@ -131,10 +152,13 @@ extern "C" int hxq_dequant_fmt(int32_t format, const uint8_t *indices, const flo
         return hxq_dequant_f32(indices, codebook, group_scale, group_offset, group_size,
                                sc_row_ptr, sc_col, sc_val, out_features, in_features, row_begin,
                                row_end, w_out, stream);
-    HXQ_REQUIRE(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12 || format == HXQ_FMT_AF6,
+    HXQ_REQUIRE(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12 ||
+                    format == HXQ_FMT_AF6 || format == HXQ_FMT_SCALAR_U16,
                 "unknown index format");
     HXQ_REQUIRE(indices && w_out, "indices and w_out are required");
     HXQ_REQUIRE((reinterpret_cast<uintptr_t>(indices) & 3u) == 0, "indices must be 4-byte aligned");
+    HXQ_REQUIRE(format != HXQ_FMT_SCALAR_U16 || (reinterpret_cast<uintptr_t>(indices) & 15u) == 0,
+                "uint16 indices must be 16-byte aligned");
     HXQ_REQUIRE((reinterpret_cast<uintptr_t>(w_out) & 15u) == 0, "w_out must be 16-byte aligned");
     HXQ_REQUIRE(out_features > 0 && in_features > 0 && in_features % 16 == 0,
                 "in_features must be a positive multiple of 16");
@@ -144,6 +168,13 @@ extern "C" int hxq_dequant_fmt(int32_t format, const uint8_t *indices, const flo
         HXQ_REQUIRE(group_scale && group_offset && group_size > 0 && group_size % 16 == 0 &&
                         in_features % group_size == 0,
                     "6-bit levels need the group affine (group_size a multiple of 16)");
+    else if (format == HXQ_FMT_SCALAR_U16)
+        HXQ_REQUIRE(codebook && n_codes >= 1 && n_codes <= kPairCodes &&
+                        (group_scale != nullptr) == (group_offset != nullptr) &&
+                        (!group_scale || (group_size > 0 && group_size % 16 == 0 &&
+                                          in_features % group_size == 0)),
+                    "uint16 indices need a 1..4096-entry codebook (affine: both factors, "
+                    "group_size a multiple of 16 dividing in_features)");
     else
         HXQ_REQUIRE(codebook && n_codes >= 1 && n_codes <= kPairCodes,
                     "pair codebooks need 1..4096 entries");
@@ -160,6 +191,7 @@ extern "C" int hxq_dequant_fmt(int32_t format, const uint8_t *indices, const flo
     switch (format) {
         case HXQ_FMT_VQ2_U16: HXQ_DQ(HXQ_FMT_VQ2_U16); break;
         case HXQ_FMT_VQ2_P12: HXQ_DQ(HXQ_FMT_VQ2_P12); break;
+        case HXQ_FMT_SCALAR_U16: HXQ_DQ(HXQ_FMT_SCALAR_U16); break;
         default: HXQ_DQ(HXQ_FMT_AF6); break;
     }
 #undef HXQ_DQ

@@ -132,10 +132,11 @@ __device__ __forceinline__ void store_y(void *y, int64_t i, int dt, float v) {
 // Index formats (HXQ_FMT_*): bytes of index data per 16 weights, and LDS
 // table floats per block.
 __host__ __device__ constexpr int fmt_bytes16(int f) {
-    return (f == HXQ_FMT_VQ2_P12 || f == HXQ_FMT_AF6) ? 12 : 16;
+    return f == HXQ_FMT_SCALAR_U16 ? 32 : (f == HXQ_FMT_VQ2_P12 || f == HXQ_FMT_AF6) ? 12 : 16;
 }
 __host__ __device__ constexpr int fmt_table_floats(int f, int nrep) {
-    return f == HXQ_FMT_SCALAR ? 256 * nrep : f == HXQ_FMT_AF6 ? 0 : 2 * kPairCodes;
+    return f == HXQ_FMT_SCALAR ? 256 * nrep : f == HXQ_FMT_AF6 ? 0
+         : f == HXQ_FMT_SCALAR_U16 ? kPairCodes : 2 * kPairCodes;
 }
 
 // Bits [bit, bit + width) of the little-endian 96/128-bit stream q (bit and
@@ -153,9 +154,10 @@ __device__ __forceinline__ u32x4 buf_load12(__amdgpu_buffer_rsrc_t r, uint32_t o
     return u32x4{v[0], v[1], v[2], 0u};
 }
 
-template <int CPS>
+// QW: 16-byte index words per 16 weights (2 for uint16 scalar indices)
+template <int CPS, int QW = 1>
 struct GemvItem {
-    u32x4 q[CPS];
+    u32x4 q[CPS * QW];
     float sc[CPS];
     float of[CPS];
 };
@@ -193,9 +195,11 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     static_assert(FMT == HXQ_FMT_AF6 || (TPW >= 1 && TBLF % (4 * NT) == 0),
                   "table/thread-count mismatch");
     static_assert(XM == 0 || FMT == HXQ_FMT_SCALAR, "fused prologues take scalar codebooks");
-    static_assert((FMT == HXQ_FMT_AF6) == AFFINE || FMT == HXQ_FMT_SCALAR,
+    static_assert((FMT == HXQ_FMT_AF6) == AFFINE || FMT == HXQ_FMT_SCALAR ||
+                      FMT == HXQ_FMT_SCALAR_U16,
                   "6-bit levels carry the affine; pair codebooks have none");
     constexpr int QB = fmt_bytes16(FMT);  // index bytes per 16 weights
+    constexpr int QW = QB > 16 ? 2 : 1;   // 16-byte words per 16 weights
     constexpr uint32_t kOob = 0x80000000u;      // buffer offset past any range: reads 0
     const int y_dtype = flags & 0xf;
     const bool xlds = (flags >> 4) & 1;
@@ -279,7 +283,8 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             }
     }
     float cbv[FMT == HXQ_FMT_SCALAR ? TPW : 1];
-    u32x4 cbq[(FMT == HXQ_FMT_VQ2_U16 || FMT == HXQ_FMT_VQ2_P12) ? TPW : 1];
+    u32x4 cbq[(FMT == HXQ_FMT_VQ2_U16 || FMT == HXQ_FMT_VQ2_P12 || FMT == HXQ_FMT_SCALAR_U16)
+                  ? TPW : 1];
     if constexpr (FMT == HXQ_FMT_SCALAR) {
         const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, 256 * 4);
 #pragma unroll
@@ -287,6 +292,11 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             const uint32_t e = 4u * (threadIdx.x + k * NT);  // first replica slot
             cbv[k] = buf_loadf(cr, (e / NREP) * 4u);
         }
+    } else if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
+        // scalar codebook [ncodes <= 4096] fp32, one copy; entries past ncodes read 0
+        const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, M.ncodes * 4);
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) cbq[k] = buf_load16(cr, 16u * (threadIdx.x + k * NT));
     } else if constexpr (FMT != HXQ_FMT_AF6) {
         // pair codebook [ncodes, 2] fp32 as is; entries past ncodes read 0
         const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, M.ncodes * 8);
@@ -305,14 +315,20 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(M.idx, out * row_bytes);
     const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(M.gs, AFFINE ? out * ngroups * 4 : 0);
     const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(M.go, AFFINE ? out * ngroups * 4 : 0);
-    auto load_item = [&](int32_t i, GemvItem<CPS> &it) {
+    auto load_item = [&](int32_t i, GemvItem<CPS, QW> &it) {
         const bool mine = i < n_mine;
         const uint32_t row = static_cast<uint32_t>(lo + rg + i * RG);
 #pragma unroll
         for (int ci = 0; ci < CPS; ++ci) {
             const uint32_t qo = mine ? row * row_bytes + koff[ci] / 16u * QB : kOob;
-            if constexpr (QB == 16) it.q[ci] = buf_load16(q_rsrc, qo);
-            else it.q[ci] = buf_load12(q_rsrc, qo);
+            if constexpr (QB == 32) {
+                it.q[2 * ci] = buf_load16(q_rsrc, qo);
+                it.q[2 * ci + 1] = buf_load16(q_rsrc, mine ? qo + 16u : kOob);
+            } else if constexpr (QB == 16) {
+                it.q[ci] = buf_load16(q_rsrc, qo);
+            } else {
+                it.q[ci] = buf_load12(q_rsrc, qo);
+            }
             if constexpr (AFFINE) {
                 const uint32_t g4 =
                     (row * static_cast<uint32_t>(ngroups) + koff[ci] / static_cast<uint32_t>(group)) * 4u;
@@ -324,7 +340,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             }
         }
     };
-    GemvItem<CPS> it[RB];
+    GemvItem<CPS, QW> it[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) load_item(b, it[b]);
     __builtin_amdgcn_sched_barrier(0);  // all prologue loads are issued before any wait
@@ -337,6 +353,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             *reinterpret_cast<float4 *>(tbl + e) = make_float4(cbv[k], cbv[k], cbv[k], cbv[k]);
         }
     } else if constexpr (FMT != HXQ_FMT_AF6) {
+        // pair table as float2 entries, or the uint16-index scalar table (one copy)
 #pragma unroll
         for (int k = 0; k < TPW; ++k)
             *reinterpret_cast<u32x4 *>(tbl + 4 * (threadIdx.x + k * NT)) = cbq[k];
@@ -456,7 +473,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     const float sc_dl0 = buf_loadf(dl_r, e0);
 
     // ---- stream
-    auto compute_item = [&](int32_t i, const GemvItem<CPS> &itm) {
+    auto compute_item = [&](int32_t i, const GemvItem<CPS, QW> &itm) {
         float acc[NX];
 #pragma unroll
         for (int n = 0; n < NX; ++n) acc[n] = 0.f;
@@ -480,6 +497,16 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
                         part[n] = fmaf(xv[ci][n][4 * d + 2], c2, part[n]);
                         part[n] = fmaf(xv[ci][n][4 * d + 3], c3, part[n]);
                     }
+                }
+            } else if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
+                // 16 uint16 indices in two words (ids masked to the 4096-entry table)
+#pragma unroll
+                for (int f = 0; f < 16; ++f) {
+                    const uint32_t id =
+                        (itm.q[2 * ci + (f >> 3)][(f >> 1) & 3] >> (16 * (f & 1))) & (kPairCodes - 1u);
+                    const float c = tbl[id];
+#pragma unroll
+                    for (int n = 0; n < NX; ++n) part[n] = fmaf(xv[ci][n][f], c, part[n]);
                 }
             } else if constexpr (FMT == HXQ_FMT_AF6) {
                 // 16 six-bit levels, little-endian bit stream
@@ -520,7 +547,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     };
     // double-buffered batches: the next batch's loads are issued before the
     // current batch is computed (it2 is the second buffer)
-    GemvItem<CPS> it2[RB];
+    GemvItem<CPS, QW> it2[RB];
     for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
 #pragma unroll
         for (int b = 0; b < RB; ++b) load_item(i0 + RB + b, it2[b]);
@@ -682,7 +709,7 @@ static int launch_one(const GemvHeader &h, const GemvMats &mats, int grid, hipSt
                        h.bb[2], h.bb[3], h.bb[4], h.bb[5], h.bb[6], mats, pro)
     if constexpr (XM != 0) {
         if (aff) HXQ_GEMV_LAUNCH(true, HXQ_F32); else HXQ_GEMV_LAUNCH(false, HXQ_F32);
-    } else if constexpr (FMT != HXQ_FMT_SCALAR) {
+    } else if constexpr (FMT != HXQ_FMT_SCALAR && FMT != HXQ_FMT_SCALAR_U16) {
         constexpr bool A = FMT == HXQ_FMT_AF6;
         switch (h.x_dtype) {
             case HXQ_F32: HXQ_GEMV_LAUNCH(A, HXQ_F32); break;
@@ -882,7 +909,8 @@ extern "C" int hxq_gemv_fmt(const void *x, int32_t x_dtype, int32_t format, cons
         return hxq_gemv(x, x_dtype, indices, codebook, group_scale, group_offset, group_size,
                         sc_row_ptr, sc_col, sc_delta, bias, y, y_dtype, n_rows, out_features,
                         in_features, stream);
-    HXQ_REQUIRE(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12 || format == HXQ_FMT_AF6,
+    HXQ_REQUIRE(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12 ||
+                    format == HXQ_FMT_AF6 || format == HXQ_FMT_SCALAR_U16,
                 "unknown index format");
     HXQ_REQUIRE(n_rows >= 1 && n_rows <= 4, "n_rows must be in [1, 4]");
     HXQ_REQUIRE(x && indices && y, "x, indices and y are required");
@@ -901,6 +929,16 @@ extern "C" int hxq_gemv_fmt(const void *x, int32_t x_dtype, int32_t format, cons
         HXQ_REQUIRE(group_scale && group_offset, "6-bit levels need group_scale and group_offset");
         HXQ_REQUIRE(group_size > 0 && group_size % 16 == 0 && in_features % group_size == 0,
                     "group_size must be a positive multiple of 16 dividing in_features");
+    } else if (format == HXQ_FMT_SCALAR_U16) {
+        HXQ_REQUIRE(codebook && n_codes >= 1 && n_codes <= kPairCodes,
+                    "uint16-index scalar codebooks need 1..4096 entries");
+        HXQ_REQUIRE(aligned16(codebook), "codebook must be 16-byte aligned");
+        const bool affine = group_scale || group_offset;
+        HXQ_REQUIRE(!affine || (group_scale && group_offset),
+                    "group_scale and group_offset must be given together");
+        HXQ_REQUIRE(!affine || (group_size > 0 && group_size % 16 == 0 &&
+                                in_features % group_size == 0),
+                    "group_size must be a positive multiple of 16 dividing in_features");
     } else {
         HXQ_REQUIRE(codebook && n_codes >= 1 && n_codes <= kPairCodes,
                     "pair codebooks need 1..4096 entries");
@@ -910,7 +948,7 @@ extern "C" int hxq_gemv_fmt(const void *x, int32_t x_dtype, int32_t format, cons
     GemvHeader h{};
     h.x = x;
     h.K = in_features;
-    h.group = format == HXQ_FMT_AF6 ? group_size : 0;
+    h.group = (format == HXQ_FMT_AF6 || format == HXQ_FMT_SCALAR_U16) ? group_size : 0;
     h.n_mats = 1;
     h.nchunks = static_cast<int32_t>((in_features + kChunk - 1) / kChunk);
     h.x_dtype = x_dtype;
@@ -922,6 +960,7 @@ extern "C" int hxq_gemv_fmt(const void *x, int32_t x_dtype, int32_t format, cons
     switch (format) {
         case HXQ_FMT_VQ2_U16: return gemv_run<0, HXQ_FMT_VQ2_U16>(h, mats, nx, stream);
         case HXQ_FMT_VQ2_P12: return gemv_run<0, HXQ_FMT_VQ2_P12>(h, mats, nx, stream);
+        case HXQ_FMT_SCALAR_U16: return gemv_run<0, HXQ_FMT_SCALAR_U16>(h, mats, nx, stream);
         default: return gemv_run<0, HXQ_FMT_AF6>(h, mats, nx, stream);
     }
 }

@@ -266,7 +266,7 @@ def gemv(x, indices, codebook, group_scale, group_offset, group_size, sc_row_ptr
 
 
 # index formats (include/hxq.h hxq_format)
-FMT_SCALAR, FMT_VQ2_U16, FMT_VQ2_P12, FMT_AF6 = 0, 1, 2, 3
+FMT_SCALAR, FMT_VQ2_U16, FMT_VQ2_P12, FMT_AF6, FMT_SCALAR_U16 = 0, 1, 2, 3, 4
 
 
 def gemv_fmt(x, fmt, indices, out_features, codebook=None, group_scale=None, group_offset=None,

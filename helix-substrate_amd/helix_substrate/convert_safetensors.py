@@ -6,7 +6,8 @@ per-tensor loading, ``:156-235`` conversion, ``:238-269`` the
 quantization_config, ``:272-347`` the directory conversion):
 
     {module}.codebook            [k] fp32
-    {module}.indices             [out, in] uint8
+    {module}.indices             [out, in / vector_dim] uint8 (int16 when the
+                                  directory's index_dtype is "uint16")
     {module}.sidecar_positions   [n] int64     (optional)
     {module}.sidecar_values      [n] fp32      (optional)
     {module}.svd_U / svd_s / svd_Vt, {module}.channel_scales (optional)
@@ -42,9 +43,13 @@ def _load_cdnav3_tensors(tensor_dir) -> Dict[str, np.ndarray]:
     meta = json.loads((tensor_dir / "meta.json").read_text())
     rows, cols = meta["shape"]
     base = _module_base(meta["tensor_name"])
+    wide = meta.get("index_dtype", "uint8") == "uint16"
+    idx = np.fromfile(tensor_dir / "indices.bin", dtype=np.uint16 if wide else np.uint8)
+    idx = idx.reshape(rows, cols // int(meta.get("vector_dim", 1)))
     out = {
         f"{base}.codebook": np.load(tensor_dir / "codebook.npy").astype(np.float32),
-        f"{base}.indices": np.fromfile(tensor_dir / "indices.bin", dtype=np.uint8).reshape(rows, cols),
+        # torch has no uint16: wide indices travel as int16 (all below 4096)
+        f"{base}.indices": idx.astype(np.int16) if wide else idx,
     }
     sc = tensor_dir / "sidecar.npz"
     if sc.exists():
@@ -97,6 +102,7 @@ def convert_cdnav3_to_safetensors(cdnav3_dir, output_path, original_model_path=N
     cdnav3_dir, output_path = Path(cdnav3_dir), Path(output_path)
     tensors: Dict[str, np.ndarray] = {}
     compressed, group_sizes = [], set()
+    k_map, vd_map = {}, {}
     n_exact = 0
     for d in sorted(cdnav3_dir.glob("*.cdnav3")):
         meta_path = d / "meta.json"
@@ -106,7 +112,13 @@ def convert_cdnav3_to_safetensors(cdnav3_dir, output_path, original_model_path=N
         if meta.get("storage_mode") == "exact":
             continue
         tensors.update(_load_cdnav3_tensors(d))
-        compressed.append(_module_base(meta["tensor_name"]))
+        base = _module_base(meta["tensor_name"])
+        compressed.append(base)
+        k = int(np.load(d / "codebook.npy", mmap_mode="r").shape[0])
+        if k != 256:  # the loader's shells need the codebook size and index width
+            k_map[base] = k
+        if int(meta.get("vector_dim", 1)) != 1:
+            vd_map[base] = int(meta["vector_dim"])
         if "group_size" in meta and (d / "group_scale.npy").exists():
             group_sizes.add(int(meta["group_size"]))
     for f in sorted(cdnav3_dir.glob("*.npy")):
@@ -124,11 +136,13 @@ def convert_cdnav3_to_safetensors(cdnav3_dir, output_path, original_model_path=N
     return {"n_compressed": len(compressed), "n_exact": n_exact, "n_from_original": n_orig,
             "n_total_keys": len(tensors), "output_bytes": size,
             "output_mb": round(size / 1024 / 1024, 1), "compressed_modules": compressed,
-            "group_size": next(iter(group_sizes)) if group_sizes else None}
+            "group_size": next(iter(group_sizes)) if group_sizes else None,
+            "module_k_map": k_map, "module_vector_dim_map": vd_map}
 
 
 def write_quantization_config(model_config_path, output_config_path, compressed_modules,
-                              manifest: Optional[dict] = None, group_size=None) -> None:
+                              manifest: Optional[dict] = None, group_size=None,
+                              module_k_map=None, module_vector_dim_map=None) -> None:
     """config.json + ``quantization_config`` (quant_method "cdna_v3")."""
     config = json.loads(Path(model_config_path).read_text())
     q = {"quant_method": "cdna_v3", "bits": 8, "n_clusters": 256,
@@ -138,6 +152,10 @@ def write_quantization_config(model_config_path, output_config_path, compressed_
         q["n_svd_routed"] = manifest.get("n_svd_routed", 0)
     if group_size:
         q["group_size"] = int(group_size)
+    if module_k_map:
+        q["module_k_map"] = dict(module_k_map)
+    if module_vector_dim_map:
+        q["module_vector_dim_map"] = dict(module_vector_dim_map)
     config["quantization_config"] = q
     out = Path(output_config_path)
     out.parent.mkdir(parents=True, exist_ok=True)
@@ -165,7 +183,8 @@ def convert_model(cdnav3_dir, model_dir, output_dir) -> dict:
         manifest = json.loads((cdnav3_dir / "manifest.json").read_text())
     if (model_dir / "config.json").exists():
         write_quantization_config(model_dir / "config.json", output_dir / "config.json",
-                                  stats["compressed_modules"], manifest, stats["group_size"])
+                                  stats["compressed_modules"], manifest, stats["group_size"],
+                                  stats["module_k_map"], stats["module_vector_dim_map"])
     for name in _TOKENIZER_FILES:
         if (model_dir / name).exists():
             shutil.copy2(model_dir / name, output_dir / name)

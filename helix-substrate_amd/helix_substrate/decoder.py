@@ -277,5 +277,16 @@ class HelixDecoder:
         self.step_persistent(n_new, out)
         return out
 
+    def close(self):
+        """Release device state in a fixed order before the process exits: wait for
+        queued work, destroy the captured graph, then drop the persistent
+        workspace (flags, layer table) and its host descriptors."""
+        torch.cuda.synchronize(self.device)
+        if self._graph is not None:
+            self._graph.reset()
+            self._graph = None
+        self._p_desc = self._p_layers = self._p_ws = None
+        torch.cuda.synchronize(self.device)
+
     def hxq_bytes_per_token(self):
         return sum(L[n].kernel_bytes() for L in self.layers for n in _PROJ)

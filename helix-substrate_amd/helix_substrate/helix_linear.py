@@ -21,8 +21,10 @@ Differences, by design:
     the reconstruction is bit-exact; contractions add ``x[col]*delta`` with
     delta = value - W_affine[pos] (the reference's delta form,
     ``helix_linear.py:188-203``);
-  * scalar codebooks of at most 256 entries (uint8 indices), or pair
-    codebooks (``vector_dim=2``, [k <= 4096, 2], reference
+  * scalar codebooks of at most 256 entries (uint8 indices) or up to 4096
+    entries (int16 indices, the reference's k > 256 storage,
+    ``helix_linear.py:166-176``), or pair codebooks (``vector_dim=2``,
+    [k <= 4096, 2], reference
     ``triton_vq2d_matmul.py``) with int16 indices [out, in/2] or the
     reference's 12-bit packing (``index_packing="12bit"``, uint8 1-D,
     ``index_packing.py``); the pair formats run the same GEMV kernel with a
@@ -73,11 +75,13 @@ class HelixLinear(nn.Module):
         if vector_dim not in (1, 2):
             raise NotImplementedError("vector_dim must be 1 (scalar) or 2 (pair codebook)")
         if vector_dim == 1:
-            if codebook.numel() > 256:
-                raise NotImplementedError("scalar codebooks above 256 entries are not supported")
+            if codebook.numel() > 4096:
+                raise NotImplementedError("scalar codebooks above 4096 entries are not supported")
             if tuple(indices.shape) != (out_features, in_features):
                 raise ValueError(f"indices shape {tuple(indices.shape)} != ({out_features}, {in_features})")
-            indices = indices.to(torch.uint8)
+            # uint8 up to 256 entries, int16 above (reference helix_linear.py:166-176)
+            indices = (indices.to(torch.int32).to(torch.int16) if codebook.numel() > 256
+                       else indices.to(torch.uint8))
         else:
             if codebook.dim() != 2 or codebook.shape[1] != 2 or codebook.shape[0] > 4096:
                 raise NotImplementedError("pair codebooks are [k <= 4096, 2]")
@@ -165,12 +169,19 @@ class HelixLinear(nn.Module):
         if self.vector_dim != 1:
             self._recompute_derived_pairs()
             return
-        self._fmt = _hxq.FMT_SCALAR
         self.index_packing = None
-        if self.indices.dtype != torch.uint8:
-            if self.codebook.numel() > 256:
-                raise NotImplementedError("uint16 indices are not supported")
+        k = self.codebook.numel()
+        if k > 4096:
+            raise NotImplementedError("scalar codebooks above 4096 entries are not supported")
+        if k > 256:
+            if self.indices.dtype != torch.int16:
+                self.register_buffer("indices",
+                                     self.indices.to(torch.int32).to(torch.int16).contiguous())
+            if self.codebook.dtype != torch.float32:
+                self.register_buffer("codebook", self.codebook.float().contiguous())
+        elif self.indices.dtype != torch.uint8:
             self.register_buffer("indices", self.indices.to(torch.uint8).contiguous())
+        self._fmt = _hxq.FMT_SCALAR_U16 if k > 256 else _hxq.FMT_SCALAR
         if self.bias is not None and self.bias.dtype != torch.float32:
             self.register_buffer("bias", self.bias.float().contiguous())
         has_affine = self.group_scale is not None
@@ -203,7 +214,8 @@ class HelixLinear(nn.Module):
                 self.register_buffer(name, None)
         # the MFMA GEMM steps K by 64 and reads one affine group per step, in
         # the layout [K/G, OUT, 2] = {scale, offset} (derived, not saved)
-        self._gemm_ok = self.in_features % 64 == 0 and (not has_affine or self.group_size % 64 == 0)
+        self._gemm_ok = (self._fmt == _hxq.FMT_SCALAR and self.in_features % 64 == 0 and
+                         (not has_affine or self.group_size % 64 == 0))
         self.register_buffer(
             "_affine_t",
             torch.stack([self.group_scale.t(), self.group_offset.t()], dim=-1).contiguous()
@@ -289,16 +301,17 @@ class HelixLinear(nn.Module):
         """The codebook as the scalar kernels read it: fp32 [256] (uint8 indices reach every
         entry).  A 256-entry fp32 codebook is used as is; a shorter one gets a zero-padded
         copy, rebuilt whenever the codebook tensor, its contents version or its device
-        changes (e.g. after load_state_dict or .to())."""
+        changes (e.g. after load_state_dict or .to()).  Codebooks above 256 entries
+        (int16 indices) are read as they are: those kernels take the entry count."""
         cb = self.codebook
         if cb.dtype == torch.float32 and cb.numel() == 256 and cb.is_contiguous():
             return cb
+        if cb.numel() > 256:
+            return cb.contiguous()
         key = (cb.data_ptr(), cb._version, cb.device, cb.numel(), cb.dtype)
         cache = getattr(self, "_kcb_cache", None)
         if cache is None or cache[0] != key:
             c = cb.reshape(-1).float()
-            if c.numel() > 256:
-                raise NotImplementedError("scalar codebooks above 256 entries are not supported")
             cache = (key, torch.cat([c, c.new_zeros(256 - c.numel())]).contiguous())
             self._kcb_cache = cache
         return cache[1]
@@ -383,8 +396,8 @@ class HelixLinear(nn.Module):
         out = torch.empty(n, self.out_features, dtype=out_dtype, device=x2.device)
         if n == 0:
             pass
-        elif self.vector_dim != 1:
-            self._forward_hip_pairs(x2, rp, col, delta, out)
+        elif self.vector_dim != 1 or self._fmt != _hxq.FMT_SCALAR:
+            self._forward_hip_fmt(x2, rp, col, delta, out)
         elif n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv"
             _hxq.gemv(x2, self.indices, self._kcb, self.group_scale, self.group_offset,
@@ -406,12 +419,15 @@ class HelixLinear(nn.Module):
             out += ((xf @ self.svd_Vt.t()) * self.svd_s.unsqueeze(0)) @ self.svd_U.t()
         return out.reshape(*orig_shape[:-1], self.out_features)
 
-    def _forward_hip_pairs(self, x2, rp, col, delta, out) -> None:
+    def _forward_hip_fmt(self, x2, rp, col, delta, out) -> None:
+        """Pair codebooks and int16-index scalar codebooks."""
         n = x2.shape[0]
         if n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv_fmt"
             _hxq.gemv_fmt(x2, self._fmt, self.indices, self.out_features, codebook=self.codebook,
-                          sc_row_ptr=rp, sc_col=col, sc_delta=delta, bias=self.bias, out=out)
+                          group_scale=self.group_scale, group_offset=self.group_offset,
+                          group_size=self.group_size, sc_row_ptr=rp, sc_col=col, sc_delta=delta,
+                          bias=self.bias, out=out)
             return
         # many rows: HIP dequant of row tiles, then the library GEMM on them
         self._last_dispatch_path = "hip_dequant_gemm"
@@ -419,7 +435,9 @@ class HelixLinear(nn.Module):
         for r0 in range(0, self.out_features, step):
             r1 = min(self.out_features, r0 + step)
             w = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features, self.in_features,
-                                 codebook=self.codebook, sc_row_ptr=rp, sc_col=col,
+                                 codebook=self.codebook, group_scale=self.group_scale,
+                                 group_offset=self.group_offset, group_size=self.group_size,
+                                 sc_row_ptr=rp, sc_col=col,
                                  sc_val=None if rp is None else self._sc_val, row_begin=r0,
                                  row_end=r1)
             y = x2 @ w.to(x2.dtype).t()
@@ -466,14 +484,22 @@ class HelixLinear(nn.Module):
             if self.has_svd and not self._cell_skip_svd:
                 tile = tile + (self.svd_U[start_row:end_row] * self.svd_s.unsqueeze(0)) @ self.svd_Vt
             return tile
-        if self.indices.is_cuda:
+        if self.indices.is_cuda and self._fmt == _hxq.FMT_SCALAR_U16:
+            tile = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features, self.in_features,
+                                    codebook=self.codebook, group_scale=self.group_scale,
+                                    group_offset=self.group_offset, group_size=self.group_size,
+                                    sc_row_ptr=self._sc_row_ptr if apply_sc else None,
+                                    sc_col=self._sc_col if apply_sc else None,
+                                    sc_val=self._sc_val if apply_sc else None,
+                                    row_begin=start_row, row_end=end_row)
+        elif self.indices.is_cuda:
             tile = _hxq.dequant_f32(self.indices, self._kcb, self.group_scale,
                                     self.group_offset, self.group_size,
                                     self._sc_row_ptr if apply_sc else None,
                                     self._sc_col if apply_sc else None,
                                     self._sc_val if apply_sc else None, start_row, end_row)
         else:
-            tile = self.codebook[self.indices[start_row:end_row].long()]
+            tile = self.codebook[self.indices[start_row:end_row].long() & 0xffff]
             if self.group_scale is not None:
                 s = self.group_scale[start_row:end_row].repeat_interleave(self.group_size, dim=1)
                 o = self.group_offset[start_row:end_row].repeat_interleave(self.group_size, dim=1)
@@ -575,8 +601,11 @@ class HelixLinear(nn.Module):
         if self.vector_dim != 1:
             b = self.indices.numel() * self.indices.element_size() + self.codebook.numel() * 4
             return b + ((self.out_features + 1) * 4 + nnz * 8 if nnz else 0)
+        wide = self.codebook.numel() > 256
         return compressed_bytes(self.out_features, self.in_features,
-                                self.group_size if self.group_scale is not None else None, nnz)
+                                self.group_size if self.group_scale is not None else None, nnz,
+                                index_bytes=2 if wide else 1,
+                                codebook_entries=self.codebook.numel() if wide else 256)
 
     def extra_repr(self) -> str:
         parts = [f"in_features={self.in_features}", f"out_features={self.out_features}"]
@@ -599,15 +628,17 @@ class HelixLinear(nn.Module):
                               group_size: int = 128) -> "HelixLinear":
         """Empty shell whose buffers a safetensors load fills; then call
         ``_recompute_derived()`` (reference helix_linear.py:1020-1119)."""
-        if vector_dim not in (1, 2) or (vector_dim == 1 and n_clusters > 256):
-            raise NotImplementedError("scalar codebooks take k <= 256, vector codebooks d = 2")
+        if vector_dim not in (1, 2) or (vector_dim == 1 and n_clusters > 4096):
+            raise NotImplementedError("scalar codebooks take k <= 4096, vector codebooks d = 2")
         inst = cls.__new__(cls)
         nn.Module.__init__(inst)
         inst._init_attrs(in_features, out_features, tensor_name, compute_dtype, vector_dim,
                          group_size)
         if vector_dim == 1:
             inst.register_buffer("codebook", torch.zeros(n_clusters, dtype=torch.float32))
-            inst.register_buffer("indices", torch.zeros(out_features, in_features, dtype=torch.uint8))
+            # int16 for k > 256, uint8 otherwise (reference helix_linear.py:1093-1100)
+            inst.register_buffer("indices", torch.zeros(
+                out_features, in_features, dtype=torch.int16 if n_clusters > 256 else torch.uint8))
         else:
             inst.register_buffer("codebook", torch.zeros(n_clusters, 2, dtype=torch.float32))
             n_pairs = out_features * (in_features // 2)

@@ -136,8 +136,9 @@ def _replace_with_helix_linear(model: nn.Module, compressed: set, compute_dtype=
         if isinstance(module, nn.Embedding):
             k = k_map.get(name, n_clusters_default)
             module.register_buffer("codebook", torch.zeros(k, dtype=torch.float32))
-            module.register_buffer("indices", torch.zeros(module.num_embeddings,
-                                                          module.embedding_dim, dtype=torch.uint8))
+            module.register_buffer("indices", torch.zeros(
+                module.num_embeddings, module.embedding_dim,
+                dtype=torch.int16 if k > 256 else torch.uint8))
             embeds.add(name)
         elif isinstance(module, nn.Linear):
             shell = HelixLinear.from_quantized_config(

@@ -95,13 +95,15 @@ def check_kernel_shapes(in_features: int, group_size: int, has_affine: bool) -> 
                          f"in_features={in_features}")
 
 
-def compressed_bytes(out_f: int, in_f: int, group_size: Optional[int], nnz: int) -> int:
+def compressed_bytes(out_f: int, in_f: int, group_size: Optional[int], nnz: int,
+                     index_bytes: int = 1, codebook_entries: int = 256) -> int:
     """Bytes one contraction must read from the compressed form (not activations).
 
-    indices 1 B/weight + scale/offset 8 B per group + CSR row_ptr 4 B/row
-    + (col 4 B + delta 4 B) per sidecar entry + codebook 1 KiB.
+    indices 1 B/weight (2 B for codebooks above 256 entries) + scale/offset 8 B
+    per group + CSR row_ptr 4 B/row + (col 4 B + delta 4 B) per sidecar entry
+    + codebook 4 B/entry (1 KiB at 256 entries).
     """
-    b = out_f * in_f + 1024
+    b = out_f * in_f * index_bytes + 4 * codebook_entries
     if group_size:
         b += out_f * (in_f // group_size) * 8
     if nnz:

@@ -5,10 +5,13 @@ Writes the directory layout of the reference ``CDNAv3Writer``
 indices.bin, sidecar.npz with fp16 values, codebook SHA-256), plus the affine
 extension files group_scale.npy / group_offset.npy with meta "group_size".
 ``write_quantized`` takes an already quantised tensor; ``write_tensor``
-quantises one (the reference's scalar ``_write_quantized`` path,
-``hxq_writer_v3.py:162-336``): k-means (or uniform) codebook, nearest-entry
-indices, percentile sidecar trimmed to ``max_corrections`` -- on the GPU for
-device tensors.
+quantises one under a ``TensorPolicy`` (reference ``write_tensor``,
+``hxq_writer_v3.py:49-89``, and the ``_write_quantized`` path, ``:162-336``):
+exact fp16 storage for 1-D tensors and exact-policy classes, otherwise a
+k-means (or uniform) codebook, nearest-entry indices (uint8 up to 256
+entries, uint16 above, scalar and pair codebooks alike: ``:174-198``),
+percentile sidecar trimmed to ``max_corrections`` -- on the GPU for device
+tensors.
 """
 from __future__ import annotations
 
@@ -20,6 +23,7 @@ from pathlib import Path
 import numpy as np
 
 from .generate_sidecars_v3 import write_sidecar_npz
+from .tensor_policy import TensorPolicy, classify_tensor, get_default_policy, get_policy
 
 
 def _safe_name(name: str) -> str:
@@ -36,7 +40,7 @@ class CDNAv3Writer:
                         group_offset=None, group_size: int = 128, extra_meta=None) -> Path:
         codebook = np.ascontiguousarray(codebook, dtype=np.float32)
         vdim = int(codebook.shape[1]) if codebook.ndim == 2 else 1
-        wide = vdim > 1 or codebook.shape[0] > 256
+        wide = codebook.shape[0] > 256
         indices = np.ascontiguousarray(indices, dtype=np.uint16 if wide else np.uint8)
         rows, cols = indices.shape[0], indices.shape[1] * vdim
         out = self.base_dir / f"{_safe_name(tensor_name)}.cdnav3"
@@ -81,19 +85,40 @@ class CDNAv3Writer:
         return {"tensor_name": tensor_name, "storage_mode": "exact", "shape": list(arr.shape),
                 "original_bytes": arr.nbytes, "compressed_bytes": out.stat().st_size}
 
-    def write_tensor(self, tensor, tensor_name: str, n_clusters: int = 256,
-                     percentile: float = 99.9, use_kmeans: bool = True,
-                     sidecar_enabled: bool = True, max_corrections: int = 512,
-                     storage_mode: str = "codebook+sidecar", tensor_class: str = "unknown",
-                     source_artifact: str = "", group_size=None, vector_dim: int = 1) -> dict:
-        """Quantise a 2-D fp32 tensor (numpy, or a device tensor for the GPU
-        path) and write its directory; returns the stats the reference writes
-        to stats.json.  group_size (extension): also fit the per-group affine
-        (least squares per row and group, sidecar positions excluded) and
-        write group_scale / group_offset.  vector_dim 2: pair codebook
-        [n_clusters <= 4096, 2] over adjacent columns and uint16 indices
-        [rows, cols / 2] (reference hxq_writer_v3.py:174-212; device tensors
+    def write_tensor(self, tensor, tensor_name: str, policy: TensorPolicy = None,
+                     source_artifact: str = "", group_size=None, **overrides) -> dict:
+        """Quantise a tensor (numpy, or a device tensor for the GPU path) and write
+        it; returns the stats the reference writes to stats.json.
+
+        policy: the reference's TensorPolicy (None: the default of the class
+        ``classify_tensor`` gives the name and shape).  ``overrides`` replace
+        policy fields (n_clusters, percentile, use_kmeans, sidecar_enabled,
+        max_corrections, storage_mode, vector_dim).  1-D tensors and exact
+        policies are written as fp16 ``.npy`` (``write_exact``).
+        group_size (extension): also fit the per-group affine (least squares
+        per row and group, sidecar positions excluded) and write group_scale /
+        group_offset.  vector_dim 2: pair codebook [n_clusters <= 4096, 2] over
+        adjacent columns (reference hxq_writer_v3.py:174-212; device tensors
         only, no affine)."""
+        import dataclasses
+
+        if policy is None:
+            policy = get_default_policy(classify_tensor(tensor_name, shape=tuple(tensor.shape)))
+        if overrides:
+            policy = dataclasses.replace(policy, **overrides)
+        if policy.storage_mode == "morpho":
+            raise NotImplementedError("the morpho codec is not part of the HXQ path")
+        if len(tensor.shape) == 1 or policy.storage_mode == "exact":
+            return self.write_exact(tensor, tensor_name)
+        if len(tensor.shape) > 2:
+            tensor = tensor.reshape(-1, tensor.shape[-1])
+        return self._write_quantized(tensor, tensor_name, policy, source_artifact, group_size)
+
+    def _write_quantized(self, tensor, tensor_name, policy, source_artifact, group_size):
+        n_clusters, percentile = policy.n_clusters, policy.percentile
+        use_kmeans, sidecar_enabled = policy.use_kmeans, policy.sidecar_enabled
+        max_corrections, storage_mode = policy.max_corrections, policy.storage_mode
+        vector_dim, tensor_class = policy.vector_dim, policy.tensor_class.value
         import torch
 
         from .generate_sidecars_v3 import find_outliers_percentile
@@ -102,8 +127,12 @@ class CDNAv3Writer:
                                   fit_group_affine)
 
         dev = isinstance(tensor, torch.Tensor) and tensor.is_cuda
+        if dev and vector_dim == 1 and n_clusters > 256:
+            raise NotImplementedError("the GPU encoder fits scalar codebooks of at most 256 "
+                                      "entries; pass a host array for n_clusters > 256")
         if not dev:
-            tensor = np.asarray(tensor, dtype=np.float32)
+            tensor = np.asarray(tensor.cpu() if isinstance(tensor, torch.Tensor) else tensor,
+                                dtype=np.float32)
         rows, cols = tensor.shape
         flat = tensor.reshape(-1).float() if dev else tensor.ravel()
         if vector_dim > 1:
@@ -177,18 +206,22 @@ class CDNAv3Writer:
         return stats
 
 
-def compress_model(model, out_dir, device=None, group_size=None, n_clusters: int = 256,
-                   percentile: float = 99.9, max_corrections: int = 512,
+def compress_model(model, out_dir, device=None, group_size=None, n_clusters=None,
+                   percentile=None, max_corrections=None,
                    skip_modules=("embed_tokens", "lm_head"), vector_dim: int = 1,
                    module_vector_dim_map=None) -> dict:
     """Encode every nn.Linear weight of `model` into ``{name}.cdnav3`` under
     out_dir (on `device` when given: the GPU encoder) and every other tensor
     (norms, embeddings, biases) as an exact fp16 ``.npy``; writes
-    manifest.json.  Modules whose name contains an entry of `skip_modules`
-    stay exact (config 1 keeps the embedding / LM head uncompressed).
-    vector_dim 2 (or a module-name substring -> vector_dim map, first match
-    wins) encodes those weights with a pair codebook of n_clusters entries
-    (device required, no affine).  Returns the manifest."""
+    manifest.json.  Each weight is written under ``get_policy(name, shape)``
+    (the reference's per-class defaults: q/k sidecars at the 99.95th
+    percentile, unclassified tensors at most 256 corrections); n_clusters /
+    percentile / max_corrections, when given, override every policy.
+    Modules whose name contains an entry of `skip_modules` stay exact
+    (config 1 keeps the embedding / LM head uncompressed).  vector_dim 2 (or
+    a module-name substring -> vector_dim map, first match wins) encodes those
+    weights with a pair codebook (device required, no affine).  Returns the
+    manifest."""
     import torch
     import torch.nn as nn
 
@@ -209,10 +242,16 @@ def compress_model(model, out_dir, device=None, group_size=None, n_clusters: int
                 if key in name:
                     vd = int(v)
                     break
-            st = w.write_tensor(src, name, n_clusters=n_clusters, percentile=percentile,
-                                max_corrections=max_corrections,
-                                group_size=None if vd > 1 else group_size,
-                                tensor_class="linear", vector_dim=vd)
+            over = {k: v for k, v in (("n_clusters", n_clusters), ("percentile", percentile),
+                                      ("max_corrections", max_corrections)) if v is not None}
+            if vd > 1:
+                over["vector_dim"] = vd
+                over.setdefault("n_clusters", 4096)
+            policy = get_policy(name, tuple(t.shape))
+            if policy.storage_mode == "exact":  # a linear the policy keeps exact
+                policy = TensorPolicy(policy.tensor_class, "codebook+sidecar")
+            st = w.write_tensor(src, name, policy=policy,
+                                group_size=None if vd > 1 else group_size, **over)
             d = w.base_dir / f"{_safe_name(name)}.cdnav3"
             st["compressed_bytes"] = sum(f.stat().st_size for f in d.iterdir()
                                          if f.name not in ("meta.json", "stats.json"))

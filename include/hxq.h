@@ -68,6 +68,11 @@ typedef enum hxq_dtype {
  *                    the per-group fp32 scale/offset (reference
  *                    triton_affine_group_matmul.py:181-259, 366-383)
  *                    (0.75 B/weight).
+ *   HXQ_FMT_SCALAR_U16  uint16 index into a <= 4096-entry fp32 codebook (a
+ *                    scalar codebook above 256 entries: reference
+ *                    helix_linear.py:166-176 int16 indices, writer index_dtype
+ *                    "uint16", hxq_writer_v3.py:187-198), optional per-group
+ *                    affine as HXQ_FMT_SCALAR (2 B/weight).
  * Both packed forms are little-endian bit streams (field i at bit 12i / 6i of
  * the row's bytes).  The uint8 affine-group format of the same reference file
  * is HXQ_FMT_SCALAR with the identity codebook cb[j] = j. */
@@ -75,7 +80,8 @@ typedef enum hxq_format {
     HXQ_FMT_SCALAR = 0,
     HXQ_FMT_VQ2_U16 = 1,
     HXQ_FMT_VQ2_P12 = 2,
-    HXQ_FMT_AF6 = 3
+    HXQ_FMT_AF6 = 3,
+    HXQ_FMT_SCALAR_U16 = 4
 } hxq_format;
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -144,8 +150,9 @@ typedef struct hxq_matrix {
  * hxq_gemv_fmt: hxq_gemv for any index format (HXQ_FMT_*); y = x W^T (+ bias),
  * 1-4 activation rows, fp32 accumulation, sidecar CSR in weight coordinates
  * (sc_delta = value - reconstruction).  Pair formats take `codebook`
- * [n_codes, 2] and no affine; HXQ_FMT_AF6 takes the affine and no codebook.
- * Indices must lie below n_codes.
+ * [n_codes, 2] and no affine; HXQ_FMT_AF6 takes the affine and no codebook;
+ * HXQ_FMT_SCALAR_U16 takes `codebook` [n_codes <= 4096] and an optional
+ * affine.  Indices must lie below n_codes (reads past it give 0).
  * Replaces: the decode branches of fused_vq2d_matmul
  * (triton_vq2d_matmul.py:171-280, with the 12-bit gather of
  * triton_gather_12bit.py:43-157) and fused_affine_group_matmul_packed6

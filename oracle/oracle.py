@@ -109,7 +109,10 @@ def _c(a, dtype):
 
 def reconstruct(indices, codebook, group_scale=None, group_offset=None, group_size=128,
                 sidecar_positions=None, sidecar_values=None, row_begin=0, row_end=None):
-    """C restatement; returns fp32 [row_end-row_begin, in_features]."""
+    """C restatement; returns fp32 [row_end-row_begin, in_features].  uint8
+    indices only (wide indices: reconstruct_np)."""
+    if np.asarray(indices).dtype.itemsize != 1:
+        raise ValueError("the C reconstruction takes uint8 indices; use reconstruct_np")
     idx = _c(indices, np.uint8)
     out_f, in_f = idx.shape
     row_end = out_f if row_end is None else row_end

@@ -151,3 +151,60 @@ def test_affine_group_entry_points(dev):
     x = torch.from_numpy(rs.randn(2, inp).astype(np.float32))
     yr = affine_group_matmul_reference(x, q6, s, o, G, b)
     assert _maxrel(yr.numpy(), oracle.linear_f64(x.numpy(), W6, b.numpy())) <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# scalar codebooks above 256 entries: uint16 indices (int16 in memory)
+# ---------------------------------------------------------------------------
+def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001):
+    rs = np.random.RandomState(seed)
+    cb = np.sort(rs.standard_normal(k).astype(np.float32) * 0.02)
+    idx = rs.randint(0, k, (out_f, in_f)).astype(np.uint16)
+    gs = go = None
+    if affine:
+        gs = rs.uniform(0.95, 1.05, (out_f, in_f // 128)).astype(np.float32)
+        go = rs.normal(0, 1e-4, (out_f, in_f // 128)).astype(np.float32)
+    nnz = int(round(density * out_f * in_f))
+    pos = np.sort(rs.choice(out_f * in_f, nnz, replace=False)).astype(np.int64)
+    val = (np.where(rs.random_sample(nnz) < 0.5, -1, 1) * rs.uniform(4, 8, nnz) * 0.02).astype(
+        np.float16).astype(np.float32)
+    t = lambda a: None if a is None else torch.from_numpy(a)
+    m = HelixLinear(in_f, out_f, t(cb), t(idx.astype(np.int16)), t(pos), t(val),
+                    group_scale=t(gs), group_offset=t(go), group_size=128)
+    return m, oracle.reconstruct_np(idx, cb, gs, go, 128, pos, val)
+
+
+@pytest.mark.parametrize("k,out_f,in_f,affine", [
+    (512, 2048, 2048, True),     # the reference's k = 512 case at config-0 size
+    (4096, 300, 1024, True),     # largest codebook, ragged rows
+    (1000, 256, 11008, False),   # long rows, no affine
+])
+def test_wide_scalar_dequant_and_gemv(dev, k, out_f, in_f, affine):
+    print(f"uint16 scalar k={k} out={out_f} in={in_f} affine={affine}", flush=True)
+    m, W = _wide_layer(out_f, in_f, k, seed=k + out_f, affine=affine)
+    m = m.to(dev)
+    assert m._fmt == _hxq.FMT_SCALAR_U16 and m.indices.dtype == torch.int16
+    np.testing.assert_array_equal(m.decode_weight().cpu().numpy().view(np.uint32), W.view(np.uint32))
+    blk = m._dequant_tile(17, 133).cpu().numpy()
+    np.testing.assert_array_equal(blk.view(np.uint32), W[17:133].view(np.uint32))
+    for n in (1, 3):
+        x = torch.randn(n, in_f, generator=torch.Generator().manual_seed(n))
+        y = m(x.to(dev))
+        assert m._last_dispatch_path == "hip_gemv_fmt"
+        assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), W)) <= 1e-5
+    xb = torch.randn(1, in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    yb = m(xb.to(dev))
+    assert yb.dtype == torch.bfloat16
+    assert _maxrel(yb.float().cpu().numpy(), oracle.linear_f64(xb.float().numpy(), W)) <= 2e-2
+
+
+def test_wide_scalar_many_rows(dev):
+    m, W = _wide_layer(384, 1024, 512, seed=5)
+    m = m.to(dev)
+    x = torch.randn(40, 1024, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    y = m(x.to(dev))
+    assert y.dtype == torch.bfloat16
+    assert _maxrel(y.float().cpu().numpy(), oracle.linear_f64(x.float().numpy(), W)) <= 2e-2
+    x32 = torch.randn(9, 1024, generator=torch.Generator().manual_seed(5))
+    y32 = m(x32.to(dev))
+    assert _maxrel(y32.cpu().numpy(), oracle.linear_f64(x32.numpy(), W)) <= 1e-5

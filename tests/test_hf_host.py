@@ -17,6 +17,7 @@ from helix_substrate import hf_quantizer  # noqa: E402,F401  (registers cdna_v3)
 from helix_substrate.convert_safetensors import convert_model  # noqa: E402
 from helix_substrate.helix_linear import HelixLinear  # noqa: E402
 from helix_substrate.hxq_writer_v3 import CDNAv3Writer, compress_model  # noqa: E402
+from helix_substrate.tensor_policy import TensorClass, TensorPolicy  # noqa: E402
 
 CFG = dict(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=4,
            num_key_value_heads=2, vocab_size=512, max_position_embeddings=64,
@@ -110,7 +111,10 @@ def test_compressed_embedding_is_reconstructed(converted, tmp_path):
     (cdna / "model_embed_tokens_weight.npy").unlink()
     (cdna / "model_embed_tokens_weight.npy.meta.json").unlink()
     emb = model.model.embed_tokens.weight.detach().float().numpy()
-    CDNAv3Writer(cdna).write_tensor(emb, "model.embed_tokens.weight", sidecar_enabled=False)
+    # embeddings default to exact storage: ask for a codebook explicitly
+    CDNAv3Writer(cdna).write_tensor(emb, "model.embed_tokens.weight",
+                                    policy=TensorPolicy(TensorClass.EMBEDDING, "codebook",
+                                                        sidecar_enabled=False))
     convert_model(cdna, tmp / "orig", tmp_path / "hf")
     loaded = AutoModelForCausalLM.from_pretrained(tmp_path / "hf").eval()
     d = cdna / "model_embed_tokens_weight.cdnav3"
@@ -119,3 +123,26 @@ def test_compressed_embedding_is_reconstructed(converted, tmp_path):
     np.testing.assert_array_equal(loaded.model.embed_tokens.weight.detach().numpy(), cb[idx])
     # tied LM head shares the rebuilt embedding
     assert torch.equal(loaded.lm_head.weight, loaded.model.embed_tokens.weight)
+
+
+def test_k512_checkpoint_round_trip(tmp_path):
+    """A checkpoint whose linears use 512-entry scalar codebooks (uint16 on
+    disk): the converter records module_k_map, from_pretrained builds int16
+    shells, and the fp32 logits equal the dense twin's."""
+    torch.manual_seed(2)
+    model = Qwen2ForCausalLM(Qwen2Config(**CFG)).eval()
+    model.save_pretrained(tmp_path / "orig")
+    compress_model(model, tmp_path / "cdna", n_clusters=512)
+    stats = convert_model(tmp_path / "cdna", tmp_path / "orig", tmp_path / "hf")
+    assert len(stats["module_k_map"]) == 14 and set(stats["module_k_map"].values()) == {512}
+    q = json.loads((tmp_path / "hf" / "config.json").read_text())["quantization_config"]
+    assert q["module_k_map"]["model.layers.1.mlp.down_proj"] == 512
+    loaded = AutoModelForCausalLM.from_pretrained(tmp_path / "hf").eval()
+    m = loaded.model.layers[0].mlp.gate_proj
+    assert isinstance(m, HelixLinear) and m.indices.dtype == torch.int16
+    assert m.codebook.numel() == 512 and int(m.indices.max()) >= 256
+    twin = _dense_twin(model, loaded)
+    ids = torch.randint(0, CFG["vocab_size"], (2, 9), generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        a, b = loaded(ids).logits, twin(ids).logits
+    assert torch.allclose(a, b, rtol=1e-5, atol=1e-5 * float(b.abs().max()))

@@ -231,5 +231,5 @@ def test_rejects_unsupported_shapes():
     T = synth.to_torch(L)
     with pytest.raises(ValueError):
         HelixLinear(120, 8, T["codebook"], T["indices"][:, :120])
-    with pytest.raises(NotImplementedError):
-        HelixLinear(128, 8, torch.zeros(512), T["indices"])
+    with pytest.raises(NotImplementedError):      # scalar codebooks hold <= 4096 entries
+        HelixLinear(128, 8, torch.zeros(4097), T["indices"])
