@@ -47,6 +47,7 @@ from .hxq_format import build_sidecar_csr, check_kernel_shapes, compressed_bytes
 
 _CPU_TILE_ROWS = 256
 _GEMV_MAX_ROWS = 4
+_GEMV_MULTI_ROW_MAX_K = 8192  # 2-4 row GEMV launches hold 8 K-chunks of 1024 per wave
 _DEQUANT_TILE_ELEMS = 1 << 24  # fp32 elements per dequantised row tile (64 MiB)
 
 
@@ -400,8 +401,10 @@ class HelixLinear(nn.Module):
             self._forward_hip_fmt(x2, rp, col, delta, out)
         elif n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv"
-            _hxq.gemv(x2, self.indices, self._kcb, self.group_scale, self.group_offset,
-                      self.group_size, rp, col, delta, self.bias, out=out)
+            for r0, r1 in self._gemv_row_groups(n):
+                _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
+                          self.group_offset, self.group_size, rp, col, delta, self.bias,
+                          out=out[r0:r1])
         elif x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
             self._last_dispatch_path = "hip_gemm"
             _hxq.gemm(x2, self.indices, self._kcb, self._affine_t, self.group_size, rp, col,
@@ -409,8 +412,7 @@ class HelixLinear(nn.Module):
         else:
             # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
             self._last_dispatch_path = "hip_gemv_rows"
-            for r0 in range(0, n, _GEMV_MAX_ROWS):
-                r1 = min(n, r0 + _GEMV_MAX_ROWS)
+            for r0, r1 in self._gemv_row_groups(n):
                 _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
                           self.group_offset, self.group_size, rp, col, delta, self.bias,
                           out=out[r0:r1])
@@ -419,15 +421,23 @@ class HelixLinear(nn.Module):
             out += ((xf @ self.svd_Vt.t()) * self.svd_s.unsqueeze(0)) @ self.svd_U.t()
         return out.reshape(*orig_shape[:-1], self.out_features)
 
+    def _gemv_row_groups(self, n):
+        """Row ranges of the GEMV launches for n activation rows: groups of up to
+        4 rows, or single rows when in_features exceeds the multi-row limit."""
+        step = _GEMV_MAX_ROWS if self.in_features <= _GEMV_MULTI_ROW_MAX_K else 1
+        return [(r0, min(n, r0 + step)) for r0 in range(0, n, step)]
+
     def _forward_hip_fmt(self, x2, rp, col, delta, out) -> None:
         """Pair codebooks and int16-index scalar codebooks."""
         n = x2.shape[0]
         if n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv_fmt"
-            _hxq.gemv_fmt(x2, self._fmt, self.indices, self.out_features, codebook=self.codebook,
-                          group_scale=self.group_scale, group_offset=self.group_offset,
-                          group_size=self.group_size, sc_row_ptr=rp, sc_col=col, sc_delta=delta,
-                          bias=self.bias, out=out)
+            for r0, r1 in self._gemv_row_groups(n):
+                _hxq.gemv_fmt(x2[r0:r1], self._fmt, self.indices, self.out_features,
+                              codebook=self.codebook, group_scale=self.group_scale,
+                              group_offset=self.group_offset, group_size=self.group_size,
+                              sc_row_ptr=rp, sc_col=col, sc_delta=delta, bias=self.bias,
+                              out=out[r0:r1])
             return
         # many rows: HIP dequant of row tiles, then the library GEMM on them
         self._last_dispatch_path = "hip_dequant_gemm"

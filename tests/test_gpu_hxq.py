@@ -246,3 +246,15 @@ def test_headline_down_gemv_bf16(dev):
     y32 = _hxq.gemv(xb.to(dev), m.indices, m.codebook, m.group_scale, m.group_offset, 128,
                     m._sc_row_ptr, m._sc_col, m._sc_delta, None, out_dtype=torch.float32)
     assert _maxrel(y32.cpu().numpy(), yr) <= TOL_F32
+
+
+@pytest.mark.parametrize("n", [2, 4])
+def test_gemv_few_rows_long_k(dev, n):
+    """2-4 activation rows with in_features above 8192 (config-1 down_proj at
+    batch 2-4): launched row by row, still within 1e-5."""
+    L, T = _layer(512, 11008, seed=60 + n)
+    m = _module(T, dev)
+    x = torch.randn(n, 11008, generator=torch.Generator().manual_seed(n))
+    y = m(x.to(dev))
+    assert m._last_dispatch_path == "hip_gemv"
+    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= TOL_F32
