@@ -134,6 +134,8 @@ class HelixLinear(nn.Module):
         self._sidecar_norms = []
         self._cell_skip_svd = False
         self._cuda_graph_mode = False
+        # threaded CPU tiles (reference helix_linear.py:160-164, HELIX_WAVE_TILES=1)
+        self._wave_enabled = os.environ.get("HELIX_WAVE_TILES", "0") == "1"
         self.has_svd = False
         self.rank = 0
         self.has_channel_scales = False
@@ -370,6 +372,9 @@ class HelixLinear(nn.Module):
             if not self.codebook.is_cuda:
                 raise RuntimeError("HelixLinear buffers are on the CPU but the input is on the GPU")
             out = self._forward_hip(x)
+        elif getattr(self, "_wave_enabled", False):
+            self._last_dispatch_path = "wave"
+            out = self._forward_wave(x)
         else:
             self._last_dispatch_path = "naive"
             out = self._forward_naive(x)
@@ -470,6 +475,48 @@ class HelixLinear(nn.Module):
         if self.bias is not None:
             out += self.bias.unsqueeze(0)
         self._apply_sidecar_this_call = True
+        return out.reshape(*orig_shape[:-1], self.out_features)
+
+    def _forward_wave(self, x: torch.Tensor) -> torch.Tensor:
+        """CPU tensors, HELIX_WAVE_TILES=1: the 256-row tiles of _forward_naive run
+        on a thread pool, one worker per allowed core, each with one intra-op
+        thread and pinned to its core (reference helix_linear.py:824-879; the
+        tile -> core order is plain round-robin).  Tiles write disjoint output
+        columns, so no synchronisation is needed beyond joining the pool."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        orig_shape = x.shape
+        x2 = x.reshape(-1, self.in_features).float()
+        if self.has_channel_scales:
+            x2 = x2 / self.channel_scales.unsqueeze(0)
+        self._apply_sidecar_this_call = (self._policy_decide(x2)
+                                         if self._sc_row_ptr is not None else True)
+        out = torch.zeros(x2.shape[0], self.out_features, dtype=torch.float32)
+        tiles = [(r0, min(r0 + _CPU_TILE_ROWS, self.out_features))
+                 for r0 in range(0, self.out_features, _CPU_TILE_ROWS)]
+        try:
+            cores = sorted(os.sched_getaffinity(0))
+        except (AttributeError, OSError):
+            cores = list(range(os.cpu_count() or 1))
+
+        def work(i, r0, r1):
+            try:
+                os.sched_setaffinity(0, {cores[i % len(cores)]})
+            except (AttributeError, OSError):
+                pass
+            out[:, r0:r1] = x2 @ self._dequant_tile(r0, r1).t()
+
+        threads = torch.get_num_threads()
+        torch.set_num_threads(1)
+        try:
+            with ThreadPoolExecutor(max_workers=min(len(cores), len(tiles))) as pool:
+                for f in [pool.submit(work, i, r0, r1) for i, (r0, r1) in enumerate(tiles)]:
+                    f.result()
+        finally:
+            torch.set_num_threads(threads)
+            self._apply_sidecar_this_call = True
+        if self.bias is not None:
+            out += self.bias.unsqueeze(0)
         return out.reshape(*orig_shape[:-1], self.out_features)
 
     # ---------------------------------------------------------- reconstruction

@@ -233,3 +233,23 @@ def test_rejects_unsupported_shapes():
         HelixLinear(120, 8, T["codebook"], T["indices"][:, :120])
     with pytest.raises(NotImplementedError):      # scalar codebooks hold <= 4096 entries
         HelixLinear(128, 8, torch.zeros(4097), T["indices"])
+
+
+def test_forward_wave_threaded_tiles_match_oracle(monkeypatch):
+    """HELIX_WAVE_TILES=1: the threaded tile path (reference _forward_wave) gives
+    the oracle contraction, like the sequential tiles."""
+    monkeypatch.setenv("HELIX_WAVE_TILES", "1")
+    L = synth.make_layer_np(700, 512, seed=21, density=0.01)   # 3 tiles, ragged last
+    b = torch.linspace(-1, 1, 700)
+    m = _module(L, bias=b)
+    assert m._wave_enabled
+    x = torch.randn(5, 512, generator=torch.Generator().manual_seed(2))
+    threads = torch.get_num_threads()
+    y = m(x)
+    assert m._last_dispatch_path == "wave" and torch.get_num_threads() == threads
+    yr = oracle.linear_f64(x.numpy(), _oracle_w(L), b.numpy())
+    assert np.abs(y.numpy() - yr).max() / np.abs(yr).max() < 1e-5
+    monkeypatch.setenv("HELIX_WAVE_TILES", "0")
+    m2 = _module(L, bias=b)
+    torch.testing.assert_close(m2(x), y, rtol=1e-6, atol=1e-6)
+    assert m2._last_dispatch_path == "naive"
