@@ -467,6 +467,28 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
     err = dec.persistent_error()
     if err:
         raise RuntimeError(f"persistent decode reported error {err}")
+    # agreement of the two paths on logits (a random-init model's greedy tokens
+    # barely vary, so token equality alone says little): the same prompt, then
+    # 4 steps each, logits compared after every step
+    logit_steps = []
+    for path in ("graph", "persistent"):
+        dec.reset()
+        if path == "persistent":
+            for t in prompt.tolist():
+                dec.tok.fill_(t)
+                dec.step_persistent(1)
+        else:
+            dec.prefill(prompt)
+        rows = []
+        for _ in range(4):
+            if path == "graph":
+                dec._graph.replay()
+            else:
+                dec.step_persistent(1)
+            rows.append(dec.logits.clone())
+        logit_steps.append(torch.stack(rows).double())
+    lg, lp = logit_steps
+    logits_rel = float((lg - lp).abs().max() / lg.abs().max())
     hxq = dec.hxq_bytes_per_token()
     lm = dec.embed.numel() * 2
     per_tok_ms = min(ms_graph, ms_pers)
@@ -477,7 +499,9 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
            "hxq_bytes_per_token": hxq, "lm_head_bytes_per_token": lm,
            "gbs_weights": round((hxq + lm) / (per_tok_ms * 1e-3) / 1e9, 1),
            "first_tokens_persistent": toks_pers[:8].cpu().tolist(),
-           "first_tokens_graph": toks_graph[:8].cpu().tolist()}
+           "first_tokens_graph": toks_graph[:8].cpu().tolist(),
+           "logits_maxrel_persistent_vs_graph_4_steps": round(logits_rel, 7)}
+    dec.close()
     del dec
     torch.cuda.empty_cache()
     return out
