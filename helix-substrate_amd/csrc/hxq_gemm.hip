@@ -33,6 +33,7 @@
 // sorted order.  Pair mode computes gate rows (tile rows 0..127) and up rows
 // (128..255) of the same 128 features and writes silu(gate) * up.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "hxq_common.h"
@@ -826,6 +827,13 @@ SplitPlan split_plan(int64_t m_rows, int64_t out_features, int64_t in_features) 
 }
 }  // namespace
 
+static int gemm_dense(const void *x, int32_t x_dtype, const uint8_t *indices,
+                      const float *codebook, const float *group_affine, int32_t group_size,
+                      const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
+                      const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
+                      int64_t out_features, int64_t in_features, void *workspace,
+                      int64_t workspace_bytes, hipStream_t stream);
+
 extern "C" int64_t hxq_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
                                             int64_t in_features) {
     if (m_rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % kBK) return 0;
@@ -850,6 +858,81 @@ extern "C" int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indice
                            int64_t out_features, int64_t in_features, void *workspace,
                            int64_t workspace_bytes, hipStream_t stream) {
     clear_error();
+    return gemm_dense(x, x_dtype, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col,
+                      sc_val, bias, y, y_dtype, m_rows, out_features, in_features, workspace,
+                      workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// hxq_gemm_noalloc: hxq_gemm_ws with the split-K partials in a static device
+// array instead of a caller workspace, for callers that cannot allocate.
+// The array is a file-scope __device__ symbol: every GPU the library runs on
+// holds its own copy (kGemmScratchBytes) until the process ends.  Host code
+// never passes the symbol itself (a host-side stand-in, not a device
+// address): the device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current, and only that pointer reaches kernels.
+// The partials are fully overwritten by every call that uses them, so nothing
+// needs clearing; calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kGemmScratchBytes = int64_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kGemmScratchBytes];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of this device's scratch array (nullptr + error on failure).
+void *scratch_of_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+        set_error("hxq_gemm_noalloc: no usable current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error(std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int64_t hxq_gemm_noalloc_max_bytes(void) { return kGemmScratchBytes; }
+
+extern "C" int hxq_gemm_noalloc(const void *x, int32_t x_dtype, const uint8_t *indices,
+                                const float *codebook, const float *group_affine,
+                                int32_t group_size, const int32_t *sc_row_ptr,
+                                const int32_t *sc_col, const float *sc_val, const float *bias,
+                                void *y, int32_t y_dtype, int64_t m_rows, int64_t out_features,
+                                int64_t in_features, hipStream_t stream) {
+    clear_error();
+    const int64_t need = hxq_gemm_workspace_bytes(m_rows, out_features, in_features);
+    HXQ_REQUIRE(need <= kGemmScratchBytes,
+                "hxq_gemm_noalloc: this shape's split-K partials need " + std::to_string(need) +
+                    " bytes, more than the static " + std::to_string(kGemmScratchBytes) +
+                    "-byte scratch (use hxq_gemm_ws with a workspace)");
+    void *ws = nullptr;
+    if (need > 0) {
+        ws = scratch_of_current_device();
+        if (ws == nullptr) return HXQ_ERR_HIP;
+    }
+    return gemm_dense(x, x_dtype, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col,
+                      sc_val, bias, y, y_dtype, m_rows, out_features, in_features, ws, need,
+                      stream);
+}
+
+static int gemm_dense(const void *x, int32_t x_dtype, const uint8_t *indices,
+                      const float *codebook, const float *group_affine, int32_t group_size,
+                      const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
+                      const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
+                      int64_t out_features, int64_t in_features, void *workspace,
+                      int64_t workspace_bytes, hipStream_t stream) {
     HXQ_REQUIRE(x && indices && codebook && y, "x, indices, codebook and y are required");
     HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16,
                 "the MFMA GEMM takes bf16 or fp16 activations (fp32 goes through hxq_gemv)");

@@ -79,6 +79,7 @@ SIGNATURES = {
     "hxq_gemv_multi_silu": [P, P, P, I32, I32, I32, I64, P],
     "hxq_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemm_ws": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64, P],
+    "hxq_gemm_noalloc": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_affine_pack": [P, P, I64, I64, P, P],
     "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
                            I64, I64, I64, P, I64, P],
@@ -126,6 +127,7 @@ SIGNATURES_I64 = {
     "hxq_outliers_workspace_bytes": [I64],
     "hxq_vq2_workspace_bytes": [I64, I32],
     "hxq_gemm_workspace_bytes": [I64, I64, I64],
+    "hxq_gemm_noalloc_max_bytes": [],
 }
 
 
@@ -409,6 +411,30 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
                            _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype), m, out_f,
                            in_f, _ptr(ws), nbytes, _stream(x))
     _check("hxq_gemm_ws", rc)
+    return out
+
+
+def gemm_noalloc(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_val,
+                 bias=None, out_dtype=None, out=None):
+    """``gemm`` through hxq_gemm_noalloc: the split-K partials go to the library's
+    static per-device scratch instead of a workspace allocated here (nothing is
+    allocated when ``out`` is given).  Overlapping calls on one GPU race."""
+    m, in_f = x.shape
+    out_f = indices.shape[0]
+    if indices.shape[1] != in_f:
+        raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
+    if out is None:
+        out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
+    _need_device(x, indices, codebook, group_affine, sc_row_ptr, sc_col, sc_val, bias, out)
+    _need_cb256(codebook)
+    _need_f32(group_affine=group_affine, sc_val=sc_val, bias=bias)
+    _need_i32(sc_row_ptr=sc_row_ptr, sc_col=sc_col)
+    with torch.cuda.device(x.device):
+        rc = lib().hxq_gemm_noalloc(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
+                                    _ptr(group_affine), int(group_size), _ptr(sc_row_ptr),
+                                    _ptr(sc_col), _ptr(sc_val), _ptr(bias), _ptr(out),
+                                    dtype_code(out.dtype), m, out_f, in_f, _stream(x))
+    _check("hxq_gemm_noalloc", rc)
     return out
 
 

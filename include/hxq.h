@@ -237,6 +237,27 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
                 int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * hxq_gemm_noalloc: hxq_gemm_ws without a workspace argument and without any
+ * allocation: the split-K partials live in a static device array of
+ * hxq_gemm_noalloc_max_bytes() bytes (64 MiB) that each GPU the library runs
+ * on holds until the process ends.  Same arguments and results as
+ * hxq_gemm_ws (same kernels, same K split).  Shapes whose partials need more
+ * than the array (hxq_gemm_workspace_bytes above the maximum) are rejected
+ * with HXQ_ERR_INVALID_ARG.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (several streams) race.  The stream must
+ * belong to the current device.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+int64_t hxq_gemm_noalloc_max_bytes(void);
+int hxq_gemm_noalloc(const void *x, int32_t x_dtype, const uint8_t *indices,
+                     const float *codebook, const float *group_affine, int32_t group_size,
+                     const int32_t *sc_row_ptr, const int32_t *sc_col, const float *sc_val,
+                     const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
+                     int64_t out_features, int64_t in_features, hipStream_t stream);
+
+/*
  * group_affine[g][o] = {group_scale[o][g], group_offset[o][g]} (fp32): the
  * GEMM layout of the per-group affine factors (n_groups = in/G).
  * No reference counterpart: the affine extension has no reference layout;
