@@ -1,0 +1,585 @@
+// HXQ prefill GEMM, register-dequant design: Y[M, OUT] = X[M, K] @ W^T with
+// W held as uint8 codebook indices (+ per-group affine, + sidecar) and never
+// written anywhere in dense form.
+//
+// Replaces fused_vq_matmul's N > 1 path (helix_substrate/triton_vq_matmul.py:
+// 249-334 _vq_gather_matmul_tiled_kernel, 634-661 dispatch, 693-698 sidecar
+// scatter_add, 724-725 bias) and the default materialise-then-BLAS
+// _forward_buffered (helix_linear.py:556-634).
+//
+// Block: 256 threads = 4 waves (one per SIMD), output tile BM x 256, K step
+// 64.  Wave w owns the 64 output columns [n0 + 64w, n0 + 64w + 64) for all
+// BM rows: (BM/32) x 2 accumulator tiles of v_mfma_f32_32x32x16_{bf16,f16}
+// (fp32, in AGPRs).  Per K step:
+//   * A (X rows, 16-bit) is staged through LDS once per block and read by
+//     all four waves (rows XOR-swizzled in 16-byte chunks: conflict-free);
+//   * B (the wave's 64 W rows x 64 k) is dequantised straight into the MFMA
+//     operand registers by the wave that uses it -- nothing of W goes to LDS
+//     and no wave waits on another for its weights.  The MFMA lane layout
+//     gives lane (c = lane % 32, h = lane / 32) the k range [8h, 8h+8) of a
+//     16-wide k substep; the kernel permutes k identically for A and B so
+//     that lane h of substep s covers physical k = 32h + 8s .. +8, i.e. a
+//     lane's B data for the whole step is the 32 contiguous index bytes
+//     [32h, 32h + 32) of its row (two 16-byte loads).  Lookups go to a
+//     codebook replicated 64x in LDS (lane l reads replica l: no bank
+//     conflicts; the byte address {0, 0, idx, 4l} is one v_perm_b32), then
+//     fma(c, scale, offset) and v_cvt_pk_bf16_f32;
+//   * B of step s+1 is built while the MFMAs of step s run (two operand
+//     buffers), global loads run two steps ahead, one barrier per step.
+// Sidecar: the entries of each group of 64 output rows are given sorted by
+// column (stable), so each wave walks one list with a wave-uniform cursor:
+// a window of 64 entries sits one per lane; the entries of a K step are the
+// window lanes whose column falls in the step (a ballot), and each is applied
+// by one indexed register write in its owning lane (v_readlane for the entry,
+// an SGPR-indexed move for the operand register) -- no per-lane cursors and
+// no divergent loops.  Later duplicates of a position come later in the list
+// and overwrite earlier ones (the reader's replace semantics).
+// Results are written once per element (split-K: fp32 partials reduced in
+// order by a second kernel): deterministic.
+#include <algorithm>
+
+#include "hxq_common.h"
+
+namespace hxq {
+namespace pg {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
+
+constexpr int kBN = 256;       // output columns per block
+constexpr int kBK = 64;        // K per step
+constexpr int kNrep = 64;      // codebook replicas (one per lane)
+constexpr int kXcds = 8;
+constexpr int kGroupRows = 8;  // tile-order group height (X row tiles)
+#ifndef HXQ_PREFILL_NJ
+#define HXQ_PREFILL_NJ 1
+#endif
+constexpr int kNJ = HXQ_PREFILL_NJ;  // 32-column subtiles per wave
+
+struct Args {
+    const uint16_t *x;       // [M, K] bf16 / fp16
+    const uint8_t *idx;      // [OUT, K]
+    const float *cb;         // [256]
+    const float2 *ga;        // [K/G, OUT] {scale, offset} or null
+    const int32_t *sc_ptr;   // [ceil(OUT/64) + 1] or null
+    const uint32_t *sc_key;  // (col << 6) | (row % 64), sorted within each 64-row group
+    const float *sc_val;
+    const float *bias;       // [OUT] or null
+    void *y;                 // [M, OUT]
+    float *part;             // split-K partials [ksplit, M, OUT] (ksplit > 1)
+    int32_t M, OUT, K, group, y_dtype, ksplit, ks_per;
+    int32_t tiles_x, tiles_y, tiles_per_xcd;
+    int32_t vec_out;         // 16-bit y, 16-byte aligned rows, no split: LDS-transposed stores
+};
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t to16(float v) { return pack2<BF16>(v, 0.f) & 0xffffu; }
+
+// Element offset of 16-byte chunk c (0..7) of LDS row r (64 elements, 128 B).
+// gfx950's LDS has 64 banks and serves 16 lanes of a 16-byte access per
+// clock: two consecutive rows fill the 64 banks, so the chunk is XORed with
+// (r / 2) % 8 -- any 16 consecutive rows then map one chunk index to 16
+// distinct (row parity, slot) pairs, conflict-free (XOR with r % 8 leaves
+// rows r and r + 8 on the same banks: measured 155 vs 220 B/clk per CU).
+__device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ ((r >> 1) & 7)) << 3); }
+
+// Tile order: blocks are dealt round-robin to the XCDs (block b runs on XCD
+// b % 8); XCD x takes the contiguous run [x * per, (x + 1) * per) of an order
+// that walks groups of kGroupRows row tiles column by column, so the blocks
+// one XCD runs together share X row tiles and W column tiles in its L2.
+__device__ __forceinline__ bool tile_of(const Args &g, int b, int &tx, int &ty) {
+    const int t = (b % kXcds) * g.tiles_per_xcd + b / kXcds;
+    if (t >= g.tiles_x * g.tiles_y) return false;
+    const int grp = t / (kGroupRows * g.tiles_x);
+    const int r0 = grp * kGroupRows;
+    const int gr = min(kGroupRows, g.tiles_y - r0);
+    const int w = t - grp * kGroupRows * g.tiles_x;
+    tx = w / gr;
+    ty = r0 + w % gr;
+    return true;
+}
+
+// NJ: 32-column subtiles per wave (2: four waves of 64 columns, one wave per
+// SIMD; 1: eight waves of 32 columns, two waves per SIMD).
+template <int NJ>
+struct BVec { typedef u32x32 type; };
+template <>
+struct BVec<1> { typedef u32x16 type; };
+
+template <int BM, bool BF16, bool AFFINE, int NJ>
+__global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const Args g) {
+    constexpr int kThreads = kBN / (32 * NJ) * 64;
+    constexpr int TM = BM / 32;           // accumulator tiles along M per wave
+    constexpr int XP = BM * 8 / kThreads; // 16-byte X chunks per thread per step
+    typedef typename BVec<NJ>::type BV;
+    constexpr int kTblBytes = 256 * kNrep * 4;
+    constexpr int kABytes = BM * kBK * 2;
+    // the table first, so it sits at LDS address 0 (lookups need no base add)
+    __shared__ __attribute__((aligned(16))) char smem[kTblBytes + 2 * kABytes];
+    float *tbl = reinterpret_cast<float *>(smem);
+    uint16_t *sA0 = reinterpret_cast<uint16_t *>(smem + kTblBytes);
+
+    int tx, ty;
+    if (!tile_of(g, blockIdx.x, tx, ty)) return;  // block-uniform
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ml = lane & 31, hh = lane >> 5;
+    const int K = g.K;
+    const int r0 = ty * BM;
+    const int n0 = tx * kBN;
+    const int nw = n0 + 32 * NJ * wave;      // first W row of this wave
+    const int kb = blockIdx.y * g.ks_per;    // first K step of this block's range
+    const int nk = min(K / kBK - kb, g.ks_per);
+    constexpr uint32_t kOob = 0x80000000u;
+
+    if (lds_offset_of(tbl) != 0) return;  // never taken: no other LDS in this kernel
+
+    // ---- global sources ----------------------------------------------------------
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.M * K * 2);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(g.idx, (int64_t)g.OUT * K);
+    const int ngroups = AFFINE ? K / g.group : 1;
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(g.ga, AFFINE ? (int64_t)ngroups * g.OUT * 8 : 0);
+    // X: thread t copies chunk t % 8 of rows t / 8 + (threads / 8) p
+    const int xc = tid & 7;
+    uint32_t x_off[XP];
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+        const int r = r0 + (tid >> 3) + (kThreads / 8) * p;
+        x_off[p] = r < g.M ? static_cast<uint32_t>((r * K + xc * 8) * 2) : kOob;
+    }
+    // W rows of this lane: nw + 32j + ml
+    uint32_t q_off[NJ];
+    uint32_t a_off[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int n = nw + 32 * j + ml;
+        q_off[j] = n < g.OUT ? static_cast<uint32_t>(n * K + 32 * hh) : kOob;
+        a_off[j] = n < g.OUT ? static_cast<uint32_t>(n * 8) : kOob;
+    }
+
+    u32x4 xv[2][XP];   // X of steps s (buffer s & 1)
+    u32x4 qv[2][2 * NJ];  // index bytes: [2j + half]
+    float2 av[2][NJ];     // {scale, offset} per j
+    auto load_step = [&](int s, int buf) {
+        const bool live = s < nk;
+        const uint32_t k0 = static_cast<uint32_t>((kb + (live ? s : 0)) * kBK);
+#pragma unroll
+        for (int p = 0; p < XP; ++p)
+            xv[buf][p] = buf_load16(xr, (x_off[p] == kOob || !live) ? kOob : x_off[p] + k0 * 2);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const uint32_t o = (q_off[j] == kOob || !live) ? kOob : q_off[j] + k0;
+            qv[buf][2 * j] = buf_load16(qr, o);
+            qv[buf][2 * j + 1] = buf_load16(qr, o == kOob ? kOob : o + 16u);
+        }
+        if constexpr (AFFINE) {
+            const uint32_t gofs = (k0 / static_cast<uint32_t>(g.group)) * static_cast<uint32_t>(g.OUT) * 8u;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + gofs;
+                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(ar, o, 0, 0);
+                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(ar, o == kOob ? kOob : o + 4u, 0, 0);
+                av[buf][j] = make_float2(__uint_as_float(lo), __uint_as_float(hi));
+            }
+        }
+    };
+    // rows r and r + (threads / 8) p share the swizzle ((r / 2) % 8): one base
+    // address, the other rows at immediate offsets
+    const int x_lds = swz(tid >> 3, xc);
+    auto store_x = [&](int buf) {
+        uint16_t *sA = sA0 + buf * (BM * kBK) + x_lds;
+#pragma unroll
+        for (int p = 0; p < XP; ++p)
+            *reinterpret_cast<u32x4 *>(sA + (kThreads / 8) * p * kBK) = xv[buf][p];
+    };
+
+    // ---- sidecar window: 64 entries of this wave's list, one per lane ---------
+    const bool has_sc = g.sc_ptr != nullptr && nw < g.OUT;
+    // this wave's rows within its 64-row sidecar group: [rlo, rlo + 32 NJ)
+    const uint32_t rlo = static_cast<uint32_t>(nw & 63);
+    int e_lo = 0, e_hi = 0;
+    if (has_sc) {
+        const int grp = nw >> 6;
+        e_lo = g.sc_ptr[grp];
+        e_hi = g.sc_ptr[grp + 1];
+        // split-K range: first entry at or past its first column (binary search)
+        const uint32_t kstart = static_cast<uint32_t>(kb * kBK) << 6;
+        int lo = e_lo, hi = kb > 0 ? e_hi : e_lo;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (g.sc_key[mid] < kstart) lo = mid + 1;
+            else hi = mid;
+        }
+        e_lo = lo;
+    }
+    int win = e_lo;  // list index of lane 0's entry
+    uint32_t wkey = 0xffffffffu;
+    float wval = 0.f;
+    auto load_window = [&]() {
+        const int e = win + lane;
+        wkey = e < e_hi ? g.sc_key[e] : 0xffffffffu;
+        wval = e < e_hi ? g.sc_val[e] : 0.f;
+    };
+    if (has_sc) load_window();
+
+    // ---- codebook table: 64 replicas, conflict-free float4 writes ---------------
+#pragma unroll
+    for (int q = 0; q < 4096 / kThreads; ++q) {
+        const int slot = tid + kThreads * q;  // float4 slot: entry slot / 16
+        const float c = g.cb[slot >> 4];
+        *reinterpret_cast<float4 *>(tbl + 4 * slot) = make_float4(c, c, c, c);
+    }
+
+    // ---- dequantise B into operand registers, one k substep at a time ----------
+    // b[16j + 4s + t] holds bf16 pairs (weights 8s + 2t, 8s + 2t + 1 of the
+    // lane's 32) of W row nw + 32j + ml: the B operand of substep s, subtile j
+    const uint32_t lane_off = static_cast<uint32_t>(lane) * 4u;
+    auto dequant_sub = [&](int buf, int s, BV &b) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const float sc = AFFINE ? av[buf][j].x : 1.f;
+            const float of = AFFINE ? av[buf][j].y : 0.f;
+#pragma unroll
+            for (int dd = 0; dd < 2; ++dd) {
+                const int d = 2 * s + dd;  // index dword (4 weights)
+                const uint32_t w = qv[buf][2 * j + (d >> 2)][d & 3];
+                float v0 = tbl_lookup0<kNrep, 0>(lane_off, w);
+                float v1 = tbl_lookup0<kNrep, 1>(lane_off, w);
+                float v2 = tbl_lookup0<kNrep, 2>(lane_off, w);
+                float v3 = tbl_lookup0<kNrep, 3>(lane_off, w);
+                if constexpr (AFFINE) {
+                    v0 = fmaf(v0, sc, of);
+                    v1 = fmaf(v1, sc, of);
+                    v2 = fmaf(v2, sc, of);
+                    v3 = fmaf(v3, sc, of);
+                }
+                b[16 * j + 2 * d] = pack2<BF16>(v0, v1);
+                b[16 * j + 2 * d + 1] = pack2<BF16>(v2, v3);
+            }
+        }
+    };
+    // Replace the sidecar entries of step s (columns [k1, k1 + 64)) in b.
+    auto patch = [&](int s, BV &b) {
+        if (!has_sc) return;
+        const uint32_t k1 = static_cast<uint32_t>((kb + s) * kBK);
+        const uint32_t klo = k1 << 6, khi = (k1 + kBK) << 6;
+        for (;;) {
+            unsigned long long m = __ballot(wkey >= klo && wkey < khi &&
+                                            (wkey & 63u) - rlo < static_cast<uint32_t>(32 * NJ));
+            while (m) {
+                const int src = __builtin_ctzll(m);
+                m &= m - 1;
+                const uint32_t key = __builtin_amdgcn_readlane(wkey, src);
+                const float val = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wval), src));
+                const uint32_t col = (key >> 6) - k1;  // 0..63
+                const uint32_t row = (key & 63u) - rlo; // row within this wave
+                const int owner = static_cast<int>((row & 31u) + 32u * (col >> 5));
+                const int reg = __builtin_amdgcn_readfirstlane(static_cast<int>(16u * (row >> 5) + ((col & 31u) >> 1)));
+                const uint32_t v16 = to16<BF16>(val);
+                const uint32_t hi = col & 1u;
+                const uint32_t old = b[reg];
+                const uint32_t upd = hi ? ((old & 0xffffu) | (v16 << 16)) : ((old & 0xffff0000u) | v16);
+                b[reg] = lane == owner ? upd : old;
+            }
+            // window used up (its last entry lies before the step's end): slide it
+            const uint32_t last = __builtin_amdgcn_readlane(wkey, 63);
+            if (win + 64 < e_hi && last < khi) {
+                win += 64;
+                load_window();
+            } else {
+                break;
+            }
+        }
+    };
+
+    // ---- accumulators -----------------------------------------------------------
+    f32x16 acc[TM][NJ];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // One step: the MFMAs of B(k) (in b, A from LDS buffer abuf), each k
+    // substep's operand registers refilled with B(k+1) from index buffer qbuf
+    // as soon as its MFMAs are issued.  The A rows 32i + ml of one substep
+    // share a swizzle: one base address per substep, rows at immediate offsets.
+    const int a_sw = (ml >> 1) & 7;
+    auto mfma_step = [&](int abuf, int qbuf, BV &b) {
+        const uint16_t *sA = sA0 + abuf * (BM * kBK) + ml * kBK;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            u32x4 bj[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                bj[j] = u32x4{b[16 * j + 4 * s], b[16 * j + 4 * s + 1], b[16 * j + 4 * s + 2],
+                              b[16 * j + 4 * s + 3]};
+            const uint16_t *as = sA + (((4 * hh + s) ^ a_sw) << 3);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(as + 32 * i * kBK);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    if constexpr (BF16)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, bj[j]), acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, bj[j]), acc[i][j], 0, 0, 0);
+                }
+            }
+            if (qbuf >= 0) dequant_sub(qbuf, s, b);
+        }
+    };
+
+    // ---- pipeline ---------------------------------------------------------------
+    // loads two steps ahead; X of step s+1 goes to LDS during step s; B of step
+    // s+1 replaces B of step s substep by substep; one barrier per step.
+    load_step(0, 0);
+    load_step(1, 1);
+    store_x(0);                 // waits for X(0)
+    __syncthreads();            // table and A(0) visible
+    BV b;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) dequant_sub(0, s, b);  // B(0)
+    patch(0, b);
+    load_step(2, 0);
+    int ks = 0;
+    for (; ks + 1 < nk; ks += 2) {
+        // step ks: A in LDS buffer 0, B(ks) in b; X(ks+1) and idx(ks+1) in buffer 1
+        store_x(1);
+        mfma_step(0, 1, b);     // b <- B(ks+1)
+        patch(ks + 1, b);
+        load_step(ks + 3, 1);
+        lds_barrier();
+        // step ks + 1: A in buffer 1; X(ks+2) and idx(ks+2) in buffer 0
+        store_x(0);
+        mfma_step(1, 0, b);     // b <- B(ks+2)
+        patch(ks + 2, b);
+        load_step(ks + 4, 0);
+        lds_barrier();
+    }
+    if (ks < nk) mfma_step(0, -1, b);  // odd step count: the last step (A in buffer 0)
+
+    // ---- epilogue: acc[i][j][r] = C[32i + 8(r/4) + 4h + r%4][nw + 32j + ml] ----
+    const bool split = g.ksplit > 1;
+    if (g.vec_out) {
+        // 16-bit outputs through LDS: each wave transposes its BM x 64 tile in a
+        // private region (the A buffers and the table are dead now), then
+        // stores rows in 16-byte pieces (eight lanes cover a 128-byte row run)
+        __syncthreads();
+        constexpr int CW = 32 * NJ;  // columns per wave
+        uint16_t *cw = reinterpret_cast<uint16_t *>(smem) + wave * (BM * CW);
+        // 16-byte chunk q of row mr: 128-byte rows (NJ = 2) take the A-tile
+        // swizzle; 64-byte rows (NJ = 1) are conflict-free as they are
+        auto cofs = [&](int mr, int q) { return NJ == 2 ? swz(mr, q) : mr * CW + 8 * q; };
+        const bool obf = g.y_dtype == HXQ_BF16;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int c = 32 * j + ml;
+            const float bv = (g.bias && nw + c < g.OUT) ? g.bias[nw + c] : 0.f;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int mr = 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    const float v = acc[i][j][r] + bv;
+                    cw[cofs(mr, c >> 3) + (c & 7)] =
+                        static_cast<uint16_t>(obf ? to16<true>(v) : to16<false>(v));
+                }
+        }
+        // same-wave LDS traffic is ordered: no barrier between the two passes
+        uint16_t *yb = static_cast<uint16_t *>(g.y);
+        constexpr int QPR = CW / 8;  // 16-byte chunks per row
+#pragma unroll 4
+        for (int t = 0; t < BM * QPR / 64; ++t) {
+            const int id = t * 64 + lane;
+            const int mr = id / QPR, q = id % QPR;
+            const int m = r0 + mr, n = nw + 8 * q;
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(cw + cofs(mr, q));
+            if (m < g.M && n < g.OUT)
+                *reinterpret_cast<u32x4 *>(yb + (int64_t)m * g.OUT + n) = v;
+        }
+        return;
+    }
+    float *dst = split ? g.part + (int64_t)blockIdx.y * g.M * g.OUT : nullptr;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int n = nw + 32 * j + ml;
+        if (n >= g.OUT) continue;
+        const float bv = (!split && g.bias) ? g.bias[n] : 0.f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = r0 + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+                if (m >= g.M) continue;
+                const int64_t o = (int64_t)m * g.OUT + n;
+                if (split) {
+                    dst[o] = acc[i][j][r];
+                } else {
+                    const float v = acc[i][j][r] + bv;
+                    if (g.y_dtype == HXQ_F32) static_cast<float *>(g.y)[o] = v;
+                    else if (g.y_dtype == HXQ_BF16) static_cast<uint16_t *>(g.y)[o] = static_cast<uint16_t>(to16<true>(v));
+                    else static_cast<uint16_t *>(g.y)[o] = static_cast<uint16_t>(to16<false>(v));
+                }
+            }
+    }
+}
+
+// Ordered split-K reduction: y = sum over ranges (in order) + bias.
+__global__ __launch_bounds__(256) void prefill_reduce_kernel(const float *__restrict__ part,
+                                                             int32_t ksplit, int64_t mn,
+                                                             int32_t out, const float *bias,
+                                                             void *y, int32_t y_dtype) {
+    const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+    if (i >= mn) return;
+    float v = part[i];
+    for (int s = 1; s < ksplit; ++s) v += part[s * mn + i];
+    if (bias) v += bias[i % out];
+    if (y_dtype == HXQ_F32) static_cast<float *>(y)[i] = v;
+    else if (y_dtype == HXQ_BF16) static_cast<uint16_t *>(y)[i] = f32_to_bf16(v);
+    else static_cast<uint16_t *>(y)[i] = f32_to_f16(v);
+}
+
+struct Plan {
+    int bm, tiles_x, tiles_y, ksplit, ks_per;
+};
+
+// K split of a tile grid: when the tiles cover fewer than all CUs, up to 8
+// ranges of >= 4 steps (fp32 partials + an ordered reduce).
+static int split_of(int64_t tiles, int nk, int cus) {
+    return tiles < cus ? static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({8, cus / tiles, nk / 4})))
+                       : 1;
+}
+
+// Row tile 256 (half the dequantisation per flop of 128) when its tiles,
+// times their K split, keep more than half the CUs busy; otherwise 128.
+// Measured on config-2 shapes: kv (2 column tiles) takes 128 at M <= 2048,
+// every other shape 256 down to M = 512.
+Plan plan(int64_t m, int64_t out, int64_t in, int cus) {
+    Plan p{};
+    p.tiles_x = static_cast<int>((out + kBN - 1) / kBN);
+    const int nk = static_cast<int>(in / kBK);
+    const int64_t t256 = p.tiles_x * ((m + 255) / 256);
+    p.bm = t256 * split_of(t256, nk, cus) * 2 > cus ? 256 : 128;
+    p.tiles_y = static_cast<int>((m + p.bm - 1) / p.bm);
+    const int ks = split_of((int64_t)p.tiles_x * p.tiles_y, nk, cus);
+    if (ks < 2) {
+        p.ksplit = 1;
+        p.ks_per = nk;
+    } else {
+        p.ks_per = (nk + ks - 1) / ks;
+        p.ksplit = (nk + p.ks_per - 1) / p.ks_per;
+    }
+    return p;
+}
+
+}  // namespace pg
+}  // namespace hxq
+
+using namespace hxq;
+
+extern "C" int64_t hxq_prefill_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
+                                                    int64_t in_features) {
+    if (m_rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % pg::kBK) return 0;
+    const pg::Plan p = pg::plan(m_rows, out_features, in_features, device_cu_count());
+    return p.ksplit > 1 ? int64_t{4} * p.ksplit * m_rows * out_features : 0;
+}
+
+extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
+                                const float *codebook, const float *group_affine,
+                                int32_t group_size, const int32_t *sc_grp_ptr,
+                                const uint32_t *sc_grp_key, const float *sc_grp_val,
+                                const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
+                                int64_t out_features, int64_t in_features, void *workspace,
+                                int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    HXQ_REQUIRE(x && indices && codebook && y, "x, indices, codebook and y are required");
+    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16,
+                "the MFMA GEMM takes bf16 or fp16 activations (fp32 goes through hxq_gemv)");
+    HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
+    HXQ_REQUIRE(m_rows > 0 && out_features > 0 && in_features > 0, "empty problem");
+    HXQ_REQUIRE(in_features % pg::kBK == 0, "in_features must be a multiple of 64");
+    HXQ_REQUIRE(in_features < (int64_t{1} << 26), "in_features must be below 2^26");
+    HXQ_REQUIRE(m_rows * in_features * 2 < (int64_t{1} << 31) &&
+                    out_features * in_features < (int64_t{1} << 31),
+                "problem too large for 32-bit offsets");
+    HXQ_REQUIRE(!group_affine || (group_size >= pg::kBK && group_size % pg::kBK == 0 &&
+                                  in_features % group_size == 0),
+                "group_size must be a multiple of 64 dividing in_features");
+    HXQ_REQUIRE(!group_affine || (in_features / group_size) * out_features * 8 < (int64_t{1} << 31),
+                "affine factors too large for 32-bit offsets");
+    HXQ_REQUIRE(!sc_grp_ptr || (sc_grp_key && sc_grp_val),
+                "the sidecar needs sc_grp_ptr, sc_grp_key and sc_grp_val");
+    HXQ_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(indices) & 15u) == 0,
+                "x and indices must be 16-byte aligned");
+    const pg::Plan p = pg::plan(m_rows, out_features, in_features, device_cu_count());
+    pg::Args a{};
+    a.x = static_cast<const uint16_t *>(x);
+    a.idx = indices;
+    a.cb = codebook;
+    a.ga = reinterpret_cast<const float2 *>(group_affine);
+    a.sc_ptr = sc_grp_ptr;
+    a.sc_key = sc_grp_key;
+    a.sc_val = sc_grp_val;
+    a.bias = bias;
+    a.y = y;
+    a.M = static_cast<int32_t>(m_rows);
+    a.OUT = static_cast<int32_t>(out_features);
+    a.K = static_cast<int32_t>(in_features);
+    a.group = group_affine ? group_size : pg::kBK;
+    a.y_dtype = y_dtype;
+    a.ksplit = p.ksplit;
+    a.ks_per = p.ks_per;
+    a.tiles_x = p.tiles_x;
+    a.tiles_y = p.tiles_y;
+    a.tiles_per_xcd = (p.tiles_x * p.tiles_y + pg::kXcds - 1) / pg::kXcds;
+    a.vec_out = p.ksplit == 1 && y_dtype != HXQ_F32 && out_features % 8 == 0 &&
+                (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    if (p.ksplit > 1) {
+        const int64_t need = int64_t{4} * p.ksplit * m_rows * out_features;
+        HXQ_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+                    "workspace too small (hxq_prefill_gemm_workspace_bytes)");
+        HXQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0,
+                    "workspace must be 16-byte aligned");
+        a.part = static_cast<float *>(workspace);
+    }
+    const dim3 grid(a.tiles_per_xcd * pg::kXcds, p.ksplit);
+    const bool bf16 = x_dtype == HXQ_BF16;
+    const bool aff = group_affine != nullptr;
+#define HXQ_PG_LAUNCH(BM_, BF_, AF_) \
+    hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ>), grid, \
+                       dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a)
+    if (p.bm == 256) {
+        if (bf16) { if (aff) HXQ_PG_LAUNCH(256, true, true); else HXQ_PG_LAUNCH(256, true, false); }
+        else { if (aff) HXQ_PG_LAUNCH(256, false, true); else HXQ_PG_LAUNCH(256, false, false); }
+    } else {
+        if (bf16) { if (aff) HXQ_PG_LAUNCH(128, true, true); else HXQ_PG_LAUNCH(128, true, false); }
+        else { if (aff) HXQ_PG_LAUNCH(128, false, true); else HXQ_PG_LAUNCH(128, false, false); }
+    }
+#undef HXQ_PG_LAUNCH
+    HXQ_LAUNCH_CHECK();
+    if (p.ksplit > 1) {
+        const int64_t mn = m_rows * out_features;
+        hipLaunchKernelGGL(pg::prefill_reduce_kernel, dim3(static_cast<uint32_t>((mn + 255) / 256)),
+                           dim3(256), 0, stream, a.part, a.ksplit, mn, a.OUT, bias, y, y_dtype);
+        HXQ_LAUNCH_CHECK();
+    }
+    return HXQ_OK;
+}

@@ -80,6 +80,7 @@ SIGNATURES = {
     "hxq_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemm_ws": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64, P],
     "hxq_gemm_noalloc": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
+    "hxq_prefill_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64, P],
     "hxq_affine_pack": [P, P, I64, I64, P, P],
     "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
                            I64, I64, I64, P, I64, P],
@@ -128,6 +129,7 @@ SIGNATURES_I64 = {
     "hxq_vq2_workspace_bytes": [I64, I32],
     "hxq_gemm_workspace_bytes": [I64, I64, I64],
     "hxq_gemm_noalloc_max_bytes": [],
+    "hxq_prefill_gemm_workspace_bytes": [I64, I64, I64],
 }
 
 
@@ -411,6 +413,34 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
                            _ptr(sc_val), _ptr(bias), _ptr(out), dtype_code(out.dtype), m, out_f,
                            in_f, _ptr(ws), nbytes, _stream(x))
     _check("hxq_gemm_ws", rc)
+    return out
+
+
+def prefill_gemm(x, indices, codebook, group_affine, group_size, sc_grp_ptr, sc_grp_key,
+                 sc_grp_val, bias=None, out_dtype=None, out=None):
+    """Y = X @ W^T (+bias) on MFMA with W dequantised into the operand registers
+    (hxq_prefill_gemm).  X bf16/fp16 [M, K]; group_affine [K/G, OUT, 2] or None;
+    sidecar in the row-group order of ``hxq_format.sidecar_row_groups``."""
+    m, in_f = x.shape
+    out_f = indices.shape[0]
+    if indices.shape[1] != in_f:
+        raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
+    if out is None:
+        out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
+    _need_device(x, indices, codebook, group_affine, sc_grp_ptr, sc_grp_key, sc_grp_val, bias, out)
+    _need_cb256(codebook)
+    _need_f32(group_affine=group_affine, sc_grp_val=sc_grp_val, bias=bias)
+    _need_i32(sc_grp_ptr=sc_grp_ptr, sc_grp_key=sc_grp_key)
+    L = lib()
+    with torch.cuda.device(x.device):
+        nbytes = L.hxq_prefill_gemm_workspace_bytes(m, out_f, in_f)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+        rc = L.hxq_prefill_gemm(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
+                                _ptr(group_affine), int(group_size), _ptr(sc_grp_ptr),
+                                _ptr(sc_grp_key), _ptr(sc_grp_val), _ptr(bias), _ptr(out),
+                                dtype_code(out.dtype), m, out_f, in_f, _ptr(ws), nbytes,
+                                _stream(x))
+    _check("hxq_prefill_gemm", rc)
     return out
 
 

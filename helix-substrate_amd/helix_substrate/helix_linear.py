@@ -43,7 +43,8 @@ import torch
 import torch.nn as nn
 
 from . import _hxq
-from .hxq_format import build_sidecar_csr, check_kernel_shapes, compressed_bytes
+from .hxq_format import (build_sidecar_csr, check_kernel_shapes, compressed_bytes,
+                         sidecar_row_groups)
 
 _CPU_TILE_ROWS = 256
 _GEMV_MAX_ROWS = 4
@@ -223,6 +224,12 @@ class HelixLinear(nn.Module):
             "_affine_t",
             torch.stack([self.group_scale.t(), self.group_offset.t()], dim=-1).contiguous()
             if has_affine else None, persistent=False)
+        # the prefill GEMM's sidecar order (per 64 output rows, by column; derived)
+        grp = (sidecar_row_groups(self._sidecar_rows, self._sidecar_cols, self._sc_val,
+                                  self.out_features, self.in_features)
+               if self._gemm_ok and self._sc_row_ptr is not None else (None, None, None))
+        for name, t in zip(("_sc_grp_ptr", "_sc_grp_key", "_sc_grp_val"), grp):
+            self.register_buffer(name, t, persistent=False)
         self.has_svd = self.svd_U is not None
         self.rank = int(self.svd_U.shape[1]) if self.has_svd else 0
         self.has_channel_scales = self.channel_scales is not None
@@ -272,6 +279,8 @@ class HelixLinear(nn.Module):
                 self.register_buffer(name, None)
         self._gemm_ok = False
         self.register_buffer("_affine_t", None, persistent=False)
+        for name in ("_sc_grp_ptr", "_sc_grp_key", "_sc_grp_val"):
+            self.register_buffer(name, None, persistent=False)
         self.has_svd = self.svd_U is not None
         self.rank = int(self.svd_U.shape[1]) if self.has_svd else 0
         self.has_channel_scales = self.channel_scales is not None
@@ -342,7 +351,7 @@ class HelixLinear(nn.Module):
     # Floating-point HXQ state the kernels read as fp32, whatever the module's dtype.
     _FP32_STATE = ("codebook", "sidecar_values", "svd_U", "svd_s", "svd_Vt", "bias",
                    "channel_scales", "group_scale", "group_offset", "_sc_val", "_sc_delta",
-                   "_sidecar_deltas", "_sidecar_vq_vals", "_affine_t")
+                   "_sidecar_deltas", "_sidecar_vq_vals", "_affine_t", "_sc_grp_val")
 
     def _apply(self, fn, recurse=True):
         """``.to()/.cuda()/.half()/.bfloat16()``: move the HXQ state with the module but
@@ -412,8 +421,11 @@ class HelixLinear(nn.Module):
                           out=out[r0:r1])
         elif x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
             self._last_dispatch_path = "hip_gemm"
-            _hxq.gemm(x2, self.indices, self._kcb, self._affine_t, self.group_size, rp, col,
-                      None if rp is None else self._sc_val, self.bias, out=out)
+            grp = rp is not None
+            _hxq.prefill_gemm(x2, self.indices, self._kcb, self._affine_t, self.group_size,
+                              self._sc_grp_ptr if grp else None,
+                              self._sc_grp_key if grp else None,
+                              self._sc_grp_val if grp else None, self.bias, out=out)
         else:
             # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
             self._last_dispatch_path = "hip_gemv_rows"

@@ -86,6 +86,31 @@ def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: to
                       vq=vq.contiguous())
 
 
+def sidecar_row_groups(rows: torch.Tensor, cols: torch.Tensor, val: torch.Tensor, out_f: int,
+                       in_f: int):
+    """The prefill GEMM's sidecar order: for each group of 64 output rows, its
+    entries sorted by column, then row (stable, so a repeated position keeps
+    its stored order and the last copy is applied last).
+
+    rows / cols / val: the CSR arrays (rows ascending, stored order within a
+    row).  Returns (grp_ptr int32 [ceil(out/64) + 1], key int32 [nnz] holding
+    the uint32 (col << 6) | (row % 64), val fp32 [nnz]).
+    """
+    if in_f >= 1 << 25:
+        raise ValueError("in_features must be below 2^25 for the prefill sidecar keys")
+    rows = rows.to(torch.int64)
+    cols = cols.to(torch.int64)
+    grp = torch.div(rows, 64, rounding_mode="floor")
+    key = (cols << 6) | (rows & 63)
+    order = torch.sort(grp * (1 << 32) + key, stable=True).indices
+    n_grp = (out_f + 63) // 64
+    counts = torch.bincount(grp, minlength=n_grp)
+    ptr = torch.zeros(n_grp + 1, dtype=torch.int64, device=rows.device)
+    ptr[1:] = torch.cumsum(counts, 0)
+    return (ptr.to(torch.int32).contiguous(), key[order].to(torch.int32).contiguous(),
+            val[order].to(torch.float32).contiguous())
+
+
 def check_kernel_shapes(in_features: int, group_size: int, has_affine: bool) -> None:
     """Shape rules of the HIP kernels (16-byte index vectors, groups of 16k)."""
     if in_features % 16 != 0:

@@ -237,6 +237,30 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
                 int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * hxq_prefill_gemm: the prefill GEMM Y = X W^T (+ bias) with W dequantised
+ * straight into the MFMA operand registers (bf16/fp16 X [m_rows, in],
+ * fp32 accumulation, y in y_dtype; in_features % 64 == 0; affine as for
+ * hxq_gemm).  The sidecar comes in the kernel's order: for each group of 64
+ * output rows g (rows [64g, 64g + 64)), its entries sorted by column then row
+ * (stable): sc_grp_ptr int32 [ceil(out/64) + 1], sc_grp_key uint32
+ * (col << 6) | (row - 64g), sc_grp_val fp32 replacement values (NULL
+ * sc_grp_ptr = no sidecar).  Shapes with few output tiles split K: a
+ * workspace of hxq_prefill_gemm_workspace_bytes(...) bytes holds fp32
+ * partials, reduced in order (deterministic).
+ * Replaces: fused_vq_matmul's N > 1 path (triton_vq_matmul.py:249-334,
+ * 634-661, 693-698, 724-725) and HelixLinear._forward_buffered
+ * (helix_linear.py:556-634).
+ */
+int64_t hxq_prefill_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
+                                         int64_t in_features);
+int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
+                     const float *codebook, const float *group_affine, int32_t group_size,
+                     const int32_t *sc_grp_ptr, const uint32_t *sc_grp_key,
+                     const float *sc_grp_val, const float *bias, void *y, int32_t y_dtype,
+                     int64_t m_rows, int64_t out_features, int64_t in_features,
+                     void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * hxq_gemm_noalloc: hxq_gemm_ws without a workspace argument and without any
  * allocation: the split-K partials live in a static device array of
  * hxq_gemm_noalloc_max_bytes() bytes (64 MiB) that each GPU the library runs

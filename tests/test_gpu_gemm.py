@@ -42,7 +42,12 @@ def _maxrel(y, y_ref):
 
 def _check(y, x16, W, bias=None):
     """BASELINE bar for any output dtype; the tight bar for fp32 outputs (a
-    16-bit output adds its own rounding of ~2^-9)."""
+    16-bit output adds its own rounding of ~2^-9).  y may hold several
+    kernels' outputs side by side ([M, k * OUT], as _gemm32 returns)."""
+    if y.shape[1] != W.shape[0]:
+        for part in torch.split(y, W.shape[0], dim=1):
+            _check(part, x16, W, bias)
+        return
     xf = x16.float().numpy()
     b = None if bias is None else bias.numpy()
     is32 = y.dtype == torch.float32
@@ -56,9 +61,15 @@ def _check(y, x16, W, bias=None):
 
 
 def _gemm32(mod, x):
-    return _hxq.gemm(x, mod.indices, mod.codebook, mod._affine_t, mod.group_size,
-                     mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias,
-                     out_dtype=torch.float32)
+    """fp32 outputs of both dense GEMM kernels (the role-split hxq_gemm and the
+    register-dequant hxq_prefill_gemm); the tight bar applies to each."""
+    a = _hxq.gemm(x, mod.indices, mod.codebook, mod._affine_t, mod.group_size,
+                  mod._sc_row_ptr, mod._sc_col, mod._sc_val, mod.bias,
+                  out_dtype=torch.float32)
+    b = _hxq.prefill_gemm(x, mod.indices, mod.codebook, mod._affine_t, mod.group_size,
+                          mod._sc_grp_ptr, mod._sc_grp_key, mod._sc_grp_val, mod.bias,
+                          out_dtype=torch.float32)
+    return torch.cat([a, b], dim=1)
 
 
 @pytest.mark.parametrize("m,out_f,in_f", [
@@ -160,7 +171,16 @@ def test_gemm_split_k_matches_unsplit_and_oracle(dev, m, out_f, in_f, density):
     yb = _hxq.gemm(*args)
     assert yb.dtype == torch.bfloat16
     _check(yb, x, W, bias)
-    assert torch.equal(mod(x.to(dev)), yb)                              # module path
+    # the register-dequant kernel (the module path) with its own K split
+    pargs = (x.to(dev), mod.indices, mod.codebook, mod._affine_t, mod.group_size,
+             mod._sc_grp_ptr, mod._sc_grp_key, mod._sc_grp_val, mod.bias)
+    ps = _hxq.prefill_gemm(*pargs, out_dtype=torch.float32)
+    _check(ps, x, W, bias)
+    assert _maxrel(ps.cpu().numpy(), yu.cpu().numpy().astype(np.float64)) <= 1e-5
+    assert torch.equal(_hxq.prefill_gemm(*pargs, out_dtype=torch.float32), ps)
+    pb = mod(x.to(dev))
+    assert mod._last_dispatch_path == "hip_gemm"
+    assert torch.equal(pb, _hxq.prefill_gemm(*pargs))                   # module path
 
 
 def _row_slice(m):

@@ -253,3 +253,18 @@ def test_forward_wave_threaded_tiles_match_oracle(monkeypatch):
     m2 = _module(L, bias=b)
     torch.testing.assert_close(m2(x), y, rtol=1e-6, atol=1e-6)
     assert m2._last_dispatch_path == "naive"
+
+
+def test_sidecar_row_groups_order():
+    """Prefill sidecar order: per 64-row group, by column then row; repeated
+    positions keep their stored order (the last copy is applied last)."""
+    from helix_substrate.hxq_format import sidecar_row_groups
+    rows = torch.tensor([0, 0, 5, 5, 63, 64, 64, 130, 130])
+    cols = torch.tensor([9, 3, 3, 3, 1, 7, 2, 0, 0])
+    val = torch.arange(9, dtype=torch.float32)
+    ptr, key, v = sidecar_row_groups(rows, cols, val, out_f=140, in_f=16)
+    assert ptr.tolist() == [0, 5, 7, 9]
+    k = key.long()
+    assert ((k >> 6).tolist(), (k & 63).tolist()) == ([1, 3, 3, 3, 9, 2, 7, 0, 0],
+                                                     [63, 0, 5, 5, 0, 0, 0, 2, 2])
+    assert v.tolist() == [4.0, 1.0, 2.0, 3.0, 0.0, 6.0, 5.0, 7.0, 8.0]
