@@ -72,9 +72,11 @@ struct Args {
     const float *sc_val;
     const float *bias;       // [OUT] or null
     void *y;                 // [M, OUT]
-    float *part;             // split-K partials [ksplit, M, OUT] (ksplit > 1)
+    float *part;             // split-K partials [ksplit, ntiles, BM, 256] (ksplit > 1)
     int32_t M, OUT, K, group, y_dtype, ksplit, ks_per;
-    int32_t tiles_x, tiles_y, tiles_per_xcd;
+    int32_t tiles_x, tiles_y;   // the whole tile grid
+    int32_t t0, ntiles;         // this launch: tiles [t0, t0 + ntiles) of the order
+    int32_t tiles_per_xcd;      // of this launch
     int32_t vec_out;         // 16-bit y, 16-byte aligned rows, no split: LDS-transposed stores
 };
 
@@ -99,15 +101,21 @@ __device__ __forceinline__ int swz(int r, int c) { return r * kBK + ((c ^ ((r >>
 // b % 8); XCD x takes the contiguous run [x * per, (x + 1) * per) of an order
 // that walks groups of kGroupRows row tiles column by column, so the blocks
 // one XCD runs together share X row tiles and W column tiles in its L2.
-__device__ __forceinline__ bool tile_of(const Args &g, int b, int &tx, int &ty) {
-    const int t = (b % kXcds) * g.tiles_per_xcd + b / kXcds;
-    if (t >= g.tiles_x * g.tiles_y) return false;
-    const int grp = t / (kGroupRows * g.tiles_x);
+__device__ __forceinline__ void order_tile(int t, int tiles_x, int tiles_y, int &tx, int &ty) {
+    const int grp = t / (kGroupRows * tiles_x);
     const int r0 = grp * kGroupRows;
-    const int gr = min(kGroupRows, g.tiles_y - r0);
-    const int w = t - grp * kGroupRows * g.tiles_x;
+    const int gr = min(kGroupRows, tiles_y - r0);
+    const int w = t - grp * kGroupRows * tiles_x;
     tx = w / gr;
     ty = r0 + w % gr;
+}
+
+// Block b of a launch over tiles [t0, t0 + ntiles): tile index tl within the
+// launch and its grid position (false for the padding blocks).
+__device__ __forceinline__ bool tile_of(const Args &g, int b, int &tl, int &tx, int &ty) {
+    tl = (b % kXcds) * g.tiles_per_xcd + b / kXcds;
+    if (tl >= g.ntiles) return false;
+    order_tile(g.t0 + tl, g.tiles_x, g.tiles_y, tx, ty);
     return true;
 }
 
@@ -131,8 +139,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     float *tbl = reinterpret_cast<float *>(smem);
     uint16_t *sA0 = reinterpret_cast<uint16_t *>(smem + kTblBytes);
 
-    int tx, ty;
-    if (!tile_of(g, blockIdx.x, tx, ty)) return;  // block-uniform
+    int tl, tx, ty;
+    if (!tile_of(g, blockIdx.x, tl, tx, ty)) return;  // block-uniform
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -416,12 +424,26 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
         }
         return;
     }
-    float *dst = split ? g.part + (int64_t)blockIdx.y * g.M * g.OUT : nullptr;
+    if (split) {
+        // this range's partial tile, compact [BM][256]; the reduce adds the
+        // ranges in order and maps the tile back to Y
+        float *dst = g.part + ((int64_t)blockIdx.y * g.ntiles + tl) * (BM * kBN);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int c = nw - n0 + 32 * j + ml;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    dst[(32 * i + 8 * (r >> 2) + 4 * hh + (r & 3)) * kBN + c] = acc[i][j][r];
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int n = nw + 32 * j + ml;
         if (n >= g.OUT) continue;
-        const float bv = (!split && g.bias) ? g.bias[n] : 0.f;
+        const float bv = g.bias ? g.bias[n] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -429,35 +451,51 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
                 const int m = r0 + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
                 if (m >= g.M) continue;
                 const int64_t o = (int64_t)m * g.OUT + n;
-                if (split) {
-                    dst[o] = acc[i][j][r];
-                } else {
-                    const float v = acc[i][j][r] + bv;
-                    if (g.y_dtype == HXQ_F32) static_cast<float *>(g.y)[o] = v;
-                    else if (g.y_dtype == HXQ_BF16) static_cast<uint16_t *>(g.y)[o] = static_cast<uint16_t>(to16<true>(v));
-                    else static_cast<uint16_t *>(g.y)[o] = static_cast<uint16_t>(to16<false>(v));
-                }
+                const float v = acc[i][j][r] + bv;
+                if (g.y_dtype == HXQ_F32) static_cast<float *>(g.y)[o] = v;
+                else if (g.y_dtype == HXQ_BF16) static_cast<uint16_t *>(g.y)[o] = static_cast<uint16_t>(to16<true>(v));
+                else static_cast<uint16_t *>(g.y)[o] = static_cast<uint16_t>(to16<false>(v));
             }
     }
 }
 
-// Ordered split-K reduction: y = sum over ranges (in order) + bias.
+// Ordered split-K reduction of a launch's compact partial tiles:
+// y[m, n] = sum over ranges (in order) + bias, for the tiles' in-range elements.
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float *__restrict__ part,
-                                                             int32_t ksplit, int64_t mn,
-                                                             int32_t out, const float *bias,
-                                                             void *y, int32_t y_dtype) {
+                                                             int32_t ksplit, int32_t ntiles,
+                                                             int32_t t0, int32_t tiles_x,
+                                                             int32_t tiles_y, int32_t bm,
+                                                             int32_t M, int32_t out,
+                                                             const float *bias, void *y,
+                                                             int32_t y_dtype) {
+    const int64_t per = (int64_t)bm * kBN;
     const int64_t i = blockIdx.x * 256ll + threadIdx.x;
-    if (i >= mn) return;
+    if (i >= per * ntiles) return;
+    const int tl = static_cast<int>(i / per);
+    const int e = static_cast<int>(i - (int64_t)tl * per);
+    int tx, ty;
+    order_tile(t0 + tl, tiles_x, tiles_y, tx, ty);
+    const int m = ty * bm + e / kBN, n = tx * kBN + e % kBN;
+    if (m >= M || n >= out) return;
+    const int64_t stride = per * ntiles;
     float v = part[i];
-    for (int s = 1; s < ksplit; ++s) v += part[s * mn + i];
-    if (bias) v += bias[i % out];
-    if (y_dtype == HXQ_F32) static_cast<float *>(y)[i] = v;
-    else if (y_dtype == HXQ_BF16) static_cast<uint16_t *>(y)[i] = f32_to_bf16(v);
-    else static_cast<uint16_t *>(y)[i] = f32_to_f16(v);
+    for (int s = 1; s < ksplit; ++s) v += part[s * stride + i];
+    if (bias) v += bias[n];
+    const int64_t o = (int64_t)m * out + n;
+    if (y_dtype == HXQ_F32) static_cast<float *>(y)[o] = v;
+    else if (y_dtype == HXQ_BF16) static_cast<uint16_t *>(y)[o] = f32_to_bf16(v);
+    else static_cast<uint16_t *>(y)[o] = f32_to_f16(v);
 }
 
+// One launch of the plan: tiles [t0, t0 + n) of the order, K split ks ways.
+struct Launch {
+    int t0, n, ks, ks_per;
+};
+
 struct Plan {
-    int bm, tiles_x, tiles_y, ksplit, ks_per;
+    int bm, tiles_x, tiles_y, nl;
+    Launch l[2];
+    int64_t ws_bytes;  // largest partial buffer of a split launch
 };
 
 // K split of a tile grid: when the tiles cover fewer than all CUs, up to 8
@@ -467,10 +505,21 @@ static int split_of(int64_t tiles, int nk, int cus) {
                        : 1;
 }
 
+static Launch launch_of(int t0, int n, int ks, int nk) {
+    Launch l{t0, n, 1, nk};
+    if (ks >= 2) {
+        l.ks_per = (nk + ks - 1) / ks;
+        l.ks = (nk + l.ks_per - 1) / l.ks_per;
+    }
+    return l;
+}
+
 // Row tile 256 (half the dequantisation per flop of 128) when its tiles,
 // times their K split, keep more than half the CUs busy; otherwise 128.
 // Measured on config-2 shapes: kv (2 column tiles) takes 128 at M <= 2048,
-// every other shape 256 down to M = 512.
+// every other shape 256 down to M = 512.  One block runs per CU, so a grid
+// of several rounds whose last round would fill under half the CUs runs
+// that tail as a second launch with K split across the idle CUs.
 Plan plan(int64_t m, int64_t out, int64_t in, int cus) {
     Plan p{};
     p.tiles_x = static_cast<int>((out + kBN - 1) / kBN);
@@ -478,14 +527,23 @@ Plan plan(int64_t m, int64_t out, int64_t in, int cus) {
     const int64_t t256 = p.tiles_x * ((m + 255) / 256);
     p.bm = t256 * split_of(t256, nk, cus) * 2 > cus ? 256 : 128;
     p.tiles_y = static_cast<int>((m + p.bm - 1) / p.bm);
-    const int ks = split_of((int64_t)p.tiles_x * p.tiles_y, nk, cus);
-    if (ks < 2) {
-        p.ksplit = 1;
-        p.ks_per = nk;
+    const int tiles = p.tiles_x * p.tiles_y;
+    const int rem = tiles % cus;
+    if (tiles < cus) {
+        p.nl = 1;
+        p.l[0] = launch_of(0, tiles, split_of(tiles, nk, cus), nk);
+    } else if (rem > 0 && 2 * rem < cus && nk >= 8) {
+        p.nl = 2;
+        p.l[0] = launch_of(0, tiles - rem, 1, nk);
+        p.l[1] = launch_of(tiles - rem, rem, split_of(rem, nk, cus), nk);
     } else {
-        p.ks_per = (nk + ks - 1) / ks;
-        p.ksplit = (nk + p.ks_per - 1) / p.ks_per;
+        p.nl = 1;
+        p.l[0] = launch_of(0, tiles, 1, nk);
     }
+    p.ws_bytes = 0;
+    for (int i = 0; i < p.nl; ++i)
+        if (p.l[i].ks > 1)
+            p.ws_bytes = std::max<int64_t>(p.ws_bytes, int64_t{4} * p.l[i].ks * p.l[i].n * p.bm * kBN);
     return p;
 }
 
@@ -497,8 +555,7 @@ using namespace hxq;
 extern "C" int64_t hxq_prefill_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
                                                     int64_t in_features) {
     if (m_rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % pg::kBK) return 0;
-    const pg::Plan p = pg::plan(m_rows, out_features, in_features, device_cu_count());
-    return p.ksplit > 1 ? int64_t{4} * p.ksplit * m_rows * out_features : 0;
+    return pg::plan(m_rows, out_features, in_features, device_cu_count()).ws_bytes;
 }
 
 extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
@@ -545,41 +602,47 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *i
     a.K = static_cast<int32_t>(in_features);
     a.group = group_affine ? group_size : pg::kBK;
     a.y_dtype = y_dtype;
-    a.ksplit = p.ksplit;
-    a.ks_per = p.ks_per;
     a.tiles_x = p.tiles_x;
     a.tiles_y = p.tiles_y;
-    a.tiles_per_xcd = (p.tiles_x * p.tiles_y + pg::kXcds - 1) / pg::kXcds;
-    a.vec_out = p.ksplit == 1 && y_dtype != HXQ_F32 && out_features % 8 == 0 &&
-                (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
-    if (p.ksplit > 1) {
-        const int64_t need = int64_t{4} * p.ksplit * m_rows * out_features;
-        HXQ_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+    if (p.ws_bytes > 0) {
+        HXQ_REQUIRE(workspace != nullptr && workspace_bytes >= p.ws_bytes,
                     "workspace too small (hxq_prefill_gemm_workspace_bytes)");
         HXQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0,
                     "workspace must be 16-byte aligned");
         a.part = static_cast<float *>(workspace);
     }
-    const dim3 grid(a.tiles_per_xcd * pg::kXcds, p.ksplit);
     const bool bf16 = x_dtype == HXQ_BF16;
     const bool aff = group_affine != nullptr;
+    const bool vec = y_dtype != HXQ_F32 && out_features % 8 == 0 &&
+                     (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    for (int li = 0; li < p.nl; ++li) {
+        const pg::Launch &L = p.l[li];
+        a.t0 = L.t0;
+        a.ntiles = L.n;
+        a.ksplit = L.ks;
+        a.ks_per = L.ks_per;
+        a.tiles_per_xcd = (L.n + pg::kXcds - 1) / pg::kXcds;
+        a.vec_out = L.ks == 1 && vec;
+        const dim3 grid(a.tiles_per_xcd * pg::kXcds, L.ks);
 #define HXQ_PG_LAUNCH(BM_, BF_, AF_) \
-    hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ>), grid, \
-                       dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a)
-    if (p.bm == 256) {
-        if (bf16) { if (aff) HXQ_PG_LAUNCH(256, true, true); else HXQ_PG_LAUNCH(256, true, false); }
-        else { if (aff) HXQ_PG_LAUNCH(256, false, true); else HXQ_PG_LAUNCH(256, false, false); }
-    } else {
-        if (bf16) { if (aff) HXQ_PG_LAUNCH(128, true, true); else HXQ_PG_LAUNCH(128, true, false); }
-        else { if (aff) HXQ_PG_LAUNCH(128, false, true); else HXQ_PG_LAUNCH(128, false, false); }
-    }
+        hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ>), grid, \
+                           dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a)
+        if (p.bm == 256) {
+            if (bf16) { if (aff) HXQ_PG_LAUNCH(256, true, true); else HXQ_PG_LAUNCH(256, true, false); }
+            else { if (aff) HXQ_PG_LAUNCH(256, false, true); else HXQ_PG_LAUNCH(256, false, false); }
+        } else {
+            if (bf16) { if (aff) HXQ_PG_LAUNCH(128, true, true); else HXQ_PG_LAUNCH(128, true, false); }
+            else { if (aff) HXQ_PG_LAUNCH(128, false, true); else HXQ_PG_LAUNCH(128, false, false); }
+        }
 #undef HXQ_PG_LAUNCH
-    HXQ_LAUNCH_CHECK();
-    if (p.ksplit > 1) {
-        const int64_t mn = m_rows * out_features;
-        hipLaunchKernelGGL(pg::prefill_reduce_kernel, dim3(static_cast<uint32_t>((mn + 255) / 256)),
-                           dim3(256), 0, stream, a.part, a.ksplit, mn, a.OUT, bias, y, y_dtype);
         HXQ_LAUNCH_CHECK();
+        if (L.ks > 1) {
+            const int64_t n = int64_t{1} * L.n * p.bm * pg::kBN;
+            hipLaunchKernelGGL(pg::prefill_reduce_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)),
+                               dim3(256), 0, stream, a.part, L.ks, L.n, L.t0, p.tiles_x, p.tiles_y,
+                               p.bm, a.M, a.OUT, bias, y, y_dtype);
+            HXQ_LAUNCH_CHECK();
+        }
     }
     return HXQ_OK;
 }
