@@ -64,8 +64,8 @@ constexpr int kNJ = HXQ_PREFILL_NJ;  // 32-column subtiles per wave
 
 struct Args {
     const uint16_t *x;       // [M, K] bf16 / fp16
-    const uint8_t *idx;      // [OUT, K]
-    const float *cb;         // [256]
+    const uint8_t *idx;      // index data, rows of K * (bits per weight) / 8 bytes
+    const float *cb;         // [256] (uint8), [n_codes] (uint16), [n_codes, 2] (pairs)
     const float2 *ga;        // [K/G, OUT] {scale, offset} or null
     const int32_t *sc_ptr;   // [ceil(OUT/64) + 1] or null
     const uint32_t *sc_key;  // (col << 6) | (row % 64), sorted within each 64-row group
@@ -73,7 +73,7 @@ struct Args {
     const float *bias;       // [OUT] or null
     void *y;                 // [M, OUT]
     float *part;             // split-K partials [ksplit, ntiles, BM, 256] (ksplit > 1)
-    int32_t M, OUT, K, group, y_dtype, ksplit, ks_per;
+    int32_t M, OUT, K, group, y_dtype, ksplit, ks_per, n_codes;
     int32_t tiles_x, tiles_y;   // the whole tile grid
     int32_t t0, ntiles;         // this launch: tiles [t0, t0 + ntiles) of the order
     int32_t tiles_per_xcd;      // of this launch
@@ -126,12 +126,23 @@ struct BVec { typedef u32x32 type; };
 template <>
 struct BVec<1> { typedef u32x16 type; };
 
-template <int BM, bool BF16, bool AFFINE, int NJ>
+// Index formats (HXQ_FMT_*): index bytes per 32 weights (one lane's share of
+// a row per K step) and whether the lookup table is a pair codebook.
+__host__ __device__ constexpr int fmt_b32(int f) {
+    return f == HXQ_FMT_SCALAR_U16 ? 64 : (f == HXQ_FMT_VQ2_P12 || f == HXQ_FMT_AF6) ? 24 : 32;
+}
+
+template <int BM, bool BF16, bool AFFINE, int NJ, int FMT>
 __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const Args g) {
     constexpr int kThreads = kBN / (32 * NJ) * 64;
     constexpr int TM = BM / 32;           // accumulator tiles along M per wave
     constexpr int XP = BM * 8 / kThreads; // 16-byte X chunks per thread per step
     typedef typename BVec<NJ>::type BV;
+    constexpr int B32 = fmt_b32(FMT);     // index bytes per lane, row and step
+    constexpr int NQ = B32 == 64 ? 4 : 2; // 16-byte (12-byte for 24) index loads per row
+    constexpr bool PAIR = FMT == HXQ_FMT_VQ2_U16 || FMT == HXQ_FMT_VQ2_P12;
+    // uint8: 256 entries x 64 replicas; uint16 scalar: 4096 floats; pairs:
+    // 4096 float2; 6-bit levels: no table (the region is sized for the largest)
     constexpr int kTblBytes = 256 * kNrep * 4;
     constexpr int kABytes = BM * kBK * 2;
     // the table first, so it sits at LDS address 0 (lookups need no base add)
@@ -157,7 +168,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
 
     // ---- global sources ----------------------------------------------------------
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.M * K * 2);
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(g.idx, (int64_t)g.OUT * K);
+    const int64_t row_bytes = (int64_t)K / 32 * B32;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(g.idx, (int64_t)g.OUT * row_bytes);
     const int ngroups = AFFINE ? K / g.group : 1;
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(g.ga, AFFINE ? (int64_t)ngroups * g.OUT * 8 : 0);
     // X: thread t copies chunk t % 8 of rows t / 8 + (threads / 8) p
@@ -174,12 +186,12 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int n = nw + 32 * j + ml;
-        q_off[j] = n < g.OUT ? static_cast<uint32_t>(n * K + 32 * hh) : kOob;
+        q_off[j] = n < g.OUT ? static_cast<uint32_t>(n * row_bytes + B32 * hh) : kOob;
         a_off[j] = n < g.OUT ? static_cast<uint32_t>(n * 8) : kOob;
     }
 
     u32x4 xv[2][XP];   // X of steps s (buffer s & 1)
-    u32x4 qv[2][2 * NJ];  // index bytes: [2j + half]
+    u32x4 qv[2][NQ * NJ]; // index bytes of row j: qv[.][NQ j .. NQ j + NQ)
     float2 av[2][NJ];     // {scale, offset} per j
     auto load_step = [&](int s, int buf) {
         const bool live = s < nk;
@@ -189,9 +201,17 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             xv[buf][p] = buf_load16(xr, (x_off[p] == kOob || !live) ? kOob : x_off[p] + k0 * 2);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const uint32_t o = (q_off[j] == kOob || !live) ? kOob : q_off[j] + k0;
-            qv[buf][2 * j] = buf_load16(qr, o);
-            qv[buf][2 * j + 1] = buf_load16(qr, o == kOob ? kOob : o + 16u);
+            const uint32_t o = (q_off[j] == kOob || !live) ? kOob : q_off[j] + k0 / 32u * B32;
+#pragma unroll
+            for (int h = 0; h < NQ; ++h) {
+                if constexpr (B32 == 24) {  // two 12-byte loads
+                    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+                    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(qr, o == kOob ? kOob : o + 12u * h, 0, 0);
+                    qv[buf][NQ * j + h] = u32x4{v[0], v[1], v[2], 0u};
+                } else {
+                    qv[buf][NQ * j + h] = buf_load16(qr, o == kOob ? kOob : o + 16u * h);
+                }
+            }
         }
         if constexpr (AFFINE) {
             const uint32_t gofs = (k0 / static_cast<uint32_t>(g.group)) * static_cast<uint32_t>(g.OUT) * 8u;
@@ -243,23 +263,82 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     };
     if (has_sc) load_window();
 
-    // ---- codebook table: 64 replicas, conflict-free float4 writes ---------------
+    // ---- lookup table ------------------------------------------------------------
+    if constexpr (FMT == HXQ_FMT_SCALAR) {
+        // 64 replicas, conflict-free float4 writes
 #pragma unroll
-    for (int q = 0; q < 4096 / kThreads; ++q) {
-        const int slot = tid + kThreads * q;  // float4 slot: entry slot / 16
-        const float c = g.cb[slot >> 4];
-        *reinterpret_cast<float4 *>(tbl + 4 * slot) = make_float4(c, c, c, c);
+        for (int q = 0; q < 4096 / kThreads; ++q) {
+            const int slot = tid + kThreads * q;  // float4 slot: entry slot / 16
+            const float c = g.cb[slot >> 4];
+            *reinterpret_cast<float4 *>(tbl + 4 * slot) = make_float4(c, c, c, c);
+        }
+    } else if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
+        for (int j = tid; j < kPairCodes; j += kThreads) tbl[j] = j < g.n_codes ? g.cb[j] : 0.f;
+    } else if constexpr (PAIR) {
+        float2 *t2 = reinterpret_cast<float2 *>(tbl);
+        for (int j = tid; j < kPairCodes; j += kThreads)
+            t2[j] = j < g.n_codes ? make_float2(g.cb[2 * j], g.cb[2 * j + 1]) : make_float2(0.f, 0.f);
     }
 
     // ---- dequantise B into operand registers, one k substep at a time ----------
     // b[16j + 4s + t] holds bf16 pairs (weights 8s + 2t, 8s + 2t + 1 of the
     // lane's 32) of W row nw + 32j + ml: the B operand of substep s, subtile j
     const uint32_t lane_off = static_cast<uint32_t>(lane) * 4u;
+    // bits [bit, bit + width) of the little-endian 192-bit stream of a 24-byte chunk
+    auto field24 = [&](const u32x4 &q0, const u32x4 &q1, int bit, int width) -> uint32_t {
+        const uint32_t d[6] = {q0[0], q0[1], q0[2], q1[0], q1[1], q1[2]};
+        const int wi = bit >> 5, sh = bit & 31;
+        const uint32_t v = sh + width <= 32 ? d[wi] >> sh : __builtin_amdgcn_alignbit(d[wi + 1], d[wi], sh);
+        return v & ((1u << width) - 1u);
+    };
     auto dequant_sub = [&](int buf, int s, BV &b) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const float sc = AFFINE ? av[buf][j].x : 1.f;
             const float of = AFFINE ? av[buf][j].y : 0.f;
+            if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
+                // weights 8s .. 8s+7: the 16 bytes of load s, eight uint16 indices
+                const u32x4 q = qv[buf][NQ * j + s];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float v0 = tbl[q[t] & (kPairCodes - 1u)];
+                    float v1 = tbl[(q[t] >> 16) & (kPairCodes - 1u)];
+                    if constexpr (AFFINE) {
+                        v0 = affine_exact(v0, sc, of);
+                        v1 = affine_exact(v1, sc, of);
+                    }
+                    b[16 * j + 4 * s + t] = pack2<BF16>(v0, v1);
+                }
+                continue;
+            } else if constexpr (FMT == HXQ_FMT_VQ2_U16) {
+                // pairs 4s .. 4s+3: dwords 2s, 2s+1 of the 32 bytes
+                const float2 *t2 = reinterpret_cast<const float2 *>(tbl);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t w = qv[buf][NQ * j + (s >> 1)][2 * (s & 1) + (t >> 1)];
+                    const float2 c = t2[(w >> (16 * (t & 1))) & (kPairCodes - 1u)];
+                    b[16 * j + 4 * s + t] = pack2<BF16>(c.x, c.y);
+                }
+                continue;
+            } else if constexpr (FMT == HXQ_FMT_VQ2_P12) {
+                // pairs 4s .. 4s+3: 12-bit fields at bit 48s + 12t
+                const float2 *t2 = reinterpret_cast<const float2 *>(tbl);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float2 c = t2[field24(qv[buf][NQ * j], qv[buf][NQ * j + 1], 48 * s + 12 * t, 12)];
+                    b[16 * j + 4 * s + t] = pack2<BF16>(c.x, c.y);
+                }
+                continue;
+            } else if constexpr (FMT == HXQ_FMT_AF6) {
+                // levels 8s .. 8s+7: 6-bit fields at bit 48s + 6f
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float v0 = static_cast<float>(field24(qv[buf][NQ * j], qv[buf][NQ * j + 1], 48 * s + 12 * t, 6));
+                    const float v1 = static_cast<float>(field24(qv[buf][NQ * j], qv[buf][NQ * j + 1], 48 * s + 12 * t + 6, 6));
+                    b[16 * j + 4 * s + t] = pack2<BF16>(affine_exact(v0, sc, of), affine_exact(v1, sc, of));
+                }
+                continue;
+            }
 #pragma unroll
             for (int dd = 0; dd < 2; ++dd) {
                 const int d = 2 * s + dd;  // index dword (4 weights)
@@ -269,10 +348,10 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
                 float v2 = tbl_lookup0<kNrep, 2>(lane_off, w);
                 float v3 = tbl_lookup0<kNrep, 3>(lane_off, w);
                 if constexpr (AFFINE) {
-                    v0 = fmaf(v0, sc, of);
-                    v1 = fmaf(v1, sc, of);
-                    v2 = fmaf(v2, sc, of);
-                    v3 = fmaf(v3, sc, of);
+                    v0 = affine_exact(v0, sc, of);
+                    v1 = affine_exact(v1, sc, of);
+                    v2 = affine_exact(v2, sc, of);
+                    v3 = affine_exact(v3, sc, of);
                 }
                 b[16 * j + 2 * d] = pack2<BF16>(v0, v1);
                 b[16 * j + 2 * d + 1] = pack2<BF16>(v2, v3);
@@ -558,23 +637,32 @@ extern "C" int64_t hxq_prefill_gemm_workspace_bytes(int64_t m_rows, int64_t out_
     return pg::plan(m_rows, out_features, in_features, device_cu_count()).ws_bytes;
 }
 
-extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
-                                const float *codebook, const float *group_affine,
-                                int32_t group_size, const int32_t *sc_grp_ptr,
+extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
+                                const uint8_t *indices, const float *codebook, int32_t n_codes,
+                                const float *group_affine, int32_t group_size,
+                                const int32_t *sc_grp_ptr,
                                 const uint32_t *sc_grp_key, const float *sc_grp_val,
                                 const float *bias, void *y, int32_t y_dtype, int64_t m_rows,
                                 int64_t out_features, int64_t in_features, void *workspace,
                                 int64_t workspace_bytes, hipStream_t stream) {
     clear_error();
-    HXQ_REQUIRE(x && indices && codebook && y, "x, indices, codebook and y are required");
+    HXQ_REQUIRE(format >= HXQ_FMT_SCALAR && format <= HXQ_FMT_SCALAR_U16, "unknown index format");
+    HXQ_REQUIRE(x && indices && y && (codebook || format == HXQ_FMT_AF6),
+                "x, indices, codebook and y are required");
     HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16,
                 "the MFMA GEMM takes bf16 or fp16 activations (fp32 goes through hxq_gemv)");
+    HXQ_REQUIRE(format == HXQ_FMT_SCALAR || format == HXQ_FMT_AF6 ||
+                    (n_codes >= 1 && n_codes <= kPairCodes),
+                "uint16 and pair codebooks need 1..4096 entries");
+    HXQ_REQUIRE(format != HXQ_FMT_AF6 || group_affine, "6-bit levels need the group affine");
+    HXQ_REQUIRE(!(format == HXQ_FMT_VQ2_U16 || format == HXQ_FMT_VQ2_P12) || !group_affine,
+                "pair codebooks take no group affine");
     HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
     HXQ_REQUIRE(m_rows > 0 && out_features > 0 && in_features > 0, "empty problem");
     HXQ_REQUIRE(in_features % pg::kBK == 0, "in_features must be a multiple of 64");
     HXQ_REQUIRE(in_features < (int64_t{1} << 26), "in_features must be below 2^26");
     HXQ_REQUIRE(m_rows * in_features * 2 < (int64_t{1} << 31) &&
-                    out_features * in_features < (int64_t{1} << 31),
+                    out_features * (in_features / 32 * pg::fmt_b32(format)) < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
     HXQ_REQUIRE(!group_affine || (group_size >= pg::kBK && group_size % pg::kBK == 0 &&
                                   in_features % group_size == 0),
@@ -591,6 +679,7 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *i
     a.x = static_cast<const uint16_t *>(x);
     a.idx = indices;
     a.cb = codebook;
+    a.n_codes = n_codes;
     a.ga = reinterpret_cast<const float2 *>(group_affine);
     a.sc_ptr = sc_grp_ptr;
     a.sc_key = sc_grp_key;
@@ -624,16 +713,29 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *i
         a.tiles_per_xcd = (L.n + pg::kXcds - 1) / pg::kXcds;
         a.vec_out = L.ks == 1 && vec;
         const dim3 grid(a.tiles_per_xcd * pg::kXcds, L.ks);
-#define HXQ_PG_LAUNCH(BM_, BF_, AF_) \
-        hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ>), grid, \
+#define HXQ_PG_LAUNCH(BM_, BF_, AF_, F_) \
+        hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ, F_>), grid, \
                            dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a)
-        if (p.bm == 256) {
-            if (bf16) { if (aff) HXQ_PG_LAUNCH(256, true, true); else HXQ_PG_LAUNCH(256, true, false); }
-            else { if (aff) HXQ_PG_LAUNCH(256, false, true); else HXQ_PG_LAUNCH(256, false, false); }
-        } else {
-            if (bf16) { if (aff) HXQ_PG_LAUNCH(128, true, true); else HXQ_PG_LAUNCH(128, true, false); }
-            else { if (aff) HXQ_PG_LAUNCH(128, false, true); else HXQ_PG_LAUNCH(128, false, false); }
+#define HXQ_PG_FMT(BM_, BF_)                                                                  \
+        switch (format) {                                                                      \
+            case HXQ_FMT_SCALAR:                                                               \
+                if (aff) HXQ_PG_LAUNCH(BM_, BF_, true, HXQ_FMT_SCALAR);                        \
+                else HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_SCALAR);                           \
+                break;                                                                         \
+            case HXQ_FMT_SCALAR_U16:                                                           \
+                if (aff) HXQ_PG_LAUNCH(BM_, BF_, true, HXQ_FMT_SCALAR_U16);                    \
+                else HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_SCALAR_U16);                       \
+                break;                                                                         \
+            case HXQ_FMT_VQ2_U16: HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_VQ2_U16); break;       \
+            case HXQ_FMT_VQ2_P12: HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_VQ2_P12); break;       \
+            default: HXQ_PG_LAUNCH(BM_, BF_, true, HXQ_FMT_AF6); break;                        \
         }
+        if (p.bm == 256) {
+            if (bf16) { HXQ_PG_FMT(256, true) } else { HXQ_PG_FMT(256, false) }
+        } else {
+            if (bf16) { HXQ_PG_FMT(128, true) } else { HXQ_PG_FMT(128, false) }
+        }
+#undef HXQ_PG_FMT
 #undef HXQ_PG_LAUNCH
         HXQ_LAUNCH_CHECK();
         if (L.ks > 1) {

@@ -80,7 +80,8 @@ SIGNATURES = {
     "hxq_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemm_ws": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64, P],
     "hxq_gemm_noalloc": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
-    "hxq_prefill_gemm": [P, I32, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64, P],
+    "hxq_prefill_gemm": [P, I32, I32, P, P, I32, P, I32, P, P, P, P, P, I32, I64, I64, I64, P, I64,
+                         P],
     "hxq_affine_pack": [P, P, I64, I64, P, P],
     "hxq_ssm_chunk_scan": [P, I32, P, I32, P, P, P, I32, P, P, P, I32, P, I64, I64, I64, I64,
                            I64, I64, I64, P, I64, P],
@@ -417,26 +418,36 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
 
 
 def prefill_gemm(x, indices, codebook, group_affine, group_size, sc_grp_ptr, sc_grp_key,
-                 sc_grp_val, bias=None, out_dtype=None, out=None):
+                 sc_grp_val, bias=None, out_dtype=None, out=None, fmt=None, out_features=None):
     """Y = X @ W^T (+bias) on MFMA with W dequantised into the operand registers
     (hxq_prefill_gemm).  X bf16/fp16 [M, K]; group_affine [K/G, OUT, 2] or None;
-    sidecar in the row-group order of ``hxq_format.sidecar_row_groups``."""
+    sidecar in the row-group order of ``hxq_format.sidecar_row_groups``.
+    fmt: FMT_* (default: uint8 scalar, indices [OUT, K]); other formats pass
+    the raw index tensor and out_features."""
     m, in_f = x.shape
-    out_f = indices.shape[0]
-    if indices.shape[1] != in_f:
-        raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
+    fmt = FMT_SCALAR if fmt is None else int(fmt)
+    if fmt == FMT_SCALAR:
+        out_f = indices.shape[0]
+        if indices.shape[1] != in_f:
+            raise RuntimeError(f"x has {in_f} features, weight expects {indices.shape[1]}")
+        _need_cb256(codebook)
+        n_codes = 256
+    else:
+        out_f = int(out_features)
+        n_codes = 0 if codebook is None else int(codebook.shape[0])
+        if codebook is not None:
+            _need_f32(codebook=codebook)
     if out is None:
         out = torch.empty(m, out_f, dtype=out_dtype or x.dtype, device=x.device)
     _need_device(x, indices, codebook, group_affine, sc_grp_ptr, sc_grp_key, sc_grp_val, bias, out)
-    _need_cb256(codebook)
     _need_f32(group_affine=group_affine, sc_grp_val=sc_grp_val, bias=bias)
     _need_i32(sc_grp_ptr=sc_grp_ptr, sc_grp_key=sc_grp_key)
     L = lib()
     with torch.cuda.device(x.device):
         nbytes = L.hxq_prefill_gemm_workspace_bytes(m, out_f, in_f)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
-        rc = L.hxq_prefill_gemm(_ptr(x), dtype_code(x.dtype), _ptr(indices), _ptr(codebook),
-                                _ptr(group_affine), int(group_size), _ptr(sc_grp_ptr),
+        rc = L.hxq_prefill_gemm(_ptr(x), dtype_code(x.dtype), fmt, _ptr(indices), _ptr(codebook),
+                                n_codes, _ptr(group_affine), int(group_size), _ptr(sc_grp_ptr),
                                 _ptr(sc_grp_key), _ptr(sc_grp_val), _ptr(bias), _ptr(out),
                                 dtype_code(out.dtype), m, out_f, in_f, _ptr(ws), nbytes,
                                 _stream(x))

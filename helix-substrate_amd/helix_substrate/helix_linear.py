@@ -218,7 +218,7 @@ class HelixLinear(nn.Module):
                 self.register_buffer(name, None)
         # the MFMA GEMM steps K by 64 and reads one affine group per step, in
         # the layout [K/G, OUT, 2] = {scale, offset} (derived, not saved)
-        self._gemm_ok = (self._fmt == _hxq.FMT_SCALAR and self.in_features % 64 == 0 and
+        self._gemm_ok = (self.in_features % 64 == 0 and
                          (not has_affine or self.group_size % 64 == 0))
         self.register_buffer(
             "_affine_t",
@@ -277,10 +277,13 @@ class HelixLinear(nn.Module):
             for name in ("_sc_row_ptr", "_sc_col", "_sc_val", "_sc_delta", "_sidecar_rows",
                          "_sidecar_cols", "_sidecar_deltas", "_sidecar_vq_vals"):
                 self.register_buffer(name, None)
-        self._gemm_ok = False
+        self._gemm_ok = self.in_features % 64 == 0
         self.register_buffer("_affine_t", None, persistent=False)
-        for name in ("_sc_grp_ptr", "_sc_grp_key", "_sc_grp_val"):
-            self.register_buffer(name, None, persistent=False)
+        grp = (sidecar_row_groups(self._sidecar_rows, self._sidecar_cols, self._sc_val,
+                                  self.out_features, self.in_features)
+               if self._gemm_ok and self._sc_row_ptr is not None else (None, None, None))
+        for name, t in zip(("_sc_grp_ptr", "_sc_grp_key", "_sc_grp_val"), grp):
+            self.register_buffer(name, t, persistent=False)
         self.has_svd = self.svd_U is not None
         self.rank = int(self.svd_U.shape[1]) if self.has_svd else 0
         self.has_channel_scales = self.channel_scales is not None
@@ -411,7 +414,18 @@ class HelixLinear(nn.Module):
         out = torch.empty(n, self.out_features, dtype=out_dtype, device=x2.device)
         if n == 0:
             pass
-        elif self.vector_dim != 1 or self._fmt != _hxq.FMT_SCALAR:
+        elif n > _GEMV_MAX_ROWS and x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
+            # every index format: W dequantised into the MFMA operand registers
+            self._last_dispatch_path = "hip_gemm"
+            grp = rp is not None
+            scalar8 = self._fmt == _hxq.FMT_SCALAR
+            _hxq.prefill_gemm(x2, self.indices, self._kcb if scalar8 else self.codebook,
+                              self._affine_t, self.group_size,
+                              self._sc_grp_ptr if grp else None,
+                              self._sc_grp_key if grp else None,
+                              self._sc_grp_val if grp else None, self.bias, out=out,
+                              fmt=self._fmt, out_features=self.out_features)
+        elif self._fmt != _hxq.FMT_SCALAR:
             self._forward_hip_fmt(x2, rp, col, delta, out)
         elif n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv"
@@ -419,13 +433,6 @@ class HelixLinear(nn.Module):
                 _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
                           self.group_offset, self.group_size, rp, col, delta, self.bias,
                           out=out[r0:r1])
-        elif x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
-            self._last_dispatch_path = "hip_gemm"
-            grp = rp is not None
-            _hxq.prefill_gemm(x2, self.indices, self._kcb, self._affine_t, self.group_size,
-                              self._sc_grp_ptr if grp else None,
-                              self._sc_grp_key if grp else None,
-                              self._sc_grp_val if grp else None, self.bias, out=out)
         else:
             # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
             self._last_dispatch_path = "hip_gemv_rows"
@@ -445,7 +452,9 @@ class HelixLinear(nn.Module):
         return [(r0, min(n, r0 + step)) for r0 in range(0, n, step)]
 
     def _forward_hip_fmt(self, x2, rp, col, delta, out) -> None:
-        """Pair codebooks and int16-index scalar codebooks."""
+        """Pair codebooks and int16-index scalar codebooks: the format GEMV for up to
+        4 rows; above that (fp32 activations, or in_features not a multiple of 64)
+        dequantised row tiles and the library GEMM."""
         n = x2.shape[0]
         if n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv_fmt"

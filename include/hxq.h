@@ -240,7 +240,10 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
  * hxq_prefill_gemm: the prefill GEMM Y = X W^T (+ bias) with W dequantised
  * straight into the MFMA operand registers (bf16/fp16 X [m_rows, in],
  * fp32 accumulation, y in y_dtype; in_features % 64 == 0; affine as for
- * hxq_gemm).  The sidecar comes in the kernel's order: for each group of 64
+ * hxq_gemm), for every index format (HXQ_FMT_*): uint8 with the 256-entry
+ * codebook, uint16 with n_codes entries, pair codebooks [n_codes, 2] (uint16
+ * or 12-bit packed indices, no affine) and 6-bit levels (affine, no
+ * codebook).  The sidecar comes in the kernel's order: for each group of 64
  * output rows g (rows [64g, 64g + 64)), its entries sorted by column then row
  * (stable): sc_grp_ptr int32 [ceil(out/64) + 1], sc_grp_key uint32
  * (col << 6) | (row - 64g), sc_grp_val fp32 replacement values (NULL
@@ -253,8 +256,9 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
  */
 int64_t hxq_prefill_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
                                          int64_t in_features);
-int hxq_prefill_gemm(const void *x, int32_t x_dtype, const uint8_t *indices,
-                     const float *codebook, const float *group_affine, int32_t group_size,
+int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format, const uint8_t *indices,
+                     const float *codebook, int32_t n_codes, const float *group_affine,
+                     int32_t group_size,
                      const int32_t *sc_grp_ptr, const uint32_t *sc_grp_key,
                      const float *sc_grp_val, const float *bias, void *y, int32_t y_dtype,
                      int64_t m_rows, int64_t out_features, int64_t in_features,

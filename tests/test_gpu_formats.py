@@ -14,7 +14,7 @@ from helix_substrate import _hxq
 from helix_substrate.affine_group import (affine_group_matmul_reference, fused_affine_group_matmul,
                                           fused_affine_group_matmul_packed6)
 from helix_substrate.helix_linear import HelixLinear
-from helix_substrate.hxq_format import build_sidecar_csr
+from helix_substrate.hxq_format import build_sidecar_csr, sidecar_row_groups
 from helix_substrate.index_packing import pack_6bit, pack_12bit
 
 pytestmark = pytest.mark.gpu
@@ -116,7 +116,8 @@ def test_pair_helix_linear_device(dev, packed):
     for n, dt, tol, path in [(1, torch.float32, 1e-5, "hip_gemv_fmt"),
                              (4, torch.bfloat16, 2e-2, "hip_gemv_fmt"),
                              (37, torch.float32, 1e-5, "hip_dequant_gemm"),
-                             (64, torch.bfloat16, 2e-2, "hip_dequant_gemm")]:
+                             (64, torch.bfloat16, 2e-2, "hip_gemm"),
+                             (300, torch.float16, 2e-2, "hip_gemm")]:
         x = torch.from_numpy(rs.randn(n, inp).astype(np.float32)).to(dt)
         y = m(x.to(dev))
         assert m._last_dispatch_path == path and y.dtype == dt
@@ -142,7 +143,8 @@ def test_affine_group_entry_points(dev):
     W6 = oracle.reconstruct_af6_np(q6.numpy(), s.float().numpy(), o.float().numpy(), G)
     p6 = pack_6bit(q6).to(dev)
     print("affine group 6-bit", flush=True)
-    for n, dt, tol in [(1, torch.float32, 1e-5), (4, torch.bfloat16, 2e-2), (20, torch.float32, 1e-5)]:
+    for n, dt, tol in [(1, torch.float32, 1e-5), (4, torch.bfloat16, 2e-2), (20, torch.float32, 1e-5),
+                       (96, torch.bfloat16, 2e-2)]:
         x = torch.from_numpy(rs.randn(n, inp).astype(np.float32)).to(dt)
         y = fused_affine_group_matmul_packed6(x.to(dev), p6, s.to(dev), o.to(dev), out, inp, G,
                                               b.to(dev))
@@ -154,24 +156,68 @@ def test_affine_group_entry_points(dev):
 
 
 # ---------------------------------------------------------------------------
+# the MFMA prefill GEMM over every index format
+# ---------------------------------------------------------------------------
+def _grp(dev, pos, val, out, inp):
+    t = torch.from_numpy
+    return [a.to(dev) for a in sidecar_row_groups(t(pos // inp), t(pos % inp), t(val), out, inp)]
+
+
+@pytest.mark.parametrize("fmt", FMTS + [_hxq.FMT_SCALAR_U16])
+@pytest.mark.parametrize("m,out,inp,G", [(300, 1000, 1024, 128),   # ragged M/OUT, split K
+                                         (1024, 2048, 2048, 64),
+                                         (5, 256, 11008, 128)])    # one row tile, long K
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_prefill_fmt_matches_oracle(dev, fmt, m, out, inp, G, xdt):
+    """Against the oracle's W: the 2e-2 bar in fp64, and 2e-5 against W rounded
+    to the activation type (all that is left is fp32 accumulation order)."""
+    if fmt == _hxq.FMT_SCALAR_U16:
+        mod, W = _wide_layer(out, inp, 3000, seed=m + out, group_size=G)
+        raw, cb, aff = mod.indices, mod.codebook, mod._affine_t
+        gp, gk, gv = mod._sc_grp_ptr, mod._sc_grp_key, mod._sc_grp_val
+        raw, cb, aff, gp, gk, gv = _dev(dev, raw, cb, aff, gp, gk, gv)
+    else:
+        raw, cb, s, o, pos, val, W, _ = _case(fmt, out, inp, G=G, seed=m + inp)
+        aff = None if s is None else np.ascontiguousarray(np.stack([s.T, o.T], axis=-1))
+        raw, cb, aff = _dev(dev, raw, cb, aff)
+        gp, gk, gv = _grp(dev, pos, val, out, inp)
+    g = torch.Generator().manual_seed(m)
+    x = torch.randn(m, inp, generator=g).to(xdt)
+    bias = torch.randn(out, generator=g) * 0.1
+    print(f"prefill fmt={fmt} m={m} out={out} in={inp} G={G} x={xdt}", flush=True)
+    y = _hxq.prefill_gemm(x.to(dev), raw, cb, aff, G, gp, gk, gv, bias=bias.to(dev),
+                          out_dtype=torch.float32, fmt=fmt, out_features=out)
+    y = y.cpu().numpy()
+    xf = x.float().numpy()
+    assert _maxrel(y, oracle.linear_np(xf, W, bias.numpy())) <= 2e-2
+    W16 = torch.from_numpy(W).to(xdt).float().numpy()
+    rel = _maxrel(y, oracle.linear_np(xf, W16, bias.numpy()))
+    assert rel <= 2e-5, rel
+    y16 = _hxq.prefill_gemm(x.to(dev), raw, cb, aff, G, gp, gk, gv, bias=bias.to(dev),
+                            fmt=fmt, out_features=out)
+    assert y16.dtype == xdt
+    assert _maxrel(y16.float().cpu().numpy(), y) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
 # scalar codebooks above 256 entries: uint16 indices (int16 in memory)
 # ---------------------------------------------------------------------------
-def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001):
+def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001, group_size=128):
     rs = np.random.RandomState(seed)
     cb = np.sort(rs.standard_normal(k).astype(np.float32) * 0.02)
     idx = rs.randint(0, k, (out_f, in_f)).astype(np.uint16)
     gs = go = None
     if affine:
-        gs = rs.uniform(0.95, 1.05, (out_f, in_f // 128)).astype(np.float32)
-        go = rs.normal(0, 1e-4, (out_f, in_f // 128)).astype(np.float32)
+        gs = rs.uniform(0.95, 1.05, (out_f, in_f // group_size)).astype(np.float32)
+        go = rs.normal(0, 1e-4, (out_f, in_f // group_size)).astype(np.float32)
     nnz = int(round(density * out_f * in_f))
     pos = np.sort(rs.choice(out_f * in_f, nnz, replace=False)).astype(np.int64)
     val = (np.where(rs.random_sample(nnz) < 0.5, -1, 1) * rs.uniform(4, 8, nnz) * 0.02).astype(
         np.float16).astype(np.float32)
     t = lambda a: None if a is None else torch.from_numpy(a)
     m = HelixLinear(in_f, out_f, t(cb), t(idx.astype(np.int16)), t(pos), t(val),
-                    group_scale=t(gs), group_offset=t(go), group_size=128)
-    return m, oracle.reconstruct_np(idx, cb, gs, go, 128, pos, val)
+                    group_scale=t(gs), group_offset=t(go), group_size=group_size)
+    return m, oracle.reconstruct_np(idx, cb, gs, go, group_size, pos, val)
 
 
 @pytest.mark.parametrize("k,out_f,in_f,affine", [
@@ -203,7 +249,7 @@ def test_wide_scalar_many_rows(dev):
     m = m.to(dev)
     x = torch.randn(40, 1024, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
     y = m(x.to(dev))
-    assert y.dtype == torch.bfloat16
+    assert y.dtype == torch.bfloat16 and m._last_dispatch_path == "hip_gemm"
     assert _maxrel(y.float().cpu().numpy(), oracle.linear_f64(x.float().numpy(), W)) <= 2e-2
     x32 = torch.randn(9, 1024, generator=torch.Generator().manual_seed(5))
     y32 = m(x32.to(dev))

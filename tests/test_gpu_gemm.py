@@ -4,9 +4,9 @@ Two bars per case:
   * the BASELINE bar: max|Y - Y_ref| / max|Y_ref| <= 2e-2 with Y_ref the fp64
     contraction of the 16-bit activations with the exact fp32 W;
   * a tight bar pinning layout, sidecar and affine handling: against W
-    rounded to the activation's 16-bit type (what the kernel multiplies),
-    the only error left is fp32 accumulation plus rare one-ulp rounding
-    flips of single weights (fma vs two roundings), so <= 2e-4.
+    rounded to the activation's 16-bit type (what the kernel multiplies,
+    the affine kept as two roundings fl(fl(c * s) + o) like the oracle), the
+    only error left is fp32 accumulation order, so <= 2e-5.
 """
 import numpy as np
 import pytest
@@ -57,7 +57,7 @@ def _check(y, x16, W, bias=None):
     if is32:
         W16 = torch.from_numpy(W).to(x16.dtype).float().numpy()
         rel = _maxrel(y, oracle.linear_np(xf, W16, b))
-        assert rel <= 2e-4, rel
+        assert rel <= 2e-5, rel
 
 
 def _gemm32(mod, x):
@@ -197,7 +197,7 @@ def _row_slice(m):
 def test_gemm_config2_shapes_m512(dev, out_f, in_f):
     """Benchmark config 2 (Qwen2.5-7B prefill) at M = 512, sigma 0.015: a row
     slice of Y against the fp64 oracle of the full reconstructed W (bf16
-    output at the 2e-2 bar; fp32 output also at the tight 2e-4 bar)."""
+    output at the 2e-2 bar; fp32 output also at the tight 2e-5 bar)."""
     m = 512
     print(f"config-2 gemm m={m} out={out_f} in={in_f}", flush=True)
     L, T = _layer(out_f, in_f, seed=out_f + 3 * in_f, sigma=0.015)
