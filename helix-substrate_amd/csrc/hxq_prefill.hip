@@ -51,6 +51,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBN = 256;       // output columns per block
 constexpr int kBK = 64;        // K per step
@@ -67,7 +68,7 @@ struct Args {
     const uint8_t *idx;      // index data, rows of K * (bits per weight) / 8 bytes
     const float *cb;         // [256] (uint8), [n_codes] (uint16), [n_codes, 2] (pairs)
     const float2 *ga;        // [K/G, OUT] {scale, offset} or null
-    const int32_t *sc_ptr;   // [ceil(OUT/64) + 1] or null
+    const int32_t *sc_ptr;   // [ceil(OUT/64) * K/64 + 1] step pointers, or null
     const uint32_t *sc_key;  // (col << 6) | (row % 64), sorted within each 64-row group
     const float *sc_val;
     const float *bias;       // [OUT] or null
@@ -190,6 +191,43 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
         a_off[j] = n < g.OUT ? static_cast<uint32_t>(n * 8) : kOob;
     }
 
+    // ---- sidecar: the entries of each K step, one per lane ----------------------
+    // sc_ptr[G * nsteps + t] is the first entry of 64-row group G whose column
+    // lies in K step t or later (the groups' lists are concatenated, so the
+    // pointer one past a group's last step starts the next group).  Per step,
+    // a wave loads 64 entries from that pointer: those before the step's end
+    // column are the step's.  Pointers are loaded two steps before their
+    // entries and entries one step before their use, all unconditionally (the
+    // loads past a range read 0 and are masked when used), so that no wait
+    // on a fresh load enters the pipeline.  Steps with more than 64 entries
+    // in a group read the rest directly (correct, slower).
+    const bool has_sc = g.sc_ptr != nullptr && nw < g.OUT;
+    const int nsteps = K / kBK;
+    const int sgrp = nw >> 6;
+    const int sp0 = sgrp * nsteps + kb;  // pointer of this block's first step
+    const int e_hi = has_sc ? g.sc_ptr[(sgrp + 1) * nsteps] : 0;  // end of the group's list
+    const __amdgpu_buffer_rsrc_t pr =
+        make_rsrc(g.sc_ptr, has_sc ? int64_t{4} * ((g.OUT + 63) / 64 * nsteps + 1) : 0);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(g.sc_key, int64_t{4} * e_hi);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(g.sc_val, int64_t{4} * e_hi);
+    // this wave's rows within its 64-row sidecar group: [rlo, rlo + 32 NJ)
+    const uint32_t rlo = static_cast<uint32_t>(nw & 63);
+    uint32_t ps[2];  // pointer of step t, loaded by load_step(t - 2) (buffer t & 1)
+    uint32_t sk[2];  // keys and values of step t (buffer t & 1)
+    float sv[2];
+    int sb[2];       // the list index of lane 0's entry in sk/sv
+    auto load_ptr = [&](int t, int buf) {
+        ps[buf] = __builtin_amdgcn_raw_buffer_load_b32(
+            pr, (has_sc && t < nk) ? static_cast<uint32_t>(sp0 + t) * 4u : kOob, 0, 0);
+    };
+    auto load_entries = [&](int t, int buf) {
+        sb[buf] = __builtin_amdgcn_readfirstlane(static_cast<int>(ps[buf]));
+        const uint32_t o = (has_sc && t < nk) ? static_cast<uint32_t>(sb[buf] + lane) * 4u : kOob;
+        sk[buf] = __builtin_amdgcn_raw_buffer_load_b32(kr, o, 0, 0);
+        sv[buf] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, o, 0, 0));
+        load_ptr(t + 2, buf);
+    };
+
     u32x4 xv[2][XP];   // X of steps s (buffer s & 1)
     u32x4 qv[2][NQ * NJ]; // index bytes of row j: qv[.][NQ j .. NQ j + NQ)
     float2 av[2][NJ];     // {scale, offset} per j
@@ -218,11 +256,11 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + gofs;
-                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(ar, o, 0, 0);
-                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(ar, o == kOob ? kOob : o + 4u, 0, 0);
-                av[buf][j] = make_float2(__uint_as_float(lo), __uint_as_float(hi));
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(ar, o, 0, 0);
+                av[buf][j] = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
             }
         }
+        load_entries(s, buf);
     };
     // rows r and r + (threads / 8) p share the swizzle ((r / 2) % 8): one base
     // address, the other rows at immediate offsets
@@ -233,35 +271,6 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
         for (int p = 0; p < XP; ++p)
             *reinterpret_cast<u32x4 *>(sA + (kThreads / 8) * p * kBK) = xv[buf][p];
     };
-
-    // ---- sidecar window: 64 entries of this wave's list, one per lane ---------
-    const bool has_sc = g.sc_ptr != nullptr && nw < g.OUT;
-    // this wave's rows within its 64-row sidecar group: [rlo, rlo + 32 NJ)
-    const uint32_t rlo = static_cast<uint32_t>(nw & 63);
-    int e_lo = 0, e_hi = 0;
-    if (has_sc) {
-        const int grp = nw >> 6;
-        e_lo = g.sc_ptr[grp];
-        e_hi = g.sc_ptr[grp + 1];
-        // split-K range: first entry at or past its first column (binary search)
-        const uint32_t kstart = static_cast<uint32_t>(kb * kBK) << 6;
-        int lo = e_lo, hi = kb > 0 ? e_hi : e_lo;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (g.sc_key[mid] < kstart) lo = mid + 1;
-            else hi = mid;
-        }
-        e_lo = lo;
-    }
-    int win = e_lo;  // list index of lane 0's entry
-    uint32_t wkey = 0xffffffffu;
-    float wval = 0.f;
-    auto load_window = [&]() {
-        const int e = win + lane;
-        wkey = e < e_hi ? g.sc_key[e] : 0xffffffffu;
-        wval = e < e_hi ? g.sc_val[e] : 0.f;
-    };
-    if (has_sc) load_window();
 
     // ---- lookup table ------------------------------------------------------------
     if constexpr (FMT == HXQ_FMT_SCALAR) {
@@ -358,36 +367,41 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             }
         }
     };
-    // Replace the sidecar entries of step s (columns [k1, k1 + 64)) in b.
-    auto patch = [&](int s, BV &b) {
-        if (!has_sc) return;
+    // Replace sidecar entries in b: the lanes set in m hold (key, value) pairs
+    // of step columns [k1, k1 + 64) and this wave's rows.
+    auto apply = [&](uint32_t key_v, float val_v, unsigned long long m, uint32_t k1, BV &b) {
+        while (m) {
+            const int src = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t key = __builtin_amdgcn_readlane(key_v, src);
+            const float val = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(val_v), src));
+            const uint32_t col = (key >> 6) - k1;  // 0..63
+            const uint32_t row = (key & 63u) - rlo; // row within this wave
+            const int owner = static_cast<int>((row & 31u) + 32u * (col >> 5));
+            const int reg = __builtin_amdgcn_readfirstlane(static_cast<int>(16u * (row >> 5) + ((col & 31u) >> 1)));
+            const uint32_t v16 = to16<BF16>(val);
+            const uint32_t hi = col & 1u;
+            const uint32_t old = b[reg];
+            const uint32_t upd = hi ? ((old & 0xffffu) | (v16 << 16)) : ((old & 0xffff0000u) | v16);
+            b[reg] = lane == owner ? upd : old;
+        }
+    };
+    // The sidecar entries of step s (buffer buf) into b.
+    auto patch = [&](int s, int buf, BV &b) {
+        if (!has_sc || s >= nk) return;  // (the pipeline's last refill is past the range)
         const uint32_t k1 = static_cast<uint32_t>((kb + s) * kBK);
-        const uint32_t klo = k1 << 6, khi = (k1 + kBK) << 6;
-        for (;;) {
-            unsigned long long m = __ballot(wkey >= klo && wkey < khi &&
-                                            (wkey & 63u) - rlo < static_cast<uint32_t>(32 * NJ));
-            while (m) {
-                const int src = __builtin_ctzll(m);
-                m &= m - 1;
-                const uint32_t key = __builtin_amdgcn_readlane(wkey, src);
-                const float val = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wval), src));
-                const uint32_t col = (key >> 6) - k1;  // 0..63
-                const uint32_t row = (key & 63u) - rlo; // row within this wave
-                const int owner = static_cast<int>((row & 31u) + 32u * (col >> 5));
-                const int reg = __builtin_amdgcn_readfirstlane(static_cast<int>(16u * (row >> 5) + ((col & 31u) >> 1)));
-                const uint32_t v16 = to16<BF16>(val);
-                const uint32_t hi = col & 1u;
-                const uint32_t old = b[reg];
-                const uint32_t upd = hi ? ((old & 0xffffu) | (v16 << 16)) : ((old & 0xffff0000u) | v16);
-                b[reg] = lane == owner ? upd : old;
-            }
-            // window used up (its last entry lies before the step's end): slide it
-            const uint32_t last = __builtin_amdgcn_readlane(wkey, 63);
-            if (win + 64 < e_hi && last < khi) {
-                win += 64;
-                load_window();
-            } else {
-                break;
+        const uint32_t khi = (k1 + kBK) << 6;
+        const uint32_t nrow = static_cast<uint32_t>(32 * NJ);
+        const uint32_t key = sk[buf];
+        apply(key, sv[buf], __ballot(sb[buf] + lane < e_hi && key < khi && (key & 63u) - rlo < nrow), k1, b);
+        if (sb[buf] + 64 < e_hi && __builtin_amdgcn_readlane(key, 63) < khi) {
+            // more than 64 entries in this step: the rest straight from the list
+            for (int ob = sb[buf] + 64; ob < e_hi; ob += 64) {
+                const int e = ob + lane;
+                const uint32_t k2 = e < e_hi ? g.sc_key[e] : 0xffffffffu;
+                const float v2 = e < e_hi ? g.sc_val[e] : 0.f;
+                apply(k2, v2, __ballot(k2 < khi && (k2 & 63u) - rlo < nrow), k1, b);
+                if (__builtin_amdgcn_readlane(k2, 63) >= khi) break;
             }
         }
     };
@@ -436,6 +450,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     // ---- pipeline ---------------------------------------------------------------
     // loads two steps ahead; X of step s+1 goes to LDS during step s; B of step
     // s+1 replaces B of step s substep by substep; one barrier per step.
+    load_ptr(0, 0);
+    load_ptr(1, 1);
     load_step(0, 0);
     load_step(1, 1);
     store_x(0);                 // waits for X(0)
@@ -443,20 +459,20 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     BV b;
 #pragma unroll
     for (int s = 0; s < 4; ++s) dequant_sub(0, s, b);  // B(0)
-    patch(0, b);
+    patch(0, 0, b);
     load_step(2, 0);
     int ks = 0;
     for (; ks + 1 < nk; ks += 2) {
         // step ks: A in LDS buffer 0, B(ks) in b; X(ks+1) and idx(ks+1) in buffer 1
         store_x(1);
         mfma_step(0, 1, b);     // b <- B(ks+1)
-        patch(ks + 1, b);
+        patch(ks + 1, 1, b);
         load_step(ks + 3, 1);
         lds_barrier();
         // step ks + 1: A in buffer 1; X(ks+2) and idx(ks+2) in buffer 0
         store_x(0);
         mfma_step(1, 0, b);     // b <- B(ks+2)
-        patch(ks + 2, b);
+        patch(ks + 2, 0, b);
         load_step(ks + 4, 0);
         lds_barrier();
     }
@@ -599,12 +615,13 @@ static Launch launch_of(int t0, int n, int ks, int nk) {
 // every other shape 256 down to M = 512.  One block runs per CU, so a grid
 // of several rounds whose last round would fill under half the CUs runs
 // that tail as a second launch with K split across the idle CUs.
-Plan plan(int64_t m, int64_t out, int64_t in, int cus) {
+// bm_max 128: formats whose 256-row kernel would not fit the register file.
+Plan plan(int64_t m, int64_t out, int64_t in, int cus, int bm_max = 256) {
     Plan p{};
     p.tiles_x = static_cast<int>((out + kBN - 1) / kBN);
     const int nk = static_cast<int>(in / kBK);
     const int64_t t256 = p.tiles_x * ((m + 255) / 256);
-    p.bm = t256 * split_of(t256, nk, cus) * 2 > cus ? 256 : 128;
+    p.bm = bm_max == 256 && t256 * split_of(t256, nk, cus) * 2 > cus ? 256 : 128;
     p.tiles_y = static_cast<int>((m + p.bm - 1) / p.bm);
     const int tiles = p.tiles_x * p.tiles_y;
     const int rem = tiles % cus;
@@ -634,7 +651,10 @@ using namespace hxq;
 extern "C" int64_t hxq_prefill_gemm_workspace_bytes(int64_t m_rows, int64_t out_features,
                                                     int64_t in_features) {
     if (m_rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % pg::kBK) return 0;
-    return pg::plan(m_rows, out_features, in_features, device_cu_count()).ws_bytes;
+    // the largest over the row-tile heights a format may use
+    const int cus = device_cu_count();
+    return std::max(pg::plan(m_rows, out_features, in_features, cus).ws_bytes,
+                    pg::plan(m_rows, out_features, in_features, cus, 128).ws_bytes);
 }
 
 extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
@@ -674,7 +694,11 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
     HXQ_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                     (reinterpret_cast<uintptr_t>(indices) & 15u) == 0,
                 "x and indices must be 16-byte aligned");
-    const pg::Plan p = pg::plan(m_rows, out_features, in_features, device_cu_count());
+    // uint16 scalar indices with the affine need more registers than the
+    // 256-row tile leaves: 128-row tiles
+    const bool u16_aff = format == HXQ_FMT_SCALAR_U16 && group_affine != nullptr;
+    const pg::Plan p = pg::plan(m_rows, out_features, in_features, device_cu_count(),
+                                u16_aff ? 128 : 256);
     pg::Args a{};
     a.x = static_cast<const uint16_t *>(x);
     a.idx = indices;
@@ -723,7 +747,7 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
                 else HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_SCALAR);                           \
                 break;                                                                         \
             case HXQ_FMT_SCALAR_U16:                                                           \
-                if (aff) HXQ_PG_LAUNCH(BM_, BF_, true, HXQ_FMT_SCALAR_U16);                    \
+                if (aff) HXQ_PG_LAUNCH(128, BF_, true, HXQ_FMT_SCALAR_U16);                    \
                 else HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_SCALAR_U16);                       \
                 break;                                                                         \
             case HXQ_FMT_VQ2_U16: HXQ_PG_LAUNCH(BM_, BF_, false, HXQ_FMT_VQ2_U16); break;       \

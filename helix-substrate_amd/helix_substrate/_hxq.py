@@ -421,7 +421,8 @@ def prefill_gemm(x, indices, codebook, group_affine, group_size, sc_grp_ptr, sc_
                  sc_grp_val, bias=None, out_dtype=None, out=None, fmt=None, out_features=None):
     """Y = X @ W^T (+bias) on MFMA with W dequantised into the operand registers
     (hxq_prefill_gemm).  X bf16/fp16 [M, K]; group_affine [K/G, OUT, 2] or None;
-    sidecar in the row-group order of ``hxq_format.sidecar_row_groups``.
+    sidecar in the row-group order of ``hxq_format.sidecar_row_groups`` (step
+    pointers, keys, values).
     fmt: FMT_* (default: uint8 scalar, indices [OUT, K]); other formats pass
     the raw index tensor and out_features."""
     m, in_f = x.shape
@@ -442,6 +443,9 @@ def prefill_gemm(x, indices, codebook, group_affine, group_size, sc_grp_ptr, sc_
     _need_device(x, indices, codebook, group_affine, sc_grp_ptr, sc_grp_key, sc_grp_val, bias, out)
     _need_f32(group_affine=group_affine, sc_grp_val=sc_grp_val, bias=bias)
     _need_i32(sc_grp_ptr=sc_grp_ptr, sc_grp_key=sc_grp_key)
+    if sc_grp_ptr is not None and sc_grp_ptr.numel() != (out_f + 63) // 64 * (in_f // 64) + 1:
+        raise ValueError("sc_grp_ptr must hold one pointer per (64-row group, 64-column step) "
+                         "plus the end (hxq_format.sidecar_row_groups)")
     L = lib()
     with torch.cuda.device(x.device):
         nbytes = L.hxq_prefill_gemm_workspace_bytes(m, out_f, in_f)

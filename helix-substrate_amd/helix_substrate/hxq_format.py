@@ -52,11 +52,13 @@ def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: to
                       codebook: torch.Tensor, group_scale: Optional[torch.Tensor] = None,
                       group_offset: Optional[torch.Tensor] = None,
                       group_size: int = 128, shape=None, recon_at=None) -> SidecarCSR:
-    """CSR over output rows from flat sidecar positions.
+    """CSR over output rows from flat sidecar positions, columns ascending
+    within a row.
 
-    Entries keep their stored order inside a row (stable sort), so a repeated
-    position resolves like the reader's ``flat[positions] = values`` (the last
-    one wins) when the dequant kernel replays them in order.
+    A repeated position keeps only its last stored value, as the reader's
+    ``flat[positions] = values`` resolves it (``hxq_reader_v3.py:118-133``):
+    every kernel then sees one entry per position, so replacement (dequant,
+    GEMM) and correction (GEMV: x[col] * (value - W_q)) agree.
     Raises ValueError on positions outside the matrix.
     """
     out_f, in_f = indices.shape if shape is None else shape
@@ -68,11 +70,15 @@ def build_sidecar_csr(positions: torch.Tensor, values: torch.Tensor, indices: to
         raise ValueError("sidecar position outside the weight matrix")
     if pos.numel() >= 2**31:
         raise ValueError("sidecar too large for int32 CSR")
-    rows = torch.div(pos, in_f, rounding_mode="floor")
-    order = torch.sort(rows, stable=True).indices
-    rows = rows[order]
-    cols = pos[order] - rows * in_f
+    order = torch.sort(pos, stable=True).indices
+    pos = pos[order]
     val = val[order]
+    if pos.numel() > 1:
+        last = torch.ones_like(pos, dtype=torch.bool)
+        last[:-1] = pos[1:] != pos[:-1]   # the last stored copy of each position
+        pos, val = pos[last], val[last]
+    rows = torch.div(pos, in_f, rounding_mode="floor")
+    cols = pos - rows * in_f
     counts = torch.bincount(rows, minlength=out_f)
     row_ptr = torch.zeros(out_f + 1, dtype=torch.int64, device=pos.device)
     row_ptr[1:] = torch.cumsum(counts, 0)
@@ -90,11 +96,14 @@ def sidecar_row_groups(rows: torch.Tensor, cols: torch.Tensor, val: torch.Tensor
                        in_f: int):
     """The prefill GEMM's sidecar order: for each group of 64 output rows, its
     entries sorted by column, then row (stable, so a repeated position keeps
-    its stored order and the last copy is applied last).
+    its stored order and the last copy is applied last), with a pointer per
+    64-column K step.
 
     rows / cols / val: the CSR arrays (rows ascending, stored order within a
-    row).  Returns (grp_ptr int32 [ceil(out/64) + 1], key int32 [nnz] holding
-    the uint32 (col << 6) | (row % 64), val fp32 [nnz]).
+    row).  Returns (step_ptr int32 [ceil(out/64) * ceil(in/64) + 1], key int32
+    [nnz] holding the uint32 (col << 6) | (row % 64), val fp32 [nnz]);
+    step_ptr[g * ceil(in/64) + t] is the first entry of group g whose column
+    lies in step t or later, and the last element is nnz.
     """
     if in_f >= 1 << 25:
         raise ValueError("in_features must be below 2^25 for the prefill sidecar keys")
@@ -104,8 +113,10 @@ def sidecar_row_groups(rows: torch.Tensor, cols: torch.Tensor, val: torch.Tensor
     key = (cols << 6) | (rows & 63)
     order = torch.sort(grp * (1 << 32) + key, stable=True).indices
     n_grp = (out_f + 63) // 64
-    counts = torch.bincount(grp, minlength=n_grp)
-    ptr = torch.zeros(n_grp + 1, dtype=torch.int64, device=rows.device)
+    n_steps = (in_f + 63) // 64
+    cell = grp * n_steps + torch.div(cols, 64, rounding_mode="floor")
+    counts = torch.bincount(cell, minlength=n_grp * n_steps)
+    ptr = torch.zeros(n_grp * n_steps + 1, dtype=torch.int64, device=rows.device)
     ptr[1:] = torch.cumsum(counts, 0)
     return (ptr.to(torch.int32).contiguous(), key[order].to(torch.int32).contiguous(),
             val[order].to(torch.float32).contiguous())

@@ -245,9 +245,11 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
  * or 12-bit packed indices, no affine) and 6-bit levels (affine, no
  * codebook).  The sidecar comes in the kernel's order: for each group of 64
  * output rows g (rows [64g, 64g + 64)), its entries sorted by column then row
- * (stable): sc_grp_ptr int32 [ceil(out/64) + 1], sc_grp_key uint32
- * (col << 6) | (row - 64g), sc_grp_val fp32 replacement values (NULL
- * sc_grp_ptr = no sidecar).  Shapes with few output tiles split K: a
+ * (stable): sc_grp_key uint32 (col << 6) | (row - 64g), sc_grp_val fp32
+ * replacement values, and sc_grp_ptr int32 [ceil(out/64) * (in/64) + 1]
+ * whose element g * (in/64) + t is the first entry of group g with a column
+ * in K step t ([64t, 64t + 64)) or later, the last element being the entry
+ * count (NULL sc_grp_ptr = no sidecar).  Shapes with few output tiles split K: a
  * workspace of hxq_prefill_gemm_workspace_bytes(...) bytes holds fp32
  * partials, reduced in order (deterministic).
  * Replaces: fused_vq_matmul's N > 1 path (triton_vq_matmul.py:249-334,

@@ -124,6 +124,31 @@ def test_gemm_dense_sidecar_rows(dev):
     _check(_gemm32(mod, x.to(dev)), x, _oracle_w(L))
 
 
+def test_prefill_sidecar_dense_block_and_repeats(dev):
+    """A 64 x 64 block fully in the sidecar (4096 entries in one row group and
+    K step: the per-step list overflows its 64-entry load), positions repeated
+    with new values (the last copy wins), under a K split."""
+    out_f, in_f, m = 256, 512, 96
+    L = synth.make_layer_np(out_f, in_f, seed=21, sidecar=False)
+    rs = np.random.RandomState(3)
+    blk = (np.arange(64, 128)[:, None] * in_f + np.arange(128, 192)[None, :]).ravel()
+    rnd = rs.choice(out_f * in_f, 130, replace=False)
+    rep = rs.choice(blk, 50, replace=False)
+    pos = np.concatenate([blk, rnd, rep]).astype(np.int64)
+    val = (rs.randn(pos.size) * 0.1).astype(np.float32)
+    L["sidecar_positions"], L["sidecar_values"] = pos, val
+    T = synth.to_torch(L)
+    mod = _module(T, dev)
+    W = _oracle_w(L)
+    assert np.array_equal(W.ravel()[rep], val[-50:])   # the last copy is the oracle's value
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    assert _hxq.lib().hxq_prefill_gemm_workspace_bytes(m, out_f, in_f) > 0   # K is split
+    _check(_gemm32(mod, x.to(dev)), x, W)
+    y = mod(x.to(dev))
+    assert mod._last_dispatch_path == "hip_gemm"
+    _check(y, x, W)
+
+
 def test_gemm_deterministic(dev):
     L, T = _layer(512, 1024, seed=13)
     mod = _module(T, dev)

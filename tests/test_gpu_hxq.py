@@ -68,6 +68,15 @@ def test_dequant_row_blocks_and_duplicates(dev):
     for r0, r1 in [(0, 300), (0, 1), (17, 133), (299, 300)]:
         blk = m._dequant_tile(r0, r1).cpu().numpy()
         np.testing.assert_array_equal(blk.view(np.uint32), W_ref[r0:r1].view(np.uint32))
+    # the GEMV's corrections and the prefill GEMM's replacements agree with it
+    x = torch.randn(2, 512, generator=torch.Generator().manual_seed(3))
+    y = m(x.to(dev))
+    assert m._last_dispatch_path == "hip_gemv"
+    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), W_ref)) <= 1e-5
+    xb = torch.randn(40, 512, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    yb = m(xb.to(dev))
+    assert m._last_dispatch_path == "hip_gemm"
+    assert _maxrel(yb.float().cpu().numpy(), oracle.linear_f64(xb.float().numpy(), W_ref)) <= 2e-2
 
 
 # ---------------------------------------------------------------------- GEMV

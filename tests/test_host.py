@@ -65,9 +65,13 @@ def test_csr_stable_for_unsorted_and_repeated_positions():
     pos = torch.tensor([40, 3, 40, 17], dtype=torch.int64)
     val = torch.tensor([1.0, 2.0, 3.0, 4.0])
     csr = build_sidecar_csr(pos, val, idx, cb)
-    assert csr.row_ptr.tolist() == [0, 1, 2, 4, 4]
-    assert csr.col.tolist() == [3, 1, 8, 8]
-    assert csr.val.tolist() == [2.0, 4.0, 1.0, 3.0]
+    # row-major order, one entry per position: the last stored value of 40 wins
+    assert csr.row_ptr.tolist() == [0, 1, 2, 3, 3]
+    assert csr.col.tolist() == [3, 1, 8]
+    assert csr.val.tolist() == [2.0, 4.0, 3.0]
+    pos2 = torch.tensor([9, 2, 9, 9, 5, 2], dtype=torch.int64)
+    csr2 = build_sidecar_csr(pos2, torch.arange(6, dtype=torch.float32), idx, cb)
+    assert csr2.col.tolist() == [2, 5, 9] and csr2.val.tolist() == [5.0, 4.0, 3.0]
     with pytest.raises(ValueError):
         build_sidecar_csr(torch.tensor([64]), torch.tensor([1.0]), idx, cb)
 
@@ -268,3 +272,8 @@ def test_sidecar_row_groups_order():
     assert ((k >> 6).tolist(), (k & 63).tolist()) == ([1, 3, 3, 3, 9, 2, 7, 0, 0],
                                                      [63, 0, 5, 5, 0, 0, 0, 2, 2])
     assert v.tolist() == [4.0, 1.0, 2.0, 3.0, 0.0, 6.0, 5.0, 7.0, 8.0]
+    # one pointer per (group, 64-column step): the first entry at that step or later
+    ptr, key, v = sidecar_row_groups(torch.tensor([0, 0, 0, 70]), torch.tensor([130, 10, 64, 199]),
+                                     torch.arange(4, dtype=torch.float32), out_f=100, in_f=200)
+    assert ptr.tolist() == [0, 1, 2, 3, 3, 3, 3, 3, 4]
+    assert (key.long() >> 6).tolist() == [10, 64, 130, 199] and v.tolist() == [1.0, 2.0, 0.0, 3.0]
