@@ -1,39 +1,42 @@
 // HXQ prefill GEMM, register-dequant design: Y[M, OUT] = X[M, K] @ W^T with
-// W held as uint8 codebook indices (+ per-group affine, + sidecar) and never
-// written anywhere in dense form.
+// W held in one of the HXQ index formats (uint8 or uint16 codebook indices,
+// uint16 or 12-bit pair-codebook indices, 6-bit affine levels; + per-group
+// affine, + sidecar) and never written anywhere in dense form.
 //
 // Replaces fused_vq_matmul's N > 1 path (helix_substrate/triton_vq_matmul.py:
 // 249-334 _vq_gather_matmul_tiled_kernel, 634-661 dispatch, 693-698 sidecar
-// scatter_add, 724-725 bias) and the default materialise-then-BLAS
+// scatter_add, 724-725 bias), the pair-codebook tiled kernel
+// (triton_vq2d_matmul.py:73-160) and the default materialise-then-BLAS
 // _forward_buffered (helix_linear.py:556-634).
 //
-// Block: 256 threads = 4 waves (one per SIMD), output tile BM x 256, K step
-// 64.  Wave w owns the 64 output columns [n0 + 64w, n0 + 64w + 64) for all
-// BM rows: (BM/32) x 2 accumulator tiles of v_mfma_f32_32x32x16_{bf16,f16}
-// (fp32, in AGPRs).  Per K step:
+// Block: 512 threads = 8 waves (two per SIMD), output tile BM x 256 (BM 256
+// or 128), K step 64.  Wave w owns the 32 output columns [n0 + 32w, +32) for
+// all BM rows: BM/32 accumulator tiles of v_mfma_f32_32x32x16_{bf16,f16}
+// (fp32).  Per K step:
 //   * A (X rows, 16-bit) is staged through LDS once per block and read by
-//     all four waves (rows XOR-swizzled in 16-byte chunks: conflict-free);
-//   * B (the wave's 64 W rows x 64 k) is dequantised straight into the MFMA
+//     all eight waves (16-byte chunks XOR-swizzled by (row / 2) % 8 for the
+//     64 banks: conflict-free);
+//   * B (the wave's 32 W rows x 64 k) is dequantised straight into the MFMA
 //     operand registers by the wave that uses it -- nothing of W goes to LDS
 //     and no wave waits on another for its weights.  The MFMA lane layout
 //     gives lane (c = lane % 32, h = lane / 32) the k range [8h, 8h+8) of a
 //     16-wide k substep; the kernel permutes k identically for A and B so
 //     that lane h of substep s covers physical k = 32h + 8s .. +8, i.e. a
-//     lane's B data for the whole step is the 32 contiguous index bytes
-//     [32h, 32h + 32) of its row (two 16-byte loads).  Lookups go to a
-//     codebook replicated 64x in LDS (lane l reads replica l: no bank
-//     conflicts; the byte address {0, 0, idx, 4l} is one v_perm_b32), then
-//     fma(c, scale, offset) and v_cvt_pk_bf16_f32;
-//   * B of step s+1 is built while the MFMAs of step s run (two operand
-//     buffers), global loads run two steps ahead, one barrier per step.
+//     lane's B data for the whole step is the contiguous index bytes of
+//     weights [32h, 32h + 32) of its row.  uint8 lookups go to a codebook
+//     replicated 64x in LDS (lane l reads replica l: no bank conflicts; the
+//     byte address {0, 0, idx, 4l} is one v_perm_b32); uint16 and pair
+//     codebooks are one 4096-entry table; 6-bit levels need none.  The
+//     affine is applied as fl(fl(c * scale) + offset) (two roundings, the
+//     reference's order), then v_cvt_pk_bf16_f32 / f16;
+//   * B of step s+1 is built while the MFMAs of step s run (substep by
+//     substep), global loads run two steps ahead, one barrier per step.
 // Sidecar: the entries of each group of 64 output rows are given sorted by
-// column (stable), so each wave walks one list with a wave-uniform cursor:
-// a window of 64 entries sits one per lane; the entries of a K step are the
-// window lanes whose column falls in the step (a ballot), and each is applied
-// by one indexed register write in its owning lane (v_readlane for the entry,
-// an SGPR-indexed move for the operand register) -- no per-lane cursors and
-// no divergent loops.  Later duplicates of a position come later in the list
-// and overwrite earlier ones (the reader's replace semantics).
+// column, with a pointer per K step.  Per step a wave loads the 64 entries
+// from its group's pointer, one per lane; those of the step and of its rows
+// are found by a ballot and each is applied by one indexed register write in
+// its owning lane (v_readlane for the entry, an SGPR-indexed move for the
+// operand register) -- no per-lane cursors and no divergent loops.
 // Results are written once per element (split-K: fp32 partials reduced in
 // order by a second kernel): deterministic.
 #include <algorithm>
