@@ -40,6 +40,7 @@
 // Results are written once per element (split-K: fp32 partials reduced in
 // order by a second kernel): deterministic.
 #include <algorithm>
+#include <type_traits>
 
 #include "hxq_common.h"
 
@@ -136,23 +137,33 @@ __host__ __device__ constexpr int fmt_b32(int f) {
     return f == HXQ_FMT_SCALAR_U16 ? 64 : (f == HXQ_FMT_VQ2_P12 || f == HXQ_FMT_AF6) ? 24 : 32;
 }
 
-template <int BM, bool BF16, bool AFFINE, int NJ, int FMT>
+// Activation types: XT 0 = fp16, 1 = bf16 (v_mfma_f32_32x32x16_{f16,bf16},
+// B packed as 16-bit pairs), 2 = fp32 (v_mfma_f32_32x32x2_f32, fp32 B: the
+// fp32 path keeps fp32 arithmetic end to end).
+template <int BM, int XT, bool AFFINE, int NJ, int FMT>
 __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const Args g) {
+    constexpr bool F32 = XT == 2;
+    constexpr bool BF16 = XT == 1;
+    static_assert(!F32 || (NJ == 1 && BM == 128), "fp32 activations: 128-row tiles, NJ = 1");
     constexpr int kThreads = kBN / (32 * NJ) * 64;
     constexpr int TM = BM / 32;           // accumulator tiles along M per wave
-    constexpr int XP = BM * 8 / kThreads; // 16-byte X chunks per thread per step
-    typedef typename BVec<NJ>::type BV;
+    constexpr int XB = F32 ? 4 : 2;       // bytes per X element
+    constexpr int XCH = kBK * XB / 16;    // 16-byte chunks per X row and step
+    constexpr int XP = BM * XCH / kThreads; // 16-byte X chunks per thread per step
+    // B operand registers: 16-bit pairs (16 per 32 columns) or fp32 (32)
+    typedef typename std::conditional<F32, u32x32, typename BVec<NJ>::type>::type BV;
     constexpr int B32 = fmt_b32(FMT);     // index bytes per lane, row and step
     constexpr int NQ = B32 == 64 ? 4 : 2; // 16-byte (12-byte for 24) index loads per row
     constexpr bool PAIR = FMT == HXQ_FMT_VQ2_U16 || FMT == HXQ_FMT_VQ2_P12;
     // uint8: 256 entries x 64 replicas; uint16 scalar: 4096 floats; pairs:
     // 4096 float2; 6-bit levels: no table (the region is sized for the largest)
     constexpr int kTblBytes = 256 * kNrep * 4;
-    constexpr int kABytes = BM * kBK * 2;
+    constexpr int kABytes = BM * kBK * XB;
     // the table first, so it sits at LDS address 0 (lookups need no base add)
     __shared__ __attribute__((aligned(16))) char smem[kTblBytes + 2 * kABytes];
     float *tbl = reinterpret_cast<float *>(smem);
     uint16_t *sA0 = reinterpret_cast<uint16_t *>(smem + kTblBytes);
+    float *sAf0 = reinterpret_cast<float *>(smem + kTblBytes);
 
     int tl, tx, ty;
     if (!tile_of(g, blockIdx.x, tl, tx, ty)) return;  // block-uniform
@@ -171,18 +182,18 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     if (lds_offset_of(tbl) != 0) return;  // never taken: no other LDS in this kernel
 
     // ---- global sources ----------------------------------------------------------
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.M * K * 2);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.M * K * XB);
     const int64_t row_bytes = (int64_t)K / 32 * B32;
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(g.idx, (int64_t)g.OUT * row_bytes);
     const int ngroups = AFFINE ? K / g.group : 1;
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(g.ga, AFFINE ? (int64_t)ngroups * g.OUT * 8 : 0);
-    // X: thread t copies chunk t % 8 of rows t / 8 + (threads / 8) p
-    const int xc = tid & 7;
+    // X: thread t copies chunk t % XCH of rows t / XCH + (threads / XCH) p
+    const int xc = tid % XCH;
     uint32_t x_off[XP];
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
-        const int r = r0 + (tid >> 3) + (kThreads / 8) * p;
-        x_off[p] = r < g.M ? static_cast<uint32_t>((r * K + xc * 8) * 2) : kOob;
+        const int r = r0 + tid / XCH + (kThreads / XCH) * p;
+        x_off[p] = r < g.M ? static_cast<uint32_t>((r * K + xc * (16 / XB)) * XB) : kOob;
     }
     // W rows of this lane: nw + 32j + ml
     uint32_t q_off[NJ];
@@ -239,7 +250,7 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
         const uint32_t k0 = static_cast<uint32_t>((kb + (live ? s : 0)) * kBK);
 #pragma unroll
         for (int p = 0; p < XP; ++p)
-            xv[buf][p] = buf_load16(xr, (x_off[p] == kOob || !live) ? kOob : x_off[p] + k0 * 2);
+            xv[buf][p] = buf_load16(xr, (x_off[p] == kOob || !live) ? kOob : x_off[p] + k0 * XB);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const uint32_t o = (q_off[j] == kOob || !live) ? kOob : q_off[j] + k0 / 32u * B32;
@@ -265,14 +276,24 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
         }
         load_entries(s, buf);
     };
-    // rows r and r + (threads / 8) p share the swizzle ((r / 2) % 8): one base
-    // address, the other rows at immediate offsets
-    const int x_lds = swz(tid >> 3, xc);
+    // rows r and r + (threads / XCH) p share the swizzle: one base address,
+    // the other rows at immediate offsets.  16-bit rows (128 B, 8 chunks):
+    // chunk ^ (r / 2) % 8; fp32 rows (256 B = the 64 banks, 16 chunks):
+    // chunk ^ r % 16, so 16 lanes reading one logical chunk of 16 rows hit
+    // 16 distinct chunks
+    const int x_lds = F32 ? (tid / XCH) * kBK + ((xc ^ ((tid / XCH) & 15)) << 2) : swz(tid >> 3, xc);
     auto store_x = [&](int buf) {
-        uint16_t *sA = sA0 + buf * (BM * kBK) + x_lds;
+        if constexpr (F32) {
+            float *sA = sAf0 + buf * (BM * kBK) + x_lds;
 #pragma unroll
-        for (int p = 0; p < XP; ++p)
-            *reinterpret_cast<u32x4 *>(sA + (kThreads / 8) * p * kBK) = xv[buf][p];
+            for (int p = 0; p < XP; ++p)
+                *reinterpret_cast<u32x4 *>(sA + (kThreads / XCH) * p * kBK) = xv[buf][p];
+        } else {
+            uint16_t *sA = sA0 + buf * (BM * kBK) + x_lds;
+#pragma unroll
+            for (int p = 0; p < XP; ++p)
+                *reinterpret_cast<u32x4 *>(sA + (kThreads / XCH) * p * kBK) = xv[buf][p];
+        }
     };
 
     // ---- lookup table ------------------------------------------------------------
@@ -370,6 +391,45 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             }
         }
     };
+    // fp32 B: b[w] holds weight w of the lane's 32 (row nw + ml); group q
+    // (weights 4q .. 4q+3) feeds MFMA substeps 4q .. 4q+3
+    auto dequant_f32 = [&](int buf, int q, BV &b) {
+        if constexpr (F32) {
+        const float sc = AFFINE ? av[buf][0].x : 1.f;
+        const float of = AFFINE ? av[buf][0].y : 0.f;
+        float v[4];
+        if constexpr (FMT == HXQ_FMT_SCALAR) {
+            const uint32_t w = qv[buf][q >> 2][q & 3];
+            v[0] = tbl_lookup0<kNrep, 0>(lane_off, w);
+            v[1] = tbl_lookup0<kNrep, 1>(lane_off, w);
+            v[2] = tbl_lookup0<kNrep, 2>(lane_off, w);
+            v[3] = tbl_lookup0<kNrep, 3>(lane_off, w);
+        } else if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t w = qv[buf][(2 * q + t) >> 2][(2 * q + t) & 3];
+                v[2 * t] = tbl[w & (kPairCodes - 1u)];
+                v[2 * t + 1] = tbl[(w >> 16) & (kPairCodes - 1u)];
+            }
+        } else if constexpr (FMT == HXQ_FMT_VQ2_U16) {
+            const float2 *t2 = reinterpret_cast<const float2 *>(tbl);
+            const uint32_t w = qv[buf][q >> 2][q & 3];
+            const float2 c0 = t2[w & (kPairCodes - 1u)];
+            const float2 c1 = t2[(w >> 16) & (kPairCodes - 1u)];
+            v[0] = c0.x; v[1] = c0.y; v[2] = c1.x; v[3] = c1.y;
+        } else if constexpr (FMT == HXQ_FMT_VQ2_P12) {
+            const float2 *t2 = reinterpret_cast<const float2 *>(tbl);
+            const float2 c0 = t2[field24(qv[buf][0], qv[buf][1], 24 * q, 12)];
+            const float2 c1 = t2[field24(qv[buf][0], qv[buf][1], 24 * q + 12, 12)];
+            v[0] = c0.x; v[1] = c0.y; v[2] = c1.x; v[3] = c1.y;
+        } else {  // 6-bit levels
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = static_cast<float>(field24(qv[buf][0], qv[buf][1], 24 * q + 6 * t, 6));
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[4 * q + t] = __float_as_uint(AFFINE ? affine_exact(v[t], sc, of) : v[t]);
+        }
+    };
     // Replace sidecar entries in b: the lanes set in m hold (key, value) pairs
     // of step columns [k1, k1 + 64) and this wave's rows.
     auto apply = [&](uint32_t key_v, float val_v, unsigned long long m, uint32_t k1, BV &b) {
@@ -381,12 +441,17 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             const uint32_t col = (key >> 6) - k1;  // 0..63
             const uint32_t row = (key & 63u) - rlo; // row within this wave
             const int owner = static_cast<int>((row & 31u) + 32u * (col >> 5));
-            const int reg = __builtin_amdgcn_readfirstlane(static_cast<int>(16u * (row >> 5) + ((col & 31u) >> 1)));
-            const uint32_t v16 = to16<BF16>(val);
-            const uint32_t hi = col & 1u;
-            const uint32_t old = b[reg];
-            const uint32_t upd = hi ? ((old & 0xffffu) | (v16 << 16)) : ((old & 0xffff0000u) | v16);
-            b[reg] = lane == owner ? upd : old;
+            if constexpr (F32) {
+                const int reg = __builtin_amdgcn_readfirstlane(static_cast<int>(col & 31u));
+                b[reg] = lane == owner ? __float_as_uint(val) : b[reg];
+            } else {
+                const int reg = __builtin_amdgcn_readfirstlane(static_cast<int>(16u * (row >> 5) + ((col & 31u) >> 1)));
+                const uint32_t v16 = to16<BF16>(val);
+                const uint32_t hi = col & 1u;
+                const uint32_t old = b[reg];
+                const uint32_t upd = hi ? ((old & 0xffffu) | (v16 << 16)) : ((old & 0xffff0000u) | v16);
+                b[reg] = lane == owner ? upd : old;
+            }
         }
     };
     // The sidecar entries of step s (buffer buf) into b.
@@ -424,6 +489,29 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     // share a swizzle: one base address per substep, rows at immediate offsets.
     const int a_sw = (ml >> 1) & 7;
     auto mfma_step = [&](int abuf, int qbuf, BV &b) {
+        if constexpr (F32) {
+            // 8 groups of 4 k substeps: one 16-byte A read per row tile (the 4
+            // k of the group), 4 MFMAs per row tile, then B(k+1) of the group
+            const float *sA = sAf0 + abuf * (BM * kBK) + ml * kBK;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float *as = sA + (((8 * hh + q) ^ (ml & 15)) << 2);
+                float4 a[TM];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const float4 *>(as + 32 * i * kBK);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float bv = __uint_as_float(b[4 * q + e]);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const float av_ = e == 0 ? a[i].x : e == 1 ? a[i].y : e == 2 ? a[i].z : a[i].w;
+                        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av_, bv, acc[i][0], 0, 0, 0);
+                    }
+                }
+                if (qbuf >= 0) dequant_f32(qbuf, q, b);
+            }
+            return;
+        }
         const uint16_t *sA = sA0 + abuf * (BM * kBK) + ml * kBK;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -460,8 +548,13 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     store_x(0);                 // waits for X(0)
     __syncthreads();            // table and A(0) visible
     BV b;
+    if constexpr (F32) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) dequant_sub(0, s, b);  // B(0)
+        for (int q = 0; q < 8; ++q) dequant_f32(0, q, b);  // B(0)
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) dequant_sub(0, s, b);  // B(0)
+    }
     patch(0, 0, b);
     load_step(2, 0);
     int ks = 0;
@@ -672,8 +765,8 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
     HXQ_REQUIRE(format >= HXQ_FMT_SCALAR && format <= HXQ_FMT_SCALAR_U16, "unknown index format");
     HXQ_REQUIRE(x && indices && y && (codebook || format == HXQ_FMT_AF6),
                 "x, indices, codebook and y are required");
-    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16,
-                "the MFMA GEMM takes bf16 or fp16 activations (fp32 goes through hxq_gemv)");
+    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16 || x_dtype == HXQ_F32,
+                "x_dtype must be fp32, bf16 or fp16");
     HXQ_REQUIRE(format == HXQ_FMT_SCALAR || format == HXQ_FMT_AF6 ||
                     (n_codes >= 1 && n_codes <= kPairCodes),
                 "uint16 and pair codebooks need 1..4096 entries");
@@ -684,7 +777,7 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
     HXQ_REQUIRE(m_rows > 0 && out_features > 0 && in_features > 0, "empty problem");
     HXQ_REQUIRE(in_features % pg::kBK == 0, "in_features must be a multiple of 64");
     HXQ_REQUIRE(in_features < (int64_t{1} << 26), "in_features must be below 2^26");
-    HXQ_REQUIRE(m_rows * in_features * 2 < (int64_t{1} << 31) &&
+    HXQ_REQUIRE(m_rows * in_features * (x_dtype == HXQ_F32 ? 4 : 2) < (int64_t{1} << 31) &&
                     out_features * (in_features / 32 * pg::fmt_b32(format)) < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
     HXQ_REQUIRE(!group_affine || (group_size >= pg::kBK && group_size % pg::kBK == 0 &&
@@ -699,9 +792,11 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
                 "x and indices must be 16-byte aligned");
     // uint16 scalar indices with the affine need more registers than the
     // 256-row tile leaves: 128-row tiles
+    // fp32 activations: 128-row tiles (the fp32 A tile doubles the LDS)
     const bool u16_aff = format == HXQ_FMT_SCALAR_U16 && group_affine != nullptr;
+    const bool f32 = x_dtype == HXQ_F32;
     const pg::Plan p = pg::plan(m_rows, out_features, in_features, device_cu_count(),
-                                u16_aff ? 128 : 256);
+                                (u16_aff || f32) ? 128 : 256);
     pg::Args a{};
     a.x = static_cast<const uint16_t *>(x);
     a.idx = indices;
@@ -758,9 +853,11 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
             default: HXQ_PG_LAUNCH(BM_, BF_, true, HXQ_FMT_AF6); break;                        \
         }
         if (p.bm == 256) {
-            if (bf16) { HXQ_PG_FMT(256, true) } else { HXQ_PG_FMT(256, false) }
+            if (bf16) { HXQ_PG_FMT(256, 1) } else { HXQ_PG_FMT(256, 0) }
+        } else if (f32) {
+            HXQ_PG_FMT(128, 2)
         } else {
-            if (bf16) { HXQ_PG_FMT(128, true) } else { HXQ_PG_FMT(128, false) }
+            if (bf16) { HXQ_PG_FMT(128, 1) } else { HXQ_PG_FMT(128, 0) }
         }
 #undef HXQ_PG_FMT
 #undef HXQ_PG_LAUNCH

@@ -420,7 +420,8 @@ def gemm(x, indices, codebook, group_affine, group_size, sc_row_ptr, sc_col, sc_
 def prefill_gemm(x, indices, codebook, group_affine, group_size, sc_grp_ptr, sc_grp_key,
                  sc_grp_val, bias=None, out_dtype=None, out=None, fmt=None, out_features=None):
     """Y = X @ W^T (+bias) on MFMA with W dequantised into the operand registers
-    (hxq_prefill_gemm).  X bf16/fp16 [M, K]; group_affine [K/G, OUT, 2] or None;
+    (hxq_prefill_gemm).  X fp32/bf16/fp16 [M, K] (fp32: fp32 MFMA, fp32 W);
+    group_affine [K/G, OUT, 2] or None;
     sidecar in the row-group order of ``hxq_format.sidecar_row_groups`` (step
     pointers, keys, values).
     fmt: FMT_* (default: uint8 scalar, indices [OUT, K]); other formats pass

@@ -12,9 +12,9 @@ Same entry points as the reference module
   out_features, in_features, group_size, bias)`` -- 6-bit levels packed four
   per 3 bytes (``index_packing.pack_6bit``): the GEMV's HXQ_FMT_AF6 decode for
   <= 4 rows (the reference supports one row); above that the MFMA prefill GEMM
-  decoding the 6-bit levels into its operand registers (bf16/fp16 activations,
-  in_features and group_size multiples of 64), else HIP dequantisation of row
-  tiles into a library GEMM.
+  decoding the 6-bit levels into its operand registers (in_features and
+  group_size multiples of 64), else HIP dequantisation of row tiles into a
+  library GEMM.
 * ``affine_group_matmul_reference`` -- the plain torch formula.
 
 Scales/offsets may be fp16 (the reference's storage) or fp32; they are used
@@ -88,7 +88,7 @@ def fused_affine_group_matmul_packed6(x, packed_indices, scales, offsets, out_fe
         return _hxq.gemv_fmt(x2, _hxq.FMT_AF6, packed_indices, out_features, group_scale=s,
                              group_offset=o, group_size=group_size, bias=b)
     y = torch.empty(n, out_features, dtype=torch.float32, device=x.device)
-    if x2.dtype != torch.float32 and in_features % 64 == 0 and group_size % 64 == 0:
+    if in_features % 64 == 0 and group_size % 64 == 0:
         # {scale, offset} in the GEMM's per-K-group layout [K/G, OUT, 2]
         aff = torch.stack([s.t(), o.t()], dim=-1).contiguous()
         return _hxq.prefill_gemm(x2, packed_indices, None, aff, group_size, None, None, None,

@@ -414,8 +414,9 @@ class HelixLinear(nn.Module):
         out = torch.empty(n, self.out_features, dtype=out_dtype, device=x2.device)
         if n == 0:
             pass
-        elif n > _GEMV_MAX_ROWS and x2.dtype in (torch.bfloat16, torch.float16) and self._gemm_ok:
+        elif n > _GEMV_MAX_ROWS and self._gemm_ok:
             # every index format: W dequantised into the MFMA operand registers
+            # (bf16/fp16 MFMA for 16-bit activations, fp32 MFMA for fp32 ones)
             self._last_dispatch_path = "hip_gemm"
             grp = rp is not None
             scalar8 = self._fmt == _hxq.FMT_SCALAR
@@ -434,7 +435,8 @@ class HelixLinear(nn.Module):
                           self.group_offset, self.group_size, rp, col, delta, self.bias,
                           out=out[r0:r1])
         else:
-            # fp32 activations keep fp32 arithmetic: GEMV over groups of 4 rows
+            # in_features not a multiple of 64 (or a group size the GEMM does not
+            # step): GEMV over groups of 4 rows, fp32 arithmetic
             self._last_dispatch_path = "hip_gemv_rows"
             for r0, r1 in self._gemv_row_groups(n):
                 _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
@@ -453,8 +455,8 @@ class HelixLinear(nn.Module):
 
     def _forward_hip_fmt(self, x2, rp, col, delta, out) -> None:
         """Pair codebooks and int16-index scalar codebooks: the format GEMV for up to
-        4 rows; above that (fp32 activations, or in_features not a multiple of 64)
-        dequantised row tiles and the library GEMM."""
+        4 rows; above that (in_features not a multiple of 64, which the prefill
+        GEMM does not take) dequantised row tiles and the library GEMM."""
         n = x2.shape[0]
         if n <= _GEMV_MAX_ROWS:
             self._last_dispatch_path = "hip_gemv_fmt"

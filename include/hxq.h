@@ -238,8 +238,9 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
 
 /*
  * hxq_prefill_gemm: the prefill GEMM Y = X W^T (+ bias) with W dequantised
- * straight into the MFMA operand registers (bf16/fp16 X [m_rows, in],
- * fp32 accumulation, y in y_dtype; in_features % 64 == 0; affine as for
+ * straight into the MFMA operand registers (X [m_rows, in] in bf16 or fp16:
+ * 16-bit MFMA on W rounded to X's type; or fp32: fp32 MFMA on the exact fp32
+ * W; fp32 accumulation, y in y_dtype; in_features % 64 == 0; affine as for
  * hxq_gemm), for every index format (HXQ_FMT_*): uint8 with the 256-entry
  * codebook, uint16 with n_codes entries, pair codebooks [n_codes, 2] (uint16
  * or 12-bit packed indices, no affine) and 6-bit levels (affine, no

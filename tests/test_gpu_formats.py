@@ -115,7 +115,7 @@ def test_pair_helix_linear_device(dev, packed):
     print(f"pair HelixLinear packed={packed}", flush=True)
     for n, dt, tol, path in [(1, torch.float32, 1e-5, "hip_gemv_fmt"),
                              (4, torch.bfloat16, 2e-2, "hip_gemv_fmt"),
-                             (37, torch.float32, 1e-5, "hip_dequant_gemm"),
+                             (37, torch.float32, 1e-5, "hip_gemm"),
                              (64, torch.bfloat16, 2e-2, "hip_gemm"),
                              (300, torch.float16, 2e-2, "hip_gemm")]:
         x = torch.from_numpy(rs.randn(n, inp).astype(np.float32)).to(dt)
@@ -167,10 +167,11 @@ def _grp(dev, pos, val, out, inp):
 @pytest.mark.parametrize("m,out,inp,G", [(300, 1000, 1024, 128),   # ragged M/OUT, split K
                                          (1024, 2048, 2048, 64),
                                          (5, 256, 11008, 128)])    # one row tile, long K
-@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
 def test_prefill_fmt_matches_oracle(dev, fmt, m, out, inp, G, xdt):
-    """Against the oracle's W: the 2e-2 bar in fp64, and 2e-5 against W rounded
-    to the activation type (all that is left is fp32 accumulation order)."""
+    """Against the oracle's W: 16-bit activations at the 2e-2 bar in fp64 and
+    at 2e-5 against W rounded to the activation type (all that is left is
+    fp32 accumulation order); fp32 activations at 1e-5 against the exact W."""
     if fmt == _hxq.FMT_SCALAR_U16:
         mod, W = _wide_layer(out, inp, 3000, seed=m + out, group_size=G)
         raw, cb, aff = mod.indices, mod.codebook, mod._affine_t
@@ -189,6 +190,9 @@ def test_prefill_fmt_matches_oracle(dev, fmt, m, out, inp, G, xdt):
                           out_dtype=torch.float32, fmt=fmt, out_features=out)
     y = y.cpu().numpy()
     xf = x.float().numpy()
+    if xdt == torch.float32:
+        assert _maxrel(y, oracle.linear_np(xf, W, bias.numpy())) <= 1e-5
+        return
     assert _maxrel(y, oracle.linear_np(xf, W, bias.numpy())) <= 2e-2
     W16 = torch.from_numpy(W).to(xdt).float().numpy()
     rel = _maxrel(y, oracle.linear_np(xf, W16, bias.numpy()))

@@ -156,13 +156,39 @@ def test_gemm_deterministic(dev):
     assert torch.equal(mod(x), mod(x))
 
 
-def test_fp32_prefill_stays_fp32(dev):
-    L, T = _layer(256, 512, seed=14)
-    mod = _module(T, dev)
-    x = torch.randn(9, 512, generator=torch.Generator().manual_seed(7))
+@pytest.mark.parametrize("m,out_f,in_f,density", [
+    (9, 256, 512, 0.001),       # few rows: one row tile, K split
+    (300, 640, 1536, 0.001),    # ragged M and OUT tiles
+    (40, 128, 512, 0.05),       # dense sidecar rows (the per-step list overflows)
+    (1024, 1024, 2048, 0.001),  # several row tiles, no split
+])
+def test_fp32_prefill_gemm_matches_oracle(dev, m, out_f, in_f, density):
+    """fp32 activations with more than 4 rows: one fp32-MFMA launch on the
+    exact fp32 W (no 16-bit rounding anywhere), 1e-5 against the fp64 oracle."""
+    print(f"fp32 prefill m={m} out={out_f} in={in_f}", flush=True)
+    L, T = _layer(out_f, in_f, seed=14 + m, density=density)
+    bias = torch.linspace(-1, 1, out_f)
+    mod = _module(T, dev, bias=bias)
+    W = _oracle_w(L)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(7))
     y = mod(x.to(dev))
-    assert mod._last_dispatch_path == "hip_gemv_rows"
-    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= 1e-5
+    assert mod._last_dispatch_path == "hip_gemm" and y.dtype == torch.float32
+    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), W, bias.numpy())) <= 1e-5
+    assert torch.equal(mod(x.to(dev)), y)   # deterministic (ordered split-K reduce)
+
+
+def test_fp32_prefill_config2_gate_up_rows(dev):
+    """The config-2 gate/up shape with fp32 activations (M = 256): a row slice
+    against the fp64 oracle at 1e-5."""
+    m, out_f, in_f = 256, 18944, 3584
+    L, T = _layer(out_f, in_f, seed=31, sigma=0.015)
+    mod = _module(T, dev)
+    x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(3))
+    y = mod(x.to(dev))
+    assert mod._last_dispatch_path == "hip_gemm"
+    rows = _row_slice(m)
+    ref = oracle.linear_np(x[rows].numpy(), _oracle_w(L))
+    assert _maxrel(y[rows].cpu().numpy(), ref) <= 1e-5
 
 
 def test_affine_pack_layout(dev):
