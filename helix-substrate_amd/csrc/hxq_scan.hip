@@ -246,6 +246,390 @@ static int launch_chunks(const ScanArgs &a, hipStream_t stream) {
     return HXQ_OK;
 }
 
+// ---------------------------------------------------------------------------
+// SSD (state-space dual) form on bf16 MFMA, for bf16 x, B and C.
+//
+// One block per (batch b, head h) walks the sequence in chunks of kQ = 64
+// tokens with the state S (P x N, fp32) in MFMA accumulators.  With cs_t the
+// inclusive prefix sum of A*dt over the chunk (fp64) and S the state at the
+// chunk's start, per chunk:
+//   y_t      = sum_{s<=t} exp(cs_t - cs_s) dt_s (C_t . B_s) x_s
+//              + exp(cs_t) (C_t . S) + D x_t
+//   S_next   = exp(cs_Q) S + sum_s exp(cs_Q - cs_s) dt_s x_s (x) B_s
+// which is the recurrence h_t = exp(A dt_t) h_{t-1} + dt_t x_t B_t of the
+// sequential scan unrolled over the chunk (mamba_scan_chunked.py:89-213 uses
+// the same intra/inter-chunk split).  The four contractions run on
+// v_mfma_f32_32x32x16_bf16:
+//   (a) CB^T = B C^T         [s, t] over n    (bf16 x bf16: exact products)
+//   (b) M  = CB o exp(cs_t - cs_s) dt_s, lower triangle, split M = Mh + Ml
+//       into two bf16 (16 mantissa bits kept; x is bf16 and exact)
+//   (c) Y  = M x              [t, p] over s    (Mh x + Ml x)
+//   (d) Z  = C S^T            [t, p] over n    (S split Sh + Sl)
+//   (e) S^T = exp(cs_Q) S^T + B^T X'  [n, p] over s, X' = exp(cs_Q - cs_s) dt_s x_s
+//       split X'h + X'l
+// (a) and (e) produce transposed tiles so that each lane holds 4 consecutive
+// elements of an LDS row (8-byte stores of M and S).
+// so every product is exact or carries a 2^-17 relative split error, with
+// fp32 accumulation: well inside the scan's 1e-4 bar.  Operands are staged
+// in LDS with k contiguous per row (C, B: n; B^T, x^T, M, X': s), 16-byte
+// chunks XOR-swizzled by row so the 16 lanes of a read hit distinct banks.
+// Block: 4 waves; wave w owns output tile (t-tile w/2, p-tile w%2) of (c)/(d),
+// tile (s-tile w%2, t-tile w/2) of (a) (none above the diagonal) and state
+// tiles (p-tile w%2, n-tiles of (e)).
+// Shapes: head_dim <= 64 (padded to 64), state <= 128 (padded to 32 NT);
+// other shapes and other dtypes use the VALU recurrence above.
+namespace ssd {
+
+constexpr int kQ = 64;        // tokens per internal chunk
+constexpr int kPP = 64;       // padded head_dim
+constexpr int kThreads = 256; // 4 waves
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element offset of 16-byte chunk c in row r of an LDS matrix of bf16 rows
+// with CPR 16-byte chunks (rows of 16 CPR bytes): the chunk is XORed with the
+// row's position among the rows that share the 64 banks.
+template <int CPR>
+__device__ __forceinline__ int sw(int r, int c) {
+    return r * CPR * 8 + ((c ^ ((r * CPR / 16) % CPR)) << 3);
+}
+
+__device__ __forceinline__ u32x4 lds16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// two fp32 -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// (a, b) -> packed bf16 hi and lo pairs with hi + lo = value to 16 mantissa bits
+__device__ __forceinline__ void split2x2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    hi = pk_bf16(a, b);
+    lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
+// 2^x (v_exp_f32)
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int NT>  // state tiles of 32 (NP = 32 NT)
+__global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
+    constexpr int NP = 32 * NT;
+    constexpr int CN = NP / 8;   // 16-byte chunks per row of n
+    constexpr int CQ = kQ / 8;   // ... per row of s (8)
+    __shared__ __attribute__((aligned(16))) uint16_t sC[kQ * NP];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[kQ * NP];
+    __shared__ __attribute__((aligned(16))) uint16_t sBt[NP * kQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sXt[kPP * kQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sM[2][kQ * kQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sXp[2][kPP * kQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sS[2][kPP * NP];
+    __shared__ double scs[kQ];
+    __shared__ float sdt[kQ], swt[kQ];
+    __shared__ __attribute__((aligned(16))) float sec[kQ];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ml = lane & 31, hh = lane >> 5;
+    const int b = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const int H = a.heads, P = a.head_dim, N = a.state, L = a.seqlen;
+    const int g = h / (H / a.ngroups);
+    const float Ah = a.A[h];
+    const float Dh = a.D ? a.D[h] : 0.f;
+    const uint16_t *xg = static_cast<const uint16_t *>(a.x);
+    const uint16_t *Bg = static_cast<const uint16_t *>(a.Bm);
+    const uint16_t *Cg = static_cast<const uint16_t *>(a.Cm);
+    const int ti = wave >> 1, pj = wave & 1;  // (c)/(d) output tile
+    // (e) state tiles: 2 p-tiles x NT n-tiles over the 4 waves: wave w takes
+    // p-tile w % 2 and n-tiles [nj0, nj0 + nst) (NT = 1: waves 2, 3 hold none)
+    const int pi = wave & 1;
+    const int nst = NT == 4 ? 2 : 1;
+    const int nj0 = NT == 4 ? 2 * (wave >> 1) : (wave >> 1);
+    const bool has_s = NT >= 2 || wave < 2;
+    // y through a buffer resource (fixed store count, masked pieces dropped)
+    const int64_t y_bytes = (int64_t)a.batch * L * H * P * (a.y_dt == HXQ_F32 ? 4 : 2);
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, y_bytes);
+    constexpr uint32_t kYOob = 0xfffffff0u;
+
+    // ---- chunk inputs: global -> registers (prefetch) -> LDS ------------------
+    // B, C: token pair u = item / CN (tokens 2u, 2u+1), n chunk item % CN
+    constexpr int BC_ITEMS = (kQ / 2) * CN;           // per matrix
+    constexpr int BC_PER = (BC_ITEMS + kThreads - 1) / kThreads;
+    u32x4 rB[BC_PER][2], rC[BC_PER][2];
+    u32x4 rX[2];  // x: token pair tid / 8, p chunk tid % 8 (256 items)
+    float rdt = 0.f;  // wave 0: dt of token lane
+    auto load_chunk = [&](int t0) {
+        if (wave == 0) {
+            const int t = t0 + lane;
+            rdt = t < L ? ld_any(a.dt, ((int64_t)b * L + t) * H + h, a.dt_dt) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < BC_PER; ++i) {
+            const int item = tid + kThreads * i;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int t = t0 + 2 * (item / CN) + e, c = item % CN;
+                const bool ok = item < BC_ITEMS && t < L && 8 * c < N;
+                const int64_t o = (((int64_t)b * L + t) * a.ngroups + g) * N + 8 * c;
+                rB[i][e] = ok ? *reinterpret_cast<const u32x4 *>(Bg + o) : u32x4{0u, 0u, 0u, 0u};
+                rC[i][e] = ok ? *reinterpret_cast<const u32x4 *>(Cg + o) : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = t0 + 2 * (tid >> 3) + e, c = tid & 7;
+            const bool ok = t < L && 8 * c < P;
+            const int64_t o = (((int64_t)b * L + t) * H + h) * P + 8 * c;
+            rX[e] = ok ? *reinterpret_cast<const u32x4 *>(xg + o) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    // the two tokens' 16-bit values of element k as one dword (token 2u low)
+    auto pair_of = [](const u32x4 &v0, const u32x4 &v1, int k) -> uint32_t {
+        const uint32_t a0 = (v0[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+        const uint32_t a1 = (v1[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+        return a0 | (a1 << 16);
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (int i = 0; i < BC_PER; ++i) {
+            const int item = tid + kThreads * i;
+            if (item >= BC_ITEMS) continue;
+            const int u = item / CN, c = item % CN;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                *reinterpret_cast<u32x4 *>(sB + sw<CN>(2 * u + e, c)) = rB[i][e];
+                *reinterpret_cast<u32x4 *>(sC + sw<CN>(2 * u + e, c)) = rC[i][e];
+            }
+            // B^T rows n = 8c + k, columns 2u, 2u+1
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                *reinterpret_cast<uint32_t *>(sBt + sw<CQ>(8 * c + k, u >> 2) + 2 * (u & 3)) =
+                    pair_of(rB[i][0], rB[i][1], k);
+        }
+        const int u = tid >> 3, c = tid & 7;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            *reinterpret_cast<uint32_t *>(sXt + sw<CQ>(8 * c + k, u >> 2) + 2 * (u & 3)) =
+                pair_of(rX[0], rX[1], k);
+    };
+
+    // ---- state ----------------------------------------------------------------
+    // S^T tiles: Sacc[j][r] = S[p = 32 pi + ml][n = 32(nj0 + j) + 8(r/4) + 4hh + r%4]
+    const int sp = 32 * pi + ml;
+    f32x16 Sacc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int n = 32 * (nj0 + j) + 8 * (r >> 2) + 4 * hh + (r & 3);
+            Sacc[j][r] = (a.h0 && has_s && j < nst && sp < P && n < N)
+                             ? a.h0[(((int64_t)b * H + h) * P + sp) * N + n] : 0.f;
+        }
+    // S -> sS (hi, lo): rows p, n contiguous; 4 consecutive n per 8-byte store
+    auto store_state = [&]() {
+        if (!has_s) return;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (j >= nst) break;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = 32 * (nj0 + j) + 8 * q + 4 * hh;
+                uint32_t h01, l01, h23, l23;
+                split2x2(Sacc[j][4 * q], Sacc[j][4 * q + 1], h01, l01);
+                split2x2(Sacc[j][4 * q + 2], Sacc[j][4 * q + 3], h23, l23);
+                const int o = sw<CN>(sp, n >> 3) + (n & 7);
+                *reinterpret_cast<uint2 *>(sS[0] + o) = make_uint2(h01, h23);
+                *reinterpret_cast<uint2 *>(sS[1] + o) = make_uint2(l01, l23);
+            }
+        }
+    };
+
+    const int nch = (L + kQ - 1) / kQ;
+    load_chunk(0);
+    store_state();
+    for (int ch = 0; ch < nch; ++ch) {
+        const int t0 = ch * kQ;
+        lds_barrier();  // the previous chunk's readers of the inputs are done
+        store_chunk();
+        const float dtv = rdt;  // this chunk's dt (wave 0), before the prefetch replaces it
+        if (ch + 1 < nch) load_chunk(t0 + kQ);
+        if (wave == 0) {
+            // cumulative log2 decay (fp64: differences of nearby prefixes stay
+            // exact; exponentials as 2^x)
+            double cs = static_cast<double>(Ah * dtv);
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(cs, off, 64);
+                if (lane >= off) cs += o;
+            }
+            cs *= 1.4426950408889634;  // log2(e)
+            const double csq = __shfl(cs, 63, 64);
+            scs[lane] = cs;
+            sdt[lane] = dtv;
+            swt[lane] = exp2_fast(static_cast<float>(csq - cs)) * dtv;
+            sec[lane] = exp2_fast(static_cast<float>(cs));
+        }
+        lds_barrier();
+
+        // (a) CB^T tile (s-tile si, t-tile ti) and (b) M; s-tile 1 of t-tile 0
+        // lies above the diagonal
+        const int si = pj;
+        if (!(ti == 0 && si == 1)) {
+            f32x16 cb;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cb[r] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < NP / 16; ++ks) {
+                const u32x4 bv = lds16(sB + sw<CN>(32 * si + ml, 2 * ks + hh));
+                const u32x4 cv = lds16(sC + sw<CN>(32 * ti + ml, 2 * ks + hh));
+                cb = mfma(bv, cv, cb);
+            }
+            // lane: t = 32 ti + ml; cb[r]: s = 32 si + 8(r/4) + 4hh + r%4
+            const int t = 32 * ti + ml;
+            const double cst = scs[t];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int s0 = 32 * si + 8 * q + 4 * hh;
+                float m[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int s = s0 + e;
+                    m[e] = s <= t ? cb[4 * q + e] * exp2_fast(static_cast<float>(cst - scs[s])) * sdt[s] : 0.f;
+                }
+                uint32_t h01, l01, h23, l23;
+                split2x2(m[0], m[1], h01, l01);
+                split2x2(m[2], m[3], h23, l23);
+                const int o = sw<CQ>(t, s0 >> 3) + (s0 & 7);
+                *reinterpret_cast<uint2 *>(sM[0] + o) = make_uint2(h01, h23);
+                *reinterpret_cast<uint2 *>(sM[1] + o) = make_uint2(l01, l23);
+            }
+        }
+        // X'[p][s] = w_s x[s][p], split; two tokens per dword
+#pragma unroll
+        for (int i = 0; i < (kPP * kQ / 2) / kThreads; ++i) {
+            const int d = tid + kThreads * i;          // dword index
+            const int p = d / (kQ / 2), u = d % (kQ / 2);
+            const int o = sw<CQ>(p, u >> 2) + 2 * (u & 3);
+            const uint32_t xx = *reinterpret_cast<const uint32_t *>(sXt + o);
+            uint32_t hi, lo;
+            split2x2(__uint_as_float(xx << 16) * swt[2 * u], __uint_as_float(xx & 0xffff0000u) * swt[2 * u + 1],
+                     hi, lo);
+            *reinterpret_cast<uint32_t *>(sXp[0] + o) = hi;
+            *reinterpret_cast<uint32_t *>(sXp[1] + o) = lo;
+        }
+        lds_barrier();
+
+        // (c) Y^T = x^T M^T over s <= end of t-tile ti; (d) Z^T = S C^T over n.
+        // Transposed tiles: lane (t = 32 ti + ml) holds 4 consecutive p per
+        // row group, stored as one 16-byte (fp32 y) or 8-byte (16-bit y) piece.
+        {
+            f32x16 yv, zv;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) yv[r] = zv[r] = 0.f;
+            for (int ks = 0; ks < 2 * (ti + 1); ++ks) {
+                const u32x4 xa = lds16(sXt + sw<CQ>(32 * pj + ml, 2 * ks + hh));
+                yv = mfma(xa, lds16(sM[0] + sw<CQ>(32 * ti + ml, 2 * ks + hh)), yv);
+                yv = mfma(xa, lds16(sM[1] + sw<CQ>(32 * ti + ml, 2 * ks + hh)), yv);
+            }
+#pragma unroll
+            for (int ks = 0; ks < NP / 16; ++ks) {
+                const u32x4 cv = lds16(sC + sw<CN>(32 * ti + ml, 2 * ks + hh));
+                zv = mfma(lds16(sS[0] + sw<CN>(32 * pj + ml, 2 * ks + hh)), cv, zv);
+                zv = mfma(lds16(sS[1] + sw<CN>(32 * pj + ml, 2 * ks + hh)), cv, zv);
+            }
+            const int t = 32 * ti + ml;
+            const float et = sec[t];
+            const bool t_ok = t0 + t < L;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int p0 = 32 * pj + 8 * q + 4 * hh;  // p0 .. p0 + 3
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xv = bf16_to_f32(sXt[sw<CQ>(p0 + e, t >> 3) + (t & 7)]);
+                    v[e] = yv[4 * q + e] + et * zv[4 * q + e] + Dh * xv;
+                }
+                // every lane stores (masked pieces go past the buffer's range), so
+                // the store count per chunk is fixed and loads are never made to
+                // wait behind stores of unknown number
+                const bool ok = t_ok && p0 < P;
+                const uint32_t yo = static_cast<uint32_t>((((int64_t)b * L + t0 + t) * H + h) * P + p0);
+                if (a.y_dt == HXQ_F32) {
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                              __float_as_uint(v[3])},
+                        yr, ok ? yo * 4u : kYOob, 0, 0);
+                } else {
+                    u32x2 w;
+                    if (a.y_dt == HXQ_BF16) {
+                        w = u32x2{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
+                    } else {
+                        w = u32x2{uint32_t(f32_to_f16(v[0])) | (uint32_t(f32_to_f16(v[1])) << 16),
+                                  uint32_t(f32_to_f16(v[2])) | (uint32_t(f32_to_f16(v[3])) << 16)};
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b64(w, yr, ok ? yo * 2u : kYOob, 0, 0);
+                }
+            }
+        }
+        lds_barrier();  // (d) has read sS
+
+        // (e) S = exp(cs_Q) S + X'^T B
+        if (has_s) {
+            const float eq = exp2_fast(static_cast<float>(scs[kQ - 1]));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (j >= nst) break;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) Sacc[j][r] *= eq;
+#pragma unroll
+                for (int ks = 0; ks < kQ / 16; ++ks) {
+                    const u32x4 bt = lds16(sBt + sw<CQ>(32 * (nj0 + j) + ml, 2 * ks + hh));
+                    Sacc[j] = mfma(bt, lds16(sXp[0] + sw<CQ>(sp, 2 * ks + hh)), Sacc[j]);
+                    Sacc[j] = mfma(bt, lds16(sXp[1] + sw<CQ>(sp, 2 * ks + hh)), Sacc[j]);
+                }
+            }
+        }
+        store_state();
+    }
+    if (a.h_final && has_s) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (j >= nst) break;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int n = 32 * (nj0 + j) + 8 * (r >> 2) + 4 * hh + (r & 3);
+                if (sp < P && n < N) a.h_final[(((int64_t)b * H + h) * P + sp) * N + n] = Sacc[j][r];
+            }
+        }
+    }
+}
+
+}  // namespace ssd
+
+// The SSD kernel's shapes and dtypes: bf16 x/B/C, head_dim <= 64, state <= 128.
+static bool ssd_eligible(const ScanArgs &a) {
+    const int64_t y_bytes = (int64_t)a.batch * a.seqlen * a.heads * a.head_dim * (a.y_dt == HXQ_F32 ? 4 : 2);
+    return a.x_dt == HXQ_BF16 && a.bc_dt == HXQ_BF16 && a.head_dim <= ssd::kPP && a.state <= 128 &&
+           a.head_dim % 8 == 0 && a.state % 8 == 0 && y_bytes < (int64_t{1} << 31);
+}
+
+static int launch_ssd(const ScanArgs &a, hipStream_t stream) {
+    const dim3 grid(a.batch * a.heads);
+    if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
+    else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
+    else hipLaunchKernelGGL(ssd::ssd_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
+}
+
 static int valid_dtype(int32_t d) { return d == HXQ_F32 || d == HXQ_BF16 || d == HXQ_F16; }
 
 }  // namespace hxq
@@ -287,6 +671,9 @@ extern "C" int hxq_ssm_chunk_scan(const void *x, int32_t x_dtype, const void *dt
     a.chunk = (int32_t)chunk;
     a.nchunks = (int32_t)((seqlen + chunk - 1) / chunk);
     a.x_dt = x_dtype; a.dt_dt = dt_dtype; a.bc_dt = bc_dtype; a.y_dt = y_dtype;
+    // bf16 x/B/C with head_dim <= 64 and state <= 128: the SSD form on MFMA
+    // (no workspace); otherwise the three-pass VALU recurrence
+    if (ssd_eligible(a)) return launch_ssd(a, stream);
     const uintptr_t wsp = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
     a.ws_state = reinterpret_cast<float *>(wsp);
     a.ws_decay = a.ws_state + (int64_t)a.nchunks * batch * heads * head_dim * state;

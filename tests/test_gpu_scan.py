@@ -111,3 +111,44 @@ def test_scan_config3_full_size_slices(dev):
                                      D[hi:hi + 1].cpu().numpy())
         assert _maxrel(y[bi:bi + 1, :, hi:hi + 1].cpu().numpy(), yr) <= TOL
         assert _maxrel(hf[bi:bi + 1, hi:hi + 1].cpu().numpy(), hr) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# bf16 x/B/C (head_dim <= 64, state <= 128): the SSD form on MFMA
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("b,L,H,P,N,G,h0", [
+    (2, 300, 8, 64, 128, 1, True),    # config-3 head and state sizes, ragged last chunk
+    (1, 64, 4, 64, 128, 2, False),    # exactly one internal chunk
+    (1, 65, 4, 64, 64, 4, True),      # one token into the second chunk; B/C per head
+    (2, 1, 4, 64, 128, 1, True),      # a single token
+    (1, 200, 8, 32, 32, 2, True),     # narrow head and state
+    (1, 130, 4, 48, 16, 1, True),     # padded head_dim (48 of 64) and state (16 of 32)
+    (1, 257, 2, 64, 128, 1, False),   # 4 full internal chunks and one token
+])
+def test_ssd_bf16_matches_oracle(dev, b, L, H, P, N, G, h0):
+    print(f"ssd b={b} L={L} H={H} P={P} N={N} G={G} h0={h0}", flush=True)
+    args = _inputs(b, L, H, P, N, G, seed=L + N + P, dtype=torch.bfloat16, h0=h0)
+    _run_and_check(dev, *args, 256)
+
+
+def test_ssd_agrees_with_recurrence_path(dev):
+    """The same bf16-representable values through the SSD kernel (bf16 tensors)
+    and through the VALU recurrence (the same values as fp32 tensors)."""
+    x, dt, A, B, C, D, hs = _inputs(2, 333, 8, 64, 128, 2, seed=41, dtype=torch.bfloat16)
+    d = lambda t: t.to(dev)
+    y1, h1 = msc.chunked_scan(d(hs), d(dt), d(A), d(x), d(B), d(C), d(D), chunk_size=128)
+    y2, h2 = msc.chunked_scan(d(hs), d(dt), d(A), d(x.float()), d(B.float()), d(C.float()), d(D),
+                              chunk_size=128)
+    assert _maxrel(y1.cpu().numpy(), y2.cpu().double().numpy()) <= TOL
+    assert _maxrel(h1.cpu().numpy(), h2.cpu().double().numpy()) <= TOL
+
+
+def test_ssd_strong_and_weak_decay(dev):
+    """A spans exp(-8)..exp(3) per token step (decay from barely any to total
+    within a step) and dt reaches 3: the fp64 log-decay prefix keeps
+    exp(cs_t - cs_s) exact where the decay is strong."""
+    b, L, H, P, N = 1, 400, 8, 64, 64
+    x, dt, A, B, C, D, hs = _inputs(b, L, H, P, N, 1, seed=5, dtype=torch.bfloat16)
+    A = -torch.exp(torch.linspace(-8.0, 3.0, H))
+    dt = dt * torch.linspace(0.1, 20.0, L)[None, :, None]
+    _run_and_check(dev, x, dt, A, B, C, D, hs, 256)
