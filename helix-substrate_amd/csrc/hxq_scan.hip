@@ -298,6 +298,14 @@ __device__ __forceinline__ int sw(int r, int c) {
     return r * CPR * 8 + ((c ^ ((r * CPR / 16) % CPR)) << 3);
 }
 
+// Rows of kQ = 64 bf16 (s contiguous: B^T, x^T, M, X'): 8 chunks, XOR with
+// ((r / 2) ^ (r / 8)) % 8 -- 16 consecutive rows read one logical chunk from
+// 16 distinct bank groups, and the transposing stores (rows 8c + k for 16
+// values of c) hit 8 distinct groups.
+__device__ __forceinline__ int swq(int r, int c) {
+    return r * 64 + ((c ^ (((r >> 1) ^ (r >> 3)) & 7)) << 3);
+}
+
 __device__ __forceinline__ u32x4 lds16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
 __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
@@ -323,7 +331,6 @@ template <int NT>  // state tiles of 32 (NP = 32 NT)
 __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
     constexpr int NP = 32 * NT;
     constexpr int CN = NP / 8;   // 16-byte chunks per row of n
-    constexpr int CQ = kQ / 8;   // ... per row of s (8)
     __shared__ __attribute__((aligned(16))) uint16_t sC[kQ * NP];
     __shared__ __attribute__((aligned(16))) uint16_t sB[kQ * NP];
     __shared__ __attribute__((aligned(16))) uint16_t sBt[NP * kQ];
@@ -331,9 +338,11 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sM[2][kQ * kQ];
     __shared__ __attribute__((aligned(16))) uint16_t sXp[2][kPP * kQ];
     __shared__ __attribute__((aligned(16))) uint16_t sS[2][kPP * NP];
-    __shared__ double scs[kQ];
-    __shared__ float sdt[kQ], swt[kQ];
-    __shared__ __attribute__((aligned(16))) float sec[kQ];
+    // per-token decay terms of a chunk, double buffered (the next chunk's are
+    // computed while this one runs)
+    __shared__ double scs2[2][kQ];
+    __shared__ float sdt2[2][kQ], swt2[2][kQ];
+    __shared__ __attribute__((aligned(16))) float sec2[2][kQ];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -344,9 +353,6 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
     const int g = h / (H / a.ngroups);
     const float Ah = a.A[h];
     const float Dh = a.D ? a.D[h] : 0.f;
-    const uint16_t *xg = static_cast<const uint16_t *>(a.x);
-    const uint16_t *Bg = static_cast<const uint16_t *>(a.Bm);
-    const uint16_t *Cg = static_cast<const uint16_t *>(a.Cm);
     const int ti = wave >> 1, pj = wave & 1;  // (c)/(d) output tile
     // (e) state tiles: 2 p-tiles x NT n-tiles over the 4 waves: wave w takes
     // p-tile w % 2 and n-tiles [nj0, nj0 + nst) (NT = 1: waves 2, 3 hold none)
@@ -360,17 +366,20 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
     constexpr uint32_t kYOob = 0xfffffff0u;
 
     // ---- chunk inputs: global -> registers (prefetch) -> LDS ------------------
+    // Buffer loads with masked pieces sent past the range: every lane issues
+    // the same loads, so wait counts stay exact across the chunk loop.
+    constexpr uint32_t kOob = 0xfffffff0u;
+    const int dtb = a.dt_dt == HXQ_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (int64_t)a.batch * L * H * P * 2);
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.Bm, (int64_t)a.batch * L * a.ngroups * N * 2);
+    const __amdgpu_buffer_rsrc_t cr = make_rsrc(a.Cm, (int64_t)a.batch * L * a.ngroups * N * 2);
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(a.dt, (int64_t)a.batch * L * H * dtb);
     // B, C: token pair u = item / CN (tokens 2u, 2u+1), n chunk item % CN
     constexpr int BC_ITEMS = (kQ / 2) * CN;           // per matrix
     constexpr int BC_PER = (BC_ITEMS + kThreads - 1) / kThreads;
     u32x4 rB[BC_PER][2], rC[BC_PER][2];
     u32x4 rX[2];  // x: token pair tid / 8, p chunk tid % 8 (256 items)
-    float rdt = 0.f;  // wave 0: dt of token lane
     auto load_chunk = [&](int t0) {
-        if (wave == 0) {
-            const int t = t0 + lane;
-            rdt = t < L ? ld_any(a.dt, ((int64_t)b * L + t) * H + h, a.dt_dt) : 0.f;
-        }
 #pragma unroll
         for (int i = 0; i < BC_PER; ++i) {
             const int item = tid + kThreads * i;
@@ -378,18 +387,44 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
             for (int e = 0; e < 2; ++e) {
                 const int t = t0 + 2 * (item / CN) + e, c = item % CN;
                 const bool ok = item < BC_ITEMS && t < L && 8 * c < N;
-                const int64_t o = (((int64_t)b * L + t) * a.ngroups + g) * N + 8 * c;
-                rB[i][e] = ok ? *reinterpret_cast<const u32x4 *>(Bg + o) : u32x4{0u, 0u, 0u, 0u};
-                rC[i][e] = ok ? *reinterpret_cast<const u32x4 *>(Cg + o) : u32x4{0u, 0u, 0u, 0u};
+                const uint32_t o = ok ? static_cast<uint32_t>(((((int64_t)b * L + t) * a.ngroups + g) * N + 8 * c) * 2) : kOob;
+                rB[i][e] = buf_load16(br, o);
+                rC[i][e] = buf_load16(cr, o);
             }
         }
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int t = t0 + 2 * (tid >> 3) + e, c = tid & 7;
             const bool ok = t < L && 8 * c < P;
-            const int64_t o = (((int64_t)b * L + t) * H + h) * P + 8 * c;
-            rX[e] = ok ? *reinterpret_cast<const u32x4 *>(xg + o) : u32x4{0u, 0u, 0u, 0u};
+            rX[e] = buf_load16(xr, ok ? static_cast<uint32_t>(((((int64_t)b * L + t) * H + h) * P + 8 * c) * 2) : kOob);
         }
+    };
+    // dt of token t0 + lane (raw bits; every wave loads it)
+    auto load_dt = [&](int t0) -> uint32_t {
+        const int t = t0 + lane;
+        const uint32_t o = t < L ? static_cast<uint32_t>((((int64_t)b * L + t) * H + h) * dtb) : kOob;
+        return dtb == 4 ? __builtin_amdgcn_raw_buffer_load_b32(dr, o, 0, 0)
+                        : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(dr, o, 0, 0));
+    };
+    auto dt_value = [&](uint32_t raw) -> float {
+        return a.dt_dt == HXQ_F32 ? __uint_as_float(raw)
+             : a.dt_dt == HXQ_BF16 ? bf16_to_f32(static_cast<uint16_t>(raw)) : f16_to_f32(static_cast<uint16_t>(raw));
+    };
+    // the decay terms of a chunk from its dt (one wave): log2-decay prefix in
+    // fp64 (differences of nearby prefixes stay exact), exponentials as 2^x
+    auto decay_terms = [&](float dtv, int buf) {
+        double cs = static_cast<double>(Ah * dtv);
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double o = __shfl_up(cs, off, 64);
+            if (lane >= off) cs += o;
+        }
+        cs *= 1.4426950408889634;  // log2(e)
+        const double csq = __shfl(cs, 63, 64);
+        scs2[buf][lane] = cs;
+        sdt2[buf][lane] = dtv;
+        swt2[buf][lane] = exp2_fast(static_cast<float>(csq - cs)) * dtv;
+        sec2[buf][lane] = exp2_fast(static_cast<float>(cs));
     };
     // the two tokens' 16-bit values of element k as one dword (token 2u low)
     auto pair_of = [](const u32x4 &v0, const u32x4 &v1, int k) -> uint32_t {
@@ -411,13 +446,13 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
             // B^T rows n = 8c + k, columns 2u, 2u+1
 #pragma unroll
             for (int k = 0; k < 8; ++k)
-                *reinterpret_cast<uint32_t *>(sBt + sw<CQ>(8 * c + k, u >> 2) + 2 * (u & 3)) =
+                *reinterpret_cast<uint32_t *>(sBt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
                     pair_of(rB[i][0], rB[i][1], k);
         }
         const int u = tid >> 3, c = tid & 7;
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-            *reinterpret_cast<uint32_t *>(sXt + sw<CQ>(8 * c + k, u >> 2) + 2 * (u & 3)) =
+            *reinterpret_cast<uint32_t *>(sXt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
                 pair_of(rX[0], rX[1], k);
     };
 
@@ -454,30 +489,24 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
 
     const int nch = (L + kQ - 1) / kQ;
     load_chunk(0);
+    uint32_t rdt = load_dt(0);
+    if (wave == 1) decay_terms(dt_value(rdt), 0);
+    rdt = load_dt(kQ);  // dt of chunk 1
     store_state();
     for (int ch = 0; ch < nch; ++ch) {
         const int t0 = ch * kQ;
+        const int db = ch & 1;
+        double *scs = scs2[db];
+        float *sdt = sdt2[db], *swt = swt2[db], *sec = sec2[db];
         lds_barrier();  // the previous chunk's readers of the inputs are done
         store_chunk();
-        const float dtv = rdt;  // this chunk's dt (wave 0), before the prefetch replaces it
         if (ch + 1 < nch) load_chunk(t0 + kQ);
-        if (wave == 0) {
-            // cumulative log2 decay (fp64: differences of nearby prefixes stay
-            // exact; exponentials as 2^x)
-            double cs = static_cast<double>(Ah * dtv);
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const double o = __shfl_up(cs, off, 64);
-                if (lane >= off) cs += o;
-            }
-            cs *= 1.4426950408889634;  // log2(e)
-            const double csq = __shfl(cs, 63, 64);
-            scs[lane] = cs;
-            sdt[lane] = dtv;
-            swt[lane] = exp2_fast(static_cast<float>(csq - cs)) * dtv;
-            sec[lane] = exp2_fast(static_cast<float>(cs));
-        }
         lds_barrier();
+        // wave 1 (no CB tile) prepares the next chunk's decay terms meanwhile
+        if (wave == 1 && ch + 1 < nch) {
+            decay_terms(dt_value(rdt), db ^ 1);
+            rdt = load_dt(t0 + 2 * kQ);
+        }
 
         // (a) CB^T tile (s-tile si, t-tile ti) and (b) M; s-tile 1 of t-tile 0
         // lies above the diagonal
@@ -507,7 +536,7 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
                 uint32_t h01, l01, h23, l23;
                 split2x2(m[0], m[1], h01, l01);
                 split2x2(m[2], m[3], h23, l23);
-                const int o = sw<CQ>(t, s0 >> 3) + (s0 & 7);
+                const int o = swq(t, s0 >> 3) + (s0 & 7);
                 *reinterpret_cast<uint2 *>(sM[0] + o) = make_uint2(h01, h23);
                 *reinterpret_cast<uint2 *>(sM[1] + o) = make_uint2(l01, l23);
             }
@@ -517,7 +546,7 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
         for (int i = 0; i < (kPP * kQ / 2) / kThreads; ++i) {
             const int d = tid + kThreads * i;          // dword index
             const int p = d / (kQ / 2), u = d % (kQ / 2);
-            const int o = sw<CQ>(p, u >> 2) + 2 * (u & 3);
+            const int o = swq(p, u >> 2) + 2 * (u & 3);
             const uint32_t xx = *reinterpret_cast<const uint32_t *>(sXt + o);
             uint32_t hi, lo;
             split2x2(__uint_as_float(xx << 16) * swt[2 * u], __uint_as_float(xx & 0xffff0000u) * swt[2 * u + 1],
@@ -535,9 +564,9 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) yv[r] = zv[r] = 0.f;
             for (int ks = 0; ks < 2 * (ti + 1); ++ks) {
-                const u32x4 xa = lds16(sXt + sw<CQ>(32 * pj + ml, 2 * ks + hh));
-                yv = mfma(xa, lds16(sM[0] + sw<CQ>(32 * ti + ml, 2 * ks + hh)), yv);
-                yv = mfma(xa, lds16(sM[1] + sw<CQ>(32 * ti + ml, 2 * ks + hh)), yv);
+                const u32x4 xa = lds16(sXt + swq(32 * pj + ml, 2 * ks + hh));
+                yv = mfma(xa, lds16(sM[0] + swq(32 * ti + ml, 2 * ks + hh)), yv);
+                yv = mfma(xa, lds16(sM[1] + swq(32 * ti + ml, 2 * ks + hh)), yv);
             }
 #pragma unroll
             for (int ks = 0; ks < NP / 16; ++ks) {
@@ -554,7 +583,7 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float xv = bf16_to_f32(sXt[sw<CQ>(p0 + e, t >> 3) + (t & 7)]);
+                    const float xv = bf16_to_f32(sXt[swq(p0 + e, t >> 3) + (t & 7)]);
                     v[e] = yv[4 * q + e] + et * zv[4 * q + e] + Dh * xv;
                 }
                 // every lane stores (masked pieces go past the buffer's range), so
@@ -591,9 +620,9 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
                 for (int r = 0; r < 16; ++r) Sacc[j][r] *= eq;
 #pragma unroll
                 for (int ks = 0; ks < kQ / 16; ++ks) {
-                    const u32x4 bt = lds16(sBt + sw<CQ>(32 * (nj0 + j) + ml, 2 * ks + hh));
-                    Sacc[j] = mfma(bt, lds16(sXp[0] + sw<CQ>(sp, 2 * ks + hh)), Sacc[j]);
-                    Sacc[j] = mfma(bt, lds16(sXp[1] + sw<CQ>(sp, 2 * ks + hh)), Sacc[j]);
+                    const u32x4 bt = lds16(sBt + swq(32 * (nj0 + j) + ml, 2 * ks + hh));
+                    Sacc[j] = mfma(bt, lds16(sXp[0] + swq(sp, 2 * ks + hh)), Sacc[j]);
+                    Sacc[j] = mfma(bt, lds16(sXp[1] + swq(sp, 2 * ks + hh)), Sacc[j]);
                 }
             }
         }
@@ -617,8 +646,10 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
 // The SSD kernel's shapes and dtypes: bf16 x/B/C, head_dim <= 64, state <= 128.
 static bool ssd_eligible(const ScanArgs &a) {
     const int64_t y_bytes = (int64_t)a.batch * a.seqlen * a.heads * a.head_dim * (a.y_dt == HXQ_F32 ? 4 : 2);
+    const int64_t bc_bytes = (int64_t)a.batch * a.seqlen * a.ngroups * a.state * 2;
     return a.x_dt == HXQ_BF16 && a.bc_dt == HXQ_BF16 && a.head_dim <= ssd::kPP && a.state <= 128 &&
-           a.head_dim % 8 == 0 && a.state % 8 == 0 && y_bytes < (int64_t{1} << 31);
+           a.head_dim % 8 == 0 && a.state % 8 == 0 && y_bytes < (int64_t{1} << 31) &&
+           bc_bytes < (int64_t{1} << 31);
 }
 
 static int launch_ssd(const ScanArgs &a, hipStream_t stream) {
