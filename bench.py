@@ -314,6 +314,35 @@ def read_traffic():
     return None
 
 
+def steady_ms(fn, dev, iters=10, warm_ms=60.0, min_ms=60.0):
+    """Average ms per call of fn in steady state: the GPU's clocks ramp up over
+    the first tens of milliseconds of sustained work, so warm up by time, then
+    time at least `iters` calls and at least min_ms of them (HIP events on
+    torch's current stream, where the library launches)."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    n_warm = 0
+    while (time.perf_counter() - t0) * 1e3 < warm_ms or n_warm < 3:
+        fn()
+        n_warm += 1
+        if n_warm % 8 == 0:
+            torch.cuda.synchronize(dev)
+    torch.cuda.synchronize(dev)
+    per = (time.perf_counter() - t0) * 1e3 / n_warm
+    n = max(iters, int(min_ms / max(per, 1e-3)) + 1)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(n):
+        fn()
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    return ev0.elapsed_time(ev1) / n
+
+
 def prefill_bench(dev, ms_tokens=(512, 2048, 8192), iters=10, cpu_seconds=15.0):
     """Config 2: HXQ prefill GEMM (W dequantised into the MFMA operand
     registers, bf16 MFMA, fp32 accumulation) at the Qwen2.5-7B shapes, M
@@ -332,31 +361,8 @@ def prefill_bench(dev, ms_tokens=(512, 2048, 8192), iters=10, cpu_seconds=15.0):
     per_layer = {"q": 2, "kv": 2, "gate_up": 2, "down": 1}
     out = {"m_tokens": list(ms_tokens), "peak_tflops_bf16": 2500.0,
            "layer": "2 q + 2 kv + 2 gate_up + down (one Qwen2.5-7B layer's projections)"}
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-
-    def timed(fn, warm_ms=60.0, min_ms=60.0):
-        # steady state: the GPU's clocks ramp up over the first tens of
-        # milliseconds of sustained work, so warm up by time, then time at
-        # least `iters` calls and at least min_ms of them
-        fn()
-        torch.cuda.synchronize(dev)
-        t0 = time.perf_counter()
-        n_warm = 0
-        while (time.perf_counter() - t0) * 1e3 < warm_ms or n_warm < 3:
-            fn()
-            n_warm += 1
-            if n_warm % 8 == 0:
-                torch.cuda.synchronize(dev)
-        torch.cuda.synchronize(dev)
-        per = (time.perf_counter() - t0) * 1e3 / n_warm
-        n = max(iters, int(min_ms / max(per, 1e-3)) + 1)
-        ev0.record()
-        for _ in range(n):
-            fn()
-        ev1.record()
-        torch.cuda.synchronize(dev)
-        return ev0.elapsed_time(ev1) / n
+    def timed(fn):
+        return steady_ms(fn, dev, iters)
 
     mods = {}
     for k, (name, (o, i)) in enumerate(shapes.items()):
@@ -525,25 +531,29 @@ def scan_bench(dev, iters=5, cpu=True):
     Bm = (torch.randn(b, L, 1, N, device=dev, generator=g) / math.sqrt(N)).to(torch.bfloat16)
     Cm = (torch.randn(b, L, 1, N, device=dev, generator=g) / math.sqrt(N)).to(torch.bfloat16)
     D = torch.rand(H, device=dev, generator=g) + 0.5
-    for _ in range(2):
-        y, hf = msc.chunked_scan(None, dt, A, x, Bm, Cm, D, chunk_size=256)
-    torch.cuda.synchronize(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(iters):
-        y, hf = msc.chunked_scan(None, dt, A, x, Bm, Cm, D, chunk_size=256)
-    ev1.record()
-    torch.cuda.synchronize(dev)
-    ms = ev0.elapsed_time(ev1) / iters
+    res = {}
+
+    def run():
+        res["y"], res["hf"] = msc.chunked_scan(None, dt, A, x, Bm, Cm, D, chunk_size=256)
+
+    ms = steady_ms(run, dev, iters)
+    y, hf = res["y"], res["hf"]
     states = b * L * H * P * N
     flops = 5.0 * states  # recurrence form: h = a*h + (dt x) B (3), y += h C (2)
     nbytes = (x.numel() * 2 + dt.numel() * 4 + Bm.numel() * 2 + Cm.numel() * 2 + y.numel() * 4
               + hf.numel() * 4 + 2 * H * 4)
+    # The bf16 inputs run the SSD form on MFMA: per (batch, head) and 64-token
+    # chunk, 176 v_mfma_f32_32x32x16_bf16 (C B^T 24, M x 24 with the hi/lo
+    # split and causal tiles, C S^T 64, state update 64) of 32768 FLOP each
+    mfma_flop = 176 * 32768.0 * b * H * ((L + 63) // 64)
     out = {"shape": {"batch": b, "seqlen": L, "heads": H, "head_dim": P, "state": N,
                      "ngroups": 1, "chunk": 256},
+           "kernel": "ssd_kernel<4> (SSD chunk form, bf16 MFMA, fp32 state)",
            "ms": round(ms, 4), "gflop_recurrence": round(flops / 1e9, 2),
            "tflops": round(flops / ms / 1e9, 2),
+           "mfma_gflop_executed": round(mfma_flop / 1e9, 2),
+           "mfma_tflops": round(mfma_flop / ms / 1e9, 1),
+           "frac_of_bf16_mfma_peak": round(mfma_flop / ms / 1e9 / 2500.0, 4),
            # VALU fp32 without packed math (packed fp32 is not used on this
            # pool): 78.6 TFLOP/s; the 157.3 figure is the packed/MFMA one
            "frac_of_fp32_valu_peak_78": round(flops / ms / 1e9 / 78.6, 4),
@@ -690,15 +700,7 @@ def mixer_bench(dev, iters=5):
     b, L = 8, 2048
     hs = torch.randn(b, L, dm, device=dev).to(torch.bfloat16)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
-    for _ in range(2):
-        out = m(hs)
-    torch.cuda.synchronize(dev)
-    ev[0].record()
-    for _ in range(iters):
-        out = m(hs)
-    ev[1].record()
-    torch.cuda.synchronize(dev)
-    ms = ev[0].elapsed_time(ev[1]) / iters
+    ms = steady_ms(lambda: m(hs), dev, iters)
     # stage split (one pass, events between stages)
     ev[0].record()
     proj = m.in_proj(hs)
@@ -751,15 +753,7 @@ def moe_bench(dev, n_layers=16, iters=3, cpu=True):
         return r
 
     r = step()
-    torch.cuda.synchronize(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(iters):
-        step()
-    ev1.record()
-    torch.cuda.synchronize(dev)
-    ms = ev0.elapsed_time(ev1) / iters
+    ms = steady_ms(step, dev, iters)
     touched = int((r.expert_counts > 0).sum())
     per_expert = 3 * (I * Hd + I * Hd // 128 * 8 + int(round(0.001 * I * Hd)) * 8) + \
         4 * (2 * (I + 1) + Hd + 1) + 3 * 1024
