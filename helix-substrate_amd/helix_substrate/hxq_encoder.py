@@ -169,12 +169,13 @@ def fit_group_affine(w, indices, codebook, group_size=128, exclude_positions=Non
 
 
 @functools.lru_cache(maxsize=2)
-def _seeding_stream(n, n_clusters, device):
+def _seeding_stream(n, n_clusters):
     """The RandomState(42) draws of the k-means++ seeding for n rows.  They do
     not depend on the data: randint(n), then per weighted draw a 100000-row
     choice without replacement (n > 100000) and the one uniform double that
     choice(len, p=...) consumes, then the uniform rows past 64.  Replayed once
-    per (n, n_clusters) and kept (host and device copies of the row sets)."""
+    per (n, n_clusters) and kept on the host only (the caller stages the row
+    sets to the device for the duration of one seeding)."""
     rs = np.random.RandomState(42)
     first = int(rs.randint(n))
     n_draw = min(n_clusters, 64)
@@ -183,10 +184,8 @@ def _seeding_stream(n, n_clusters, device):
         rows_h.append(rs.choice(n, 100000, replace=False) if n > 100000 else None)
         us.append(float(rs.random_sample()))
     tail = rs.choice(n, n_clusters - 64, replace=False) if n_clusters > 64 else None
-    rows_d = None
-    if n > 100000 and rows_h:
-        rows_d = torch.from_numpy(np.stack(rows_h)).to(device)
-    return first, rows_h, rows_d, us, tail
+    rows_all = np.stack(rows_h) if n > 100000 and rows_h else None
+    return first, rows_h, rows_all, us, tail
 
 
 def _weighted_draw(p, u):
@@ -217,7 +216,9 @@ def kmeanspp_init(data, n_clusters):
     numpy does.  Returns the seeds as a host fp32 [n_clusters, 2] array."""
     host = data.cpu().numpy()
     n = host.shape[0]
-    first, rows_h, rows_d, us, tail = _seeding_stream(n, n_clusters, str(data.device))
+    first, rows_h, rows_all, us, tail = _seeding_stream(n, n_clusters)
+    # device copy of the subsample rows for this seeding only (freed on return)
+    rows_d = None if rows_all is None else torch.from_numpy(rows_all).to(data.device)
     seeds = np.zeros((n_clusters, 2), dtype=np.float32)
     seeds[0] = host[first]
     n_draw = min(n_clusters, 64)
