@@ -91,3 +91,52 @@ def test_mixer_prefill_and_steps_match_oracle(dev):
     for t in range(64, 70):
         o = m.step(hs[:, t].to(dev).to(torch.bfloat16), st)
         assert _rel(o.float().cpu().numpy(), ref[:, t]) <= 2e-2, t
+
+
+@pytest.mark.parametrize("W,L,pdt", [(4, 37, torch.bfloat16), (2, 16, torch.float16),
+                                     (3, 5, torch.bfloat16), (1, 20, torch.bfloat16)])
+def test_conv_split_16bit_vector_path(dev, W, L, pdt):
+    """16-bit proj and outputs with channel counts and offsets multiples of 8 take the
+    8-channel vector kernel; it must equal the scalar kernel (fp32 proj holding the same
+    values) rounded once to the 16-bit type, conv state and dt included."""
+    b, I, G, N, H, d_mlp = 2, 256, 2, 64, 8, 8
+    cd = I + 2 * G * N
+    pw = 2 * d_mlp + 2 * I + 2 * G * N + H
+    g = torch.Generator().manual_seed(W * 10 + L)
+    proj = torch.randn(b, L, pw, generator=g).to(pdt)
+    w = (torch.randn(cd, W, generator=g) * 0.5).to(dev)
+    cb = (torch.randn(cd, generator=g) * 0.1).to(dev)
+    dtb = torch.randn(H, generator=g).to(dev)
+    print(f"conv_split vector W={W} L={L} {pdt}", flush=True)
+    cs16 = torch.full((b, cd, W), float("nan"), device=dev)
+    cs32 = torch.full((b, cd, W), float("nan"), device=dev)
+    x, B, C, dt = _hxq.mamba2_conv_split(proj.to(dev), w, cb, dtb, 1e-3, float("inf"), d_mlp, I,
+                                         G, N, H, conv_state=cs16)
+    assert x.dtype == pdt
+    xr, Br, Cr, dtr = _hxq.mamba2_conv_split(proj.float().to(dev), w, cb, dtb, 1e-3, float("inf"),
+                                             d_mlp, I, G, N, H, out_dtype=torch.float32,
+                                             conv_state=cs32)
+    for got, ref in ((x, xr), (B, Br), (C, Cr)):
+        assert torch.equal(got, ref.to(pdt))
+    assert torch.equal(dt, dtr)
+    assert torch.equal(cs16, cs32)
+
+
+@pytest.mark.parametrize("width,ydt,odt", [(4096, torch.float32, torch.bfloat16),
+                                           (2048, torch.bfloat16, torch.float32),
+                                           (8192, torch.float32, torch.float32)])
+def test_gated_rmsnorm_register_path(dev, width, ydt, odt):
+    """Rows of 2048/4096/8192 (one group) take the register kernel; against the oracle
+    (1e-5 for fp32 outputs, one bf16 rounding otherwise)."""
+    rows, stride = 40, width + 512
+    g = torch.Generator().manual_seed(width)
+    y = torch.randn(rows, width, generator=g).to(ydt)
+    proj = torch.randn(rows, stride, generator=g).to(torch.bfloat16)
+    w = torch.randn(width, generator=g)
+    print(f"gated rmsnorm width={width} y={ydt} out={odt}", flush=True)
+    out = _hxq.gated_rmsnorm(y.to(dev), proj.to(dev)[:, 256:256 + width], w.to(dev), 1e-5,
+                             out_dtype=odt)
+    ref = oracle.gated_rmsnorm_np(y.float().numpy(), proj[:, 256:256 + width].float().numpy(),
+                                  w.numpy(), 1e-5)
+    assert out.dtype == odt
+    assert _rel(out.float().cpu().numpy(), ref) <= (1e-5 if odt == torch.float32 else 8e-3)
