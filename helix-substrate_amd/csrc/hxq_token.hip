@@ -97,22 +97,23 @@ struct Mat {
     int64_t out;
 };
 
-// A matrix descriptor read from the layer table into scalar registers (the
-// table lives in ordinary device memory, which the compiler cannot prove
-// read-only, so it would otherwise keep every field in vector registers).
-__device__ __forceinline__ Mat umat(const Mat &m) {
-    Mat r;
-    r.idx = uptr(m.idx);
-    r.cb = uptr(m.cb);
-    r.gs = uptr(m.gs);
-    r.go = uptr(m.go);
-    r.rp = uptr(m.rp);
-    r.col = uptr(m.col);
-    r.delta = uptr(m.delta);
-    r.bias = uptr(m.bias);
-    r.out = static_cast<int64_t>(ufl64(static_cast<uint64_t>(m.out)));
-    return r;
+// Reads a value of the launch's tables (plan, layers), which the host
+// writes before the launch and nothing changes during it, with scalar loads
+// through the constant address space: the fields land in scalar registers,
+// and the loads count in lgkmcnt only -- no vector-memory wait (which would
+// also wait for the previous stage's output stores) precedes a stage.
+template <typename T>
+__device__ __forceinline__ T kload(const T &ref) {
+#if __HIP_DEVICE_COMPILE__
+    typedef __attribute__((address_space(4))) const T cT;
+    return *__builtin_bit_cast(const cT *, &ref);
+#else
+    return ref;  // the host pass only parses device functions
+#endif
 }
+
+// A matrix descriptor read from the layer table into scalar registers.
+__device__ __forceinline__ Mat umat(const Mat &m) { return kload(m); }
 
 struct Layer {
     Mat m[7];
@@ -128,7 +129,7 @@ struct Plan {
     int32_t qkv_b1, qkv_b2;            // blocks [0,b1) q, [b1,b2) k, [b2,nb) v
     int32_t s_qkv, s_o, s_gu, s_down;  // K slices per wave group
     int32_t lds_red;                   // float offset of the red/ent area in LDS
-    int32_t pad_;
+    int32_t o_b0;                      // first block of the o stage (blocks before it run attention)
     const uint16_t *embed;
     const float *final_norm;
     int32_t *tok;
@@ -212,11 +213,18 @@ __device__ __forceinline__ uint32_t ll_lo(float v, uint32_t e) { return (__float
 __device__ __forceinline__ uint32_t ll_bf16w(float v, uint32_t e) {
     return (static_cast<uint32_t>(f32_to_bf16(v)) << 16) | e;
 }
-// two words at p (8-byte aligned), one coherent store
-__device__ __forceinline__ void ll_store2(uint32_t *p, uint32_t a, uint32_t b) {
-    __hip_atomic_store(reinterpret_cast<uint64_t *>(p),
-                       static_cast<uint64_t>(a) | (static_cast<uint64_t>(b) << 32), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+// Coherent word stores through a buffer resource whose base is the output
+// array (byte offsets).  Buffer stores, not flat ones: a flat access in
+// flight makes the compiler wait for every outstanding load at the next
+// wait, which would serialise the following stage's weight stream.
+constexpr int64_t kAnyBytes = 0x7fffffff;  // output arrays are < 2 GiB
+// two words at byte offset off (8-byte aligned), one store
+__device__ __forceinline__ void ll_store2(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t a, uint32_t b) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{a, b}, r, off, 0, kCoh);
+}
+__device__ __forceinline__ void ll_store1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t a) {
+    __builtin_amdgcn_raw_buffer_store_b32(a, r, off, 0, kCoh);
 }
 __device__ __forceinline__ uint2 coh_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -274,6 +282,8 @@ __device__ __forceinline__ bool gave_up(const Plan &P, uint64_t t0) {
     if (e != 0 || wall_clock64() - t0 > kTimeoutTicks) {
         if ((threadIdx.x & 63) == 0)
             __hip_atomic_store(P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // complete before this path rejoins the stream code (see ll_store2)
+        __builtin_amdgcn_s_waitcnt(0);
         return true;
     }
     return false;
@@ -419,10 +429,11 @@ __device__ __forceinline__ Geo geo_qkv(const Plan &P, const Layer &L, int wave) 
     return G;
 }
 
+// rows of matrix mi spread over blocks [b0, nblocks)
 __device__ __forceinline__ Geo geo_plain(const Plan &P, const Layer &L, int mi, int32_t K, int S,
-                                         int wave) {
+                                         int wave, int b0 = 0) {
     Geo G;
-    const int b = blockIdx.x, nb = P.nblocks;
+    const int b = static_cast<int>(blockIdx.x) - b0, nb = P.nblocks - b0;
     G.m0 = G.m1 = umat(L.m[mi]);
     G.nseg = 1;
     G.seg = 0;
@@ -451,32 +462,35 @@ __device__ __forceinline__ Geo geo_pair(const Plan &P, const Layer &L, int wave)
     return G;
 }
 
+// Issues the index words and affine factors of rows [t0, t0 + RB) of the
+// wave's share.  Every load is issued on every path -- rows and chunks
+// outside the share get an out-of-range offset (no traffic, zeros) -- so the
+// number of loads in flight never depends on a branch and the waits before
+// each batch's use count exactly the loads issued after it.  Without affine
+// factors both factor buffers have no records: scales and offsets read 0,
+// and row_dot adds `nonaff` (1) to the scale.
 __device__ __forceinline__ void load_batch(const Mat &M, const Seg &g, int32_t K, int32_t group,
                                            int64_t t0, int lane, Batch &b) {
     const bool affine = M.gs != nullptr;
-    const int64_t ngroups = affine ? K / group : 0;
+    const uint32_t gsz = group > 0 ? static_cast<uint32_t>(group) : 1u;
+    const uint32_t ngroups = affine ? static_cast<uint32_t>(K) / gsz : 0u;
     const __amdgpu_buffer_rsrc_t qr = urs(M.idx, M.out * K);
     const __amdgpu_buffer_rsrc_t sr = urs(M.gs, affine ? M.out * ngroups * 4 : 0);
     const __amdgpu_buffer_rsrc_t orr = urs(M.go, affine ? M.out * ngroups * 4 : 0);
+    const int32_t nm = static_cast<int32_t>(g.n_mine);
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-        const int64_t t = t0 + r;
-        const bool mine = t < g.n_mine;
-        const uint32_t row = static_cast<uint32_t>(g.lo + g.rg + t * g.RG);
+        const int32_t t = static_cast<int32_t>(t0) + r;
+        const bool mine = t < nm;
+        const uint32_t row = static_cast<uint32_t>(g.lo + g.rg) + static_cast<uint32_t>(t * g.RG);
 #pragma unroll
         for (int ci = 0; ci < CPS; ++ci) {
-            const int k0 = (g.c_lo + ci) * kChunk + lane * 16;
-            const bool ok = mine && ci < g.nc && k0 < K;
+            const uint32_t k0 = static_cast<uint32_t>((g.c_lo + ci) * kChunk + lane * 16);
+            const bool ok = mine && ci < g.nc && k0 < static_cast<uint32_t>(K);
+            const uint32_t g4 = (row * ngroups + k0 / gsz) * 4u;
             b.q[r][ci] = buf_load16(qr, ok ? row * static_cast<uint32_t>(K) + k0 : kOob);
-            if (affine) {
-                const uint32_t g4 = (row * static_cast<uint32_t>(ngroups) +
-                                     static_cast<uint32_t>(k0) / static_cast<uint32_t>(group)) * 4u;
-                b.sc[r][ci] = buf_loadf(sr, ok ? g4 : kOob);
-                b.of[r][ci] = buf_loadf(orr, ok ? g4 : kOob);
-            } else {
-                b.sc[r][ci] = 1.f;
-                b.of[r][ci] = 0.f;
-            }
+            b.sc[r][ci] = buf_loadf(sr, ok ? g4 : kOob);
+            b.of[r][ci] = buf_loadf(orr, ok ? g4 : kOob);
         }
     }
 }
@@ -494,10 +508,10 @@ __device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, P
             const uint32_t f = tid + k * kThreads;  // float4 slot of the table
             p.cbv[s][k] = buf_loadf(cr, (f * 4u / NREP) * 4u);
         }
+        // the block's CSR range: scalar loads (read-only table), no vector wait
         const bool has_sc = M.rp != nullptr;
-        const __amdgpu_buffer_rsrc_t rr = urs(M.rp, has_sc ? (M.out + 1) * 4 : 0);
-        p.b0[s] = buf_loadi(rr, static_cast<uint32_t>(G.lo * 4));
-        p.b1[s] = buf_loadi(rr, static_cast<uint32_t>((G.lo + G.n) * 4));
+        p.b0[s] = has_sc ? kload(M.rp[G.lo]) : 0;
+        p.b1[s] = has_sc ? kload(M.rp[G.lo + G.n]) : 0;
     }
     __builtin_amdgcn_sched_barrier(0);  // small loads first: they return first
     const Mat &Mw = G.seg ? G.m1 : G.m0;
@@ -517,7 +531,8 @@ __device__ __forceinline__ float tok_lookup(uint32_t lane_seg, uint32_t w) {
 }
 
 __device__ __forceinline__ float row_dot(uint32_t lane_seg, const Batch &b, int r,
-                                         const float (&xv)[CPS][16], const float (&xs)[CPS]) {
+                                         const float (&xv)[CPS][16], const float (&xs)[CPS],
+                                         float nonaff) {
     float acc = 0.f;
 #pragma unroll
     for (int ci = 0; ci < CPS; ++ci) {
@@ -534,7 +549,7 @@ __device__ __forceinline__ float row_dot(uint32_t lane_seg, const Batch &b, int 
             part = fmaf(xv[ci][4 * d + 2], c2, part);
             part = fmaf(xv[ci][4 * d + 3], c3, part);
         }
-        acc = fmaf(part, b.sc[r][ci], acc);
+        acc = fmaf(part, b.sc[r][ci] + nonaff, acc);
         acc = fmaf(b.of[r][ci], xs[ci], acc);
     }
     return acc;
@@ -575,6 +590,9 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
         // K <= 4096: one float4 per thread
         const bool mine = t * 4 < K;
         const uint32_t o4 = mine ? static_cast<uint32_t>(t) * 16u : kOob;
+        // the norm weights are constant: issued ahead of the poll, so they
+        // have landed when the activations have
+        const u32x4 w = buf_load16(urs(X.w, static_cast<int64_t>(K) * 4), o4);
         float r[4];
         if (X.emb) {
             const __amdgpu_buffer_rsrc_t er = urs(X.emb, static_cast<int64_t>(K) * 2);
@@ -595,6 +613,9 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             // after the prefetched batch, with data sampled now -- so wait
             // for the batch first and sample later
             __builtin_amdgcn_s_waitcnt(kVmcnt0);
+            // pins the norm-weight load above the poll (the compiler would
+            // otherwise sink it to its use, a round trip after the poll)
+            asm volatile("" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]));
             const uint64_t t0 = wall_clock64();
             for (int it = 1;; ++it) {
                 a0 = coh_load16(br, o8);
@@ -614,10 +635,6 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             r[2] = ll_f32(a1[0], a1[1]) + ll_f32(d1[0], d1[1]);
             r[3] = ll_f32(a1[2], a1[3]) + ll_f32(d1[2], d1[3]);
         }
-        const u32x4 w = buf_load16(urs(X.w, static_cast<int64_t>(K) * 4), o4);
-        __builtin_amdgcn_sched_barrier(0);
-        after();  // loads that may return after the activations
-        __builtin_amdgcn_sched_barrier(0);
         if (X.res_out && blockIdx.x == 0 && mine) {
             const __amdgpu_buffer_rsrc_t rr = urs(X.res_out, static_cast<int64_t>(K) * 8);
             const u32x4 v0{ll_hi(r[0], X.eo), ll_lo(r[0], X.eo), ll_hi(r[1], X.eo), ll_lo(r[1], X.eo)};
@@ -664,9 +681,6 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             if (__all(ok)) break;
             if (it % kPollCheck == 0 && gave_up(P, t0)) break;
         }
-        __builtin_amdgcn_sched_barrier(0);
-        after();
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int i = t + j * kThreads;
@@ -680,6 +694,14 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
         }
     }
     lds_barrier();  // xl complete
+    // Every wave has polled and the activation is in LDS: the stream's next
+    // loads go out now.  Issued by a wave that finished polling early, they
+    // would queue ahead of the other waves' polls (a CU returns vector loads
+    // in issue order); issued before the norm, their issue (the memory
+    // pipeline takes a batch only as fast as it drains) would hold the norm.
+    __builtin_amdgcn_sched_barrier(0);
+    after();
+    __builtin_amdgcn_sched_barrier(0);
     const Seg &g = G.g;
 #pragma unroll
     for (int ci = 0; ci < CPS; ++ci) {
@@ -709,12 +731,33 @@ enum { YF32 = 0, YACT = 1 };
 __device__ __forceinline__ float row_total(const Mat &M, int r, int S, const float *red,
                                            int32_t j0, int32_t j1, int32_t b0, const float *ent,
                                            const float *xl) {
+    // The terms are added in a fixed order (slices, then sidecar entries in
+    // CSR order); they are read four at a time so the LDS reads overlap
+    // (padding adds 0).
     float v = 0.f;
-    for (int s = 0; s < S; ++s) v += red[r * S + s];
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        float p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) p[u] = red[r * S + min(s0 + u, S - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v += s0 + u < S ? p[u] : 0.f;
+    }
     if (M.rp) {
-        for (int32_t j = j0; j < j1; ++j) {
-            const int32_t e = j - b0;
-            v += e < kEnt ? ent[e] : xl[M.col[j]] * M.delta[j];
+        for (int32_t j = j0; j < j1; j += 4) {
+            float p[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int32_t e = min(j + u, j1 - 1) - b0;
+                p[u] = ent[min(e, kEnt - 1)];
+                if (e >= kEnt) {  // past the LDS-staged entries (rare): from memory
+                    const int32_t jj = min(j + u, j1 - 1);
+                    const float d = buf_loadf(urs(M.delta, kAnyBytes), static_cast<uint32_t>(jj) * 4u);
+                    const int32_t c = buf_loadi(urs(M.col, kAnyBytes), static_cast<uint32_t>(jj) * 4u);
+                    p[u] = xl[c] * d;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v += j + u < j1 ? p[u] : 0.f;
         }
     }
     return v;
@@ -780,24 +823,29 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     const Seg &g = G.g;
     float *redw = red + G.seg * kRedCap;
     const uint32_t lane_seg = (static_cast<uint32_t>(G.seg) << 16) | (static_cast<uint32_t>(lane) * 4u);
-    auto compute = [&](int64_t t0, const Batch &b) {
+    const float nonaff = Mw.gs != nullptr ? 0.f : 1.f;
+    const int32_t n_mine = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(g.n_mine));
+    auto compute = [&](int32_t t0, const Batch &b) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const int64_t tt = t0 + r;
-            if (tt < g.n_mine) {
-                const float v = wave_sum_lane63(row_dot(lane_seg, b, r, xv, xs));
+            const int32_t tt = t0 + r;
+            if (tt < n_mine) {
+                const float v = wave_sum_lane63(row_dot(lane_seg, b, r, xv, xs, nonaff));
                 if (lane == kWave - 1) redw[(g.rg + tt * g.RG) * g.S + g.s_id] = v;
             }
             __builtin_amdgcn_sched_barrier(0);  // one row's lookups in flight at a time
         }
     };
-    for (int64_t i0 = 0; i0 < g.n_mine; i0 += 2 * RB) {
+    // The stream ends with no load in flight, so nothing after it (the final
+    // pass, the next stage) waits on a load that lands in a reused register
+    // -- such a wait would also wait for this stage's output stores.
+    for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
         compute(i0, pf.bt[0]);
-        if (i0 + RB >= g.n_mine) break;
+        if (i0 + RB >= n_mine) break;
         load_batch(Mw, g, K, group, i0 + 2 * RB, lane, pf.bt[0]);
         __builtin_amdgcn_sched_barrier(0);
         compute(i0 + RB, pf.bt[1]);
-        if (i0 + 2 * RB >= g.n_mine) break;
+        if (i0 + 2 * RB >= n_mine) break;
         load_batch(Mw, g, K, group, i0 + 3 * RB, lane, pf.bt[1]);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -809,11 +857,13 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
         const int S = g.S;
         const float v0 = row_total(G.m0, t, S, red, rps[t], rps[t + 1], rps[0], ent, xl) + bias[0];
         if constexpr (YM == YF32) {
-            ll_store2(y + 2 * (G.y_off + row), ll_hi(v0, ey), ll_lo(v0, ey));
+            ll_store2(urs(y, kAnyBytes), static_cast<uint32_t>(G.y_off + row) * 8u, ll_hi(v0, ey),
+                      ll_lo(v0, ey));
         } else {
             const float v1 = row_total(G.m1, t, S, red + kRedCap, rps[kRps + t],
                                        rps[kRps + t + 1], rps[kRps], ent + kEnt, xl) + bias[1];
-            coh_store_u32(y + row, ll_bf16w(v0 / (1.f + expf(-v0)) * v1, ey));
+            ll_store1(urs(y, kAnyBytes), static_cast<uint32_t>(row) * 4u,
+                      ll_bf16w(v0 / (1.f + expf(-v0)) * v1, ey));
         }
     }
     // the next stage rebuilds the tables and xl in LDS: every thread is past
@@ -890,7 +940,7 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t / kWave;
     const int64_t row = static_cast<int64_t>(P.n_kv) * D;  // cache elements between positions
-    const uint16_t *kc = uptr(L.kc), *vcache = uptr(L.vc);
+    const uint16_t *kc = kload(L.kc), *vcache = kload(L.vc);
     // earlier positions' cache rows
     const __amdgpu_buffer_rsrc_t kr = urs(kc, static_cast<int64_t>(P.max_seq) * row * 2);
     const __amdgpu_buffer_rsrc_t vr = urs(vcache, static_cast<int64_t>(P.max_seq) * row * 2);
@@ -1062,7 +1112,8 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
             v0 += part[w * D + d];
             v1 += part[w * D + d + 1];
         }
-        ll_store2(attn + static_cast<int64_t>(h) * D + d, ll_bf16w(v0 * inv, ea), ll_bf16w(v1 * inv, ea));
+        ll_store2(urs(attn, kAnyBytes), static_cast<uint32_t>(h * D + d) * 4u, ll_bf16w(v0 * inv, ea),
+                  ll_bf16w(v1 * inv, ea));
     }
     return true;
 }
@@ -1242,7 +1293,7 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         X.base = P.res + static_cast<int64_t>(l) * P.ls_hid;
         X.delta = l == 0 ? nullptr : P.dn + static_cast<int64_t>(l - 1) * P.ls_hid;
         X.emb = l == 0 ? P.embed + static_cast<int64_t>(tok) * P.hidden : nullptr;
-        X.w = uptr(L.in_norm);
+        X.w = kload(L.in_norm);
         X.res_out = P.ra + static_cast<int64_t>(l) * P.ls_hid;
         X.eb = ll_epoch(t0 - 1);  // res[l]: the previous layer's stage 4
         X.ed = ll_epoch(t0);      // dn[l-1]: the previous layer's stage 5
@@ -1251,17 +1302,20 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
                                   tid, lane);
     }
     tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
-    const Geo Go = geo_plain(P, L, kO, P.n_heads * kHeadDim, P.s_o, wave);
     // 2. attention (block h = query head h); the other blocks go straight on
     // to the o stage's prefetch
     if (static_cast<int>(blockIdx.x) < P.n_heads) {
         attention(P, L, P.qkv + static_cast<int64_t>(l) * P.ls_qkv, e1,
                   P.attn + static_cast<int64_t>(l) * P.ls_attn, e2, blockIdx.x, pos, smem, rope);
-        lds_barrier();  // attention's LDS is reused by the o stage
+        lds_barrier();  // attention's LDS is reused by the next stage
     }
-    prefetch(Go, P.group, tid, pf);
-    // 3. o = W_o attn
-    {
+    // 3. o = W_o attn, on blocks [o_b0, nblocks): with o_b0 = n_heads the
+    // attention blocks, which finish attention after everyone else has
+    // started o, skip it and go on to the gate/up stage, instead of being
+    // the last o producers every layer
+    if (static_cast<int>(blockIdx.x) >= P.o_b0) {
+        const Geo Go = geo_plain(P, L, kO, P.n_heads * kHeadDim, P.s_o, wave, P.o_b0);
+        prefetch(Go, P.group, tid, pf);
         tid = fresh_v(tid), lane = tid & 63;
         XSrc X{};
         X.xb = P.attn + static_cast<int64_t>(l) * P.ls_attn;
@@ -1277,7 +1331,7 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         XSrc X{};
         X.base = P.ra + static_cast<int64_t>(l) * P.ls_hid;
         X.delta = P.o + static_cast<int64_t>(l) * P.ls_hid;
-        X.w = uptr(L.post_norm);
+        X.w = kload(L.post_norm);
         X.res_out = P.res + static_cast<int64_t>(l + 1) * P.ls_hid;
         X.eb = e1;
         X.ed = e3;
@@ -1323,6 +1377,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(const Plan *__restri
     if (blockIdx.x == 0 && threadIdx.x == 0 && out_ids) out_ids[step] = tok;
     float2 *rope = reinterpret_cast<float2 *>(smem + P.lds_red + 2 * kRedCap + 2 * kEnt + 2 * kRps + 64);
     if (static_cast<int>(blockIdx.x) < P.n_heads) rope_table(P, pos, rope);  // read after barriers
+    // Nothing of the prologue stays in flight into the layer loop: a load
+    // pending at the loop entry would make the compiler wait at the top of
+    // every layer, and that wait would also cover the previous layer's
+    // output stores.
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
 #pragma clang loop unroll(disable)
     for (int l = 0; l < P.n_layers; ++l)
         if (!do_layer<HC>(P, l, pos, target, smem, rope, wave, tok)) return;
@@ -1527,7 +1586,10 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     const int nch_o = (d->n_heads * kHeadDim + kChunk - 1) / kChunk;
     const int nch_i = (d->intermediate + kChunk - 1) / kChunk;
     const int64_t rows_qkv = std::max({(rq + bq - 1) / bq, (rk + bk - 1) / bk, (rk + bv - 1) / bv});
-    const int64_t rows_o = (d->hidden + nb - 1) / nb;
+    // o rows go to the blocks that do not run attention, when they are the
+    // large majority (attention blocks finish last and would hold o back)
+    const int o_b0 = nb - d->n_heads >= 3 * nb / 4 ? d->n_heads : 0;
+    const int64_t rows_o = (d->hidden + (nb - o_b0) - 1) / (nb - o_b0);
     const int64_t rows_gu = (d->intermediate + nb - 1) / nb;
     const int64_t rows_d = (d->hidden + nb - 1) / nb;
     Plan P{};
@@ -1542,6 +1604,7 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     P.nblocks = nb;
     P.eps = d->rms_eps;
     P.theta = d->rope_theta;
+    P.o_b0 = o_b0;
     P.qkv_b1 = bq;
     P.qkv_b2 = bq + bk;
     P.s_qkv = choose_slices(rows_qkv, kWaves, nch_h);
