@@ -496,7 +496,8 @@ __device__ __forceinline__ void load_batch(const Mat &M, const Seg &g, int32_t K
 }
 
 // Everything a stage needs that does not depend on the barrier.
-__device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, Pre &p) {
+__device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, Pre &p,
+                                         bool with_batch = true, int buf = 0) {
     const int lane = tid & 63;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -515,7 +516,7 @@ __device__ __forceinline__ void prefetch(const Geo &G, int32_t group, int tid, P
     }
     __builtin_amdgcn_sched_barrier(0);  // small loads first: they return first
     const Mat &Mw = G.seg ? G.m1 : G.m0;
-    load_batch(Mw, G.g, G.K, group, 0, lane, p.bt[0]);
+    if (with_batch) load_batch(Mw, G.g, G.K, group, 0, lane, p.bt[buf]);
 }
 
 // Codebook lookup of byte B of the packed index word w.  Tables start at LDS
@@ -763,9 +764,20 @@ __device__ __forceinline__ float row_total(const Mat &M, int r, int S, const flo
     return v;
 }
 
-template <int HC, int XM, int YM>
+struct NoNext {
+    __device__ void operator()() const {}
+};
+
+// B0: the buffer holding the stage's first batch; PRE1: the second batch
+// is loaded after the poll (without it the stage has at most one batch per
+// wave, and the other buffer belongs to the next stage's prefetch).
+// next(): issued when the stream is done (both buffers free) -- the next
+// stage's first batch, which then lands during this stage's final pass and
+// the next stage's wait instead of after the next stage begins.
+template <int HC, int XM, int YM, int B0 = 0, bool PRE1 = true, typename Next = NoNext>
 __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, const XSrc &X,
-                                         uint32_t *y, uint32_t ey, float *smem, int tid, int lane) {
+                                         uint32_t *y, uint32_t ey, float *smem, int tid, int lane,
+                                         Next next = Next{}) {
     const int32_t K = G.K, group = P.group;
     float *xl = smem + (G.nseg == 2 ? 2 * kTbl : kTbl);
     float *red = smem + P.lds_red;                           // [2][kRedCap]
@@ -810,7 +822,9 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     float xv[CPS][16], xs[CPS];
     const Mat &Mw = G.seg ? G.m1 : G.m0;
     load_x<HC, XM>(P, X, G, t, lane, xl, misc + 16, xv, xs,  // ends with a barrier: xl ready
-                   [&] { load_batch(Mw, G.g, K, group, RB, lane, pf.bt[1]); });
+                   [&] {
+                       if constexpr (PRE1) load_batch(Mw, G.g, K, group, RB, lane, pf.bt[1 - B0]);
+                   });
     // the loads above have landed by now (they were issued before x's)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -840,15 +854,17 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     // pass, the next stage) waits on a load that lands in a reused register
     // -- such a wait would also wait for this stage's output stores.
     for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
-        compute(i0, pf.bt[0]);
-        if (i0 + RB >= n_mine) break;
-        load_batch(Mw, g, K, group, i0 + 2 * RB, lane, pf.bt[0]);
+        compute(i0, pf.bt[B0]);
+        if (!PRE1 || i0 + RB >= n_mine) break;
+        load_batch(Mw, g, K, group, i0 + 2 * RB, lane, pf.bt[B0]);
         __builtin_amdgcn_sched_barrier(0);
-        compute(i0 + RB, pf.bt[1]);
+        compute(i0 + RB, pf.bt[1 - B0]);
         if (i0 + 2 * RB >= n_mine) break;
-        load_batch(Mw, g, K, group, i0 + 3 * RB, lane, pf.bt[1]);
+        load_batch(Mw, g, K, group, i0 + 3 * RB, lane, pf.bt[1 - B0]);
         __builtin_amdgcn_sched_barrier(0);
     }
+    next();
+    __builtin_amdgcn_sched_barrier(0);
     lds_barrier();  // red and ent complete
 
     // final pass: one thread per row of the block
@@ -1275,9 +1291,9 @@ __device__ void final_argmax(const Plan &P, float *smem) {
 // inside the layer.  Every stage issues its compressed-weight loads first.
 template <int HC>
 __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t &target,
-                                         float *smem, const float2 *rope, int wave0, int tok) {
+                                         float *smem, const float2 *rope, int wave0, int tok,
+                                         Pre &pf) {
     const Layer &L = P.layers[l];
-    Pre pf;
     const uint32_t t0 = target;  // the previous layer's last stage (its down output)
     const uint32_t e1 = ll_epoch(t0 + 1), e2 = ll_epoch(t0 + 2), e3 = ll_epoch(t0 + 3);
     const uint32_t e4 = ll_epoch(t0 + 4), e5 = ll_epoch(t0 + 5);
@@ -1288,7 +1304,8 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
     // 1. r = x + delta -> ra; q/k/v = W norm(r)
     {
         const Geo G = geo_qkv(P, L, wave);
-        prefetch(G, P.group, tid, pf);
+        // after layer 0 the previous layer's down stage loaded the first batch
+        prefetch(G, P.group, tid, pf, l == 0);
         XSrc X{};
         X.base = P.res + static_cast<int64_t>(l) * P.ls_hid;
         X.delta = l == 0 ? nullptr : P.dn + static_cast<int64_t>(l - 1) * P.ls_hid;
@@ -1314,19 +1331,32 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
     // started o, skip it and go on to the gate/up stage, instead of being
     // the last o producers every layer
     if (static_cast<int>(blockIdx.x) >= P.o_b0) {
+        // The o weights (at most one batch per wave: the host checks) go to
+        // bt[1]; the gate/up stage's first batch goes to bt[0] now, so it
+        // streams while o waits for attention rather than after o.
         const Geo Go = geo_plain(P, L, kO, P.n_heads * kHeadDim, P.s_o, wave, P.o_b0);
-        prefetch(Go, P.group, tid, pf);
+        prefetch(Go, P.group, tid, pf, true, 1);
+        {
+            const Geo Gp = geo_pair(P, L, wave);
+            load_batch(Gp.seg ? Gp.m1 : Gp.m0, Gp.g, Gp.K, P.group, 0, lane, pf.bt[0]);
+        }
         tid = fresh_v(tid), lane = tid & 63;
         XSrc X{};
         X.xb = P.attn + static_cast<int64_t>(l) * P.ls_attn;
         X.eb = e2;
-        run_gemv<HC, XBF16, YF32>(P, Go, pf, X, P.o + static_cast<int64_t>(l) * P.ls_hid, e3, smem,
-                                  tid, lane);
+        run_gemv<HC, XBF16, YF32, 1, false>(P, Go, pf, X, P.o + static_cast<int64_t>(l) * P.ls_hid,
+                                            e3, smem, tid, lane);
+    } else {
+        // attention blocks: the gate/up stage's first batch (written as the
+        // other branch of the o stage, so no earlier batch stays live across
+        // attention)
+        const Geo Gp = geo_pair(P, L, wave);
+        load_batch(Gp.seg ? Gp.m1 : Gp.m0, Gp.g, Gp.K, P.group, 0, lane, pf.bt[0]);
     }
     {
         tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
         const Geo Gp = geo_pair(P, L, wave);
-        prefetch(Gp, P.group, tid, pf);
+        prefetch(Gp, P.group, tid, pf, false);  // first batch: loaded above
         // 4. r = ra + o -> res[l+1]; act = silu(W_g norm(r)) * (W_u norm(r))
         XSrc X{};
         X.base = P.ra + static_cast<int64_t>(l) * P.ls_hid;
@@ -1348,7 +1378,12 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         X.xb = P.act + static_cast<int64_t>(l) * P.ls_act;
         X.eb = e4;
         run_gemv<HC, XBF16, YF32>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid, e5, smem,
-                                  tid, lane);
+                                  tid, lane, [&] {
+                                      if (l + 1 < P.n_layers) {
+                                          const Geo G1 = geo_qkv(P, P.layers[l + 1], wave);
+                                          load_batch(G1.m0, G1.g, G1.K, P.group, 0, lane, pf.bt[0]);
+                                      }
+                                  });
     }
     return true;
 }
@@ -1382,9 +1417,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(const Plan *__restri
     // every layer, and that wait would also cover the previous layer's
     // output stores.
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    Pre pf;  // weight batches; a stage may load the next stage's first batch
 #pragma clang loop unroll(disable)
     for (int l = 0; l < P.n_layers; ++l)
-        if (!do_layer<HC>(P, l, pos, target, smem, rope, wave, tok)) return;
+        if (!do_layer<HC>(P, l, pos, target, smem, rope, wave, tok, pf)) return;
     // the last layer's outputs are complete everywhere once every block has
     // arrived (arriving waits for the block's stores)
     arrive(P, target);
@@ -1612,6 +1648,8 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     P.s_gu = choose_slices(rows_gu, kWaves / 2, nch_h);
     P.s_down = choose_slices(rows_d, kWaves, nch_i);
     HXQ_REQUIRE(P.s_qkv > 0 && P.s_o > 0 && P.s_gu > 0 && P.s_down > 0, "no slice split fits");
+    HXQ_REQUIRE((rows_o + kWaves / P.s_o - 1) / (kWaves / P.s_o) <= RB,
+                "o stage needs more than one batch per wave");
     HXQ_REQUIRE(rows_qkv <= kThreads && rows_o <= kThreads && rows_gu <= kThreads &&
                     rows_qkv * P.s_qkv <= kRedCap && rows_o * P.s_o <= kRedCap &&
                     rows_gu * P.s_gu <= kRedCap && rows_d * P.s_down <= kRedCap,
