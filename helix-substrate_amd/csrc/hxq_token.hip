@@ -126,10 +126,11 @@ struct Layer {
 struct Plan {
     int32_t hidden, n_layers, n_heads, n_kv, inter, vocab, max_seq, group, nblocks;
     float eps, theta;
-    int32_t qkv_b1, qkv_b2;            // blocks [0,b1) q, [b1,b2) k, [b2,nb) v
+    int32_t qkv_b1, qkv_b2;            // blocks [qkv_b0,b1) q, [b1,b2) k, [b2,nb) v
     int32_t s_qkv, s_o, s_gu, s_down;  // K slices per wave group
     int32_t lds_red;                   // float offset of the red/ent area in LDS
     int32_t o_b0;                      // first block of the o stage (blocks before it run attention)
+    int32_t qkv_b0, pad_;              // first block of the q/k/v stage (likewise)
     const uint16_t *embed;
     const float *final_norm;
     int32_t *tok;
@@ -414,7 +415,7 @@ __device__ __forceinline__ Geo geo_qkv(const Plan &P, const Layer &L, int wave) 
     Geo G;
     const int b = blockIdx.x, nb = P.nblocks;
     const int mi = b < P.qkv_b1 ? 0 : b < P.qkv_b2 ? 1 : 2;
-    const int bs = mi == 0 ? 0 : mi == 1 ? P.qkv_b1 : P.qkv_b2;
+    const int bs = mi == 0 ? P.qkv_b0 : mi == 1 ? P.qkv_b1 : P.qkv_b2;
     const int be = mi == 0 ? P.qkv_b1 : mi == 1 ? P.qkv_b2 : nb;
     G.m0 = G.m1 = umat(L.m[mi]);
     G.nseg = 1;
@@ -570,6 +571,7 @@ struct XSrc {
     const uint16_t *emb;
     const float *w;
     uint32_t *res_out;
+    int32_t res_blk;  // the block that stores res_out
     const uint32_t *xb;
     uint32_t eb, ed, eo;
 };
@@ -636,7 +638,7 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             r[2] = ll_f32(a1[0], a1[1]) + ll_f32(d1[0], d1[1]);
             r[3] = ll_f32(a1[2], a1[3]) + ll_f32(d1[2], d1[3]);
         }
-        if (X.res_out && blockIdx.x == 0 && mine) {
+        if (X.res_out && static_cast<int>(blockIdx.x) == X.res_blk && mine) {
             const __amdgpu_buffer_rsrc_t rr = urs(X.res_out, static_cast<int64_t>(K) * 8);
             const u32x4 v0{ll_hi(r[0], X.eo), ll_lo(r[0], X.eo), ll_hi(r[1], X.eo), ll_lo(r[1], X.eo)};
             const u32x4 v1{ll_hi(r[2], X.eo), ll_lo(r[2], X.eo), ll_hi(r[3], X.eo), ll_lo(r[3], X.eo)};
@@ -1301,8 +1303,11 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
     // Each stage starts from fresh copies of the thread / wave ids, so values
     // derived from them are recomputed per stage rather than kept live.
     int tid = fresh_v(static_cast<int>(threadIdx.x)), wave = fresh_s(wave0), lane = tid & 63;
-    // 1. r = x + delta -> ra; q/k/v = W norm(r)
-    {
+    // 1. r = x + delta -> ra; q/k/v = W norm(r), on blocks [qkv_b0,
+    // nblocks): with qkv_b0 = n_heads the attention blocks start attention
+    // (loading this layer's K/V cache rows) at once, so those loads stream
+    // while the q/k/v projection runs instead of after it
+    if (static_cast<int>(blockIdx.x) >= P.qkv_b0) {
         const Geo G = geo_qkv(P, L, wave);
         // after layer 0 the previous layer's down stage loaded the first batch
         prefetch(G, P.group, tid, pf, l == 0);
@@ -1312,6 +1317,7 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         X.emb = l == 0 ? P.embed + static_cast<int64_t>(tok) * P.hidden : nullptr;
         X.w = kload(L.in_norm);
         X.res_out = P.ra + static_cast<int64_t>(l) * P.ls_hid;
+        X.res_blk = P.qkv_b0;
         X.eb = ll_epoch(t0 - 1);  // res[l]: the previous layer's stage 4
         X.ed = ll_epoch(t0);      // dn[l-1]: the previous layer's stage 5
         X.eo = e1;
@@ -1363,6 +1369,7 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         X.delta = P.o + static_cast<int64_t>(l) * P.ls_hid;
         X.w = kload(L.post_norm);
         X.res_out = P.res + static_cast<int64_t>(l + 1) * P.ls_hid;
+        X.res_blk = 0;
         X.eb = e1;
         X.ed = e3;
         X.eo = e4;
@@ -1379,7 +1386,8 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
         X.eb = e4;
         run_gemv<HC, XBF16, YF32>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid, e5, smem,
                                   tid, lane, [&] {
-                                      if (l + 1 < P.n_layers) {
+                                      if (l + 1 < P.n_layers &&
+                                          static_cast<int>(blockIdx.x) >= P.qkv_b0) {
                                           const Geo G1 = geo_qkv(P, P.layers[l + 1], wave);
                                           load_batch(G1.m0, G1.g, G1.K, P.group, 0, lane, pf.bt[0]);
                                       }
@@ -1610,21 +1618,23 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     HXQ_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
     char *ws = static_cast<char *>(workspace);
 
+    // The attention blocks [0, n_heads) skip the q/k/v and o stages when the
+    // other blocks are the large majority (they would finish last).
+    const int att_b0 = nb - d->n_heads >= 3 * nb / 4 ? d->n_heads : 0;
     // q/k/v block split in proportion to rows (every matrix at least one block)
+    const int nbq = nb - att_b0;
     const int64_t rq = int64_t{d->n_heads} * kHeadDim, rk = int64_t{d->n_kv_heads} * kHeadDim;
     const int64_t rt = rq + 2 * rk;
-    int bq = static_cast<int>((nb * rq + rt / 2) / rt);
-    int bk = static_cast<int>((nb * rk + rt / 2) / rt);
-    bq = std::max(1, std::min(bq, nb - 2));
-    bk = std::max(1, std::min(bk, nb - bq - 1));
-    const int bv = nb - bq - bk;
+    int bq = static_cast<int>((nbq * rq + rt / 2) / rt);
+    int bk = static_cast<int>((nbq * rk + rt / 2) / rt);
+    bq = std::max(1, std::min(bq, nbq - 2));
+    bk = std::max(1, std::min(bk, nbq - bq - 1));
+    const int bv = nbq - bq - bk;
     const int nch_h = (d->hidden + kChunk - 1) / kChunk;
     const int nch_o = (d->n_heads * kHeadDim + kChunk - 1) / kChunk;
     const int nch_i = (d->intermediate + kChunk - 1) / kChunk;
     const int64_t rows_qkv = std::max({(rq + bq - 1) / bq, (rk + bk - 1) / bk, (rk + bv - 1) / bv});
-    // o rows go to the blocks that do not run attention, when they are the
-    // large majority (attention blocks finish last and would hold o back)
-    const int o_b0 = nb - d->n_heads >= 3 * nb / 4 ? d->n_heads : 0;
+    const int o_b0 = att_b0;
     const int64_t rows_o = (d->hidden + (nb - o_b0) - 1) / (nb - o_b0);
     const int64_t rows_gu = (d->intermediate + nb - 1) / nb;
     const int64_t rows_d = (d->hidden + nb - 1) / nb;
@@ -1641,8 +1651,9 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     P.eps = d->rms_eps;
     P.theta = d->rope_theta;
     P.o_b0 = o_b0;
-    P.qkv_b1 = bq;
-    P.qkv_b2 = bq + bk;
+    P.qkv_b0 = att_b0;
+    P.qkv_b1 = att_b0 + bq;
+    P.qkv_b2 = att_b0 + bq + bk;
     P.s_qkv = choose_slices(rows_qkv, kWaves, nch_h);
     P.s_o = choose_slices(rows_o, kWaves, nch_o);
     P.s_gu = choose_slices(rows_gu, kWaves / 2, nch_h);
