@@ -256,6 +256,28 @@ __device__ __forceinline__ float wave_max_all(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// The kWaves (16) per-wave values at a (16-byte aligned LDS), read with four
+// 16-byte loads in flight; sum in index order / maximum.
+__device__ __forceinline__ void lds16(const float *a, float (&v)[kWaves]) {
+#pragma unroll
+    for (int i = 0; i < kWaves / 4; ++i) {
+        const float4 f = reinterpret_cast<const float4 *>(a)[i];
+        v[4 * i] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+    }
+}
+__device__ __forceinline__ float sum16(const float *a) {
+    float v[kWaves];
+    lds16(a, v);
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) t += v[i];
+    return t;
+}
+
+
 // Redefines a value with an empty asm so the compiler recomputes whatever
 // derives from it instead of keeping it live from an earlier stage.
 __device__ __forceinline__ int fresh_s(int v) {
@@ -651,9 +673,7 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
         ss = wave_sum_all(ss);
         if (lane == 0) part[t / kWave] = ss;
         lds_barrier();
-        float tot = 0.f;
-#pragma unroll
-        for (int i = 0; i < kWaves; ++i) tot += part[i];
+        const float tot = sum16(part);
         const float inv = rsqrtf(tot / K + P.eps);
         if (mine)
             *reinterpret_cast<float4 *>(xl + 4 * t) =
@@ -897,8 +917,11 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
     lds_barrier();
+    float w[kWaves];
+    lds16(red, w);
     float t = -FLT_MAX;
-    for (int i = 0; i < kWaves; ++i) t = fmaxf(t, red[i]);
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) t = fmaxf(t, w[i]);
     return t;
 }
 
@@ -907,9 +930,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
     lds_barrier();
-    float t = 0.f;
-    for (int i = 0; i < kWaves; ++i) t += red[i];
-    return t;
+    return sum16(red);
 }
 
 
@@ -1044,9 +1065,11 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         qs[t + D / 2] = q1;
         rope_rot(kv0, kv1, cs, a, b);
         const int64_t base = static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D;
-        if (writer) {
-            L.kc[base + t] = f32_to_bf16(a);
-            L.kc[base + t + D / 2] = f32_to_bf16(b);
+        if (writer) {  // buffer stores (a flat store in flight would make every later LDS wait
+                       // of this stage also wait for it)
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(a), kr, static_cast<uint32_t>((base + t) * 2), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(b), kr,
+                                                  static_cast<uint32_t>((base + t + D / 2) * 2), 0, 0);
         }
         kn[t] = bf16r(a);
         kn[t + D / 2] = bf16r(b);
@@ -1056,7 +1079,10 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     } else if (t < D / 2 + D) {
         const int j = t - D / 2;
         const float v = vv;
-        if (writer) L.vc[static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D + j] = f32_to_bf16(v);
+        if (writer)
+            __builtin_amdgcn_raw_buffer_store_b16(
+                f32_to_bf16(v), vr,
+                static_cast<uint32_t>((static_cast<int64_t>(pos) * row + static_cast<int64_t>(kvh) * D + j) * 2), 0, 0);
         vn[j] = bf16r(v);
     }
     lds_barrier();  // LDS only: the cache stores are read by later launches
@@ -1066,14 +1092,24 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         if (t == pos) {
             s0 = *spos;
         } else {
+            // q (the same for every lane) is read 16 values at a time, four
+            // 16-byte LDS reads in flight per round
 #pragma unroll
-            for (int c = 0; c < D / 8; ++c)
+            for (int c0 = 0; c0 < D / 8; c0 += 2) {
+                float4 qv[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int d = c * 8 + 2 * e;
-                    s0 = fmaf(qs[d], __uint_as_float(kw[c][e] << 16), s0);
-                    s1 = fmaf(qs[d + 1], __uint_as_float(kw[c][e] & 0xffff0000u), s1);
+                for (int i = 0; i < 4; ++i) qv[i] = reinterpret_cast<const float4 *>(qs)[2 * c0 + i];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const float q8[8] = {qv[2 * c].x, qv[2 * c].y, qv[2 * c].z, qv[2 * c].w,
+                                         qv[2 * c + 1].x, qv[2 * c + 1].y, qv[2 * c + 1].z, qv[2 * c + 1].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s0 = fmaf(q8[2 * e], __uint_as_float(kw[c0 + c][e] << 16), s0);
+                        s1 = fmaf(q8[2 * e + 1], __uint_as_float(kw[c0 + c][e] & 0xffff0000u), s1);
+                    }
                 }
+            }
         }
         sc[t] = s0 + s1;
         mx = s0 + s1;
@@ -1125,10 +1161,14 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     lds_barrier();
     if (t < D / 2) {
         const int d = 2 * t;
+        float2 pw[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) pw[w] = *reinterpret_cast<const float2 *>(part + w * D + d);
         float v0 = 0.f, v1 = 0.f;
+#pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            v0 += part[w * D + d];
-            v1 += part[w * D + d + 1];
+            v0 += pw[w].x;
+            v1 += pw[w].y;
         }
         ll_store2(urs(attn, kAnyBytes), static_cast<uint32_t>(h * D + d) * 4u, ll_bf16w(v0 * inv, ea),
                   ll_bf16w(v1 * inv, ea));
