@@ -37,6 +37,7 @@
 #include <type_traits>
 
 #include "hxq_common.h"
+#include "hxq_prefill.h"
 
 namespace hxq {
 
@@ -714,6 +715,28 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64
 }
 
 // y[t, :] = sum_s w[t, s] * O[assign_pos[t*k + s], :], slots in order.
+
+// H[r, j] = silu(GU[r, j]) * GU[r, I + j] (GU fp32 [rows, 2I]), rounded to
+// x's 16-bit type: the SwiGLU product of the paired gate/up grouped launch.
+template <bool BF16>
+__global__ __launch_bounds__(256) void moe_silu_mul_kernel(const float *__restrict__ gu, int64_t rows,
+                                                          int32_t inter, uint16_t *__restrict__ h) {
+    const int64_t n = rows * inter;
+    for (int64_t i = (int64_t{blockIdx.x} * 256 + threadIdx.x) * 4; i < n; i += int64_t{gridDim.x} * 1024) {
+        const int64_t r = i / inter;
+        const int32_t c = static_cast<int32_t>(i - r * inter);
+        const float4 g = *reinterpret_cast<const float4 *>(gu + r * 2 * inter + c);
+        const float4 u = *reinterpret_cast<const float4 *>(gu + r * 2 * inter + inter + c);
+        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+        uint16_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float v = gv[k] / (1.f + expf(-gv[k])) * uv[k];
+            o[k] = BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+        }
+        *reinterpret_cast<uint2 *>(h + i) = make_uint2(o[0] | (uint32_t{o[1]} << 16), o[2] | (uint32_t{o[3]} << 16));
+    }
+}
 template <int YDT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const float *wts,
                                                           const int32_t *pos, int32_t k,
@@ -1043,6 +1066,23 @@ extern "C" int hxq_moe_grouped_gemm(const void *x, int32_t x_dtype, int64_t x_ro
     HXQ_REQUIRE(x_rows * in_features * 2 < (int64_t{1} << 31), "x too large for 32-bit offsets");
     HXQ_REQUIRE(sorted_rows || x_rows >= n_assign, "without sorted_rows x holds n_assign rows");
     if (int rc = check_bank(bank, "bank", out_features, in_features, group_size)) return rc;
+    if (pg::grouped_ok(bank, out_features, in_features, group_size)) {
+        pg::GroupedReq r{};
+        r.x = x;
+        r.x_dtype = x_dtype;
+        r.x_rows = x_rows;
+        r.rows = sorted_rows;
+        r.seg = expert_offsets;
+        r.n_exp = n_experts;
+        r.n_assign = n_assign;
+        r.bank0 = bank;
+        r.out0 = out_features;
+        r.in = in_features;
+        r.group = group_size;
+        r.y = y;
+        r.y_dtype = y_dtype;
+        return pg::grouped_gemm(r, stream);
+    }
     GemmArgs a{};
     a.x = static_cast<const uint16_t *>(x);
     a.rows = sorted_rows;
@@ -1065,7 +1105,9 @@ extern "C" int64_t hxq_moe_ffn_workspace_bytes(int64_t n_tokens, int64_t hidden,
     if (n_tokens <= 0 || hidden <= 0 || intermediate <= 0 || top_k <= 0) return -1;
     const int64_t na = n_tokens * top_k;
     const int64_t h_bytes = ((na * intermediate * 2 + 255) / 256) * 256;
-    return h_bytes + na * hidden * 4 + 256;
+    const int64_t o_bytes = ((na * hidden * 4 + 255) / 256) * 256;
+    // + the fp32 gate|up outputs of the register-dequant path
+    return h_bytes + o_bytes + na * 2 * intermediate * 4 + 256;
 }
 
 extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int64_t hidden,
@@ -1102,38 +1144,89 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     uint16_t *H = static_cast<uint16_t *>(workspace);
     float *O = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                          ((na * intermediate * 2 + 255) / 256) * 256);
-    // 1) H = silu(X_e Wg_e^T) * (X_e Wu_e^T), rows in expert-sorted order
-    GemmArgs a{};
-    a.x = static_cast<const uint16_t *>(x);
-    a.rows = sorted_rows;
-    a.seg = expert_offsets;
-    a.w[0] = wset_of(gate);
-    a.w[1] = wset_of(up);
-    a.y = H;
-    a.M = static_cast<int32_t>(na);
-    a.OUT = static_cast<int32_t>(intermediate);
-    a.K = static_cast<int32_t>(hidden);
-    a.group = group_size > 0 ? group_size : kBK;
-    a.y_dtype = x_dtype;
-    a.n_experts = n_experts;
-    a.x_rows = static_cast<int32_t>(n_tokens);
-    if (int rc = grouped_launch<true>(a, na, bf16, stream)) return rc;
-    // 2) O = H_e Wd_e^T (fp32, sorted order)
-    GemmArgs d{};
-    d.x = H;
-    d.rows = nullptr;
-    d.seg = expert_offsets;
-    d.w[0] = wset_of(down);
-    d.w[1] = d.w[0];
-    d.y = O;
-    d.M = static_cast<int32_t>(na);
-    d.OUT = static_cast<int32_t>(hidden);
-    d.K = static_cast<int32_t>(intermediate);
-    d.group = a.group;
-    d.y_dtype = HXQ_F32;
-    d.n_experts = n_experts;
-    d.x_rows = static_cast<int32_t>(na);
-    if (int rc = grouped_launch<false>(d, na, bf16, stream)) return rc;
+    float *GU = reinterpret_cast<float *>(reinterpret_cast<char *>(O) + ((na * hidden * 4 + 255) / 256) * 256);
+    const bool reg = pg::grouped_ok(gate, intermediate, hidden, group_size) &&
+                     pg::grouped_ok(up, intermediate, hidden, group_size) &&
+                     pg::grouped_ok(down, hidden, intermediate, group_size) && intermediate % 256 == 0;
+    if (reg) {
+        // 1) GU = [X_e Wg_e^T | X_e Wu_e^T] (one grouped launch, fp32), H = silu(G) * U
+        pg::GroupedReq r{};
+        r.x = x;
+        r.x_dtype = x_dtype;
+        r.x_rows = n_tokens;
+        r.rows = sorted_rows;
+        r.seg = expert_offsets;
+        r.n_exp = n_experts;
+        r.n_assign = na;
+        r.bank0 = gate;
+        r.bank1 = up;
+        r.out0 = intermediate;
+        r.out1 = intermediate;
+        r.in = hidden;
+        r.group = group_size;
+        r.y = GU;
+        r.y_dtype = HXQ_F32;
+        if (int rc = pg::grouped_gemm(r, stream)) return rc;
+        const int64_t n4 = na * intermediate / 4;
+        const dim3 sg(static_cast<uint32_t>(std::min<int64_t>((n4 + 255) / 256, 4096)));
+        if (bf16)
+            hipLaunchKernelGGL(moe_silu_mul_kernel<true>, sg, dim3(256), 0, stream, GU, na,
+                               static_cast<int32_t>(intermediate), H);
+        else
+            hipLaunchKernelGGL(moe_silu_mul_kernel<false>, sg, dim3(256), 0, stream, GU, na,
+                               static_cast<int32_t>(intermediate), H);
+        HXQ_LAUNCH_CHECK();
+        // 2) O = H_e Wd_e^T (fp32, sorted order)
+        pg::GroupedReq d{};
+        d.x = H;
+        d.x_dtype = x_dtype;
+        d.x_rows = na;
+        d.rows = nullptr;
+        d.seg = expert_offsets;
+        d.n_exp = n_experts;
+        d.n_assign = na;
+        d.bank0 = down;
+        d.out0 = hidden;
+        d.in = intermediate;
+        d.group = group_size;
+        d.y = O;
+        d.y_dtype = HXQ_F32;
+        if (int rc = pg::grouped_gemm(d, stream)) return rc;
+    }
+    if (!reg) {
+        // 1) H = silu(X_e Wg_e^T) * (X_e Wu_e^T), rows in expert-sorted order
+        GemmArgs a{};
+        a.x = static_cast<const uint16_t *>(x);
+        a.rows = sorted_rows;
+        a.seg = expert_offsets;
+        a.w[0] = wset_of(gate);
+        a.w[1] = wset_of(up);
+        a.y = H;
+        a.M = static_cast<int32_t>(na);
+        a.OUT = static_cast<int32_t>(intermediate);
+        a.K = static_cast<int32_t>(hidden);
+        a.group = group_size > 0 ? group_size : kBK;
+        a.y_dtype = x_dtype;
+        a.n_experts = n_experts;
+        a.x_rows = static_cast<int32_t>(n_tokens);
+        if (int rc = grouped_launch<true>(a, na, bf16, stream)) return rc;
+        // 2) O = H_e Wd_e^T (fp32, sorted order)
+        GemmArgs d{};
+        d.x = H;
+        d.rows = nullptr;
+        d.seg = expert_offsets;
+        d.w[0] = wset_of(down);
+        d.w[1] = d.w[0];
+        d.y = O;
+        d.M = static_cast<int32_t>(na);
+        d.OUT = static_cast<int32_t>(hidden);
+        d.K = static_cast<int32_t>(intermediate);
+        d.group = a.group;
+        d.y_dtype = HXQ_F32;
+        d.n_experts = n_experts;
+        d.x_rows = static_cast<int32_t>(na);
+        if (int rc = grouped_launch<false>(d, na, bf16, stream)) return rc;
+    }
     // 3) y[t] = sum_s w[t,s] O[pos(t,s)]
     const dim3 grid((hidden + 255) / 256, n_tokens);
     if (y_dtype == HXQ_F32)

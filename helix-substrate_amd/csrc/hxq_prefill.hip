@@ -39,6 +39,7 @@
 // operand register) -- no per-lane cursors and no divergent loops.
 // Results are written once per element (split-K: fp32 partials reduced in
 // order by a second kernel): deterministic.
+#include "hxq_prefill.h"
 #include <algorithm>
 #include <type_traits>
 
@@ -83,7 +84,55 @@ struct Args {
     int32_t t0, ntiles;         // this launch: tiles [t0, t0 + ntiles) of the order
     int32_t tiles_per_xcd;      // of this launch
     int32_t vec_out;         // 16-bit y, 16-byte aligned rows, no split: LDS-transposed stores
+    // Grouped (expert) launches: output rows are the sorted assignment list,
+    // expert e owning rows [seg[e], seg[e+1]); X row of output row r is
+    // rows[r] (rows null: r) of x_rows; output columns [0, out_split) come
+    // from bank 0 (idx .. sc_val above), [out_split, OUT) from bank 1; each
+    // bank stacks its experts at the strides below (elements of each array).
+    const int32_t *rows;
+    const int32_t *seg;
+    int32_t n_exp, out_split, x_rows, grp_tiles_x, grp_per_xcd;
+    int64_t idx_es, cb_es, ga_es, scp_es;
+    const uint8_t *idx1;
+    const float *cb1;
+    const float2 *ga1;
+    const int32_t *sc_ptr1;
+    const uint32_t *sc_key1;
+    const float *sc_val1;
 };
+
+// Row tile rt of a grouped launch: the expert e whose segment holds it, its
+// first sorted row and the segment end.  Every wave computes it alike (lanes
+// cover experts e, e + 64, ...; a wave scan of the per-expert tile counts).
+__device__ __forceinline__ bool grouped_tile(const Args &g, int bm, int rt, int &e, int &row0,
+                                             int &rend) {
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    for (int c0 = 0; c0 < g.n_exp; c0 += 64) {
+        const int ee = c0 + lane;
+        const int a = ee < g.n_exp ? g.seg[ee] : 0;
+        const int b = ee < g.n_exp ? g.seg[ee + 1] : 0;
+        const int nt = (b - a + bm - 1) / bm;
+        int inc = nt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int v = __shfl_up(inc, d);
+            if (lane >= d) inc += v;
+        }
+        const int tot = __shfl(inc, 63);
+        if (rt < base + tot) {
+            const unsigned long long m = __ballot(base + inc > rt);
+            const int L = __builtin_ctzll(m);
+            // wave-uniform results, in scalar registers (they form buffer bases)
+            e = __builtin_amdgcn_readfirstlane(c0 + L);
+            row0 = __builtin_amdgcn_readfirstlane(__shfl(a, L) + (rt - base - __shfl(inc - nt, L)) * bm);
+            rend = __builtin_amdgcn_readfirstlane(__shfl(b, L));
+            return true;
+        }
+        base += tot;
+    }
+    return false;
+}
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -140,7 +189,7 @@ __host__ __device__ constexpr int fmt_b32(int f) {
 // Activation types: XT 0 = fp16, 1 = bf16 (v_mfma_f32_32x32x16_{f16,bf16},
 // B packed as 16-bit pairs), 2 = fp32 (v_mfma_f32_32x32x2_f32, fp32 B: the
 // fp32 path keeps fp32 arithmetic end to end).
-template <int BM, int XT, bool AFFINE, int NJ, int FMT>
+template <int BM, int XT, bool AFFINE, int NJ, int FMT, bool GRP = false>
 __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const Args g) {
     constexpr bool F32 = XT == 2;
     constexpr bool BF16 = XT == 1;
@@ -165,16 +214,52 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     uint16_t *sA0 = reinterpret_cast<uint16_t *>(smem + kTblBytes);
     float *sAf0 = reinterpret_cast<float *>(smem + kTblBytes);
 
-    int tl, tx, ty;
-    if (!tile_of(g, blockIdx.x, tl, tx, ty)) return;  // block-uniform
+    int tl, tx, ty = 0;
+    // this block's rows, their bound, and its weight bank (output columns
+    // [wbase, wbase + wout) are rows [0, wout) of the bank's matrix)
+    int r0, mlim, wbase = 0, wout = g.OUT;
+    const uint8_t *gidx = g.idx;
+    const float *gcb = g.cb;
+    const float2 *gga = g.ga;
+    const int32_t *gscp = g.sc_ptr;
+    const uint32_t *gkey = g.sc_key;
+    const float *gval = g.sc_val;
+    if constexpr (GRP) {
+        // row tile rt runs on XCD rt % 8 with all its column tiles (they share
+        // its X rows in that XCD's L2); blocks are dispatched in order, so the
+        // real tiles (row tiles below the routing's count) go first on every XCD
+        const int j = blockIdx.x / kXcds;
+        const int rt = static_cast<int>(blockIdx.x % kXcds) + kXcds * (j / g.grp_tiles_x);
+        tx = j % g.grp_tiles_x;
+        tl = rt * g.grp_tiles_x + tx;
+        int e, row0, rend;
+        if (!grouped_tile(g, BM, rt, e, row0, rend)) return;  // block-uniform
+        r0 = row0;
+        mlim = rend;
+        const bool b1 = tx * kBN >= g.out_split;
+        wbase = b1 ? g.out_split : 0;
+        wout = b1 ? g.OUT - g.out_split : g.out_split;
+        gidx = (b1 ? g.idx1 : g.idx) + e * g.idx_es;
+        gcb = (b1 ? g.cb1 : g.cb) + e * g.cb_es;
+        const float2 *ga = b1 ? g.ga1 : g.ga;
+        gga = ga ? ga + e * g.ga_es : nullptr;
+        const int32_t *sp = b1 ? g.sc_ptr1 : g.sc_ptr;
+        gscp = sp ? sp + e * g.scp_es : nullptr;
+        gkey = b1 ? g.sc_key1 : g.sc_key;
+        gval = b1 ? g.sc_val1 : g.sc_val;
+    } else {
+        if (!tile_of(g, blockIdx.x, tl, tx, ty)) return;  // block-uniform
+        r0 = ty * BM;
+        mlim = g.M;
+    }
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ml = lane & 31, hh = lane >> 5;
     const int K = g.K;
-    const int r0 = ty * BM;
     const int n0 = tx * kBN;
-    const int nw = n0 + 32 * NJ * wave;      // first W row of this wave
+    const int nw = n0 + 32 * NJ * wave;      // first output column of this wave
+    const int nwr = nw - wbase;              // its first row of the bank's matrix
     const int kb = blockIdx.y * g.ks_per;    // first K step of this block's range
     const int nk = min(K / kBK - kb, g.ks_per);
     constexpr uint32_t kOob = 0x80000000u;
@@ -182,27 +267,28 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     if (lds_offset_of(tbl) != 0) return;  // never taken: no other LDS in this kernel
 
     // ---- global sources ----------------------------------------------------------
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)g.M * K * XB);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)(GRP ? g.x_rows : g.M) * K * XB);
     const int64_t row_bytes = (int64_t)K / 32 * B32;
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(g.idx, (int64_t)g.OUT * row_bytes);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(gidx, (int64_t)wout * row_bytes);
     const int ngroups = AFFINE ? K / g.group : 1;
-    const __amdgpu_buffer_rsrc_t ar = make_rsrc(g.ga, AFFINE ? (int64_t)ngroups * g.OUT * 8 : 0);
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(gga, AFFINE ? (int64_t)ngroups * wout * 8 : 0);
     // X: thread t copies chunk t % XCH of rows t / XCH + (threads / XCH) p
     const int xc = tid % XCH;
     uint32_t x_off[XP];
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
         const int r = r0 + tid / XCH + (kThreads / XCH) * p;
-        x_off[p] = r < g.M ? static_cast<uint32_t>((r * K + xc * (16 / XB)) * XB) : kOob;
+        const int xrow = GRP && g.rows && r < mlim ? g.rows[r] : r;
+        x_off[p] = r < mlim ? static_cast<uint32_t>((xrow * K + xc * (16 / XB)) * XB) : kOob;
     }
     // W rows of this lane: nw + 32j + ml
     uint32_t q_off[NJ];
     uint32_t a_off[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int n = nw + 32 * j + ml;
-        q_off[j] = n < g.OUT ? static_cast<uint32_t>(n * row_bytes + B32 * hh) : kOob;
-        a_off[j] = n < g.OUT ? static_cast<uint32_t>(n * 8) : kOob;
+        const int n = nwr + 32 * j + ml;
+        q_off[j] = n < wout ? static_cast<uint32_t>(n * row_bytes + B32 * hh) : kOob;
+        a_off[j] = n < wout ? static_cast<uint32_t>(n * 8) : kOob;
     }
 
     // ---- sidecar: the entries of each K step, one per lane ----------------------
@@ -215,17 +301,17 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
     // loads past a range read 0 and are masked when used), so that no wait
     // on a fresh load enters the pipeline.  Steps with more than 64 entries
     // in a group read the rest directly (correct, slower).
-    const bool has_sc = g.sc_ptr != nullptr && nw < g.OUT;
+    const bool has_sc = gscp != nullptr && nwr < wout;
     const int nsteps = K / kBK;
-    const int sgrp = nw >> 6;
+    const int sgrp = nwr >> 6;
     const int sp0 = sgrp * nsteps + kb;  // pointer of this block's first step
-    const int e_hi = has_sc ? g.sc_ptr[(sgrp + 1) * nsteps] : 0;  // end of the group's list
+    const int e_hi = has_sc ? gscp[(sgrp + 1) * nsteps] : 0;  // end of the group's list
     const __amdgpu_buffer_rsrc_t pr =
-        make_rsrc(g.sc_ptr, has_sc ? int64_t{4} * ((g.OUT + 63) / 64 * nsteps + 1) : 0);
-    const __amdgpu_buffer_rsrc_t kr = make_rsrc(g.sc_key, int64_t{4} * e_hi);
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(g.sc_val, int64_t{4} * e_hi);
+        make_rsrc(gscp, has_sc ? int64_t{4} * ((wout + 63) / 64 * nsteps + 1) : 0);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(gkey, int64_t{4} * e_hi);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(gval, int64_t{4} * e_hi);
     // this wave's rows within its 64-row sidecar group: [rlo, rlo + 32 NJ)
-    const uint32_t rlo = static_cast<uint32_t>(nw & 63);
+    const uint32_t rlo = static_cast<uint32_t>(nwr & 63);
     uint32_t ps[2];  // pointer of step t, loaded by load_step(t - 2) (buffer t & 1)
     uint32_t sk[2];  // keys and values of step t (buffer t & 1)
     float sv[2];
@@ -266,7 +352,7 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             }
         }
         if constexpr (AFFINE) {
-            const uint32_t gofs = (k0 / static_cast<uint32_t>(g.group)) * static_cast<uint32_t>(g.OUT) * 8u;
+            const uint32_t gofs = (k0 / static_cast<uint32_t>(g.group)) * static_cast<uint32_t>(wout) * 8u;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + gofs;
@@ -302,15 +388,15 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
 #pragma unroll
         for (int q = 0; q < 4096 / kThreads; ++q) {
             const int slot = tid + kThreads * q;  // float4 slot: entry slot / 16
-            const float c = g.cb[slot >> 4];
+            const float c = gcb[slot >> 4];
             *reinterpret_cast<float4 *>(tbl + 4 * slot) = make_float4(c, c, c, c);
         }
     } else if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
-        for (int j = tid; j < kPairCodes; j += kThreads) tbl[j] = j < g.n_codes ? g.cb[j] : 0.f;
+        for (int j = tid; j < kPairCodes; j += kThreads) tbl[j] = j < g.n_codes ? gcb[j] : 0.f;
     } else if constexpr (PAIR) {
         float2 *t2 = reinterpret_cast<float2 *>(tbl);
         for (int j = tid; j < kPairCodes; j += kThreads)
-            t2[j] = j < g.n_codes ? make_float2(g.cb[2 * j], g.cb[2 * j + 1]) : make_float2(0.f, 0.f);
+            t2[j] = j < g.n_codes ? make_float2(gcb[2 * j], gcb[2 * j + 1]) : make_float2(0.f, 0.f);
     }
 
     // ---- dequantise B into operand registers, one k substep at a time ----------
@@ -466,8 +552,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             // more than 64 entries in this step: the rest straight from the list
             for (int ob = sb[buf] + 64; ob < e_hi; ob += 64) {
                 const int e = ob + lane;
-                const uint32_t k2 = e < e_hi ? g.sc_key[e] : 0xffffffffu;
-                const float v2 = e < e_hi ? g.sc_val[e] : 0.f;
+                const uint32_t k2 = e < e_hi ? gkey[e] : 0xffffffffu;
+                const float v2 = e < e_hi ? gval[e] : 0.f;
                 apply(k2, v2, __ballot(k2 < khi && (k2 & 63u) - rlo < nrow), k1, b);
                 if (__builtin_amdgcn_readlane(k2, 63) >= khi) break;
             }
@@ -610,7 +696,7 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
             const int mr = id / QPR, q = id % QPR;
             const int m = r0 + mr, n = nw + 8 * q;
             const u32x4 v = *reinterpret_cast<const u32x4 *>(cw + cofs(mr, q));
-            if (m < g.M && n < g.OUT)
+            if (m < mlim && n < g.OUT)
                 *reinterpret_cast<u32x4 *>(yb + (int64_t)m * g.OUT + n) = v;
         }
         return;
@@ -640,7 +726,7 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const 
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = r0 + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
-                if (m >= g.M) continue;
+                if (m >= mlim) continue;
                 const int64_t o = (int64_t)m * g.OUT + n;
                 const float v = acc[i][j][r] + bv;
                 if (g.y_dtype == HXQ_F32) static_cast<float *>(g.y)[o] = v;
@@ -737,6 +823,90 @@ Plan plan(int64_t m, int64_t out, int64_t in, int cus, int bm_max = 256) {
         if (p.l[i].ks > 1)
             p.ws_bytes = std::max<int64_t>(p.ws_bytes, int64_t{4} * p.l[i].ks * p.l[i].n * p.bm * kBN);
     return p;
+}
+
+bool grouped_ok(const hxq_expert_bank *b, int64_t out, int64_t in, int32_t group) {
+    return b && b->indices && b->codebook && in % kBK == 0 && in < (int64_t{1} << 26) &&
+           (!b->group_affine || (group >= kBK && group % kBK == 0 && in % group == 0)) &&
+           (!b->sc_row_ptr || (b->sc_grp_ptr && b->sc_grp_key && b->sc_grp_val)) &&
+           out * in < (int64_t{1} << 31) &&
+           (!b->group_affine || (in / group) * out * 8 < (int64_t{1} << 31));
+}
+
+int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
+    HXQ_REQUIRE(r.x && r.seg && r.bank0 && r.y, "x, expert_offsets, bank and y are required");
+    HXQ_REQUIRE(r.x_dtype == HXQ_BF16 || r.x_dtype == HXQ_F16, "x must be bf16 or fp16");
+    HXQ_REQUIRE(r.y_dtype >= HXQ_F32 && r.y_dtype <= HXQ_F16, "bad y_dtype");
+    HXQ_REQUIRE(r.n_exp >= 1 && r.n_exp <= 256, "n_experts must be in 1..256");
+    HXQ_REQUIRE(r.n_assign > 0 && r.x_rows > 0 && r.out0 > 0 && r.in > 0, "empty problem");
+    HXQ_REQUIRE(r.rows || r.x_rows >= r.n_assign, "without sorted_rows x holds n_assign rows");
+    HXQ_REQUIRE(grouped_ok(r.bank0, r.out0, r.in, r.group), "bank not eligible for the grouped kernel");
+    HXQ_REQUIRE(!r.bank1 || (r.out1 > 0 && r.out0 % kBN == 0 && grouped_ok(r.bank1, r.out1, r.in, r.group) &&
+                             (r.bank0->group_affine != nullptr) == (r.bank1->group_affine != nullptr)),
+                "the second bank needs out0 % 256 == 0 and the same affine layout");
+    const int64_t out = r.out0 + (r.bank1 ? r.out1 : 0);
+    HXQ_REQUIRE(r.x_rows * r.in * 2 < (int64_t{1} << 31) && r.n_assign * out * 4 < (int64_t{1} << 31),
+                "problem too large for 32-bit offsets");
+    HXQ_REQUIRE((reinterpret_cast<uintptr_t>(r.x) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(r.bank0->indices) & 15u) == 0 &&
+                    (!r.bank1 || (reinterpret_cast<uintptr_t>(r.bank1->indices) & 15u) == 0),
+                "x and indices must be 16-byte aligned");
+    Args a{};
+    a.x = static_cast<const uint16_t *>(r.x);
+    a.y = r.y;
+    a.M = static_cast<int32_t>(r.n_assign);
+    a.OUT = static_cast<int32_t>(out);
+    a.K = static_cast<int32_t>(r.in);
+    const bool aff = r.bank0->group_affine != nullptr;
+    a.group = aff ? r.group : kBK;
+    a.y_dtype = r.y_dtype;
+    a.ksplit = 1;
+    a.ks_per = static_cast<int32_t>(r.in / kBK);
+    a.n_codes = 256;
+    a.rows = r.rows;
+    a.seg = r.seg;
+    a.n_exp = r.n_exp;
+    a.out_split = static_cast<int32_t>(r.bank1 ? r.out0 : out);
+    a.x_rows = static_cast<int32_t>(r.x_rows);
+    auto bank = [&](const hxq_expert_bank *b, const uint8_t *&idx, const float *&cb, const float2 *&ga,
+                    const int32_t *&sp, const uint32_t *&key, const float *&val) {
+        idx = b->indices;
+        cb = b->codebook;
+        ga = reinterpret_cast<const float2 *>(b->group_affine);
+        sp = b->sc_row_ptr ? b->sc_grp_ptr : nullptr;
+        key = b->sc_grp_key;
+        val = b->sc_grp_val;
+    };
+    bank(r.bank0, a.idx, a.cb, a.ga, a.sc_ptr, a.sc_key, a.sc_val);
+    if (r.bank1) bank(r.bank1, a.idx1, a.cb1, a.ga1, a.sc_ptr1, a.sc_key1, a.sc_val1);
+    else bank(r.bank0, a.idx1, a.cb1, a.ga1, a.sc_ptr1, a.sc_key1, a.sc_val1);
+    // both banks have the same per-expert shape (out0 == out1 when paired)
+    const int64_t wo = r.out0;
+    HXQ_REQUIRE(!r.bank1 || r.out1 == r.out0, "paired banks must have the same shape");
+    a.idx_es = wo * r.in;
+    a.cb_es = 256;
+    a.ga_es = aff ? (r.in / a.group) * wo : 0;
+    a.scp_es = (wo + 63) / 64 * (r.in / kBK) + 1;
+    // 256-row tiles when the experts average more than 192 rows, else 128
+    const int bm = r.n_assign / r.n_exp > 192 ? 256 : 128;
+    a.grp_tiles_x = static_cast<int32_t>((out + kBN - 1) / kBN);
+    const int64_t row_tiles = (r.n_assign + bm - 1) / bm + r.n_exp;  // upper bound over any routing
+    a.grp_per_xcd = static_cast<int32_t>((row_tiles + kXcds - 1) / kXcds * a.grp_tiles_x);
+    const dim3 grid(static_cast<uint32_t>(a.grp_per_xcd) * kXcds);
+    const bool bf16 = r.x_dtype == HXQ_BF16;
+#define HXQ_PG_GRP(BM_, BF_, AF_) \
+    hipLaunchKernelGGL((prefill_kernel<BM_, BF_, AF_, kNJ, HXQ_FMT_SCALAR, true>), grid, \
+                       dim3(kBN / (32 * kNJ) * 64), 0, stream, a)
+    if (bm == 256) {
+        if (bf16) { if (aff) HXQ_PG_GRP(256, 1, true); else HXQ_PG_GRP(256, 1, false); }
+        else { if (aff) HXQ_PG_GRP(256, 0, true); else HXQ_PG_GRP(256, 0, false); }
+    } else {
+        if (bf16) { if (aff) HXQ_PG_GRP(128, 1, true); else HXQ_PG_GRP(128, 1, false); }
+        else { if (aff) HXQ_PG_GRP(128, 0, true); else HXQ_PG_GRP(128, 0, false); }
+    }
+#undef HXQ_PG_GRP
+    HXQ_LAUNCH_CHECK();
+    return HXQ_OK;
 }
 
 }  // namespace pg

@@ -210,7 +210,6 @@ __global__ __launch_bounds__(256) void scan_step_kernel(const ScanArgs a, float 
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const int64_t total = (int64_t)a.batch * a.heads * a.head_dim;
     if (i >= total) return;
-    const int p = static_cast<int>(i % a.head_dim);
     const int hh = static_cast<int>((i / a.head_dim) % a.heads);
     const int b = static_cast<int>(i / ((int64_t)a.head_dim * a.heads));
     const int g = hh / (a.heads / a.ngroups);

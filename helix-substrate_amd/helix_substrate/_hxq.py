@@ -44,6 +44,7 @@ class HxqExpertBank(ctypes.Structure):
     _fields_ = [
         ("indices", P), ("codebook", P), ("group_affine", P),
         ("sc_row_ptr", P), ("sc_col", P), ("sc_val", P),
+        ("sc_grp_ptr", P), ("sc_grp_key", P), ("sc_grp_val", P),
     ]
 
 
@@ -567,12 +568,14 @@ def moe_route(logits, top_k, renormalize=False):
 
 def _bank(b):
     _need_device(b["indices"], b["codebook"], b.get("group_affine"), b.get("sc_row_ptr"),
-                 b.get("sc_col"), b.get("sc_val"))
+                 b.get("sc_col"), b.get("sc_val"), b.get("sc_grp_ptr"), b.get("sc_grp_key"),
+                 b.get("sc_grp_val"))
     if b["codebook"].dtype != torch.float32 or b["codebook"].shape[-1] != 256:
         raise ValueError("expert banks take fp32 codebooks [E, 256]")
     return HxqExpertBank(*(0 if b.get(k) is None else b[k].data_ptr()
                            for k in ("indices", "codebook", "group_affine", "sc_row_ptr",
-                                     "sc_col", "sc_val")))
+                                     "sc_col", "sc_val", "sc_grp_ptr", "sc_grp_key",
+                                     "sc_grp_val")))
 
 
 def moe_grouped_gemm(x, sorted_rows, expert_offsets, bank, n_assign, out_dtype=torch.float32):

@@ -28,6 +28,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _hxq
+from .hxq_format import sidecar_row_groups
 
 
 def _csr_of(positions, values, out_f, in_f, device):
@@ -67,12 +68,22 @@ def stack_bank(layers, device=None):
         go = torch.stack([torch.as_tensor(L["group_offset"]).to(dev).float()
                           for L in layers]).contiguous()
     rps, cols, vals = [], [], []
+    gptrs, gkeys, gvals = [], [], []
     base = 0
     for L in layers:
         rp, c, v = _csr_of(L.get("sidecar_positions"), L.get("sidecar_values"), out_f, in_f, dev)
         rps.append(rp + base)
         cols.append(c)
         vals.append(v)
+        if in_f % 64 == 0:
+            # the register-dequant kernel's order (per 64 rows, by column; the
+            # step pointers absolute into the concatenated lists)
+            rows = torch.repeat_interleave(torch.arange(out_f, device=dev),
+                                           (rp[1:] - rp[:-1]).to(torch.int64))
+            gp, gk, gv = sidecar_row_groups(rows, c, v, out_f, in_f)
+            gptrs.append(gp + base)
+            gkeys.append(gk)
+            gvals.append(gv)
         base += int(c.numel())
     if base >= 2 ** 31:
         raise ValueError("too many sidecar entries for 32-bit offsets")
@@ -82,7 +93,10 @@ def stack_bank(layers, device=None):
             "group_affine": ga,
             "group_size": int(layers[0].get("group_size") or 0) if affine else 0,
             "sc_row_ptr": torch.stack(rps).contiguous(),
-            "sc_col": torch.cat(cols).contiguous(), "sc_val": torch.cat(vals).contiguous()}
+            "sc_col": torch.cat(cols).contiguous(), "sc_val": torch.cat(vals).contiguous(),
+            "sc_grp_ptr": torch.stack(gptrs).contiguous() if gptrs else None,
+            "sc_grp_key": torch.cat(gkeys).contiguous() if gptrs else None,
+            "sc_grp_val": torch.cat(gvals).contiguous() if gptrs else None}
 
 
 def bank_to(bank, device):

@@ -317,6 +317,15 @@ typedef struct hxq_expert_bank {
     const int32_t *sc_row_ptr;
     const int32_t *sc_col;
     const float *sc_val;
+    /* The same sidecar in the prefill GEMM's order (see hxq_prefill_gemm), per
+     * expert: sc_grp_ptr [E, ceil(out/64) * in/64 + 1] holding ABSOLUTE
+     * offsets into sc_grp_key / sc_grp_val.  With it (or without any
+     * sidecar) the grouped entry points below run the register-dequant MFMA
+     * kernel of hxq_prefill_gemm; NULL with a CSR sidecar: the LDS-dequant
+     * kernel of hxq_gemm. */
+    const int32_t *sc_grp_ptr;
+    const uint32_t *sc_grp_key;
+    const float *sc_grp_val;
 } hxq_expert_bank;
 
 /*
@@ -340,8 +349,9 @@ int hxq_moe_route(const float *logits, int64_t n_tokens, int32_t n_experts, int3
  * Grouped GEMM: for each expert e and each sorted position pos in its
  * segment, Y[pos, :] = X[row(pos), :] @ W_e^T with row(pos) = sorted_rows[pos]
  * (or pos itself when sorted_rows is NULL, X then holding n_assign rows).
- * X bf16/fp16 [x_rows, in]; Y y_dtype [n_assign, out].  W_e dequantised into
- * LDS and multiplied with MFMA as in hxq_gemm.
+ * X bf16/fp16 [x_rows, in]; Y y_dtype [n_assign, out].  W_e dequantised
+ * straight into MFMA operand registers as in hxq_prefill_gemm (uint8
+ * indices; banks with sc_grp_*) or into LDS as in hxq_gemm (otherwise).
  * Replaces: HelixLinear.forward per expert (helix_linear.py:318-361) on that
  * expert's token rows.
  */
@@ -353,11 +363,16 @@ int hxq_moe_grouped_gemm(const void *x, int32_t x_dtype, int64_t x_rows,
 
 /*
  * Whole SwiGLU MoE FFN from a routing (hxq_moe_route):
- *   H = silu(X Wg_e^T) * (X Wu_e^T)   (16-bit, x's dtype; one grouped launch)
+ *   H = silu(X Wg_e^T) * (X Wu_e^T)   (16-bit, x's dtype)
  *   O = H Wd_e^T                       (fp32, sorted order)
+ * With register-dequant banks (sc_grp_*, see hxq_expert_bank) gate and up
+ * run as one grouped launch into fp32 [n_assign, 2 * intermediate] (the
+ * workspace holds it), then the SiLU product; otherwise one LDS-dequant
+ * launch with the SiLU-product epilogue.
  *   y[t] = sum_s topk_weights[t, s] * O[assign_pos[t*top_k + s]]  (slots in order)
  * x bf16/fp16 [n_tokens, hidden]; y y_dtype [n_tokens, hidden].  `workspace`
- * (device, 256-B aligned, >= hxq_moe_ffn_workspace_bytes) holds H and O.
+ * (device, 256-B aligned, >= hxq_moe_ffn_workspace_bytes) holds H, O and the
+ * fp32 gate/up outputs.
  * Replaces: the expert loop of OlmoeSparseMoeBlock.forward with HelixLinear
  * experts (helix_linear.py:318-361 per expert projection).
  */
