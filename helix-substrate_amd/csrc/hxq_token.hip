@@ -66,6 +66,9 @@ constexpr int kMaxSeq = 1024;
 static_assert(kMaxSeq + 3 * kHeadDim + kWaves * kHeadDim + kWaves + 1 <= kVStage,
               "attention scratch overlaps the staged V rows");
 constexpr int kLmRB = 1;                      // LM-head rows per load batch
+constexpr int kLmBuf = 2;                     // LM-head load batches in flight per wave
+constexpr int kLmPol = 2;                     // LM-head row loads: nt (read once per token)
+constexpr int kLmStage = 64;                  // float offset of the block's logits in LDS
 constexpr uint32_t kOob = 0x80000000u;        // buffer offset past any range: reads 0
 constexpr int kCoh = 16;                      // cache policy sc1: coherent across XCDs
 constexpr int kVmcnt0 = 0x0F70;               // s_waitcnt vmcnt(0) (expcnt, lgkmcnt untouched)
@@ -749,40 +752,43 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
 //   YACT: pair stage, bf16 act[row] = silu(gate) * up.
 enum { YF32 = 0, YACT = 1 };
 
-// Sum of one row: slices, then sidecar entries in CSR order (the caller
-// adds the bias).
-__device__ __forceinline__ float row_total(const Mat &M, int r, int S, const float *red,
-                                           int32_t j0, int32_t j1, int32_t b0, const float *ent,
-                                           const float *xl) {
-    // The terms are added in a fixed order (slices, then sidecar entries in
-    // CSR order); they are read four at a time so the LDS reads overlap
-    // (padding adds 0).
+// Lanes per row of the final pass: the most (up to 16) that keep every row
+// of the block within one 1024-thread pass.
+__device__ __forceinline__ int final_lanes(int64_t n) {
+    int L = 16;
+    while (L > 1 && n * L > kThreads) L >>= 1;
+    return L;
+}
+
+// Lane q's share of row r: slices q, q + L, ... and sidecar entries j0 + q,
+// j0 + q + L, ... (the caller reduces over the row's L lanes, then adds the
+// bias).  Entries past the LDS-staged ones (rare) are read from memory.
+__device__ __forceinline__ float row_part(const Mat &M, int r, int q, int L, int S, const float *red,
+                                          int32_t j0, int32_t j1, int32_t b0, const float *ent,
+                                          const float *xl) {
     float v = 0.f;
-    for (int s0 = 0; s0 < S; s0 += 4) {
-        float p[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) p[u] = red[r * S + min(s0 + u, S - 1)];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v += s0 + u < S ? p[u] : 0.f;
-    }
+    for (int s = q; s < S; s += L) v += red[r * S + s];
     if (M.rp) {
-        for (int32_t j = j0; j < j1; j += 4) {
-            float p[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int32_t e = min(j + u, j1 - 1) - b0;
-                p[u] = ent[min(e, kEnt - 1)];
-                if (e >= kEnt) {  // past the LDS-staged entries (rare): from memory
-                    const int32_t jj = min(j + u, j1 - 1);
-                    const float d = buf_loadf(urs(M.delta, kAnyBytes), static_cast<uint32_t>(jj) * 4u);
-                    const int32_t c = buf_loadi(urs(M.col, kAnyBytes), static_cast<uint32_t>(jj) * 4u);
-                    p[u] = xl[c] * d;
-                }
+        for (int32_t j = j0 + q; j < j1; j += L) {
+            const int32_t e = j - b0;
+            float p = ent[min(e, kEnt - 1)];
+            if (e >= kEnt) {
+                const float d = buf_loadf(urs(M.delta, kAnyBytes), static_cast<uint32_t>(j) * 4u);
+                const int32_t c = buf_loadi(urs(M.col, kAnyBytes), static_cast<uint32_t>(j) * 4u);
+                p = xl[c] * d;
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v += j + u < j1 ? p[u] : 0.f;
+            v += p;
         }
     }
+    return v;
+}
+
+// Sum over the aligned group of L lanes (L a power of two up to 16), in a
+// fixed order: every lane of the wave takes part.
+__device__ __forceinline__ float group_sum(float v, int L) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1)
+        if (m < L) v += __shfl_xor(v, m, kWave);
     return v;
 }
 
@@ -812,6 +818,7 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     // queue behind the prefetched batches (which the stream needs first
     // anyway); row pointers and sidecar products go to LDS, so few registers
     // stay live during the stream.
+    const int fl = final_lanes(G.n);  // lanes per row of the final pass
     int32_t rpv[2] = {0, 0}, ecol[2] = {0, 0}, nent[2] = {0, 0};
     float edl[2] = {0.f, 0.f}, bias[2] = {0.f, 0.f};
 #pragma unroll
@@ -821,7 +828,8 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
         const __amdgpu_buffer_rsrc_t rr = urs(M.rp, M.rp ? (M.out + 1) * 4 : 0);
         rpv[s] = buf_loadi(rr, t <= G.n ? static_cast<uint32_t>((G.lo + t) * 4) : kOob);
         const __amdgpu_buffer_rsrc_t br = urs(M.bias, M.bias ? M.out * 4 : 0);
-        bias[s] = buf_loadf(br, t < G.n ? static_cast<uint32_t>((G.lo + t) * 4) : kOob);
+        // the final pass's lane 0 of row t / L adds the bias
+        bias[s] = buf_loadf(br, t % fl == 0 && t / fl < G.n ? static_cast<uint32_t>((G.lo + t / fl) * 4) : kOob);
         const int32_t b0 = __builtin_amdgcn_readfirstlane(pf.b0[s]);
         const int32_t b1 = __builtin_amdgcn_readfirstlane(pf.b1[s]);
         nent[s] = M.rp ? b1 - b0 : 0;
@@ -889,19 +897,27 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();  // red and ent complete
 
-    // final pass: one thread per row of the block
-    if (t < G.n) {
-        const int64_t row = G.lo + t;
+    // final pass: fl lanes per row of the block (rows r = t / fl < n)
+    if (t < ((G.n * fl + kWave - 1) & ~(kWave - 1))) {  // whole waves: the lane sums shuffle
+        const int r = t / fl, q = t % fl;
+        const bool live = r < G.n;
+        const int rr = live ? r : 0;
         const int S = g.S;
-        const float v0 = row_total(G.m0, t, S, red, rps[t], rps[t + 1], rps[0], ent, xl) + bias[0];
+        float v0 = live ? row_part(G.m0, rr, q, fl, S, red, rps[rr], rps[rr + 1], rps[0], ent, xl) : 0.f;
+        v0 = group_sum(v0, fl) + bias[0];
+        const int64_t row = G.lo + r;
         if constexpr (YM == YF32) {
-            ll_store2(urs(y, kAnyBytes), static_cast<uint32_t>(G.y_off + row) * 8u, ll_hi(v0, ey),
-                      ll_lo(v0, ey));
+            if (live && q == 0)
+                ll_store2(urs(y, kAnyBytes), static_cast<uint32_t>(G.y_off + row) * 8u, ll_hi(v0, ey),
+                          ll_lo(v0, ey));
         } else {
-            const float v1 = row_total(G.m1, t, S, red + kRedCap, rps[kRps + t],
-                                       rps[kRps + t + 1], rps[kRps], ent + kEnt, xl) + bias[1];
-            ll_store1(urs(y, kAnyBytes), static_cast<uint32_t>(row) * 4u,
-                      ll_bf16w(v0 / (1.f + expf(-v0)) * v1, ey));
+            float v1 = live ? row_part(G.m1, rr, q, fl, S, red + kRedCap, rps[kRps + rr],
+                                       rps[kRps + rr + 1], rps[kRps], ent + kEnt, xl)
+                            : 0.f;
+            v1 = group_sum(v1, fl) + bias[1];
+            if (live && q == 0)
+                ll_store1(urs(y, kAnyBytes), static_cast<uint32_t>(row) * 4u,
+                          ll_bf16w(v0 / (1.f + expf(-v0)) * v1, ey));
         }
     }
     // the next stage rebuilds the tables and xl in LDS: every thread is past
@@ -1181,23 +1197,32 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
 // ---------------------------------------------------------------------------
 template <int HC>
 struct LmPre {
-    u32x4 w[2][kLmRB][2 * HC];  // 16-byte loads (8 weights) per lane and row
+    u32x4 w[kLmBuf][kLmRB][2 * HC];  // 16-byte loads (8 weights) per lane and row
 };
 
+// Row t of wave w in block b is ((t * nblocks + b) * 16 + w): at any moment
+// the whole grid reads one compact window of the table, which keeps the DRAM
+// row buffers open (one contiguous range per block would give 256 streams
+// spread over the whole table).
+__device__ __forceinline__ int64_t lm_row(const Plan &P, int wave, int64_t t) {
+    return (t * P.nblocks + static_cast<int>(blockIdx.x)) * kWaves + wave;
+}
+
 template <int HC>
-__device__ __forceinline__ void lm_load(const Plan &P, int64_t lo, int64_t n, int wave, int lane,
-                                        int64_t t0, u32x4 (&w)[kLmRB][2 * HC]) {
+__device__ __forceinline__ void lm_load(const Plan &P, int wave, int lane, int64_t t0,
+                                        u32x4 (&w)[kLmRB][2 * HC]) {
     const int32_t K = P.hidden;
     const __amdgpu_buffer_rsrc_t er = urs(P.embed, static_cast<int64_t>(P.vocab) * K * 2);
 #pragma unroll
     for (int r = 0; r < kLmRB; ++r) {
-        const int64_t rl = wave + (t0 + r) * kWaves;
-        const bool mine = rl < n;
-        const uint32_t rowb = static_cast<uint32_t>((lo + rl) * K * 2);
+        const int64_t row = lm_row(P, wave, t0 + r);
+        const bool mine = row < P.vocab;
+        const uint32_t rowb = static_cast<uint32_t>(row * K * 2);
 #pragma unroll
         for (int c = 0; c < 2 * HC; ++c) {
             const uint32_t col = c * 512 + lane * 8;
-            w[r][c] = buf_load16(er, mine && col < static_cast<uint32_t>(K) ? rowb + col * 2 : kOob);
+            w[r][c] = __builtin_amdgcn_raw_buffer_load_b128(
+                er, mine && col < static_cast<uint32_t>(K) ? rowb + col * 2 : kOob, 0, kLmPol);
         }
     }
 }
@@ -1205,9 +1230,7 @@ __device__ __forceinline__ void lm_load(const Plan &P, int64_t lo, int64_t n, in
 template <int HC>
 __device__ void lm_head(const Plan &P, LmPre<HC> &pf, float *smem, int wave, int lane) {
     const int32_t K = P.hidden;
-    const int b = blockIdx.x, nb = P.nblocks;
-    const int64_t lo = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b) / static_cast<uint32_t>(nb);
-    const int64_t n = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b + 1) / static_cast<uint32_t>(nb) - lo;
+    const int b = blockIdx.x;
     // h = bf16(final_norm * r * inv), r = xa + dn; lane holds columns c*512 + lane*8 + j
     float hx[2 * HC][8];
     float ss = 0.f;
@@ -1220,33 +1243,48 @@ __device__ void lm_head(const Plan &P, LmPre<HC> &pf, float *smem, int wave, int
     for (int c = 0; c < 2 * HC; ++c) {
         const uint32_t col = c * 512 + lane * 8;
         const bool ok = col < static_cast<uint32_t>(K);
+        u32x4 a[4], d[4];  // all eight loads in flight together
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const u32x4 a = coh_load16(ar, ok ? col * 8 + 16u * v : kOob);
-            const u32x4 d = coh_load16(dr, ok ? col * 8 + 16u * v : kOob);
-            hx[c][2 * v] = ll_f32(a[0], a[1]) + ll_f32(d[0], d[1]);
-            hx[c][2 * v + 1] = ll_f32(a[2], a[3]) + ll_f32(d[2], d[3]);
+            a[v] = coh_load16(ar, ok ? col * 8 + 16u * v : kOob);
+            d[v] = coh_load16(dr, ok ? col * 8 + 16u * v : kOob);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            hx[c][2 * v] = ll_f32(a[v][0], a[v][1]) + ll_f32(d[v][0], d[v][1]);
+            hx[c][2 * v + 1] = ll_f32(a[v][2], a[v][3]) + ll_f32(d[v][2], d[v][3]);
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss = fmaf(hx[c][j], hx[c][j], ss);
     }
     ss = wave_sum_all(ss);
     const float inv = rsqrtf(ss / K + P.eps);
+    u32x4 nw[2 * HC][2];  // the norm weights: every load issued before the first use
 #pragma unroll
     for (int c = 0; c < 2 * HC; ++c) {
         const uint32_t col = c * 512 + lane * 8;
         const bool ok = col < static_cast<uint32_t>(K);
 #pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const u32x4 w = buf_load16(wr, ok ? col * 4 + 16u * v : kOob);
+        for (int v = 0; v < 2; ++v) nw[c][v] = buf_load16(wr, ok ? col * 4 + 16u * v : kOob);
+    }
+#pragma unroll
+    for (int c = 0; c < 2 * HC; ++c) {
+        const bool ok = c * 512 + lane * 8 < K;
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                hx[c][4 * v + j] = ok ? bf16r(__uint_as_float(w[j]) * (hx[c][4 * v + j] * inv)) : 0.f;
-        }
+                hx[c][4 * v + j] = ok ? bf16r(__uint_as_float(nw[c][v][j]) * (hx[c][4 * v + j] * inv)) : 0.f;
     }
     float best = -FLT_MAX;
     int bi = 0x7fffffff;
-    const int64_t n_mine = n > wave ? (n - wave + kWaves - 1) / kWaves : 0;
+    const int64_t step = static_cast<int64_t>(P.nblocks) * kWaves;  // rows per t
+    const int64_t first = static_cast<int64_t>(b) * kWaves + wave;   // row at t = 0
+    const int64_t n_mine = P.vocab > first ? (P.vocab - first + step - 1) / step : 0;
+    // the block's logits collect in LDS and leave in one coalesced pass after
+    // the stream: a store inside the stream would sit in the same in-order
+    // counter as the row loads
+    float *lg = smem + kLmStage;
     auto compute = [&](int64_t t0, const u32x4 (&w)[kLmRB][2 * HC]) {
 #pragma unroll
         for (int r = 0; r < kLmRB; ++r) {
@@ -1261,23 +1299,22 @@ __device__ void lm_head(const Plan &P, LmPre<HC> &pf, float *smem, int wave, int
                         acc = fmaf(__uint_as_float(w[r][c][e] & 0xffff0000u), hx[c][2 * e + 1], acc);
                     }
                 const float v = wave_sum_lane63(acc);
-                const int64_t row = lo + wave + t * kWaves;
                 if (lane == kWave - 1) {
-                    P.logits[row] = v;
-                    if (v > best) { best = v; bi = static_cast<int>(row); }
+                    lg[t * kWaves + wave] = v;
+                    if (v > best) { best = v; bi = static_cast<int>(first + t * step); }
                 }
             }
         }
     };
-    for (int64_t i0 = 0; i0 < n_mine; i0 += 2 * kLmRB) {
-        compute(i0, pf.w[0]);
-        if (i0 + kLmRB >= n_mine) break;
-        lm_load<HC>(P, lo, n, wave, lane, i0 + 2 * kLmRB, pf.w[0]);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(i0 + kLmRB, pf.w[1]);
-        if (i0 + 2 * kLmRB >= n_mine) break;
-        lm_load<HC>(P, lo, n, wave, lane, i0 + 3 * kLmRB, pf.w[1]);
-        __builtin_amdgcn_sched_barrier(0);
+    // no early exits: batches past the range load nothing (out-of-range
+    // offsets), so each batch waits only for its own loads
+    for (int64_t i0 = 0; i0 < n_mine; i0 += kLmBuf * kLmRB) {
+#pragma unroll
+        for (int s = 0; s < kLmBuf; ++s) {
+            compute(i0 + s * kLmRB, pf.w[s]);
+            lm_load<HC>(P, wave, lane, i0 + (kLmBuf + s) * kLmRB, pf.w[s]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     float *bv = smem;
     int *bix = reinterpret_cast<int *>(smem + kWaves);
@@ -1286,6 +1323,14 @@ __device__ void lm_head(const Plan &P, LmPre<HC> &pf, float *smem, int wave, int
         bix[wave] = bi;
     }
     __syncthreads();
+    // wave 0 has the most rows; lg[t * 16 + w] is row lm_row(w, t)
+    const int64_t n_stage = (P.vocab > b * kWaves ? (P.vocab - b * kWaves + step - 1) / step : 0) * kWaves;
+    const __amdgpu_buffer_rsrc_t lr = urs(P.logits, static_cast<int64_t>(P.vocab) * 4);
+    for (int i = threadIdx.x; i < n_stage; i += blockDim.x) {
+        const int64_t row = lm_row(P, i % kWaves, i / kWaves);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lg[i]), lr,
+                                              row < P.vocab ? static_cast<uint32_t>(row) * 4u : kOob, 0, 0);
+    }
     if (threadIdx.x == 0) {
         float v = -FLT_MAX;
         int i = 0x7fffffff;
@@ -1474,11 +1519,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(const Plan *__restri
     arrive(P, target);
     {
         LmPre<HC> lpf;
-        const int b = blockIdx.x, nb = P.nblocks;
-        const int64_t lo = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b) / static_cast<uint32_t>(nb);
-        const int64_t n = static_cast<uint32_t>(P.vocab) * static_cast<uint32_t>(b + 1) / static_cast<uint32_t>(nb) - lo;
-        lm_load<HC>(P, lo, n, wave, lane, 0, lpf.w[0]);
-        lm_load<HC>(P, lo, n, wave, lane, kLmRB, lpf.w[1]);
+#pragma unroll
+        for (int s = 0; s < kLmBuf; ++s) lm_load<HC>(P, wave, lane, s * kLmRB, lpf.w[s]);
         if (!wait_all(P, target, sh)) return;
         lm_head<HC>(P, lpf, smem, wave, lane);
     }
@@ -1678,6 +1720,8 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     const int64_t rows_o = (d->hidden + (nb - o_b0) - 1) / (nb - o_b0);
     const int64_t rows_gu = (d->intermediate + nb - 1) / nb;
     const int64_t rows_d = (d->hidden + nb - 1) / nb;
+    HXQ_REQUIRE((d->vocab + nb * kWaves - 1) / (nb * kWaves) * kWaves + kLmStage <= lds_red_offset(d),
+                "vocab too large for the block count");
     Plan P{};
     P.hidden = d->hidden;
     P.n_layers = d->n_layers;
