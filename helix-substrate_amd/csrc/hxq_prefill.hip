@@ -190,7 +190,8 @@ __host__ __device__ constexpr int fmt_b32(int f) {
 // B packed as 16-bit pairs), 2 = fp32 (v_mfma_f32_32x32x2_f32, fp32 B: the
 // fp32 path keeps fp32 arithmetic end to end).
 template <int BM, int XT, bool AFFINE, int NJ, int FMT, bool GRP = false>
-__global__ __launch_bounds__(kBN / (32 * NJ) * 64, 1) void prefill_kernel(const Args g) {
+// 64-row tiles (80 KB of LDS) run two blocks per CU: four waves per SIMD
+__global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefill_kernel(const Args g) {
     constexpr bool F32 = XT == 2;
     constexpr bool BF16 = XT == 1;
     static_assert(!F32 || (NJ == 1 && BM == 128), "fp32 activations: 128-row tiles, NJ = 1");
@@ -833,6 +834,9 @@ bool grouped_ok(const hxq_expert_bank *b, int64_t out, int64_t in, int32_t group
            (!b->group_affine || (in / group) * out * 8 < (int64_t{1} << 31));
 }
 
+#ifndef GRP_BM64_MAX
+#define GRP_BM64_MAX 96
+#endif
 int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     HXQ_REQUIRE(r.x && r.seg && r.bank0 && r.y, "x, expert_offsets, bank and y are required");
     HXQ_REQUIRE(r.x_dtype == HXQ_BF16 || r.x_dtype == HXQ_F16, "x must be bf16 or fp16");
@@ -887,8 +891,9 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     a.cb_es = 256;
     a.ga_es = aff ? (r.in / a.group) * wo : 0;
     a.scp_es = (wo + 63) / 64 * (r.in / kBK) + 1;
-    // 256-row tiles when the experts average more than 192 rows, else 128
-    const int bm = r.n_assign / r.n_exp > 192 ? 256 : 128;
+    // 256-row tiles when the experts average more than 192 rows, 128 above 96, else 64
+    const int64_t mean_rows = r.n_assign / r.n_exp;
+    const int bm = mean_rows > 192 ? 256 : mean_rows > GRP_BM64_MAX ? 128 : 64;
     a.grp_tiles_x = static_cast<int32_t>((out + kBN - 1) / kBN);
     const int64_t row_tiles = (r.n_assign + bm - 1) / bm + r.n_exp;  // upper bound over any routing
     a.grp_per_xcd = static_cast<int32_t>((row_tiles + kXcds - 1) / kXcds * a.grp_tiles_x);
@@ -900,6 +905,9 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     if (bm == 256) {
         if (bf16) { if (aff) HXQ_PG_GRP(256, 1, true); else HXQ_PG_GRP(256, 1, false); }
         else { if (aff) HXQ_PG_GRP(256, 0, true); else HXQ_PG_GRP(256, 0, false); }
+    } else if (bm == 64) {
+        if (bf16) { if (aff) HXQ_PG_GRP(64, 1, true); else HXQ_PG_GRP(64, 1, false); }
+        else { if (aff) HXQ_PG_GRP(64, 0, true); else HXQ_PG_GRP(64, 0, false); }
     } else {
         if (bf16) { if (aff) HXQ_PG_GRP(128, 1, true); else HXQ_PG_GRP(128, 1, false); }
         else { if (aff) HXQ_PG_GRP(128, 0, true); else HXQ_PG_GRP(128, 0, false); }
