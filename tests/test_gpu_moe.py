@@ -49,8 +49,9 @@ def test_route_matches_oracle(dev, T, E, k, renorm):
 
 @pytest.mark.parametrize("T,E,k,out_f,in_f", [
     (200, 8, 2, 256, 512),      # ragged segments
-    (300, 4, 1, 384, 256),      # expert 0 takes > 128 rows -> several row tiles
+    (300, 4, 1, 384, 256),      # expert 0 takes > 128 rows -> several 64-row tiles
     (64, 16, 4, 128, 1024),     # empty experts
+    (600, 4, 1, 256, 512),      # 150 rows per expert on average: 128-row tiles
 ])
 def test_grouped_gemm_matches_oracle(dev, T, E, k, out_f, in_f):
     layers, bank = _bank(E, out_f, in_f, seed=out_f + E, dev=dev, group_size=64, sigma=0.015)
