@@ -716,18 +716,21 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64
 
 // y[t, :] = sum_s w[t, s] * O[assign_pos[t*k + s], :], slots in order.
 
-// H[r, j] = silu(GU[r, j]) * GU[r, I + j] (GU fp32 [rows, 2I]), rounded to
-// x's 16-bit type: the SwiGLU product of the paired gate/up grouped launch.
+// H[r, j] = silu(GU[r, j]) * GU[r, I + j] (GU [rows, 2I] in x's 16-bit type,
+// as the projections' outputs are), rounded to x's 16-bit type: the SwiGLU
+// product of the paired gate/up grouped launch.
 template <bool BF16>
-__global__ __launch_bounds__(256) void moe_silu_mul_kernel(const float *__restrict__ gu, int64_t rows,
+__global__ __launch_bounds__(256) void moe_silu_mul_kernel(const uint16_t *__restrict__ gu, int64_t rows,
                                                           int32_t inter, uint16_t *__restrict__ h) {
     const int64_t n = rows * inter;
+    auto f = [](uint32_t b) { return BF16 ? bf16_to_f32(static_cast<uint16_t>(b)) : f16_to_f32(static_cast<uint16_t>(b)); };
     for (int64_t i = (int64_t{blockIdx.x} * 256 + threadIdx.x) * 4; i < n; i += int64_t{gridDim.x} * 1024) {
         const int64_t r = i / inter;
         const int32_t c = static_cast<int32_t>(i - r * inter);
-        const float4 g = *reinterpret_cast<const float4 *>(gu + r * 2 * inter + c);
-        const float4 u = *reinterpret_cast<const float4 *>(gu + r * 2 * inter + inter + c);
-        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+        const uint2 g = *reinterpret_cast<const uint2 *>(gu + r * 2 * inter + c);
+        const uint2 u = *reinterpret_cast<const uint2 *>(gu + r * 2 * inter + inter + c);
+        const float gv[4] = {f(g.x & 0xffffu), f(g.x >> 16), f(g.y & 0xffffu), f(g.y >> 16)};
+        const float uv[4] = {f(u.x & 0xffffu), f(u.x >> 16), f(u.y & 0xffffu), f(u.y >> 16)};
         uint16_t o[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -737,19 +740,34 @@ __global__ __launch_bounds__(256) void moe_silu_mul_kernel(const float *__restri
         *reinterpret_cast<uint2 *>(h + i) = make_uint2(o[0] | (uint32_t{o[1]} << 16), o[2] | (uint32_t{o[3]} << 16));
     }
 }
-template <int YDT>
+// V consecutive columns per thread (V = 4 when hidden % 4 == 0: 16-byte
+// loads of O); each column's slots are added in order either way.
+template <int YDT, int V>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const float *wts,
                                                           const int32_t *pos, int32_t k,
                                                           int32_t hidden, void *y) {
     const int t = blockIdx.y;
-    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int c = (blockIdx.x * 256 + threadIdx.x) * V;
     if (c >= hidden) return;
-    float acc = 0.f;
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
     for (int s = 0; s < k; ++s) {
         const int64_t a = (int64_t)t * k + s;
-        acc = fmaf(wts[a], O[(int64_t)pos[a] * hidden + c], acc);
+        const float w = wts[a];
+        const float *o = O + (int64_t)pos[a] * hidden + c;
+        if constexpr (V == 4) {
+            const float4 f = *reinterpret_cast<const float4 *>(o);
+            acc[0] = fmaf(w, f.x, acc[0]);
+            acc[1] = fmaf(w, f.y, acc[1]);
+            acc[2] = fmaf(w, f.z, acc[2]);
+            acc[3] = fmaf(w, f.w, acc[3]);
+        } else {
+            acc[0] = fmaf(w, o[0], acc[0]);
+        }
     }
-    store_act<YDT>(y, (int64_t)t * hidden + c, acc);
+#pragma unroll
+    for (int v = 0; v < V; ++v) store_act<YDT>(y, (int64_t)t * hidden + c + v, acc[v]);
 }
 
 // y = sum over the split-K ranges in range order (+ bias), in y's dtype.
@@ -1106,8 +1124,8 @@ extern "C" int64_t hxq_moe_ffn_workspace_bytes(int64_t n_tokens, int64_t hidden,
     const int64_t na = n_tokens * top_k;
     const int64_t h_bytes = ((na * intermediate * 2 + 255) / 256) * 256;
     const int64_t o_bytes = ((na * hidden * 4 + 255) / 256) * 256;
-    // + the fp32 gate|up outputs of the register-dequant path
-    return h_bytes + o_bytes + na * 2 * intermediate * 4 + 256;
+    // + the 16-bit gate|up outputs of the register-dequant path
+    return h_bytes + o_bytes + na * 2 * intermediate * 2 + 256;
 }
 
 extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int64_t hidden,
@@ -1144,12 +1162,12 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     uint16_t *H = static_cast<uint16_t *>(workspace);
     float *O = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                          ((na * intermediate * 2 + 255) / 256) * 256);
-    float *GU = reinterpret_cast<float *>(reinterpret_cast<char *>(O) + ((na * hidden * 4 + 255) / 256) * 256);
+    uint16_t *GU = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(O) + ((na * hidden * 4 + 255) / 256) * 256);
     const bool reg = pg::grouped_ok(gate, intermediate, hidden, group_size) &&
                      pg::grouped_ok(up, intermediate, hidden, group_size) &&
                      pg::grouped_ok(down, hidden, intermediate, group_size) && intermediate % 256 == 0;
     if (reg) {
-        // 1) GU = [X_e Wg_e^T | X_e Wu_e^T] (one grouped launch, fp32), H = silu(G) * U
+        // 1) GU = [X_e Wg_e^T | X_e Wu_e^T] (one grouped launch, x's 16-bit type), H = silu(G) * U
         pg::GroupedReq r{};
         r.x = x;
         r.x_dtype = x_dtype;
@@ -1165,7 +1183,7 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
         r.in = hidden;
         r.group = group_size;
         r.y = GU;
-        r.y_dtype = HXQ_F32;
+        r.y_dtype = x_dtype;
         if (int rc = pg::grouped_gemm(r, stream)) return rc;
         const int64_t n4 = na * intermediate / 4;
         const dim3 sg(static_cast<uint32_t>(std::min<int64_t>((n4 + 255) / 256, 4096)));
@@ -1228,16 +1246,21 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
         if (int rc = grouped_launch<false>(d, na, bf16, stream)) return rc;
     }
     // 3) y[t] = sum_s w[t,s] O[pos(t,s)]
-    const dim3 grid((hidden + 255) / 256, n_tokens);
-    if (y_dtype == HXQ_F32)
-        hipLaunchKernelGGL(moe_combine_kernel<HXQ_F32>, grid, dim3(256), 0, stream, O,
-                           topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y);
-    else if (y_dtype == HXQ_BF16)
-        hipLaunchKernelGGL(moe_combine_kernel<HXQ_BF16>, grid, dim3(256), 0, stream, O,
-                           topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y);
-    else
-        hipLaunchKernelGGL(moe_combine_kernel<HXQ_F16>, grid, dim3(256), 0, stream, O,
-                           topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y);
+    const bool v4 = hidden % 4 == 0;
+    const dim3 grid((hidden + (v4 ? 1023 : 255)) / (v4 ? 1024 : 256), n_tokens);
+#define HXQ_COMBINE(YDT)                                                                     \
+    do {                                                                                      \
+        if (v4)                                                                               \
+            hipLaunchKernelGGL((moe_combine_kernel<YDT, 4>), grid, dim3(256), 0, stream, O,   \
+                               topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y); \
+        else                                                                                  \
+            hipLaunchKernelGGL((moe_combine_kernel<YDT, 1>), grid, dim3(256), 0, stream, O,   \
+                               topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y); \
+    } while (0)
+    if (y_dtype == HXQ_F32) HXQ_COMBINE(HXQ_F32);
+    else if (y_dtype == HXQ_BF16) HXQ_COMBINE(HXQ_BF16);
+    else HXQ_COMBINE(HXQ_F16);
+#undef HXQ_COMBINE
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }

@@ -872,6 +872,8 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     a.n_exp = r.n_exp;
     a.out_split = static_cast<int32_t>(r.bank1 ? r.out0 : out);
     a.x_rows = static_cast<int32_t>(r.x_rows);
+    // 16-bit outputs leave through the LDS-transposed 16-byte row stores
+    a.vec_out = r.y_dtype != HXQ_F32 && out % 8 == 0 && (reinterpret_cast<uintptr_t>(r.y) & 15u) == 0;
     auto bank = [&](const hxq_expert_bank *b, const uint8_t *&idx, const float *&cb, const float2 *&ga,
                     const int32_t *&sp, const uint32_t *&key, const float *&val) {
         idx = b->indices;

@@ -366,13 +366,14 @@ int hxq_moe_grouped_gemm(const void *x, int32_t x_dtype, int64_t x_rows,
  *   H = silu(X Wg_e^T) * (X Wu_e^T)   (16-bit, x's dtype)
  *   O = H Wd_e^T                       (fp32, sorted order)
  * With register-dequant banks (sc_grp_*, see hxq_expert_bank) gate and up
- * run as one grouped launch into fp32 [n_assign, 2 * intermediate] (the
- * workspace holds it), then the SiLU product; otherwise one LDS-dequant
- * launch with the SiLU-product epilogue.
+ * run as one grouped launch into [n_assign, 2 * intermediate] in x's dtype
+ * (each projection's output rounded like the module's; the workspace holds
+ * it), then the SiLU product; otherwise one LDS-dequant launch with the
+ * SiLU-product epilogue on the fp32 sums.
  *   y[t] = sum_s topk_weights[t, s] * O[assign_pos[t*top_k + s]]  (slots in order)
  * x bf16/fp16 [n_tokens, hidden]; y y_dtype [n_tokens, hidden].  `workspace`
  * (device, 256-B aligned, >= hxq_moe_ffn_workspace_bytes) holds H, O and the
- * fp32 gate/up outputs.
+ * gate/up outputs.
  * Replaces: the expert loop of OlmoeSparseMoeBlock.forward with HelixLinear
  * experts (helix_linear.py:318-361 per expert projection).
  */

@@ -33,7 +33,8 @@ def _bank(n, out_f, in_f, seed, dev, **kw):
 
 
 @pytest.mark.parametrize("T,E,k,renorm", [(512, 64, 8, False), (37, 8, 2, True), (1, 4, 1, False),
-                                          (300, 16, 16, False)])
+                                          (300, 16, 16, False), (100, 256, 8, True),
+                                          (3000, 32, 12, False)])
 def test_route_matches_oracle(dev, T, E, k, renorm):
     lg = _skewed_logits(T, E, T + E, dev)
     r = _hxq.moe_route(lg, k, renorm)
