@@ -662,6 +662,9 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int3
 // Count (PLACE = false) or place (PLACE = true) the assignments of expert
 // blockIdx.x.  4 waves split the assignment list into contiguous quarters;
 // positions follow assignment order (token-major), so they are deterministic.
+// A wave reads its quarter kSortU rounds of 64 ids at a time, all requested
+// before the first is used (one round trip per 512 ids, not per 64).
+constexpr int kSortU = 8;
 template <bool PLACE>
 __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64_t n_assign,
                                                        int32_t E, int32_t k, int32_t *counts,
@@ -673,9 +676,16 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64
     const int64_t per = ((n_assign + 255) / 256) * 64;  // multiple of 64
     const int64_t a0 = wave * per, a1 = min(a0 + per, n_assign);
     int cnt = 0;
-    for (int64_t a = a0; a < a1; a += 64) {
-        const bool hit = a + lane < a1 && ids[a + lane] == e;
-        cnt += __popcll(__ballot(hit));
+    for (int64_t a = a0; a < a1; a += 64 * kSortU) {
+        int v[kSortU];
+#pragma unroll
+        for (int u = 0; u < kSortU; ++u) {
+            const int64_t aa = a + 64 * u + lane;
+            v[u] = ids[aa < a1 ? aa : a0];  // in range: a0 < a1 here
+        }
+#pragma unroll
+        for (int u = 0; u < kSortU; ++u)
+            cnt += __popcll(__ballot(a + 64 * u + lane < a1 && v[u] == e));
     }
     if (!PLACE) {
         if (lane == 0) wsum[wave] = cnt;
@@ -702,15 +712,25 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64
         if (e == E - 1) offsets[E] = off + wsum[0] + wsum[1] + wsum[2] + wsum[3];
     }
     const unsigned long long below = (1ull << lane) - 1ull;
-    for (int64_t a = a0; a < a1; a += 64) {
-        const bool hit = a + lane < a1 && ids[a + lane] == e;
-        const unsigned long long mask = __ballot(hit);
-        if (hit) {
-            const int pos = base + __popcll(mask & below);
-            sorted_rows[pos] = static_cast<int32_t>((a + lane) / k);
-            assign_pos[a + lane] = pos;
+    for (int64_t a = a0; a < a1; a += 64 * kSortU) {
+        int v[kSortU];
+#pragma unroll
+        for (int u = 0; u < kSortU; ++u) {
+            const int64_t aa = a + 64 * u + lane;
+            v[u] = ids[aa < a1 ? aa : a0];
         }
-        base += __popcll(mask);
+#pragma unroll
+        for (int u = 0; u < kSortU; ++u) {
+            const int64_t aa = a + 64 * u + lane;
+            const bool hit = aa < a1 && v[u] == e;
+            const unsigned long long mask = __ballot(hit);
+            if (hit) {
+                const int pos = base + __popcll(mask & below);
+                sorted_rows[pos] = static_cast<int32_t>(aa / k);
+                assign_pos[aa] = pos;
+            }
+            base += __popcll(mask);
+        }
     }
 }
 
