@@ -603,8 +603,43 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
 // MoE routing: softmax over experts, top-k (ties -> lower expert id), and the
 // expert-sorted assignment lists.
 // ---------------------------------------------------------------------------
+// Wave64 reductions on DPP (row shuffles, row mirrors and row broadcasts:
+// VALU operations, where a __shfl_xor is an LDS permute with its round trip);
+// every lane receives the result.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_fmax(float v) {
+    const int s = __builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL,
+                                              ROW_MASK, 0xf, false);
+    return fmaxf(v, __int_as_float(s));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_imin(int v) {
+    const int s = __builtin_amdgcn_update_dpp(0x7fffffff, v, CTRL, ROW_MASK, 0xf, false);
+    return min(v, s);
+}
+__device__ __forceinline__ float wave_fmax_all(float v) {
+    v = dpp_fmax<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_fmax<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_fmax<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_fmax<0x140, 0xf>(v);  // row_mirror
+    v = dpp_fmax<0x142, 0xa>(v);  // row_bcast:15
+    v = dpp_fmax<0x143, 0xc>(v);  // row_bcast:31: lane 63 holds the maximum
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ int wave_imin_all(int v) {
+    v = dpp_imin<0xb1, 0xf>(v);
+    v = dpp_imin<0x4e, 0xf>(v);
+    v = dpp_imin<0x141, 0xf>(v);
+    v = dpp_imin<0x140, 0xf>(v);
+    v = dpp_imin<0x142, 0xa>(v);
+    v = dpp_imin<0x143, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // One wave per token; lane l holds logits l, l + 64, ... (E <= 256).  The
-// softmax denominator and each of the k picks are wave reductions.
+// softmax denominator and each of the k picks are wave reductions: a pick is
+// the wave maximum of the lanes' best values, then the lowest expert id among
+// the lanes holding it (ties -> lower expert id).
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int32_t T, int32_t E,
                                                        int32_t k, int32_t renorm, int32_t *ids,
                                                        float *wts) {
@@ -620,8 +655,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int3
         v[j] = e < E ? l[e] : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, kWave));
+    mx = wave_fmax_all(mx);
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -630,7 +664,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int3
     float picked = 0.f, my_w = 0.f;
     int my_id = 0;
     for (int s = 0; s < k; ++s) {
-        // best (value, id) of this lane, then across the wave; ties -> lower id
+        // best (value, id) of this lane; ties -> lower id
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
@@ -638,19 +672,15 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int3
             const int e = lane + 64 * j;
             if (e < E && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
         }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, kWave);
-            const int oi = __shfl_xor(bi, m, kWave);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        const float wv = wave_fmax_all(bv);
+        const int wi = wave_imin_all(bv == wv ? bi : 0x7fffffff);
         // remove the pick from its owner lane
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j == bi) v[j] = -INFINITY;
-        const float p = expf(bv - mx) / sum;
+            if (lane + 64 * j == wi) v[j] = -INFINITY;
+        const float p = expf(wv - mx) / sum;
         picked += p;
-        if (lane == s) { my_id = bi; my_w = p; }
+        if (lane == s) { my_id = wi; my_w = p; }
     }
     // lanes 0..k-1 hold the picks in order (k <= 64)
     if (lane < k) {
