@@ -63,6 +63,9 @@ def parse():
     ap.add_argument("--decode", type=int, default=1,
                     help="also run the config-1 greedy decode loop (tok/s, 128-token prompt, "
                          "256 new tokens)")
+    ap.add_argument("--decode7b", type=int, default=1,
+                    help="also run the greedy decode loop at the Qwen2.5-7B shapes (28 layers, "
+                         "hidden 3584, SwiGLU 18944; 128-token prompt, 128 new tokens)")
     return ap.parse_args()
 
 
@@ -257,11 +260,15 @@ def main():
     }
     del graph
     layer0 = layers[0]  # the CPU baseline's sample
-    if args.decode:
+    if args.decode or args.decode7b:
         del layers, descs, outs
         torch.cuda.empty_cache()
+    if args.decode:
         result["decode_config1"] = decode_bench(dev, args.layers)
         result["decode_tok_s"] = result["decode_config1"]["tok_s"]
+    if args.decode7b:
+        from helix_substrate.decoder import QWEN25_7B
+        result["decode_qwen7b"] = decode_bench(dev, QWEN25_7B.n_layers, n_new=128, base=QWEN25_7B)
     if args.prefill:
         result["prefill_config2"] = prefill_bench(dev, cpu_seconds=args.cpu_seconds)
     if args.gemv7b:
@@ -579,10 +586,12 @@ def scan_bench(dev, iters=5, cpu=True):
     return out
 
 
-def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
+def decode_bench(dev, n_layers, prompt_len=128, n_new=256, base=None):
     """Config 1 decode loop: Qwen2.5-3B-shaped (36 layers, hidden 2048, 16/2
-    heads of 128, SwiGLU 11008, vocab 151936, RoPE theta 1e6), random-init,
-    every projection HXQ (config-0 recipe), bf16 tied embedding / LM head.
+    heads of 128, SwiGLU 11008, vocab 151936, RoPE theta 1e6), or the shapes
+    of `base` (Qwen2.5-7B: 28 layers, hidden 3584, 28/4 heads, SwiGLU 18944,
+    vocab 152064), random-init, every projection HXQ (config-0 recipe), bf16
+    tied embedding / LM head.
     Greedy decode of n_new tokens after a prompt of uniform random ids, two
     ways, no host sync inside either loop:
       persistent: one cooperative launch per token (hxq_decoder_step: every
@@ -594,7 +603,7 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256):
     import torch
     from helix_substrate.decoder import QWEN25_3B, DecoderConfig, HelixDecoder
 
-    cfg = DecoderConfig(**{**QWEN25_3B.__dict__, "n_layers": n_layers,
+    cfg = DecoderConfig(**{**(base or QWEN25_3B).__dict__, "n_layers": n_layers,
                            "max_seq": prompt_len + n_new + 8})
     t0 = time.time()
     dec = HelixDecoder.synthetic(cfg, seed=0, device=dev)

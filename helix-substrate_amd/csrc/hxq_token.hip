@@ -436,6 +436,23 @@ __device__ __forceinline__ Seg make_seg(int64_t lo, int64_t n, int w, int nw, in
 
 __device__ __forceinline__ int nchunks_of(int32_t K) { return (K + kChunk - 1) / kChunk; }
 
+// Pass p of wave w in a two-pass stage (K above kWaves chunks): slice
+// w + kWaves * p is chunk w + kWaves * p alone, over every row of the block
+// (S = nchunks slices in all; a slice past the last chunk has no rows).
+__device__ __forceinline__ Seg make_seg_pass(int64_t lo, int64_t n, int w, int p, int nchunks) {
+    Seg g;
+    g.lo = lo;
+    g.n = n;
+    g.S = nchunks;
+    g.RG = 1;
+    g.rg = 0;
+    g.s_id = w + kWaves * p;
+    g.c_lo = g.s_id;
+    g.nc = g.s_id < nchunks ? 1 : 0;
+    g.n_mine = g.nc ? n : 0;
+    return g;
+}
+
 __device__ __forceinline__ Geo geo_qkv(const Plan &P, const Layer &L, int wave) {
     Geo G;
     const int b = blockIdx.x, nb = P.nblocks;
@@ -685,18 +702,19 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
                             bf16r(__uint_as_float(w[2]) * (r[2] * inv)),
                             bf16r(__uint_as_float(w[3]) * (r[3] * inv)));
     } else {
-        // K <= 16384: at most two pieces of 8 values (8 words, 32 bytes) per thread
+        // K <= XP * 8192: at most XP pieces of 8 values (8 words, 32 bytes) per thread
+        constexpr int XP = HC == 4 ? 3 : 2;
         const __amdgpu_buffer_rsrc_t xr = urs(X.xb, static_cast<int64_t>(K) * 4);
-        u32x4 w[2][2];
-        bool have[2];
+        u32x4 w[XP][2];
+        bool have[XP];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) have[j] = (t + j * kThreads) * 8 < K;
+        for (int j = 0; j < XP; ++j) have[j] = (t + j * kThreads) * 8 < K;
         __builtin_amdgcn_s_waitcnt(kVmcnt0);  // sample after the prefetched batch (see above)
         const uint64_t t0 = wall_clock64();
         for (int it = 1;; ++it) {
             bool ok = true;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < XP; ++j) {
                 const uint32_t off = have[j] ? static_cast<uint32_t>(t + j * kThreads) * 32u : kOob;
                 w[j][0] = coh_load16(xr, off);
                 w[j][1] = coh_load16(xr, off + 16u);
@@ -708,7 +726,7 @@ __device__ __forceinline__ void load_x(const Plan &P, const XSrc &X, const Geo &
             if (it % kPollCheck == 0 && gave_up(P, t0)) break;
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < XP; ++j) {
             const int i = t + j * kThreads;
             if (have[j]) {
                 float4 *dst = reinterpret_cast<float4 *>(xl + 8 * i);
@@ -802,7 +820,10 @@ struct NoNext {
 // next(): issued when the stream is done (both buffers free) -- the next
 // stage's first batch, which then lands during this stage's final pass and
 // the next stage's wait instead of after the next stage begins.
-template <int HC, int XM, int YM, int B0 = 0, bool PRE1 = true, typename Next = NoNext>
+// NP = 2: the stage's K has more than kWaves chunks; G.g is pass 0 of
+// make_seg_pass and each wave streams the block's rows once per pass (its
+// second chunk's activations are reloaded from LDS between the passes).
+template <int HC, int XM, int YM, int B0 = 0, bool PRE1 = true, int NP = 1, typename Next = NoNext>
 __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, const XSrc &X,
                                          uint32_t *y, uint32_t ey, float *smem, int tid, int lane,
                                          Next next = Next{}) {
@@ -869,13 +890,59 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     const uint32_t lane_seg = (static_cast<uint32_t>(G.seg) << 16) | (static_cast<uint32_t>(lane) * 4u);
     const float nonaff = Mw.gs != nullptr ? 0.f : 1.f;
     const int32_t n_mine = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(g.n_mine));
+    // Items of the stream: pass 0's rows padded to whole batch pairs (the two
+    // batches in flight at the start are pass 0's), then pass 1's rows.  A
+    // wave with no pass-0 rows has none in pass 1 either (its slices are
+    // chunks w and w + kWaves).
+    const Seg g1 = NP == 2 ? make_seg_pass(G.lo, G.n, __builtin_amdgcn_readfirstlane(t >> 6), 1,
+                                           nchunks_of(K))
+                           : g;
+    const int32_t n0p = NP == 2 ? (n_mine + 2 * RB - 1) / (2 * RB) * (2 * RB) : n_mine;
+    const int32_t n_all = NP == 2 ? n0p + __builtin_amdgcn_readfirstlane(static_cast<int32_t>(g1.n_mine))
+                                  : n_mine;
+    // the batch of items [t0, t0 + RB): every load issued on both passes
+    // (the pass only selects scalar fields)
+    auto load_item = [&](int32_t t0, Batch &b) {
+        const bool p1 = NP == 2 && t0 >= n0p;
+        Seg gs = g;
+        gs.lo = p1 ? g1.lo : g.lo;
+        gs.rg = p1 ? g1.rg : g.rg;
+        gs.RG = p1 ? g1.RG : g.RG;
+        gs.c_lo = p1 ? g1.c_lo : g.c_lo;
+        gs.nc = p1 ? g1.nc : g.nc;
+        gs.n_mine = p1 ? g1.n_mine : g.n_mine;
+        load_batch(Mw, gs, K, group, p1 ? t0 - n0p : t0, lane, b);
+    };
     auto compute = [&](int32_t t0, const Batch &b) {
+        const bool p1 = NP == 2 && t0 >= n0p;
+        if constexpr (NP == 2) {
+            if (t0 == n0p) {
+                // pass 1: this wave's second chunk of the activation
+                const int k0 = g1.c_lo * kChunk + lane * 16;
+                const bool ok = g1.nc > 0 && k0 < K;
+                float t2 = 0.f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float4 f = ok ? reinterpret_cast<const float4 *>(xl + k0)[v]
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+                    xv[0][4 * v] = f.x;
+                    xv[0][4 * v + 1] = f.y;
+                    xv[0][4 * v + 2] = f.z;
+                    xv[0][4 * v + 3] = f.w;
+                    t2 += (f.x + f.y) + (f.z + f.w);
+                }
+                xs[0] = t2;
+            }
+        }
+        const int32_t lt = p1 ? t0 - n0p : t0;
+        const int32_t nm = p1 ? static_cast<int32_t>(g1.n_mine) : n_mine;
+        const int32_t s_id = p1 ? g1.s_id : g.s_id;
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const int32_t tt = t0 + r;
-            if (tt < n_mine) {
+            const int32_t tt = lt + r;
+            if (tt < nm) {
                 const float v = wave_sum_lane63(row_dot(lane_seg, b, r, xv, xs, nonaff));
-                if (lane == kWave - 1) redw[(g.rg + tt * g.RG) * g.S + g.s_id] = v;
+                if (lane == kWave - 1) redw[(g.rg + tt * g.RG) * g.S + s_id] = v;
             }
             __builtin_amdgcn_sched_barrier(0);  // one row's lookups in flight at a time
         }
@@ -883,14 +950,14 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
     // The stream ends with no load in flight, so nothing after it (the final
     // pass, the next stage) waits on a load that lands in a reused register
     // -- such a wait would also wait for this stage's output stores.
-    for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
+    for (int32_t i0 = 0; i0 < n_all; i0 += 2 * RB) {
         compute(i0, pf.bt[B0]);
-        if (!PRE1 || i0 + RB >= n_mine) break;
-        load_batch(Mw, g, K, group, i0 + 2 * RB, lane, pf.bt[B0]);
+        if (!PRE1 || i0 + RB >= n_all) break;
+        load_item(i0 + 2 * RB, pf.bt[B0]);
         __builtin_amdgcn_sched_barrier(0);
         compute(i0 + RB, pf.bt[1 - B0]);
-        if (i0 + 2 * RB >= n_mine) break;
-        load_batch(Mw, g, K, group, i0 + 3 * RB, lane, pf.bt[1 - B0]);
+        if (i0 + 2 * RB >= n_all) break;
+        load_item(i0 + 3 * RB, pf.bt[1 - B0]);
         __builtin_amdgcn_sched_barrier(0);
     }
     next();
@@ -1463,14 +1530,18 @@ __device__ __forceinline__ bool do_layer(const Plan &P, int l, int pos, uint32_t
     }
     {
         tid = fresh_v(tid), wave = fresh_s(wave), lane = tid & 63;
-        const Geo Gd = geo_plain(P, L, kD, P.inter, P.s_down, wave);
+        // hidden above 2048 (HC 4): intermediate may exceed kWaves chunks, so
+        // the down stage streams its rows in two chunk passes
+        constexpr int NPD = HC == 4 ? 2 : 1;
+        Geo Gd = geo_plain(P, L, kD, P.inter, P.s_down, wave);
+        if constexpr (NPD == 2) Gd.g = make_seg_pass(Gd.lo, Gd.n, wave, 0, nchunks_of(P.inter));
         prefetch(Gd, P.group, tid, pf);
         // 5. dn = W_d act
         XSrc X{};
         X.xb = P.act + static_cast<int64_t>(l) * P.ls_act;
         X.eb = e4;
-        run_gemv<HC, XBF16, YF32>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid, e5, smem,
-                                  tid, lane, [&] {
+        run_gemv<HC, XBF16, YF32, 0, true, NPD>(P, Gd, pf, X, P.dn + static_cast<int64_t>(l) * P.ls_hid,
+                                                e5, smem, tid, lane, [&] {
                                       if (l + 1 < P.n_layers &&
                                           static_cast<int>(blockIdx.x) >= P.qkv_b0) {
                                           const Geo G1 = geo_qkv(P, P.layers[l + 1], wave);
@@ -1601,7 +1672,7 @@ static size_t lds_bytes(const hxq_decoder *d) {
                              64 + kHeadDim);
 }
 
-static int hc_of(const hxq_decoder *d) { return d->hidden <= 1024 ? 1 : 2; }
+static int hc_of(const hxq_decoder *d) { return d->hidden <= 1024 ? 1 : d->hidden <= 2048 ? 2 : 4; }
 
 }  // namespace tok
 }  // namespace hxq
@@ -1639,16 +1710,18 @@ static int check_mat(const hxq_matrix &m, int64_t out, int64_t in, int32_t group
 static int validate(const hxq_decoder *d, int nb) {
     HXQ_REQUIRE(d && d->layers && d->embed && d->final_norm && d->token && d->pos && d->logits,
                 "descriptor pointers are required");
-    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 2048 && d->hidden % 512 == 0,
-                "hidden must be 512..2048, a multiple of 512");
+    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 4096 && d->hidden % 512 == 0,
+                "hidden must be 512..4096, a multiple of 512");
     HXQ_REQUIRE(d->head_dim == kHeadDim, "head_dim must be 128");
     HXQ_REQUIRE(d->n_layers >= 1 && d->n_heads >= 1 && d->n_kv_heads >= 1 &&
                     d->n_heads % d->n_kv_heads == 0 && d->n_heads <= nb,
                 "bad head counts");
     HXQ_REQUIRE(d->n_heads * kHeadDim <= CPS * kChunk * kWaves, "too many heads");
-    HXQ_REQUIRE(d->intermediate >= 16 && d->intermediate % 16 == 0 &&
-                    d->intermediate <= CPS * kChunk * kWaves,
-                "intermediate must be a multiple of 16, at most 16384");
+    // one chunk per wave and stage; above hidden 2048 the down stage takes two
+    // chunk passes (the activation load covers 3 x 8192 values)
+    const int64_t max_inter = hc_of(d) == 4 ? 3 * 8 * kThreads : CPS * kChunk * kWaves;
+    HXQ_REQUIRE(d->intermediate >= 16 && d->intermediate % 16 == 0 && d->intermediate <= max_inter,
+                "intermediate must be a multiple of 16, at most 16384 (24576 above hidden 2048)");
     HXQ_REQUIRE(d->max_seq >= 1 && d->max_seq <= kMaxSeq, "max_seq must be 1..1024");
     HXQ_REQUIRE(d->vocab >= 1 && static_cast<int64_t>(d->vocab) * d->hidden * 2 < (int64_t{1} << 32),
                 "vocab too large");
@@ -1741,7 +1814,7 @@ extern "C" int hxq_decoder_init(const hxq_decoder *d, void *workspace, int64_t w
     P.s_qkv = choose_slices(rows_qkv, kWaves, nch_h);
     P.s_o = choose_slices(rows_o, kWaves, nch_o);
     P.s_gu = choose_slices(rows_gu, kWaves / 2, nch_h);
-    P.s_down = choose_slices(rows_d, kWaves, nch_i);
+    P.s_down = hc_of(d) == 4 ? nch_i : choose_slices(rows_d, kWaves, nch_i);
     HXQ_REQUIRE(P.s_qkv > 0 && P.s_o > 0 && P.s_gu > 0 && P.s_down > 0, "no slice split fits");
     HXQ_REQUIRE((rows_o + kWaves / P.s_o - 1) / (kWaves / P.s_o) <= RB,
                 "o stage needs more than one batch per wave");
@@ -1821,9 +1894,10 @@ extern "C" int hxq_decoder_step(const hxq_decoder *d, void *workspace, int32_t n
                                 int32_t *out_ids, hipStream_t stream) {
     clear_error();
     HXQ_REQUIRE(d && workspace && n_steps >= 0, "bad arguments");
-    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 2048, "hidden must be 512..2048");
+    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 4096, "hidden must be 512..4096");
     if (hc_of(d) == 1) return launch_steps<1>(d, workspace, n_steps, out_ids, stream);
-    return launch_steps<2>(d, workspace, n_steps, out_ids, stream);
+    if (hc_of(d) == 2) return launch_steps<2>(d, workspace, n_steps, out_ids, stream);
+    return launch_steps<4>(d, workspace, n_steps, out_ids, stream);
 }
 
 extern "C" int hxq_decoder_error(const void *workspace, const hxq_decoder *d, int32_t *err_out,

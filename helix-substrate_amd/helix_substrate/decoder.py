@@ -40,6 +40,8 @@ class DecoderConfig:
 
 QWEN25_3B = DecoderConfig(hidden=2048, n_layers=36, n_heads=16, n_kv_heads=2, head_dim=128,
                           intermediate=11008, vocab=151936)
+QWEN25_7B = DecoderConfig(hidden=3584, n_layers=28, n_heads=28, n_kv_heads=4, head_dim=128,
+                          intermediate=18944, vocab=152064)
 
 _PROJ = ("q", "k", "v", "o", "gate", "up", "down")
 

@@ -115,7 +115,13 @@ CFG2 = DecoderConfig(hidden=2048, n_layers=2, n_heads=16, n_kv_heads=2, head_dim
                      intermediate=1408, vocab=4096, rope_theta=1e6, rms_eps=1e-6, max_seq=96)
 
 
-@pytest.mark.parametrize("cfg", [CFG, CFG2], ids=["hidden512", "hidden2048"])
+# Qwen2.5-7B's layer shapes (hidden 3584, 28/4 heads, intermediate 18944): the
+# down stage's 19 chunks of K exceed the 16 waves, so it streams in two passes
+CFG7 = DecoderConfig(hidden=3584, n_layers=2, n_heads=28, n_kv_heads=4, head_dim=128,
+                     intermediate=18944, vocab=4096, rope_theta=1e6, rms_eps=1e-6, max_seq=64)
+
+
+@pytest.mark.parametrize("cfg", [CFG, CFG2, CFG7], ids=["hidden512", "hidden2048", "qwen7b_layers"])
 def test_persistent_step_matches_launch_sequence_and_oracle(dev, cfg):
     """hxq_decoder_step (one launch per token) against the per-kernel launch
     sequence on the same weights (5e-3 of max|logit|: the two paths sum the
@@ -129,6 +135,7 @@ def test_persistent_step_matches_launch_sequence_and_oracle(dev, cfg):
         b = HelixDecoder.synthetic(cfg, seed=3, device=dev, layer_fn=mk)
         b.persistent_init()
         prompt = [7, 0, cfg.vocab - 1, 100, 55, 3]
+        print(f"persistent step hidden={cfg.hidden} inter={cfg.intermediate}", flush=True)
         ref = _oracle_logits(a, prompt)
         for t, tok in enumerate(prompt):
             a.tok.fill_(tok)
