@@ -203,7 +203,7 @@ def test_persistent_rejects_position_out_of_range(dev):
     assert int(b.pos.item()) == 1
 
 
-@pytest.mark.parametrize("hidden", [512, 2048])
+@pytest.mark.parametrize("hidden", [512, 2048, 3584])
 def test_persistent_long_context_matches_launch_sequence(dev, hidden):
     """Teacher-forced decode to position ~680: the persistent kernel's attention
     preloads the first 128 value rows into registers, stages the next ones in
