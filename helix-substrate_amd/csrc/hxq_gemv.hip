@@ -11,7 +11,7 @@
 // 16 weights instead of one per weight).  This changes rounding relative to
 // dequantising first; it stays far inside the 1e-5 relative bound.
 //
-// Work decomposition (wave64, 512-thread blocks = 8 waves, 2 blocks per CU):
+// Work decomposition (wave64, 512-thread blocks = 8 waves, 1 or 2 blocks per CU):
 //   * the index matrix is streamed in "chunks" of 1024 columns: lane l of a
 //     wave loads the 16 bytes at columns [16l, 16l+16) with one dwordx4 load,
 //     so one wave load covers 1 KiB of one row, fully coalesced;
@@ -21,7 +21,8 @@
 //     CPS chunks, whose activations stay in registers for the whole kernel;
 //   * each wave walks its rows in batches of RB rows, issuing every load of a
 //     batch before computing it; two blocks per CU (16 waves) hide the
-//     latency; loads are clamped to valid addresses instead of branched
+//     latency of large launches, small ones run one block per CU (fewer
+//     codebook tables to build); loads are clamped to valid addresses instead of branched
 //     around, and results of out-of-range rows are not stored;
 //   * the 256-entry codebook lives in LDS replicated NREP times with entry j
 //     of replica r at dword j*NREP + r; lane l reads replica l % NREP, so the
@@ -629,8 +630,18 @@ static int env_int(const char *name, int dflt) {
 }
 
 static const GemvTuning &tuning() {
-    static const GemvTuning t{env_int("HXQ_GEMV_S", 0), env_int("HXQ_GEMV_BPC", 2)};
+    static const GemvTuning t{env_int("HXQ_GEMV_S", 0), env_int("HXQ_GEMV_BPC", 0)};
     return t;
+}
+
+// Blocks per CU (0 = by size): one-row launches of fewer than 8192 output rows
+// run one block per CU -- half the codebook tables to build, and a CU's eight
+// waves still keep enough rows in flight (config 1: q+k+v 8.5 -> 6.2 us, o
+// 6.4 -> 5.8 us, down 11.4 -> 11.3 us) -- larger ones (gate+up, 22016 rows:
+// 13.5 us against 13.9) and multi-row launches two.
+static int blocks_per_cu(int64_t total_rows, int n_x) {
+    if (tuning().bpc > 0) return tuning().bpc;
+    return n_x == 1 && total_rows < 8192 ? 1 : 2;
 }
 
 struct GemvPlan {
@@ -647,7 +658,7 @@ static int plan_gemv(GemvHeader &h, GemvMats &mats, int n_x, GemvPlan &pl, bool 
     int64_t total = 0;
     for (int m = 0; m < h.n_mats; ++m) total += mats.m[m].out;
     const int cus = device_cu_count();
-    const int64_t target = (int64_t)cus * std::max(1, tuning().bpc);
+    const int64_t target = (int64_t)cus * blocks_per_cu(total, n_x);
     // blocks per matrix proportional to its rows; at most 512/n_x rows a block
     const int64_t max_rows = (kWaves * kWave) / n_x;
     int64_t grid = 0;
