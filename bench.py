@@ -26,7 +26,10 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "helix-substrate_amd"))
 
+# MI355X published peaks: the roofline denominators.  device_info() prints the
+# figures the device reports (CU count, clocks, bus width) beside them.
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, KV = 2048, 11008, 256
 N_LAYERS = 36
 PROJ = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
@@ -63,6 +66,9 @@ def parse():
     ap.add_argument("--decode", type=int, default=1,
                     help="also run the config-1 greedy decode loop (tok/s, 128-token prompt, "
                          "256 new tokens)")
+    ap.add_argument("--config0", type=int, default=1,
+                    help="also time config 0 (one 2048x2048 HXQ layer, fp32 x) over 64 "
+                         "distinct copies in one HIP graph")
     ap.add_argument("--decode7b", type=int, default=1,
                     help="also run the greedy decode loop at the Qwen2.5-7B shapes (28 layers, "
                          "hidden 3584, SwiGLU 18944; 128-token prompt, 128 new tokens)")
@@ -263,12 +269,17 @@ def main():
     if args.decode or args.decode7b:
         del layers, descs, outs
         torch.cuda.empty_cache()
+    persistent = not under_profiler()
+    if (args.decode or args.decode7b) and not persistent:
+        print("[bench] rocprofv3 detected: the persistent (cooperative-launch) decode legs are "
+              "skipped; the graph decode path is timed alone", file=sys.stderr, flush=True)
     if args.decode:
-        result["decode_config1"] = decode_bench(dev, args.layers)
+        result["decode_config1"] = decode_bench(dev, args.layers, persistent=persistent)
         result["decode_tok_s"] = result["decode_config1"]["tok_s"]
     if args.decode7b:
         from helix_substrate.decoder import QWEN25_7B
-        result["decode_qwen7b"] = decode_bench(dev, QWEN25_7B.n_layers, n_new=128, base=QWEN25_7B)
+        result["decode_qwen7b"] = decode_bench(dev, QWEN25_7B.n_layers, n_new=128, base=QWEN25_7B,
+                                               persistent=persistent)
     if args.prefill:
         result["prefill_config2"] = prefill_bench(dev, cpu_seconds=args.cpu_seconds)
     if args.gemv7b:
@@ -283,9 +294,105 @@ def main():
         result["encode_cdnav3_pairs"] = encode_pairs_bench(dev, cpu=args.cpu_seconds > 0)
     if args.formats:
         result["formats_gateup"] = formats_bench(dev)
+    if args.config0:
+        result["config0_layer"] = config0_bench(dev, cpu=args.cpu_seconds > 0)
+    result["device"] = device_info(dev)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(layer0, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def device_info(dev):
+    """What the device reports, beside the published peaks the rooflines use:
+    HBM bytes/s from the memory clock and bus width (2 transfers per clock),
+    dense bf16 MFMA from CUs x engine clock x 2048 FMA per CU per clock (the
+    gfx950 dense bf16 rate).  The reported clocks are not always the peak
+    ones, so these are printed, not used."""
+    import torch
+
+    p = torch.cuda.get_device_properties(dev)
+    out = {"name": p.name, "gcn_arch": getattr(p, "gcnArchName", ""),
+           "cus": p.multi_processor_count, "hbm_bytes": p.total_memory}
+    try:
+        from helix_substrate import _hxq
+        out.update(_hxq.device_clocks())
+    except (AttributeError, RuntimeError):
+        return out
+    if out.get("mem_clock_khz") and out.get("bus_width_bits"):
+        out["hbm_gbs_from_clocks"] = round(2 * out["mem_clock_khz"] * 1e3
+                                           * out["bus_width_bits"] / 8 / 1e9, 1)
+    if out.get("clock_khz"):
+        out["bf16_tflops_from_clocks"] = round(out["cus"] * out["clock_khz"] * 1e3
+                                               * 2048 * 2 / 1e12, 1)
+    out["peaks_used"] = {"hbm_gbs": HBM_PEAK_GBS, "bf16_tflops": BF16_PEAK_TFLOPS,
+                         "source": "MI355X published"}
+    return out
+
+
+def config0_bench(dev, copies=64, cpu=True):
+    """Config 0: the single 2048 x 2048 HXQ layer (fp32 x [1, 2048], fp32 y, no
+    bias), 4.52 MB per launch -- too small to time alone, so 64 distinct
+    copies (289 MB, above the 256 MB Infinity Cache) run back to back in one
+    HIP graph.  cpu_baseline: the reference's CPU path (oracle/cpu_path
+    forward_naive, fp32, 256-row tiles) on one copy."""
+    import torch
+    from helix_substrate import _hxq, synth
+    from helix_substrate.helix_linear import HelixLinear
+
+    mods = []
+    for c in range(copies):
+        L = synth.make_layer_torch(2048, 2048, seed=50_000 + c, device=dev)
+        mods.append(HelixLinear(2048, 2048, L["codebook"], L["indices"], L["sidecar_positions"],
+                                L["sidecar_values"], group_scale=L["group_scale"],
+                                group_offset=L["group_offset"], group_size=128))
+    x = torch.randn(1, 2048, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+    ys = [torch.empty(1, 2048, device=dev) for _ in mods]
+
+    def launch():
+        for m, y in zip(mods, ys):
+            _hxq.gemv(x, m.indices, m._kcb, m.group_scale, m.group_offset, 128, m._sc_row_ptr,
+                      m._sc_col, m._sc_delta, None, out=y)
+
+    launch()
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            launch()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    ms = steady_ms(g.replay, dev, iters=20)
+    per_layer = mods[0].kernel_bytes() + 2 * 2048 * 4
+    out = {"workload": "config0: one 2048x2048 HXQ layer, fp32 x [1,2048], y fp32; 64 distinct "
+                       "copies per graph replay",
+           "bytes_per_layer": per_layer, "us_per_layer": round(1000.0 * ms / copies, 3),
+           "gbs": round(per_layer * copies / (ms * 1e-3) / 1e9, 1)}
+    out["frac_of_hbm_peak"] = round(out["gbs"] / HBM_PEAK_GBS, 4)
+    if cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import cpu_path
+
+        m = mods[0]
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        cpu_args = dict(indices=m.indices.cpu(), codebook=m.codebook.cpu(),
+                        group_scale=m.group_scale.cpu(), group_offset=m.group_offset.cpu(),
+                        group_size=128, sc_rows=m._sidecar_rows.cpu(),
+                        sc_cols=m._sidecar_cols.cpu(), sc_deltas=m._sidecar_deltas.cpu())
+        xc = x.cpu()
+        cpu_path.forward_naive(xc, **cpu_args)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 2.0 or n < 3:
+            cpu_path.forward_naive(xc, **cpu_args)
+            n += 1
+        el = (time.perf_counter() - t0) / n
+        out["cpu_baseline"] = {"us_per_layer": round(el * 1e6, 1),
+                               "gbs": round(per_layer / el / 1e9, 3),
+                               "sample": f"reference _forward_naive restated (torch CPU), {n} "
+                                         f"calls of copy 0",
+                               "kind": "port", "cores": torch.get_num_threads()}
+    del g
+    return out
 
 
 def traffic_probe(dev):
@@ -560,12 +667,9 @@ def scan_bench(dev, iters=5, cpu=True):
            "tflops": round(flops / ms / 1e9, 2),
            "mfma_gflop_executed": round(mfma_flop / 1e9, 2),
            "mfma_tflops": round(mfma_flop / ms / 1e9, 1),
-           "frac_of_bf16_mfma_peak": round(mfma_flop / ms / 1e9 / 2500.0, 4),
-           # VALU fp32 without packed math (packed fp32 is not used on this
-           # pool): 78.6 TFLOP/s; the 157.3 figure is the packed/MFMA one
-           "frac_of_fp32_valu_peak_78": round(flops / ms / 1e9 / 78.6, 4),
+           "frac_of_bf16_mfma_peak": round(mfma_flop / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
            "gbs": round(nbytes / ms / 1e6, 1), "bytes": nbytes,
-           "frac_of_hbm_peak": round(nbytes / ms / 1e6 / 8000.0, 4)}
+           "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
     if cpu:
         sys.path.insert(0, str(ROOT / "oracle"))
         import cpu_path
@@ -586,7 +690,14 @@ def scan_bench(dev, iters=5, cpu=True):
     return out
 
 
-def decode_bench(dev, n_layers, prompt_len=128, n_new=256, base=None):
+def under_profiler():
+    """True inside rocprofv3 (its tool library is preloaded and it exports
+    ROCPROF* settings)."""
+    return ("rocprof" in os.environ.get("LD_PRELOAD", "")
+            or any(k.startswith("ROCPROF") for k in os.environ))
+
+
+def decode_bench(dev, n_layers, prompt_len=128, n_new=256, base=None, persistent=True):
     """Config 1 decode loop: Qwen2.5-3B-shaped (36 layers, hidden 2048, 16/2
     heads of 128, SwiGLU 11008, vocab 151936, RoPE theta 1e6), or the shapes
     of `base` (Qwen2.5-7B: 28 layers, hidden 3584, 28/4 heads, SwiGLU 18944,
@@ -599,7 +710,9 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256, base=None):
       graph:      one HIP-graph replay per token of the per-kernel sequence
                   (HXQ GEMVs + norm/RoPE/attention/SiLU kernels + bf16 LM
                   head GEMV + argmax).
-    tok_s is the faster of the two."""
+    tok_s is the faster of the two.  persistent=False times the graph path only
+    (the bench passes it under rocprofv3: every profiled process that made
+    cooperative launches ended with SIGSEGV in the profiler's exit path)."""
     import torch
     from helix_substrate.decoder import QWEN25_3B, DecoderConfig, HelixDecoder
 
@@ -629,6 +742,16 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256, base=None):
     dec.prefill(prompt)
     torch.cuda.synchronize(dev)
     ms_graph, toks_graph = timed(lambda: dec.generate(n_new))
+    if not persistent:
+        out = {"layers": n_layers, "prompt": prompt_len, "new_tokens": n_new,
+               "ms_per_token": round(ms_graph, 4), "tok_s": round(1000.0 / ms_graph, 1),
+               "ms_per_token_graph": round(ms_graph, 4), "persistent": "skipped (profiler)",
+               "hxq_bytes_per_token": dec.hxq_bytes_per_token(),
+               "lm_head_bytes_per_token": dec.embed.numel() * 2}
+        dec.close()
+        del dec
+        torch.cuda.empty_cache()
+        return out
     # persistent path: same prompt fed token by token, then the measured run
     dec.reset()
     dec.persistent_init()

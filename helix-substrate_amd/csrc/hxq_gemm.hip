@@ -663,21 +663,28 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int3
     sum = wave_sum(sum);
     float picked = 0.f, my_w = 0.f;
     int my_id = 0;
+    // entries already picked, one bit per j: skipped by later picks, so an
+    // expert is never picked twice even when fewer than k logits are finite
+    // (the remaining picks are then the lowest unpicked ids at -inf, weight 0)
+    uint32_t taken = 0;
     for (int s = 0; s < k; ++s) {
-        // best (value, id) of this lane; ties -> lower id
+        // best (value, id) of this lane among its unpicked entries; ties -> lower id
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = lane + 64 * j;
-            if (e < E && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+            if (e < E && !(taken >> j & 1u) && (v[j] > bv || (v[j] == bv && e < bi))) {
+                bv = v[j];
+                bi = e;
+            }
         }
         const float wv = wave_fmax_all(bv);
         const int wi = wave_imin_all(bv == wv ? bi : 0x7fffffff);
-        // remove the pick from its owner lane
+        // mark the pick in its owner lane
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j == wi) v[j] = -INFINITY;
+            if (lane + 64 * j == wi) taken |= 1u << j;
         const float p = expf(wv - mx) / sum;
         picked += p;
         if (lane == s) { my_id = wi; my_w = p; }

@@ -293,16 +293,21 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             const uint32_t e = 4u * (threadIdx.x + k * NT);  // first replica slot
             cbv[k] = buf_loadf(cr, (e / NREP) * 4u);
         }
-    } else if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
-        // scalar codebook [ncodes <= 4096] fp32, one copy; entries past ncodes read 0
-        const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, M.ncodes * 4);
-#pragma unroll
-        for (int k = 0; k < TPW; ++k) cbq[k] = buf_load16(cr, 16u * (threadIdx.x + k * NT));
     } else if constexpr (FMT != HXQ_FMT_AF6) {
-        // pair codebook [ncodes, 2] fp32 as is; entries past ncodes read 0
-        const __amdgpu_buffer_rsrc_t cr = make_rsrc(M.cb, M.ncodes * 8);
+        // scalar codebook [ncodes <= 4096] fp32 or pair codebook [ncodes, 2]
+        // fp32, one copy.  Four one-dword loads per 16-byte slot: the range
+        // check of a single dword is exact, so entries past ncodes read 0
+        // whatever ncodes % 4 is (a 16-byte load straddling the end of the
+        // table would depend on how the hardware checks a partial range).
+        const __amdgpu_buffer_rsrc_t cr =
+            make_rsrc(M.cb, M.ncodes * (FMT == HXQ_FMT_SCALAR_U16 ? 4 : 8));
 #pragma unroll
-        for (int k = 0; k < TPW; ++k) cbq[k] = buf_load16(cr, 16u * (threadIdx.x + k * NT));
+        for (int k = 0; k < TPW; ++k) {
+            const uint32_t b = 16u * (threadIdx.x + k * NT);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                cbq[k][j] = static_cast<uint32_t>(buf_loadi(cr, b + 4u * j));
+        }
     }
     const __amdgpu_buffer_rsrc_t rp_r = make_rsrc(M.rp, has_sc ? (out + 1) * 4 : 0);
     // final-pass outputs: thread t handles (row lo + t / NX, activation t % NX)

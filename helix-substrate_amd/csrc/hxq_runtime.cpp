@@ -34,4 +34,20 @@ int device_cu_count() {
 
 extern "C" const char *hxq_last_error(void) { return hxq::g_last_error.c_str(); }
 
-extern "C" int hxq_abi_version(void) { return 1; }
+extern "C" int hxq_abi_version(void) { return HXQ_ABI_VERSION; }
+
+extern "C" int hxq_device_clocks(int32_t *clock_khz, int32_t *mem_clock_khz,
+                                 int32_t *bus_width_bits) {
+    hxq::clear_error();
+    HXQ_REQUIRE(clock_khz && mem_clock_khz && bus_width_bits, "output pointers are required");
+    int dev = 0;
+    HXQ_HIP_TRY(hipGetDevice(&dev));
+    int v = 0;
+    HXQ_HIP_TRY(hipDeviceGetAttribute(&v, hipDeviceAttributeClockRate, dev));
+    *clock_khz = v;
+    HXQ_HIP_TRY(hipDeviceGetAttribute(&v, hipDeviceAttributeMemoryClockRate, dev));
+    *mem_clock_khz = v;
+    HXQ_HIP_TRY(hipDeviceGetAttribute(&v, hipDeviceAttributeMemoryBusWidth, dev));
+    *bus_width_bits = v;
+    return HXQ_OK;
+}

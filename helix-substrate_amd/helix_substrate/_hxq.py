@@ -71,6 +71,7 @@ class HxqDecoder(ctypes.Structure):
 
 # name -> argtypes; every function returns int (hxq_status)
 SIGNATURES = {
+    "hxq_device_clocks": [P, P, P],
     "hxq_dequant_f32": [P, P, P, P, I32, P, P, P, I64, I64, I64, I64, P, P],
     "hxq_gemv": [P, I32, P, P, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
     "hxq_gemv_fmt": [P, I32, I32, P, P, I32, P, P, I32, P, P, P, P, P, I32, I64, I64, I64, P],
@@ -139,8 +140,13 @@ def library_path() -> Path:
     return Path(os.environ.get("HXQ_LIBRARY", Path(__file__).resolve().parent / _LIB_NAME))
 
 
+# HXQ_ABI_VERSION of include/hxq.h that the ctypes signatures below follow
+ABI_VERSION = 2
+
+
 def lib():
-    """Load libhxq.so once; raise if it was not built."""
+    """Load libhxq.so once; raise if it was not built or was built from another
+    ABI version."""
     global _lib
     if _lib is None:
         path = library_path()
@@ -158,12 +164,24 @@ def lib():
         L.hxq_last_error.restype = ctypes.c_char_p
         L.hxq_abi_version.argtypes = []
         L.hxq_abi_version.restype = ctypes.c_int
+        if L.hxq_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{path} has ABI version {L.hxq_abi_version()}, these bindings expect "
+                f"{ABI_VERSION} (include/hxq.h HXQ_ABI_VERSION): rebuild the library")
         for name, argtypes in SIGNATURES_I64.items():
             fn = getattr(L, name)
             fn.argtypes = argtypes
             fn.restype = I64
         _lib = L
     return _lib
+
+
+def device_clocks():
+    """Clocks the current device reports: {"clock_khz", "mem_clock_khz",
+    "bus_width_bits"}."""
+    vals = [ctypes.c_int32(0) for _ in range(3)]
+    _check("hxq_device_clocks", lib().hxq_device_clocks(*[ctypes.byref(v) for v in vals]))
+    return dict(zip(("clock_khz", "mem_clock_khz", "bus_width_bits"), (v.value for v in vals)))
 
 
 def _check(name: str, rc: int) -> None:

@@ -407,6 +407,10 @@ class HelixLinear(nn.Module):
         if x2.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             x2 = x2.float()
         x2 = x2.contiguous()
+        if x2.data_ptr() % 16:
+            # a contiguous view at an odd storage offset: the kernels read x
+            # with 16-byte loads, so give them an aligned copy
+            x2 = x2.clone()
         n = x2.shape[0]
         svd_on = self.has_svd and not self._cell_skip_svd
         out_dtype = torch.float32 if svd_on else x2.dtype
@@ -502,10 +506,14 @@ class HelixLinear(nn.Module):
 
     def _forward_wave(self, x: torch.Tensor) -> torch.Tensor:
         """CPU tensors, HELIX_WAVE_TILES=1: the 256-row tiles of _forward_naive run
-        on a thread pool, one worker per allowed core, each with one intra-op
-        thread and pinned to its core (reference helix_linear.py:824-879; the
-        tile -> core order is plain round-robin).  Tiles write disjoint output
-        columns, so no synchronisation is needed beyond joining the pool."""
+        on a thread pool, one worker per allowed core, each pinned once to its
+        own core (reference helix_linear.py:824-879).  Tiles write disjoint
+        output columns, so no synchronisation is needed beyond joining the pool.
+        For the duration of the call torch's intra-op thread count is set to 1
+        process-wide (each worker's matmul runs on its own core), which also
+        applies to torch work in other threads until the call returns."""
+        import itertools
+        import threading
         from concurrent.futures import ThreadPoolExecutor
 
         orig_shape = x.shape
@@ -521,19 +529,27 @@ class HelixLinear(nn.Module):
             cores = sorted(os.sched_getaffinity(0))
         except (AttributeError, OSError):
             cores = list(range(os.cpu_count() or 1))
+        n_workers = min(len(cores), len(tiles))
+        slot = itertools.count()
+        slot_lock = threading.Lock()
 
-        def work(i, r0, r1):
+        def pin():
+            # worker i of the pool takes core i: no two live workers share a core
+            with slot_lock:
+                i = next(slot)
             try:
                 os.sched_setaffinity(0, {cores[i % len(cores)]})
             except (AttributeError, OSError):
                 pass
+
+        def work(r0, r1):
             out[:, r0:r1] = x2 @ self._dequant_tile(r0, r1).t()
 
         threads = torch.get_num_threads()
         torch.set_num_threads(1)
         try:
-            with ThreadPoolExecutor(max_workers=min(len(cores), len(tiles))) as pool:
-                for f in [pool.submit(work, i, r0, r1) for i, (r0, r1) in enumerate(tiles)]:
+            with ThreadPoolExecutor(max_workers=n_workers, initializer=pin) as pool:
+                for f in [pool.submit(work, r0, r1) for r0, r1 in tiles]:
                     f.result()
         finally:
             torch.set_num_threads(threads)

@@ -87,8 +87,23 @@ typedef enum hxq_format {
 /* Message for the last failed call on this thread ("" if none). */
 const char *hxq_last_error(void);
 
-/* ABI version of this library (bumped on any signature change). */
+/*
+ * ABI version of this library (bumped on any signature or struct-layout
+ * change).  A caller compares hxq_abi_version() with the HXQ_ABI_VERSION it
+ * was built against and refuses to run on a mismatch.
+ *   1: first release.
+ *   2: hxq_expert_bank gained sc_grp_ptr / sc_grp_key / sc_grp_val (the
+ *      per-step sidecar lists of the register-dequant grouped GEMM).
+ */
+#define HXQ_ABI_VERSION 2
 int hxq_abi_version(void);
+
+/*
+ * Clocks the current device reports: peak engine clock and memory clock in
+ * kHz, memory bus width in bits (for printing next to the published peaks).
+ * No counterpart in the reference (its benchmarks hard-code device figures).
+ */
+int hxq_device_clocks(int32_t *clock_khz, int32_t *mem_clock_khz, int32_t *bus_width_bits);
 
 /*
  * Reconstruct rows [row_begin, row_end) of W into w_out

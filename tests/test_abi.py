@@ -45,7 +45,10 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.hxq_abi_version() >= 1
+    from helix_substrate import _hxq
+    assert lib.hxq_abi_version() == _hxq.ABI_VERSION
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "hxq.h").read_text()
+    assert f"#define HXQ_ABI_VERSION {_hxq.ABI_VERSION}" in hdr
 
 
 def test_python_signatures_cover_header(lib):

@@ -30,6 +30,7 @@ def _dense(m):
 
 
 def _oracle_logits(dec, tokens):
+    cfg = dec.cfg
     layers = []
     for L in dec.layers:
         d = {n: _dense(L[n]) for n in ("q", "k", "v", "o", "gate", "up", "down")}
@@ -38,8 +39,8 @@ def _oracle_logits(dec, tokens):
                  post_norm=L["post_norm"].cpu().numpy())
         layers.append(d)
     return oracle.qwen2_logits_np(tokens, dec.embed.float().cpu().numpy(), layers,
-                                  dec.final_norm.cpu().numpy(), CFG.n_heads, CFG.n_kv_heads,
-                                  CFG.head_dim, CFG.rope_theta, CFG.rms_eps)
+                                  dec.final_norm.cpu().numpy(), cfg.n_heads, cfg.n_kv_heads,
+                                  cfg.head_dim, cfg.rope_theta, cfg.rms_eps)
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -121,7 +122,22 @@ CFG7 = DecoderConfig(hidden=3584, n_layers=2, n_heads=28, n_kv_heads=4, head_dim
                      intermediate=18944, vocab=4096, rope_theta=1e6, rms_eps=1e-6, max_seq=64)
 
 
-@pytest.mark.parametrize("cfg", [CFG, CFG2, CFG7], ids=["hidden512", "hidden2048", "qwen7b_layers"])
+# the largest hidden size the persistent kernel accepts (the activation load
+# covers 1024 threads x 4 values exactly; the LM head splits into 8 pieces)
+CFG4096 = DecoderConfig(hidden=4096, n_layers=2, n_heads=32, n_kv_heads=8, head_dim=128,
+                        intermediate=14336, vocab=4096, rope_theta=1e6, rms_eps=1e-6, max_seq=64)
+
+
+def _layer_fn(cfg):
+    """numpy layers (group 64) for small shapes; the device generator (group
+    128, the config-0 recipe) where numpy would take tens of seconds."""
+    if cfg.hidden * cfg.intermediate <= 2048 * 2048:
+        return lambda o, i, s: synth.make_layer_np(o, i, seed=s, group_size=64)
+    return None
+
+
+@pytest.mark.parametrize("cfg", [CFG, CFG2, CFG7, CFG4096],
+                         ids=["hidden512", "hidden2048", "qwen7b_layers", "hidden4096"])
 def test_persistent_step_matches_launch_sequence_and_oracle(dev, cfg):
     """hxq_decoder_step (one launch per token) against the per-kernel launch
     sequence on the same weights (5e-3 of max|logit|: the two paths sum the
@@ -130,7 +146,7 @@ def test_persistent_step_matches_launch_sequence_and_oracle(dev, cfg):
     global CFG
     saved, CFG = CFG, cfg
     try:
-        mk = lambda o, i, s: synth.make_layer_np(o, i, seed=s, group_size=64)
+        mk = _layer_fn(cfg)
         a = HelixDecoder.synthetic(cfg, seed=3, device=dev, layer_fn=mk)
         b = HelixDecoder.synthetic(cfg, seed=3, device=dev, layer_fn=mk)
         b.persistent_init()
@@ -203,7 +219,7 @@ def test_persistent_rejects_position_out_of_range(dev):
     assert int(b.pos.item()) == 1
 
 
-@pytest.mark.parametrize("hidden", [512, 2048, 3584])
+@pytest.mark.parametrize("hidden", [512, 2048, 3584, 4096])
 def test_persistent_long_context_matches_launch_sequence(dev, hidden):
     """Teacher-forced decode to position ~680: the persistent kernel's attention
     preloads the first 128 value rows into registers, stages the next ones in
@@ -247,3 +263,39 @@ def test_persistent_long_context_matches_launch_sequence(dev, hidden):
             assert d <= 2e-2 * vc_a[:len(prompt)].float().abs().max().item()
     finally:
         CFG = saved
+
+
+def test_persistent_config1_shape_matches_launch_sequence_and_oracle(dev):
+    """Benchmark config 1's layer shape at full size (hidden 2048, 16/2 heads,
+    SwiGLU 11008 -- eleven K chunks in the down stage -- and the 151,936-row
+    bf16 LM head), two layers, config-0 weights (group 128).  132 teacher-forced
+    tokens; at sampled positions on both sides of 128 (where the attention's
+    register-resident value rows end) the persistent kernel's logits against
+    the per-kernel launch sequence (5e-3 of max|logit|) and the fp64 oracle
+    (2e-2), and its greedy token against the argmax of its own logits."""
+    cfg = DecoderConfig(hidden=2048, n_layers=2, n_heads=16, n_kv_heads=2, head_dim=128,
+                        intermediate=11008, vocab=151936, rope_theta=1e6, rms_eps=1e-6,
+                        max_seq=160)
+    a = HelixDecoder.synthetic(cfg, seed=8, device=dev)
+    b = HelixDecoder.synthetic(cfg, seed=8, device=dev)
+    b.persistent_init()
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab, 132).tolist()
+    checks = (0, 1, 5, 64, 127, 128, 129, 131)
+    print(f"config-1 persistent step tokens={len(prompt)}", flush=True)
+    ref = _oracle_logits(a, prompt)
+    for t, tok in enumerate(prompt):
+        a.tok.fill_(tok)
+        b.tok.fill_(tok)
+        a._step_launches()
+        b.step_persistent(1)
+        if t in checks:
+            la, lb = a.logits.cpu().numpy(), b.logits.cpu().numpy()
+            scale = np.abs(la).max()
+            assert np.abs(la - lb).max() <= 5e-3 * scale, (t, np.abs(la - lb).max() / scale)
+            assert np.abs(lb - ref[t]).max() <= 2e-2 * np.abs(ref[t]).max(), t
+            assert np.abs(la - ref[t]).max() <= 2e-2 * np.abs(ref[t]).max(), t
+            assert int(b.tok.item()) == int(np.argmax(lb))
+    assert b.persistent_error() == 0
+    assert int(b.pos.item()) == len(prompt)
+    a.close()
+    b.close()

@@ -99,6 +99,27 @@ def test_gemv_fmt_matches_oracle(dev, fmt, out, inp, n, xdt):
     assert _maxrel(y.cpu().numpy(), ref) <= (1e-5 if xdt == torch.float32 else 2e-2)
 
 
+@pytest.mark.parametrize("fmt", [_hxq.FMT_VQ2_U16, _hxq.FMT_VQ2_P12])
+@pytest.mark.parametrize("k", [1001, 999])
+def test_gemv_fmt_odd_pair_count(dev, fmt, k):
+    """A pair codebook whose byte size is not a multiple of 16 (the table's
+    last 16-byte slot holds one pair): the GEMV against the oracle and against
+    the dequant kernel's W on the same inputs."""
+    out, inp = 640, 2048
+    raw, cb, s, o, pos, val, W, W0 = _case(fmt, out, inp, k=k, seed=k)
+    rp, col, sval, delta = _csr(dev, pos, val, W0, out, inp)
+    raw_d, cb_d = _dev(dev, raw, cb)
+    print(f"gemv fmt={fmt} odd pair count k={k}", flush=True)
+    Wd = _hxq.dequant_fmt(fmt, raw_d, out, inp, codebook=cb_d, sc_row_ptr=rp, sc_col=col,
+                          sc_val=sval)
+    np.testing.assert_array_equal(Wd.cpu().numpy(), W)
+    x = torch.randn(2, inp, generator=torch.Generator().manual_seed(k))
+    y = _hxq.gemv_fmt(x.to(dev), fmt, raw_d, out, codebook=cb_d, sc_row_ptr=rp, sc_col=col,
+                      sc_delta=delta)
+    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), W)) <= 1e-5
+    assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), Wd.cpu().numpy())) <= 1e-5
+
+
 @pytest.mark.parametrize("packed", [False, True])
 def test_pair_helix_linear_device(dev, packed):
     rs = np.random.RandomState(6)
@@ -228,6 +249,8 @@ def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001, group_size=128
     (512, 2048, 2048, True),     # the reference's k = 512 case at config-0 size
     (4096, 300, 1024, True),     # largest codebook, ragged rows
     (1000, 256, 11008, False),   # long rows, no affine
+    (257, 300, 1024, True),      # table ends one entry into a 16-byte slot
+    (258, 512, 2048, False),     # ... two entries into it
 ])
 def test_wide_scalar_dequant_and_gemv(dev, k, out_f, in_f, affine):
     print(f"uint16 scalar k={k} out={out_f} in={in_f} affine={affine}", flush=True)

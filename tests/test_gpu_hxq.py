@@ -267,3 +267,20 @@ def test_gemv_few_rows_long_k(dev, n):
     y = m(x.to(dev))
     assert m._last_dispatch_path == "hip_gemv"
     assert _maxrel(y.cpu().numpy(), oracle.linear_f64(x.numpy(), _oracle_w(L))) <= TOL_F32
+
+
+@pytest.mark.parametrize("dt,n", [(torch.float32, 1), (torch.bfloat16, 3), (torch.bfloat16, 40),
+                                  (torch.float32, 9)])
+def test_unaligned_contiguous_view(dev, dt, n):
+    """x a contiguous view at a storage offset that is not 16-byte aligned (the
+    kernels read x with 16-byte loads): forward computes, on the GEMV (<= 4
+    rows) and GEMM paths alike, and equals the aligned input's result."""
+    L, T = _layer(384, 512, seed=31)
+    mod = _module(T, dev)
+    buf = torch.randn(n * 512 + 1, generator=torch.Generator().manual_seed(n)).to(dt).to(dev)
+    x = buf[1:].view(n, 512)
+    assert x.is_contiguous() and x.data_ptr() % 16 != 0
+    y = mod(x)
+    assert torch.equal(y, mod(x.clone()))
+    ref = oracle.linear_f64(x.float().cpu().numpy(), _oracle_w(L))
+    assert _maxrel(y.float().cpu().numpy(), ref) <= (TOL_F32 if dt == torch.float32 else TOL_BF16)

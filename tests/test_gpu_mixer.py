@@ -140,3 +140,30 @@ def test_gated_rmsnorm_register_path(dev, width, ydt, odt):
                                   w.numpy(), 1e-5)
     assert out.dtype == odt
     assert _rel(out.float().cpu().numpy(), ref) <= (1e-5 if odt == torch.float32 else 8e-3)
+
+
+def test_mixer_config3_shape_matches_oracle(dev):
+    """Benchmark config 3's mixer at full width: d_model 2048, d_inner 4096
+    (64 heads of 64), d_state 128, one group (4352 conv channels), group-128
+    HXQ in_proj 8512 x 2048 and out_proj 2048 x 4096, chunk 256.  bf16
+    prefill of 2 x 160 tokens (crossing the scan kernel's 64-token chunks)
+    then 3 cached single-token steps, against the fp64 oracle at the bf16
+    bar; the final conv and SSM states too."""
+    m, Win, Wout, p = _mixer(d_model=2048, heads=64, head_dim=64, state=128, seed=21,
+                             device=dev, group_size=128, chunk_size=256)
+    b, L, n_step = 2, 160, 3
+    hs = torch.randn(b, L + n_step, 2048, generator=torch.Generator().manual_seed(4))
+    hs16 = hs.to(torch.bfloat16)
+    print(f"config-3 mixer b={b} L={L}", flush=True)
+    ref, conv_ref, h_ref = _oracle(m, Win, Wout, {k: v.cpu() for k, v in p.items()},
+                                   hs16[:, :L].float().numpy())
+    st = m.new_state(b, dev)
+    out = m(hs16[:, :L].to(dev), st)
+    assert out.dtype == torch.bfloat16
+    assert _rel(out.float().cpu().numpy(), ref) <= 2e-2
+    assert _rel(st[0].cpu().numpy(), conv_ref) <= 2e-2
+    assert _rel(st[1].cpu().numpy(), h_ref) <= 2e-2
+    full, _, _ = _oracle(m, Win, Wout, {k: v.cpu() for k, v in p.items()}, hs16.float().numpy())
+    for t in range(L, L + n_step):
+        o = m.step(hs16[:, t].to(dev), st)
+        assert _rel(o.float().cpu().numpy(), full[:, t]) <= 2e-2, t

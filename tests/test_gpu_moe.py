@@ -48,6 +48,29 @@ def test_route_matches_oracle(dev, T, E, k, renorm):
     assert np.array_equal(r.assign_pos.cpu().numpy(), pos)
 
 
+@pytest.mark.parametrize("renorm", [False, True])
+def test_route_masked_experts_no_duplicates(dev, renorm):
+    """Masked experts (-inf logits) and k above the number of finite logits:
+    every token still gets k distinct experts (the finite ones by logit, then
+    the lowest masked ids at weight 0), as torch.topk and the oracle do."""
+    T, E, k = 70, 16, 6
+    g = torch.Generator().manual_seed(11)
+    lg = torch.randn(T, E, generator=g)
+    n_fin = torch.randint(1, k, (T,), generator=g)       # 1..k-1 finite logits per token
+    for t in range(T):
+        masked = torch.randperm(E, generator=g)[n_fin[t]:]
+        lg[t, masked] = float("-inf")
+    r = _hxq.moe_route(lg.to(dev), k, renorm)
+    ids = r.topk_ids.cpu().numpy()
+    assert all(len(set(row)) == k for row in ids.tolist())
+    ids_o, w_o = oracle.moe_route_np(lg.numpy(), k, renorm)
+    assert np.array_equal(ids, ids_o)
+    np.testing.assert_allclose(r.topk_weights.cpu().numpy(), w_o, rtol=1e-6, atol=0)
+    top = torch.topk(lg, k, dim=1)
+    fin = torch.isfinite(top.values)
+    assert torch.equal(torch.from_numpy(ids)[fin].long(), top.indices[fin])
+
+
 @pytest.mark.parametrize("T,E,k,out_f,in_f", [
     (200, 8, 2, 256, 512),      # ragged segments
     (300, 4, 1, 384, 256),      # expert 0 takes > 128 rows -> several 64-row tiles

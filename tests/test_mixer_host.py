@@ -38,22 +38,25 @@ def test_softplus_and_gated_norm_closed_forms():
     assert np.abs(oracle.gated_rmsnorm_np(v, np.zeros_like(v), np.ones(2), 1e-5)).max() == 0.0
 
 
-def _mixer(d_model=128, heads=4, head_dim=32, state=16, ngroups=1, seed=0, device="cpu"):
+def _mixer(d_model=128, heads=4, head_dim=32, state=16, ngroups=1, seed=0, device="cpu",
+           group_size=64, chunk_size=None):
     I = heads * head_dim
     pw = 2 * I + 2 * ngroups * state + heads
-    Lin = synth.make_layer_np(pw, d_model, seed=seed, group_size=64)
-    Lout = synth.make_layer_np(d_model, I, seed=seed + 1, group_size=64)
+    Lin = synth.make_layer_np(pw, d_model, seed=seed, group_size=group_size)
+    Lout = synth.make_layer_np(d_model, I, seed=seed + 1, group_size=group_size)
     mk = lambda L: HelixLinear(L["indices"].shape[1], L["indices"].shape[0],
                                torch.from_numpy(L["codebook"]), torch.from_numpy(L["indices"]),
                                torch.from_numpy(L["sidecar_positions"]),
                                torch.from_numpy(L["sidecar_values"]),
                                group_scale=torch.from_numpy(L["group_scale"]),
-                               group_offset=torch.from_numpy(L["group_offset"]), group_size=64)
+                               group_offset=torch.from_numpy(L["group_offset"]),
+                               group_size=group_size)
     p = random_mixer_params(d_model, heads, head_dim, state, ngroups, 4, seed=seed)
     m = HelixMamba2Mixer(mk(Lin), mk(Lout), p["conv_weight"], p["conv_bias"], p["dt_bias"],
                          p["A_log"], p["D"], p["norm_weight"], num_heads=heads,
                          head_dim=head_dim, ssm_state_size=state, n_groups=ngroups, eps=1e-5,
-                         time_step_min=1e-3)
+                         time_step_min=1e-3, **({} if chunk_size is None else
+                                                {"chunk_size": chunk_size}))
     Win, Wout = oracle.reconstruct(**Lin), oracle.reconstruct(**Lout)
     return m.to(device), Win, Wout, p
 
