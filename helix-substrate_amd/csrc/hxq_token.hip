@@ -1710,8 +1710,11 @@ static int check_mat(const hxq_matrix &m, int64_t out, int64_t in, int32_t group
 static int validate(const hxq_decoder *d, int nb) {
     HXQ_REQUIRE(d && d->layers && d->embed && d->final_norm && d->token && d->pos && d->logits,
                 "descriptor pointers are required");
-    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 4096 && d->hidden % 512 == 0,
-                "hidden must be 512..4096, a multiple of 512");
+    // two codebook tables plus the hidden-wide activation row must fit the
+    // 160 KB of LDS next to the staging areas: hidden 3584 is the largest
+    // multiple of 512 that does
+    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 3584 && d->hidden % 512 == 0,
+                "hidden must be 512..3584, a multiple of 512");
     HXQ_REQUIRE(d->head_dim == kHeadDim, "head_dim must be 128");
     HXQ_REQUIRE(d->n_layers >= 1 && d->n_heads >= 1 && d->n_kv_heads >= 1 &&
                     d->n_heads % d->n_kv_heads == 0 && d->n_heads <= nb,
@@ -1894,7 +1897,7 @@ extern "C" int hxq_decoder_step(const hxq_decoder *d, void *workspace, int32_t n
                                 int32_t *out_ids, hipStream_t stream) {
     clear_error();
     HXQ_REQUIRE(d && workspace && n_steps >= 0, "bad arguments");
-    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 4096, "hidden must be 512..4096");
+    HXQ_REQUIRE(d->hidden >= 512 && d->hidden <= 3584, "hidden must be 512..3584");
     if (hc_of(d) == 1) return launch_steps<1>(d, workspace, n_steps, out_ids, stream);
     if (hc_of(d) == 2) return launch_steps<2>(d, workspace, n_steps, out_ids, stream);
     return launch_steps<4>(d, workspace, n_steps, out_ids, stream);

@@ -616,7 +616,7 @@ int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capac
  * ignored), fp32 norm weights and bf16 caches [max_seq, n_kv_heads, 128].
  * hxq_decoder: sizes, a HOST array of layers, device embedding / final norm,
  * device token and position words, device fp32 logits [vocab].
- * Limits: hidden 512..4096 (multiple of 512), head_dim 128, max_seq <= 1024,
+ * Limits: hidden 512..3584 (multiple of 512), head_dim 128, max_seq <= 1024,
  * n_heads <= number of compute units, intermediate <= 16384 (above hidden
  * 2048: <= 24576 within the 160 KB LDS budget, e.g. Qwen2.5-7B's 18944).
  * hxq_decoder_init copies the layer table into `workspace` (device, 256-byte
