@@ -635,7 +635,7 @@ def scan_bench(dev, iters=5, cpu=True):
     import math
 
     import torch
-    from helix_substrate import mamba_scan_chunked as msc
+    from helix_substrate import ssm_scan as msc
 
     b, L, H, P, N = 8, 2048, 64, 64, 128
     g = torch.Generator(device=dev).manual_seed(0)

@@ -22,7 +22,7 @@ from torch import nn
 
 from . import _hxq
 from .helix_linear import HelixLinear
-from .mamba_scan_chunked import DEFAULT_CHUNK_SIZE, sequential_scan
+from .ssm_scan import DEFAULT_CHUNK_SIZE, sequential_scan
 
 
 class HelixMamba2Mixer(nn.Module):
@@ -33,7 +33,7 @@ class HelixMamba2Mixer(nn.Module):
     def __init__(self, in_proj: HelixLinear, out_proj: HelixLinear, conv_weight, conv_bias,
                  dt_bias, A_log, D, norm_weight, *, num_heads, head_dim, ssm_state_size,
                  n_groups=1, eps=1e-5, time_step_min=0.0, time_step_max=float("inf"),
-                 d_mlp=0, chunk_size=DEFAULT_CHUNK_SIZE):
+                 d_mlp=0, chunk_size=DEFAULT_CHUNK_SIZE, norm_group_size=None):
         super().__init__()
         self.in_proj, self.out_proj = in_proj, out_proj
         self.num_heads, self.head_dim = int(num_heads), int(head_dim)
@@ -45,6 +45,10 @@ class HelixMamba2Mixer(nn.Module):
         self.time_step_min, self.time_step_max = float(time_step_min), float(time_step_max)
         self.variance_epsilon = float(eps)
         self.chunk_size = int(chunk_size)
+        # gated RMSNorm groups: the whole d_inner (Mamba2) or d_inner / n_groups (Zamba2)
+        self.norm_group_size = int(norm_group_size or self.intermediate_size)
+        if self.intermediate_size % self.norm_group_size:
+            raise ValueError("norm_group_size must divide the intermediate size")
         proj_width = (2 * self.d_mlp + 2 * self.intermediate_size
                       + 2 * self.n_groups * self.ssm_state_size + self.num_heads)
         if in_proj.out_features != proj_width:
@@ -99,7 +103,7 @@ class HelixMamba2Mixer(nn.Module):
             state[1].copy_(h)
         gate, _, _ = self._split(proj.view(b * L, -1))
         z = _hxq.gated_rmsnorm(y.view(b * L, -1), gate, self.norm_weight, self.variance_epsilon,
-                               out_dtype=dtype)
+                               group_size=self.norm_group_size, out_dtype=dtype)
         return self.out_proj(z).view(b, L, -1)
 
     def _forward_cpu(self, hs, state):
@@ -129,8 +133,9 @@ class HelixMamba2Mixer(nn.Module):
 
     def _gated_norm(self, y, gate):
         h = y.float() * F.silu(gate.float())
-        var = h.pow(2).mean(-1, keepdim=True)
-        return self.norm_weight * (h * torch.rsqrt(var + self.variance_epsilon))
+        hg = h.unflatten(-1, (-1, self.norm_group_size))
+        hg = hg * torch.rsqrt(hg.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
+        return self.norm_weight * hg.flatten(-2)
 
     # -- single token ------------------------------------------------------------
     def step(self, hidden_state, state):
@@ -149,7 +154,7 @@ class HelixMamba2Mixer(nn.Module):
             y = _hxq.ssm_decode_step(ssm_state, x, dt, A, B, C, self.D)
             gate, _, _ = self._split(proj)
             z = _hxq.gated_rmsnorm(y.view(b, -1), gate, self.norm_weight, self.variance_epsilon,
-                                   out_dtype=dtype)
+                                   group_size=self.norm_group_size, out_dtype=dtype)
             return self.out_proj(z)
         gate, xbc, dt = self._split(proj)
         conv_state.copy_(torch.roll(conv_state, shifts=-1, dims=-1))
@@ -170,6 +175,115 @@ class HelixMamba2Mixer(nn.Module):
         y = (ssm_state * C[:, :, None, :]).sum(-1) + self.D[None, :, None] * x
         z = self._gated_norm(y.reshape(b, -1), gate.float())
         return self.out_proj(z.to(dtype))
+
+
+    # -- transformers' mixer contract --------------------------------------------
+    @classmethod
+    def from_hf(cls, mod):
+        """Build from a transformers 5.x ``Mamba2Mixer`` or ``Zamba2MambaMixer``.
+        ``in_proj`` / ``out_proj`` are the HF module's own (``HelixLinear`` once
+        the HXQ quantizer has replaced them, else ``nn.Linear``); the small
+        parameters are copied to fp32.  dt is clamped to the module's
+        ``time_step_limit`` (Zamba2: ``(time_step_min, inf)``); the gated norm
+        takes the module's group size (Zamba2) or the whole d_inner (Mamba2)."""
+        lo, hi = getattr(mod, "time_step_limit", (0.0, float("inf")))
+        norm = mod.norm
+        det = lambda t: None if t is None else t.detach()
+        return cls(mod.in_proj, mod.out_proj, det(mod.conv1d.weight), det(mod.conv1d.bias),
+                   det(mod.dt_bias), det(mod.A_log), det(mod.D), det(norm.weight),
+                   num_heads=mod.num_heads, head_dim=mod.head_dim,
+                   ssm_state_size=mod.ssm_state_size, n_groups=mod.n_groups,
+                   eps=norm.variance_epsilon, time_step_min=lo, time_step_max=hi,
+                   chunk_size=mod.chunk_size, norm_group_size=getattr(norm, "group_size", None))
+
+    def hf_forward(self, hidden_states, cache_params=None, attention_mask=None, layer_idx=0):
+        """transformers' mixer forward (``Mamba2Mixer.forward`` /
+        ``Zamba2MambaMixer.forward``, transformers 5.x) on device tensors, every
+        stage a HIP launch.  With ``cache_params`` (HF's linear-attention cache)
+        it covers the three cases the HF forward has: prefill (stores the last
+        ``conv_kernel_size`` raw xBC columns and the fp32 final SSM state),
+        a multi-token continuation (the cached columns are prepended to the
+        convolution's input and the cached state is the scan's initial state)
+        and the single-token step (conv state and SSM state updated in place).
+        A 2-D ``attention_mask`` zeroes padded positions before in_proj and
+        after the convolution, as HF's ``apply_mask_to_padding_states``."""
+        if not hidden_states.is_cuda:
+            raise RuntimeError("hf_forward runs the HIP kernels: pass device tensors")
+        b, L, _ = hidden_states.shape
+        dtype = hidden_states.dtype
+        mask = attention_mask
+        if mask is not None and bool((mask == 1).all()):
+            mask = None
+        hs = hidden_states if mask is None else (hidden_states * mask[:, :, None]).to(dtype)
+        proj = self.in_proj(hs).contiguous()                          # [b, L, proj_width]
+        d, I, cd, H = self.d_mlp, self.intermediate_size, self.conv_dim, self.num_heads
+        G, N, W = self.n_groups, self.ssm_state_size, self.conv_kernel_size
+        A = -torch.exp(self.A_log)
+        conv = (self.conv_weight, self.conv_bias, self.dt_bias, self.time_step_min,
+                self.time_step_max, d, I, G, N, H)
+        layer = None if cache_params is None else cache_params.layers[layer_idx]
+        use_prev = cache_params is not None and cache_params.has_previous_state(layer_idx)
+        if use_prev and L == 1 and not layer.record_past:
+            conv_state, ssm_state = layer.conv_states[0], layer.recurrent_states[0]
+            cs = _f32_view(conv_state)
+            x, B, C, dt = _hxq.mamba2_conv_step(proj[:, 0].contiguous(), cs, *conv)
+            h = _f32_view(ssm_state)
+            y = _hxq.ssm_decode_step(h, x, dt, A, B, C, self.D)         # [b, H, P] fp32
+            if cs is not conv_state:
+                conv_state.copy_(cs)
+            if h is not ssm_state:
+                ssm_state.copy_(h)
+            y = y.reshape(b, 1, I)
+        else:
+            src, prefix = proj, 0
+            if cache_params is not None:
+                xbc_t = proj[..., 2 * d + I:2 * d + I + cd].transpose(1, 2)   # [b, cd, L]
+                full = cache_params.update_conv_state(xbc_t, layer_idx, conv_kernel_size=W)
+                if use_prev:
+                    # continuation: the cached raw columns go in front of the new
+                    # ones, their gate / dt slots zero (those rows are dropped)
+                    prefix = full.shape[-1] - L
+                    src = proj.new_zeros(b, prefix + L, proj.shape[-1])
+                    src[:, :prefix, 2 * d + I:2 * d + I + cd] = \
+                        full[..., :prefix].transpose(1, 2).to(proj.dtype)
+                    src[:, prefix:] = proj
+            x, B, C, dt = _hxq.mamba2_conv_split(src, *conv)
+            if prefix:
+                x, B, C, dt = (t[:, prefix:].contiguous() for t in (x, B, C, dt))
+            if mask is not None:
+                m = mask[:, :, None, None]
+                x, B, C = ((t * m).to(t.dtype) for t in (x, B, C))
+            h0 = layer.recurrent_states[0] if use_prev else None
+            y, h = _hxq.ssm_chunk_scan(x, dt, A, B, C, self.D, h0, chunk=self.chunk_size,
+                                       out_dtype=torch.float32, want_final=cache_params is not None)
+            if cache_params is not None:
+                cache_params.update_recurrent_state(h, layer_idx=layer_idx)
+            y = y.reshape(b, L, I)
+        gate = proj.view(b * L, -1)[:, 2 * d:2 * d + I]
+        z = _hxq.gated_rmsnorm(y.view(b * L, I), gate, self.norm_weight, self.variance_epsilon,
+                               group_size=self.norm_group_size, out_dtype=dtype)
+        return self.out_proj(z).view(b, L, -1)
+
+
+def _f32_view(t):
+    """t itself when fp32 and contiguous (updated in place), else an fp32 copy
+    (copied back by the caller)."""
+    return t if t.dtype == torch.float32 and t.is_contiguous() else t.float().contiguous()
+
+
+def hf_core(mod):
+    """The HelixMamba2Mixer behind a transformers mixer module (built on first
+    use and kept on the module outside its parameters and submodules; rebuilt
+    when a parameter is replaced, moved or modified in place)."""
+    params = (mod.conv1d.weight, mod.conv1d.bias, mod.dt_bias, mod.A_log, mod.D, mod.norm.weight)
+    key = tuple(None if p is None else (p.data_ptr(), p._version, str(p.device)) for p in params)
+    core = mod.__dict__.get("_helix_core")
+    if (core is None or core._hf_key != key or core.in_proj is not mod.in_proj
+            or core.out_proj is not mod.out_proj):
+        core = HelixMamba2Mixer.from_hf(mod).to(mod.dt_bias.device)
+        core._hf_key = key
+        mod.__dict__["_helix_core"] = core
+    return core
 
 
 def mamba2_13b_dims():

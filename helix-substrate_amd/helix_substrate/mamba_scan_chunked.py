@@ -1,66 +1,77 @@
-"""Mamba/Mamba2 selective scan with the reference's function signatures
-(``helix_substrate/mamba_scan_chunked.py:42-213``, ``triton_mamba_scan.py:246-416``).
+"""Selective scan entry points plus the transformers patch, importable under
+the reference's module name (``helix_substrate/mamba_scan_chunked.py``).
 
-Device tensors run the chunk-parallel HIP scan in ``libhxq.so`` (fp32 state);
-CPU tensors run the token loop in torch.  ``B``/``C`` may be given per head
-``[b, L, H, N]`` (as the reference passes them after ``repeat_interleave``) or
-per group ``[b, L, G, N]`` with G dividing H (no expansion needed).
+As in the reference, importing this module patches transformers' Mamba2
+mixers (``apply_patch`` runs at import, ``mamba_scan_chunked.py:394-408``).
+The reference replaces ``Zamba2MambaMixer.torch_forward`` with its chunked
+scan; transformers 5.x mixers have no ``torch_forward``, so here the
+``forward`` of ``Mamba2Mixer`` and ``Zamba2MambaMixer`` is wrapped instead:
+device inputs run ``HelixMamba2Mixer.hf_forward`` (HIP conv/split, chunked
+scan or single-token state update, gated RMSNorm, with the HF cache object),
+CPU inputs run the original forward.  Set ``HELIX_MAMBA_PATCH=0`` to import
+without patching.
 """
 from __future__ import annotations
 
-import torch
+import os
 
-from . import _hxq
+from .ssm_scan import (DEFAULT_CHUNK_SIZE, chunked_scan, decode_step,  # noqa: F401
+                       sequential_scan, triton_mamba_decode_step, triton_scan)
 
-DEFAULT_CHUNK_SIZE = 256
-
-
-def sequential_scan(h, dt, A, hidden_states, B, C, D):
-    """Token-by-token scan.  h [b, H, P, N] (initial state), dt [b, L, H], A [H],
-    hidden_states [b, L, H, P], B/C [b, L, G, N], D [H, 1] or [H].
-    Returns (y [b, L, H, P], h_final)."""
-    if hidden_states.is_cuda:
-        return chunked_scan(h, dt, A, hidden_states, B, C, D, chunk_size=hidden_states.shape[1])
-    batch, seq_len, heads = dt.shape
-    rep = heads // B.shape[2]
-    Bh = B.float().repeat_interleave(rep, dim=2) if rep > 1 else B.float()
-    Ch = C.float().repeat_interleave(rep, dim=2) if rep > 1 else C.float()
-    x = hidden_states.float()
-    Dv = D.float().reshape(-1)
-    h = h.float().clone()
-    y = torch.zeros(batch, seq_len, heads, x.shape[-1], dtype=torch.float32)
-    for t in range(seq_len):
-        dA = torch.exp(A.float() * dt[:, t, :].float())
-        dx = dt[:, t, :, None].float() * x[:, t]
-        h = dA[:, :, None, None] * h + dx[:, :, :, None] * Bh[:, t, :, None, :]
-        y[:, t] = (h * Ch[:, t, :, None, :]).sum(-1) + Dv[None, :, None] * x[:, t]
-    return y, h
+_ORIGINAL = {}
 
 
-def chunked_scan(h, dt, A, hidden_states, B, C, D, chunk_size=DEFAULT_CHUNK_SIZE):
-    """Chunk-parallel scan (same contract as sequential_scan).  ``h`` may be None
-    (zero initial state)."""
-    if not hidden_states.is_cuda:
-        if h is None:
-            b, _, H, P = hidden_states.shape
-            h = torch.zeros(b, H, P, B.shape[-1])
-        return sequential_scan(h, dt, A, hidden_states, B, C, D)
-    return _hxq.ssm_chunk_scan(hidden_states.contiguous(), dt.contiguous(), A, B.contiguous(),
-                               C.contiguous(), D, None if h is None else h, chunk=chunk_size)
+def _mixer_classes():
+    """transformers' Mamba2-family mixer classes present in this install."""
+    out = []
+    try:
+        from transformers.models.mamba2.modeling_mamba2 import Mamba2Mixer
+        out.append(Mamba2Mixer)
+    except ImportError:
+        pass
+    try:
+        from transformers.models.zamba2.modeling_zamba2 import Zamba2MambaMixer
+        out.append(Zamba2MambaMixer)
+    except ImportError:
+        pass
+    return out
 
 
-triton_scan = chunked_scan  # name of the reference's GPU entry point
+def _patched(original):
+    def forward(self, hidden_states, cache_params=None, attention_mask=None, **kwargs):
+        if not hidden_states.is_cuda:
+            return original(self, hidden_states, cache_params=cache_params,
+                            attention_mask=attention_mask, **kwargs)
+        from .mamba2_mixer import hf_core
+        return hf_core(self).hf_forward(hidden_states, cache_params=cache_params,
+                                        attention_mask=attention_mask, layer_idx=self.layer_idx)
+
+    forward.__wrapped__ = original
+    forward.__doc__ = original.__doc__
+    return forward
 
 
-def decode_step(h, dt, A, x, B, C, D):
-    """Single token: h [b, H, P, N] updated in place; dt [b, H], x [b, H, P],
-    B/C [b, G, N].  Returns y [b, H, P] (reference triton_mamba_decode_step)."""
-    if not h.is_cuda:
-        y, hn = sequential_scan(h, dt[:, None], A, x[:, None], B[:, None], C[:, None], D)
-        h.copy_(hn)
-        return y[:, 0]
-    return _hxq.ssm_decode_step(h, x.contiguous(), dt.contiguous(), A, B.contiguous(),
-                                C.contiguous(), D)
+def apply_patch():
+    """Route the device forward of transformers' Mamba2Mixer / Zamba2MambaMixer
+    through the HIP mixer (idempotent).  Returns True when a class was found."""
+    classes = _mixer_classes()
+    for cls in classes:
+        if cls not in _ORIGINAL:
+            _ORIGINAL[cls] = cls.forward
+            cls.forward = _patched(cls.forward)
+    return bool(classes)
 
 
-triton_mamba_decode_step = decode_step
+def remove_patch():
+    """Restore the original forwards."""
+    for cls, fwd in list(_ORIGINAL.items()):
+        cls.forward = fwd
+        del _ORIGINAL[cls]
+
+
+def is_patched():
+    return bool(_ORIGINAL)
+
+
+if os.environ.get("HELIX_MAMBA_PATCH", "1") != "0":
+    apply_patch()

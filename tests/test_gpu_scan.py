@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle
-from helix_substrate import mamba_scan_chunked as msc
+from helix_substrate import ssm_scan as msc
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
