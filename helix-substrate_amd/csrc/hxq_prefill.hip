@@ -80,6 +80,10 @@ struct Args {
     void *y;                 // [M, OUT]
     float *part;             // split-K partials [ksplit, ntiles, BM, 256] (ksplit > 1)
     int32_t M, OUT, K, group, y_dtype, ksplit, ks_per, n_codes;
+    // affine groups per row (ceil(K / group): K may be padded past the last
+    // group); group % 64 != 0: each lane finds its own group; group % 32 != 0:
+    // a lane's 32 weights span two groups (one per 16)
+    int32_t ngroups, g_lane, g16;
     int32_t tiles_x, tiles_y;   // the whole tile grid
     int32_t t0, ntiles;         // this launch: tiles [t0, t0 + ntiles) of the order
     int32_t tiles_per_xcd;      // of this launch
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, (int64_t)(GRP ? g.x_rows : g.M) * K * XB);
     const int64_t row_bytes = (int64_t)K / 32 * B32;
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(gidx, (int64_t)wout * row_bytes);
-    const int ngroups = AFFINE ? K / g.group : 1;
+    const int ngroups = AFFINE ? g.ngroups : 1;
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(gga, AFFINE ? (int64_t)ngroups * wout * 8 : 0);
     // X: thread t copies chunk t % XCH of rows t / XCH + (threads / XCH) p
     const int xc = tid % XCH;
@@ -331,7 +335,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
 
     u32x4 xv[2][XP];   // X of steps s (buffer s & 1)
     u32x4 qv[2][NQ * NJ]; // index bytes of row j: qv[.][NQ j .. NQ j + NQ)
-    float2 av[2][NJ];     // {scale, offset} per j
+    float2 av[2][NJ];     // {scale, offset} per j (weights 0..15 of the lane's 32)
+    float2 av2[2][NJ];    // ... of weights 16..31 (the same group unless g16)
     auto load_step = [&](int s, int buf) {
         const bool live = s < nk;
         const uint32_t k0 = static_cast<uint32_t>((kb + (live ? s : 0)) * kBK);
@@ -353,12 +358,26 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
             }
         }
         if constexpr (AFFINE) {
-            const uint32_t gofs = (k0 / static_cast<uint32_t>(g.group)) * static_cast<uint32_t>(wout) * 8u;
+            // the lane's weights are physical k0 + 32 hh + [0, 32): one group
+            // for the whole step when group % 64 == 0 (uniform), else per lane
+            const uint32_t G = static_cast<uint32_t>(g.group);
+            const uint32_t row8 = static_cast<uint32_t>(wout) * 8u;
+            const uint32_t ga = g.g_lane ? (k0 + 32u * hh) / G : k0 / G;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + gofs;
+                const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + ga * row8;
                 const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(ar, o, 0, 0);
                 av[buf][j] = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+                av2[buf][j] = av[buf][j];
+            }
+            if (g.g16) {
+                const uint32_t gb = (k0 + 32u * hh + 16u) / G;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + gb * row8;
+                    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(ar, o, 0, 0);
+                    av2[buf][j] = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+                }
             }
         }
         load_entries(s, buf);
@@ -414,8 +433,9 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     auto dequant_sub = [&](int buf, int s, BV &b) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const float sc = AFFINE ? av[buf][j].x : 1.f;
-            const float of = AFFINE ? av[buf][j].y : 0.f;
+            // substep s holds weights 8s .. 8s+7: the first 16 for s < 2
+            const float sc = AFFINE ? (s < 2 ? av[buf][j].x : av2[buf][j].x) : 1.f;
+            const float of = AFFINE ? (s < 2 ? av[buf][j].y : av2[buf][j].y) : 0.f;
             if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
                 // weights 8s .. 8s+7: the 16 bytes of load s, eight uint16 indices
                 const u32x4 q = qv[buf][NQ * j + s];
@@ -482,8 +502,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     // (weights 4q .. 4q+3) feeds MFMA substeps 4q .. 4q+3
     auto dequant_f32 = [&](int buf, int q, BV &b) {
         if constexpr (F32) {
-        const float sc = AFFINE ? av[buf][0].x : 1.f;
-        const float of = AFFINE ? av[buf][0].y : 0.f;
+        const float sc = AFFINE ? (q < 4 ? av[buf][0].x : av2[buf][0].x) : 1.f;
+        const float of = AFFINE ? (q < 4 ? av[buf][0].y : av2[buf][0].y) : 0.f;
         float v[4];
         if constexpr (FMT == HXQ_FMT_SCALAR) {
             const uint32_t w = qv[buf][q >> 2][q & 3];
@@ -863,6 +883,7 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     a.K = static_cast<int32_t>(r.in);
     const bool aff = r.bank0->group_affine != nullptr;
     a.group = aff ? r.group : kBK;
+    a.ngroups = static_cast<int32_t>(r.in / a.group);
     a.y_dtype = r.y_dtype;
     a.ksplit = 1;
     a.ks_per = static_cast<int32_t>(r.in / kBK);
@@ -960,10 +981,10 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
     HXQ_REQUIRE(m_rows * in_features * (x_dtype == HXQ_F32 ? 4 : 2) < (int64_t{1} << 31) &&
                     out_features * (in_features / 32 * pg::fmt_b32(format)) < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
-    HXQ_REQUIRE(!group_affine || (group_size >= pg::kBK && group_size % pg::kBK == 0 &&
-                                  in_features % group_size == 0),
-                "group_size must be a multiple of 64 dividing in_features");
-    HXQ_REQUIRE(!group_affine || (in_features / group_size) * out_features * 8 < (int64_t{1} << 31),
+    HXQ_REQUIRE(!group_affine || (group_size >= 16 && group_size % 16 == 0),
+                "group_size must be a positive multiple of 16");
+    const int64_t ngroups = group_affine ? (in_features + group_size - 1) / group_size : 1;
+    HXQ_REQUIRE(!group_affine || ngroups * out_features * 8 < (int64_t{1} << 31),
                 "affine factors too large for 32-bit offsets");
     HXQ_REQUIRE(!sc_grp_ptr || (sc_grp_key && sc_grp_val),
                 "the sidecar needs sc_grp_ptr, sc_grp_key and sc_grp_val");
@@ -992,6 +1013,9 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
     a.OUT = static_cast<int32_t>(out_features);
     a.K = static_cast<int32_t>(in_features);
     a.group = group_affine ? group_size : pg::kBK;
+    a.ngroups = static_cast<int32_t>(ngroups);
+    a.g_lane = a.group % pg::kBK != 0;
+    a.g16 = a.group % 32 != 0;
     a.y_dtype = y_dtype;
     a.tiles_x = p.tiles_x;
     a.tiles_y = p.tiles_y;

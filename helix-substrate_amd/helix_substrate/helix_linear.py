@@ -43,13 +43,14 @@ import torch
 import torch.nn as nn
 
 from . import _hxq
-from .hxq_format import (build_sidecar_csr, check_kernel_shapes, compressed_bytes,
+from .index_packing import pack_12bit, unpack_12bit
+from .hxq_format import (build_sidecar_csr, check_kernel_shapes, compressed_bytes, pad_columns,
+                         padded_in_features,
                          sidecar_row_groups)
 
 _CPU_TILE_ROWS = 256
 _GEMV_MAX_ROWS = 4
 _GEMV_MULTI_ROW_MAX_K = 8192  # 2-4 row GEMV launches hold 8 K-chunks of 1024 per wave
-_DEQUANT_TILE_ELEMS = 1 << 24  # fp32 elements per dequantised row tile (64 MiB)
 
 
 class HelixLinear(nn.Module):
@@ -216,14 +217,19 @@ class HelixLinear(nn.Module):
             for name in ("_sc_row_ptr", "_sc_col", "_sc_val", "_sc_delta", "_sidecar_rows",
                          "_sidecar_cols", "_sidecar_deltas", "_sidecar_vq_vals"):
                 self.register_buffer(name, None)
-        # the MFMA GEMM steps K by 64 and reads one affine group per step, in
-        # the layout [K/G, OUT, 2] = {scale, offset} (derived, not saved)
-        self._gemm_ok = (self.in_features % 64 == 0 and
-                         (not has_affine or self.group_size % 64 == 0))
-        self.register_buffer(
-            "_affine_t",
-            torch.stack([self.group_scale.t(), self.group_offset.t()], dim=-1).contiguous()
-            if has_affine else None, persistent=False)
+        # the MFMA GEMM reads the affine in the layout [K/G, OUT, 2] = {scale,
+        # offset} (derived, not saved); with K padded to a multiple of 64 it
+        # gets zero groups covering the padded columns
+        self._gemm_ok = True
+        aff_t = None
+        if has_affine:
+            aff_t = torch.stack([self.group_scale.t(), self.group_offset.t()], dim=-1)
+            n_pad = -(-padded_in_features(self.in_features) // self.group_size) - aff_t.shape[0]
+            if n_pad:
+                aff_t = torch.cat([aff_t, aff_t.new_zeros(n_pad, *aff_t.shape[1:])])
+            aff_t = aff_t.contiguous()
+        self.register_buffer("_affine_t", aff_t, persistent=False)
+        self._build_kernel_layout()
         # the prefill GEMM's sidecar order (per 64 output rows, by column; derived)
         grp = (sidecar_row_groups(self._sidecar_rows, self._sidecar_cols, self._sc_val,
                                   self.out_features, self.in_features)
@@ -245,8 +251,8 @@ class HelixLinear(nn.Module):
             raise NotImplementedError("pair codebooks are [k <= 4096, 2]")
         if self.group_scale is not None or self.group_offset is not None:
             raise NotImplementedError("pair codebooks take no group affine")
-        if self.in_features % 16:
-            raise ValueError(f"in_features={self.in_features} must be a multiple of 16")
+        if self.in_features % 2:
+            raise ValueError(f"in_features={self.in_features} must be even for pair codebooks")
         if self.codebook.dtype != torch.float32:
             self.register_buffer("codebook", self.codebook.float().contiguous())
         n_pairs = self.out_features * (self.in_features // 2)
@@ -277,8 +283,9 @@ class HelixLinear(nn.Module):
             for name in ("_sc_row_ptr", "_sc_col", "_sc_val", "_sc_delta", "_sidecar_rows",
                          "_sidecar_cols", "_sidecar_deltas", "_sidecar_vq_vals"):
                 self.register_buffer(name, None)
-        self._gemm_ok = self.in_features % 64 == 0
+        self._gemm_ok = True
         self.register_buffer("_affine_t", None, persistent=False)
+        self._build_kernel_layout()
         grp = (sidecar_row_groups(self._sidecar_rows, self._sidecar_cols, self._sc_val,
                                   self.out_features, self.in_features)
                if self._gemm_ok and self._sc_row_ptr is not None else (None, None, None))
@@ -289,6 +296,36 @@ class HelixLinear(nn.Module):
         self.has_channel_scales = self.channel_scales is not None
         self.register_buffer("codebook_f16", self.codebook.half().contiguous()
                              if self.compute_dtype == torch.float16 else None)
+
+    def _build_kernel_layout(self) -> None:
+        """in_features not a multiple of 64: the kernels read a copy of the index
+        rows padded with zero columns to padded_in_features (12-bit packed pairs
+        are unpacked, padded and packed again) and activations padded likewise
+        per call.  Padded columns multiply zero activations and, with the
+        affine, fall in zero (scale, offset) groups, so results equal the
+        unpadded contraction.  The stored ``indices`` keep the reference
+        layout."""
+        K = self.in_features
+        self._kin = padded_in_features(K)
+        if self._kin == K:
+            self.register_buffer("_kidx", None, persistent=False)
+            return
+        if self.vector_dim == 1:
+            padded = pad_columns(self.indices, self._kin)
+        elif self.index_packing == "12bit":
+            vals = unpack_12bit(self.indices, self.out_features * (K // 2))
+            padded = pack_12bit(pad_columns(vals.reshape(self.out_features, K // 2), self._kin // 2))
+        else:
+            padded = pad_columns(self.indices, self._kin // 2)
+        self.register_buffer("_kidx", padded.contiguous(), persistent=False)
+
+    def _kernel_rows(self, x2: torch.Tensor, need: int):
+        """(activations, index rows) for a kernel whose K must be a multiple of
+        `need` (16: GEMV, 64: GEMM): the stored layout when in_features is one,
+        else the padded copy and x padded with zero columns."""
+        if self.in_features % need == 0:
+            return x2, self.indices
+        return pad_columns(x2, self._kin), self._kidx
 
     def _pair_index_at(self, rows: torch.Tensor, pairs: torch.Tensor) -> torch.Tensor:
         """Pair index at (row, pair column), from int16 or 12-bit packed storage."""
@@ -418,74 +455,46 @@ class HelixLinear(nn.Module):
         out = torch.empty(n, self.out_features, dtype=out_dtype, device=x2.device)
         if n == 0:
             pass
-        elif n > _GEMV_MAX_ROWS and self._gemm_ok:
-            # every index format: W dequantised into the MFMA operand registers
-            # (bf16/fp16 MFMA for 16-bit activations, fp32 MFMA for fp32 ones)
+        elif n > _GEMV_MAX_ROWS:
+            # every index format and any K: W dequantised into the MFMA operand
+            # registers (bf16/fp16 MFMA for 16-bit activations, fp32 MFMA for
+            # fp32 ones)
             self._last_dispatch_path = "hip_gemm"
+            xk, idx = self._kernel_rows(x2, 64)
             grp = rp is not None
             scalar8 = self._fmt == _hxq.FMT_SCALAR
-            _hxq.prefill_gemm(x2, self.indices, self._kcb if scalar8 else self.codebook,
+            _hxq.prefill_gemm(xk, idx, self._kcb if scalar8 else self.codebook,
                               self._affine_t, self.group_size,
                               self._sc_grp_ptr if grp else None,
                               self._sc_grp_key if grp else None,
                               self._sc_grp_val if grp else None, self.bias, out=out,
                               fmt=self._fmt, out_features=self.out_features)
-        elif self._fmt != _hxq.FMT_SCALAR:
-            self._forward_hip_fmt(x2, rp, col, delta, out)
-        elif n <= _GEMV_MAX_ROWS:
-            self._last_dispatch_path = "hip_gemv"
-            for r0, r1 in self._gemv_row_groups(n):
-                _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
-                          self.group_offset, self.group_size, rp, col, delta, self.bias,
-                          out=out[r0:r1])
         else:
-            # in_features not a multiple of 64 (or a group size the GEMM does not
-            # step): GEMV over groups of 4 rows, fp32 arithmetic
-            self._last_dispatch_path = "hip_gemv_rows"
-            for r0, r1 in self._gemv_row_groups(n):
-                _hxq.gemv(x2[r0:r1], self.indices, self._kcb, self.group_scale,
-                          self.group_offset, self.group_size, rp, col, delta, self.bias,
-                          out=out[r0:r1])
+            xk, idx = self._kernel_rows(x2, 16)
+            if self._fmt != _hxq.FMT_SCALAR:
+                self._last_dispatch_path = "hip_gemv_fmt"
+            else:
+                self._last_dispatch_path = "hip_gemv"
+            for r0, r1 in self._gemv_row_groups(n, xk.shape[1]):
+                if self._fmt != _hxq.FMT_SCALAR:
+                    _hxq.gemv_fmt(xk[r0:r1], self._fmt, idx, self.out_features,
+                                  codebook=self.codebook, group_scale=self.group_scale,
+                                  group_offset=self.group_offset, group_size=self.group_size,
+                                  sc_row_ptr=rp, sc_col=col, sc_delta=delta, bias=self.bias,
+                                  out=out[r0:r1])
+                else:
+                    _hxq.gemv(xk[r0:r1], idx, self._kcb, self.group_scale, self.group_offset,
+                              self.group_size, rp, col, delta, self.bias, out=out[r0:r1])
         if svd_on:
             xf = x2.float()
             out += ((xf @ self.svd_Vt.t()) * self.svd_s.unsqueeze(0)) @ self.svd_U.t()
         return out.reshape(*orig_shape[:-1], self.out_features)
 
-    def _gemv_row_groups(self, n):
-        """Row ranges of the GEMV launches for n activation rows: groups of up to
-        4 rows, or single rows when in_features exceeds the multi-row limit."""
-        step = _GEMV_MAX_ROWS if self.in_features <= _GEMV_MULTI_ROW_MAX_K else 1
+    def _gemv_row_groups(self, n, k):
+        """Row ranges of the GEMV launches for n activation rows of k columns:
+        groups of up to 4 rows, or single rows above the multi-row K limit."""
+        step = _GEMV_MAX_ROWS if k <= _GEMV_MULTI_ROW_MAX_K else 1
         return [(r0, min(n, r0 + step)) for r0 in range(0, n, step)]
-
-    def _forward_hip_fmt(self, x2, rp, col, delta, out) -> None:
-        """Pair codebooks and int16-index scalar codebooks: the format GEMV for up to
-        4 rows; above that (in_features not a multiple of 64, which the prefill
-        GEMM does not take) dequantised row tiles and the library GEMM."""
-        n = x2.shape[0]
-        if n <= _GEMV_MAX_ROWS:
-            self._last_dispatch_path = "hip_gemv_fmt"
-            for r0, r1 in self._gemv_row_groups(n):
-                _hxq.gemv_fmt(x2[r0:r1], self._fmt, self.indices, self.out_features,
-                              codebook=self.codebook, group_scale=self.group_scale,
-                              group_offset=self.group_offset, group_size=self.group_size,
-                              sc_row_ptr=rp, sc_col=col, sc_delta=delta, bias=self.bias,
-                              out=out[r0:r1])
-            return
-        # many rows: HIP dequant of row tiles, then the library GEMM on them
-        self._last_dispatch_path = "hip_dequant_gemm"
-        step = max(1, _DEQUANT_TILE_ELEMS // self.in_features)
-        for r0 in range(0, self.out_features, step):
-            r1 = min(self.out_features, r0 + step)
-            w = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features, self.in_features,
-                                 codebook=self.codebook, group_scale=self.group_scale,
-                                 group_offset=self.group_offset, group_size=self.group_size,
-                                 sc_row_ptr=rp, sc_col=col,
-                                 sc_val=None if rp is None else self._sc_val, row_begin=r0,
-                                 row_end=r1)
-            y = x2 @ w.to(x2.dtype).t()
-            if self.bias is not None:
-                y = y + self.bias[r0:r1].to(y.dtype)
-            out[:, r0:r1] = y
 
     def _forward_naive(self, x: torch.Tensor) -> torch.Tensor:
         """CPU tensors: 256-row tiles, fp32 (reference helix_linear.py:783-822)."""
@@ -565,14 +574,18 @@ class HelixLinear(nn.Module):
         On the GPU this is the bit-exact HIP dequant kernel.
         """
         apply_sc = getattr(self, "_apply_sidecar_this_call", True)
+        # the dequant kernels take rows of a multiple of 16 columns: otherwise
+        # the padded rows, cut back to in_features
+        K = self.in_features
+        kidx, kin = (self.indices, K) if K % 16 == 0 else (self._kidx, self._kin)
         if self.vector_dim != 1:
             if self.indices.is_cuda:
-                tile = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features,
-                                        self.in_features, codebook=self.codebook,
+                tile = _hxq.dequant_fmt(self._fmt, kidx, self.out_features, kin,
+                                        codebook=self.codebook,
                                         sc_row_ptr=self._sc_row_ptr if apply_sc else None,
                                         sc_col=self._sc_col if apply_sc else None,
                                         sc_val=self._sc_val if apply_sc else None,
-                                        row_begin=start_row, row_end=end_row)
+                                        row_begin=start_row, row_end=end_row)[:, :K]
             else:
                 tile = self.codebook[self._pair_rows(start_row, end_row)].reshape(
                     end_row - start_row, self.in_features)
@@ -581,19 +594,19 @@ class HelixLinear(nn.Module):
                 tile = tile + (self.svd_U[start_row:end_row] * self.svd_s.unsqueeze(0)) @ self.svd_Vt
             return tile
         if self.indices.is_cuda and self._fmt == _hxq.FMT_SCALAR_U16:
-            tile = _hxq.dequant_fmt(self._fmt, self.indices, self.out_features, self.in_features,
+            tile = _hxq.dequant_fmt(self._fmt, kidx, self.out_features, kin,
                                     codebook=self.codebook, group_scale=self.group_scale,
                                     group_offset=self.group_offset, group_size=self.group_size,
                                     sc_row_ptr=self._sc_row_ptr if apply_sc else None,
                                     sc_col=self._sc_col if apply_sc else None,
                                     sc_val=self._sc_val if apply_sc else None,
-                                    row_begin=start_row, row_end=end_row)
+                                    row_begin=start_row, row_end=end_row)[:, :K]
         elif self.indices.is_cuda:
-            tile = _hxq.dequant_f32(self.indices, self._kcb, self.group_scale,
+            tile = _hxq.dequant_f32(kidx, self._kcb, self.group_scale,
                                     self.group_offset, self.group_size,
                                     self._sc_row_ptr if apply_sc else None,
                                     self._sc_col if apply_sc else None,
-                                    self._sc_val if apply_sc else None, start_row, end_row)
+                                    self._sc_val if apply_sc else None, start_row, end_row)[:, :K]
         else:
             tile = self.codebook[self.indices[start_row:end_row].long() & 0xffff]
             if self.group_scale is not None:

@@ -123,12 +123,28 @@ def sidecar_row_groups(rows: torch.Tensor, cols: torch.Tensor, val: torch.Tensor
 
 
 def check_kernel_shapes(in_features: int, group_size: int, has_affine: bool) -> None:
-    """Shape rules of the HIP kernels (16-byte index vectors, groups of 16k)."""
-    if in_features % 16 != 0:
-        raise ValueError(f"in_features={in_features} must be a multiple of 16")
+    """Shape rules of the HIP kernels: any in_features (rows whose length is not
+    a multiple of 64 are read from a zero-padded copy, ``padded_in_features``);
+    affine groups of a multiple of 16 columns that divide in_features."""
+    if in_features < 1:
+        raise ValueError(f"in_features={in_features} must be positive")
     if has_affine and (group_size <= 0 or group_size % 16 or in_features % group_size):
         raise ValueError(f"group_size={group_size} must be a multiple of 16 dividing "
                          f"in_features={in_features}")
+
+
+def padded_in_features(in_features: int) -> int:
+    """Columns of the kernels' index rows: in_features rounded up to 64 (the
+    prefill GEMM's K step; also a multiple of the GEMV's 16)."""
+    return -(-int(in_features) // 64) * 64
+
+
+def pad_columns(t: torch.Tensor, n_cols: int) -> torch.Tensor:
+    """t [rows, c] -> [rows, n_cols] with zero columns appended (t itself when
+    c == n_cols)."""
+    if t.shape[-1] == n_cols:
+        return t
+    return torch.cat([t, t.new_zeros(*t.shape[:-1], n_cols - t.shape[-1])], dim=-1).contiguous()
 
 
 def compressed_bytes(out_f: int, in_f: int, group_size: Optional[int], nnz: int,

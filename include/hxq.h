@@ -255,8 +255,8 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
  * hxq_prefill_gemm: the prefill GEMM Y = X W^T (+ bias) with W dequantised
  * straight into the MFMA operand registers (X [m_rows, in] in bf16 or fp16:
  * 16-bit MFMA on W rounded to X's type; or fp32: fp32 MFMA on the exact fp32
- * W; fp32 accumulation, y in y_dtype; in_features % 64 == 0; affine as for
- * hxq_gemm), for every index format (HXQ_FMT_*): uint8 with the 256-entry
+ * W; fp32 accumulation, y in y_dtype; in_features % 64 == 0), for every
+ * index format (HXQ_FMT_*): uint8 with the 256-entry
  * codebook, uint16 with n_codes entries, pair codebooks [n_codes, 2] (uint16
  * or 12-bit packed indices, no affine) and 6-bit levels (affine, no
  * codebook).  The sidecar comes in the kernel's order: for each group of 64
@@ -265,7 +265,12 @@ int hxq_gemm_ws(const void *x, int32_t x_dtype, const uint8_t *indices,
  * replacement values, and sc_grp_ptr int32 [ceil(out/64) * (in/64) + 1]
  * whose element g * (in/64) + t is the first entry of group g with a column
  * in K step t ([64t, 64t + 64)) or later, the last element being the entry
- * count (NULL sc_grp_ptr = no sidecar).  Shapes with few output tiles split K: a
+ * count (NULL sc_grp_ptr = no sidecar).  group_affine is fp32
+ * [ceil(in / group_size), out, 2] {scale, offset} (the layout hxq_affine_pack
+ * writes) for any group_size that is a positive multiple of 16; a caller
+ * whose true K is not a multiple of 64 pads X and the index rows with zero
+ * columns up to in_features and the affine with groups of (0, 0), so the
+ * padded columns contribute nothing.  Shapes with few output tiles split K: a
  * workspace of hxq_prefill_gemm_workspace_bytes(...) bytes holds fp32
  * partials, reduced in order (deterministic).
  * Replaces: fused_vq_matmul's N > 1 path (triton_vq_matmul.py:249-334,

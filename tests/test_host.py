@@ -233,10 +233,34 @@ def test_compressed_bytes_config0():
 def test_rejects_unsupported_shapes():
     L = synth.make_layer_np(8, 128, seed=1)
     T = synth.to_torch(L)
-    with pytest.raises(ValueError):
-        HelixLinear(120, 8, T["codebook"], T["indices"][:, :120])
+    with pytest.raises(ValueError):               # affine groups must divide in_features
+        HelixLinear(120, 8, T["codebook"], T["indices"][:, :120],
+                    group_scale=torch.ones(8, 1), group_offset=torch.zeros(8, 1), group_size=128)
     with pytest.raises(NotImplementedError):      # scalar codebooks hold <= 4096 entries
         HelixLinear(128, 8, torch.zeros(4097), T["indices"])
+
+
+@pytest.mark.parametrize("in_f,kw", [(120, {}), (100, {}), (1, {}), (4000, {"group_size": 32}),
+                                     (96, {"group_size": 48})])
+def test_any_in_features_kernel_layout(in_f, kw):
+    """in_features that are not a multiple of 64: the kernels' padded copy of
+    the index rows (zero columns up to the next multiple of 64) and the
+    affine's zero groups; the CPU forward is unchanged (oracle)."""
+    L = (synth.make_layer_np(40, in_f, seed=in_f, density=0.01, **kw) if kw else
+         synth.make_layer_np(40, in_f, seed=in_f, density=0.01, affine=False))
+    m = _module(L)
+    kp = -(-in_f // 64) * 64
+    assert m._kin == kp
+    assert m._kidx.shape == (40, kp)
+    assert torch.equal(m._kidx[:, :in_f], m.indices) and not m._kidx[:, in_f:].any()
+    if kw:
+        G = kw["group_size"]
+        assert m._affine_t.shape == (-(-kp // G), 40, 2)
+        assert not m._affine_t[in_f // G:].any()
+    x = torch.randn(3, in_f, generator=torch.Generator().manual_seed(1))
+    W = oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
+                           L["group_size"], L["sidecar_positions"], L["sidecar_values"])
+    np.testing.assert_allclose(m(x).numpy(), oracle.linear_f64(x.numpy(), W), rtol=1e-5, atol=1e-6)
 
 
 def test_forward_wave_threaded_tiles_match_oracle(monkeypatch):
