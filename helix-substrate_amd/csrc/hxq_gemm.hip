@@ -797,6 +797,19 @@ __global__ __launch_bounds__(256) void moe_silu_mul_kernel(const uint16_t *__res
         *reinterpret_cast<uint2 *>(h + i) = make_uint2(o[0] | (uint32_t{o[1]} << 16), o[2] | (uint32_t{o[3]} << 16));
     }
 }
+// fp32 activations: h = silu(g) * u in fp32, [rows, 2 * inter] -> [rows, inter]
+__global__ __launch_bounds__(256) void moe_silu_mul_f32_kernel(const float *__restrict__ gu, int64_t rows,
+                                                              int32_t inter, float *__restrict__ h) {
+    const int64_t n = rows * inter;
+    for (int64_t i = (int64_t{blockIdx.x} * 256 + threadIdx.x) * 4; i < n; i += int64_t{gridDim.x} * 1024) {
+        const int64_t r = i / inter;
+        const int32_t c = static_cast<int32_t>(i - r * inter);
+        const float4 g = *reinterpret_cast<const float4 *>(gu + r * 2 * inter + c);
+        const float4 u = *reinterpret_cast<const float4 *>(gu + r * 2 * inter + inter + c);
+        auto f = [](float a, float b) { return a / (1.f + expf(-a)) * b; };
+        *reinterpret_cast<float4 *>(h + i) = make_float4(f(g.x, u.x), f(g.y, u.y), f(g.z, u.z), f(g.w, u.w));
+    }
+}
 // V consecutive columns per thread (V = 4 when hidden % 4 == 0: 16-byte
 // loads of O); each column's slots are added in order either way.
 template <int YDT, int V>
@@ -1179,10 +1192,11 @@ extern "C" int64_t hxq_moe_ffn_workspace_bytes(int64_t n_tokens, int64_t hidden,
                                                int64_t intermediate, int32_t top_k) {
     if (n_tokens <= 0 || hidden <= 0 || intermediate <= 0 || top_k <= 0) return -1;
     const int64_t na = n_tokens * top_k;
-    const int64_t h_bytes = ((na * intermediate * 2 + 255) / 256) * 256;
+    // sized for fp32 activations (16-bit ones use the first half of H and GU)
+    const int64_t h_bytes = ((na * intermediate * 4 + 255) / 256) * 256;
     const int64_t o_bytes = ((na * hidden * 4 + 255) / 256) * 256;
-    // + the 16-bit gate|up outputs of the register-dequant path
-    return h_bytes + o_bytes + na * 2 * intermediate * 2 + 256;
+    // + the gate|up outputs of the register-dequant path
+    return h_bytes + o_bytes + na * 2 * intermediate * 4 + 256;
 }
 
 extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int64_t hidden,
@@ -1196,7 +1210,8 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     clear_error();
     HXQ_REQUIRE(x && topk_weights && expert_offsets && sorted_rows && assign_pos && y &&
                     workspace, "all pointers are required");
-    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16, "x must be bf16 or fp16");
+    HXQ_REQUIRE(x_dtype == HXQ_BF16 || x_dtype == HXQ_F16 || x_dtype == HXQ_F32,
+                "x must be fp32, bf16 or fp16");
     HXQ_REQUIRE(y_dtype >= HXQ_F32 && y_dtype <= HXQ_F16, "bad y_dtype");
     HXQ_REQUIRE(n_experts >= 1 && n_experts <= 256, "n_experts must be in 1..256");
     HXQ_REQUIRE(top_k >= 1 && top_k <= n_experts, "top_k must be in 1..n_experts");
@@ -1205,7 +1220,7 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
                 "hidden and intermediate must be multiples of 64");
     const int64_t na = n_tokens * top_k;
     HXQ_REQUIRE(na * std::max(hidden, intermediate) * 4 < (int64_t{1} << 31) &&
-                    n_tokens * hidden * 2 < (int64_t{1} << 31),
+                    n_tokens * hidden * 4 < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
     const int64_t need = hxq_moe_ffn_workspace_bytes(n_tokens, hidden, intermediate, top_k);
     HXQ_REQUIRE(workspace_bytes >= need, "workspace too small (hxq_moe_ffn_workspace_bytes)");
@@ -1216,13 +1231,17 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     HXQ_REQUIRE((gate->group_affine != nullptr) == (up->group_affine != nullptr),
                 "gate and up must agree on the affine");
     const bool bf16 = x_dtype == HXQ_BF16;
+    const bool f32 = x_dtype == HXQ_F32;
+    // H and GU hold x's type (fp32 activations: fp32 throughout)
     uint16_t *H = static_cast<uint16_t *>(workspace);
     float *O = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                         ((na * intermediate * 2 + 255) / 256) * 256);
+                                         ((na * intermediate * 4 + 255) / 256) * 256);
     uint16_t *GU = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(O) + ((na * hidden * 4 + 255) / 256) * 256);
     const bool reg = pg::grouped_ok(gate, intermediate, hidden, group_size) &&
                      pg::grouped_ok(up, intermediate, hidden, group_size) &&
                      pg::grouped_ok(down, hidden, intermediate, group_size) && intermediate % 256 == 0;
+    HXQ_REQUIRE(reg || !f32, "fp32 activations need the register-dequant grouped kernel "
+                             "(uint8 indices, group_size a multiple of 64, intermediate a multiple of 256)");
     if (reg) {
         // 1) GU = [X_e Wg_e^T | X_e Wu_e^T] (one grouped launch, x's 16-bit type), H = silu(G) * U
         pg::GroupedReq r{};
@@ -1244,7 +1263,11 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
         if (int rc = pg::grouped_gemm(r, stream)) return rc;
         const int64_t n4 = na * intermediate / 4;
         const dim3 sg(static_cast<uint32_t>(std::min<int64_t>((n4 + 255) / 256, 4096)));
-        if (bf16)
+        if (f32)
+            hipLaunchKernelGGL(moe_silu_mul_f32_kernel, sg, dim3(256), 0, stream,
+                               reinterpret_cast<const float *>(GU), na,
+                               static_cast<int32_t>(intermediate), reinterpret_cast<float *>(H));
+        else if (bf16)
             hipLaunchKernelGGL(moe_silu_mul_kernel<true>, sg, dim3(256), 0, stream, GU, na,
                                static_cast<int32_t>(intermediate), H);
         else

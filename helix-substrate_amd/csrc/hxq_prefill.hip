@@ -859,7 +859,8 @@ bool grouped_ok(const hxq_expert_bank *b, int64_t out, int64_t in, int32_t group
 #endif
 int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     HXQ_REQUIRE(r.x && r.seg && r.bank0 && r.y, "x, expert_offsets, bank and y are required");
-    HXQ_REQUIRE(r.x_dtype == HXQ_BF16 || r.x_dtype == HXQ_F16, "x must be bf16 or fp16");
+    HXQ_REQUIRE(r.x_dtype == HXQ_BF16 || r.x_dtype == HXQ_F16 || r.x_dtype == HXQ_F32,
+                "x must be fp32, bf16 or fp16");
     HXQ_REQUIRE(r.y_dtype >= HXQ_F32 && r.y_dtype <= HXQ_F16, "bad y_dtype");
     HXQ_REQUIRE(r.n_exp >= 1 && r.n_exp <= 256, "n_experts must be in 1..256");
     HXQ_REQUIRE(r.n_assign > 0 && r.x_rows > 0 && r.out0 > 0 && r.in > 0, "empty problem");
@@ -869,7 +870,8 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
                              (r.bank0->group_affine != nullptr) == (r.bank1->group_affine != nullptr)),
                 "the second bank needs out0 % 256 == 0 and the same affine layout");
     const int64_t out = r.out0 + (r.bank1 ? r.out1 : 0);
-    HXQ_REQUIRE(r.x_rows * r.in * 2 < (int64_t{1} << 31) && r.n_assign * out * 4 < (int64_t{1} << 31),
+    HXQ_REQUIRE(r.x_rows * r.in * (r.x_dtype == HXQ_F32 ? 4 : 2) < (int64_t{1} << 31) &&
+                    r.n_assign * out * 4 < (int64_t{1} << 31),
                 "problem too large for 32-bit offsets");
     HXQ_REQUIRE((reinterpret_cast<uintptr_t>(r.x) & 15u) == 0 &&
                     (reinterpret_cast<uintptr_t>(r.bank0->indices) & 15u) == 0 &&
@@ -915,8 +917,10 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
     a.ga_es = aff ? (r.in / a.group) * wo : 0;
     a.scp_es = (wo + 63) / 64 * (r.in / kBK) + 1;
     // 256-row tiles when the experts average more than 192 rows, 128 above 96, else 64
+    // (fp32 activations: 128-row tiles always, the fp32 A tile doubles the LDS)
     const int64_t mean_rows = r.n_assign / r.n_exp;
-    const int bm = mean_rows > 192 ? 256 : mean_rows > GRP_BM64_MAX ? 128 : 64;
+    const bool f32 = r.x_dtype == HXQ_F32;
+    const int bm = f32 ? 128 : mean_rows > 192 ? 256 : mean_rows > GRP_BM64_MAX ? 128 : 64;
     a.grp_tiles_x = static_cast<int32_t>((out + kBN - 1) / kBN);
     const int64_t row_tiles = (r.n_assign + bm - 1) / bm + r.n_exp;  // upper bound over any routing
     a.grp_per_xcd = static_cast<int32_t>((row_tiles + kXcds - 1) / kXcds * a.grp_tiles_x);
@@ -925,7 +929,9 @@ int grouped_gemm(const GroupedReq &r, hipStream_t stream) {
 #define HXQ_PG_GRP(BM_, BF_, AF_) \
     hipLaunchKernelGGL((prefill_kernel<BM_, BF_, AF_, kNJ, HXQ_FMT_SCALAR, true>), grid, \
                        dim3(kBN / (32 * kNJ) * 64), 0, stream, a)
-    if (bm == 256) {
+    if (f32) {
+        if (aff) HXQ_PG_GRP(128, 2, true); else HXQ_PG_GRP(128, 2, false);
+    } else if (bm == 256) {
         if (bf16) { if (aff) HXQ_PG_GRP(256, 1, true); else HXQ_PG_GRP(256, 1, false); }
         else { if (aff) HXQ_PG_GRP(256, 0, true); else HXQ_PG_GRP(256, 0, false); }
     } else if (bm == 64) {

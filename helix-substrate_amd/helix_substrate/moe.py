@@ -188,8 +188,8 @@ class HelixMoeExperts(nn.Module):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         if x2.is_cuda:
-            if x2.dtype not in (torch.bfloat16, torch.float16):
-                raise RuntimeError("the grouped MoE kernels take bf16 or fp16 activations")
+            if x2.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+                x2 = x2.float()
             r = _hxq.moe_route(router_logits.reshape(x2.shape[0], -1), self.top_k,
                                self.norm_topk_prob)
             y = _hxq.moe_ffn(x2.contiguous(), r, self.banks["gate"], self.banks["up"],

@@ -138,6 +138,28 @@ def test_moe_ffn_matches_oracle(dev, T, E, k, H, I, renorm):
     assert torch.equal(y32, _hxq.moe_ffn(x.to(dev), r, bg, bu, bd, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("T,E,k,H,I,renorm", [(128, 8, 2, 256, 256, False),
+                                              (33, 16, 4, 512, 512, True)])
+def test_moe_ffn_fp32_activations(dev, T, E, k, H, I, renorm):
+    """fp32 activations (the reference's per-expert HelixLinear takes any
+    dtype): fp32 MFMA on the exact fp32 W, fp32 SiLU product, fp32 output,
+    1e-5 against the fp64 oracle."""
+    g, bg = _bank(E, I, H, seed=110, dev=dev, group_size=64)
+    u, bu = _bank(E, I, H, seed=210, dev=dev, group_size=64)
+    d, bd = _bank(E, H, I, seed=310, dev=dev, group_size=64)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(6))
+    lg = _skewed_logits(T, E, 10, dev)
+    m = moe.HelixMoeExperts(bg, bu, bd, top_k=k, norm_topk_prob=renorm)
+    print(f"moe fp32 T={T} E={E} k={k}", flush=True)
+    y = m(x.to(dev), lg)
+    assert m._last_dispatch_path == "hip_moe" and y.dtype == torch.float32
+    ids, w = oracle.moe_route_np(lg.cpu().numpy(), k, renorm)
+    ref = oracle.moe_ffn_np(x.numpy(), ids, w, [oracle.reconstruct(**L) for L in g],
+                            [oracle.reconstruct(**L) for L in u],
+                            [oracle.reconstruct(**L) for L in d])
+    assert _maxrel(y.cpu().numpy(), ref) <= 1e-5
+
+
 def test_moe_config4_layer_slice(dev):
     """Config 4 (OLMoE: hidden 2048, 64 experts x SwiGLU 1024, top-8, 512
     tokens) on the GPU; a few tokens are checked against the oracle, which
