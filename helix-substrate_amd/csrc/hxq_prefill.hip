@@ -193,7 +193,11 @@ __host__ __device__ constexpr int fmt_b32(int f) {
 // Activation types: XT 0 = fp16, 1 = bf16 (v_mfma_f32_32x32x16_{f16,bf16},
 // B packed as 16-bit pairs), 2 = fp32 (v_mfma_f32_32x32x2_f32, fp32 B: the
 // fp32 path keeps fp32 arithmetic end to end).
-template <int BM, int XT, bool AFFINE, int NJ, int FMT, bool GRP = false>
+// GM, the affine group layout: 0 group % 64 == 0 (one group per K step);
+// 1 group % 32 == 0 (each lane finds its own group); 2 group % 16 == 0 (a
+// lane's 32 weights span two groups: a second set of factors per row).  The
+// per-lane forms cost registers, so the common layout keeps its own build.
+template <int BM, int XT, bool AFFINE, int NJ, int FMT, bool GRP = false, int GM = 0>
 // 64-row tiles (80 KB of LDS) run two blocks per CU: four waves per SIMD
 __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefill_kernel(const Args g) {
     constexpr bool F32 = XT == 2;
@@ -336,7 +340,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     u32x4 xv[2][XP];   // X of steps s (buffer s & 1)
     u32x4 qv[2][NQ * NJ]; // index bytes of row j: qv[.][NQ j .. NQ j + NQ)
     float2 av[2][NJ];     // {scale, offset} per j (weights 0..15 of the lane's 32)
-    float2 av2[2][NJ];    // ... of weights 16..31 (the same group unless g16)
+    constexpr bool G16 = GM == 2;
+    float2 av2[G16 ? 2 : 1][NJ];  // GM 2: ... of weights 16..31
     auto load_step = [&](int s, int buf) {
         const bool live = s < nk;
         const uint32_t k0 = static_cast<uint32_t>((kb + (live ? s : 0)) * kBK);
@@ -362,15 +367,14 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
             // for the whole step when group % 64 == 0 (uniform), else per lane
             const uint32_t G = static_cast<uint32_t>(g.group);
             const uint32_t row8 = static_cast<uint32_t>(wout) * 8u;
-            const uint32_t ga = g.g_lane ? (k0 + 32u * hh) / G : k0 / G;
+            const uint32_t ga = GM == 0 ? k0 / G : (k0 + 32u * hh) / G;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const uint32_t o = (a_off[j] == kOob || !live) ? kOob : a_off[j] + ga * row8;
                 const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(ar, o, 0, 0);
                 av[buf][j] = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
-                av2[buf][j] = av[buf][j];
             }
-            if (g.g16) {
+            if constexpr (G16) {
                 const uint32_t gb = (k0 + 32u * hh + 16u) / G;
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
@@ -434,8 +438,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             // substep s holds weights 8s .. 8s+7: the first 16 for s < 2
-            const float sc = AFFINE ? (s < 2 ? av[buf][j].x : av2[buf][j].x) : 1.f;
-            const float of = AFFINE ? (s < 2 ? av[buf][j].y : av2[buf][j].y) : 0.f;
+            const float sc = AFFINE ? (G16 && s >= 2 ? av2[G16 ? buf : 0][j].x : av[buf][j].x) : 1.f;
+            const float of = AFFINE ? (G16 && s >= 2 ? av2[G16 ? buf : 0][j].y : av[buf][j].y) : 0.f;
             if constexpr (FMT == HXQ_FMT_SCALAR_U16) {
                 // weights 8s .. 8s+7: the 16 bytes of load s, eight uint16 indices
                 const u32x4 q = qv[buf][NQ * j + s];
@@ -502,8 +506,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     // (weights 4q .. 4q+3) feeds MFMA substeps 4q .. 4q+3
     auto dequant_f32 = [&](int buf, int q, BV &b) {
         if constexpr (F32) {
-        const float sc = AFFINE ? (q < 4 ? av[buf][0].x : av2[buf][0].x) : 1.f;
-        const float of = AFFINE ? (q < 4 ? av[buf][0].y : av2[buf][0].y) : 0.f;
+        const float sc = AFFINE ? (G16 && q >= 4 ? av2[G16 ? buf : 0][0].x : av[buf][0].x) : 1.f;
+        const float of = AFFINE ? (G16 && q >= 4 ? av2[G16 ? buf : 0][0].y : av[buf][0].y) : 0.f;
         float v[4];
         if constexpr (FMT == HXQ_FMT_SCALAR) {
             const uint32_t w = qv[buf][q >> 2][q & 3];
@@ -1045,9 +1049,18 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
         a.tiles_per_xcd = (L.n + pg::kXcds - 1) / pg::kXcds;
         a.vec_out = L.ks == 1 && vec;
         const dim3 grid(a.tiles_per_xcd * pg::kXcds, L.ks);
-#define HXQ_PG_LAUNCH(BM_, BF_, AF_, F_) \
-        hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ, F_>), grid, \
-                           dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a)
+#define HXQ_PG_LAUNCH(BM_, BF_, AF_, F_)                                                      \
+        do {                                                                                  \
+            if ((AF_) && a.g16)                                                               \
+                hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ, F_, false, 2>), \
+                                   grid, dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a);  \
+            else if ((AF_) && a.g_lane)                                                       \
+                hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ, F_, false, 1>), \
+                                   grid, dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a);  \
+            else                                                                              \
+                hipLaunchKernelGGL((pg::prefill_kernel<BM_, BF_, AF_, pg::kNJ, F_>), grid,     \
+                                   dim3(pg::kBN / (32 * pg::kNJ) * 64), 0, stream, a);        \
+        } while (0)
 #define HXQ_PG_FMT(BM_, BF_)                                                                  \
         switch (format) {                                                                      \
             case HXQ_FMT_SCALAR:                                                               \
