@@ -27,6 +27,7 @@
 // are read as LDS broadcasts; per-split y partials are summed through LDS in a
 // fixed order (deterministic).
 #include <algorithm>
+#include <cstdlib>
 
 #include "hxq_common.h"
 
@@ -640,6 +641,336 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
     }
 }
 
+// Accumulator tile -> MFMA operand.  An accumulator holds, in lane (c, h),
+// the values at k = 8 (r / 4) + 4 h + r % 4 (r = 0..15) of column c; an A or
+// B operand of a 16-wide k step ks2 wants k = 16 ks2 + 8 h + 0..7 of the same
+// column.  Lane h = 0 has k 0..3 and 8..11 of each step, lane h = 1 has 4..7
+// and 12..15: v_permlane32_swap of the two 4-value groups gives each lane the
+// other half's group.  The values are split into bf16 hi + lo (16 mantissa
+// bits); op[ks2][0] is hi, op[ks2][1] lo.
+__device__ __forceinline__ void acc_to_op(const f32x16 &m, u32x4 (&op)[2][2]) {
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+        const int q0 = 2 * ks2, q1 = 2 * ks2 + 1;
+        uint32_t xh0, xl0, xh1, xl1, yh0, yl0, yh1, yl1;
+        split2x2(m[4 * q0], m[4 * q0 + 1], xh0, xl0);
+        split2x2(m[4 * q0 + 2], m[4 * q0 + 3], xh1, xl1);
+        split2x2(m[4 * q1], m[4 * q1 + 1], yh0, yl0);
+        split2x2(m[4 * q1 + 2], m[4 * q1 + 3], yh1, yl1);
+        const auto h0 = __builtin_amdgcn_permlane32_swap(xh0, yh0, false, false);
+        const auto h1 = __builtin_amdgcn_permlane32_swap(xh1, yh1, false, false);
+        const auto l0 = __builtin_amdgcn_permlane32_swap(xl0, yl0, false, false);
+        const auto l1 = __builtin_amdgcn_permlane32_swap(xl1, yl1, false, false);
+        op[ks2][0] = u32x4{h0[0], h1[0], h0[1], h1[1]};
+        op[ks2][1] = u32x4{l0[0], l1[0], l0[1], l1[1]};
+    }
+}
+
+// The SSD chunk form with two blocks per CU (74.5 KB of LDS at state 128).
+// Same math and splits as ssd_kernel; what changes is where the fp32 operands
+// live: each (c)/(d) wave (t-tile ti, p-tile pj) computes the decay-masked
+// M tiles of its own t rows (the pair of waves with the same ti both do) and
+// turns them into (c)'s B operand in registers; the state stays in the (e)
+// waves' accumulators and becomes (d)'s A operand in registers, each wave
+// contracting its own n tiles for both t tiles and handing the other t
+// tile's partial to its partner through LDS; X' = w x is formed from x^T
+// where (e) reads it.  Three barriers per chunk.
+template <int NT>  // state tiles of 32 (NP = 32 NT)
+__global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
+    constexpr int NP = 32 * NT;
+    constexpr int CN = NP / 8;   // 16-byte chunks per row of n
+    __shared__ __attribute__((aligned(16))) uint16_t sC[kQ * NP];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[kQ * NP];
+    __shared__ __attribute__((aligned(16))) uint16_t sBt[NP * kQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sXt[kPP * kQ];
+    // (d) partials handed between the two waves of a p tile: [pj][t tile][r][lane]
+    __shared__ __attribute__((aligned(16))) float sZ[2][2][16][64];
+    __shared__ double scs2[2][kQ];
+    __shared__ float sdt2[2][kQ], swt2[2][kQ];
+    __shared__ __attribute__((aligned(16))) float sec2[2][kQ];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ml = lane & 31, hh = lane >> 5;
+    const int b = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const int H = a.heads, P = a.head_dim, N = a.state, L = a.seqlen;
+    const int g = h / (H / a.ngroups);
+    const float Ah = a.A[h];
+    const float Dh = a.D ? a.D[h] : 0.f;
+    const int ti = wave >> 1, pj = wave & 1;  // (c)/(d) output tile; (e) p tile
+    // (e) state tiles: p tile pj, n tiles [nj0, nj0 + nst) (NT = 1: waves 2, 3 hold none)
+    const int nst = NT == 4 ? 2 : 1;
+    const int nj0 = NT == 4 ? 2 * ti : ti;
+    const bool has_s = NT >= 2 || wave < 2;
+    const int sp = 32 * pj + ml;
+    const int64_t y_bytes = (int64_t)a.batch * L * H * P * (a.y_dt == HXQ_F32 ? 4 : 2);
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, y_bytes);
+    constexpr uint32_t kYOob = 0xfffffff0u;
+
+    // ---- chunk inputs (as ssd_kernel) ------------------------------------------
+    constexpr uint32_t kOob = 0xfffffff0u;
+    const int dtb = a.dt_dt == HXQ_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (int64_t)a.batch * L * H * P * 2);
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.Bm, (int64_t)a.batch * L * a.ngroups * N * 2);
+    const __amdgpu_buffer_rsrc_t cr = make_rsrc(a.Cm, (int64_t)a.batch * L * a.ngroups * N * 2);
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(a.dt, (int64_t)a.batch * L * H * dtb);
+    constexpr int BC_ITEMS = (kQ / 2) * CN;
+    constexpr int BC_PER = (BC_ITEMS + kThreads - 1) / kThreads;
+    u32x4 rB[BC_PER][2], rC[BC_PER][2];
+    u32x4 rX[2];
+    auto load_chunk = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < BC_PER; ++i) {
+            const int item = tid + kThreads * i;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int t = t0 + 2 * (item / CN) + e, c = item % CN;
+                const bool ok = item < BC_ITEMS && t < L && 8 * c < N;
+                const uint32_t o = ok ? static_cast<uint32_t>(((((int64_t)b * L + t) * a.ngroups + g) * N + 8 * c) * 2) : kOob;
+                rB[i][e] = buf_load16(br, o);
+                rC[i][e] = buf_load16(cr, o);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = t0 + 2 * (tid >> 3) + e, c = tid & 7;
+            const bool ok = t < L && 8 * c < P;
+            rX[e] = buf_load16(xr, ok ? static_cast<uint32_t>(((((int64_t)b * L + t) * H + h) * P + 8 * c) * 2) : kOob);
+        }
+    };
+    auto load_dt = [&](int t0) -> uint32_t {
+        const int t = t0 + lane;
+        const uint32_t o = t < L ? static_cast<uint32_t>((((int64_t)b * L + t) * H + h) * dtb) : kOob;
+        return dtb == 4 ? __builtin_amdgcn_raw_buffer_load_b32(dr, o, 0, 0)
+                        : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(dr, o, 0, 0));
+    };
+    auto dt_value = [&](uint32_t raw) -> float {
+        return a.dt_dt == HXQ_F32 ? __uint_as_float(raw)
+             : a.dt_dt == HXQ_BF16 ? bf16_to_f32(static_cast<uint16_t>(raw)) : f16_to_f32(static_cast<uint16_t>(raw));
+    };
+    auto decay_terms = [&](float dtv, int buf) {
+        double cs = static_cast<double>(Ah * dtv);
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double o = __shfl_up(cs, off, 64);
+            if (lane >= off) cs += o;
+        }
+        cs *= 1.4426950408889634;  // log2(e)
+        const double csq = __shfl(cs, 63, 64);
+        scs2[buf][lane] = cs;
+        sdt2[buf][lane] = dtv;
+        swt2[buf][lane] = exp2_fast(static_cast<float>(csq - cs)) * dtv;
+        sec2[buf][lane] = exp2_fast(static_cast<float>(cs));
+    };
+    auto pair_of = [](const u32x4 &v0, const u32x4 &v1, int k) -> uint32_t {
+        const uint32_t a0 = (v0[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+        const uint32_t a1 = (v1[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+        return a0 | (a1 << 16);
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (int i = 0; i < BC_PER; ++i) {
+            const int item = tid + kThreads * i;
+            if (item >= BC_ITEMS) continue;
+            const int u = item / CN, c = item % CN;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                *reinterpret_cast<u32x4 *>(sB + sw<CN>(2 * u + e, c)) = rB[i][e];
+                *reinterpret_cast<u32x4 *>(sC + sw<CN>(2 * u + e, c)) = rC[i][e];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                *reinterpret_cast<uint32_t *>(sBt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
+                    pair_of(rB[i][0], rB[i][1], k);
+        }
+        const int u = tid >> 3, c = tid & 7;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            *reinterpret_cast<uint32_t *>(sXt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
+                pair_of(rX[0], rX[1], k);
+    };
+
+    // ---- state: Sacc[j][r] = S[p = 32 pj + ml][n = 32(nj0 + j) + 8(r/4) + 4hh + r%4]
+    // h0 / h_final through buffer resources: elements outside (p < P, n < N)
+    // take an offset past the range (reads give 0, writes are dropped), so no
+    // per-element lane masks stay live across the chunk loop
+    const int64_t st_bytes = (int64_t)a.batch * H * P * N * 4;
+    const __amdgpu_buffer_rsrc_t h0r = make_rsrc(a.h0, a.h0 ? st_bytes : 0);
+    const __amdgpu_buffer_rsrc_t hfr = make_rsrc(a.h_final, a.h_final ? st_bytes : 0);
+    auto st_off = [&](int j, int r) -> uint32_t {
+        const int n = 32 * (nj0 + j) + 8 * (r >> 2) + 4 * hh + (r & 3);
+        return (has_s && j < nst && sp < P && n < N)
+                   ? static_cast<uint32_t>(((((int64_t)b * H + h) * P + sp) * N + n) * 4) : kOob;
+    };
+    f32x16 Sacc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            Sacc[j][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h0r, st_off(j, r), 0, 0));
+
+    const int nch = (L + kQ - 1) / kQ;
+    load_chunk(0);
+    uint32_t rdt = load_dt(0);
+    if (wave == 0) decay_terms(dt_value(rdt), 0);
+    rdt = load_dt(kQ);
+    for (int ch = 0; ch < nch; ++ch) {
+        const int t0 = ch * kQ;
+        const int db = ch & 1;
+        const double *scs = scs2[db];
+        const float *sdt = sdt2[db], *swt = swt2[db], *sec = sec2[db];
+        lds_barrier();  // the previous chunk's readers of the inputs and partials are done
+        store_chunk();
+        lds_barrier();
+        if (wave == 0 && ch + 1 < nch) {
+            decay_terms(dt_value(rdt), db ^ 1);
+            rdt = load_dt(t0 + 2 * kQ);
+        }
+
+        // (a)+(b): the M tiles of t tile ti (s tiles 0..ti), as (c)'s B operand
+        const int t = 32 * ti + ml;
+        const double cst = scs[t];
+        u32x4 mop[2][2][2];  // [s tile][k step][hi, lo]
+#pragma unroll
+        for (int si = 0; si < 2; ++si) {
+            if (si > ti) break;
+            f32x16 cb;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cb[r] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < NP / 16; ++ks) {
+                const u32x4 bv = lds16(sB + sw<CN>(32 * si + ml, 2 * ks + hh));
+                const u32x4 cv = lds16(sC + sw<CN>(32 * ti + ml, 2 * ks + hh));
+                cb = mfma(bv, cv, cb);
+            }
+            // cb[r]: s = 32 si + 8(r/4) + 4hh + r%4 of column t
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int s = 32 * si + 8 * (r >> 2) + 4 * hh + (r & 3);
+                cb[r] = s <= t ? cb[r] * exp2_fast(static_cast<float>(cst - scs[s])) * sdt[s] : 0.f;
+            }
+            acc_to_op(cb, mop[si]);
+        }
+
+        // (d): Z^T partials over this wave's n tiles, for its own t tile (kept)
+        // and the partner's (handed over through LDS)
+        f32x16 zown, zoth;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) zown[r] = zoth[r] = 0.f;
+        if (has_s) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (j >= nst) break;
+                u32x4 sop[2][2];
+                acc_to_op(Sacc[j], sop);
+#pragma unroll
+                for (int ks2 = 0; ks2 < 2; ++ks2) {
+                    const int c = 4 * (nj0 + j) + 2 * ks2 + hh;  // 16-byte chunk of n
+                    const u32x4 cvo = lds16(sC + sw<CN>(32 * ti + ml, c));
+                    const u32x4 cvp = lds16(sC + sw<CN>(32 * (ti ^ 1) + ml, c));
+                    zown = mfma(sop[ks2][0], cvo, zown);
+                    zoth = mfma(sop[ks2][0], cvp, zoth);
+                    zown = mfma(sop[ks2][1], cvo, zown);
+                    zoth = mfma(sop[ks2][1], cvp, zoth);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sZ[pj][ti ^ 1][r][lane] = zoth[r];
+        // the next chunk's inputs: issued once P1's operands are dead (their
+        // registers are free), landing while (c) and (e) run
+        if (ch + 1 < nch) load_chunk(t0 + kQ);
+        lds_barrier();
+
+        // (c) Y^T = x^T M^T over s <= end of t tile ti; y = Y + exp(cs_t) Z + D x
+        {
+            f32x16 yv, zv = zown;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                yv[r] = 0.f;
+                zv[r] += sZ[pj][ti][r][lane];
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                if (ks >= 2 * (ti + 1)) break;
+                const u32x4 xa = lds16(sXt + swq(32 * pj + ml, 2 * ks + hh));
+                yv = mfma(xa, mop[ks >> 1][ks & 1][0], yv);
+                yv = mfma(xa, mop[ks >> 1][ks & 1][1], yv);
+            }
+            const float et = sec[t];
+            const bool t_ok = t0 + t < L;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int p0 = 32 * pj + 8 * q + 4 * hh;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xv = bf16_to_f32(sXt[swq(p0 + e, t >> 3) + (t & 7)]);
+                    v[e] = yv[4 * q + e] + et * zv[4 * q + e] + Dh * xv;
+                }
+                const bool ok = t_ok && p0 < P;
+                const uint32_t yo = static_cast<uint32_t>((((int64_t)b * L + t0 + t) * H + h) * P + p0);
+                if (a.y_dt == HXQ_F32) {
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                              __float_as_uint(v[3])},
+                        yr, ok ? yo * 4u : kYOob, 0, 0);
+                } else {
+                    u32x2 w;
+                    if (a.y_dt == HXQ_BF16) {
+                        w = u32x2{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
+                    } else {
+                        w = u32x2{uint32_t(f32_to_f16(v[0])) | (uint32_t(f32_to_f16(v[1])) << 16),
+                                  uint32_t(f32_to_f16(v[2])) | (uint32_t(f32_to_f16(v[3])) << 16)};
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b64(w, yr, ok ? yo * 2u : kYOob, 0, 0);
+                }
+            }
+        }
+
+        // (e) S = exp(cs_Q) S + X'^T B, X'[s][p] = w_s x[s][p] formed from x^T
+        if (has_s) {
+            const float eq = exp2_fast(static_cast<float>(scs[kQ - 1]));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (j >= nst) break;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) Sacc[j][r] *= eq;
+            }
+#pragma unroll
+            for (int ks = 0; ks < kQ / 16; ++ks) {
+                const u32x4 xx = lds16(sXt + swq(sp, 2 * ks + hh));
+                const int s0 = 16 * ks + 8 * hh;
+                u32x4 xh, xl;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const float x0 = __uint_as_float(xx[d] << 16) * swt[s0 + 2 * d];
+                    const float x1 = __uint_as_float(xx[d] & 0xffff0000u) * swt[s0 + 2 * d + 1];
+                    uint32_t hv, lv;
+                    split2x2(x0, x1, hv, lv);
+                    xh[d] = hv;
+                    xl[d] = lv;
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if (j >= nst) break;
+                    const u32x4 bt = lds16(sBt + swq(32 * (nj0 + j) + ml, 2 * ks + hh));
+                    Sacc[j] = mfma(bt, xh, Sacc[j]);
+                    Sacc[j] = mfma(bt, xl, Sacc[j]);
+                }
+            }
+        }
+    }
+    if (a.h_final) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sacc[j][r]), hfr, st_off(j, r), 0, 0);
+    }
+}
+
 }  // namespace ssd
 
 // The SSD kernel's shapes and dtypes: bf16 x/B/C, head_dim <= 64, state <= 128.
@@ -651,11 +982,27 @@ static bool ssd_eligible(const ScanArgs &a) {
            bc_bytes < (int64_t{1} << 31);
 }
 
+// HXQ_SSD_V1=1 (read once per process) keeps the one-block-per-CU kernel with
+// its LDS operand copies (comparison runs).
+static bool ssd_v1() {
+    static const bool v = [] {
+        const char *e = getenv("HXQ_SSD_V1");
+        return e && atoi(e) != 0;
+    }();
+    return v;
+}
+
 static int launch_ssd(const ScanArgs &a, hipStream_t stream) {
     const dim3 grid(a.batch * a.heads);
-    if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
-    else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
-    else hipLaunchKernelGGL(ssd::ssd_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
+    if (ssd_v1()) {
+        if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
+        else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
+        else hipLaunchKernelGGL(ssd::ssd_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
+    } else {
+        if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd2_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
+        else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd2_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
+        else hipLaunchKernelGGL(ssd::ssd2_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
+    }
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }
