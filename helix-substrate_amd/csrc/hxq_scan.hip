@@ -288,6 +288,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Element offset of 16-byte chunk c in row r of an LDS matrix of bf16 rows
@@ -641,6 +643,21 @@ __global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
     }
 }
 
+// Rows of kPP = 64 bf16 (x in natural order, rows s): 8 chunks, XOR with
+// (r / 2) % 8 -- the transposing reads below touch rows r0 + {0..3, 8..11}
+// at four consecutive chunks, which this spreads over all 64 banks.
+__device__ __forceinline__ int swx(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) << 3); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, result lane 4q + c gets as
+// element e the element c of the 8 bytes addressed by lane 4e + q.
+__device__ __forceinline__ u32x2 lds_tr(const uint16_t *p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4 *)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
 // Accumulator tile -> MFMA operand.  An accumulator holds, in lane (c, h),
 // the values at k = 8 (r / 4) + 4 h + r % 4 (r = 0..15) of column c; an A or
 // B operand of a 16-wide k step ks2 wants k = 16 ks2 + 8 h + 0..7 of the same
@@ -666,27 +683,35 @@ __device__ __forceinline__ void acc_to_op(const f32x16 &m, u32x4 (&op)[2][2]) {
     }
 }
 
-// The SSD chunk form with two blocks per CU (74.5 KB of LDS at state 128).
-// Same math and splits as ssd_kernel; what changes is where the fp32 operands
-// live: each (c)/(d) wave (t-tile ti, p-tile pj) computes the decay-masked
-// M tiles of its own t rows (the pair of waves with the same ti both do) and
-// turns them into (c)'s B operand in registers; the state stays in the (e)
-// waves' accumulators and becomes (d)'s A operand in registers, each wave
-// contracting its own n tiles for both t tiles and handing the other t
-// tile's partial to its partner through LDS; X' = w x is formed from x^T
-// where (e) reads it.  Three barriers per chunk.
+// The SSD chunk form with two blocks per CU (70.5 KB of LDS at state 128).
+// Same math and splits as ssd_kernel; what changes is where the operands live:
+//  - the three decay-masked M tiles (t, s) = (0, 0), (1, 0), (1, 1) are built
+//    once each, by waves 0, 2, 3 (wave 1 computes the next chunk's decay
+//    terms instead), with D added on the diagonal so that (c)'s product
+//    carries y's D x term, and handed to (c) in B-operand form through LDS;
+//  - the state stays in the (e) waves' accumulators and becomes (d)'s A
+//    operand in registers (v_permlane32_swap), each wave contracting its own
+//    n tiles for both t tiles and handing the other t tile's partial to its
+//    partner through LDS;
+//  - B^T and x^T operands come from the s-major B and x tiles through
+//    transposing LDS reads (ds_read_b64_tr_b16), so no transposed copies are
+//    stored; X' = w x is formed where (e) reads x^T.
+// The next chunk's inputs are loaded into registers right after the current
+// chunk is stored to LDS.  Three barriers per chunk.
 template <int NT>  // state tiles of 32 (NP = 32 NT)
 __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
     constexpr int NP = 32 * NT;
     constexpr int CN = NP / 8;   // 16-byte chunks per row of n
     __shared__ __attribute__((aligned(16))) uint16_t sC[kQ * NP];
     __shared__ __attribute__((aligned(16))) uint16_t sB[kQ * NP];
-    __shared__ __attribute__((aligned(16))) uint16_t sBt[NP * kQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sXt[kPP * kQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sX[kQ * kPP];
     // (d) partials handed between the two waves of a p tile: [pj][t tile][r][lane]
     __shared__ __attribute__((aligned(16))) float sZ[2][2][16][64];
-    __shared__ double scs2[2][kQ];
-    __shared__ float sdt2[2][kQ], swt2[2][kQ];
+    // M tiles (t, s) = (0, 0), (1, 0), (1, 1) in (c)'s B-operand form, each built
+    // by one wave: [tile][k step][hi, lo][lane]
+    __shared__ __attribute__((aligned(16))) u32x4 sM[3][2][2][64];
+    __shared__ __attribute__((aligned(16))) double scs2[2][kQ];
+    __shared__ __attribute__((aligned(16))) float sdt2[2][kQ], swt2[2][kQ];
     __shared__ __attribute__((aligned(16))) float sec2[2][kQ];
 
     const int tid = threadIdx.x;
@@ -763,11 +788,6 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
         swt2[buf][lane] = exp2_fast(static_cast<float>(csq - cs)) * dtv;
         sec2[buf][lane] = exp2_fast(static_cast<float>(cs));
     };
-    auto pair_of = [](const u32x4 &v0, const u32x4 &v1, int k) -> uint32_t {
-        const uint32_t a0 = (v0[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-        const uint32_t a1 = (v1[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-        return a0 | (a1 << 16);
-    };
     auto store_chunk = [&]() {
 #pragma unroll
         for (int i = 0; i < BC_PER; ++i) {
@@ -779,16 +799,28 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
                 *reinterpret_cast<u32x4 *>(sB + sw<CN>(2 * u + e, c)) = rB[i][e];
                 *reinterpret_cast<u32x4 *>(sC + sw<CN>(2 * u + e, c)) = rC[i][e];
             }
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                *reinterpret_cast<uint32_t *>(sBt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
-                    pair_of(rB[i][0], rB[i][1], k);
         }
-        const int u = tid >> 3, c = tid & 7;
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            *reinterpret_cast<uint32_t *>(sXt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
-                pair_of(rX[0], rX[1], k);
+        for (int e = 0; e < 2; ++e)
+            *reinterpret_cast<u32x4 *>(sX + swx(2 * (tid >> 3) + e, tid & 7)) = rX[e];
+    };
+    // Operands with k = s read from the s-major tiles by transposing reads:
+    // lane 16G + 4e + q addresses row s = 16 ks + 8 (G / 2) + 4 half + e and
+    // column 16 (G % 2) + 4q of its 32-wide tile, so that lane l receives
+    // column l % 32 at s = 16 ks + 8 (l / 32) + 4 half + 0..3.
+    const int tr_s = 8 * ((lane >> 4) >> 1) + ((lane >> 2) & 3);
+    const int tr_m = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    auto x_op = [&](int ks) -> u32x4 {  // x^T: p = 32 pj + l % 32
+        const int c = (32 * pj + tr_m) >> 3, o = tr_m & 7;
+        const u32x2 lo = lds_tr(sX + swx(16 * ks + tr_s, c) + o);
+        const u32x2 hi = lds_tr(sX + swx(16 * ks + tr_s + 4, c) + o);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    auto bt_op = [&](int ks, int nt) -> u32x4 {  // B^T: n = 32 nt + l % 32
+        const int n = 32 * nt + tr_m;
+        const u32x2 lo = lds_tr(sB + sw<CN>(16 * ks + tr_s, n >> 3) + (n & 7));
+        const u32x2 hi = lds_tr(sB + sw<CN>(16 * ks + tr_s + 4, n >> 3) + (n & 7));
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
 
     // ---- state: Sacc[j][r] = S[p = 32 pj + ml][n = 32(nj0 + j) + 8(r/4) + 4hh + r%4]
@@ -813,7 +845,7 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
     const int nch = (L + kQ - 1) / kQ;
     load_chunk(0);
     uint32_t rdt = load_dt(0);
-    if (wave == 0) decay_terms(dt_value(rdt), 0);
+    if (wave == 1) decay_terms(dt_value(rdt), 0);
     rdt = load_dt(kQ);
     for (int ch = 0; ch < nch; ++ch) {
         const int t0 = ch * kQ;
@@ -822,36 +854,58 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
         const float *sdt = sdt2[db], *swt = swt2[db], *sec = sec2[db];
         lds_barrier();  // the previous chunk's readers of the inputs and partials are done
         store_chunk();
+        // the next chunk's inputs: issued a whole chunk ahead of their store
+        if (ch + 1 < nch) load_chunk(t0 + kQ);
         lds_barrier();
-        if (wave == 0 && ch + 1 < nch) {
+        if (wave == 1 && ch + 1 < nch) {
             decay_terms(dt_value(rdt), db ^ 1);
             rdt = load_dt(t0 + 2 * kQ);
         }
 
-        // (a)+(b): the M tiles of t tile ti (s tiles 0..ti), as (c)'s B operand
-        const int t = 32 * ti + ml;
-        const double cst = scs[t];
-        u32x4 mop[2][2][2];  // [s tile][k step][hi, lo]
-#pragma unroll
-        for (int si = 0; si < 2; ++si) {
-            if (si > ti) break;
+        // (a)+(b): M tile (mt, ms) of this wave -- waves 0, 2, 3 build (0, 0),
+        // (1, 0), (1, 1); wave 1 builds none and computes the decay terms --
+        // with D on the diagonal (y's D x term rides in (c)'s product)
+        if (wave != 1) {
+            const int mt = wave >> 1, ms = wave == 2 ? 0 : mt;
+            const int t = 32 * mt + ml;
+            // t made opaque per chunk: the 16 lane masks below are then formed
+            // in VALU here instead of being hoisted into loop-long SGPRs
+            int tq = t;
+            asm volatile("" : "+v"(tq));
+            const double cst = scs[t];
             f32x16 cb;
 #pragma unroll
             for (int r = 0; r < 16; ++r) cb[r] = 0.f;
 #pragma unroll
             for (int ks = 0; ks < NP / 16; ++ks) {
-                const u32x4 bv = lds16(sB + sw<CN>(32 * si + ml, 2 * ks + hh));
-                const u32x4 cv = lds16(sC + sw<CN>(32 * ti + ml, 2 * ks + hh));
+                const u32x4 bv = lds16(sB + sw<CN>(32 * ms + ml, 2 * ks + hh));
+                const u32x4 cv = lds16(sC + sw<CN>(32 * mt + ml, 2 * ks + hh));
                 cb = mfma(bv, cv, cb);
             }
-            // cb[r]: s = 32 si + 8(r/4) + 4hh + r%4 of column t
+            // cb[4q + e]: s = 32 ms + 8q + 4hh + e of column t; the four s of a q
+            // are consecutive, so their cs and dt come in 16-byte reads
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int s = 32 * si + 8 * (r >> 2) + 4 * hh + (r & 3);
-                cb[r] = s <= t ? cb[r] * exp2_fast(static_cast<float>(cst - scs[s])) * sdt[s] : 0.f;
+            for (int q = 0; q < 4; ++q) {
+                const int sb = 32 * ms + 8 * q + 4 * hh;
+                const f64x2 c01 = *reinterpret_cast<const f64x2 *>(scs + sb);
+                const f64x2 c23 = *reinterpret_cast<const f64x2 *>(scs + sb + 2);
+                const f32x4 d4 = *reinterpret_cast<const f32x4 *>(sdt + sb);
+                const double cs4[4] = {c01[0], c01[1], c23[0], c23[1]};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int s = sb + e;
+                    const float v = cb[4 * q + e] * exp2_fast(static_cast<float>(cst - cs4[e])) * d4[e];
+                    cb[4 * q + e] = s < tq ? v : (s == tq ? v + Dh : 0.f);
+                }
             }
-            acc_to_op(cb, mop[si]);
+            u32x4 mop[2][2];
+            acc_to_op(cb, mop);
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl) sM[mt + ms][k2][hl][lane] = mop[k2][hl];
         }
+        const int t = 32 * ti + ml;
 
         // (d): Z^T partials over this wave's n tiles, for its own t tile (kept)
         // and the partner's (handed over through LDS)
@@ -880,7 +934,6 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
         for (int r = 0; r < 16; ++r) sZ[pj][ti ^ 1][r][lane] = zoth[r];
         // the next chunk's inputs: issued once P1's operands are dead (their
         // registers are free), landing while (c) and (e) run
-        if (ch + 1 < nch) load_chunk(t0 + kQ);
         lds_barrier();
 
         // (c) Y^T = x^T M^T over s <= end of t tile ti; y = Y + exp(cs_t) Z + D x
@@ -894,9 +947,9 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 if (ks >= 2 * (ti + 1)) break;
-                const u32x4 xa = lds16(sXt + swq(32 * pj + ml, 2 * ks + hh));
-                yv = mfma(xa, mop[ks >> 1][ks & 1][0], yv);
-                yv = mfma(xa, mop[ks >> 1][ks & 1][1], yv);
+                const u32x4 xa = x_op(ks);
+                yv = mfma(xa, sM[ti + (ks >> 1)][ks & 1][0][lane], yv);
+                yv = mfma(xa, sM[ti + (ks >> 1)][ks & 1][1][lane], yv);
             }
             const float et = sec[t];
             const bool t_ok = t0 + t < L;
@@ -905,10 +958,7 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
                 const int p0 = 32 * pj + 8 * q + 4 * hh;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float xv = bf16_to_f32(sXt[swq(p0 + e, t >> 3) + (t & 7)]);
-                    v[e] = yv[4 * q + e] + et * zv[4 * q + e] + Dh * xv;
-                }
+                for (int e = 0; e < 4; ++e) v[e] = yv[4 * q + e] + et * zv[4 * q + e];
                 const bool ok = t_ok && p0 < P;
                 const uint32_t yo = static_cast<uint32_t>((((int64_t)b * L + t0 + t) * H + h) * P + p0);
                 if (a.y_dt == HXQ_F32) {
@@ -940,13 +990,16 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
             }
 #pragma unroll
             for (int ks = 0; ks < kQ / 16; ++ks) {
-                const u32x4 xx = lds16(sXt + swq(sp, 2 * ks + hh));
+                const u32x4 xx = x_op(ks);
                 const int s0 = 16 * ks + 8 * hh;
+                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(swt + s0);
+                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(swt + s0 + 4);
+                const float w8[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
                 u32x4 xh, xl;
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const float x0 = __uint_as_float(xx[d] << 16) * swt[s0 + 2 * d];
-                    const float x1 = __uint_as_float(xx[d] & 0xffff0000u) * swt[s0 + 2 * d + 1];
+                    const float x0 = __uint_as_float(xx[d] << 16) * w8[2 * d];
+                    const float x1 = __uint_as_float(xx[d] & 0xffff0000u) * w8[2 * d + 1];
                     uint32_t hv, lv;
                     split2x2(x0, x1, hv, lv);
                     xh[d] = hv;
@@ -955,7 +1008,7 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     if (j >= nst) break;
-                    const u32x4 bt = lds16(sBt + swq(32 * (nj0 + j) + ml, 2 * ks + hh));
+                    const u32x4 bt = bt_op(ks, nj0 + j);
                     Sacc[j] = mfma(bt, xh, Sacc[j]);
                     Sacc[j] = mfma(bt, xl, Sacc[j]);
                 }
