@@ -29,7 +29,8 @@ namespace hxq {
 namespace enc {
 
 constexpr int kThreads = 256;
-constexpr int kMaxK = 256;
+constexpr int kMaxK = 256;     // scalar codebooks with uint8 indices
+constexpr int kMaxKW = 4096;   // wide scalar codebooks (uint16 indices)
 
 // fp32 -> uint32 whose unsigned order is numpy's sort order (NaN last).
 __device__ __forceinline__ uint32_t sort_key(float f) {
@@ -105,15 +106,16 @@ __device__ __forceinline__ bool stage_codebook(const float *cb, int k, float *s_
     return *s_flag != 0;
 }
 
+template <typename IT, int KM>
 __global__ __launch_bounds__(kThreads) void assign_kernel(const float *x, int64_t n, const float *cb,
-                                                          int k, uint8_t *idx) {
-    __shared__ float s_cb[kMaxK];
+                                                          int k, IT *idx) {
+    __shared__ float s_cb[KM];
     __shared__ int s_flag;
     const bool sorted = stage_codebook(cb, k, s_cb, &s_flag);
     for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kThreads) {
         const float v = x[i];
-        idx[i] = static_cast<uint8_t>(sorted ? nearest_sorted(v, s_cb, k) : nearest_scan(v, s_cb, k));
+        idx[i] = static_cast<IT>(sorted ? nearest_sorted(v, s_cb, k) : nearest_scan(v, s_cb, k));
     }
 }
 
@@ -226,20 +228,21 @@ __global__ __launch_bounds__(kMaxK) void kmeans_init_kernel(const uint32_t *keys
 
 // Lloyd step 1: assignment + per-block cluster counts.  Block b owns the
 // contiguous elements [b * per, (b + 1) * per).
+template <typename IT, int KM>
 __global__ __launch_bounds__(kThreads) void km_assign_kernel(const float *x, int64_t n, int64_t per,
-                                                             const float *cb, int k, uint8_t *idx,
+                                                             const float *cb, int k, IT *idx,
                                                              int32_t *blk_counts, const int32_t *done) {
     if (*done) return;
-    __shared__ float s_cb[kMaxK];
+    __shared__ float s_cb[KM];
     __shared__ int s_flag;
-    __shared__ int32_t s_cnt[kMaxK];
-    for (int j = threadIdx.x; j < kMaxK; j += kThreads) s_cnt[j] = 0;
+    __shared__ int32_t s_cnt[KM];
+    for (int j = threadIdx.x; j < KM; j += kThreads) s_cnt[j] = 0;
     const bool sorted = stage_codebook(cb, k, s_cb, &s_flag);
     const int64_t lo = blockIdx.x * per, hi = min(n, lo + per);
     for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) {
         const float v = x[i];
         const int c = sorted ? nearest_sorted(v, s_cb, k) : nearest_scan(v, s_cb, k);
-        idx[i] = static_cast<uint8_t>(c);
+        idx[i] = static_cast<IT>(c);
         atomicAdd(&s_cnt[c], 1);
     }
     __syncthreads();
@@ -247,12 +250,12 @@ __global__ __launch_bounds__(kThreads) void km_assign_kernel(const float *x, int
 }
 
 // Lloyd step 2: exclusive offsets, cluster-major then block order (stable)
-__global__ __launch_bounds__(kMaxK) void km_offsets_kernel(int32_t *blk_counts, int nblk, int k, int32_t *starts,
+template <int KM>
+__global__ __launch_bounds__(kThreads) void km_offsets_kernel(int32_t *blk_counts, int nblk, int k, int32_t *starts,
                                   int32_t *counts, const int32_t *done) {
     if (*done) return;
-    __shared__ int32_t tot[kMaxK];
-    const int j = threadIdx.x;
-    if (j < k) {
+    __shared__ int32_t tot[KM];
+    for (int j = threadIdx.x; j < k; j += kThreads) {
         int32_t s = 0;
         for (int b = 0; b < nblk; ++b) {
             const int32_t c = blk_counts[(int64_t)b * k + j];
@@ -263,6 +266,7 @@ __global__ __launch_bounds__(kMaxK) void km_offsets_kernel(int32_t *blk_counts, 
         counts[j] = s;
     }
     __syncthreads();
+    const int j = threadIdx.x;
     if (j == 0) {
         int32_t s = 0;
         for (int c = 0; c < k; ++c) { starts[c] = s; s += tot[c]; }
@@ -271,20 +275,21 @@ __global__ __launch_bounds__(kMaxK) void km_offsets_kernel(int32_t *blk_counts, 
 
 // Lloyd step 3: stable scatter of the values into cluster-contiguous order
 // (within a cluster, elements keep their index order)
+template <typename IT, int KM>
 __global__ __launch_bounds__(kThreads) void km_scatter_kernel(const float *x, int64_t n, int64_t per,
-                                                              const uint8_t *idx, const int32_t *blk_offs,
+                                                              const IT *idx, const int32_t *blk_offs,
                                                               const int32_t *starts, int k, float *out,
                                                               const int32_t *done) {
     if (*done) return;
     constexpr int W = kThreads / kWave;
-    __shared__ int32_t base[kMaxK];
-    __shared__ int32_t wcnt[W][kMaxK];
+    __shared__ int32_t base[KM];
+    __shared__ int32_t wcnt[W][KM];
     for (int j = threadIdx.x; j < k; j += kThreads)
         base[j] = starts[j] + blk_offs[blockIdx.x * (int64_t)k + j];
     const int lane = threadIdx.x & 63, w = threadIdx.x / kWave;
     const int64_t lo = blockIdx.x * per, hi = min(n, lo + per);
     for (int64_t c0 = lo; c0 < hi; c0 += kThreads) {
-        for (int j = threadIdx.x; j < W * kMaxK; j += kThreads) (&wcnt[0][0])[j] = 0;
+        for (int j = threadIdx.x; j < W * KM; j += kThreads) (&wcnt[0][0])[j] = 0;
         __syncthreads();
         const int64_t i = c0 + threadIdx.x;
         const bool ok = i < hi;
@@ -432,21 +437,22 @@ __global__ __launch_bounds__(kThreads) void km_sum_kernel(const float *sorted_va
 }
 
 // Lloyd step 4b: movement and convergence over the k new means.
-__global__ __launch_bounds__(kMaxK) void km_update_kernel(const float *means, int k, float *cb,
+template <int KM>
+__global__ __launch_bounds__(kThreads) void km_update_kernel(const float *means, int k, float *cb,
                                                           const double *abs_tol, int32_t *done,
                                                           int32_t *iters) {
 #pragma clang fp contract(off)
     if (*done) return;
-    __shared__ float s_new[kMaxK];
-    __shared__ float s_delta[kMaxK];
-    const int j = threadIdx.x;
-    if (j < k) {
+    __shared__ float s_new[KM];
+    __shared__ float s_delta[KM];
+    __shared__ int s_conv;
+    for (int j = threadIdx.x; j < k; j += kThreads) {
         const float v = means[j];
         s_new[j] = v;
         s_delta[j] = fabsf(v - cb[j]);
     }
     __syncthreads();
-    if (j == 0) {
+    if (threadIdx.x == 0) {
         float m = 0.f;
         bool nan = false;
         for (int c = 0; c < k; ++c) {
@@ -455,12 +461,13 @@ __global__ __launch_bounds__(kMaxK) void km_update_kernel(const float *means, in
         }
         // numpy's max propagates NaN; NaN < tol is false: no convergence
         const bool conv = !nan && static_cast<double>(m) < *abs_tol;
-        s_delta[0] = conv ? 1.f : 0.f;
+        s_conv = conv ? 1 : 0;
         *iters += 1;
         if (conv) *done = 1;
     }
     __syncthreads();
-    if (j < k && s_delta[0] == 0.f) cb[j] = s_new[j];
+    if (s_conv == 0)
+        for (int j = threadIdx.x; j < k; j += kThreads) cb[j] = s_new[j];
 }
 
 // ---------------------------------------------------------------------------
@@ -614,14 +621,15 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-__global__ __launch_bounds__(kThreads) void affine_fit_kernel(const float *w, const uint8_t *idx,
+template <typename IT, int KM>
+__global__ __launch_bounds__(kThreads) void affine_fit_kernel(const float *w, const IT *idx,
                                                               const float *cb, int k, int64_t rows,
                                                               int64_t cols, int group,
                                                               const uint32_t *bits, float *scale,
                                                               float *offset) {
 #pragma clang fp contract(off)
-    __shared__ float s_cb[kMaxK];
-    for (int j = threadIdx.x; j < kMaxK; j += kThreads) s_cb[j] = j < k ? cb[j] : 0.f;
+    __shared__ float s_cb[KM];
+    for (int j = threadIdx.x; j < KM; j += kThreads) s_cb[j] = j < k ? cb[j] : 0.f;
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t ngroups = cols / group;
@@ -634,7 +642,8 @@ __global__ __launch_bounds__(kThreads) void affine_fit_kernel(const float *w, co
         const int64_t e = base + t;
         const bool skip = bits && ((bits[e >> 5] >> (e & 31)) & 1u);
         if (!skip) {
-            const double c = static_cast<double>(s_cb[idx[e]]);
+            // an index past the table (a caller error) reads a zero entry, in bounds
+            const double c = static_cast<double>(s_cb[min(static_cast<int>(idx[e]), KM - 1)]);
             const double x = static_cast<double>(w[e]);
             sc = sc + c;
             sw = sw + x;
@@ -911,16 +920,27 @@ static PairPlan pair_plan(int64_t n) {
 using namespace hxq;
 using namespace hxq::enc;
 
-extern "C" int hxq_assign_nearest(const float *x, int64_t n, const float *codebook, int32_t k,
-                                  uint8_t *indices, hipStream_t stream) {
+template <typename IT, int KM>
+static int assign_nearest_impl(const float *x, int64_t n, const float *codebook, int32_t k,
+                               IT *indices, hipStream_t stream) {
     clear_error();
     HXQ_REQUIRE(x && codebook && indices, "x, codebook and indices are required");
-    HXQ_REQUIRE(n >= 0 && k >= 1 && k <= kMaxK, "k must be 1..256");
+    HXQ_REQUIRE(n >= 0 && k >= 1 && k <= KM, KM == kMaxK ? "k must be 1..256" : "k must be 1..4096");
     if (n == 0) return HXQ_OK;
-    hipLaunchKernelGGL(assign_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream, x, n, codebook,
-                       k, indices);
+    hipLaunchKernelGGL((assign_kernel<IT, KM>), dim3(grid_for(n)), dim3(kThreads), 0, stream, x, n,
+                       codebook, k, indices);
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
+}
+
+extern "C" int hxq_assign_nearest(const float *x, int64_t n, const float *codebook, int32_t k,
+                                  uint8_t *indices, hipStream_t stream) {
+    return assign_nearest_impl<uint8_t, kMaxK>(x, n, codebook, k, indices, stream);
+}
+
+extern "C" int hxq_assign_nearest_wide(const float *x, int64_t n, const float *codebook, int32_t k,
+                                       uint16_t *indices, hipStream_t stream) {
+    return assign_nearest_impl<uint16_t, kMaxKW>(x, n, codebook, k, indices, stream);
 }
 
 extern "C" int64_t hxq_sort_workspace_bytes(int64_t n) {
@@ -957,10 +977,10 @@ struct KmLayout {
         const int64_t nblk = (n + 4095) / 4096;
         vals = align256(4 * next_pow2(n));
         blk = vals + align256(4 * n);
-        starts = blk + align256(4 * nblk * kMaxK);
-        counts = starts + 4 * kMaxK;
-        means = counts + 4 * kMaxK;
-        tol = means + 4 * kMaxK;
+        starts = blk + align256(4 * nblk * kMaxKW);
+        counts = starts + 4 * kMaxKW;
+        means = counts + 4 * kMaxKW;
+        tol = means + 4 * kMaxKW;
         done = tol + 8;
         total = align256(done + 8);
     }
@@ -986,15 +1006,16 @@ extern "C" int hxq_kmeans_init(const float *x, int64_t n, void *workspace, int64
     return HXQ_OK;
 }
 
-extern "C" int hxq_kmeans_run(const float *x, int64_t n, const double *percentiles01, int32_t k,
-                              int32_t max_iters, double rtol, void *workspace,
-                              int64_t workspace_bytes, float *codebook, uint8_t *assignments,
-                              int32_t *iters, hipStream_t stream) {
+template <typename IT, int KM>
+static int kmeans_run_impl(const float *x, int64_t n, const double *percentiles01, int32_t k,
+                           int32_t max_iters, double rtol, void *workspace, int64_t workspace_bytes,
+                           float *codebook, IT *assignments, int32_t *iters, hipStream_t stream) {
     clear_error();
     HXQ_REQUIRE(x && percentiles01 && workspace && codebook && assignments && iters, "bad arguments");
     // max_iters == 0 leaves the reference's assignments unbound (an error there)
-    HXQ_REQUIRE(n >= 1 && n < (int64_t{1} << 31) && k >= 1 && k <= kMaxK && max_iters >= 1,
-                "bad sizes (n 1..2^31-1, k 1..256, max_iters >= 1)");
+    HXQ_REQUIRE(n >= 1 && n < (int64_t{1} << 31) && k >= 1 && k <= KM && max_iters >= 1,
+                KM == kMaxK ? "bad sizes (n 1..2^31-1, k 1..256, max_iters >= 1)"
+                            : "bad sizes (n 1..2^31-1, k 1..4096, max_iters >= 1)");
     HXQ_REQUIRE(workspace_bytes >= hxq_kmeans_workspace_bytes(n), "workspace too small");
     char *ws = static_cast<char *>(workspace);
     const int64_t nblk = (n + 4095) / 4096;
@@ -1012,23 +1033,39 @@ extern "C" int hxq_kmeans_run(const float *x, int64_t n, const double *percentil
     HXQ_LAUNCH_CHECK();
     const int64_t per = 4096;
     for (int it = 0; it < max_iters; ++it) {
-        hipLaunchKernelGGL(km_assign_kernel, dim3(static_cast<uint32_t>(nblk)), dim3(kThreads), 0,
-                           stream, x, n, per, codebook, k, assignments, blk, done);
+        hipLaunchKernelGGL((km_assign_kernel<IT, KM>), dim3(static_cast<uint32_t>(nblk)), dim3(kThreads),
+                           0, stream, x, n, per, codebook, k, assignments, blk, done);
         HXQ_LAUNCH_CHECK();
-        hipLaunchKernelGGL(km_offsets_kernel, dim3(1), dim3(kMaxK), 0, stream, blk,
+        hipLaunchKernelGGL(km_offsets_kernel<KM>, dim3(1), dim3(kThreads), 0, stream, blk,
                            static_cast<int>(nblk), k, starts, counts, done);
         HXQ_LAUNCH_CHECK();
-        hipLaunchKernelGGL(km_scatter_kernel, dim3(static_cast<uint32_t>(nblk)), dim3(kThreads), 0,
-                           stream, x, n, per, assignments, blk, starts, k, vals, done);
+        hipLaunchKernelGGL((km_scatter_kernel<IT, KM>), dim3(static_cast<uint32_t>(nblk)), dim3(kThreads),
+                           0, stream, x, n, per, assignments, blk, starts, k, vals, done);
         HXQ_LAUNCH_CHECK();
         hipLaunchKernelGGL(km_sum_kernel, dim3(k), dim3(kThreads), 0, stream, vals, starts, counts,
                            codebook, means, done);
         HXQ_LAUNCH_CHECK();
-        hipLaunchKernelGGL(km_update_kernel, dim3(1), dim3(kMaxK), 0, stream, means, k, codebook,
+        hipLaunchKernelGGL(km_update_kernel<KM>, dim3(1), dim3(kThreads), 0, stream, means, k, codebook,
                            abs_tol, done, iters);
         HXQ_LAUNCH_CHECK();
     }
     return HXQ_OK;
+}
+
+extern "C" int hxq_kmeans_run(const float *x, int64_t n, const double *percentiles01, int32_t k,
+                              int32_t max_iters, double rtol, void *workspace,
+                              int64_t workspace_bytes, float *codebook, uint8_t *assignments,
+                              int32_t *iters, hipStream_t stream) {
+    return kmeans_run_impl<uint8_t, kMaxK>(x, n, percentiles01, k, max_iters, rtol, workspace,
+                                           workspace_bytes, codebook, assignments, iters, stream);
+}
+
+extern "C" int hxq_kmeans_run_wide(const float *x, int64_t n, const double *percentiles01, int32_t k,
+                                   int32_t max_iters, double rtol, void *workspace,
+                                   int64_t workspace_bytes, float *codebook, uint16_t *assignments,
+                                   int32_t *iters, hipStream_t stream) {
+    return kmeans_run_impl<uint16_t, kMaxKW>(x, n, percentiles01, k, max_iters, rtol, workspace,
+                                             workspace_bytes, codebook, assignments, iters, stream);
 }
 
 extern "C" int64_t hxq_select_workspace_bytes(void) { return sizeof(SelState); }
@@ -1087,14 +1124,15 @@ extern "C" int64_t hxq_affine_fit_workspace_bytes(int64_t rows, int64_t cols) {
     return rows <= 0 || cols <= 0 ? 0 : 4 * ((rows * cols + 31) / 32);
 }
 
-extern "C" int hxq_affine_fit(const float *w, const uint8_t *indices, const float *codebook,
-                              int32_t k, int64_t rows, int64_t cols, int32_t group_size,
-                              const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
-                              int64_t workspace_bytes, float *scale, float *offset,
-                              hipStream_t stream) {
+template <typename IT, int KM>
+static int affine_fit_impl(const float *w, const IT *indices, const float *codebook, int32_t k,
+                           int64_t rows, int64_t cols, int32_t group_size,
+                           const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
+                           int64_t workspace_bytes, float *scale, float *offset, hipStream_t stream) {
     clear_error();
     HXQ_REQUIRE(w && indices && codebook && scale && offset, "bad arguments");
-    HXQ_REQUIRE(k >= 1 && k <= kMaxK && rows >= 1 && cols >= 1, "bad sizes (k 1..256)");
+    HXQ_REQUIRE(k >= 1 && k <= KM && rows >= 1 && cols >= 1,
+                KM == kMaxK ? "bad sizes (k 1..256)" : "bad sizes (k 1..4096)");
     HXQ_REQUIRE(group_size >= 1 && cols % group_size == 0, "cols must be a multiple of group_size");
     HXQ_REQUIRE(n_exclude >= 0 && (n_exclude == 0 || exclude_positions), "bad exclusion list");
     uint32_t *bits = nullptr;
@@ -1114,10 +1152,30 @@ extern "C" int hxq_affine_fit(const float *w, const uint8_t *indices, const floa
     const int64_t per_block = kThreads / kWave;
     const int64_t blocks = (units + per_block - 1) / per_block;
     HXQ_REQUIRE(blocks < (int64_t{1} << 31), "too many groups");
-    hipLaunchKernelGGL(affine_fit_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
-                       stream, w, indices, codebook, k, rows, cols, group_size, bits, scale, offset);
+    hipLaunchKernelGGL((affine_fit_kernel<IT, KM>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads),
+                       0, stream, w, indices, codebook, k, rows, cols, group_size, bits, scale, offset);
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
+}
+
+extern "C" int hxq_affine_fit(const float *w, const uint8_t *indices, const float *codebook,
+                              int32_t k, int64_t rows, int64_t cols, int32_t group_size,
+                              const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
+                              int64_t workspace_bytes, float *scale, float *offset,
+                              hipStream_t stream) {
+    return affine_fit_impl<uint8_t, kMaxK>(w, indices, codebook, k, rows, cols, group_size,
+                                           exclude_positions, n_exclude, workspace, workspace_bytes,
+                                           scale, offset, stream);
+}
+
+extern "C" int hxq_affine_fit_wide(const float *w, const uint16_t *indices, const float *codebook,
+                                   int32_t k, int64_t rows, int64_t cols, int32_t group_size,
+                                   const int64_t *exclude_positions, int64_t n_exclude,
+                                   void *workspace, int64_t workspace_bytes, float *scale,
+                                   float *offset, hipStream_t stream) {
+    return affine_fit_impl<uint16_t, kMaxKW>(w, indices, codebook, k, rows, cols, group_size,
+                                             exclude_positions, n_exclude, workspace,
+                                             workspace_bytes, scale, offset, stream);
 }
 
 extern "C" int64_t hxq_vq2_workspace_bytes(int64_t n, int32_t k) {

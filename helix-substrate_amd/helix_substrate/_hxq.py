@@ -105,14 +105,17 @@ SIGNATURES = {
     "hxq_moe_grouped_gemm": [P, I32, I64, P, P, I64, I32, P, I32, P, I32, I64, I64, P],
     "hxq_moe_ffn": [P, I32, I64, I64, I64, I32, I32, P, P, P, P, P, P, P, I32, P, I64, P, I32, P],
     "hxq_assign_nearest": [P, I64, P, I32, P, P],
+    "hxq_assign_nearest_wide": [P, I64, P, I32, P, P],
     "hxq_vq2_assign": [P, I64, P, I32, P, P, I64, P],
     "hxq_vq2_update": [P, I64, P, I32, P, P, P, P, I64, P],
     "hxq_vq2_min_dist": [P, I64, P, I64, P, I32, P, P, I64, P],
     "hxq_kmeans_init": [P, I64, P, I64, P, P],
     "hxq_kmeans_run": [P, I64, P, I32, I32, ctypes.c_double, P, I64, P, P, P, P],
+    "hxq_kmeans_run_wide": [P, I64, P, I32, I32, ctypes.c_double, P, I64, P, P, P, P],
     "hxq_select_f32": [P, I64, P, I32, P, P, P, I64, P],
     "hxq_outliers_f32": [P, I64, P, I64, P, P, P, P, I64, P],
     "hxq_affine_fit": [P, P, P, I32, I64, I64, I32, P, I64, P, I64, P, P, P],
+    "hxq_affine_fit_wide": [P, P, P, I32, I64, I64, I32, P, I64, P, I64, P, P, P],
     "hxq_decoder_init": [P, P, I64, P],
     "hxq_decoder_step": [P, P, I32, P, P],
     "hxq_decoder_error": [P, P, P, P],
@@ -141,7 +144,7 @@ def library_path() -> Path:
 
 
 # HXQ_ABI_VERSION of include/hxq.h that the ctypes signatures below follow
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def lib():
@@ -885,23 +888,31 @@ def vq2_update(x, indices, centroids, out=None, max_delta=None, workspace=None):
 
 
 def assign_nearest(x, codebook, out=None):
-    """indices (uint8, shape of x) = argmin_j |x - codebook[j]| (first on ties)."""
+    """indices (shape of x) = argmin_j |x - codebook[j]| (first on ties):
+    uint8 for codebooks of up to 256 entries, int16 holding the uint16 ids
+    above that (up to 4096)."""
     xf = x.reshape(-1)
     _need_device(xf, codebook)
     if xf.dtype != torch.float32 or codebook.dtype != torch.float32:
         raise RuntimeError("assign_nearest takes fp32 data and codebook")
     xf = xf.contiguous()
     cb = codebook.contiguous()
+    wide = cb.numel() > 256
+    dt = torch.int16 if wide else torch.uint8
     if out is None:
-        out = torch.empty(xf.numel(), dtype=torch.uint8, device=xf.device)
-    rc = lib().hxq_assign_nearest(_ptr(xf), xf.numel(), _ptr(cb), cb.numel(), _ptr(out), _stream(xf))
-    _check("hxq_assign_nearest", rc)
+        out = torch.empty(xf.numel(), dtype=dt, device=xf.device)
+    elif out.dtype != dt or out.numel() != xf.numel() or not out.is_contiguous():
+        raise RuntimeError(f"assign_nearest: out must be a contiguous {dt} tensor of x's size")
+    fn = lib().hxq_assign_nearest_wide if wide else lib().hxq_assign_nearest
+    rc = fn(_ptr(xf), xf.numel(), _ptr(cb), cb.numel(), _ptr(out), _stream(xf))
+    _check("hxq_assign_nearest_wide" if wide else "hxq_assign_nearest", rc)
     return out.view(x.shape)
 
 
 def kmeans_1d(sample, n_clusters=256, max_iters=10, rtol=0.001):
     """The reference's _simple_kmeans on a device fp32 vector: returns
-    (codebook fp32 [k], assignments uint8 [n], iterations run)."""
+    (codebook fp32 [k], assignments [n], iterations run); assignments are
+    uint8 for k <= 256 and int16 holding the uint16 ids up to k = 4096."""
     import numpy as np
     x = sample.reshape(-1).contiguous()
     _need_device(x)
@@ -915,12 +926,16 @@ def kmeans_1d(sample, n_clusters=256, max_iters=10, rtol=0.001):
                                                 _stream(x)))
     k = min(int(n_clusters), int(n_unique.item()))
     q01 = torch.from_numpy(np.linspace(0, 100, k) / np.float32(100)).to(x.device)
+    if k > 4096:
+        raise RuntimeError("kmeans_1d fits codebooks of at most 4096 entries")
+    wide = k > 256
     cb = torch.empty(k, dtype=torch.float32, device=x.device)
-    asg = torch.empty(n, dtype=torch.uint8, device=x.device)
+    asg = torch.empty(n, dtype=torch.int16 if wide else torch.uint8, device=x.device)
     iters = torch.empty(1, dtype=torch.int32, device=x.device)
-    _check("hxq_kmeans_run", L.hxq_kmeans_run(_ptr(x), n, _ptr(q01), k, int(max_iters), float(rtol),
-                                              _ptr(ws), ws.numel(), _ptr(cb), _ptr(asg), _ptr(iters),
-                                              _stream(x)))
+    fn = L.hxq_kmeans_run_wide if wide else L.hxq_kmeans_run
+    _check("hxq_kmeans_run", fn(_ptr(x), n, _ptr(q01), k, int(max_iters), float(rtol),
+                                _ptr(ws), ws.numel(), _ptr(cb), _ptr(asg), _ptr(iters),
+                                _stream(x)))
     return cb, asg, int(iters.item())
 
 
@@ -1006,8 +1021,11 @@ def affine_fit(w, indices, codebook, group_size, exclude_positions=None):
     if cols % group_size:
         raise RuntimeError("cols must be a multiple of group_size")
     wf = w.float().contiguous()
-    idx = indices.to(torch.uint8).contiguous()
     cb = codebook.float().contiguous()
+    wide = cb.numel() > 256
+    if wide and indices.dtype not in (torch.int16, torch.int32, torch.int64):
+        raise RuntimeError("affine_fit: a codebook above 256 entries takes int16/int32/int64 indices")
+    idx = indices.to(torch.int16 if wide else torch.uint8).contiguous()
     ng = cols // group_size
     scale = torch.empty(rows, ng, dtype=torch.float32, device=w.device)
     offset = torch.empty(rows, ng, dtype=torch.float32, device=w.device)
@@ -1022,8 +1040,9 @@ def affine_fit(w, indices, codebook, group_size, exclude_positions=None):
             raise RuntimeError("exclude_positions out of range")
         ws = torch.empty(int(L.hxq_affine_fit_workspace_bytes(rows, cols)), dtype=torch.uint8,
                          device=w.device)
-    _check("hxq_affine_fit", L.hxq_affine_fit(_ptr(wf), _ptr(idx), _ptr(cb), cb.numel(), rows, cols,
-                                              int(group_size), _ptr(ex), n_ex, _ptr(ws),
-                                              0 if ws is None else ws.numel(), _ptr(scale),
-                                              _ptr(offset), _stream(wf)))
+    fn = L.hxq_affine_fit_wide if wide else L.hxq_affine_fit
+    _check("hxq_affine_fit", fn(_ptr(wf), _ptr(idx), _ptr(cb), cb.numel(), rows, cols,
+                                int(group_size), _ptr(ex), n_ex, _ptr(ws),
+                                0 if ws is None else ws.numel(), _ptr(scale),
+                                _ptr(offset), _stream(wf)))
     return scale, offset

@@ -12,11 +12,18 @@ init, same first-index argmin, cluster means summed in numpy's order).
 The pair encoder (``vector_kmeans`` / ``build_vector_codebook_and_assign``,
 reference ``_vector_kmeans``, ``hxq_encoder.py:210-315``, and
 ``CDNAv3Writer._build_vector_codebook_and_assign``, ``hxq_writer_v3.py:
-338-420``) takes device tensors: the k-means++ seeding draws from the
+338-420``): on device tensors the k-means++ seeding draws from the
 reference's RandomState(42) stream on the host (sequential, at most 64 draws)
-with its distances computed on the device; the Lloyd steps and the assignment
-of every pair run as HIP kernels; all reproduce the reference's numpy CPU
-arithmetic.
+with its distances computed on the device, and the Lloyd steps and the
+assignment of every pair run as HIP kernels; numpy arrays run the
+reference's CPU branch (matmul-form distances, bincount updates, chunked
+argmin).  Both reproduce the reference's numpy CPU arithmetic.
+
+Scalar codebooks of 257..4096 entries take uint16 indices on both paths
+(int16 tensors holding the ids on the device); the k-means assigns with
+integer ids, as the reference's GPU branch (``_gpu_kmeans``,
+``hxq_encoder.py:180-207``) does -- its CPU branch casts the assignments to
+uint8 (``:160``), which would fold clusters mod 256.
 """
 from __future__ import annotations
 
@@ -59,14 +66,17 @@ def _simple_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
         return cb, asg
     data = np.asarray(data, dtype=np.float32).ravel()
     k = min(int(n_clusters), len(np.unique(data)))
+    if k > 4096:
+        raise ValueError("scalar codebooks hold at most 4096 entries")
     centroids = np.percentile(data, np.linspace(0, 100, k)).astype(np.float32)
     cb_range = float(centroids[-1] - centroids[0])
     if cb_range < 1e-30:
         cb_range = 1.0
     abs_tol = rtol * cb_range
-    assignments = np.zeros(data.size, dtype=np.uint8)
+    ity = np.uint8 if k <= 256 else np.uint16
+    assignments = np.zeros(data.size, dtype=ity)
     for _ in range(max_iters):
-        assignments = chunked_assign(data, centroids).astype(np.uint8)
+        assignments = chunked_assign(data, centroids).astype(ity)
         # members of each cluster in index order, contiguous (stable sort)
         order = np.argsort(assignments, kind="stable")
         vals = data[order]
@@ -238,14 +248,72 @@ def kmeanspp_init(data, n_clusters):
     return seeds
 
 
+def _pair_dists_np(X, C):
+    """Squared distances in the reference's matmul form, fp32:
+    |x|^2 + |c|^2 - 2 x.c (hxq_encoder.py:282-287)."""
+    C_sq = np.sum(C ** 2, axis=1, keepdims=True).T
+    X_sq = np.sum(X ** 2, axis=1, keepdims=True)
+    return X_sq + C_sq - 2.0 * (X @ C.T)
+
+
+def _pair_assign_np(X, C, chunk):
+    out = np.empty(X.shape[0], dtype=np.int32)
+    for s in range(0, X.shape[0], chunk):
+        out[s:s + chunk] = np.argmin(_pair_dists_np(X[s:s + chunk], C), axis=1)
+    return out
+
+
+def _vector_kmeans_np(data, n_clusters, max_iters, rtol):
+    """The reference's _vector_kmeans CPU branch (hxq_encoder.py:210-315) on a
+    host fp32 [n, d] array: k-means++ seeding from RandomState(42) (fresh
+    100000-row subsamples when n > 100000), bincount Lloyd updates (fp64
+    sums, fp32 centroids), chunked argmin assignment."""
+    n, d = data.shape
+    k = min(int(n_clusters), n)
+    rng = np.random.RandomState(42)
+    cent = np.zeros((k, d), dtype=np.float32)
+    cent[0] = data[rng.randint(n)]
+    for i in range(1, min(k, 64)):
+        sub = data[rng.choice(n, 100000, replace=False)] if n > 100000 else data
+        dists = _pair_dists_np(sub, cent[:i])
+        np.maximum(dists, 0, out=dists)
+        nearest = dists.min(axis=1)
+        cent[i] = sub[rng.choice(len(sub), p=nearest / max(nearest.sum(), 1e-30))]
+    if k > 64:
+        cent[64:] = data[rng.choice(n, k - 64, replace=False)]
+    rng_w = float(cent.max() - cent.min())
+    abs_tol = rtol * (rng_w if rng_w >= 1e-30 else 1.0)
+    chunk = max(10000, n // 10)
+    steps = 0
+    for _ in range(max_iters):
+        steps += 1
+        asg = _pair_assign_np(data, cent, chunk)
+        counts = np.bincount(asg, minlength=k).astype(np.float32)
+        new = np.zeros_like(cent)
+        for j in range(d):
+            sums = np.bincount(asg, weights=data[:, j], minlength=k)
+            new[:, j] = np.where(counts > 0, sums / np.maximum(counts, 1), cent[:, j])
+        if float(np.max(np.abs(new - cent))) < abs_tol:
+            break
+        cent = new
+    asg = _pair_assign_np(data, cent, chunk)
+    return cent.astype(np.float32), asg.astype(np.uint8 if k <= 256 else np.uint16), steps
+
+
 def vector_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
-    """Pair k-means on device rows data (fp32 [n, 2]): (centroids fp32
-    [k, 2], assignments int16 [n] of the final pass, update steps taken),
-    k = min(n_clusters, n).  Stops when the largest centroid move is below
-    rtol * (max - min over the seeds), keeping the centroids of before that
-    update, as the reference does."""
+    """Pair k-means on rows data (fp32 [n, 2]): (centroids fp32 [k, 2],
+    assignments of the final pass, update steps taken), k = min(n_clusters,
+    n).  Stops when the largest centroid move is below rtol * (max - min over
+    the seeds), keeping the centroids of before that update, as the reference
+    does.  Device tensors run the HIP kernels (int16 assignments); numpy
+    arrays the reference's CPU branch (uint8 / uint16 assignments)."""
     if not _is_device(data):
-        raise RuntimeError("vector_kmeans takes a device tensor")
+        data = np.asarray(data.cpu() if isinstance(data, torch.Tensor) else data, np.float32)
+        if data.ndim != 2 or data.shape[1] != 2:
+            raise NotImplementedError("the pair encoder handles vector_dim 2")
+        if not 1 <= min(int(n_clusters), data.shape[0]) <= 4096:
+            raise ValueError("pair codebooks hold 1..4096 entries")
+        return _vector_kmeans_np(data, n_clusters, max_iters, rtol)
     if data.dim() != 2 or data.shape[1] != 2:
         raise NotImplementedError("the pair encoder handles vector_dim 2")
     data = data.float().contiguous()
@@ -275,17 +343,29 @@ def vector_kmeans(data, n_clusters, max_iters=10, rtol=0.001):
 
 def build_vector_codebook_and_assign(tensor, n_clusters, vector_dim=2, max_iters=10):
     """CDNAv3Writer._build_vector_codebook_and_assign for vector_dim 2:
-    adjacent column pairs of the device tensor [rows, cols], k-means fitted on
-    a RandomState(42) subsample of at most KMEANS_MAX_SAMPLES pairs, every
-    pair assigned with the fitted codebook.  Returns (codebook fp32 [k, 2],
-    indices int16 [rows, cols / 2])."""
+    adjacent column pairs of the tensor [rows, cols], k-means fitted on a
+    RandomState(42) subsample of at most KMEANS_MAX_SAMPLES pairs, every pair
+    assigned with the fitted codebook.  Returns (codebook fp32 [k, 2],
+    indices [rows, cols / 2]): int16 device tensors for a device tensor;
+    numpy uint8 (k <= 256) or uint16 for a host array, whose assignment is
+    the reference's chunked CPU argmin (hxq_writer_v3.py:373-420, chunks of
+    50000 pairs)."""
     if vector_dim != 2:
         raise NotImplementedError("the pair encoder handles vector_dim 2")
-    if not _is_device(tensor):
-        raise RuntimeError("build_vector_codebook_and_assign takes a device tensor")
     rows, cols = tensor.shape
     if cols % 2:
         raise ValueError(f"in_features ({cols}) must be divisible by vector_dim (2)")
+    if not _is_device(tensor):
+        vec = np.ascontiguousarray(
+            np.asarray(tensor.cpu() if isinstance(tensor, torch.Tensor) else tensor,
+                       np.float32).reshape(-1, 2))
+        fit = vec
+        if vec.shape[0] > KMEANS_MAX_SAMPLES:
+            fit = vec[_sample_index(int(vec.shape[0]), KMEANS_MAX_SAMPLES)]
+        cb, _, _ = vector_kmeans(fit, n_clusters, max_iters=max_iters)
+        idx = _pair_assign_np(vec, cb, 50000)
+        idx = idx.astype(np.uint8 if cb.shape[0] <= 256 else np.uint16)
+        return cb, idx.reshape(rows, cols // 2)
     vec = tensor.float().contiguous().reshape(-1, 2)
     fit = vec
     if vec.shape[0] > KMEANS_MAX_SAMPLES:

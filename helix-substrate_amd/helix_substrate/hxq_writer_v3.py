@@ -98,8 +98,10 @@ class CDNAv3Writer:
         group_size (extension): also fit the per-group affine (least squares
         per row and group, sidecar positions excluded) and write group_scale /
         group_offset.  vector_dim 2: pair codebook [n_clusters <= 4096, 2] over
-        adjacent columns (reference hxq_writer_v3.py:174-212; device tensors
-        only, no affine)."""
+        adjacent columns (reference hxq_writer_v3.py:174-212; no affine).
+        Scalar codebooks of 257..4096 entries write uint16 indices.  Device
+        tensors run the GPU encoder, host arrays the reference's numpy
+        arithmetic; both give the same file."""
         import dataclasses
 
         if policy is None:
@@ -127,9 +129,6 @@ class CDNAv3Writer:
                                   fit_group_affine)
 
         dev = isinstance(tensor, torch.Tensor) and tensor.is_cuda
-        if dev and vector_dim == 1 and n_clusters > 256:
-            raise NotImplementedError("the GPU encoder fits scalar codebooks of at most 256 "
-                                      "entries; pass a host array for n_clusters > 256")
         if not dev:
             tensor = np.asarray(tensor.cpu() if isinstance(tensor, torch.Tensor) else tensor,
                                 dtype=np.float32)
@@ -138,10 +137,9 @@ class CDNAv3Writer:
         if vector_dim > 1:
             if group_size:
                 raise NotImplementedError("the per-group affine is fitted for scalar codebooks")
-            if not dev:
-                raise RuntimeError("the pair encoder takes a device tensor")
             codebook, indices = build_vector_codebook_and_assign(tensor, n_clusters, vector_dim)
-            recon = codebook[indices.reshape(-1).long()].reshape(-1)
+            recon = (codebook[indices.reshape(-1).long()] if dev
+                     else codebook[indices.reshape(-1).astype(np.int64)]).reshape(-1)
         else:
             codebook = (build_kmeans_codebook(flat, n_clusters) if use_kmeans
                         else build_uniform_codebook(flat, n_clusters))

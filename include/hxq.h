@@ -94,8 +94,11 @@ const char *hxq_last_error(void);
  *   1: first release.
  *   2: hxq_expert_bank gained sc_grp_ptr / sc_grp_key / sc_grp_val (the
  *      per-step sidecar lists of the register-dequant grouped GEMM).
+ *   3: wide scalar encoder entry points (hxq_assign_nearest_wide,
+ *      hxq_kmeans_run_wide, hxq_affine_fit_wide); hxq_kmeans_workspace_bytes
+ *      sizes for codebooks of up to 4096 entries.
  */
-#define HXQ_ABI_VERSION 2
+#define HXQ_ABI_VERSION 3
 int hxq_abi_version(void);
 
 /*
@@ -540,6 +543,22 @@ int hxq_kmeans_init(const float *x, int64_t n, void *workspace, int64_t workspac
 int hxq_kmeans_run(const float *x, int64_t n, const double *percentiles01, int32_t k,
                    int32_t max_iters, double rtol, void *workspace, int64_t workspace_bytes,
                    float *codebook, uint8_t *assignments, int32_t *iters, hipStream_t stream);
+/*
+ * Wide scalar codebooks (257..4096 entries, uint16 indices): the same
+ * algorithms and arithmetic as hxq_assign_nearest / hxq_kmeans_run /
+ * hxq_affine_fit with k <= 4096 (the same k-means workspace).
+ *   Replace: the scalar path of CDNAv3Writer._write_quantized for
+ *   n_clusters > 256 (helix_substrate/hxq_writer_v3.py:189-198, uint16
+ *   indices), _simple_kmeans on its GPU branch (_gpu_kmeans,
+ *   helix_substrate/hxq_encoder.py:180-207: integer assignments, so every
+ *   cluster above 255 is updated; the CPU branch's uint8 cast at :160 would
+ *   fold clusters mod 256).
+ */
+int hxq_assign_nearest_wide(const float *x, int64_t n, const float *codebook, int32_t k,
+                            uint16_t *indices, hipStream_t stream);
+int hxq_kmeans_run_wide(const float *x, int64_t n, const double *percentiles01, int32_t k,
+                        int32_t max_iters, double rtol, void *workspace, int64_t workspace_bytes,
+                        float *codebook, uint16_t *assignments, int32_t *iters, hipStream_t stream);
 int64_t hxq_select_workspace_bytes(void);
 int hxq_select_f32(const float *x, int64_t n, const int64_t *ranks, int32_t m, float *values,
                    int32_t *nan_count, void *workspace, int64_t workspace_bytes,
@@ -598,6 +617,11 @@ int hxq_affine_fit(const float *w, const uint8_t *indices, const float *codebook
                    int64_t rows, int64_t cols, int32_t group_size,
                    const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
                    int64_t workspace_bytes, float *scale, float *offset, hipStream_t stream);
+/* hxq_affine_fit for uint16 indices and codebooks of up to 4096 entries. */
+int hxq_affine_fit_wide(const float *w, const uint16_t *indices, const float *codebook, int32_t k,
+                        int64_t rows, int64_t cols, int32_t group_size,
+                        const int64_t *exclude_positions, int64_t n_exclude, void *workspace,
+                        int64_t workspace_bytes, float *scale, float *offset, hipStream_t stream);
 int64_t hxq_outliers_workspace_bytes(int64_t n);
 int hxq_outliers_f32(const float *x, int64_t n, const float *lohi, int64_t capacity,
                      int64_t *positions, float *values, int64_t *count, void *workspace,

@@ -320,12 +320,74 @@ def test_vector_kmeans_oracle_seeding():
     assert len({tuple(s) for s in seeds[64:].tolist()}) == 136
 
 
-def test_pair_writer_takes_device_tensors(tmp_path):
+@pytest.mark.parametrize("k", [16, 300])
+def test_pair_writer_host_arrays_match_oracle(tmp_path, k):
+    # host arrays run the reference's CPU branch: codebook and indices equal
+    # the oracle's, uint8 up to 256 entries and uint16 above
+    from helix_substrate.hxq_reader_v3 import CDNAv3Reader
     from helix_substrate.hxq_writer_v3 import CDNAv3Writer
 
-    with pytest.raises(RuntimeError):
-        CDNAv3Writer(tmp_path).write_tensor(np.zeros((4, 8), np.float32), "w", n_clusters=16,
-                                            vector_dim=2)
+    w = (np.random.RandomState(5).standard_t(5, (96, 256)) * 0.02).astype(np.float32)
+    CDNAv3Writer(tmp_path).write_tensor(w, "p.weight", n_clusters=k, vector_dim=2,
+                                        sidecar_enabled=False)
+    d = tmp_path / "p_weight.cdnav3"
+    cb_o, idx_o = oracle.build_vector_codebook_np(w, k)
+    cb = np.load(d / "codebook.npy")
+    idx = np.fromfile(d / "indices.bin", np.uint8 if k <= 256 else np.uint16).reshape(96, 128)
+    np.testing.assert_array_equal(cb, cb_o)
+    np.testing.assert_array_equal(idx, np.asarray(idx_o).reshape(96, 128))
+    np.testing.assert_array_equal(CDNAv3Reader(d).reconstruct(), cb[idx.astype(np.int64)].reshape(96, 256))
+
+
+def test_host_vector_kmeans_matches_oracle():
+    # the product's numpy pair k-means (seeding on 100000-row subsamples above
+    # 100000 rows, more than 64 seeds) equals the oracle's
+    rs = np.random.RandomState(6)
+    for n, k in [(3000, 64), (120_001, 80)]:
+        x = _pairs(rs, n)
+        cb, a, steps = hxq_encoder.vector_kmeans(x, k, max_iters=3)
+        cb_o, a_o, steps_o = oracle.vector_kmeans_np(x, k, max_iters=3)
+        np.testing.assert_array_equal(cb, cb_o)
+        np.testing.assert_array_equal(a, a_o)
+        assert steps == steps_o
+
+
+@pytest.mark.parametrize("k", [512, 1000])
+def test_module_cpu_kmeans_wide_matches_oracle(k):
+    # 257..4096 entries: integer cluster ids in the Lloyd updates (uint16)
+    x = (np.random.RandomState(k).standard_t(5, 30000) * 0.02).astype(np.float32)
+    cb, a = hxq_encoder._simple_kmeans(x, k)
+    cb_o, a_o, _ = oracle.kmeans_np(x, k)
+    assert a.dtype == np.uint16 and int(a.max()) >= 256
+    np.testing.assert_array_equal(cb, cb_o)
+    np.testing.assert_array_equal(a, a_o)
+
+
+def test_subsampled_codebooks_recover_a_finite_value_set():
+    # Pins the writer's subsample (kmeans_sample_np) and the pair codebook
+    # builder (build_vector_codebook_np) beyond their parts: data made of
+    # exactly k distinct values (pairs), more elements than the 500000-sample
+    # cap.  The sample holds every value; percentile / k-means++ seeding puts
+    # one centroid on each (a value already chosen has distance 0); each
+    # cluster is then copies of one value, whose fp64 / fp32 mean is exact.
+    # So the codebook is the value set and every element reconstructs exactly.
+    rs = np.random.RandomState(7)
+    vals = np.sort(rs.standard_normal(24).astype(np.float32))
+    flat = vals[rs.randint(0, 24, 700_000)]
+    sample = oracle.kmeans_sample_np(flat)
+    assert sample.size == 500_000 and set(np.unique(sample)) == set(vals)
+    cb, a, _ = oracle.kmeans_np(sample, 24)
+    np.testing.assert_array_equal(cb, vals)
+    np.testing.assert_array_equal(cb[oracle.assign_nearest_np(flat, cb)], flat)
+    pv = rs.standard_normal((16, 2)).astype(np.float32)
+    w = pv[rs.randint(0, 16, 600_000)].reshape(1200, 1000)   # 600000 pairs
+    pcb, pidx = oracle.build_vector_codebook_np(w, 16)
+    assert {tuple(r) for r in pcb.tolist()} == {tuple(r) for r in pv.tolist()}
+    np.testing.assert_array_equal(pcb[np.asarray(pidx).reshape(-1).astype(np.int64)].reshape(w.shape), w)
+    # the product's host path gives the same files' contents
+    hcb, hidx = hxq_encoder.build_vector_codebook_and_assign(w, 16)
+    np.testing.assert_array_equal(hcb, pcb)
+    np.testing.assert_array_equal(hidx.reshape(-1), np.asarray(pidx).reshape(-1))
 
 
 def test_seeding_stream_replay_matches_randomstate():

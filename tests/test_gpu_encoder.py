@@ -352,3 +352,92 @@ def test_vector_kmeans_edge_cases(dev):
     one, a1, _ = hxq_encoder.vector_kmeans(torch.from_numpy(const).to(dev), 1)
     np.testing.assert_array_equal(one.cpu().numpy(), const[:1])
     assert int(a1.abs().sum()) == 0
+
+
+# ---------------------------------------------------------------------------
+# wide scalar codebooks (257..4096 entries, uint16 ids in int16 tensors)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["sorted4096", "unsorted1000", "specials300"])
+def test_assign_wide_matches_oracle(dev, case):
+    rs = np.random.RandomState(31)
+    x = _weights(rs, 1 << 20)
+    if case == "sorted4096":
+        cb = np.sort(_weights(rs, 4096))
+    elif case == "unsorted1000":
+        cb = _weights(rs, 1000)
+    else:
+        cb = np.sort(_weights(rs, 300))
+        x[:6] = [np.nan, np.inf, -np.inf, 0.0, cb[299], cb[0]]
+        cb[7] = np.nan   # unsorted path
+    print(f"assign wide case={case} k={cb.size}", flush=True)
+    got = _hxq.assign_nearest(torch.from_numpy(x).to(dev), torch.from_numpy(cb).to(dev))
+    assert got.dtype == torch.int16
+    np.testing.assert_array_equal(got.cpu().numpy().astype(np.uint16), oracle.assign_nearest_np(x, cb))
+
+
+@pytest.mark.parametrize("n,k", [(20000, 512), (40000, 3000), (9000, 4096)])
+def test_kmeans_wide_matches_oracle(dev, n, k):
+    data = _weights(np.random.RandomState(n + k), n)
+    print(f"kmeans wide n={n} k={k}", flush=True)
+    cb, asg, it = _hxq.kmeans_1d(torch.from_numpy(data).to(dev), k, 10, 0.001)
+    cb_o, asg_o, it_o = oracle.kmeans_np(data, k)
+    assert asg.dtype == torch.int16
+    np.testing.assert_array_equal(cb.cpu().numpy(), cb_o)
+    np.testing.assert_array_equal(asg.cpu().numpy().astype(np.uint16), asg_o)
+    assert it == it_o
+
+
+def test_affine_fit_wide_matches_oracle(dev):
+    rs = np.random.RandomState(32)
+    rows, cols, G, k = 256, 512, 128, 2000
+    cb = np.sort(_weights(rs, k))
+    idx = rs.randint(0, k, (rows, cols)).astype(np.uint16)
+    w = (cb[idx] * rs.uniform(0.9, 1.1, (rows, 1)) + _weights(rs, rows * cols, 0.003)
+         .reshape(rows, cols)).astype(np.float32)
+    ex = np.sort(rs.choice(rows * cols, 300, replace=False)).astype(np.int64)
+    print("affine_fit wide", flush=True)
+    s, o = _hxq.affine_fit(torch.from_numpy(w).to(dev), torch.from_numpy(idx.astype(np.int16)).to(dev),
+                           torch.from_numpy(cb).to(dev), G, torch.from_numpy(ex).to(dev))
+    s_o, o_o = oracle.affine_fit_np(w, idx, cb, G, ex)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_o)
+    np.testing.assert_array_equal(o.cpu().numpy(), o_o)
+
+
+@pytest.mark.parametrize("k,G", [(1024, 128), (4096, None)])
+def test_write_tensor_wide_gpu_matches_cpu(dev, tmp_path, k, G):
+    rs = np.random.RandomState(33)
+    t = (_weights(rs, 384 * 512).reshape(384, 512) * rs.uniform(0.5, 2, (384, 1))).astype(np.float32)
+    print(f"write_tensor wide k={k} G={G}", flush=True)
+    kw = {"n_clusters": k}
+    if G:
+        kw["group_size"] = G
+    CDNAv3Writer(tmp_path / "gpu").write_tensor(torch.from_numpy(t).to(dev), "m.weight", **kw)
+    CDNAv3Writer(tmp_path / "cpu").write_tensor(t, "m.weight", **kw)
+    files = ["codebook.npy", "indices.bin"] + (["group_scale.npy", "group_offset.npy"] if G else [])
+    for f in files:
+        assert (tmp_path / "gpu" / "m_weight.cdnav3" / f).read_bytes() == \
+            (tmp_path / "cpu" / "m_weight.cdnav3" / f).read_bytes(), f
+    _same_sidecar(tmp_path / "gpu" / "m_weight.cdnav3", tmp_path / "cpu" / "m_weight.cdnav3")
+
+
+@pytest.mark.parametrize("k", [64, 600])
+def test_write_tensor_pairs_gpu_matches_host(dev, tmp_path, k):
+    # the pair writer gives the same files from a device tensor and a host array
+    rs = np.random.RandomState(34)
+    t = _weights(rs, 256 * 512).reshape(256, 512)
+    print(f"write_tensor pairs gpu/host k={k}", flush=True)
+    CDNAv3Writer(tmp_path / "gpu").write_tensor(torch.from_numpy(t).to(dev), "p.weight", n_clusters=k,
+                                                vector_dim=2)
+    CDNAv3Writer(tmp_path / "cpu").write_tensor(t, "p.weight", n_clusters=k, vector_dim=2)
+    for f in ("codebook.npy", "indices.bin"):
+        assert (tmp_path / "gpu" / "p_weight.cdnav3" / f).read_bytes() == \
+            (tmp_path / "cpu" / "p_weight.cdnav3" / f).read_bytes(), f
+    _same_sidecar(tmp_path / "gpu" / "p_weight.cdnav3", tmp_path / "cpu" / "p_weight.cdnav3")
+
+
+def _same_sidecar(a, b):
+    # the npz holds a write time: compare the arrays
+    with np.load(a / "sidecar.npz") as za, np.load(b / "sidecar.npz") as zb:
+        for key in ("positions", "values"):
+            np.testing.assert_array_equal(za[key], zb[key])
