@@ -656,14 +656,14 @@ def scan_bench(dev, iters=5, cpu=True):
     flops = 5.0 * states  # recurrence form: h = a*h + (dt x) B (3), y += h C (2)
     nbytes = (x.numel() * 2 + dt.numel() * 4 + Bm.numel() * 2 + Cm.numel() * 2 + y.numel() * 4
               + hf.numel() * 4 + 2 * H * 4)
-    # The bf16 inputs run the SSD form on MFMA (ssd2_kernel): per (batch, head)
+    # The bf16 inputs run the SSD form on MFMA (ssd_kernel): per (batch, head)
     # and 64-token chunk, 176 v_mfma_f32_32x32x16_bf16 of 32768 FLOP each --
     # C B^T 24 (three causal 32x32 tiles over n = 128), M x 24 (hi/lo split,
     # causal tiles), C S^T 64 and the state update 64 (hi/lo splits)
     mfma_flop = 176 * 32768.0 * b * H * ((L + 63) // 64)
     out = {"shape": {"batch": b, "seqlen": L, "heads": H, "head_dim": P, "state": N,
                      "ngroups": 1, "chunk": 256},
-           "kernel": "ssd2_kernel<4> (SSD chunk form, bf16 MFMA, fp32 state, 2 blocks per CU)",
+           "kernel": "ssd_kernel<4> (SSD chunk form, bf16 MFMA, fp32 state, 2 blocks per CU)",
            "ms": round(ms, 4), "gflop_recurrence": round(flops / 1e9, 2),
            "tflops": round(flops / ms / 1e9, 2),
            "mfma_gflop_executed": round(mfma_flop / 1e9, 2),

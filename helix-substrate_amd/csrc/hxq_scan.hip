@@ -27,7 +27,6 @@
 // are read as LDS broadcasts; per-split y partials are summed through LDS in a
 // fixed order (deterministic).
 #include <algorithm>
-#include <cstdlib>
 
 #include "hxq_common.h"
 
@@ -261,21 +260,18 @@ static int launch_chunks(const ScanArgs &a, hipStream_t stream) {
 // the same intra/inter-chunk split).  The four contractions run on
 // v_mfma_f32_32x32x16_bf16:
 //   (a) CB^T = B C^T         [s, t] over n    (bf16 x bf16: exact products)
-//   (b) M  = CB o exp(cs_t - cs_s) dt_s, lower triangle, split M = Mh + Ml
-//       into two bf16 (16 mantissa bits kept; x is bf16 and exact)
+//   (b) M  = CB o exp(cs_t - cs_s) dt_s, lower triangle, + D on the diagonal,
+//       split M = Mh + Ml into two bf16 (16 mantissa bits kept; x is bf16 and
+//       exact)
 //   (c) Y  = M x              [t, p] over s    (Mh x + Ml x)
 //   (d) Z  = C S^T            [t, p] over n    (S split Sh + Sl)
 //   (e) S^T = exp(cs_Q) S^T + B^T X'  [n, p] over s, X' = exp(cs_Q - cs_s) dt_s x_s
 //       split X'h + X'l
-// (a) and (e) produce transposed tiles so that each lane holds 4 consecutive
-// elements of an LDS row (8-byte stores of M and S).
 // so every product is exact or carries a 2^-17 relative split error, with
-// fp32 accumulation: well inside the scan's 1e-4 bar.  Operands are staged
-// in LDS with k contiguous per row (C, B: n; B^T, x^T, M, X': s), 16-byte
-// chunks XOR-swizzled by row so the 16 lanes of a read hit distinct banks.
-// Block: 4 waves; wave w owns output tile (t-tile w/2, p-tile w%2) of (c)/(d),
-// tile (s-tile w%2, t-tile w/2) of (a) (none above the diagonal) and state
-// tiles (p-tile w%2, n-tiles of (e)).
+// fp32 accumulation: well inside the scan's 1e-4 bar.  C and B are staged in
+// LDS with n contiguous per row, x with p contiguous, 16-byte chunks
+// XOR-swizzled by row so the lanes of a read hit distinct banks; operands
+// whose k is s (B^T, x^T) come from those tiles by transposing reads.
 // Shapes: head_dim <= 64 (padded to 64), state <= 128 (padded to 32 NT);
 // other shapes and other dtypes use the VALU recurrence above.
 namespace ssd {
@@ -300,14 +296,6 @@ __device__ __forceinline__ int sw(int r, int c) {
     return r * CPR * 8 + ((c ^ ((r * CPR / 16) % CPR)) << 3);
 }
 
-// Rows of kQ = 64 bf16 (s contiguous: B^T, x^T, M, X'): 8 chunks, XOR with
-// ((r / 2) ^ (r / 8)) % 8 -- 16 consecutive rows read one logical chunk from
-// 16 distinct bank groups, and the transposing stores (rows 8c + k for 16
-// values of c) hit 8 distinct groups.
-__device__ __forceinline__ int swq(int r, int c) {
-    return r * 64 + ((c ^ (((r >> 1) ^ (r >> 3)) & 7)) << 3);
-}
-
 __device__ __forceinline__ u32x4 lds16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
 __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
@@ -328,320 +316,6 @@ __device__ __forceinline__ void split2x2(float a, float b, uint32_t &hi, uint32_
 
 // 2^x (v_exp_f32)
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-template <int NT>  // state tiles of 32 (NP = 32 NT)
-__global__ __launch_bounds__(kThreads, 1) void ssd_kernel(const ScanArgs a) {
-    constexpr int NP = 32 * NT;
-    constexpr int CN = NP / 8;   // 16-byte chunks per row of n
-    __shared__ __attribute__((aligned(16))) uint16_t sC[kQ * NP];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[kQ * NP];
-    __shared__ __attribute__((aligned(16))) uint16_t sBt[NP * kQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sXt[kPP * kQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sM[2][kQ * kQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sXp[2][kPP * kQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sS[2][kPP * NP];
-    // per-token decay terms of a chunk, double buffered (the next chunk's are
-    // computed while this one runs)
-    __shared__ double scs2[2][kQ];
-    __shared__ float sdt2[2][kQ], swt2[2][kQ];
-    __shared__ __attribute__((aligned(16))) float sec2[2][kQ];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ml = lane & 31, hh = lane >> 5;
-    const int b = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
-    const int H = a.heads, P = a.head_dim, N = a.state, L = a.seqlen;
-    const int g = h / (H / a.ngroups);
-    const float Ah = a.A[h];
-    const float Dh = a.D ? a.D[h] : 0.f;
-    const int ti = wave >> 1, pj = wave & 1;  // (c)/(d) output tile
-    // (e) state tiles: 2 p-tiles x NT n-tiles over the 4 waves: wave w takes
-    // p-tile w % 2 and n-tiles [nj0, nj0 + nst) (NT = 1: waves 2, 3 hold none)
-    const int pi = wave & 1;
-    const int nst = NT == 4 ? 2 : 1;
-    const int nj0 = NT == 4 ? 2 * (wave >> 1) : (wave >> 1);
-    const bool has_s = NT >= 2 || wave < 2;
-    // y through a buffer resource (fixed store count, masked pieces dropped)
-    const int64_t y_bytes = (int64_t)a.batch * L * H * P * (a.y_dt == HXQ_F32 ? 4 : 2);
-    const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, y_bytes);
-    constexpr uint32_t kYOob = 0xfffffff0u;
-
-    // ---- chunk inputs: global -> registers (prefetch) -> LDS ------------------
-    // Buffer loads with masked pieces sent past the range: every lane issues
-    // the same loads, so wait counts stay exact across the chunk loop.
-    constexpr uint32_t kOob = 0xfffffff0u;
-    const int dtb = a.dt_dt == HXQ_F32 ? 4 : 2;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (int64_t)a.batch * L * H * P * 2);
-    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.Bm, (int64_t)a.batch * L * a.ngroups * N * 2);
-    const __amdgpu_buffer_rsrc_t cr = make_rsrc(a.Cm, (int64_t)a.batch * L * a.ngroups * N * 2);
-    const __amdgpu_buffer_rsrc_t dr = make_rsrc(a.dt, (int64_t)a.batch * L * H * dtb);
-    // B, C: token pair u = item / CN (tokens 2u, 2u+1), n chunk item % CN
-    constexpr int BC_ITEMS = (kQ / 2) * CN;           // per matrix
-    constexpr int BC_PER = (BC_ITEMS + kThreads - 1) / kThreads;
-    u32x4 rB[BC_PER][2], rC[BC_PER][2];
-    u32x4 rX[2];  // x: token pair tid / 8, p chunk tid % 8 (256 items)
-    auto load_chunk = [&](int t0) {
-#pragma unroll
-        for (int i = 0; i < BC_PER; ++i) {
-            const int item = tid + kThreads * i;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int t = t0 + 2 * (item / CN) + e, c = item % CN;
-                const bool ok = item < BC_ITEMS && t < L && 8 * c < N;
-                const uint32_t o = ok ? static_cast<uint32_t>(((((int64_t)b * L + t) * a.ngroups + g) * N + 8 * c) * 2) : kOob;
-                rB[i][e] = buf_load16(br, o);
-                rC[i][e] = buf_load16(cr, o);
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int t = t0 + 2 * (tid >> 3) + e, c = tid & 7;
-            const bool ok = t < L && 8 * c < P;
-            rX[e] = buf_load16(xr, ok ? static_cast<uint32_t>(((((int64_t)b * L + t) * H + h) * P + 8 * c) * 2) : kOob);
-        }
-    };
-    // dt of token t0 + lane (raw bits; every wave loads it)
-    auto load_dt = [&](int t0) -> uint32_t {
-        const int t = t0 + lane;
-        const uint32_t o = t < L ? static_cast<uint32_t>((((int64_t)b * L + t) * H + h) * dtb) : kOob;
-        return dtb == 4 ? __builtin_amdgcn_raw_buffer_load_b32(dr, o, 0, 0)
-                        : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(dr, o, 0, 0));
-    };
-    auto dt_value = [&](uint32_t raw) -> float {
-        return a.dt_dt == HXQ_F32 ? __uint_as_float(raw)
-             : a.dt_dt == HXQ_BF16 ? bf16_to_f32(static_cast<uint16_t>(raw)) : f16_to_f32(static_cast<uint16_t>(raw));
-    };
-    // the decay terms of a chunk from its dt (one wave): log2-decay prefix in
-    // fp64 (differences of nearby prefixes stay exact), exponentials as 2^x
-    auto decay_terms = [&](float dtv, int buf) {
-        double cs = static_cast<double>(Ah * dtv);
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const double o = __shfl_up(cs, off, 64);
-            if (lane >= off) cs += o;
-        }
-        cs *= 1.4426950408889634;  // log2(e)
-        const double csq = __shfl(cs, 63, 64);
-        scs2[buf][lane] = cs;
-        sdt2[buf][lane] = dtv;
-        swt2[buf][lane] = exp2_fast(static_cast<float>(csq - cs)) * dtv;
-        sec2[buf][lane] = exp2_fast(static_cast<float>(cs));
-    };
-    // the two tokens' 16-bit values of element k as one dword (token 2u low)
-    auto pair_of = [](const u32x4 &v0, const u32x4 &v1, int k) -> uint32_t {
-        const uint32_t a0 = (v0[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-        const uint32_t a1 = (v1[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-        return a0 | (a1 << 16);
-    };
-    auto store_chunk = [&]() {
-#pragma unroll
-        for (int i = 0; i < BC_PER; ++i) {
-            const int item = tid + kThreads * i;
-            if (item >= BC_ITEMS) continue;
-            const int u = item / CN, c = item % CN;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                *reinterpret_cast<u32x4 *>(sB + sw<CN>(2 * u + e, c)) = rB[i][e];
-                *reinterpret_cast<u32x4 *>(sC + sw<CN>(2 * u + e, c)) = rC[i][e];
-            }
-            // B^T rows n = 8c + k, columns 2u, 2u+1
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                *reinterpret_cast<uint32_t *>(sBt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
-                    pair_of(rB[i][0], rB[i][1], k);
-        }
-        const int u = tid >> 3, c = tid & 7;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            *reinterpret_cast<uint32_t *>(sXt + swq(8 * c + k, u >> 2) + 2 * (u & 3)) =
-                pair_of(rX[0], rX[1], k);
-    };
-
-    // ---- state ----------------------------------------------------------------
-    // S^T tiles: Sacc[j][r] = S[p = 32 pi + ml][n = 32(nj0 + j) + 8(r/4) + 4hh + r%4]
-    const int sp = 32 * pi + ml;
-    f32x16 Sacc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int n = 32 * (nj0 + j) + 8 * (r >> 2) + 4 * hh + (r & 3);
-            Sacc[j][r] = (a.h0 && has_s && j < nst && sp < P && n < N)
-                             ? a.h0[(((int64_t)b * H + h) * P + sp) * N + n] : 0.f;
-        }
-    // S -> sS (hi, lo): rows p, n contiguous; 4 consecutive n per 8-byte store
-    auto store_state = [&]() {
-        if (!has_s) return;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            if (j >= nst) break;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = 32 * (nj0 + j) + 8 * q + 4 * hh;
-                uint32_t h01, l01, h23, l23;
-                split2x2(Sacc[j][4 * q], Sacc[j][4 * q + 1], h01, l01);
-                split2x2(Sacc[j][4 * q + 2], Sacc[j][4 * q + 3], h23, l23);
-                const int o = sw<CN>(sp, n >> 3) + (n & 7);
-                *reinterpret_cast<uint2 *>(sS[0] + o) = make_uint2(h01, h23);
-                *reinterpret_cast<uint2 *>(sS[1] + o) = make_uint2(l01, l23);
-            }
-        }
-    };
-
-    const int nch = (L + kQ - 1) / kQ;
-    load_chunk(0);
-    uint32_t rdt = load_dt(0);
-    if (wave == 1) decay_terms(dt_value(rdt), 0);
-    rdt = load_dt(kQ);  // dt of chunk 1
-    store_state();
-    for (int ch = 0; ch < nch; ++ch) {
-        const int t0 = ch * kQ;
-        const int db = ch & 1;
-        double *scs = scs2[db];
-        float *sdt = sdt2[db], *swt = swt2[db], *sec = sec2[db];
-        lds_barrier();  // the previous chunk's readers of the inputs are done
-        store_chunk();
-        if (ch + 1 < nch) load_chunk(t0 + kQ);
-        lds_barrier();
-        // wave 1 (no CB tile) prepares the next chunk's decay terms meanwhile
-        if (wave == 1 && ch + 1 < nch) {
-            decay_terms(dt_value(rdt), db ^ 1);
-            rdt = load_dt(t0 + 2 * kQ);
-        }
-
-        // (a) CB^T tile (s-tile si, t-tile ti) and (b) M; s-tile 1 of t-tile 0
-        // lies above the diagonal
-        const int si = pj;
-        if (!(ti == 0 && si == 1)) {
-            f32x16 cb;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) cb[r] = 0.f;
-#pragma unroll
-            for (int ks = 0; ks < NP / 16; ++ks) {
-                const u32x4 bv = lds16(sB + sw<CN>(32 * si + ml, 2 * ks + hh));
-                const u32x4 cv = lds16(sC + sw<CN>(32 * ti + ml, 2 * ks + hh));
-                cb = mfma(bv, cv, cb);
-            }
-            // lane: t = 32 ti + ml; cb[r]: s = 32 si + 8(r/4) + 4hh + r%4
-            const int t = 32 * ti + ml;
-            const double cst = scs[t];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int s0 = 32 * si + 8 * q + 4 * hh;
-                float m[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int s = s0 + e;
-                    m[e] = s <= t ? cb[4 * q + e] * exp2_fast(static_cast<float>(cst - scs[s])) * sdt[s] : 0.f;
-                }
-                uint32_t h01, l01, h23, l23;
-                split2x2(m[0], m[1], h01, l01);
-                split2x2(m[2], m[3], h23, l23);
-                const int o = swq(t, s0 >> 3) + (s0 & 7);
-                *reinterpret_cast<uint2 *>(sM[0] + o) = make_uint2(h01, h23);
-                *reinterpret_cast<uint2 *>(sM[1] + o) = make_uint2(l01, l23);
-            }
-        }
-        // X'[p][s] = w_s x[s][p], split; two tokens per dword
-#pragma unroll
-        for (int i = 0; i < (kPP * kQ / 2) / kThreads; ++i) {
-            const int d = tid + kThreads * i;          // dword index
-            const int p = d / (kQ / 2), u = d % (kQ / 2);
-            const int o = swq(p, u >> 2) + 2 * (u & 3);
-            const uint32_t xx = *reinterpret_cast<const uint32_t *>(sXt + o);
-            uint32_t hi, lo;
-            split2x2(__uint_as_float(xx << 16) * swt[2 * u], __uint_as_float(xx & 0xffff0000u) * swt[2 * u + 1],
-                     hi, lo);
-            *reinterpret_cast<uint32_t *>(sXp[0] + o) = hi;
-            *reinterpret_cast<uint32_t *>(sXp[1] + o) = lo;
-        }
-        lds_barrier();
-
-        // (c) Y^T = x^T M^T over s <= end of t-tile ti; (d) Z^T = S C^T over n.
-        // Transposed tiles: lane (t = 32 ti + ml) holds 4 consecutive p per
-        // row group, stored as one 16-byte (fp32 y) or 8-byte (16-bit y) piece.
-        {
-            f32x16 yv, zv;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) yv[r] = zv[r] = 0.f;
-            for (int ks = 0; ks < 2 * (ti + 1); ++ks) {
-                const u32x4 xa = lds16(sXt + swq(32 * pj + ml, 2 * ks + hh));
-                yv = mfma(xa, lds16(sM[0] + swq(32 * ti + ml, 2 * ks + hh)), yv);
-                yv = mfma(xa, lds16(sM[1] + swq(32 * ti + ml, 2 * ks + hh)), yv);
-            }
-#pragma unroll
-            for (int ks = 0; ks < NP / 16; ++ks) {
-                const u32x4 cv = lds16(sC + sw<CN>(32 * ti + ml, 2 * ks + hh));
-                zv = mfma(lds16(sS[0] + sw<CN>(32 * pj + ml, 2 * ks + hh)), cv, zv);
-                zv = mfma(lds16(sS[1] + sw<CN>(32 * pj + ml, 2 * ks + hh)), cv, zv);
-            }
-            const int t = 32 * ti + ml;
-            const float et = sec[t];
-            const bool t_ok = t0 + t < L;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int p0 = 32 * pj + 8 * q + 4 * hh;  // p0 .. p0 + 3
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float xv = bf16_to_f32(sXt[swq(p0 + e, t >> 3) + (t & 7)]);
-                    v[e] = yv[4 * q + e] + et * zv[4 * q + e] + Dh * xv;
-                }
-                // every lane stores (masked pieces go past the buffer's range), so
-                // the store count per chunk is fixed and loads are never made to
-                // wait behind stores of unknown number
-                const bool ok = t_ok && p0 < P;
-                const uint32_t yo = static_cast<uint32_t>((((int64_t)b * L + t0 + t) * H + h) * P + p0);
-                if (a.y_dt == HXQ_F32) {
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                              __float_as_uint(v[3])},
-                        yr, ok ? yo * 4u : kYOob, 0, 0);
-                } else {
-                    u32x2 w;
-                    if (a.y_dt == HXQ_BF16) {
-                        w = u32x2{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])};
-                    } else {
-                        w = u32x2{uint32_t(f32_to_f16(v[0])) | (uint32_t(f32_to_f16(v[1])) << 16),
-                                  uint32_t(f32_to_f16(v[2])) | (uint32_t(f32_to_f16(v[3])) << 16)};
-                    }
-                    __builtin_amdgcn_raw_buffer_store_b64(w, yr, ok ? yo * 2u : kYOob, 0, 0);
-                }
-            }
-        }
-        lds_barrier();  // (d) has read sS
-
-        // (e) S = exp(cs_Q) S + X'^T B
-        if (has_s) {
-            const float eq = exp2_fast(static_cast<float>(scs[kQ - 1]));
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if (j >= nst) break;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) Sacc[j][r] *= eq;
-#pragma unroll
-                for (int ks = 0; ks < kQ / 16; ++ks) {
-                    const u32x4 bt = lds16(sBt + swq(32 * (nj0 + j) + ml, 2 * ks + hh));
-                    Sacc[j] = mfma(bt, lds16(sXp[0] + swq(sp, 2 * ks + hh)), Sacc[j]);
-                    Sacc[j] = mfma(bt, lds16(sXp[1] + swq(sp, 2 * ks + hh)), Sacc[j]);
-                }
-            }
-        }
-        store_state();
-    }
-    if (a.h_final && has_s) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            if (j >= nst) break;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int n = 32 * (nj0 + j) + 8 * (r >> 2) + 4 * hh + (r & 3);
-                if (sp < P && n < N) a.h_final[(((int64_t)b * H + h) * P + sp) * N + n] = Sacc[j][r];
-            }
-        }
-    }
-}
 
 // Rows of kPP = 64 bf16 (x in natural order, rows s): 8 chunks, XOR with
 // (r / 2) % 8 -- the transposing reads below touch rows r0 + {0..3, 8..11}
@@ -683,8 +357,9 @@ __device__ __forceinline__ void acc_to_op(const f32x16 &m, u32x4 (&op)[2][2]) {
     }
 }
 
-// The SSD chunk form with two blocks per CU (70.5 KB of LDS at state 128).
-// Same math and splits as ssd_kernel; what changes is where the operands live:
+// The SSD chunk form, two 4-wave blocks per CU (70.5 KB of LDS at state 128).
+// Wave w owns output tile (t-tile w/2, p-tile w%2) of (c) and (d) and state
+// tiles (p-tile w%2, n-tiles of half the state) of (e).  Where the operands live:
 //  - the three decay-masked M tiles (t, s) = (0, 0), (1, 0), (1, 1) are built
 //    once each, by waves 0, 2, 3 (wave 1 computes the next chunk's decay
 //    terms instead), with D added on the diagonal so that (c)'s product
@@ -699,7 +374,7 @@ __device__ __forceinline__ void acc_to_op(const f32x16 &m, u32x4 (&op)[2][2]) {
 // The next chunk's inputs are loaded into registers right after the current
 // chunk is stored to LDS.  Three barriers per chunk.
 template <int NT>  // state tiles of 32 (NP = 32 NT)
-__global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void ssd_kernel(const ScanArgs a) {
     constexpr int NP = 32 * NT;
     constexpr int CN = NP / 8;   // 16-byte chunks per row of n
     __shared__ __attribute__((aligned(16))) uint16_t sC[kQ * NP];
@@ -733,7 +408,7 @@ __global__ __launch_bounds__(kThreads, 2) void ssd2_kernel(const ScanArgs a) {
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, y_bytes);
     constexpr uint32_t kYOob = 0xfffffff0u;
 
-    // ---- chunk inputs (as ssd_kernel) ------------------------------------------
+    // ---- chunk inputs: B and C rows of two tokens and x rows, 16 bytes a lane ----
     constexpr uint32_t kOob = 0xfffffff0u;
     const int dtb = a.dt_dt == HXQ_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (int64_t)a.batch * L * H * P * 2);
@@ -1035,27 +710,11 @@ static bool ssd_eligible(const ScanArgs &a) {
            bc_bytes < (int64_t{1} << 31);
 }
 
-// HXQ_SSD_V1=1 (read once per process) keeps the one-block-per-CU kernel with
-// its LDS operand copies (comparison runs).
-static bool ssd_v1() {
-    static const bool v = [] {
-        const char *e = getenv("HXQ_SSD_V1");
-        return e && atoi(e) != 0;
-    }();
-    return v;
-}
-
 static int launch_ssd(const ScanArgs &a, hipStream_t stream) {
     const dim3 grid(a.batch * a.heads);
-    if (ssd_v1()) {
-        if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
-        else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
-        else hipLaunchKernelGGL(ssd::ssd_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
-    } else {
-        if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd2_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
-        else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd2_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
-        else hipLaunchKernelGGL(ssd::ssd2_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
-    }
+    if (a.state <= 32) hipLaunchKernelGGL(ssd::ssd_kernel<1>, grid, dim3(ssd::kThreads), 0, stream, a);
+    else if (a.state <= 64) hipLaunchKernelGGL(ssd::ssd_kernel<2>, grid, dim3(ssd::kThreads), 0, stream, a);
+    else hipLaunchKernelGGL(ssd::ssd_kernel<4>, grid, dim3(ssd::kThreads), 0, stream, a);
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }
