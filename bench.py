@@ -797,6 +797,9 @@ def decode_bench(dev, n_layers, prompt_len=128, n_new=256, base=None, persistent
            "gbs_weights": round((hxq + lm) / (per_tok_ms * 1e-3) / 1e9, 1),
            "first_tokens_persistent": toks_pers[:8].cpu().tolist(),
            "first_tokens_graph": toks_graph[:8].cpu().tolist(),
+           "first_tokens_note": "the random-init network's argmax is one token at every step "
+                                "(also with the embedding scaled 50x), so the paths are "
+                                "compared on logits below, not on tokens",
            "logits_maxrel_persistent_vs_graph_4_steps": round(logits_rel, 7)}
     dec.close()
     del dec
