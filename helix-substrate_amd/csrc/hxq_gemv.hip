@@ -27,9 +27,10 @@
 //   * the 256-entry codebook lives in LDS replicated NREP times with entry j
 //     of replica r at dword j*NREP + r; lane l reads replica l % NREP, so the
 //     random lookups of one wave hit distinct banks (no bank conflicts);
-//   * row partials go to LDS; the sidecar corrections of the block's rows are
-//     summed by one thread per row at the end; a final pass adds slices,
-//     sidecar and bias in a fixed order (deterministic, no atomics).
+//   * row partials go to LDS; the sidecar products x[col] * delta of the
+//     block's entries go to LDS during the stream; a final pass with up to 64
+//     lanes per output row adds slices, sidecar entries and bias, the row's
+//     lanes reducing in a fixed xor order (deterministic, no atomics).
 #include <algorithm>
 
 #include "hxq_common.h"
@@ -176,10 +177,15 @@ constexpr int kEntCap = 512;  // sidecar entries per block staged in LDS
 //   stream    batches of RB rows per wave, loads of a batch issued together,
 //             double-buffered (batch i+1 in flight while batch i computes);
 //             rows a wave does not own get an out-of-range buffer offset
-//             (no memory traffic) and are not computed;
-//   epilogue  sidecar values x[col]*delta -> LDS; one thread per output row
-//             adds slices, its sidecar entries (CSR order) and bias, and
-//             stores y.  Fixed summation order: deterministic.
+//             (no memory traffic) and are not computed; after its first batch
+//             (whose wait covers the col/delta loads issued before the loop)
+//             each thread writes its sidecar entry's x[col]*delta to LDS;
+//   epilogue  LPR lanes per output row (the largest power of two <= 64 that
+//             fits the block's rows in one pass): lane q adds slices q, q+LPR,
+//             ... and sidecar entries j0+q, j0+q+LPR, ... (CSR order), then
+//             the lanes reduce by xor shuffles; bias, store.  Fixed summation
+//             order: deterministic.  (One thread per row with a serial loop
+//             over the row's entries cost 1.3 us on the config-1 down launch.)
 // Barriers order LDS only (lds_barrier), so prefetched loads stay in flight.
 // Occupancy target: 4 waves per SIMD (two 8-wave blocks per CU, <= 128 VGPRs);
 // the long-row variant (4 chunks per slice) accepts 2.
@@ -311,7 +317,12 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     }
     const __amdgpu_buffer_rsrc_t rp_r = make_rsrc(M.rp, has_sc ? (out + 1) * 4 : 0);
     // final-pass outputs: thread t handles (row lo + t / NX, activation t % NX)
-    const int64_t my_rl = threadIdx.x / NX;
+    // final pass: LPR lanes per (row, activation) item, LPR a power of two <= 64
+    int lg_lpr = 0;
+    while (lg_lpr < 6 && (n_rows * NX) << (lg_lpr + 1) <= NT) ++lg_lpr;
+    const int LPR = 1 << lg_lpr;
+    const int my_item = static_cast<int>(threadIdx.x) >> lg_lpr, my_q = threadIdx.x & (LPR - 1);
+    const int64_t my_rl = my_item / NX;
     const int32_t my_j0 = buf_loadi(rp_r, static_cast<uint32_t>((lo + my_rl) * 4));
     const int32_t my_j1 = buf_loadi(rp_r, static_cast<uint32_t>((lo + my_rl + 1) * 4));
     const int32_t blk_j0 = buf_loadi(rp_r, static_cast<uint32_t>(lo * 4));
@@ -551,26 +562,6 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
             if (lane == kWave - 1) red[(rl * NX + n) * S + s_id] = v;
         }
     };
-    // double-buffered batches: the next batch's loads are issued before the
-    // current batch is computed (it2 is the second buffer)
-    GemvItem<CPS, QW> it2[RB];
-    for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
-#pragma unroll
-        for (int b = 0; b < RB; ++b) load_item(i0 + RB + b, it2[b]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int b = 0; b < RB; ++b)
-            if (i0 + b < n_mine) compute_item(i0 + b, it[b]);
-        if (i0 + RB >= n_mine) break;
-#pragma unroll
-        for (int b = 0; b < RB; ++b) load_item(i0 + 2 * RB + b, it[b]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int b = 0; b < RB; ++b)
-            if (i0 + RB + b < n_mine) compute_item(i0 + RB + b, it2[b]);
-    }
-
-    // ---- epilogue
     auto xval = [&](int n, int32_t c) -> float {
         if (xlds) return xl[n * K + c];
         if constexpr (XM == 1) {
@@ -582,8 +573,10 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
         }
         return load_x1(x, n * K + c, XT);
     };
-    lds_barrier();  // red complete
-    if (has_sc) {
+    // the sidecar products x[col] * delta of this block's entries, into LDS:
+    // after a thread's first batch (its col/delta loads have landed by then)
+    bool ent_done = !has_sc;
+    auto compute_ent = [&]() {
         const int32_t lim = nent < kEntCap ? nent : kEntCap;
         for (int32_t e = threadIdx.x; e < lim; e += NT) {
             int32_t c;
@@ -598,22 +591,52 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
 #pragma unroll
             for (int n = 0; n < NX; ++n) ent[e * NX + n] = xval(n, c) * dv;
         }
+        ent_done = true;
+    };
+    // double-buffered batches: the next batch's loads are issued before the
+    // current batch is computed (it2 is the second buffer)
+    GemvItem<CPS, QW> it2[RB];
+    for (int32_t i0 = 0; i0 < n_mine; i0 += 2 * RB) {
+#pragma unroll
+        for (int b = 0; b < RB; ++b) load_item(i0 + RB + b, it2[b]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+            if (i0 + b < n_mine) compute_item(i0 + b, it[b]);
+        if (!ent_done) compute_ent();
+        if (i0 + RB >= n_mine) break;
+#pragma unroll
+        for (int b = 0; b < RB; ++b) load_item(i0 + 2 * RB + b, it[b]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+            if (i0 + RB + b < n_mine) compute_item(i0 + RB + b, it2[b]);
     }
-    lds_barrier();
-    if (threadIdx.x < n_rows * NX) {
-        const int n = static_cast<int>(threadIdx.x % NX);
+
+    // ---- epilogue
+    if (!ent_done) compute_ent();
+    lds_barrier();  // red and ent complete
+    {
+        // lane q of an item adds slices q, q + LPR, ... and sidecar entries
+        // j0 + q, j0 + q + LPR, ...; the item's lanes then reduce in a fixed
+        // xor order (deterministic)
+        const bool live = my_item < n_rows * NX;
+        const int n = my_item % NX;
         float v = 0.f;
-        for (int s2 = 0; s2 < S; ++s2) v += red[threadIdx.x * S + s2];
-        if (has_sc) {
-            float scs = 0.f;
-            for (int32_t j = my_j0; j < my_j1; ++j) {
-                const int32_t e = j - blk_j0;
-                scs += e < kEntCap ? ent[e * NX + n] : xval(n, M.col[j]) * M.delta[j];
+        if (live) {
+            for (int s2 = my_q; s2 < S; s2 += LPR) v += red[my_item * S + s2];
+            if (has_sc) {
+                for (int32_t j = my_j0 + my_q; j < my_j1; j += LPR) {
+                    const int32_t e = j - blk_j0;
+                    v += e < kEntCap ? ent[e * NX + n] : xval(n, M.col[j]) * M.delta[j];
+                }
             }
-            v += scs;
         }
-        const int64_t row = lo + my_rl;
-        store_y(M.y, n * out + row, y_dtype, v + (M.bias ? M.bias[row] : 0.f));
+        for (int m = LPR >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+        if (live && my_q == 0) {
+            const int64_t row = lo + my_rl;
+            store_y(M.y, n * out + row, y_dtype, v + (M.bias ? M.bias[row] : 0.f));
+        }
     }
 }
 
