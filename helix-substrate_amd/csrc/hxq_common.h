@@ -172,4 +172,18 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     return v;                    // lane 63 holds the wave total
 }
 
+// A value the kernel only reads and that nothing writes during the launch,
+// loaded with a scalar load through the constant address space (the value
+// lands in scalar registers; the load counts in lgkmcnt only, so using it
+// waits for no vector-memory load).  The address must be wave-uniform.
+template <typename T>
+__device__ __forceinline__ T kload(const T &ref) {
+#if __HIP_DEVICE_COMPILE__
+    typedef __attribute__((address_space(4))) const T cT;
+    return *__builtin_bit_cast(const cT *, &ref);
+#else
+    return ref;  // the host pass only parses device functions
+#endif
+}
+
 }  // namespace hxq

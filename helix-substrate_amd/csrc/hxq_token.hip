@@ -100,20 +100,11 @@ struct Mat {
     int64_t out;
 };
 
-// Reads a value of the launch's tables (plan, layers), which the host
-// writes before the launch and nothing changes during it, with scalar loads
-// through the constant address space: the fields land in scalar registers,
-// and the loads count in lgkmcnt only -- no vector-memory wait (which would
-// also wait for the previous stage's output stores) precedes a stage.
-template <typename T>
-__device__ __forceinline__ T kload(const T &ref) {
-#if __HIP_DEVICE_COMPILE__
-    typedef __attribute__((address_space(4))) const T cT;
-    return *__builtin_bit_cast(const cT *, &ref);
-#else
-    return ref;  // the host pass only parses device functions
-#endif
-}
+// The launch's tables (plan, layers) are written by the host before the
+// launch and nothing changes them during it: they are read with kload
+// (hxq_common.h), scalar loads whose fields land in scalar registers and count
+// in lgkmcnt only -- no vector-memory wait (which would also wait for the
+// previous stage's output stores) precedes a stage.
 
 // A matrix descriptor read from the layer table into scalar registers.
 __device__ __forceinline__ Mat umat(const Mat &m) { return kload(m); }
