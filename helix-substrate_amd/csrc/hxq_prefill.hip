@@ -30,7 +30,8 @@
 //     affine is applied as fl(fl(c * scale) + offset) (two roundings, the
 //     reference's order), then v_cvt_pk_bf16_f32 / f16;
 //   * B of step s+1 is built while the MFMAs of step s run (substep by
-//     substep), global loads run two steps ahead, one barrier per step.
+//     substep), index loads run two steps ahead and X loads one, one barrier
+//     per step.
 // Sidecar: the entries of each group of 64 output rows are given sorted by
 // column, with a pointer per K step.  Per step a wave loads the 64 entries
 // from its group's pointer, one per lane; those of the step and of its rows
@@ -337,17 +338,21 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
         load_ptr(t + 2, buf);
     };
 
-    u32x4 xv[2][XP];   // X of steps s (buffer s & 1)
+    u32x4 xv[XP];      // X of the next step, on its way to LDS
     u32x4 qv[2][NQ * NJ]; // index bytes of row j: qv[.][NQ j .. NQ j + NQ)
     float2 av[2][NJ];     // {scale, offset} per j (weights 0..15 of the lane's 32)
     constexpr bool G16 = GM == 2;
     float2 av2[G16 ? 2 : 1][NJ];  // GM 2: ... of weights 16..31
-    auto load_step = [&](int s, int buf) {
+    auto load_x = [&](int s) {
         const bool live = s < nk;
         const uint32_t k0 = static_cast<uint32_t>((kb + (live ? s : 0)) * kBK);
 #pragma unroll
         for (int p = 0; p < XP; ++p)
-            xv[buf][p] = buf_load16(xr, (x_off[p] == kOob || !live) ? kOob : x_off[p] + k0 * XB);
+            xv[p] = buf_load16(xr, (x_off[p] == kOob || !live) ? kOob : x_off[p] + k0 * XB);
+    };
+    auto load_step = [&](int s, int buf) {
+        const bool live = s < nk;
+        const uint32_t k0 = static_cast<uint32_t>((kb + (live ? s : 0)) * kBK);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const uint32_t o = (q_off[j] == kOob || !live) ? kOob : q_off[j] + k0 / 32u * B32;
@@ -397,12 +402,12 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
             float *sA = sAf0 + buf * (BM * kBK) + x_lds;
 #pragma unroll
             for (int p = 0; p < XP; ++p)
-                *reinterpret_cast<u32x4 *>(sA + (kThreads / XCH) * p * kBK) = xv[buf][p];
+                *reinterpret_cast<u32x4 *>(sA + (kThreads / XCH) * p * kBK) = xv[p];
         } else {
             uint16_t *sA = sA0 + buf * (BM * kBK) + x_lds;
 #pragma unroll
             for (int p = 0; p < XP; ++p)
-                *reinterpret_cast<u32x4 *>(sA + (kThreads / XCH) * p * kBK) = xv[buf][p];
+                *reinterpret_cast<u32x4 *>(sA + (kThreads / XCH) * p * kBK) = xv[p];
         }
     };
 
@@ -650,13 +655,17 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     };
 
     // ---- pipeline ---------------------------------------------------------------
-    // loads two steps ahead; X of step s+1 goes to LDS during step s; B of step
-    // s+1 replaces B of step s substep by substep; one barrier per step.
+    // index, affine and sidecar loads two steps ahead; X one step ahead, its
+    // registers written to LDS at the end of the step before its use (16 fewer
+    // live registers than a second X buffer; X rows are mostly L2 hits); B of
+    // step s+1 replaces B of step s substep by substep; one barrier per step.
     load_ptr(0, 0);
     load_ptr(1, 1);
+    load_x(0);
     load_step(0, 0);
     load_step(1, 1);
     store_x(0);                 // waits for X(0)
+    load_x(1);
     __syncthreads();            // table and A(0) visible
     BV b;
     if constexpr (F32) {
@@ -670,17 +679,19 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
     load_step(2, 0);
     int ks = 0;
     for (; ks + 1 < nk; ks += 2) {
-        // step ks: A in LDS buffer 0, B(ks) in b; X(ks+1) and idx(ks+1) in buffer 1
-        store_x(1);
+        // step ks: A in LDS buffer 0, B(ks) in b, idx(ks+1) in buffer 1, X(ks+1) in xv
         mfma_step(0, 1, b);     // b <- B(ks+1)
         patch(ks + 1, 1, b);
         load_step(ks + 3, 1);
+        store_x(1);
+        load_x(ks + 2);
         lds_barrier();
-        // step ks + 1: A in buffer 1; X(ks+2) and idx(ks+2) in buffer 0
-        store_x(0);
+        // step ks + 1: A in buffer 1, idx(ks+2) in buffer 0, X(ks+2) in xv
         mfma_step(1, 0, b);     // b <- B(ks+2)
         patch(ks + 2, 0, b);
         load_step(ks + 4, 0);
+        store_x(0);
+        load_x(ks + 3);
         lds_barrier();
     }
     if (ks < nk) mfma_step(0, -1, b);  // odd step count: the last step (A in buffer 0)

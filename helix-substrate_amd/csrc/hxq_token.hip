@@ -1205,19 +1205,36 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         a0 = fmaf(p, __uint_as_float(vw[u] << 16), a0);
         a1 = fmaf(p, __uint_as_float(vw[u] & 0xffff0000u), a1);
     }
-    for (int t0 = wave + 8 * kWaves; t0 < pos; t0 += 8 * kWaves) {
+    // Positions [vbeg, vend) from the V rows staged in LDS, then [vend, pos)
+    // from memory, each in increasing order (the same accumulation order as
+    // one loop).  Two loops, so that no register of the LDS loop is also the
+    // target of a buffer load: otherwise the compiler waits vmcnt(0) before
+    // the LDS reads, which on this target also waits for the K/V stores above.
+    for (int t0 = wave + vbeg; t0 < vend; t0 += 8 * kWaves) {
+        uint32_t w[8];
+        float p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int tt = t0 + u * kWaves;
+            const bool ok = tt < vend;
+            w[u] = vst[(ok ? tt - vbeg : 0) * (D / 2) + lane];
+            p[u] = ok ? sc[tt] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a0 = fmaf(p[u], __uint_as_float(w[u] << 16), a0);
+            a1 = fmaf(p[u], __uint_as_float(w[u] & 0xffff0000u), a1);
+        }
+    }
+    for (int t0 = vend + ((wave - vend) % kWaves + kWaves) % kWaves; t0 < pos; t0 += 8 * kWaves) {
         uint32_t w[8];
         float p[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int tt = t0 + u * kWaves;
             const bool ok = tt < pos;
-            if (tt < vend) {
-                w[u] = vst[(tt - vbeg) * (D / 2) + lane];
-            } else {
-                w[u] = __builtin_amdgcn_raw_buffer_load_b32(
-                    vr, ok ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
-            }
+            w[u] = __builtin_amdgcn_raw_buffer_load_b32(
+                vr, ok ? static_cast<uint32_t>(tt * row * 2) + voff : kOob, 0, 0);
             p[u] = ok ? sc[tt] : 0.f;
         }
 #pragma unroll
