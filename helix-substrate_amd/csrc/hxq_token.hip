@@ -63,7 +63,7 @@ constexpr int kRps = 1028;                    // CSR row pointers per segment st
 constexpr int kHeadDim = 128;
 constexpr int kVStage = 3584;                  // float offset of attention's staged V rows in LDS
 constexpr int kMaxSeq = 1024;
-static_assert(kMaxSeq + 3 * kHeadDim + kWaves * kHeadDim + kWaves + 1 <= kVStage,
+static_assert(kMaxSeq + 3 * kHeadDim + kWaves * kHeadDim + 2 * kWaves + 1 <= kVStage,
               "attention scratch overlaps the staged V rows");
 constexpr int kLmRB = 1;                      // LM-head rows per load batch
 constexpr int kLmBuf = 2;                     // LM-head load batches in flight per wave
@@ -986,9 +986,10 @@ __device__ __forceinline__ void run_gemv(const Plan &P, const Geo &G, Pre &pf, c
 // ---------------------------------------------------------------------------
 // attention (one block per query head)
 // ---------------------------------------------------------------------------
+// Block-wide maximum / sum through red (kWaves floats that no wave reads
+// between the previous barrier and this call: one barrier per reduction).
 __device__ __forceinline__ float block_max(float v, float *red) {
     v = wave_max_all(v);
-    lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
     lds_barrier();
     float w[kWaves];
@@ -1001,7 +1002,6 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum_all(v);
-    lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / kWave] = v;
     lds_barrier();
     return sum16(red);
@@ -1045,24 +1045,35 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     float *kn = qs + D;                   // [D]
     float *vn = kn + D;                   // [D]
     float *part = vn + D;                 // [kWaves][D]
-    float *red = part + kWaves * D;       // [kWaves]
-    float *spos = red + kWaves;           // [1] score of position pos
+    float *red = part + kWaves * D;       // [kWaves] block maximum
+    float *red2 = red + kWaves;           // [kWaves] block sum
+    float *spos = red2 + kWaves;          // [1] score of position pos
     const int grp = P.n_heads / P.n_kv;
     const int kvh = h / grp;
     const int n = pos + 1;
-    const int t = threadIdx.x;
-    const int lane = t & 63, wave = t / kWave;
+    // ids redefined here, so that the compiler derives the per-position
+    // masks below in this stage instead of hoisting them out of the layer
+    // loop (masks kept live across the loop spill)
+    const int t = fresh_v(static_cast<int>(threadIdx.x));
+    const int lane = t & 63, wave = fresh_s(__builtin_amdgcn_readfirstlane(t / kWave));
     const int64_t row = static_cast<int64_t>(P.n_kv) * D;  // cache elements between positions
     const uint16_t *kc = kload(L.kc), *vcache = kload(L.vc);
     // earlier positions' cache rows
     const __amdgpu_buffer_rsrc_t kr = urs(kc, static_cast<int64_t>(P.max_seq) * row * 2);
     const __amdgpu_buffer_rsrc_t vr = urs(vcache, static_cast<int64_t>(P.max_seq) * row * 2);
-    u32x4 kw[D / 8];
+    // key rows: the four threads of quad t / 4 hold positions t / 4 + kThreads / 4 * k
+    // (k < 4), thread t % 4 a quarter of each row (dims 32 (t % 4) + 0..31)
+    constexpr int kQP = kThreads / 4;  // positions per quad round
+    u32x4 kw[kMaxSeq / kQP][4];
     {
-        const bool mine = t < pos;
-        const uint32_t base = static_cast<uint32_t>((t * row + static_cast<int64_t>(kvh) * D) * 2);
+        const int qd = t & 3;
 #pragma unroll
-        for (int c = 0; c < D / 8; ++c) kw[c] = buf_load16(kr, mine ? base + 16u * c : kOob);
+        for (int k = 0; k < kMaxSeq / kQP; ++k) {
+            const int pk = (t >> 2) + kQP * k;
+            const uint32_t base = static_cast<uint32_t>((pk * row + static_cast<int64_t>(kvh) * D + 32 * qd) * 2);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kw[k][c] = buf_load16(kr, pk < pos ? base + 16u * c : kOob);
+        }
     }
     uint32_t vw[8];
     const uint32_t voff = static_cast<uint32_t>((static_cast<int64_t>(kvh) * D + 2 * lane) * 2);
@@ -1161,32 +1172,43 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
     }
     lds_barrier();  // LDS only: the cache stores are read by later launches
     float mx = -FLT_MAX;
-    if (t < n) {  // n <= max_seq <= kThreads: one position per thread
-        float s0 = 0.f, s1 = 0.f;
-        if (t == pos) {
-            s0 = *spos;
-        } else {
-            // q (the same for every lane) is read 16 values at a time, four
-            // 16-byte LDS reads in flight per round
+    {
+        // scores: each quad sums its position's four quarter dot products
+        // (two quad DPP adds); q's quarter is read 16 values at a time, four
+        // 16-byte LDS reads in flight per round
+        const int qd = t & 3;
+        const float sp = *spos;
 #pragma unroll
-            for (int c0 = 0; c0 < D / 8; c0 += 2) {
-                float4 qv[4];
+        for (int k = 0; k < kMaxSeq / kQP; ++k) {
+            if (kQP * k < n) {  // block-uniform
+                const int pk = (t >> 2) + kQP * k;
+                float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) qv[i] = reinterpret_cast<const float4 *>(qs)[2 * c0 + i];
+                for (int c0 = 0; c0 < 4; c0 += 2) {
+                    float4 qv[4];
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const float q8[8] = {qv[2 * c].x, qv[2 * c].y, qv[2 * c].z, qv[2 * c].w,
-                                         qv[2 * c + 1].x, qv[2 * c + 1].y, qv[2 * c + 1].z, qv[2 * c + 1].w};
+                    for (int i = 0; i < 4; ++i) qv[i] = reinterpret_cast<const float4 *>(qs)[8 * qd + 2 * c0 + i];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        s0 = fmaf(q8[2 * e], __uint_as_float(kw[c0 + c][e] << 16), s0);
-                        s1 = fmaf(q8[2 * e + 1], __uint_as_float(kw[c0 + c][e] & 0xffff0000u), s1);
+                    for (int c = 0; c < 2; ++c) {
+                        const float q8[8] = {qv[2 * c].x, qv[2 * c].y, qv[2 * c].z, qv[2 * c].w,
+                                             qv[2 * c + 1].x, qv[2 * c + 1].y, qv[2 * c + 1].z, qv[2 * c + 1].w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            s0 = fmaf(q8[2 * e], __uint_as_float(kw[k][c0 + c][e] << 16), s0);
+                            s1 = fmaf(q8[2 * e + 1], __uint_as_float(kw[k][c0 + c][e] & 0xffff0000u), s1);
+                        }
                     }
+                }
+                float sq = s0 + s1;
+                sq += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sq), 0xb1, 0xf, 0xf, false));
+                sq += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sq), 0x4e, 0xf, 0xf, false));
+                if (pk == pos) sq = sp;
+                if (pk < n) {
+                    if (qd == 0) sc[pk] = sq;
+                    mx = fmaxf(mx, sq);
                 }
             }
         }
-        sc[t] = s0 + s1;
-        mx = s0 + s1;
     }
     mx = block_max(mx, red);
     float sum = 0.f;
@@ -1195,7 +1217,7 @@ __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const u
         sc[t] = p;
         sum = p;
     }
-    sum = block_sum(sum, red);
+    sum = block_sum(sum, red2);
     const float inv = 1.f / sum;
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
