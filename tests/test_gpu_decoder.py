@@ -218,17 +218,19 @@ def test_persistent_rejects_position_out_of_range(dev):
     assert int(b.pos.item()) == 1
 
 
-@pytest.mark.parametrize("hidden", [512, 2048, 3584])
-def test_persistent_long_context_matches_launch_sequence(dev, hidden):
-    """Teacher-forced decode to position ~680: the persistent kernel's attention
-    preloads the first 128 value rows into registers, stages the next ones in
-    LDS (buffer-to-LDS loads) and reads the rest from memory; every range is
+@pytest.mark.parametrize("hidden,max_seq", [(512, 704), (2048, 704), (3584, 704), (512, 1024)])
+def test_persistent_long_context_matches_launch_sequence(dev, hidden, max_seq):
+    """Teacher-forced decode to position ~690 and, at hidden 512, to the
+    1024-position maximum: the persistent kernel's attention takes key rows
+    256 positions per quad round (four rounds at the maximum), preloads the
+    first 128 value rows into registers, stages the next ones in LDS
+    (buffer-to-LDS loads) and reads the rest from memory; every range is
     crossed here.  Logits against the per-kernel launch sequence (5e-3 of
     max|logit|) at sampled positions, and the KV caches written by both."""
     global CFG
     cfg = DecoderConfig(hidden=hidden, n_layers=2, n_heads=hidden // 128, n_kv_heads=2,
                         head_dim=128, intermediate=768, vocab=1000, rope_theta=1e6,
-                        rms_eps=1e-6, max_seq=704)
+                        rms_eps=1e-6, max_seq=max_seq)
     saved, CFG = CFG, cfg
     try:
         mk = lambda o, i, s: synth.make_layer_np(o, i, seed=s, group_size=64)
@@ -236,8 +238,10 @@ def test_persistent_long_context_matches_launch_sequence(dev, hidden):
         b = HelixDecoder.synthetic(cfg, seed=6, device=dev, layer_fn=mk)
         b.persistent_init()
         rng = np.random.default_rng(7)
-        prompt = rng.integers(0, cfg.vocab, 690).tolist()
-        checks = {0, 1, 127, 128, 129, 200, 400, 600, 640, 689}
+        n_tok = max_seq - 14
+        prompt = rng.integers(0, cfg.vocab, n_tok).tolist()
+        checks = {t for t in (0, 1, 127, 128, 129, 200, 255, 256, 400, 511, 512, 600, 640, 767, 768,
+                              900, n_tok - 1) if t < n_tok}
         # the fp64 oracle of the same math at the bf16 bar (hidden 512: cheap in numpy)
         ref = _oracle_logits(a, prompt) if hidden == 512 else None
         print(f"long context hidden={hidden} tokens={len(prompt)}", flush=True)
