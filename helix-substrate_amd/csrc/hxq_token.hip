@@ -1028,14 +1028,16 @@ __device__ __forceinline__ void rope_table(const Plan &P, int pos, float2 *tab) 
 
 // One block per query head: softmax(q . k_t * D^-1/2, t <= pos) . v_t over
 // the head's KV group (head h reads kv head h / (n_heads / n_kv)).
-//   The cache rows of earlier positions do not depend on this token: each
-//   thread's key row (position = thread) and each wave's first eight value
-//   rows are loaded BEFORE waiting for the q/k/v producers (`wait`), so they
-//   arrive while the block waits.  Then q and the new key are rotated
-//   (angle table in LDS), the new key/value are stored into the caches by
-//   the first head of each group, scores are one position per thread,
-//   softmax by block reductions, and the output is summed by wave over
-//   positions (lane = 2 dims) and across waves in LDS.
+//   The cache rows of earlier positions do not depend on this token: the
+//   key rows (quad t / 4 holds positions t / 4 + 256 k, each thread a
+//   32-dim quarter) and each wave's first eight value rows are loaded BEFORE
+//   waiting for the q/k/v producers, so they arrive while the block waits;
+//   later value rows go to LDS by buffer-to-LDS loads.  Then q and the new
+//   key are rotated (angle table in LDS), the new key/value are stored into
+//   the caches by the first head of each group, scores are one position per
+//   quad (two quad DPP adds), softmax by block reductions (one barrier
+//   each), and the output is summed by wave over positions (lane = 2 dims)
+//   and across waves in LDS.
 __device__ __forceinline__ bool attention(const Plan &P, const Layer &L, const uint32_t *qkv, uint32_t eq,
                           uint32_t *attn, uint32_t ea, int h,
                           int pos, float *smem, const float2 *rope) {
