@@ -122,13 +122,6 @@ __device__ __forceinline__ int32_t buf_loadi(__amdgpu_buffer_rsrc_t r, uint32_t 
     return static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
-// Full wave64 sum; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-    return v;
-}
-
 typedef __attribute__((address_space(3))) const float lds_cfloat;
 
 // LDS byte address of a pointer into LDS.
@@ -171,6 +164,33 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
     return v;                    // lane 63 holds the wave total
 }
+
+// Sum over each aligned group of L lanes (L a power of two <= 64); every lane
+// of a group ends with the group's total.  Lane distance 1 and 2 (quad
+// permutes), 4 (row_half_mirror: the quads hold equal sums by then, so the
+// mirrored lane of the other quad stands for lane ^ 4), 8 (row_ror:8), 16 and
+// 32 (v_permlane16_swap / v_permlane32_swap of the value with itself: the two
+// results are the lane's value and that of lane ^ 16 / ^ 32).  Fixed order,
+// deterministic, and no LDS round trip (an xor shuffle is an LDS permute).
+// Every lane of the wave must be active.
+__device__ __forceinline__ float lane_group_sum(float v, int L) {
+    if (L > 1) v = dpp_add<0xb1, 0xf>(v);
+    if (L > 2) v = dpp_add<0x4e, 0xf>(v);
+    if (L > 4) v = dpp_add<0x141, 0xf>(v);
+    if (L > 8) v = dpp_add<0x128, 0xf>(v);
+    if (L > 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if (L > 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return v;
+}
+
+// Full wave64 sum; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) { return lane_group_sum(v, kWave); }
 
 // A value the kernel only reads and that nothing writes during the launch,
 // loaded with a scalar load through the constant address space (the value

@@ -30,7 +30,8 @@
 //   * row partials go to LDS; the sidecar products x[col] * delta of the
 //     block's entries go to LDS during the stream; a final pass with up to 64
 //     lanes per output row adds slices, sidecar entries and bias, the row's
-//     lanes reducing in a fixed xor order (deterministic, no atomics).
+//     lanes reducing in a fixed order by DPP and lane swaps (deterministic,
+//     no atomics, no LDS round trips).
 #include <algorithm>
 
 #include "hxq_common.h"
@@ -183,7 +184,7 @@ constexpr int kEntCap = 512;  // sidecar entries per block staged in LDS
 //   epilogue  LPR lanes per output row (the largest power of two <= 64 that
 //             fits the block's rows in one pass): lane q adds slices q, q+LPR,
 //             ... and sidecar entries j0+q, j0+q+LPR, ... (CSR order), then
-//             the lanes reduce by xor shuffles; bias, store.  Fixed summation
+//             the lanes reduce by DPP and lane swaps; bias, store.  Fixed summation
 //             order: deterministic.  (One thread per row with a serial loop
 //             over the row's entries cost 1.3 us on the config-1 down launch.)
 // Barriers order LDS only (lds_barrier), so prefetched loads stay in flight.
@@ -619,7 +620,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
     {
         // lane q of an item adds slices q, q + LPR, ... and sidecar entries
         // j0 + q, j0 + q + LPR, ...; the item's lanes then reduce in a fixed
-        // xor order (deterministic)
+        // order by DPP and lane swaps (deterministic, no LDS round trips)
         const bool live = my_item < n_rows * NX;
         const int n = my_item % NX;
         float v = 0.f;
@@ -632,7 +633,7 @@ __global__ __launch_bounds__(WAVES * kWave, CPS == 4 ? 2 : 4) void gemv_kernel(
                 }
             }
         }
-        for (int m = LPR >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+        v = lane_group_sum(v, LPR);
         if (live && my_q == 0) {
             const int64_t row = lo + my_rl;
             store_y(M.y, n * out + row, y_dtype, v + (M.bias ? M.bias[row] : 0.f));

@@ -794,12 +794,7 @@ __device__ __forceinline__ float row_part(const Mat &M, int r, int q, int L, int
 
 // Sum over the aligned group of L lanes (L a power of two up to 16), in a
 // fixed order: every lane of the wave takes part.
-__device__ __forceinline__ float group_sum(float v, int L) {
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1)
-        if (m < L) v += __shfl_xor(v, m, kWave);
-    return v;
-}
+__device__ __forceinline__ float group_sum(float v, int L) { return lane_group_sum(v, L); }
 
 struct NoNext {
     __device__ void operator()() const {}
