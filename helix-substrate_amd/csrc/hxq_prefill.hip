@@ -118,20 +118,23 @@ __device__ __forceinline__ bool grouped_tile(const Args &g, int bm, int rt, int 
         const int a = ee < g.n_exp ? g.seg[ee] : 0;
         const int b = ee < g.n_exp ? g.seg[ee + 1] : 0;
         const int nt = (b - a + bm - 1) / bm;
+        // inclusive scan of nt over the wave by DPP (row_shr 1, 2, 4, 8 within
+        // rows, then row_bcast:15 / :31 across them): no LDS round trips
         int inc = nt;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int v = __shfl_up(inc, d);
-            if (lane >= d) inc += v;
-        }
-        const int tot = __shfl(inc, 63);
+        inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xf, 0xf, false);
+        inc += __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xf, 0xf, false);
+        inc += __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xf, 0xf, false);
+        inc += __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xf, 0xf, false);
+        inc += __builtin_amdgcn_update_dpp(0, inc, 0x142, 0xa, 0xf, false);
+        inc += __builtin_amdgcn_update_dpp(0, inc, 0x143, 0xc, 0xf, false);
+        const int tot = __builtin_amdgcn_readlane(inc, 63);
         if (rt < base + tot) {
             const unsigned long long m = __ballot(base + inc > rt);
-            const int L = __builtin_ctzll(m);
+            const int L = __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
             // wave-uniform results, in scalar registers (they form buffer bases)
-            e = __builtin_amdgcn_readfirstlane(c0 + L);
-            row0 = __builtin_amdgcn_readfirstlane(__shfl(a, L) + (rt - base - __shfl(inc - nt, L)) * bm);
-            rend = __builtin_amdgcn_readfirstlane(__shfl(b, L));
+            e = c0 + L;
+            row0 = __builtin_amdgcn_readlane(a, L) + (rt - base - __builtin_amdgcn_readlane(inc - nt, L)) * bm;
+            rend = __builtin_amdgcn_readlane(b, L);
             return true;
         }
         base += tot;
