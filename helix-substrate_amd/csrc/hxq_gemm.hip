@@ -777,24 +777,31 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64
 // as the projections' outputs are), rounded to x's 16-bit type: the SwiGLU
 // product of the paired gate/up grouped launch.
 template <bool BF16>
+// 8 values per thread, 16-byte accesses (inter % 8 == 0, rows * inter < 2^31:
+// the host checks both); silu(g) = g * rcp(1 + exp(-g)) (hardware exp and
+// reciprocal, ~1 ulp each: far inside the 16-bit rounding of the result)
 __global__ __launch_bounds__(256) void moe_silu_mul_kernel(const uint16_t *__restrict__ gu, int64_t rows,
                                                           int32_t inter, uint16_t *__restrict__ h) {
-    const int64_t n = rows * inter;
+    const int32_t cpr = inter >> 3;
+    const int32_t n = static_cast<int32_t>(rows) * cpr;
     auto f = [](uint32_t b) { return BF16 ? bf16_to_f32(static_cast<uint16_t>(b)) : f16_to_f32(static_cast<uint16_t>(b)); };
-    for (int64_t i = (int64_t{blockIdx.x} * 256 + threadIdx.x) * 4; i < n; i += int64_t{gridDim.x} * 1024) {
-        const int64_t r = i / inter;
-        const int32_t c = static_cast<int32_t>(i - r * inter);
-        const uint2 g = *reinterpret_cast<const uint2 *>(gu + r * 2 * inter + c);
-        const uint2 u = *reinterpret_cast<const uint2 *>(gu + r * 2 * inter + inter + c);
-        const float gv[4] = {f(g.x & 0xffffu), f(g.x >> 16), f(g.y & 0xffffu), f(g.y >> 16)};
-        const float uv[4] = {f(u.x & 0xffffu), f(u.x >> 16), f(u.y & 0xffffu), f(u.y >> 16)};
-        uint16_t o[4];
+    auto silu_mul = [&](uint32_t g16, uint32_t u16) -> uint32_t {
+        const float gv = f(g16);
+        const float v = gv * __builtin_amdgcn_rcpf(1.f + __expf(-gv)) * f(u16);
+        return BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+    };
+    for (int32_t i = static_cast<int32_t>(blockIdx.x * 256 + threadIdx.x); i < n;
+         i += static_cast<int32_t>(gridDim.x * 256)) {
+        const int32_t r = i / cpr;
+        const int32_t c = (i - r * cpr) * 8;
+        const uint4 g = *reinterpret_cast<const uint4 *>(gu + static_cast<int64_t>(r) * 2 * inter + c);
+        const uint4 u = *reinterpret_cast<const uint4 *>(gu + static_cast<int64_t>(r) * 2 * inter + inter + c);
+        const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+        uint32_t o[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float v = gv[k] / (1.f + expf(-gv[k])) * uv[k];
-            o[k] = BF16 ? f32_to_bf16(v) : f32_to_f16(v);
-        }
-        *reinterpret_cast<uint2 *>(h + i) = make_uint2(o[0] | (uint32_t{o[1]} << 16), o[2] | (uint32_t{o[3]} << 16));
+        for (int k = 0; k < 4; ++k)
+            o[k] = silu_mul(gw[k] & 0xffffu, uw[k] & 0xffffu) | (silu_mul(gw[k] >> 16, uw[k] >> 16) << 16);
+        *reinterpret_cast<uint4 *>(h + static_cast<int64_t>(r) * inter + c) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 // fp32 activations: h = silu(g) * u in fp32, [rows, 2 * inter] -> [rows, inter]
@@ -811,9 +818,10 @@ __global__ __launch_bounds__(256) void moe_silu_mul_f32_kernel(const float *__re
     }
 }
 // V consecutive columns per thread (V = 4 when hidden % 4 == 0: 16-byte
-// loads of O); each column's slots are added in order either way.
-template <int YDT, int V>
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const float *wts,
+// loads of fp32 O, 8-byte loads of 16-bit O); each column's slots are added
+// in order, in fp32, either way.
+template <int OT, int YDT, int V>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const void *Ov, const float *wts,
                                                           const int32_t *pos, int32_t k,
                                                           int32_t hidden, void *y) {
     const int t = blockIdx.y;
@@ -825,15 +833,32 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *O, const 
     for (int s = 0; s < k; ++s) {
         const int64_t a = (int64_t)t * k + s;
         const float w = wts[a];
-        const float *o = O + (int64_t)pos[a] * hidden + c;
-        if constexpr (V == 4) {
-            const float4 f = *reinterpret_cast<const float4 *>(o);
-            acc[0] = fmaf(w, f.x, acc[0]);
-            acc[1] = fmaf(w, f.y, acc[1]);
-            acc[2] = fmaf(w, f.z, acc[2]);
-            acc[3] = fmaf(w, f.w, acc[3]);
+        const int64_t oi = (int64_t)pos[a] * hidden + c;
+        if constexpr (OT == HXQ_F32) {
+            const float *o = static_cast<const float *>(Ov) + oi;
+            if constexpr (V == 4) {
+                const float4 f = *reinterpret_cast<const float4 *>(o);
+                acc[0] = fmaf(w, f.x, acc[0]);
+                acc[1] = fmaf(w, f.y, acc[1]);
+                acc[2] = fmaf(w, f.z, acc[2]);
+                acc[3] = fmaf(w, f.w, acc[3]);
+            } else {
+                acc[0] = fmaf(w, o[0], acc[0]);
+            }
         } else {
-            acc[0] = fmaf(w, o[0], acc[0]);
+            const uint16_t *o = static_cast<const uint16_t *>(Ov) + oi;
+            auto f = [](uint32_t b) {
+                return OT == HXQ_BF16 ? bf16_to_f32(static_cast<uint16_t>(b)) : f16_to_f32(static_cast<uint16_t>(b));
+            };
+            if constexpr (V == 4) {
+                const uint2 q = *reinterpret_cast<const uint2 *>(o);
+                acc[0] = fmaf(w, f(q.x & 0xffffu), acc[0]);
+                acc[1] = fmaf(w, f(q.x >> 16), acc[1]);
+                acc[2] = fmaf(w, f(q.y & 0xffffu), acc[2]);
+                acc[3] = fmaf(w, f(q.y >> 16), acc[3]);
+            } else {
+                acc[0] = fmaf(w, f(o[0]), acc[0]);
+            }
         }
     }
 #pragma unroll
@@ -1240,6 +1265,9 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     const bool reg = pg::grouped_ok(gate, intermediate, hidden, group_size) &&
                      pg::grouped_ok(up, intermediate, hidden, group_size) &&
                      pg::grouped_ok(down, hidden, intermediate, group_size) && intermediate % 256 == 0;
+    // expert outputs O: x's 16-bit type on the register-dequant path (the
+    // reference's experts return x's type too), fp32 otherwise
+    const int32_t o_dt = reg && !f32 ? x_dtype : HXQ_F32;
     HXQ_REQUIRE(reg || !f32, "fp32 activations need the register-dequant grouped kernel "
                              "(uint8 indices, group_size a multiple of 64, intermediate a multiple of 256)");
     if (reg) {
@@ -1261,7 +1289,7 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
         r.y = GU;
         r.y_dtype = x_dtype;
         if (int rc = pg::grouped_gemm(r, stream)) return rc;
-        const int64_t n4 = na * intermediate / 4;
+        const int64_t n4 = na * intermediate / (f32 ? 4 : 8);  // values per thread: 4 (fp32), 8
         const dim3 sg(static_cast<uint32_t>(std::min<int64_t>((n4 + 255) / 256, 4096)));
         if (f32)
             hipLaunchKernelGGL(moe_silu_mul_f32_kernel, sg, dim3(256), 0, stream,
@@ -1274,7 +1302,7 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
             hipLaunchKernelGGL(moe_silu_mul_kernel<false>, sg, dim3(256), 0, stream, GU, na,
                                static_cast<int32_t>(intermediate), H);
         HXQ_LAUNCH_CHECK();
-        // 2) O = H_e Wd_e^T (fp32, sorted order)
+        // 2) O = H_e Wd_e^T (sorted order; x's type: the combine sums in fp32)
         pg::GroupedReq d{};
         d.x = H;
         d.x_dtype = x_dtype;
@@ -1288,7 +1316,7 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
         d.in = intermediate;
         d.group = group_size;
         d.y = O;
-        d.y_dtype = HXQ_F32;
+        d.y_dtype = o_dt;
         if (int rc = pg::grouped_gemm(d, stream)) return rc;
     }
     if (!reg) {
@@ -1328,18 +1356,25 @@ extern "C" int hxq_moe_ffn(const void *x, int32_t x_dtype, int64_t n_tokens, int
     // 3) y[t] = sum_s w[t,s] O[pos(t,s)]
     const bool v4 = hidden % 4 == 0;
     const dim3 grid((hidden + (v4 ? 1023 : 255)) / (v4 ? 1024 : 256), n_tokens);
-#define HXQ_COMBINE(YDT)                                                                     \
+#define HXQ_COMBINE(OT, YDT)                                                                 \
     do {                                                                                      \
         if (v4)                                                                               \
-            hipLaunchKernelGGL((moe_combine_kernel<YDT, 4>), grid, dim3(256), 0, stream, O,   \
+            hipLaunchKernelGGL((moe_combine_kernel<OT, YDT, 4>), grid, dim3(256), 0, stream, O, \
                                topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y); \
         else                                                                                  \
-            hipLaunchKernelGGL((moe_combine_kernel<YDT, 1>), grid, dim3(256), 0, stream, O,   \
+            hipLaunchKernelGGL((moe_combine_kernel<OT, YDT, 1>), grid, dim3(256), 0, stream, O, \
                                topk_weights, assign_pos, top_k, static_cast<int32_t>(hidden), y); \
     } while (0)
-    if (y_dtype == HXQ_F32) HXQ_COMBINE(HXQ_F32);
-    else if (y_dtype == HXQ_BF16) HXQ_COMBINE(HXQ_BF16);
-    else HXQ_COMBINE(HXQ_F16);
+#define HXQ_COMBINE_Y(OT)                                                                    \
+    do {                                                                                      \
+        if (y_dtype == HXQ_F32) HXQ_COMBINE(OT, HXQ_F32);                                     \
+        else if (y_dtype == HXQ_BF16) HXQ_COMBINE(OT, HXQ_BF16);                              \
+        else HXQ_COMBINE(OT, HXQ_F16);                                                        \
+    } while (0)
+    if (o_dt == HXQ_F32) HXQ_COMBINE_Y(HXQ_F32);
+    else if (o_dt == HXQ_BF16) HXQ_COMBINE_Y(HXQ_BF16);
+    else HXQ_COMBINE_Y(HXQ_F16);
+#undef HXQ_COMBINE_Y
 #undef HXQ_COMBINE
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
