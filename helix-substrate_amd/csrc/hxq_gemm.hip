@@ -696,23 +696,25 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *logits, int3
     }
 }
 
-// Count (PLACE = false) or place (PLACE = true) the assignments of expert
-// blockIdx.x.  4 waves split the assignment list into contiguous quarters;
+// Count and place the assignments of expert blockIdx.x (its offset is the
+// number of assignments to lower experts, counted in the same pass over the
+// list).  4 waves split the assignment list into contiguous quarters;
 // positions follow assignment order (token-major), so they are deterministic.
 // A wave reads its quarter kSortU rounds of 64 ids at a time, all requested
 // before the first is used (one round trip per 512 ids, not per 64).
 constexpr int kSortU = 8;
-template <bool PLACE>
 __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64_t n_assign,
                                                        int32_t E, int32_t k, int32_t *counts,
                                                        int32_t *offsets, int32_t *sorted_rows,
                                                        int32_t *assign_pos) {
-    __shared__ int wsum[4];
+    __shared__ int wsum[4], psum[4];
     const int e = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t per = ((n_assign + 255) / 256) * 64;  // multiple of 64
     const int64_t a0 = wave * per, a1 = min(a0 + per, n_assign);
-    int cnt = 0;
+    // one pass counts this expert's assignments and those of lower experts
+    // (the expert's global offset), so no second launch waits for all counts
+    int cnt = 0, lt = 0;
     for (int64_t a = a0; a < a1; a += 64 * kSortU) {
         int v[kSortU];
 #pragma unroll
@@ -721,32 +723,25 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int32_t *ids, int64
             v[u] = ids[aa < a1 ? aa : a0];  // in range: a0 < a1 here
         }
 #pragma unroll
-        for (int u = 0; u < kSortU; ++u)
-            cnt += __popcll(__ballot(a + 64 * u + lane < a1 && v[u] == e));
+        for (int u = 0; u < kSortU; ++u) {
+            const bool in = a + 64 * u + lane < a1;
+            cnt += __popcll(__ballot(in && v[u] == e));
+            lt += __popcll(__ballot(in && v[u] < e));
+        }
     }
-    if (!PLACE) {
-        if (lane == 0) wsum[wave] = cnt;
-        __syncthreads();
-        if (threadIdx.x == 0) counts[e] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-        return;
-    }
-    // global offset of this expert: sum of counts of experts before it
-    int pre = 0;
-    for (int i = threadIdx.x; i < e; i += 256) pre += counts[i];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) pre += __shfl_xor(pre, m, kWave);
-    __shared__ int psum[4];
     if (lane == 0) {
-        psum[wave] = pre;
+        psum[wave] = lt;
         wsum[wave] = cnt;
     }
     __syncthreads();
     const int off = psum[0] + psum[1] + psum[2] + psum[3];
+    const int tot = wsum[0] + wsum[1] + wsum[2] + wsum[3];
     int base = off;
     for (int w = 0; w < wave; ++w) base += wsum[w];
     if (threadIdx.x == 0) {
+        counts[e] = tot;
         offsets[e] = off;
-        if (e == E - 1) offsets[E] = off + wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        if (e == E - 1) offsets[E] = off + tot;
     }
     const unsigned long long below = (1ull << lane) - 1ull;
     for (int64_t a = a0; a < a1; a += 64 * kSortU) {
@@ -1152,13 +1147,8 @@ extern "C" int hxq_moe_route(const float *logits, int64_t n_tokens, int32_t n_ex
                        logits, static_cast<int32_t>(n_tokens), n_experts, top_k, renormalize,
                        topk_ids, topk_weights);
     HXQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(moe_sort_kernel<false>, dim3(n_experts), dim3(256), 0, stream, topk_ids,
-                       n_assign, n_experts, top_k, expert_counts, expert_offsets, sorted_rows,
-                       assign_pos);
-    HXQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(moe_sort_kernel<true>, dim3(n_experts), dim3(256), 0, stream, topk_ids,
-                       n_assign, n_experts, top_k, expert_counts, expert_offsets, sorted_rows,
-                       assign_pos);
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(n_experts), dim3(256), 0, stream, topk_ids, n_assign,
+                       n_experts, top_k, expert_counts, expert_offsets, sorted_rows, assign_pos);
     HXQ_LAUNCH_CHECK();
     return HXQ_OK;
 }
