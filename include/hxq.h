@@ -387,13 +387,15 @@ int hxq_moe_grouped_gemm(const void *x, int32_t x_dtype, int64_t x_rows,
 /*
  * Whole SwiGLU MoE FFN from a routing (hxq_moe_route):
  *   H = silu(X Wg_e^T) * (X Wu_e^T)   (x's dtype)
- *   O = H Wd_e^T                       (fp32, sorted order)
+ *   O = H Wd_e^T                       (sorted order; x's dtype with register-dequant
+ *                                       banks, as the reference's experts return it,
+ *                                       else fp32)
  * With register-dequant banks (sc_grp_*, see hxq_expert_bank) gate and up
  * run as one grouped launch into [n_assign, 2 * intermediate] in x's dtype
  * (each projection's output rounded like the module's; the workspace holds
  * it), then the SiLU product; otherwise one LDS-dequant launch with the
  * SiLU-product epilogue on the fp32 sums.
- *   y[t] = sum_s topk_weights[t, s] * O[assign_pos[t*top_k + s]]  (slots in order)
+ *   y[t] = sum_s topk_weights[t, s] * O[assign_pos[t*top_k + s]]  (slots in order, fp32 sum)
  * x bf16/fp16 [n_tokens, hidden], or fp32 (fp32 MFMA on the exact fp32 W,
  * fp32 H; register-dequant banks only); y y_dtype [n_tokens, hidden].  `workspace`
  * (device, 256-B aligned, >= hxq_moe_ffn_workspace_bytes) holds H, O and the
