@@ -16,6 +16,7 @@
 namespace hxq {
 
 constexpr int kConvT = 16;       // time steps per prefill conv block
+constexpr int kConvTB = 4;       // time steps whose inputs one round requests together
 constexpr int kMaxConvW = 8;     // supported conv widths 1..8
 
 struct ConvArgs {
@@ -174,33 +175,50 @@ __global__ __launch_bounds__(256) void conv_split_vec_kernel(const ConvArgs a) {
     else if (c0 < a.d_inner + a.gn) { dst = static_cast<uint16_t *>(a.B); dstride = a.gn; doff = c0 - a.d_inner; }
     else { dst = static_cast<uint16_t *>(a.C); dstride = a.gn; doff = c0 - a.d_inner - a.gn; }
     const bool obf = a.out_dt == HXQ_BF16;
-    for (int t = t0; t < t1; ++t) {
-        float cur[8];
-        load8(t, cur);
-        uint32_t o[4];
+    // kConvTB time steps per round: their inputs are all requested before the
+    // first is used (one memory round trip per round, not per step)
+    for (int tb = t0; tb < t1; tb += kConvTB) {
+        u32x4 qin[kConvTB];
 #pragma unroll
-        for (int j2 = 0; j2 < 4; ++j2) {
-            float r[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int j = 2 * j2 + e;
-                float acc = bias[j];
-#pragma unroll
-                for (int k = 0; k < W - 1; ++k) acc = fmaf(w[j][k], win[k][j], acc);
-                acc = fmaf(w[j][W - 1], cur[j], acc);
-                r[e] = silu(acc);
-            }
-            o[j2] = obf ? (uint32_t(f32_to_bf16(r[0])) | (uint32_t(f32_to_bf16(r[1])) << 16))
-                        : (uint32_t(f32_to_f16(r[0])) | (uint32_t(f32_to_f16(r[1])) << 16));
+        for (int i = 0; i < kConvTB; ++i) {
+            const int t = min(tb + i, t1 - 1);  // past t1: a repeat of a loaded row, unused
+            qin[i] = *reinterpret_cast<const u32x4 *>(proj + (row0 + t) * a.proj_width + a.xbc_off + c0);
         }
-        *reinterpret_cast<u32x4 *>(dst + (row0 + t) * dstride + doff) = u32x4{o[0], o[1], o[2], o[3]};
 #pragma unroll
-        for (int k = 0; k + 1 < W - 1; ++k)
+        for (int i = 0; i < kConvTB; ++i) {
+            const int t = tb + i;
+            if (t >= t1) break;
+            float cur[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) win[k][j] = win[k + 1][j];
-        if constexpr (W > 1) {
+            for (int j = 0; j < 8; ++j) {
+                const uint16_t h = static_cast<uint16_t>(qin[i][j >> 1] >> (16 * (j & 1)));
+                cur[j] = BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+            }
+            uint32_t o[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) win[W - 2][j] = cur[j];
+            for (int j2 = 0; j2 < 4; ++j2) {
+                float r[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int j = 2 * j2 + e;
+                    float acc = bias[j];
+#pragma unroll
+                    for (int k = 0; k < W - 1; ++k) acc = fmaf(w[j][k], win[k][j], acc);
+                    acc = fmaf(w[j][W - 1], cur[j], acc);
+                    r[e] = silu(acc);
+                }
+                o[j2] = obf ? (uint32_t(f32_to_bf16(r[0])) | (uint32_t(f32_to_bf16(r[1])) << 16))
+                            : (uint32_t(f32_to_f16(r[0])) | (uint32_t(f32_to_f16(r[1])) << 16));
+            }
+            *reinterpret_cast<u32x4 *>(dst + (row0 + t) * dstride + doff) = u32x4{o[0], o[1], o[2], o[3]};
+#pragma unroll
+            for (int k = 0; k + 1 < W - 1; ++k)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) win[k][j] = win[k + 1][j];
+            if constexpr (W > 1) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) win[W - 2][j] = cur[j];
+            }
         }
     }
     // conv_state after the last step: the last W raw inputs (zero before t=0)
