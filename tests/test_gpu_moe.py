@@ -138,6 +138,31 @@ def test_moe_ffn_matches_oracle(dev, T, E, k, H, I, renorm):
     assert torch.equal(y32, _hxq.moe_ffn(x.to(dev), r, bg, bu, bd, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_moe_ffn_16bit_expert_outputs(dev, dt):
+    """The register-dequant path (intermediate a multiple of 256) keeps the
+    expert outputs in x's 16-bit type and sums each token's slots in fp32:
+    fp16 and bf16 x, outputs in x's type and fp32, against the fp64 oracle at
+    the 16-bit bar."""
+    T, E, k, H, I = 96, 8, 2, 256, 256
+    g, bg = _bank(E, I, H, seed=120, dev=dev, group_size=64)
+    u, bu = _bank(E, I, H, seed=220, dev=dev, group_size=64)
+    d, bd = _bank(E, H, I, seed=320, dev=dev, group_size=64)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(8)).to(dt)
+    lg = _skewed_logits(T, E, 11, dev)
+    m = moe.HelixMoeExperts(bg, bu, bd, top_k=k)
+    y = m(x.to(dev), lg)
+    assert m._last_dispatch_path == "hip_moe" and y.dtype == dt
+    ids, w = oracle.moe_route_np(lg.cpu().numpy(), k, False)
+    ref = oracle.moe_ffn_np(x.float().numpy(), ids, w, [oracle.reconstruct(**L) for L in g],
+                            [oracle.reconstruct(**L) for L in u],
+                            [oracle.reconstruct(**L) for L in d])
+    assert _maxrel(y.float().cpu().numpy(), ref) <= 2e-2
+    r = _hxq.moe_route(lg, k, False)
+    y32 = _hxq.moe_ffn(x.to(dev), r, bg, bu, bd, out_dtype=torch.float32)
+    assert _maxrel(y32.cpu().numpy(), ref) <= 2e-2
+
+
 @pytest.mark.parametrize("T,E,k,H,I,renorm", [(128, 8, 2, 256, 256, False),
                                               (33, 16, 4, 512, 512, True)])
 def test_moe_ffn_fp32_activations(dev, T, E, k, H, I, renorm):
