@@ -777,15 +777,21 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
 
 // Ordered split-K reduction of a launch's compact partial tiles:
 // y[m, n] = sum over ranges (in order) + bias, for the tiles' in-range elements.
+// Four consecutive outputs of one tile row per thread: the ks partials of
+// each are loaded together (16-byte loads, all requested before the first
+// is used) and summed in range order, as one element at a time would; y
+// takes 8- or 16-byte stores when vec (out % 4 == 0 and y 16-byte aligned),
+// element stores at the edge of the matrix.
+constexpr int kRedKs = 8;  // the plan splits K at most 8 ways
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float *__restrict__ part,
                                                              int32_t ksplit, int32_t ntiles,
                                                              int32_t t0, int32_t tiles_x,
                                                              int32_t tiles_y, int32_t bm,
                                                              int32_t M, int32_t out,
                                                              const float *bias, void *y,
-                                                             int32_t y_dtype) {
+                                                             int32_t y_dtype, int32_t vec) {
     const int64_t per = (int64_t)bm * kBN;
-    const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+    const int64_t i = (blockIdx.x * 256ll + threadIdx.x) * 4;
     if (i >= per * ntiles) return;
     const int tl = static_cast<int>(i / per);
     const int e = static_cast<int>(i - (int64_t)tl * per);
@@ -794,13 +800,39 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float *__rest
     const int m = ty * bm + e / kBN, n = tx * kBN + e % kBN;
     if (m >= M || n >= out) return;
     const int64_t stride = per * ntiles;
-    float v = part[i];
-    for (int s = 1; s < ksplit; ++s) v += part[s * stride + i];
-    if (bias) v += bias[n];
+    float4 pv[kRedKs];
+#pragma unroll
+    for (int s = 0; s < kRedKs; ++s)
+        if (s < ksplit) pv[s] = *reinterpret_cast<const float4 *>(part + s * stride + i);
+    float v[4] = {pv[0].x, pv[0].y, pv[0].z, pv[0].w};
+#pragma unroll
+    for (int s = 1; s < kRedKs; ++s)
+        if (s < ksplit) {
+            v[0] += pv[s].x;
+            v[1] += pv[s].y;
+            v[2] += pv[s].z;
+            v[3] += pv[s].w;
+        }
+    const int nv = min(4, out - n);
+    if (bias)
+        for (int j = 0; j < nv; ++j) v[j] += bias[n + j];
     const int64_t o = (int64_t)m * out + n;
-    if (y_dtype == HXQ_F32) static_cast<float *>(y)[o] = v;
-    else if (y_dtype == HXQ_BF16) static_cast<uint16_t *>(y)[o] = f32_to_bf16(v);
-    else static_cast<uint16_t *>(y)[o] = f32_to_f16(v);
+    if (vec && nv == 4) {
+        if (y_dtype == HXQ_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(y) + o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            const bool b16 = y_dtype == HXQ_BF16;
+            auto h = [&](float x) { return static_cast<uint32_t>(b16 ? f32_to_bf16(x) : f32_to_f16(x)); };
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + o) =
+                make_uint2(h(v[0]) | (h(v[1]) << 16), h(v[2]) | (h(v[3]) << 16));
+        }
+        return;
+    }
+    for (int j = 0; j < nv; ++j) {
+        if (y_dtype == HXQ_F32) static_cast<float *>(y)[o + j] = v[j];
+        else if (y_dtype == HXQ_BF16) static_cast<uint16_t *>(y)[o + j] = f32_to_bf16(v[j]);
+        else static_cast<uint16_t *>(y)[o + j] = f32_to_f16(v[j]);
+    }
 }
 
 // One launch of the plan: tiles [t0, t0 + n) of the order, K split ks ways.
@@ -1100,10 +1132,12 @@ extern "C" int hxq_prefill_gemm(const void *x, int32_t x_dtype, int32_t format,
 #undef HXQ_PG_LAUNCH
         HXQ_LAUNCH_CHECK();
         if (L.ks > 1) {
-            const int64_t n = int64_t{1} * L.n * p.bm * pg::kBN;
+            HXQ_REQUIRE(L.ks <= pg::kRedKs, "K split above the reduce's limit");
+            const int64_t n = int64_t{1} * L.n * p.bm * pg::kBN / 4;  // four outputs per thread
+            const int32_t vec = a.OUT % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
             hipLaunchKernelGGL(pg::prefill_reduce_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)),
                                dim3(256), 0, stream, a.part, L.ks, L.n, L.t0, p.tiles_x, p.tiles_y,
-                               p.bm, a.M, a.OUT, bias, y, y_dtype);
+                               p.bm, a.M, a.OUT, bias, y, y_dtype, vec);
             HXQ_LAUNCH_CHECK();
         }
     }
