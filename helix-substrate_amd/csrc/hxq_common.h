@@ -92,6 +92,12 @@ __device__ __forceinline__ float affine_exact(float c, float s, float o) {
     return t + o;
 }
 
+// The affine as one rounding, fl(c * s + o): the form of the reference's GPU
+// kernel (a contracted multiply-add) and what the GEMMs take for 16-bit
+// operands, which round it to bf16/fp16 right after (2^-9 relative against
+// an fp32 difference of at most one ulp).
+__device__ __forceinline__ float affine_fma(float c, float s, float o) { return fmaf(c, s, o); }
+
 // Workgroup barrier that orders LDS only: it waits for this wave's LDS
 // traffic (lgkmcnt) but leaves global loads in flight, so prefetched data
 // can stream in across the barrier.  Use it where no global stores need to

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kGemmThreads, 3) void gemm_kernel(const GemmArgs g)
     #pragma unroll
                         for (int b = 0; b < 4; ++b) {
                             const float c = lookup(part_of(i), w, b);
-                            v[b] = AFFINE ? affine_exact(c, so[i].x, so[i].y) : c;
+                            v[b] = AFFINE ? affine_fma(c, so[i].x, so[i].y) : c;
                         }
                         pk[dd * 2] = pack2<BF16>(v[0], v[1]);
                         pk[dd * 2 + 1] = pack2<BF16>(v[2], v[3]);

@@ -27,8 +27,11 @@
 //     replicated 64x in LDS (lane l reads replica l: no bank conflicts; the
 //     byte address {0, 0, idx, 4l} is one v_perm_b32); uint16 and pair
 //     codebooks are one 4096-entry table; 6-bit levels need none.  The
-//     affine is applied as fl(fl(c * scale) + offset) (two roundings, the
-//     reference's order), then v_cvt_pk_bf16_f32 / f16;
+//     affine is one FMA, fl(c * scale + offset), for 16-bit operands (the
+//     form of the reference's GPU kernel, triton_affine_group_matmul.py:99;
+//     rounded to 16 bits right after) and fl(fl(c * scale) + offset), the
+//     reference's PyTorch order, for fp32 activations; then
+//     v_cvt_pk_bf16_f32 / f16;
 //   * B of step s+1 is built while the MFMAs of step s run (substep by
 //     substep), index loads run two steps ahead and X loads one, one barrier
 //     per step.
@@ -456,8 +459,8 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
                     float v0 = tbl[q[t] & (kPairCodes - 1u)];
                     float v1 = tbl[(q[t] >> 16) & (kPairCodes - 1u)];
                     if constexpr (AFFINE) {
-                        v0 = affine_exact(v0, sc, of);
-                        v1 = affine_exact(v1, sc, of);
+                        v0 = affine_fma(v0, sc, of);
+                        v1 = affine_fma(v1, sc, of);
                     }
                     b[16 * j + 4 * s + t] = pack2<BF16>(v0, v1);
                 }
@@ -487,7 +490,7 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
                 for (int t = 0; t < 4; ++t) {
                     const float v0 = static_cast<float>(field24(qv[buf][NQ * j], qv[buf][NQ * j + 1], 48 * s + 12 * t, 6));
                     const float v1 = static_cast<float>(field24(qv[buf][NQ * j], qv[buf][NQ * j + 1], 48 * s + 12 * t + 6, 6));
-                    b[16 * j + 4 * s + t] = pack2<BF16>(affine_exact(v0, sc, of), affine_exact(v1, sc, of));
+                    b[16 * j + 4 * s + t] = pack2<BF16>(affine_fma(v0, sc, of), affine_fma(v1, sc, of));
                 }
                 continue;
             }
@@ -500,10 +503,10 @@ __global__ __launch_bounds__(kBN / (32 * NJ) * 64, BM == 64 ? 4 : 1) void prefil
                 float v2 = tbl_lookup0<kNrep, 2>(lane_off, w);
                 float v3 = tbl_lookup0<kNrep, 3>(lane_off, w);
                 if constexpr (AFFINE) {
-                    v0 = affine_exact(v0, sc, of);
-                    v1 = affine_exact(v1, sc, of);
-                    v2 = affine_exact(v2, sc, of);
-                    v3 = affine_exact(v3, sc, of);
+                    v0 = affine_fma(v0, sc, of);
+                    v1 = affine_fma(v1, sc, of);
+                    v2 = affine_fma(v2, sc, of);
+                    v3 = affine_fma(v3, sc, of);
                 }
                 b[16 * j + 2 * d] = pack2<BF16>(v0, v1);
                 b[16 * j + 2 * d + 1] = pack2<BF16>(v2, v3);

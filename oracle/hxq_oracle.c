@@ -15,6 +15,13 @@
  *                            op order idx->value*scale then +offset follows
  *                            triton_affine_group_matmul.py:379):
  *                            W[o,k] = fl(fl(cb[idx]*s[o,k/G]) + off[o,k/G]).
+ *   hxq_oracle_reconstruct_fma  the same W with the affine as one rounding,
+ *                            fl(cb[idx]*s + off) (C99 fmaf, correctly rounded
+ *                            in glibc): the form the reference's GPU kernel
+ *                            computes (triton_affine_group_matmul.py:99, Triton
+ *                            contracts the multiply-add) and the GEMM kernels'
+ *                            16-bit operands take before their bf16/fp16
+ *                            rounding.
  *   hxq_oracle_linear_f64    x @ W^T (+bias), fp64 accumulation.  The reference
  *                            computes the same contraction with torch matmul
  *                            (helix_linear.py:809-820, triton_vq_matmul.py:521).
@@ -53,12 +60,12 @@ int hxq_oracle_version(void) { return 1; }
  * sc_pos are flat row-major positions into the full [out, in] matrix
  * (the on-disk sidecar.npz layout), sc_val the replacement values.
  */
-int hxq_oracle_reconstruct(const uint8_t *idx, const float *codebook,
-                           const float *group_scale, const float *group_offset,
-                           int32_t group_size, const int64_t *sc_pos,
-                           const float *sc_val, int64_t nnz,
-                           int64_t out_features, int64_t in_features,
-                           int64_t row_begin, int64_t row_end, float *w_out)
+static int reconstruct_rows(const uint8_t *idx, const float *codebook,
+                            const float *group_scale, const float *group_offset,
+                            int32_t group_size, const int64_t *sc_pos,
+                            const float *sc_val, int64_t nnz,
+                            int64_t out_features, int64_t in_features,
+                            int64_t row_begin, int64_t row_end, float *w_out, int fused)
 {
     if (row_begin < 0 || row_end > out_features || row_begin > row_end)
         return 1;
@@ -73,8 +80,12 @@ int hxq_oracle_reconstruct(const uint8_t *idx, const float *codebook,
             float v = codebook[irow[k]];
             if (has_affine) {
                 const int64_t g = o * n_groups + k / group_size;
-                volatile float t = v * group_scale[g]; /* first rounding */
-                v = t + group_offset[g];               /* second rounding */
+                if (fused) {
+                    v = fmaf(v, group_scale[g], group_offset[g]); /* one rounding */
+                } else {
+                    volatile float t = v * group_scale[g]; /* first rounding */
+                    v = t + group_offset[g];               /* second rounding */
+                }
             }
             wrow[k] = v;
         }
@@ -89,6 +100,31 @@ int hxq_oracle_reconstruct(const uint8_t *idx, const float *codebook,
             w_out[p - lo] = sc_val[i];
     }
     return 0;
+}
+
+int hxq_oracle_reconstruct(const uint8_t *idx, const float *codebook,
+                           const float *group_scale, const float *group_offset,
+                           int32_t group_size, const int64_t *sc_pos,
+                           const float *sc_val, int64_t nnz,
+                           int64_t out_features, int64_t in_features,
+                           int64_t row_begin, int64_t row_end, float *w_out)
+{
+    return reconstruct_rows(idx, codebook, group_scale, group_offset, group_size, sc_pos,
+                            sc_val, nnz, out_features, in_features, row_begin, row_end,
+                            w_out, 0);
+}
+
+/* As hxq_oracle_reconstruct, the affine as fl(cb[idx] * s + off). */
+int hxq_oracle_reconstruct_fma(const uint8_t *idx, const float *codebook,
+                               const float *group_scale, const float *group_offset,
+                               int32_t group_size, const int64_t *sc_pos,
+                               const float *sc_val, int64_t nnz,
+                               int64_t out_features, int64_t in_features,
+                               int64_t row_begin, int64_t row_end, float *w_out)
+{
+    return reconstruct_rows(idx, codebook, group_scale, group_offset, group_size, sc_pos,
+                            sc_val, nnz, out_features, in_features, row_begin, row_end,
+                            w_out, 1);
 }
 
 /* y[m, o] = sum_k x[m, k] * w[o, k] (+ bias[o]); every product and sum in fp64. */

@@ -82,6 +82,8 @@ def _load():
         lib.hxq_oracle_reconstruct.argtypes = [P, P, P, P, ctypes.c_int32, P, P, I64,
                                                I64, I64, I64, I64, P]
         lib.hxq_oracle_reconstruct.restype = ctypes.c_int
+        lib.hxq_oracle_reconstruct_fma.argtypes = lib.hxq_oracle_reconstruct.argtypes
+        lib.hxq_oracle_reconstruct_fma.restype = ctypes.c_int
         lib.hxq_oracle_linear_f64.argtypes = [P, I64, P, I64, I64, P, P]
         lib.hxq_oracle_linear_f64.restype = ctypes.c_int
         lib.hxq_oracle_ssm_scan_f64.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, I64,
@@ -108,9 +110,13 @@ def _c(a, dtype):
 # --------------------------------------------------------------------------
 
 def reconstruct(indices, codebook, group_scale=None, group_offset=None, group_size=128,
-                sidecar_positions=None, sidecar_values=None, row_begin=0, row_end=None):
+                sidecar_positions=None, sidecar_values=None, row_begin=0, row_end=None,
+                fma=False):
     """C restatement; returns fp32 [row_end-row_begin, in_features].  uint8
-    indices only (wide indices: reconstruct_np)."""
+    indices only (wide indices: reconstruct_np).  fma=True takes the affine as
+    one rounding, fl(c * s + o): the reference GPU kernel's form
+    (triton_affine_group_matmul.py:99, a contracted multiply-add) and what
+    the GEMM kernels round to 16 bits for their operands."""
     if np.asarray(indices).dtype.itemsize != 1:
         raise ValueError("the C reconstruction takes uint8 indices; use reconstruct_np")
     idx = _c(indices, np.uint8)
@@ -123,17 +129,40 @@ def reconstruct(indices, codebook, group_scale=None, group_offset=None, group_si
     val = _c(sidecar_values, np.float32)
     nnz = 0 if pos is None else pos.size
     w = np.empty((row_end - row_begin, in_f), dtype=np.float32)
-    rc = _load().hxq_oracle_reconstruct(_ptr(idx), _ptr(cb), _ptr(s), _ptr(o), int(group_size),
-                                        _ptr(pos), _ptr(val), nnz, out_f, in_f, row_begin,
-                                        row_end, _ptr(w))
+    lib = _load()
+    fn = lib.hxq_oracle_reconstruct_fma if fma else lib.hxq_oracle_reconstruct
+    rc = fn(_ptr(idx), _ptr(cb), _ptr(s), _ptr(o), int(group_size), _ptr(pos), _ptr(val),
+            nnz, out_f, in_f, row_begin, row_end, _ptr(w))
     if rc != 0:
         raise ValueError(f"hxq_oracle_reconstruct failed (rc={rc})")
     return w
 
 
+def fma_f32(a, b, c):
+    """fl(a * b + c) for fp32 arrays with ONE rounding (C99 fmaf), elementwise.
+
+    a * b is exact in fp64 (24 + 24 significand bits); r = fl64(a*b + c) and
+    its error e (Knuth's TwoSum, exact) give the exact sum r + e.  Rounding r
+    to fp32 is then correct except where r sits exactly on an fp32 midpoint
+    with e != 0 (an fp32 midpoint is an fp64 number, so no other midpoint can
+    lie between r and the exact sum): there the sign of e picks the side."""
+    p = np.asarray(a, np.float32).astype(np.float64) * np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    r = p + c64
+    bb = r - p
+    e = (p - (r - bb)) + (c64 - bb)
+    f = r.astype(np.float32)
+    d = r - f.astype(np.float64)                      # exact (Sterbenz)
+    toward = np.nextafter(f, np.where(d > 0, np.float32(np.inf), np.float32(-np.inf)))
+    gap = np.abs(toward.astype(np.float64) - f.astype(np.float64))
+    flip = (d != 0) & (2 * np.abs(d) == gap) & (e != 0) & (np.sign(e) == np.sign(d))
+    return np.where(flip, toward, f).astype(np.float32)
+
+
 def reconstruct_np(indices, codebook, group_scale=None, group_offset=None, group_size=128,
-                   sidecar_positions=None, sidecar_values=None):
-    """numpy restatement (float32 arithmetic rounds after every op)."""
+                   sidecar_positions=None, sidecar_values=None, fma=False):
+    """numpy restatement (float32 arithmetic rounds after every op; fma=True:
+    the affine as one rounding, as reconstruct)."""
     idx = np.asarray(indices)
     cb = np.asarray(codebook, dtype=np.float32)
     w = cb[idx]
@@ -142,8 +171,11 @@ def reconstruct_np(indices, codebook, group_scale=None, group_offset=None, group
         g = in_f // group_size
         s = np.repeat(np.asarray(group_scale, np.float32).reshape(out_f, g), group_size, axis=1)
         o = np.repeat(np.asarray(group_offset, np.float32).reshape(out_f, g), group_size, axis=1)
-        w = (w * s).astype(np.float32)
-        w = (w + o).astype(np.float32)
+        if fma:
+            w = fma_f32(w, s, o)
+        else:
+            w = (w * s).astype(np.float32)
+            w = (w + o).astype(np.float32)
     if sidecar_positions is not None:
         flat = w.ravel().copy()
         flat[np.asarray(sidecar_positions, np.int64)] = np.asarray(sidecar_values, np.float32)
@@ -780,15 +812,17 @@ def reconstruct_vq2_np(pair_indices, codebook, positions=None, values=None):
     return w
 
 
-def reconstruct_af6_np(levels, scale, offset, group_size, positions=None, values=None):
+def reconstruct_af6_np(levels, scale, offset, group_size, positions=None, values=None,
+                       fma=False):
     """Per-group affine of integer levels (reference
     affine_group_matmul_reference, triton_affine_group_matmul.py:366-383):
-    W = idx * scale + offset as two fp32 operations; sidecar values replace."""
+    W = idx * scale + offset as two fp32 operations (fma=True: one rounding,
+    the GPU kernel's form at :99); sidecar values replace."""
     q = np.asarray(levels).astype(np.float32)
     rows, cols = q.shape
     s = np.repeat(np.asarray(scale, np.float32), group_size, axis=1)
     o = np.repeat(np.asarray(offset, np.float32), group_size, axis=1)
-    w = ((q * s).astype(np.float32) + o).astype(np.float32)
+    w = fma_f32(q, s, o) if fma else ((q * s).astype(np.float32) + o).astype(np.float32)
     if positions is not None and len(positions):
         flat = w.reshape(-1)
         flat[np.asarray(positions, np.int64)] = np.asarray(values, np.float32)

@@ -3,7 +3,8 @@ any multiple of 16, on the fused HIP kernels: the module keeps the reference
 layout and the kernels read zero-padded index rows (and zero affine groups)
 with zero-padded activations.  Against the fp64 oracle of the exact W:
 dequant bit-exact; GEMV 1e-5 (fp32 x) / 2e-2 (bf16 x); prefill GEMM 1e-5
-(fp32 x) / 2e-2 and 2e-5 against W rounded to bf16 (bf16 x)."""
+(fp32 x) / 2e-2 and 2e-5 against W (the affine as one rounding, the 16-bit
+operand form) rounded to bf16 (bf16 x)."""
 import numpy as np
 import pytest
 import torch
@@ -20,7 +21,7 @@ def _maxrel(y, ref):
     return float(np.abs(np.asarray(y, np.float64) - ref).max() / np.abs(ref).max())
 
 
-def _scalar(out_f, in_f, G, seed):
+def _scalar(out_f, in_f, G, seed, fma=False):
     L = (synth.make_layer_np(out_f, in_f, seed=seed, group_size=G, density=0.005) if G else
          synth.make_layer_np(out_f, in_f, seed=seed, affine=False, density=0.005))
     T = synth.to_torch(L)
@@ -28,9 +29,10 @@ def _scalar(out_f, in_f, G, seed):
                     T["sidecar_values"], bias=torch.linspace(-0.5, 0.5, out_f),
                     group_scale=T["group_scale"], group_offset=T["group_offset"],
                     group_size=G or 128)
-    W = oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
-                           L["group_size"], L["sidecar_positions"], L["sidecar_values"])
-    return m, W
+    args = (L["indices"], L["codebook"], L["group_scale"], L["group_offset"], L["group_size"],
+            L["sidecar_positions"], L["sidecar_values"])
+    W = oracle.reconstruct(*args)
+    return (m, W, oracle.reconstruct(*args, fma=True)) if fma else (m, W)
 
 
 def _check_module(m, W, dev, rows=(1, 3, 40)):
@@ -69,9 +71,10 @@ def test_scalar_any_k(dev, out_f, in_f, G):
 @pytest.mark.parametrize("in_f,G", [(4000, 32), (2048, 16), (3072, 96)])
 def test_bf16_gemm_tight_bar_any_group(dev, in_f, G):
     """bf16 activations on the GEMM: against W rounded to bf16 with the affine
-    as two roundings, only fp32 accumulation order is left (2e-5)."""
+    as one rounding (the operand form), only fp32 accumulation order is left
+    (2e-5)."""
     from helix_substrate import _hxq
-    m, W = _scalar(320, in_f, G, seed=G)
+    m, W, Wf = _scalar(320, in_f, G, seed=G, fma=True)
     m = m.to(dev)
     x = torch.randn(64, in_f, generator=torch.Generator().manual_seed(G)).to(torch.bfloat16)
     y = m(x.to(dev)).float().cpu().numpy()
@@ -80,7 +83,7 @@ def test_bf16_gemm_tight_bar_any_group(dev, in_f, G):
                             m._sc_grp_val, m.bias, out_dtype=torch.float32).cpu().numpy()
     b = m.bias.cpu().numpy()
     xf = x.float().numpy()
-    W16 = torch.from_numpy(W).to(torch.bfloat16).float().numpy()
+    W16 = torch.from_numpy(Wf).to(torch.bfloat16).float().numpy()
     assert _maxrel(y, oracle.linear_f64(xf, W, b)) <= 2e-2
     assert _maxrel(y32, oracle.linear_np(xf, W16, b)) <= 2e-5
 

@@ -24,16 +24,17 @@ def _maxrel(y, ref):
     return float(np.abs(np.asarray(y, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
 
 
-def _case(fmt, out, inp, k=4096, G=128, nsc=0.001, seed=0):
+def _case(fmt, out, inp, k=4096, G=128, nsc=0.001, seed=0, fma=False):
     """(raw index tensor, codebook, scale, offset, positions, values, W, W
-    without the sidecar) -- the oracle's reconstructions."""
+    without the sidecar) -- the oracle's reconstructions (fma: the 6-bit
+    affine as one rounding, the 16-bit operand form)."""
     rs = np.random.RandomState(seed)
     if fmt == _hxq.FMT_AF6:
         q = rs.randint(0, 64, (out, inp))
         s = rs.uniform(0.5, 1.5, (out, inp // G)).astype(np.float16).astype(np.float32) * 1e-3
         o = (rs.randn(out, inp // G) * 1e-2).astype(np.float16).astype(np.float32)
         raw, cb = pack_6bit(torch.from_numpy(q)), None
-        rec = lambda p, v: oracle.reconstruct_af6_np(q, s, o, G, p, v)
+        rec = lambda p, v: oracle.reconstruct_af6_np(q, s, o, G, p, v, fma=fma)
     else:
         cb = (rs.randn(k, 2) * 0.02).astype(np.float32)
         idx = rs.randint(0, k, (out, inp // 2))
@@ -192,14 +193,16 @@ def _grp(dev, pos, val, out, inp):
 def test_prefill_fmt_matches_oracle(dev, fmt, m, out, inp, G, xdt):
     """Against the oracle's W: 16-bit activations at the 2e-2 bar in fp64 and
     at 2e-5 against W rounded to the activation type (all that is left is
-    fp32 accumulation order); fp32 activations at 1e-5 against the exact W."""
+    fp32 accumulation order; the affine there as one rounding, the operand
+    form); fp32 activations at 1e-5 against the exact W."""
     if fmt == _hxq.FMT_SCALAR_U16:
-        mod, W = _wide_layer(out, inp, 3000, seed=m + out, group_size=G)
+        mod, W, Wf = _wide_layer(out, inp, 3000, seed=m + out, group_size=G, fma=True)
         raw, cb, aff = mod.indices, mod.codebook, mod._affine_t
         gp, gk, gv = mod._sc_grp_ptr, mod._sc_grp_key, mod._sc_grp_val
         raw, cb, aff, gp, gk, gv = _dev(dev, raw, cb, aff, gp, gk, gv)
     else:
         raw, cb, s, o, pos, val, W, _ = _case(fmt, out, inp, G=G, seed=m + inp)
+        Wf = W if s is None else _case(fmt, out, inp, G=G, seed=m + inp, fma=True)[6]
         aff = None if s is None else np.ascontiguousarray(np.stack([s.T, o.T], axis=-1))
         raw, cb, aff = _dev(dev, raw, cb, aff)
         gp, gk, gv = _grp(dev, pos, val, out, inp)
@@ -215,7 +218,7 @@ def test_prefill_fmt_matches_oracle(dev, fmt, m, out, inp, G, xdt):
         assert _maxrel(y, oracle.linear_np(xf, W, bias.numpy())) <= 1e-5
         return
     assert _maxrel(y, oracle.linear_np(xf, W, bias.numpy())) <= 2e-2
-    W16 = torch.from_numpy(W).to(xdt).float().numpy()
+    W16 = torch.from_numpy(Wf).to(xdt).float().numpy()
     rel = _maxrel(y, oracle.linear_np(xf, W16, bias.numpy()))
     assert rel <= 2e-5, rel
     y16 = _hxq.prefill_gemm(x.to(dev), raw, cb, aff, G, gp, gk, gv, bias=bias.to(dev),
@@ -227,7 +230,7 @@ def test_prefill_fmt_matches_oracle(dev, fmt, m, out, inp, G, xdt):
 # ---------------------------------------------------------------------------
 # scalar codebooks above 256 entries: uint16 indices (int16 in memory)
 # ---------------------------------------------------------------------------
-def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001, group_size=128):
+def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001, group_size=128, fma=False):
     rs = np.random.RandomState(seed)
     cb = np.sort(rs.standard_normal(k).astype(np.float32) * 0.02)
     idx = rs.randint(0, k, (out_f, in_f)).astype(np.uint16)
@@ -242,7 +245,10 @@ def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001, group_size=128
     t = lambda a: None if a is None else torch.from_numpy(a)
     m = HelixLinear(in_f, out_f, t(cb), t(idx.astype(np.int16)), t(pos), t(val),
                     group_scale=t(gs), group_offset=t(go), group_size=group_size)
-    return m, oracle.reconstruct_np(idx, cb, gs, go, group_size, pos, val)
+    W = oracle.reconstruct_np(idx, cb, gs, go, group_size, pos, val)
+    if not fma:
+        return m, W
+    return m, W, oracle.reconstruct_np(idx, cb, gs, go, group_size, pos, val, fma=True)
 
 
 @pytest.mark.parametrize("k,out_f,in_f,affine", [

@@ -4,10 +4,12 @@ Two bars per case:
   * the BASELINE bar: max|Y - Y_ref| / max|Y_ref| <= 2e-2 with Y_ref the fp64
     contraction of the 16-bit activations with the exact fp32 W;
   * a tight bar pinning layout, sidecar and affine handling: against W
-    rounded to the activation's 16-bit type (what the kernel multiplies,
-    the affine kept as two roundings fl(fl(c * s) + o) like the oracle), the
-    only error left is fp32 accumulation order, so <= 2e-5.
+    rounded to the activation's 16-bit type (what the kernel multiplies, the
+    affine taken as one rounding fl(c * s + o) before that, as the
+    reference's GPU kernel does), the only error left is fp32 accumulation
+    order, so <= 2e-5.
 """
+import collections
 import functools
 
 import numpy as np
@@ -33,9 +35,15 @@ def _module(T, dev, bias=None):
                        group_offset=T["group_offset"], group_size=T["group_size"]).to(dev)
 
 
+Ws = collections.namedtuple("Ws", "exact fused")
+
+
 def _oracle_w(L):
-    return oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
-                              L["group_size"], L["sidecar_positions"], L["sidecar_values"])
+    """The oracle's W with the affine as two roundings (exact: the BASELINE
+    bar's W) and as one (fused: the 16-bit operands' form)."""
+    args = (L["indices"], L["codebook"], L["group_scale"], L["group_offset"], L["group_size"],
+            L["sidecar_positions"], L["sidecar_values"])
+    return Ws(oracle.reconstruct(*args), oracle.reconstruct(*args, fma=True))
 
 
 def _maxrel(y, y_ref):
@@ -46,18 +54,18 @@ def _check(y, x16, W, bias=None):
     """BASELINE bar for any output dtype; the tight bar for fp32 outputs (a
     16-bit output adds its own rounding of ~2^-9).  y may hold several
     kernels' outputs side by side ([M, k * OUT], as _gemm32 returns)."""
-    if y.shape[1] != W.shape[0]:
-        for part in torch.split(y, W.shape[0], dim=1):
+    if y.shape[1] != W.exact.shape[0]:
+        for part in torch.split(y, W.exact.shape[0], dim=1):
             _check(part, x16, W, bias)
         return
     xf = x16.float().numpy()
     b = None if bias is None else bias.numpy()
     is32 = y.dtype == torch.float32
     y = y.float().cpu().numpy()
-    ref = oracle.linear_np(xf, W, b)
+    ref = oracle.linear_np(xf, W.exact, b)
     assert _maxrel(y, ref) <= 2e-2
     if is32:
-        W16 = torch.from_numpy(W).to(x16.dtype).float().numpy()
+        W16 = torch.from_numpy(W.fused).to(x16.dtype).float().numpy()
         rel = _maxrel(y, oracle.linear_np(xf, W16, b))
         assert rel <= 2e-5, rel
 
@@ -142,7 +150,7 @@ def test_prefill_sidecar_dense_block_and_repeats(dev):
     T = synth.to_torch(L)
     mod = _module(T, dev)
     W = _oracle_w(L)
-    assert np.array_equal(W.ravel()[rep], val[-50:])   # the last copy is the oracle's value
+    assert np.array_equal(W.exact.ravel()[rep], val[-50:])   # the last copy is the oracle's value
     x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
     assert _hxq.lib().hxq_prefill_gemm_workspace_bytes(m, out_f, in_f) > 0   # K is split
     _check(_gemm32(mod, x.to(dev)), x, W)
@@ -171,7 +179,7 @@ def test_fp32_prefill_gemm_matches_oracle(dev, m, out_f, in_f, density):
     L, T = _layer(out_f, in_f, seed=14 + m, density=density)
     bias = torch.linspace(-1, 1, out_f)
     mod = _module(T, dev, bias=bias)
-    W = _oracle_w(L)
+    W = _oracle_w(L).exact
     x = torch.randn(m, in_f, generator=torch.Generator().manual_seed(7))
     y = mod(x.to(dev))
     assert mod._last_dispatch_path == "hip_gemm" and y.dtype == torch.float32
@@ -189,7 +197,7 @@ def test_fp32_prefill_config2_gate_up_rows(dev):
     y = mod(x.to(dev))
     assert mod._last_dispatch_path == "hip_gemm"
     rows = _row_slice(m)
-    ref = oracle.linear_np(x[rows].numpy(), _oracle_w(L))
+    ref = oracle.linear_np(x[rows].numpy(), _oracle_w(L).exact)
     assert _maxrel(y[rows].cpu().numpy(), ref) <= 1e-5
 
 

@@ -94,7 +94,9 @@ def test_grouped_gemm_matches_oracle(dev, T, E, k, out_f, in_f):
         W = oracle.reconstruct(**layers[e])
         ref = oracle.linear_np(xf[rows[lo:hi]], W)
         assert _maxrel(y[lo:hi], ref) <= 2e-2
-        W16 = torch.from_numpy(W).to(torch.bfloat16).float().numpy()
+        # the operand form: the affine as one rounding, then bf16
+        Wf = oracle.reconstruct(**layers[e], fma=True)
+        W16 = torch.from_numpy(Wf).to(torch.bfloat16).float().numpy()
         assert _maxrel(y[lo:hi], oracle.linear_np(xf[rows[lo:hi]], W16)) <= 2e-4, e
 
 

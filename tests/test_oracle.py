@@ -58,6 +58,81 @@ def test_affine_keeps_two_roundings(impl):
     assert np.float32(2.0**-11) != np.float32(2.0**-11 + 2.0**-24)
 
 
+def _round_f32_exact(q):
+    """The fp32 nearest the rational q, ties to even significand: brute force
+    over the neighbours of a first guess, distances in exact rationals."""
+    from fractions import Fraction
+    f = np.float32(float(q))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    return min(cands, key=lambda c: (abs(Fraction(float(c)) - q),
+                                     int(np.array(c, np.float32).view(np.uint32)) & 1))
+
+
+def _fused_both(c, s, o):
+    """oracle.fma_f32 and the C restatement (fma=True), element by element."""
+    n = len(c)
+    cb = np.zeros(256, np.float32)
+    idx = np.zeros((n, 16), np.uint8)
+    out = []
+    for lo in range(0, n, 256):
+        k = min(256, n - lo)
+        cb[:k] = c[lo:lo + k]
+        idx[:k] = np.arange(k, dtype=np.uint8)[:, None]
+        w = oracle.reconstruct(idx[:k], cb, s[lo:lo + k, None], o[lo:lo + k, None], 16, fma=True)
+        out.append(w[:, 0])
+    return oracle.fma_f32(c, s, o), np.concatenate(out)
+
+
+def test_fused_affine_is_one_exact_rounding():
+    """fl(c * s + o) against exact rational arithmetic: random codebook-like
+    operands, plus the two-rounding counter-example above and a case whose
+    fp64 sum lands exactly on an fp32 midpoint below the exact value (the
+    TwoSum correction) -- a naive fp64-then-fp32 rounding fails that one."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    n = 6000
+    c = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    s = rng.uniform(0.5, 2.0, n).astype(np.float32)
+    o = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    u = np.float32(1 + 2.0**-12)
+    mid_c = np.float32(2.0**-12 * (1 + 2.0**-23))
+    mid_s = np.float32(2.0**-12 * (1 - 2.0**-23))
+    mid_o = np.float32(1 + 2.0**-23)
+    c = np.append(c, [u, mid_c]).astype(np.float32)
+    s = np.append(s, [u, mid_s]).astype(np.float32)
+    o = np.append(o, [-1.0, mid_o]).astype(np.float32)
+    want = np.array([_round_f32_exact(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(d)))
+                     for a, b, d in zip(c, s, o)], np.float32)
+    for got in _fused_both(c, s, o):
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert want[-2] == np.float32(2.0**-11 + 2.0**-24)
+    assert want[-1] == np.float32(1 + 2.0**-23)
+    naive = (c.astype(np.float64) * s.astype(np.float64) + o.astype(np.float64)).astype(np.float32)
+    assert naive[-1] != want[-1]
+    two = ((c * s).astype(np.float32) + o).astype(np.float32)
+    assert np.count_nonzero(two != want) > 0        # the random part tells the forms apart
+
+
+def test_fused_reconstruct_c_numpy_af6_agree():
+    from helix_substrate import synth
+
+    L = synth.make_layer_np(96, 512, seed=12, density=0.01)
+    args = (L["indices"], L["codebook"], L["group_scale"], L["group_offset"], 128,
+            L["sidecar_positions"], L["sidecar_values"])
+    a = oracle.reconstruct(*args, fma=True)
+    b = oracle.reconstruct_np(*args, fma=True)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.count_nonzero(a != oracle.reconstruct(*args)) > 0
+    np.testing.assert_array_equal(a.ravel()[L["sidecar_positions"]], L["sidecar_values"])
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 64, (8, 256))
+    sc = rng.uniform(1e-3, 2e-3, (8, 4)).astype(np.float32)
+    of = (rng.standard_normal((8, 4)) * 1e-2).astype(np.float32)
+    w = oracle.reconstruct_af6_np(q, sc, of, 64, fma=True)
+    ref = oracle.fma_f32(q.astype(np.float32), np.repeat(sc, 64, 1), np.repeat(of, 64, 1))
+    np.testing.assert_array_equal(w.view(np.uint32), ref.view(np.uint32))
+
+
 def test_no_affine_is_plain_gather():
     rng = np.random.default_rng(0)
     cb = rng.normal(size=256).astype(np.float32)
