@@ -17,6 +17,9 @@ Reference functions restated (file:line under the reference checkout):
   sidecar *replaces* values.  The per-group affine extension
   ``fl(fl(cb[idx]*s) + off)`` has no reference implementation; its op order
   follows ``triton_affine_group_matmul.py:379`` (value*scale, then +offset).
+  ``fma=True`` (and ``fma_f32``) gives the single-rounding form
+  ``fl(cb[idx]*s + off)`` of the reference's Triton kernel
+  (``triton_affine_group_matmul.py:99``), the GEMMs' 16-bit operand form.
 * ``linear_f64``       -- ``x @ W^T + bias`` (``helix_linear.py:809-820``) in fp64.
 * ``ssm_scan_f64``     -- ``sequential_scan`` (``mamba_scan_chunked.py:42-86``).
 * ``moe_route_np`` / ``moe_sorted_lists_np`` / ``moe_ffn_np`` -- the OLMoE
