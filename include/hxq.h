@@ -26,6 +26,11 @@
  *     W[o,k] = fl(fl(codebook[idx[o,k]] * s[o,k/G]) + off[o,k/G])  (affine)
  *     W[o,k] = codebook[idx[o,k]]                                   (no affine)
  *     W[o,k] = sc_val  where (o,k) is a sidecar position (replacement).
+ *   GEMMs with bf16/fp16 activations multiply W rounded to the activation
+ *   type, the affine taken there as one rounding, fl(codebook * s + off),
+ *   as the reference's GPU kernel computes it
+ *   (triton_affine_group_matmul.py:99); everything that produces or
+ *   contracts fp32 W uses the two-rounding form above.
  */
 #ifndef HXQ_H
 #define HXQ_H
