@@ -201,6 +201,60 @@ def test_fp32_prefill_config2_gate_up_rows(dev):
     assert _maxrel(y[rows].cpu().numpy(), ref) <= 1e-5
 
 
+def _to16(a, dt):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dt).float().numpy()
+
+
+def _form_splitting_triples(dt, n, seed):
+    """n codebook-like (c, s, o) whose 16-bit operand differs between the
+    single-rounding affine fl(c * s + o) and the two-rounding fl(fl(c * s) + o)."""
+    rng = np.random.default_rng(seed)
+    cs, ss, os_ = [], [], []
+    while len(cs) < n:
+        c = (rng.standard_normal(1 << 20) * 0.05).astype(np.float32)
+        s = rng.uniform(0.5, 2.0, c.size).astype(np.float32)
+        o = (rng.standard_normal(c.size) * 0.02).astype(np.float32)
+        two = ((c * s).astype(np.float32) + o).astype(np.float32)
+        m = np.nonzero(_to16(oracle.fma_f32(c, s, o), dt) != _to16(two, dt))[0]
+        cs += list(c[m]); ss += list(s[m]); os_ += list(o[m])
+    return (np.array(cs[:n], np.float32), np.array(ss[:n], np.float32),
+            np.array(os_[:n], np.float32))
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_operands_bit_exact_one_hot(dev, dt):
+    """x = I: every output element is one operand times 1, so the fp32 outputs
+    of both GEMM kernels (and the 16-bit module output) are the operand matrix
+    itself, checked bit for bit against the oracle's W with the affine as one
+    rounding, rounded to x's type.  Rows 0..63 each hold a triple whose 16-bit
+    operand the two-rounding form gets wrong (column 5, affine group 0)."""
+    out_f, in_f, G = 256, 128, 64
+    c, s, o = _form_splitting_triples(dt, 64, seed=11 if dt == torch.bfloat16 else 12)
+    rng = np.random.default_rng(5)
+    cb = np.concatenate([c, (rng.standard_normal(192) * 0.05).astype(np.float32)])
+    idx = rng.integers(64, 256, (out_f, in_f)).astype(np.uint8)
+    idx[np.arange(64), 5] = np.arange(64)
+    gs = rng.uniform(0.5, 2.0, (out_f, in_f // G)).astype(np.float32)
+    go = (rng.standard_normal((out_f, in_f // G)) * 0.02).astype(np.float32)
+    gs[:64, 0], go[:64, 0] = s, o
+    pos = np.sort(rng.choice(out_f * in_f, 40, replace=False)).astype(np.int64)
+    pos = pos[(pos // in_f >= 64) | (pos % in_f != 5)]        # keep the crafted entries
+    val = (rng.standard_normal(pos.size) * 0.1).astype(np.float32)
+    args = (idx, cb, gs, go, G, pos, val)
+    Wf = _to16(oracle.reconstruct(*args, fma=True), dt)
+    Wt = _to16(oracle.reconstruct(*args), dt)
+    assert np.count_nonzero(Wf[:64, 5] != Wt[:64, 5]) == 64     # the forms differ there
+    t = torch.from_numpy
+    mod = HelixLinear(in_f, out_f, t(cb), t(idx), t(pos), t(val), group_scale=t(gs),
+                      group_offset=t(go), group_size=G).to(dev)
+    x = torch.eye(in_f, dtype=dt, device=dev)
+    y = mod(x)
+    assert mod._last_dispatch_path == "hip_gemm" and y.dtype == dt
+    np.testing.assert_array_equal(y.float().cpu().numpy().T.view(np.uint32), Wf.view(np.uint32))
+    for part in torch.split(_gemm32(mod, x), out_f, dim=1):
+        np.testing.assert_array_equal(part.cpu().numpy().T.view(np.uint32), Wf.view(np.uint32))
+
+
 def test_affine_pack_layout(dev):
     gs = torch.randn(300, 7, device=dev)
     go = torch.randn(300, 7, device=dev)
