@@ -81,6 +81,50 @@ def test_dequant_row_blocks_and_duplicates(dev):
 
 # ---------------------------------------------------------------------- GEMV
 
+def _mat(m):
+    return dict(indices=m.indices, codebook=m._kcb, group_scale=m.group_scale,
+                group_offset=m.group_offset, sc_row_ptr=m._sc_row_ptr, sc_col=m._sc_col,
+                sc_delta=m._sc_delta, bias=None)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_gemv_one_hot_columns_bit_exact(dev, xdt):
+    """x = e_k: the GEMV's folded affine s * sum(x c) + o * sum(x) is then
+    fl(fl(c s) + o) and every other term adds an exact zero, so y = W[:, k]
+    bit for bit against the oracle's two-rounding W.  At a sidecar position
+    the correction x[col] * delta gives fl(W_affine + delta), delta =
+    fl(value - W_affine) as the CSR stores it (restated in numpy here).
+    Every column through the 4-row launch; a spread of columns through the
+    1-row launch and the two-matrix launch of the headline gate+up step."""
+    out_f, in_f, group = 320, 256, 128
+    L, T = _layer(out_f, in_f, seed=77, density=0.01)
+    m = _module(T, dev)
+    pos, val = L["sidecar_positions"], L["sidecar_values"].astype(np.float32)
+    assert np.unique(pos).size == pos.size
+    Wa = oracle.reconstruct(L["indices"], L["codebook"], L["group_scale"], L["group_offset"],
+                            group)
+    flat = Wa.ravel().copy()
+    flat[pos] = (flat[pos] + (val - flat[pos]).astype(np.float32)).astype(np.float32)
+    want = flat.reshape(out_f, in_f)
+    bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)
+    mat = _mat(m)
+    for k0 in range(0, in_f, 4):
+        x = torch.zeros(4, in_f, dtype=xdt)
+        x[torch.arange(4), torch.arange(k0, k0 + 4)] = 1
+        y = _hxq.gemv(x.to(dev), m.indices, m._kcb, m.group_scale, m.group_offset, group,
+                      m._sc_row_ptr, m._sc_col, m._sc_delta, None, out_dtype=torch.float32)
+        np.testing.assert_array_equal(bits(y.cpu().numpy()), bits(want[:, k0:k0 + 4].T))
+    for k in (0, 1, 63, 64, 127, 128, 200, 255):
+        x = torch.zeros(1, in_f, dtype=xdt)
+        x[0, k] = 1
+        y = _hxq.gemv(x.to(dev), m.indices, m._kcb, m.group_scale, m.group_offset, group,
+                      m._sc_row_ptr, m._sc_col, m._sc_delta, None, out_dtype=torch.float32)
+        np.testing.assert_array_equal(bits(y.cpu().numpy()[0]), bits(want[:, k]))
+        y0, y1 = _hxq.gemv_multi(x.to(dev), [mat, mat], group, out_dtype=torch.float32)
+        np.testing.assert_array_equal(bits(y0.cpu().numpy()[0]), bits(want[:, k]))
+        np.testing.assert_array_equal(bits(y1.cpu().numpy()[0]), bits(want[:, k]))
+
+
 @pytest.mark.parametrize("out_f,in_f,group", [
     (2048, 2048, 128),     # config 0 / q, o
     (256, 2048, 128),      # k, v
