@@ -251,6 +251,75 @@ def _wide_layer(out_f, in_f, k, seed, affine=True, density=0.001, group_size=128
     return m, W, oracle.reconstruct_np(idx, cb, gs, go, group_size, pos, val, fma=True)
 
 
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _corrected(W0, pos, delta):
+    """W without the sidecar plus fl(W + delta) at the (sorted, unique)
+    positions: what a one-hot GEMV returns."""
+    flat = W0.ravel().copy()
+    flat[pos] = (flat[pos] + delta).astype(np.float32)
+    return flat.reshape(W0.shape)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_fmt_one_hot_bit_exact(dev, fmt):
+    """x = e_k: the GEMV's output is column k of the oracle's W bit for bit
+    (the 6-bit levels' affine folded as fl(fl(q s) + o); sidecar positions
+    fl(W + delta), delta as the CSR stores it).  x = I (bf16, fp16): the
+    prefill GEMM's fp32 output is its operand matrix, W with the affine as one
+    rounding rounded to x's type (pair codebooks: the entries themselves)."""
+    out, inp, G = 300, 256, 64
+    raw, cb, s, o, pos, val, W, W0 = _case(fmt, out, inp, k=1000, G=G, seed=31)
+    assert np.unique(pos).size == pos.size
+    rp, col, _, delta = _csr(dev, pos, val, W0, out, inp)
+    raw_d, cb_d, s_d, o_d = _dev(dev, raw, cb, s, o)
+    want = _corrected(W0, pos, delta.cpu().numpy())
+    print(f"one-hot fmt={fmt}", flush=True)
+    for k0 in range(0, inp, 4):
+        x = torch.zeros(4, inp)
+        x[torch.arange(4), torch.arange(k0, k0 + 4)] = 1
+        y = _hxq.gemv_fmt(x.to(dev), fmt, raw_d, out, codebook=cb_d, group_scale=s_d,
+                          group_offset=o_d, group_size=G, sc_row_ptr=rp, sc_col=col,
+                          sc_delta=delta)
+        np.testing.assert_array_equal(_bits(y.cpu().numpy()), _bits(want[:, k0:k0 + 4].T))
+    Wf = W if s is None else _case(fmt, out, inp, k=1000, G=G, seed=31, fma=True)[6]
+    aff = None if s is None else np.ascontiguousarray(np.stack([s.T, o.T], axis=-1))
+    (aff_d,) = _dev(dev, aff)
+    gp, gk, gv = _grp(dev, pos, val, out, inp)
+    for dt in (torch.bfloat16, torch.float16):
+        x = torch.eye(inp, dtype=dt, device=dev)
+        y = _hxq.prefill_gemm(x, raw_d, cb_d, aff_d, G, gp, gk, gv, out_dtype=torch.float32,
+                              fmt=fmt, out_features=out)
+        want16 = torch.from_numpy(Wf).to(dt).float().numpy()
+        np.testing.assert_array_equal(_bits(y.cpu().numpy().T), _bits(want16))
+
+
+def test_wide_scalar_one_hot_bit_exact(dev):
+    """uint16 scalar indices (1000-entry codebook, group affine): one-hot GEMV
+    columns bit for bit against the oracle's W (sidecar positions fl(W +
+    delta)); the module's 16-bit output for x = I is the GEMM operand matrix."""
+    out_f, in_f, G = 300, 256, 64
+    m, W, Wf = _wide_layer(out_f, in_f, 1000, seed=41, group_size=G, density=0.01, fma=True)
+    pos = m._sidecar_rows.numpy() * in_f + m._sidecar_cols.numpy()
+    W0 = oracle.reconstruct_np(m.indices.numpy().astype(np.int64) & 0xffff, m.codebook.numpy(),
+                               m.group_scale.numpy(), m.group_offset.numpy(), G)
+    want = _corrected(W0, pos, m._sc_delta.numpy())
+    m = m.to(dev)
+    for k0 in range(0, in_f, 4):
+        x = torch.zeros(4, in_f)
+        x[torch.arange(4), torch.arange(k0, k0 + 4)] = 1
+        y = m(x.to(dev))
+        assert m._last_dispatch_path == "hip_gemv_fmt"
+        np.testing.assert_array_equal(_bits(y.cpu().numpy()), _bits(want[:, k0:k0 + 4].T))
+    for dt in (torch.bfloat16, torch.float16):
+        y = m(torch.eye(in_f, dtype=dt, device=dev))
+        assert m._last_dispatch_path == "hip_gemm" and y.dtype == dt
+        want16 = torch.from_numpy(Wf).to(dt).float().numpy()
+        np.testing.assert_array_equal(_bits(y.float().cpu().numpy().T), _bits(want16))
+
+
 @pytest.mark.parametrize("k,out_f,in_f,affine", [
     (512, 2048, 2048, True),     # the reference's k = 512 case at config-0 size
     (4096, 300, 1024, True),     # largest codebook, ragged rows
