@@ -71,6 +71,30 @@ def test_route_masked_experts_no_duplicates(dev, renorm):
     assert torch.equal(torch.from_numpy(ids)[fin].long(), top.indices[fin])
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_grouped_gemm_one_hot_bit_exact(dev, dt):
+    """Token t's activation row is e_t, so assignment i's fp32 output row is
+    column sorted_rows[i] of its expert's operand matrix -- the expert's W with
+    the affine as one rounding, rounded to x's type -- bit for bit.  Experts
+    with 0, 5, 64, 65, 130 and 200 rows (up to four 64-row tiles)."""
+    E, out_f, in_f = 6, 256, 256
+    layers, bank = _bank(E, out_f, in_f, seed=91, dev=dev, group_size=64, sigma=0.015,
+                         density=0.01)
+    counts = [0, 5, 64, 65, 130, 200]
+    rng = np.random.default_rng(4)
+    rows = np.concatenate([np.sort(rng.choice(in_f, c, replace=False)) for c in counts])
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    t = torch.from_numpy
+    x = torch.eye(in_f, dtype=dt, device=dev)
+    y = _hxq.moe_grouped_gemm(x, t(rows.astype(np.int32)).to(dev), t(offs).to(dev), bank,
+                              int(offs[-1]), out_dtype=torch.float32).cpu().numpy()
+    for e in range(E):
+        Wf = torch.from_numpy(oracle.reconstruct(**layers[e], fma=True)).to(dt).float().numpy()
+        got = np.ascontiguousarray(y[offs[e]:offs[e + 1]])
+        want = np.ascontiguousarray(Wf[:, rows[offs[e]:offs[e + 1]]].T)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=str(e))
+
+
 @pytest.mark.parametrize("T,E,k,out_f,in_f", [
     (200, 8, 2, 256, 512),      # ragged segments
     (300, 4, 1, 384, 256),      # expert 0 takes > 128 rows -> several 64-row tiles
