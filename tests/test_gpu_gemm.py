@@ -221,15 +221,18 @@ def _form_splitting_triples(dt, n, seed):
             np.array(os_[:n], np.float32))
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 def test_operands_bit_exact_one_hot(dev, dt):
     """x = I: every output element is one operand times 1, so the fp32 outputs
-    of both GEMM kernels (and the 16-bit module output) are the operand matrix
+    of both GEMM kernels (and the module output) are the operand matrix
     itself, checked bit for bit against the oracle's W with the affine as one
-    rounding, rounded to x's type.  Rows 0..63 each hold a triple whose 16-bit
-    operand the two-rounding form gets wrong (column 5, affine group 0)."""
+    rounding, rounded to x's type -- and, for fp32 activations (the fp32-MFMA
+    variant), against the exact two-rounding W.  Rows 0..63 each hold a triple
+    whose bf16/fp16 operand the two forms round differently (column 5, affine
+    group 0)."""
     out_f, in_f, G = 256, 128, 64
-    c, s, o = _form_splitting_triples(dt, 64, seed=11 if dt == torch.bfloat16 else 12)
+    c, s, o = _form_splitting_triples(torch.float16 if dt == torch.float16 else torch.bfloat16,
+                                      64, seed=12 if dt == torch.float16 else 11)
     rng = np.random.default_rng(5)
     cb = np.concatenate([c, (rng.standard_normal(192) * 0.05).astype(np.float32)])
     idx = rng.integers(64, 256, (out_f, in_f)).astype(np.uint8)
@@ -241,8 +244,12 @@ def test_operands_bit_exact_one_hot(dev, dt):
     pos = pos[(pos // in_f >= 64) | (pos % in_f != 5)]        # keep the crafted entries
     val = (rng.standard_normal(pos.size) * 0.1).astype(np.float32)
     args = (idx, cb, gs, go, G, pos, val)
-    Wf = _to16(oracle.reconstruct(*args, fma=True), dt)
-    Wt = _to16(oracle.reconstruct(*args), dt)
+    if dt == torch.float32:
+        Wf = oracle.reconstruct(*args)
+        Wt = oracle.reconstruct(*args, fma=True)
+    else:
+        Wf = _to16(oracle.reconstruct(*args, fma=True), dt)
+        Wt = _to16(oracle.reconstruct(*args), dt)
     assert np.count_nonzero(Wf[:64, 5] != Wt[:64, 5]) == 64     # the forms differ there
     t = torch.from_numpy
     mod = HelixLinear(in_f, out_f, t(cb), t(idx), t(pos), t(val), group_scale=t(gs),
@@ -251,6 +258,8 @@ def test_operands_bit_exact_one_hot(dev, dt):
     y = mod(x)
     assert mod._last_dispatch_path == "hip_gemm" and y.dtype == dt
     np.testing.assert_array_equal(y.float().cpu().numpy().T.view(np.uint32), Wf.view(np.uint32))
+    if dt == torch.float32:     # one kernel: the prefill GEMM's fp32-MFMA variant
+        return
     for part in torch.split(_gemm32(mod, x), out_f, dim=1):
         np.testing.assert_array_equal(part.cpu().numpy().T.view(np.uint32), Wf.view(np.uint32))
 
